@@ -1,0 +1,74 @@
+"""ctypes binding of ``libecdecode.so`` (the C ABI declared in ``include/ecdecode.h``).
+
+The library is built in-tree by ``estudiocanciones_amd.build``; if it is missing, every
+call fails loudly -- there is no CPU or eager-PyTorch fallback for the decode path.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_double, c_float, c_int, c_long, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libecdecode.so"
+
+ECD_OK = 0
+ECD_EINVAL = -22
+ECD_ENOTSUP = -95
+
+_P = c_void_p
+# name -> argtypes, in the order of include/ecdecode.h
+SIGNATURES = {
+    "ecd_gemv_i8": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int, _P],
+    "ecd_gemv_i8_tuned": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int,
+                          c_int, c_int, _P],
+    "ecd_rmsnorm": [_P, c_long, _P, _P, c_long, c_int, c_int, c_float, _P],
+    "ecd_rope_kv_write": [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P],
+    "ecd_decode_attn": [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
+                        c_int, c_float, _P],
+    "ecd_attn_combine": [_P, _P, _P, _P, c_int, c_int, c_int, _P],
+    "ecd_silu_mul": [_P, _P, c_int, c_int, _P],
+    "ecd_embed_sum_i8": [_P, _P, _P, c_long, _P, c_int, c_int, c_int, c_int, _P],
+    "ecd_embed_i8": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, c_int, c_int, _P],
+    "ecd_quantize_rows_i8": [_P, _P, _P, _P, c_int, c_int, _P],
+    "ecd_rope_table": [_P, c_int, c_int, c_double, c_double, c_double, c_double, c_double, _P],
+    "ecd_copy_bytes": [_P, _P, c_long, _P],
+}
+
+_lib = None
+
+
+class ECDError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once and declare every entry point's signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ECDError(
+                f"{LIB_PATH} is not built; run `python -m estudiocanciones_amd.build` "
+                "(the decode path has no fallback)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = c_int
+        handle.ecd_version.argtypes = []
+        handle.ecd_version.restype = ctypes.c_char_p
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, name: str) -> None:
+    if rc == ECD_OK:
+        return
+    if rc == ECD_EINVAL:
+        raise ValueError(f"{name}: invalid argument")
+    if rc == ECD_ENOTSUP:
+        raise NotImplementedError(f"{name}: shape not supported by the gfx950 kernels")
+    raise ECDError(f"{name}: HIP launch failed (hipError_t {rc})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

@@ -1,0 +1,80 @@
+// Shared types and helpers for the gfx950 decode-path kernels.
+//
+// Every kernel in this library is launched on a caller-supplied hipStream_t,
+// allocates nothing and never synchronises, so a whole frame of launches can be
+// captured into one hipGraph by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ecdecode.h"
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define ECD_WAVE 64
+
+// Status codes (ECD_OK, ECD_EINVAL, ECD_ENOTSUP) come from ecdecode.h; positive values are
+// hipError_t codes from a launch.
+
+namespace ecd {
+
+__device__ __forceinline__ float h2f(f16 h) { return (float)h; }
+__device__ __forceinline__ f16 f2h(float f) { return (f16)f; }  // v_cvt_f16_f32: round to nearest even
+
+// Four signed int8 codes packed in one dword -> two f16x2 holding the exact
+// integer values.  u = q ^ 0x80 is q + 128 as an unsigned byte; placing it under
+// the exponent byte 0x64 gives the half 1024 + u, and subtracting 1152 leaves q.
+// Every step is exact (|q| <= 128 < 1024).
+__device__ __forceinline__ void i8x4_to_f16(uint32_t v, f16x2& lo, f16x2& hi) {
+  const uint32_t u = v ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0,u1
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2,u3
+  const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+  lo = __builtin_bit_cast(f16x2, a) - bias;
+  hi = __builtin_bit_cast(f16x2, b) - bias;
+}
+
+// 16 int8 codes (one 16-byte load) -> two f16x8 (codes 0..7 and 8..15).
+__device__ __forceinline__ void i8x16_to_f16(const u32x4& v, f16x8& lo, f16x8& hi) {
+  f16x2 a0, a1, b0, b1, c0, c1, d0, d1;
+  i8x4_to_f16(v.x, a0, a1);
+  i8x4_to_f16(v.y, b0, b1);
+  i8x4_to_f16(v.z, c0, c1);
+  i8x4_to_f16(v.w, d0, d1);
+  lo = (f16x8){a0.x, a0.y, a1.x, a1.y, b0.x, b0.y, b1.x, b1.y};
+  hi = (f16x8){c0.x, c0.y, c1.x, c1.y, d0.x, d0.y, d1.x, d1.y};
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __host__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+}  // namespace ecd
+
+// Launch-error plumbing shared by the entry points.
+static inline int ecd_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ECD_OK : (int)e;
+}

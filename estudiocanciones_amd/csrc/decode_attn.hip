@@ -1,0 +1,299 @@
+// GQA flash-decoding attention over the static KV cache, gfx950.
+//
+// Reference semantics (app/kernels.py:111-167): row r (batch b = r / S) attends to cache
+// slots [0, pos[r]] of kv head kh with its G = Hq / Hk query heads; scores are
+// fp32( q . k ) * scale, softmax with natural exp and a running max, the probabilities
+// are rounded to fp16 before the P.V product (fp32 accumulation), the running sum uses
+// the unrounded fp32 probabilities.  The attended range is cut into `nsplit` chunks of
+// ceil(ceil(len / nsplit) / 16) * 16 tokens; each split writes (m, l, acc) partials that
+// the combine kernel merges with a log-sum-exp rescale (empty splits have m = -inf).
+//
+// Kernel shape: one wave per (split, kv head, row).  Each 16-token tile is
+//   S^T = K_tile . Q^T   on v_mfma_f32_16x16x32_f16: the K rows are the A operand (lane l
+//                        loads 16 contiguous bytes of token t0 + (l & 15)), Q^T the B operand
+//                        (query head g = l & 15, zero for g >= G), so lane l ends holding
+//                        scores of tokens t0 + 4 (l >> 4) + r, r = 0..3, for head l & 15;
+//   P.V on the VALU:     lane l owns the d-chunk 8 (l & 15) .. +8 (plus 128-wide repeats)
+//                        and the token phase l >> 4; the probabilities it needs live in
+//                        the same 16-lane row and arrive through lane shuffles.
+// Each K and V byte of the attended range is read once per (row, kv head): the G query
+// heads of a group share it (no repeat_kv copy).
+#include "common.h"
+
+namespace ecd {
+
+template <int HD, int G>
+__global__ __launch_bounds__(64) void decode_attn_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+    const int64_t* __restrict__ pos, f16* __restrict__ o, float* __restrict__ pm,
+    float* __restrict__ pl, float* __restrict__ pa, int S, int Hq, int Hk, int L, float scale,
+    int nsplit) {
+  static_assert(HD % 32 == 0 && HD <= 512, "head_dim must be a multiple of 32");
+  static_assert(G >= 1 && G <= 16, "query heads per kv head must be 1..16");
+  constexpr int NKC = HD / 32;
+  constexpr int NDP = (HD + 127) / 128;
+
+  const int lane = threadIdx.x;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+  const int b = r / S;
+  const long praw = pos[r];
+  const int ln = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));
+  const int per = (ln + nsplit - 1) / nsplit;
+  const int chunk = ((per + 15) / 16) * 16;
+  const int lo = sp * chunk;
+  const int hi = min(ln, lo + chunk);
+
+  const long cbase = ((long)b * Hk + kh) * (long)L * HD;
+  const f16* kb = kc + cbase;
+  const f16* vb = vc + cbase;
+
+  f16x8 qf[NKC];
+  {
+    const bool gv = row < G;
+    const f16* qp = q + ((long)r * Hq + kh * G + (gv ? row : 0)) * HD + 8 * grp;
+#pragma unroll
+    for (int i = 0; i < NKC; ++i) {
+      if (gv)
+        qf[i] = *(const f16x8*)(qp + 32 * i);
+      else
+        qf[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  float acc[G][NDP][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][j][e] = 0.f;
+
+  for (int t0 = lo; t0 < hi; t0 += 16) {
+    f16x8 kf[NKC];
+    {
+      const int tk = min(t0 + row, hi - 1);
+      const f16* kp = kb + (long)tk * HD + 8 * grp;
+#pragma unroll
+      for (int i = 0; i < NKC; ++i) kf[i] = *(const f16x8*)(kp + 32 * i);
+    }
+    f16x8 vv[4][NDP];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int t = t0 + 4 * grp + rr;
+      const int tv = min(t, hi - 1);
+      const f16* vp = vb + (long)tv * HD + 8 * row;
+#pragma unroll
+      for (int j = 0; j < NDP; ++j) {
+        if (8 * (row + 16 * j) < HD && t < hi)
+          vv[rr][j] = *(const f16x8*)(vp + 128 * j);
+        else
+          vv[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+
+    f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[i], qf[i], st, 0, 0, 0);
+
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int t = t0 + 4 * grp + rr;
+      sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
+      mx = fmaxf(mx, sc[rr]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __expf(m_run - m_new);
+    float pr[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pr[rr] = __expf(sc[rr] - m_new);
+      ps += pr[rr];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int src = 16 * grp + g;
+      const float ag = __shfl(alpha, src, 64);
+      float pg[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) pg[rr] = (float)(f16)__shfl(pr[rr], src, 64);
+#pragma unroll
+      for (int j = 0; j < NDP; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float a = acc[g][j][e] * ag;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)vv[rr][j][e];
+          acc[g][j][e] = a;
+        }
+    }
+  }
+
+  // merge the four token phases (lane groups) of every d-chunk
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = acc[g][j][e];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        acc[g][j][e] = a;
+      }
+
+  const long hbase = (long)r * Hq + kh * G;
+  if (nsplit == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float lg = __shfl(l_run, g, 64);
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < NDP; ++j) {
+          const int d = 8 * (row + 16 * j);
+          if (d < HD) {
+            f16x8 ov;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ov[e] = (f16)(acc[g][j][e] / lg);
+            *(f16x8*)(o + (hbase + g) * HD + d) = ov;
+          }
+        }
+      }
+    }
+  } else {
+    if (lane < G) {
+      const long pidx = (hbase + lane) * nsplit + sp;
+      pm[pidx] = m_run;
+      pl[pidx] = l_run;
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const long pidx = (hbase + g) * nsplit + sp;
+#pragma unroll
+        for (int j = 0; j < NDP; ++j) {
+          const int d = 8 * (row + 16 * j);
+          if (d < HD) {
+            float* dst = pa + pidx * HD + d;
+            *(f32x4*)dst = (f32x4){acc[g][j][0], acc[g][j][1], acc[g][j][2], acc[g][j][3]};
+            *(f32x4*)(dst + 4) = (f32x4){acc[g][j][4], acc[g][j][5], acc[g][j][6], acc[g][j][7]};
+          }
+        }
+      }
+    }
+  }
+}
+
+// o[rh, d] = sum_s w_s pa[rh, s, d] / sum_s w_s pl[rh, s],  w_s = exp(pm[rh, s] - max_s pm)
+// with w_s = 0 for empty splits (app/kernels.py:156-167).
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ pm,
+                                                           const float* __restrict__ pl,
+                                                           const float* __restrict__ pa,
+                                                           f16* __restrict__ o, int HD,
+                                                           int nsplit) {
+  const long rh = blockIdx.x;
+  const float* mrow = pm + rh * nsplit;
+  const float* lrow = pl + rh * nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, mrow[s]);
+  float den = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float m = mrow[s];
+    const float w = m > -INFINITY ? __expf(m - M) : 0.f;
+    den += lrow[s] * w;
+  }
+  for (int d = threadIdx.x; d < HD; d += 128) {
+    float a = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float m = mrow[s];
+      const float w = m > -INFINITY ? __expf(m - M) : 0.f;
+      a += pa[(rh * nsplit + s) * HD + d] * w;
+    }
+    o[rh * HD + d] = (f16)(a / den);
+  }
+}
+
+template <int HD>
+static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* kc,
+                     const f16* vc, const int64_t* pos, f16* o, float* pm, float* pl, float* pa,
+                     int S, int Hq, int Hk, int L, float scale, int nsplit) {
+#define ECD_ATTN_G(G_)                                                                    \
+  case G_:                                                                                \
+    hipLaunchKernelGGL((decode_attn_kernel<HD, G_>), grid, dim3(64), 0, st, q, kc, vc, pos, o, \
+                       pm, pl, pa, S, Hq, Hk, L, scale, nsplit);                          \
+    return ECD_OK;
+  switch (G) {
+    ECD_ATTN_G(1)
+    ECD_ATTN_G(2)
+    ECD_ATTN_G(3)
+    ECD_ATTN_G(4)
+    ECD_ATTN_G(6)
+    ECD_ATTN_G(8)
+    default:
+      return ECD_ENOTSUP;
+  }
+#undef ECD_ATTN_G
+}
+
+}  // namespace ecd
+
+using namespace ecd;
+
+extern "C" {
+
+int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t* pos, void* o,
+                    float* pm, float* pl, float* pa, int R, int S, int Hq, int Hk, int L, int HD,
+                    int nsplit, float scale, void* stream) {
+  if (!q || !kc || !vc || !pos || R <= 0 || S <= 0 || Hq <= 0 || Hk <= 0 || L <= 0 || HD <= 0 ||
+      nsplit <= 0 || (Hq % Hk) != 0)
+    return ECD_EINVAL;
+  if (nsplit == 1 && !o) return ECD_EINVAL;
+  if (nsplit > 1 && (!pm || !pl || !pa)) return ECD_EINVAL;
+  const int G = Hq / Hk;
+  dim3 grid(nsplit, Hk, R);
+  hipStream_t st = (hipStream_t)stream;
+  const f16 *qh = (const f16*)q, *kh = (const f16*)kc, *vh = (const f16*)vc;
+  f16* oh = (f16*)o;
+  int rc;
+  switch (HD) {
+    case 64:
+      rc = launch_hd<64>(G, grid, st, qh, kh, vh, pos, oh, pm, pl, pa, S, Hq, Hk, L, scale, nsplit);
+      break;
+    case 128:
+      rc = launch_hd<128>(G, grid, st, qh, kh, vh, pos, oh, pm, pl, pa, S, Hq, Hk, L, scale, nsplit);
+      break;
+    case 256:
+      rc = launch_hd<256>(G, grid, st, qh, kh, vh, pos, oh, pm, pl, pa, S, Hq, Hk, L, scale, nsplit);
+      break;
+    case 384:
+      rc = launch_hd<384>(G, grid, st, qh, kh, vh, pos, oh, pm, pl, pa, S, Hq, Hk, L, scale, nsplit);
+      break;
+    default:
+      rc = ECD_ENOTSUP;
+  }
+  if (rc != ECD_OK) return rc;
+  return ecd_launch_status();
+}
+
+int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,
+                     int nsplit, void* stream) {
+  if (!pm || !pl || !pa || !o || RH <= 0 || HD <= 0 || nsplit <= 0) return ECD_EINVAL;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(RH), dim3(128), 0, (hipStream_t)stream, pm, pl, pa,
+                     (f16*)o, HD, nsplit);
+  return ecd_launch_status();
+}
+
+}  // extern "C"

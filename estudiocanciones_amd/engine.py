@@ -1,0 +1,440 @@
+"""HeartMuLa decode engine on gfx950: int8 weights, static KV cache, HIP kernels, hipGraphs.
+
+Mirrors the fast path of the reference engine (app/engine.py) with the same classes,
+method names and tensor layouts -- ``Linear``, ``fuse``, ``Emb``, ``Block``, ``Stack``
+(``alloc``/``free``/``__call__``/``decode``) and ``HeartMuLaLite`` (``_sample``,
+``_guided``, ``_embed_audio``, ``_frame_fast``, ``_step``, ``generate``, ``_capture``,
+``release``) -- but every op of the per-frame step is a hand-written HIP kernel reached
+through the C ABI of ``libecdecode.so`` (see ``kernels.py``); sampling stays on PyTorch GPU
+ops exactly as in the reference.  Differences from the reference, all deliberate:
+
+* stacks are shape-parametric (``dim`` per stack) instead of the global ``DIM = 3072``
+  (app/engine.py:19, :116, :161), so a 1024-wide decoder can be expressed;
+* the prompt pass (``Stack.__call__``) runs through the same decode kernels with one row
+  per prompt position (row r attends [0, pos[r]] == causal attention), instead of SDPA with
+  ``repeat_interleave``; ``int8_mm`` keeps the reference's dense numerics for M > 16 rows;
+* the prompt arrives as token ids (tokenisation is host string work, out of scope);
+* the text-embedding table lives on the GPU (one gather per song);
+* decode attention over caches of at most 128 slots uses one split (direct output,
+  no combine pass); longer caches use the reference's 16 splits.
+"""
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import torch
+
+from . import _ffi
+from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, int8_mm,
+                      next_power_of_2, rms as krms, stream_ptr)
+
+AUDIO_VOCAB = 8197
+N_CB = 8
+MUQ_DIM = 512
+DIM = 3072
+TEXT_BOS, TEXT_EOS, AUDIO_EOS, EMPTY_ID = 128000, 128001, 8193, 0
+FRAME_MS = 80
+
+BACKBONE = dict(layers=28, heads=24, kv_heads=8, max_seq=8192, dim=DIM)
+# the reference's depth decoder (app/engine.py:24; head_dim = 3072 // 8 = 384)
+DECODER = dict(layers=3, heads=8, kv_heads=4, max_seq=2048, dim=DIM)
+# the 1024-wide 4-layer decoder shape of the benchmark configuration
+DECODER_1024 = dict(layers=4, heads=8, kv_heads=2, max_seq=2048, dim=1024)
+
+
+# ---------------------------------------------------------------- RoPE (Llama-3 scaled)
+def rope_cache(head_dim: int, max_seq: int, base=500_000, scale=32, low=1, high=4, old=8192,
+               device="cuda"):
+    """[max_seq, head_dim / 2, 2] float32 (cos, sin) built on the GPU (app/engine.py:28-43)."""
+    dev = torch.device(device)
+    out = torch.empty(max_seq, head_dim // 2, 2, device=dev, dtype=torch.float32)
+    _ffi.call("ecd_rope_table", out.data_ptr(), max_seq, head_dim, float(base), float(scale),
+              float(low), float(high), float(old), stream_ptr(dev))
+    return out
+
+
+# ---------------------------------------------------------------- linear layers
+class Linear:
+    """int8 per-output-channel linear layer (app/engine.py:62-79)."""
+
+    def __init__(self, w=None, q8=None, s8=None):
+        if q8 is None:
+            raise NotImplementedError("the gfx950 decode path runs int8 per-channel weights only")
+        self.w, self.q8, self.s8 = None, q8, s8
+
+    def __call__(self, x, res=None):
+        return int8_mm(x, self.q8, self.s8, res)
+
+    @property
+    def nbytes(self):
+        return self.q8.numel() + self.s8.numel() * 2
+
+
+def fuse(parts):
+    """Row-concatenate layers that read the same input (q|k|v, w1|w3), app/engine.py:82-86."""
+    return Linear(q8=torch.cat([p.q8 for p in parts]).contiguous(),
+                  s8=torch.cat([p.s8 for p in parts]).contiguous())
+
+
+class Emb:
+    """int8 per-row embedding table (app/engine.py:89-104)."""
+
+    def __init__(self, w=None, q8=None, s8=None):
+        if q8 is None:
+            raise NotImplementedError("the gfx950 decode path runs int8 embedding tables only")
+        self.w, self.q8, self.s8 = None, q8.contiguous(), s8.contiguous()
+
+    def __call__(self, idx):
+        """fp16(q8[idx]) * s8[idx] -> [*idx.shape, D]."""
+        idx = idx.to(torch.int64).contiguous()
+        D = self.q8.shape[1]
+        out = torch.empty(*idx.shape, D, device=self.q8.device, dtype=torch.float16)
+        n = idx.numel()
+        if n:
+            rows = self.q8.shape[0]
+            _ffi.call("ecd_embed_i8", idx.data_ptr(), 1, self.q8.data_ptr(), self.s8.data_ptr(),
+                      rows, 0, rows, None, out.data_ptr(), n, D, stream_ptr(out.device))
+        return out
+
+    def gather(self, tok, cb, vocab, even=None):
+        """One codebook: rows tok[:, 0] + cb * vocab -> [B, D]; with ``even`` [B, D] the result
+        is the interleave [2B, D] (even rows = even, odd rows = embeddings)."""
+        B = tok.shape[0]
+        D = self.q8.shape[1]
+        out = torch.empty((2 * B if even is not None else B), D, device=self.q8.device,
+                          dtype=torch.float16)
+        _ffi.call("ecd_embed_i8", tok.data_ptr(), tok.stride(0), self.q8.data_ptr(),
+                  self.s8.data_ptr(), self.q8.shape[0], int(cb), int(vocab),
+                  even.data_ptr() if even is not None else None, out.data_ptr(), B, D,
+                  stream_ptr(out.device))
+        return out
+
+    def sum_codebooks(self, tok, vocab):
+        """sum_c Emb(tok[:, c] + c * vocab) accumulated in fp32, one fp16 rounding (:348)."""
+        tok = tok.contiguous()
+        B, C = tok.shape
+        D = self.q8.shape[1]
+        out = torch.empty(B, D, device=self.q8.device, dtype=torch.float16)
+        _ffi.call("ecd_embed_sum_i8", tok.data_ptr(), self.q8.data_ptr(), self.s8.data_ptr(),
+                  self.q8.shape[0], out.data_ptr(), B, C, D, int(vocab), stream_ptr(out.device))
+        return out
+
+    @property
+    def nbytes(self):
+        return self.q8.numel() + self.s8.numel() * 2
+
+
+# ---------------------------------------------------------------- static-cache transformer
+class Block:
+    def __init__(self, p, pre, heads, kv_heads, dim=DIM):
+        self.qkv = fuse([p(pre + f"attn.{n}_proj.weight") for n in ("q", "k", "v")])
+        self.o = p(pre + "attn.output_proj.weight")
+        self.w13 = fuse([p(pre + "mlp.w1.weight"), p(pre + "mlp.w3.weight")])
+        self.w2 = p(pre + "mlp.w2.weight")
+        self.n1, self.n2 = p(pre + "sa_norm.scale", norm=True), p(pre + "mlp_norm.scale", norm=True)
+        self.h, self.kvh = heads, kv_heads
+        self.hd = dim // heads
+        self.kc = self.vc = None
+
+    def alloc(self, B, L, dev, dtype):
+        self.kc = torch.zeros(B, self.kvh, L, self.hd, device=dev, dtype=dtype)
+        self.vc = torch.zeros_like(self.kc)
+
+
+class Stack:
+    def __init__(self, p, prefix, cfg):
+        dim = cfg.get("dim", DIM)
+        self.blocks = [Block(p, f"{prefix}.layers.{i}.", cfg["heads"], cfg["kv_heads"], dim)
+                       for i in range(cfg["layers"])]
+        self.norm = p(f"{prefix}.norm.scale", norm=True)
+        self.rope = None
+        self.dim = dim
+        self.hd = dim // cfg["heads"]
+        self.max_seq = cfg["max_seq"]
+        self.nsplit = 16
+
+    def alloc(self, B, L, dev, dtype):
+        self.rope = rope_cache(self.hd, max(L, 16), device=dev)
+        self.nsplit = 1 if L <= 128 else 16
+        for b in self.blocks:
+            b.alloc(B, L, dev, dtype)
+
+    def free(self):
+        for b in self.blocks:
+            b.kc = b.vc = None
+
+    def __call__(self, x, pos, attn_len=None, mask=None):
+        """Prompt pass (app/engine.py:174-178): x [B, S, D], pos [B, S] absolute positions
+        (causal).  Runs the decode kernels with one row per position; row (b, s) attends
+        [0, pos[b, s]], which is the causal mask of the reference's SDPA call."""
+        if mask is not None:
+            raise NotImplementedError("explicit attention masks are not part of the fast path")
+        B, S, D = x.shape
+        h = self.decode(x.reshape(B * S, D), pos.reshape(B * S).to(torch.int64).contiguous(), S)
+        return h.reshape(B, S, D)
+
+    def decode(self, x, pos, S):
+        """Fast path for few rows (app/engine.py:180-211): x [R, D] with R = B*S (row r -> batch
+        r // S), pos [R] absolute positions; row r attends [0, pos[r]]."""
+        R = x.shape[0]
+        ns = self.nsplit
+        for b in self.blocks:
+            Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
+            qkv = b.qkv(krms(x, b.n1))
+            q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
+            _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
+                                      HD=HD, HALF=next_power_of_2(HD // 2))
+            o = torch.empty_like(q)
+            HDP = next_power_of_2(HD)
+            if ns > 1:
+                pm = torch.empty(R * Hq * ns, device=x.device)
+                pl = torch.empty_like(pm)
+                pa = torch.empty(R * Hq * ns, HD, device=x.device)
+            else:
+                pm = pl = pa = o
+            _attn[(R, Hk, ns)](q, b.kc, b.vc, pos, o, pm, pl, pa, S, Hq, Hk, L, 1.0 / math.sqrt(HD),
+                               HD=HD, HDP=HDP, G=Hq // Hk, BLK=64 if HD <= 128 else 16, NSPLIT=ns,
+                               num_warps=4)
+            if ns > 1:
+                _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, HDP=HDP, NSPLIT=ns)
+            x = b.o(o, res=x)
+            a = b.w13(krms(x, b.n2))
+            Fd = a.shape[1] // 2
+            mm = torch.empty(R, Fd, device=x.device, dtype=x.dtype)
+            _silu_mul[(R, cdiv(Fd, 1024))](a, mm, Fd, BLOCK=1024)
+            x = b.w2(mm, res=x)
+        return krms(x, self.norm)
+
+
+# ---------------------------------------------------------------- weights
+class _TensorSource:
+    """Name -> tensor access over a safetensors file or an in-memory dict."""
+
+    def __init__(self, weights, dev):
+        self.meta = {}
+        if isinstance(weights, (str, Path)):
+            from safetensors import safe_open
+            self._f = safe_open(str(weights), "pt", device=str(dev))
+            self._keys = set(self._f.keys())
+            self.meta = json.loads((self._f.metadata() or {}).get("lite", "{}"))
+            self._get = self._f.get_tensor
+        else:
+            self._keys = set(weights.keys())
+            self._get = lambda k: weights[k].to(dev)
+
+    def __contains__(self, k):
+        return k in self._keys
+
+    def get(self, k):
+        return self._get(k)
+
+
+# ---------------------------------------------------------------- model
+class HeartMuLaLite:
+    """Backbone + depth decoder of HeartMuLa on the gfx950 decode kernels (app/engine.py:215-477).
+
+    ``weights`` is a ``mula_int8.safetensors``-format file or a dict of tensors with the same
+    names (``<name>.q8`` int8, ``<name>.s8`` bf16, norm ``.scale`` bf16)."""
+
+    def __init__(self, weights, device="cuda", dtype=None, backbone=BACKBONE, decoder=DECODER):
+        self.dev = torch.device(device)
+        if self.dev.type != "cuda":
+            raise RuntimeError("HeartMuLaLite (gfx950 path) needs a ROCm GPU device")
+        if dtype is None:
+            dtype = torch.float16
+        if dtype != torch.float16:
+            raise TypeError("the gfx950 decode kernels compute in float16 (app/engine.py:219-222)")
+        self.dt = dtype
+        self.fast = True
+        f = _TensorSource(weights, self.dev)
+        self.meta = f.meta
+
+        def p(name, norm=False):
+            if name in f:
+                t = f.get(name).to(dtype)
+                return t if norm else Linear(w=t)
+            q8, s8 = f.get(name + ".q8"), f.get(name + ".s8")
+            return Linear(q8=q8.contiguous(), s8=s8.to(dtype).contiguous())
+
+        def emb(name):
+            if name in f:
+                return Emb(w=f.get(name).to(dtype))
+            return Emb(q8=f.get(name + ".q8"), s8=f.get(name + ".s8").to(dtype))
+
+        self.bb_cfg, self.dec_cfg = dict(backbone), dict(decoder)
+        self.backbone = Stack(p, "backbone", backbone)
+        self.decoder = Stack(p, "decoder", decoder)
+        self.text_emb = emb("text_embeddings.weight")
+        self.audio_emb = emb("audio_embeddings.weight")
+        self.uncond = f.get("unconditional_text_embedding.weight").to(dtype)
+        self.projection = p("projection.weight")
+        self.c0_head = p("codebook0_head.weight")
+        self.audio_head = [p(f"audio_head.{i}") for i in range(N_CB - 1)]
+        self.muq_b = f.get("muq_linear.bias").to(dtype)
+        self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
+        self.graphs = {}
+        self.N = self.B = None
+
+    # -------------------------------------------------- sampling (as in the reference)
+    @staticmethod
+    def _sample(logits, topk, temp, noise=None):
+        """app/engine.py:291-298; ``noise`` replaces the Exponential(1) draws (tests)."""
+        logits = logits / temp
+        thr = torch.topk(logits, topk)[0][..., -1, None]
+        logits = logits.masked_fill(logits < thr, -float("inf"))
+        probs = torch.softmax(torch.log_softmax(logits, -1), -1)
+        qe = torch.empty_like(probs).exponential_(1) if noise is None else noise
+        return torch.argmax(probs / qe, -1, keepdim=True)
+
+    def _guided(self, logits, cfg, topk, temp, noise=None):
+        N = self.N
+        if self.B == 2 * N:
+            logits = logits[N:] + (logits[:N] - logits[N:]) * cfg
+        s = self._sample(logits.float(), topk, temp, noise)
+        return torch.cat([s, s], 0) if self.B == 2 * N else s
+
+    def _embed_audio(self, cb, tok):
+        """Embedding of codebook ``cb`` for tokens tok [B, 1] -> [B, D] (app/engine.py:307-308)."""
+        return self.audio_emb.gather(tok, cb, AUDIO_VOCAB)
+
+    # -------------------------------------------------- one frame (backbone + 7 decoder passes)
+    def _frame_fast(self, last_h, cfg, topk, temp, forced=None, logits_out=None, noise=None):
+        """app/engine.py:328-343.  ``forced`` [B, 8] replaces the samples (teacher forcing),
+        ``logits_out`` collects the 8 logit tensors, ``noise`` [8, N, V] fixes the draws."""
+        B = self.B
+        if getattr(self, "_dpos", None) is None or self._dpos[0].shape[0] != 2 * B:
+            self._dpos = [torch.arange(2, device=self.dev).repeat(B)] + [
+                torch.full((B,), i + 1, dtype=torch.long, device=self.dev) for i in range(1, N_CB - 1)]
+
+        def pick(i, lg):
+            if logits_out is not None:
+                logits_out.append(lg)
+            if forced is not None:
+                return forced[:, i:i + 1]
+            return self._guided(lg, cfg, topk, temp, None if noise is None else noise[i])
+
+        c0 = pick(0, self.c0_head(last_h))
+        samples = [c0]
+        # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
+        x = self.audio_emb.gather(c0, 0, AUDIO_VOCAB, even=last_h)
+        h = self.decoder.decode(self.projection(x), self._dpos[0], 2)[1::2]
+        for i in range(1, N_CB):
+            ci = pick(i, self.audio_head[i - 1](h))
+            samples.append(ci)
+            if i < N_CB - 1:
+                h = self.decoder.decode(self.projection(self._embed_audio(i, ci)), self._dpos[i], 1)
+        return torch.cat(samples, 1)
+
+    def _step(self, tok, pos, bucket, cfg, topk, temp, **kw):
+        """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349)."""
+        h = self.audio_emb.sum_codebooks(tok, AUDIO_VOCAB)
+        return self._frame_fast(self.backbone.decode(h, pos[:, 0].contiguous(), 1), cfg, topk, temp, **kw)
+
+    # -------------------------------------------------- caches
+    def alloc(self, n, L, cfg_scale=1.5):
+        """Static caches for n takes and backbone capacity L (app/engine.py:380-388)."""
+        self.N = n
+        self.B = 2 * n if cfg_scale != 1.0 else n
+        self.backbone.alloc(self.B, L, self.dev, self.dt)
+        self.decoder.alloc(self.B, N_CB, self.dev, self.dt)
+
+    # -------------------------------------------------- generation
+    @torch.inference_mode()
+    def generate(self, text, muq_idx, *, max_ms=60_000, temperature=1.0, topk=50, cfg_scale=1.5,
+                 seed=None, use_graphs=True, progress=None, abort=None, n=1):
+        """app/engine.py:374-448 with the prompt given as token ids ``text`` [P] (int64) and the
+        muq slot index.  Returns [8, T] if n == 1, else a list of n such tensors."""
+        if seed is not None and seed >= 0:
+            torch.manual_seed(seed)
+        text = torch.as_tensor(text, dtype=torch.int64)
+        P = int(text.numel())
+        n_frames = max_ms // FRAME_MS
+        L = P + n_frames + 2
+        self.alloc(n, L + 256, cfg_scale)
+        N, B = self.N, self.B
+        te = self.text_emb(text.to(self.dev))                                  # [P, D]
+        h = te.unsqueeze(0).repeat(B, 1, 1)
+        h[:N, muq_idx] = self.muq_b
+        if B == 2 * N:
+            h[N:] = self.uncond[0]
+        pos = torch.arange(P, device=self.dev).unsqueeze(0).expand(B, P)
+        hb = self.backbone(h, pos, P, None)
+        tok = self._frame_fast(hb[:, -1].contiguous(), cfg_scale, topk, temperature)
+
+        out = torch.empty(n_frames + 1, N, N_CB, dtype=torch.long, device=self.dev)
+        out[0] = tok[:N]
+        cur_pos = P
+        ends = [None] * N
+        static = None
+        CHECK = 25
+        last = n_frames
+        bucket = L + 256
+        for i in range(n_frames):
+            if abort and abort():
+                self.release()
+                return None
+            if use_graphs:
+                key = (B, bucket, topk, float(temperature), float(cfg_scale))
+                if static is None:
+                    static = dict(tok=tok.clone(), pos=torch.zeros(B, 1, dtype=torch.long, device=self.dev))
+                static["tok"].copy_(tok)
+                static["pos"].fill_(cur_pos)
+                g = self.graphs.get(key)
+                if g is None:
+                    g = self._capture(static, bucket, cfg_scale, topk, temperature)
+                    self.graphs[key] = g
+                g[0].replay()
+                tok = g[1]
+            else:
+                p_t = torch.full((B, 1), cur_pos, dtype=torch.long, device=self.dev)
+                tok = self._step(tok, p_t, bucket, cfg_scale, topk, temperature)
+            out[i + 1] = tok[:N]
+            cur_pos += 1
+            if (i + 1) % CHECK == 0 or i == n_frames - 1:
+                a = max(1, i + 2 - CHECK)
+                eos = (out[a: i + 2] >= AUDIO_EOS).any(-1).cpu()
+                for c in range(N):
+                    if ends[c] is None and eos[:, c].any():
+                        ends[c] = a + int(eos[:, c].nonzero()[0, 0])
+                if all(e is not None for e in ends):
+                    last = i + 1
+                    break
+                if progress:
+                    progress((i + 1) * FRAME_MS / 1000, max_ms / 1000)
+        res = []
+        for c in range(N):
+            T = ends[c] if ends[c] is not None else last + 1
+            res.append(out[:T, c].t().clone())
+        self.release()
+        return res[0] if n == 1 else res
+
+    def _capture(self, static, bucket, cfg, topk, temp):
+        """One eager warm-up then capture of ``_step`` into a hipGraph (app/engine.py:450-461)."""
+        s = torch.cuda.Stream(device=self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            self._step(static["tok"], static["pos"], bucket, cfg, topk, temp)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=getattr(self, "_pool", None)):
+            out = self._step(static["tok"], static["pos"], bucket, cfg, topk, temp)
+        self._pool = g.pool()
+        return g, out
+
+    def release(self):
+        self.graphs.clear()
+        self._pool = None
+        self.backbone.free()
+        self.decoder.free()
+        torch.cuda.empty_cache()
+
+    def vram_weights(self):
+        tot = 0
+        for st in (self.backbone, self.decoder):
+            for b in st.blocks:
+                tot += sum(l.nbytes for l in (b.qkv, b.o, b.w13, b.w2))
+        tot += self.audio_emb.nbytes + sum(l.nbytes for l in self.audio_head)
+        tot += self.c0_head.nbytes + self.projection.nbytes
+        return tot

@@ -1,0 +1,228 @@
+"""Decode-path kernels with the entry points of the reference's ``app/kernels.py``.
+
+Same names, argument order and tensor layouts as the reference, so an engine written
+against it runs unchanged:
+
+    int8_mm(x, w, s, res=None)                                   app/kernels.py:40-54
+    rms(x, w, eps=1e-5)                                          app/kernels.py:70-74
+    _rope_cache[grid](qkv, rope, pos, q, kc, vc, S, Hq, Hk, L, HD=, HALF=)    :78-107
+    _attn[grid](q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale,
+                HD=, HDP=, G=, BLK=, NSPLIT=, num_warps=)                     :111-153
+    _attn_combine[grid](pm, pl, pa, o, HD=, HDP=, NSPLIT=)                    :156-167
+    _silu_mul[grid](x, y, F_, BLOCK=)                                         :171-180
+
+Every call goes to a hand-written gfx950 HIP kernel through the C ABI of
+``libecdecode.so``, on the current HIP stream, so it can be captured in a hipGraph.
+The Triton tiling knobs (HALF, HDP, BLK, BLOCK, num_warps) are accepted for drop-in
+compatibility and checked for consistency, but the HIP kernels choose their own tiling;
+the grid must be the one the reference launches with.  Tensors must be fp16 (the
+reference GPU default, app/engine.py:219-222) and live on a ROCm device.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _ffi
+
+__all__ = ["int8_mm", "rms", "_rope_cache", "_attn", "_attn_combine", "_silu_mul",
+           "next_power_of_2", "cdiv", "stream_ptr"]
+
+
+def next_power_of_2(n: int) -> int:
+    """Host helper the reference engine takes from Triton (app/engine.py:192,194)."""
+    n = int(n)
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+def cdiv(a: int, b: int) -> int:
+    return -(-int(a) // int(b))
+
+
+def stream_ptr(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str) -> torch.device:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name}: the decode path runs only on a ROCm GPU tensor (got {t.device})")
+    return t.device
+
+
+def _f16(t: torch.Tensor, name: str) -> None:
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name}: expected float16, got {t.dtype}")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------- GEMV int8 (+ optional residual)
+def int8_mm(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, res: torch.Tensor | None = None):
+    """x [..., K] fp16, w [N, K] int8, s [N] fp16 -> [..., N] (+ res).
+
+    M = prod(x.shape[:-1]) <= 16 uses the reference GEMV numerics (scale after the fp32
+    dot product); M > 16 uses its dequantise-then-GEMM numerics (app/kernels.py:46-49)."""
+    dev = _dev(x, "int8_mm")
+    _f16(x, "int8_mm x")
+    if w.dtype != torch.int8 or w.dim() != 2 or not w.is_contiguous():
+        raise TypeError("int8_mm: w must be a contiguous [N, K] int8 tensor")
+    if s.dtype != torch.float16 or s.numel() != w.shape[0] or not s.is_contiguous():
+        raise TypeError("int8_mm: s must be a contiguous [N] float16 tensor")
+    shp = x.shape
+    K = shp[-1]
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"int8_mm: x has K={K}, w has K={w.shape[1]}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) < K:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    y = torch.empty(M, N, device=dev, dtype=torch.float16)
+    r2 = None
+    if res is not None:
+        _f16(res, "int8_mm res")
+        r2 = res.reshape(M, N)
+        if r2.stride(-1) != 1 or r2.stride(0) < N:
+            r2 = r2.contiguous()
+    if M == 0:
+        return y.reshape(*shp[:-1], N)
+    _ffi.call("ecd_gemv_i8", x2.data_ptr(), x2.stride(0), w.data_ptr(), s.data_ptr(), _ptr(r2),
+              r2.stride(0) if r2 is not None else 0, y.data_ptr(), N, M, N, K, int(M > 16),
+              stream_ptr(dev))
+    return y.reshape(*shp[:-1], N)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rms(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5):
+    """x [R, D] fp16, w [D] fp16 -> fp16(fp16(x * rsqrt(mean(x^2) + eps)) * w)."""
+    dev = _dev(x, "rms")
+    _f16(x, "rms x")
+    _f16(w, "rms w")
+    R, D = x.shape
+    if w.numel() != D:
+        raise ValueError("rms: weight size mismatch")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    y = torch.empty(R, D, device=dev, dtype=torch.float16)
+    _ffi.call("ecd_rmsnorm", x.data_ptr(), x.stride(0), w.data_ptr(), y.data_ptr(), D, R, D,
+              float(eps), stream_ptr(dev))
+    return y
+
+
+class _Launcher:
+    """``kernel[grid](...)`` call syntax of the reference's Triton launchers."""
+
+    def __init__(self, name, fn, grid_fn):
+        self.__name__ = name
+        self._fn = fn
+        self._grid_fn = grid_fn
+
+    def __getitem__(self, grid):
+        grid = tuple(grid) if isinstance(grid, (tuple, list)) else (grid,)
+
+        def launch(*args, **kwargs):
+            want = self._grid_fn(*args, **kwargs)
+            if tuple(grid) != tuple(want):
+                raise ValueError(f"{self.__name__}: grid {grid} does not match the launch {want}")
+            return self._fn(*args, **kwargs)
+
+        return launch
+
+    def __call__(self, *args, **kwargs):  # direct call without a grid
+        return self._fn(*args, **kwargs)
+
+
+# ---------------------------------------------------------------- RoPE + KV-cache write
+def _rope_cache_impl(qkv, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, HALF=None):
+    dev = _dev(qkv, "_rope_cache")
+    for t, n in ((qkv, "qkv"), (q, "q"), (kc, "kc"), (vc, "vc")):
+        _f16(t, f"_rope_cache {n}")
+        if not t.is_contiguous():
+            raise ValueError(f"_rope_cache: {n} must be contiguous")
+    if rope.dtype != torch.float32 or not rope.is_contiguous():
+        raise TypeError("_rope_cache: rope table must be contiguous float32 [L, HD/2, 2]")
+    if pos.dtype != torch.int64 or not pos.is_contiguous():
+        raise TypeError("_rope_cache: pos must be contiguous int64")
+    if HALF is not None and HALF < HD // 2:
+        raise ValueError("_rope_cache: HALF must cover HD // 2")
+    R = qkv.shape[0]
+    if qkv.shape[1] != (Hq + 2 * Hk) * HD or q.numel() != R * Hq * HD or pos.numel() != R:
+        raise ValueError("_rope_cache: shape mismatch")
+    if kc.shape[-1] != HD or kc.shape[-2] != L or kc.shape[1] != Hk or kc.shape[0] * S < R:
+        raise ValueError("_rope_cache: cache must be [B, Hk, L, HD] with B >= R / S")
+    if rope.shape[0] < L or rope.shape[1] != HD // 2:
+        raise ValueError("_rope_cache: rope table must have >= L rows of HD/2 pairs")
+    _ffi.call("ecd_rope_kv_write", qkv.data_ptr(), rope.data_ptr(), pos.data_ptr(), q.data_ptr(),
+              kc.data_ptr(), vc.data_ptr(), R, S, Hq, Hk, L, HD, stream_ptr(dev))
+
+
+_rope_cache = _Launcher("_rope_cache", _rope_cache_impl,
+                        lambda qkv, rope, pos, q, kc, vc, S, Hq, Hk, L, HD=None, HALF=None:
+                        (qkv.shape[0], Hq + Hk))
+
+
+# ---------------------------------------------------------------- decode attention
+def _attn_impl(q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale, HD, HDP=None, G=None,
+               BLK=None, NSPLIT=16, num_warps=None):
+    dev = _dev(q, "_attn")
+    for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (o, "o")):
+        _f16(t, f"_attn {n}")
+        if not t.is_contiguous():
+            raise ValueError(f"_attn: {n} must be contiguous")
+    if pos.dtype != torch.int64 or not pos.is_contiguous():
+        raise TypeError("_attn: pos must be contiguous int64")
+    if G is not None and G != Hq // Hk:
+        raise ValueError("_attn: G must equal Hq // Hk")
+    R = q.shape[0]
+    if q.numel() != R * Hq * HD or pos.numel() != R or o.numel() != R * Hq * HD:
+        raise ValueError("_attn: shape mismatch")
+    if kc.shape[-1] != HD or kc.shape[-2] != L or kc.shape[1] != Hk or kc.shape[0] * S < R:
+        raise ValueError("_attn: cache must be [B, Hk, L, HD] with B >= R / S")
+    if NSPLIT > 1:
+        need = R * Hq * NSPLIT
+        for t, n, k in ((pm, "pm", need), (pl, "pl", need), (pa, "pa", need * HD)):
+            if t.dtype != torch.float32 or t.numel() < k or not t.is_contiguous():
+                raise ValueError(f"_attn: {n} must be float32 with >= {k} elements")
+        ptrs = (pm.data_ptr(), pl.data_ptr(), pa.data_ptr())
+    else:
+        ptrs = (None, None, None)
+    _ffi.call("ecd_decode_attn", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(),
+              o.data_ptr(), *ptrs, R, S, Hq, Hk, L, HD, int(NSPLIT), float(scale), stream_ptr(dev))
+
+
+_attn = _Launcher("_attn", _attn_impl,
+                  lambda q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale, HD=None, HDP=None,
+                  G=None, BLK=None, NSPLIT=16, num_warps=None: (q.shape[0], Hk, NSPLIT))
+
+
+def _attn_combine_impl(pm, pl, pa, o, HD, HDP=None, NSPLIT=16):
+    dev = _dev(o, "_attn_combine")
+    _f16(o, "_attn_combine o")
+    RH = o.numel() // HD
+    for t, n, k in ((pm, "pm", RH * NSPLIT), (pl, "pl", RH * NSPLIT), (pa, "pa", RH * NSPLIT * HD)):
+        if t.dtype != torch.float32 or t.numel() < k or not t.is_contiguous():
+            raise ValueError(f"_attn_combine: {n} must be float32 with >= {k} elements")
+    _ffi.call("ecd_attn_combine", pm.data_ptr(), pl.data_ptr(), pa.data_ptr(), o.data_ptr(), RH,
+              HD, int(NSPLIT), stream_ptr(dev))
+
+
+_attn_combine = _Launcher("_attn_combine", _attn_combine_impl,
+                          lambda pm, pl, pa, o, HD=None, HDP=None, NSPLIT=16: (o.numel() // HD,))
+
+
+# ---------------------------------------------------------------- SiLU(a) * b
+def _silu_mul_impl(x, y, F_, BLOCK=None):
+    dev = _dev(x, "_silu_mul")
+    _f16(x, "_silu_mul x")
+    _f16(y, "_silu_mul y")
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("_silu_mul: tensors must be contiguous")
+    R = y.numel() // F_
+    if x.numel() != 2 * R * F_:
+        raise ValueError("_silu_mul: x must be [R, 2F] for y [R, F]")
+    _ffi.call("ecd_silu_mul", x.data_ptr(), y.data_ptr(), R, F_, stream_ptr(dev))
+
+
+_silu_mul = _Launcher("_silu_mul", _silu_mul_impl,
+                      lambda x, y, F_, BLOCK=1024: (y.numel() // F_, cdiv(F_, BLOCK)))

@@ -1,0 +1,123 @@
+/*
+ * ecdecode.h -- C ABI of the MI355X (gfx950) per-frame decode path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed as
+ * `void* stream` (0 = the null stream).  Nothing allocates, frees or synchronises, so a
+ * caller may capture any sequence of these calls into one hipGraph.  Tensors are dense,
+ * row-major, fp16 unless stated ("f16" below is IEEE binary16 stored as 16 bits).
+ *
+ * Return value: 0 on success; ECD_EINVAL (-22) for an argument rejected on the host before
+ * any launch; ECD_ENOTSUP (-95) for a shape the library does not implement; a positive
+ * hipError_t code if the launch itself failed.
+ *
+ * Reference interfaces replaced (paths relative to the EstudioCanciones repository):
+ *   app/kernels.py   -- Triton kernels and their Python launchers
+ *   app/engine.py    -- the engine that launches them, RoPE table, embeddings
+ *   app/convert_final.py -- the offline int8 quantiser
+ */
+#ifndef ECDECODE_H
+#define ECDECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ECD_OK 0
+#define ECD_EINVAL (-22)
+#define ECD_ENOTSUP (-95)
+
+/* int8 per-output-channel GEMV / skinny GEMM with optional residual.
+ * Replaces int8_mm + _gemv8 (app/kernels.py:40-54, :20-37) and its dense fallback for
+ * M > 16 rows (app/kernels.py:46-49).
+ *   x [M, K] f16 with row stride ldx (elements); w [N, K] int8 (K contiguous); s [N] f16;
+ *   res [M, N] f16 with row stride ldr, or NULL; y [M, N] f16 with row stride ldy.
+ *   dense = 0: y = f16(f32(s[n]) * sum_k x*q)          (the reference's M <= 16 path)
+ *   dense = 1: y = f16(sum_k x * f16(f16(q) * s[n]))   (the reference's M > 16 path)
+ *   then y = f16(y + res) when res is given. */
+int ecd_gemv_i8(const void* x, long ldx, const void* w, const void* s, const void* res, long ldr,
+                void* y, long ldy, int M, int N, int K, int dense, void* stream);
+
+/* Same as ecd_gemv_i8 with an explicit tile choice (nt = 16-row tiles per block,
+ * kw = waves splitting K; 0 = library default).  Replaces the autotuned launch
+ * parameters of _gemv8 (app/kernels.py:12-19). */
+int ecd_gemv_i8_tuned(const void* x, long ldx, const void* w, const void* s, const void* res,
+                      long ldr, void* y, long ldy, int M, int N, int K, int dense, int nt, int kw,
+                      void* stream);
+
+/* RMSNorm: y = f16(f16(x * inv) * w), inv = 1/sqrt(sum(x^2)/D + eps).
+ * Replaces rms/_rms (app/kernels.py:58-74); torch twin app/engine.py:56-58.
+ *   x [R, D] stride ldx, w [D], y [R, D] stride ldy. */
+int ecd_rmsnorm(const void* x, long ldx, const void* w, void* y, long ldy, int R, int D,
+                float eps, void* stream);
+
+/* Interleaved RoPE of the q and k heads of a fused qkv row plus the KV-cache write.
+ * Replaces _rope_cache (app/kernels.py:78-107) as launched at app/engine.py:191-192.
+ *   qkv [R, (Hq + 2Hk) * HD]; rope [>= L, HD/2, 2] f32 (cos, sin); pos [R] int64;
+ *   q [R, Hq * HD] (output); kc, vc [B, Hk, L, HD] written at [r / S, kh, pos[r], :].
+ *   A row whose pos is outside [0, L) writes no cache slot. */
+int ecd_rope_kv_write(const void* qkv, const float* rope, const int64_t* pos, void* q, void* kc,
+                      void* vc, int R, int S, int Hq, int Hk, int L, int HD, void* stream);
+
+/* GQA flash-decoding attention of each row over cache slots [0, pos[r]].
+ * Replaces _attn (app/kernels.py:111-153) as launched at app/engine.py:194-202.
+ *   q [R, Hq * HD]; kc, vc [B, Hk, L, HD]; pos [R] int64.
+ *   nsplit == 1: writes o [R, Hq * HD] directly (pm/pl/pa unused, may be NULL).
+ *   nsplit  > 1: writes partials pm, pl [R * Hq * nsplit] f32 and pa [R * Hq * nsplit, HD] f32
+ *                indexed (r * Hq + h) * nsplit + split, for ecd_attn_combine.
+ *   HD in {64, 128, 256, 384}; Hq / Hk in {1, 2, 3, 4, 6, 8}. */
+int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t* pos, void* o,
+                    float* pm, float* pl, float* pa, int R, int S, int Hq, int Hk, int L, int HD,
+                    int nsplit, float scale, void* stream);
+
+/* Log-sum-exp merge of the split partials into o [RH, HD] f16 (RH = R * Hq).
+ * Replaces _attn_combine (app/kernels.py:156-167), launched at app/engine.py:204. */
+int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,
+                     int nsplit, void* stream);
+
+/* y[r, c] = f16(f16(silu(x[r, c])) * x[r, F + c]) for x [R, 2F], y [R, F].
+ * Replaces _silu_mul (app/kernels.py:171-180), launched at app/engine.py:209. */
+int ecd_silu_mul(const void* x, void* y, int R, int F, void* stream);
+
+/* Backbone input: out[b] = f16(sum_c f16(f16(q[row]) * s[row])), row = tok[b, c] + c * vocab.
+ * Replaces Emb.__call__ + .sum(1, dtype) (app/engine.py:89-104, :348).
+ *   tok [B, C] int64; table [rows, D] int8; scales [rows] f16; out [B, D].  A token outside
+ *   [0, vocab), or whose row is >= rows, contributes nothing. */
+int ecd_embed_sum_i8(const int64_t* tok, const void* table, const void* scales, long rows,
+                     void* out, int B, int C, int D, int vocab, void* stream);
+
+/* One-codebook embedding: e[b] = f16(f16(q[row]) * s[row]), row = tok[b * tok_stride] + cb * vocab
+ * (zero for a token outside [0, vocab) or a row >= rows; table [rows, D], scales [rows]).
+ * even == NULL: out[b] = e[b] (out [B, D]).
+ * even != NULL: out[2b] = even[b], out[2b + 1] = e[b] (out [2B, D]), the two-row input of the
+ *               first decoder pass.
+ * Replaces _embed_audio (app/engine.py:307-308) and the stack at app/engine.py:336. */
+int ecd_embed_i8(const int64_t* tok, long tok_stride, const void* table, const void* scales,
+                 long rows, int cb, int vocab, const void* even, void* out, int B, int D,
+                 void* stream);
+
+/* Per-row symmetric int8 quantiser of w [N, K] f32: s = max(max|w|, 1e-8) / 127,
+ * q = clamp(round_half_even(w / s), -127, 127); s_bf16 [N] (bf16 bits, nearest even) and/or
+ * s_f16 [N] (the f16 value of that bf16) -- either may be NULL, not both.
+ * Replaces q8_rows (app/convert_final.py:17-21) and the load cast at app/engine.py:241. */
+int ecd_quantize_rows_i8(const float* w, void* q, void* s_bf16, void* s_f16, int N, int K,
+                         void* stream);
+
+/* Llama-3 scaled RoPE table out [max_seq, head_dim / 2, 2] f32 (cos, sin), on the device.
+ * Replaces rope_cache (app/engine.py:28-43) built at Stack.alloc (app/engine.py:165-166). */
+int ecd_rope_table(float* out, int max_seq, int head_dim, double base, double scale, double low,
+                   double high, double old, void* stream);
+
+/* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
+ * counterpart: a kernel of known HBM traffic used to calibrate hardware byte counters. */
+int ecd_copy_bytes(const void* src, void* dst, long nbytes, void* stream);
+
+/* Library version string (static storage). */
+const char* ecd_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ECDECODE_H */

@@ -1,0 +1,73 @@
+"""Shared test helpers: seeded inputs and small model weights built with the oracle's
+quantiser (so the GPU engine and the oracle read identical int8 codes)."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.numerics import bf16_bits
+from oracle.quant import q8_rows
+
+AUDIO_VOCAB = 8197
+N_CB = 8
+
+ATOL = 2e-3   # fp16 kernel outputs: max-abs 2e-3 ...
+RTOL = 1e-2   # ... or 1e-2 relative
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def randn16(seed, *shape, std=1.0):
+    return (rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
+
+
+def tiny_cfgs(ffn=512):
+    bb = dict(layers=2, heads=2, kv_heads=1, max_seq=8192, dim=256, ffn=ffn)
+    dec = dict(layers=2, heads=2, kv_heads=1, max_seq=2048, dim=256, ffn=ffn)
+    return bb, dec
+
+
+def model_weights_np(backbone, decoder, seed=0, std=0.02, emb_std=1.0, text_vocab=64):
+    """Random-init weights in the int8 file layout, quantised by the oracle (numpy)."""
+    from estudiocanciones_amd.quant import weight_shapes  # pure-python shape table
+    g = rng(seed)
+    lin, dense = weight_shapes(backbone, decoder, text_vocab)
+    out = {}
+    for name, (N, K) in lin.items():
+        sd = emb_std if "embeddings" in name else std
+        w = g.standard_normal((N, K), dtype=np.float32) * np.float32(sd)
+        out[name + ".q8"], out[name + ".s8"] = q8_rows(w)
+    for name, shp in dense.items():
+        if name.endswith(".scale"):
+            t = 1.0 + 0.02 * g.standard_normal(shp, dtype=np.float32)
+        else:
+            t = g.standard_normal(shp, dtype=np.float32) * np.float32(emb_std if "embedding" in name else std)
+        out[name] = bf16_bits(t)
+    return out
+
+
+def to_torch(weights_np, dev):
+    """numpy file-layout dict -> torch tensors on dev (bf16 bit patterns become bfloat16)."""
+    import torch
+    out = {}
+    for k, v in weights_np.items():
+        if v.dtype == np.uint16:
+            out[k] = torch.from_numpy(v.astype(np.int16)).view(torch.bfloat16).to(dev)
+        else:
+            out[k] = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    return out
+
+
+def assert_close16(got, want, atol=ATOL, rtol=RTOL, what=""):
+    got = np.asarray(got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    err = np.abs(got - want)
+    bound = atol + rtol * np.abs(want)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{bad.size} elements outside atol={atol} rtol={rtol}; "
+            f"worst at {i}: got {got[i]} want {want[i]} (max abs err {err.max():.3e})")

@@ -1,0 +1,80 @@
+"""The C-ABI library loads without a GPU, exports every entry point declared in
+include/ecdecode.h, and rejects bad arguments on the host before any launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ecdecode.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(ecd_\w+)\s*\(", text)
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "ecd_gemv_i8" in names and "ecd_decode_attn" in names
+    assert len(names) == len(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    from estudiocanciones_amd import _ffi
+    lib = _ffi.lib()
+    for name in declared():
+        assert hasattr(lib, name), f"{name} declared in ecdecode.h but not exported"
+    # and the binding declares exactly the same entry points
+    assert set(_ffi.SIGNATURES) | {"ecd_version"} == set(declared())
+    assert lib.ecd_version().startswith(b"ecdecode")
+
+
+def test_signatures_match_header_arity():
+    from estudiocanciones_amd import _ffi
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, argtypes in _ffi.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        assert m, name
+        nargs = len([a for a in m.group(1).split(",") if a.strip()])
+        assert nargs == len(argtypes), f"{name}: header has {nargs} args, binding {len(argtypes)}"
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.ecd_gemv_i8(None, 64, None, None, None, 0, None, 64, 1, 64, 64, 0, None),
+    lambda L: L.ecd_gemv_i8(8, 32, 8, 8, None, 0, 8, 64, 1, 64, 64, 0, None),     # ldx < K
+    lambda L: L.ecd_gemv_i8(8, 64, 8, 8, None, 0, 8, 64, 0, 64, 64, 0, None),     # M = 0
+    lambda L: L.ecd_rmsnorm(None, 8, None, None, 8, 1, 8, 1e-5, None),
+    lambda L: L.ecd_rope_kv_write(8, 8, 8, 8, 8, 8, 1, 1, 3, 2, 8, 128, None),    # Hq % Hk
+    lambda L: L.ecd_rope_kv_write(8, 8, 8, 8, 8, 8, 1, 1, 4, 2, 8, 127, None),    # odd HD
+    lambda L: L.ecd_decode_attn(8, 8, 8, 8, 8, None, None, None, 1, 1, 8, 2, 8, 128, 16, 0.1, None),
+    lambda L: L.ecd_decode_attn(8, 8, 8, 8, None, None, None, None, 1, 1, 8, 2, 8, 128, 1, 0.1, None),
+    lambda L: L.ecd_attn_combine(None, None, None, None, 1, 128, 16, None),
+    lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
+    lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
+    lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0
+    lambda L: L.ecd_embed_i8(8, 1, 8, 8, 0, 0, 8197, None, 8, 1, 8, None),        # rows 0
+    lambda L: L.ecd_quantize_rows_i8(8, 8, None, None, 1, 8, None),               # no scale out
+    lambda L: L.ecd_rope_table(None, 8, 128, 5e5, 32.0, 1.0, 4.0, 8192.0, None),
+    lambda L: L.ecd_rope_table(8, 8, 127, 5e5, 32.0, 1.0, 4.0, 8192.0, None),
+    lambda L: L.ecd_copy_bytes(8, 8, 15, None),
+])
+def test_host_argument_validation(call):
+    """Invalid arguments return ECD_EINVAL before any HIP call (no GPU needed)."""
+    from estudiocanciones_amd import _ffi
+    assert call(_ffi.lib()) == _ffi.ECD_EINVAL
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    """The product path has no CPU fallback: CPU tensors raise instead of computing."""
+    import torch
+    from estudiocanciones_amd.kernels import int8_mm, rms
+    x = torch.zeros(2, 64, dtype=torch.float16)
+    w = torch.zeros(8, 64, dtype=torch.int8)
+    s = torch.ones(8, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        int8_mm(x, w, s)
+    with pytest.raises(RuntimeError):
+        rms(x, torch.ones(64, dtype=torch.float16))
