@@ -28,7 +28,7 @@ import torch
 
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, int8_mm,
-                      next_power_of_2, rms as krms, stream_ptr)
+                      next_power_of_2, rms as krms, sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
 N_CB = 8
@@ -300,43 +300,58 @@ class HeartMuLaLite:
         return self.audio_emb.gather(tok, cb, AUDIO_VOCAB)
 
     # -------------------------------------------------- one frame (backbone + 7 decoder passes)
-    def _frame_fast(self, last_h, cfg, topk, temp, forced=None, logits_out=None, noise=None):
-        """app/engine.py:328-343.  ``forced`` [B, 8] replaces the samples (teacher forcing),
-        ``logits_out`` collects the 8 logit tensors, ``noise`` [8, N, V] fixes the draws."""
+    def _frame_fast(self, last_h, cfg, topk, temp, pos=None, forced=None, logits_out=None,
+                    noise=None):
+        """app/engine.py:328-343.  Sampling is one fused kernel per codebook (CFG, temperature,
+        top-k, Exponential race) writing straight into the [B, 8] token tensor; its draws are
+        keyed by the seed and the frame position ``pos`` (int64 device tensor, first element).
+        ``forced`` [B, 8] replaces the samples (teacher forcing), ``logits_out`` collects the
+        8 logit tensors, ``noise`` [8, N, V] fixes the Exponential draws (tests)."""
         B = self.B
         if getattr(self, "_dpos", None) is None or self._dpos[0].shape[0] != 2 * B:
             self._dpos = [torch.arange(2, device=self.dev).repeat(B)] + [
                 torch.full((B,), i + 1, dtype=torch.long, device=self.dev) for i in range(1, N_CB - 1)]
+        if forced is None:
+            samples = torch.empty(B, N_CB, dtype=torch.long, device=self.dev)
+            if pos is None:
+                pos = self._pos_prompt
+        else:
+            samples = forced
 
         def pick(i, lg):
             if logits_out is not None:
                 logits_out.append(lg)
-            if forced is not None:
-                return forced[:, i:i + 1]
-            return self._guided(lg, cfg, topk, temp, None if noise is None else noise[i])
+            if forced is None:
+                sample_topk(lg, self.N, cfg, temp, topk, samples[:, i], seed=self._seed, pos=pos,
+                            salt=i, noise=None if noise is None else noise[i])
+            return samples[:, i:i + 1]
 
         c0 = pick(0, self.c0_head(last_h))
-        samples = [c0]
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
         x = self.audio_emb.gather(c0, 0, AUDIO_VOCAB, even=last_h)
         h = self.decoder.decode(self.projection(x), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
             ci = pick(i, self.audio_head[i - 1](h))
-            samples.append(ci)
             if i < N_CB - 1:
                 h = self.decoder.decode(self.projection(self._embed_audio(i, ci)), self._dpos[i], 1)
-        return torch.cat(samples, 1)
+        return samples
 
     def _step(self, tok, pos, bucket, cfg, topk, temp, **kw):
         """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349)."""
         h = self.audio_emb.sum_codebooks(tok, AUDIO_VOCAB)
-        return self._frame_fast(self.backbone.decode(h, pos[:, 0].contiguous(), 1), cfg, topk, temp, **kw)
+        return self._frame_fast(self.backbone.decode(h, pos[:, 0].contiguous(), 1), cfg, topk, temp,
+                                pos=pos, **kw)
 
     # -------------------------------------------------- caches
-    def alloc(self, n, L, cfg_scale=1.5):
-        """Static caches for n takes and backbone capacity L (app/engine.py:380-388)."""
+    def alloc(self, n, L, cfg_scale=1.5, seed=None):
+        """Static caches for n takes and backbone capacity L (app/engine.py:380-388), and the
+        sampler's seed (drawn from torch's host generator when not given)."""
         self.N = n
         self.B = 2 * n if cfg_scale != 1.0 else n
+        if seed is None or seed < 0:
+            seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        self._seed = torch.tensor([seed], dtype=torch.int64, device=self.dev)
+        self._pos_prompt = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self.backbone.alloc(self.B, L, self.dev, self.dt)
         self.decoder.alloc(self.B, N_CB, self.dev, self.dt)
 
@@ -353,6 +368,7 @@ class HeartMuLaLite:
         n_frames = max_ms // FRAME_MS
         L = P + n_frames + 2
         self.alloc(n, L + 256, cfg_scale)
+        self._pos_prompt.fill_(P - 1)
         N, B = self.N, self.B
         te = self.text_emb(text.to(self.dev))                                  # [P, D]
         h = te.unsqueeze(0).repeat(B, 1, 1)

@@ -226,3 +226,29 @@ def _silu_mul_impl(x, y, F_, BLOCK=None):
 
 _silu_mul = _Launcher("_silu_mul", _silu_mul_impl,
                       lambda x, y, F_, BLOCK=1024: (y.numel() // F_, cdiv(F_, BLOCK)))
+
+
+# ---------------------------------------------------------------- fused sampler
+def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, noise=None):
+    """CFG mix + temperature + top-k + softmax(log_softmax) + Exponential race in one kernel
+    (the math of _sample/_guided, app/engine.py:291-305).
+
+    logits [B, V] fp16 (B = 2N: cond rows then uncond rows; B = N: no CFG); out: int64 view
+    with out[b] the token slot of row b (any row stride).  The Exponential(1) draws come from
+    a counter-based Philox keyed by seed (int64 device scalar) at frame position pos (int64
+    device scalar) and ``salt``, or from ``noise`` [N, V] float32 when given."""
+    dev = _dev(logits, "sample_topk")
+    _f16(logits, "sample_topk logits")
+    B, V = logits.shape
+    if logits.stride(-1) != 1:
+        raise ValueError("sample_topk: logits rows must be contiguous")
+    if out.dtype != torch.int64 or out.shape[0] != B:
+        raise ValueError("sample_topk: out must be int64 with one slot per row")
+    if noise is not None:
+        if noise.dtype != torch.float32 or tuple(noise.shape) != (N, V) or not noise.is_contiguous():
+            raise ValueError("sample_topk: noise must be contiguous float32 [N, V]")
+    elif seed is None or pos is None:
+        raise ValueError("sample_topk: seed and pos device scalars are required without noise")
+    _ffi.call("ecd_sample_topk", logits.data_ptr(), logits.stride(0), B, N, float(cfg), float(temp),
+              int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt), out.data_ptr(),
+              out.stride(0), stream_ptr(dev))

@@ -109,6 +109,16 @@ int ecd_quantize_rows_i8(const float* w, void* q, void* s_bf16, void* s_f16, int
 int ecd_rope_table(float* out, int max_seq, int head_dim, double base, double scale, double low,
                    double high, double old, void* stream);
 
+/* CFG + temperature + top-k + Exponential-race sampler over [B, V] f16 logits (B = 2N with CFG:
+ * rows 0..N-1 conditional, N..2N-1 unconditional; B = N without).  For each take n the token is
+ * written to out[n * out_stride] (and out[(n + N) * out_stride] with CFG).  The Exponential(1)
+ * draws come from Philox4x32-10 keyed by *seed and countered by (index, take, *pos, salt), or
+ * from noise [N, V] f32 when noise != NULL.  V <= 8704.
+ * Replaces _sample and _guided (app/engine.py:291-305) -- ~25 PyTorch kernels per call. */
+int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float temp, int topk,
+                    int V, const float* noise, const int64_t* seed, const int64_t* pos, int salt,
+                    int64_t* out, long out_stride, void* stream);
+
 /* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
  * counterpart: a kernel of known HBM traffic used to calibrate hardware byte counters. */
 int ecd_copy_bytes(const void* src, void* dst, long nbytes, void* stream);

@@ -1,0 +1,101 @@
+"""The fused sampler kernel against the oracle's restatement of _sample/_guided
+(app/engine.py:291-305): exact tokens with injected Exponential draws, greedy at top-k 1,
+threshold ties kept, and the Philox draws reproducing the top-k softmax distribution."""
+import numpy as np
+import pytest
+
+from helpers import rng
+from oracle.model import cfg_mix, sample
+
+pytestmark = pytest.mark.gpu
+
+V = 8197
+
+
+def T(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("N,cfg_on,topk,temp", [(4, True, 50, 1.0), (1, True, 50, 0.7),
+                                                (3, False, 50, 1.0), (2, True, 1, 1.0),
+                                                (4, True, 8197, 1.3)])
+def test_sampler_matches_oracle_with_noise(dev, N, cfg_on, topk, temp):
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    g = rng(100 + N + topk)
+    B = 2 * N if cfg_on else N
+    for trial in range(6):
+        logits = (g.standard_normal((B, V), dtype=np.float32) * 3).astype(np.float16)
+        noise = g.exponential(1.0, (N, V)).astype(np.float32)
+        lg = cfg_mix(logits, N, 1.5) if cfg_on else logits
+        want = sample(lg.astype(np.float32), topk, temp, noise)[:, 0]
+        out = torch.full((B,), -1, dtype=torch.int64, device=dev)
+        sample_topk(T(logits, dev), N, 1.5, temp, topk, out, noise=T(noise, dev))
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:N], want), (trial, got[:N], want)
+        if cfg_on:
+            assert np.array_equal(got[N:], got[:N])
+
+
+def test_sampler_threshold_ties_kept(dev):
+    """Values equal to the k-th largest stay eligible (mask is logits < thr)."""
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    logits = np.full((1, V), -5.0, np.float16)
+    logits[0, [10, 20, 30, 40]] = 2.0            # 4-way tie at the top, top-k = 2
+    hits = set()
+    g = rng(7)
+    for t in range(40):
+        noise = g.exponential(1.0, (1, V)).astype(np.float32)
+        out = torch.zeros(1, dtype=torch.int64, device=dev)
+        sample_topk(T(logits, dev), 1, 1.5, 1.0, 2, out, noise=T(noise, dev))
+        hits.add(int(out.item()))
+    assert hits <= {10, 20, 30, 40} and len(hits) >= 3
+
+
+def test_sampler_philox_distribution(dev):
+    """4096 draws (64 takes x 64 codebook salts) from one logit row: all inside the top-50 set
+    and the empirical distribution within total-variation 0.06 of softmax(top-50)."""
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    Nt = 64
+    row = (rng(8).standard_normal(V, dtype=np.float32) * 2).astype(np.float16)
+    logits = np.tile(row, (Nt, 1))
+    lt = T(logits, dev)
+    seed = torch.tensor([12345], dtype=torch.int64, device=dev)
+    pos = torch.tensor([777], dtype=torch.int64, device=dev)
+    counts = np.zeros(V)
+    for salt in range(64):
+        out = torch.zeros(Nt, dtype=torch.int64, device=dev)
+        sample_topk(lt, Nt, 1.0, 1.0, 50, out, seed=seed, pos=pos, salt=salt)
+        np.add.at(counts, out.cpu().numpy(), 1)
+    x = row.astype(np.float64)
+    thr = np.sort(x)[-50]
+    top = np.nonzero(x >= thr)[0]                   # values tied with the 50th stay eligible
+    assert 50 <= top.size < 80
+    assert counts[np.setdiff1d(np.arange(V), top)].sum() == 0
+    p = np.zeros(V)
+    p[top] = np.exp(x[top] - x[top].max())
+    p /= p.sum()
+    tv = 0.5 * np.abs(counts / counts.sum() - p).sum()
+    assert tv < 0.06, tv
+
+
+def test_sampler_seed_and_position_change_draws(dev):
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    Nt = 64
+    row = np.zeros(V, np.float16)                   # uniform over the top-k set
+    lt = T(np.tile(row, (Nt, 1)), dev)
+
+    def draw(seed, p):
+        out = torch.zeros(Nt, dtype=torch.int64, device=dev)
+        sample_topk(lt, Nt, 1.0, 1.0, V, out, seed=torch.tensor([seed], device=dev),
+                    pos=torch.tensor([p], device=dev), salt=0)
+        return out.cpu().numpy()
+
+    a = draw(1, 5)
+    assert np.array_equal(a, draw(1, 5))           # reproducible
+    assert not np.array_equal(a, draw(2, 5))       # seed matters
+    assert not np.array_equal(a, draw(1, 6))       # frame position matters
