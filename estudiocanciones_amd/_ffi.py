@@ -34,6 +34,16 @@ SIGNATURES = {
     "ecd_sample_topk": [_P, c_long, c_int, c_int, c_float, c_float, c_int, c_int, _P, _P, _P, c_int,
                         _P, c_long, _P],
     "ecd_copy_bytes": [_P, _P, c_long, _P],
+    "ecd_packed_bytes": [c_int, c_int],
+    "ecd_pack_i8": [_P, c_int, c_int, c_int, _P, _P],
+    "ecd_gemv_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int, c_int,
+                     c_int, _P],
+    "ecd_rms_gemv_i8p": [_P, c_long, _P, c_float, _P, _P, _P, c_long, c_int, c_int, c_int, c_int, _P],
+    "ecd_rms_qkv_rope": [_P, c_long, _P, c_float, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int,
+                         c_int, c_int, c_int, c_int, c_int, _P],
+    "ecd_rms_w13_silu": [_P, c_long, _P, c_float, _P, _P, _P, c_int, c_int, c_int, c_int, _P],
+    "ecd_embed_gemv_i8p": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, _P, _P, c_long, c_int,
+                           c_int, c_int, c_int, _P],
 }
 
 _lib = None
@@ -55,7 +65,7 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = argtypes
-            fn.restype = c_int
+            fn.restype = c_long if name == "ecd_packed_bytes" else c_int
         handle.ecd_version.argtypes = []
         handle.ecd_version.restype = ctypes.c_char_p
         _lib = handle

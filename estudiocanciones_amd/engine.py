@@ -27,8 +27,9 @@ from pathlib import Path
 import torch
 
 from . import _ffi
-from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, int8_mm,
-                      next_power_of_2, rms as krms, sample_topk, stream_ptr)
+from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
+                      gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms, rms_qkv_rope,
+                      rms_w13_silu, sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
 N_CB = 8
@@ -63,8 +64,26 @@ class Linear:
         if q8 is None:
             raise NotImplementedError("the gfx950 decode path runs int8 per-channel weights only")
         self.w, self.q8, self.s8 = None, q8, s8
+        self.qp = self.sp = None
+        self.N, self.K = q8.shape
+
+    def pack(self, interleave=False):
+        """Add the lane-ordered tile copy used by the fused GEMVs (K % 64 == 0).  With
+        ``interleave`` the w1 | w3 halves become (a_j, b_j) row pairs (scales likewise)."""
+        if self.K % 64:
+            return self
+        self.qp = pack_i8(self.q8, interleave)
+        if interleave:
+            F = self.N // 2
+            self.sp = torch.stack([self.s8[:F], self.s8[F:]], 1).reshape(-1).contiguous()
+        else:
+            self.sp = self.s8
+        return self
 
     def __call__(self, x, res=None):
+        if self.qp is not None and self.sp is self.s8 and x.dim() == 2 and x.stride(1) == 1 \
+                and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0:
+            return gemv_packed(x, self.qp, self.s8, self.N, self.K, res)
         return int8_mm(x, self.q8, self.s8, res)
 
     @property
@@ -177,34 +196,60 @@ class Stack:
 
     def decode(self, x, pos, S):
         """Fast path for few rows (app/engine.py:180-211): x [R, D] with R = B*S (row r -> batch
-        r // S), pos [R] absolute positions; row r attends [0, pos[r]]."""
+        r // S), pos [R] absolute positions; row r attends [0, pos[r]].
+
+        Per layer: rms+qkv+RoPE/KV write (one kernel), attention (+ split combine),
+        O projection + residual, rms+w1|w3+SiLU*mul (one kernel), w2 + residual."""
+        if any(b.qkv.qp is None for b in self.blocks):
+            return self.decode_reference(x, pos, S)
         R = x.shape[0]
         ns = self.nsplit
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
-            qkv = b.qkv(krms(x, b.n1))
+            q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
+            rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L, HD)
+            o = self._attention(b, q, pos, S, ns)
+            x = b.o(o, res=x)
+            mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2)
+            x = b.w2(mm, res=x)
+        return krms(x, self.norm)
+
+    def _attention(self, b, q, pos, S, ns):
+        R = q.shape[0]
+        Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
+        o = torch.empty_like(q)
+        HDP = next_power_of_2(HD)
+        if ns > 1:
+            pm = torch.empty(R * Hq * ns, device=q.device)
+            pl = torch.empty_like(pm)
+            pa = torch.empty(R * Hq * ns, HD, device=q.device)
+        else:
+            pm = pl = pa = o
+        _attn[(R, Hk, ns)](q, b.kc, b.vc, pos, o, pm, pl, pa, S, Hq, Hk, L, 1.0 / math.sqrt(HD),
+                           HD=HD, HDP=HDP, G=Hq // Hk, BLK=64 if HD <= 128 else 16, NSPLIT=ns,
+                           num_warps=4)
+        if ns > 1:
+            _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, HDP=HDP, NSPLIT=ns)
+        return o
+
+    def decode_reference(self, x, pos, S):
+        """The reference's launch sequence (app/engine.py:180-211) through the drop-in kernel
+        entry points of kernels.py (unpacked weights, one launch per reference kernel)."""
+        R = x.shape[0]
+        ns = self.nsplit
+        for b in self.blocks:
+            Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
+            qkv = int8_mm(krms(x, b.n1), b.qkv.q8, b.qkv.s8)
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
             _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
                                       HD=HD, HALF=next_power_of_2(HD // 2))
-            o = torch.empty_like(q)
-            HDP = next_power_of_2(HD)
-            if ns > 1:
-                pm = torch.empty(R * Hq * ns, device=x.device)
-                pl = torch.empty_like(pm)
-                pa = torch.empty(R * Hq * ns, HD, device=x.device)
-            else:
-                pm = pl = pa = o
-            _attn[(R, Hk, ns)](q, b.kc, b.vc, pos, o, pm, pl, pa, S, Hq, Hk, L, 1.0 / math.sqrt(HD),
-                               HD=HD, HDP=HDP, G=Hq // Hk, BLK=64 if HD <= 128 else 16, NSPLIT=ns,
-                               num_warps=4)
-            if ns > 1:
-                _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, HDP=HDP, NSPLIT=ns)
-            x = b.o(o, res=x)
-            a = b.w13(krms(x, b.n2))
+            o = self._attention(b, q, pos, S, ns)
+            x = int8_mm(o, b.o.q8, b.o.s8, x)
+            a = int8_mm(krms(x, b.n2), b.w13.q8, b.w13.s8)
             Fd = a.shape[1] // 2
             mm = torch.empty(R, Fd, device=x.device, dtype=x.dtype)
             _silu_mul[(R, cdiv(Fd, 1024))](a, mm, Fd, BLOCK=1024)
-            x = b.w2(mm, res=x)
+            x = int8_mm(mm, b.w2.q8, b.w2.s8, x)
         return krms(x, self.norm)
 
 
@@ -266,12 +311,20 @@ class HeartMuLaLite:
         self.bb_cfg, self.dec_cfg = dict(backbone), dict(decoder)
         self.backbone = Stack(p, "backbone", backbone)
         self.decoder = Stack(p, "decoder", decoder)
+        for st in (self.backbone, self.decoder):
+            for b in st.blocks:
+                b.qkv.pack()
+                b.o.pack()
+                b.w13.pack(interleave=True)
+                b.w2.pack()
         self.text_emb = emb("text_embeddings.weight")
         self.audio_emb = emb("audio_embeddings.weight")
         self.uncond = f.get("unconditional_text_embedding.weight").to(dtype)
         self.projection = p("projection.weight")
         self.c0_head = p("codebook0_head.weight")
         self.audio_head = [p(f"audio_head.{i}") for i in range(N_CB - 1)]
+        for lin in [self.projection, self.c0_head, *self.audio_head]:
+            lin.pack()
         self.muq_b = f.get("muq_linear.bias").to(dtype)
         self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
         self.graphs = {}
@@ -328,13 +381,22 @@ class HeartMuLaLite:
 
         c0 = pick(0, self.c0_head(last_h))
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
-        x = self.audio_emb.gather(c0, 0, AUDIO_VOCAB, even=last_h)
-        h = self.decoder.decode(self.projection(x), self._dpos[0], 2)[1::2]
+        h = self.decoder.decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
             ci = pick(i, self.audio_head[i - 1](h))
             if i < N_CB - 1:
-                h = self.decoder.decode(self.projection(self._embed_audio(i, ci)), self._dpos[i], 1)
+                h = self.decoder.decode(self._project(ci, i), self._dpos[i], 1)
         return samples
+
+    def _project(self, tok, cb, even=None):
+        """projection(_embed_audio(cb, tok)) -- with ``even`` the interleave (even[b], emb[b]) --
+        as one GEMV whose prologue gathers the int8 embedding rows (app/engine.py:336-342)."""
+        pr, e = self.projection, self.audio_emb
+        if pr.qp is None:
+            x = e.gather(tok, cb, AUDIO_VOCAB, even=even)
+            return pr(x)
+        ev = None if even is None else even.contiguous()
+        return embed_gemv_packed(tok, e.q8, e.s8, cb, AUDIO_VOCAB, pr.qp, pr.s8, pr.N, even=ev)
 
     def _step(self, tok, pos, bucket, cfg, topk, temp, **kw):
         """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349)."""

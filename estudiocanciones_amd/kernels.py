@@ -252,3 +252,99 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
     _ffi.call("ecd_sample_topk", logits.data_ptr(), logits.stride(0), B, N, float(cfg), float(temp),
               int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt), out.data_ptr(),
               out.stride(0), stream_ptr(dev))
+
+
+# ---------------------------------------------------------------- packed weights + fused GEMVs
+def pack_i8(w: torch.Tensor, interleave: bool = False) -> torch.Tensor:
+    """Lane-ordered 16 x 64 tile layout of an int8 [N, K] matrix (K % 64 == 0) for the fused
+    GEMVs.  With ``interleave`` the two halves of w are row-interleaved (w1 | w3 -> pairs)."""
+    dev = _dev(w, "pack_i8")
+    if w.dtype != torch.int8 or w.dim() != 2 or not w.is_contiguous():
+        raise TypeError("pack_i8: w must be a contiguous [N, K] int8 tensor")
+    N, K = w.shape
+    if K % 64 or (interleave and N % 2):
+        raise ValueError("pack_i8: K must be a multiple of 64 (and N even to interleave)")
+    out = torch.empty(-(-N // 16) * 16 * K, dtype=torch.int8, device=dev)
+    _ffi.call("ecd_pack_i8", w.data_ptr(), N, K, int(interleave), out.data_ptr(), stream_ptr(dev))
+    return out
+
+
+def _check_x(x, K, name):
+    _dev(x, name)
+    _f16(x, name + " x")
+    if x.dim() != 2 or x.shape[1] != K or x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        raise ValueError(f"{name}: x must be [M, {K}] fp16 with unit inner stride, 16-byte rows")
+
+
+def gemv_packed(x, wp, s, N, K, res=None, out=None):
+    """y = int8_mm(x, w, s, res) on packed weights (same numerics)."""
+    _check_x(x, K, "gemv_packed")
+    M = x.shape[0]
+    y = out if out is not None else torch.empty(M, N, device=x.device, dtype=torch.float16)
+    if res is not None:
+        _f16(res, "gemv_packed res")
+        if res.shape != (M, N) or res.stride(1) != 1:
+            raise ValueError("gemv_packed: res must be [M, N] with unit inner stride")
+    _ffi.call("ecd_gemv_i8p", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(), _ptr(res),
+              res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0), M, N, K,
+              int(M > 16), 0, 0, stream_ptr(x.device))
+    return y
+
+
+def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5):
+    """int8_mm(rms(x, nw), w, s) in one kernel."""
+    _check_x(x, K, "rms_gemv_packed")
+    M = x.shape[0]
+    y = torch.empty(M, N, device=x.device, dtype=torch.float16)
+    _ffi.call("ecd_rms_gemv_i8p", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
+              s.data_ptr(), y.data_ptr(), N, M, N, K, int(M > 16), stream_ptr(x.device))
+    return y
+
+
+def rms_qkv_rope(x, nw, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, eps=1e-5):
+    """rms -> fused q|k|v GEMV -> RoPE of q and k -> q out, k/v into the cache at pos (one kernel)."""
+    K = x.shape[1]
+    _check_x(x, K, "rms_qkv_rope")
+    M = x.shape[0]
+    if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+        raise ValueError("rms_qkv_rope: pos must be contiguous int64 [M]")
+    if kc.shape != (kc.shape[0], Hk, L, HD) or kc.shape[0] * S < M or vc.shape != kc.shape:
+        raise ValueError("rms_qkv_rope: caches must be [B, Hk, L, HD] with B * S >= M")
+    if rope.shape[0] < L or rope.shape[1] != HD // 2 or rope.dtype != torch.float32:
+        raise ValueError("rms_qkv_rope: rope table must be float32 [>= L, HD/2, 2]")
+    if q.numel() != M * Hq * HD or not (q.is_contiguous() and kc.is_contiguous() and vc.is_contiguous()):
+        raise ValueError("rms_qkv_rope: q/kc/vc must be contiguous")
+    _ffi.call("ecd_rms_qkv_rope", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
+              s.data_ptr(), rope.data_ptr(), pos.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+              M, S, Hq, Hk, L, HD, K, int(M > 16), stream_ptr(x.device))
+
+
+def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5):
+    """rms -> [w1 | w3] GEMV on row-interleaved packed weights -> fp16(silu(a)) * b, [M, F]."""
+    K = x.shape[1]
+    _check_x(x, K, "rms_w13_silu")
+    M = x.shape[0]
+    mm = torch.empty(M, F, device=x.device, dtype=torch.float16)
+    _ffi.call("ecd_rms_w13_silu", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
+              s_il.data_ptr(), mm.data_ptr(), M, F, K, int(M > 16), stream_ptr(x.device))
+    return mm
+
+
+def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None):
+    """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
+    interleave (even[b], emb[b]) and the output has 2B rows."""
+    dev = _dev(tok, "embed_gemv_packed")
+    if tok.dtype != torch.int64:
+        raise TypeError("embed_gemv_packed: tok must be int64")
+    B = tok.shape[0]
+    K = table.shape[1]
+    M = 2 * B if even is not None else B
+    if even is not None:
+        _f16(even, "embed_gemv_packed even")
+        if even.shape != (B, K) or not even.is_contiguous() or even.data_ptr() % 16:
+            raise ValueError("embed_gemv_packed: even must be contiguous [B, K]")
+    y = torch.empty(M, N, device=dev, dtype=torch.float16)
+    _ffi.call("ecd_embed_gemv_i8p", tok.data_ptr(), tok.stride(0), table.data_ptr(), tscale.data_ptr(),
+              table.shape[0], int(cb), int(vocab), _ptr(even), wp.data_ptr(), s.data_ptr(),
+              y.data_ptr(), N, M, N, K, int(M > 16), stream_ptr(dev))
+    return y
