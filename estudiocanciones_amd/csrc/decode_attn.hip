@@ -72,15 +72,13 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][j][e] = 0.f;
 
-  for (int t0 = lo; t0 < hi; t0 += 16) {
-    f16x8 kf[NKC];
-    {
-      const int tk = min(t0 + row, hi - 1);
-      const f16* kp = kb + (long)tk * HD + 8 * grp;
+  f16x8 kf[NKC];
+  f16x8 vv[4][NDP];
+  auto load_tile = [&](int t0, f16x8 (&kd)[NKC], f16x8 (&vd)[4][NDP]) {
+    const int tk = min(t0 + row, hi - 1);
+    const f16* kp = kb + (long)tk * HD + 8 * grp;
 #pragma unroll
-      for (int i = 0; i < NKC; ++i) kf[i] = *(const f16x8*)(kp + 32 * i);
-    }
-    f16x8 vv[4][NDP];
+    for (int i = 0; i < NKC; ++i) kd[i] = *(const f16x8*)(kp + 32 * i);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int t = t0 + 4 * grp + rr;
@@ -89,12 +87,20 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
 #pragma unroll
       for (int j = 0; j < NDP; ++j) {
         if (8 * (row + 16 * j) < HD && t < hi)
-          vv[rr][j] = *(const f16x8*)(vp + 128 * j);
+          vd[rr][j] = *(const f16x8*)(vp + 128 * j);
         else
-          vv[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+          vd[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
+  };
+  if (lo < hi) load_tile(lo, kf, vv);
 
+  for (int t0 = lo; t0 < hi; t0 += 16) {
+    // double buffering for the narrow heads: the next tile's loads fly during this tile's math
+    f16x8 kn[NKC];
+    f16x8 vn[4][NDP];
+    constexpr bool DB = HD <= 128;
+    if (DB && t0 + 16 < hi) load_tile(t0 + 16, kn, vn);
     f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[i], qf[i], st, 0, 0, 0);
@@ -139,6 +145,18 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
           for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)vv[rr][j][e];
           acc[g][j][e] = a;
         }
+    }
+    if (t0 + 16 < hi) {
+      if (DB) {
+#pragma unroll
+        for (int i = 0; i < NKC; ++i) kf[i] = kn[i];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+          for (int j = 0; j < NDP; ++j) vv[rr][j] = vn[rr][j];
+      } else {
+        load_tile(t0 + 16, kf, vv);
+      }
     }
   }
 
@@ -198,29 +216,59 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
 }
 
 // o[rh, d] = sum_s w_s pa[rh, s, d] / sum_s w_s pl[rh, s],  w_s = exp(pm[rh, s] - max_s pm)
-// with w_s = 0 for empty splits (app/kernels.py:156-167).
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ pm,
+// with w_s = 0 for empty splits (app/kernels.py:156-167).  Every partial load of the block is
+// issued before the weights are known, so the kernel costs one memory round trip.
+constexpr int CMB_MAXS = 32;
+
+// One block per (row, head), one thread per d (blockDim = HD rounded up to 64).
+__global__ __launch_bounds__(512) void attn_combine_kernel(const float* __restrict__ pm,
                                                            const float* __restrict__ pl,
                                                            const float* __restrict__ pa,
                                                            f16* __restrict__ o, int HD,
                                                            int nsplit) {
   const long rh = blockIdx.x;
+  const int d = threadIdx.x;
+  __shared__ float s_w[CMB_MAXS];
+  __shared__ float s_den;
+  if (nsplit <= CMB_MAXS) {
+    float av[CMB_MAXS];
+#pragma unroll
+    for (int sp = 0; sp < CMB_MAXS; ++sp)
+      if (sp < nsplit && d < HD) av[sp] = pa[(rh * nsplit + sp) * HD + d];
+    if (d < 64) {
+      const float mv = d < nsplit ? pm[rh * nsplit + d] : -INFINITY;
+      const float lv = d < nsplit ? pl[rh * nsplit + d] : 0.f;
+      const float M = wave_max(mv);
+      const float w = mv > -INFINITY ? __expf(mv - M) : 0.f;
+      const float den = wave_sum(lv * w);
+      if (d < nsplit) s_w[d] = w;
+      if (d == 0) s_den = den;
+    }
+    __syncthreads();
+    if (d < HD) {
+      float acc = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < CMB_MAXS; ++sp)
+        if (sp < nsplit) acc += av[sp] * s_w[sp];
+      o[rh * HD + d] = (f16)(acc / s_den);
+    }
+    return;
+  }
+  // many splits: plain loops
   const float* mrow = pm + rh * nsplit;
   const float* lrow = pl + rh * nsplit;
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, mrow[s]);
+  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, mrow[sp]);
   float den = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float m = mrow[s];
-    const float w = m > -INFINITY ? __expf(m - M) : 0.f;
-    den += lrow[s] * w;
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float m = mrow[sp];
+    den += lrow[sp] * (m > -INFINITY ? __expf(m - M) : 0.f);
   }
-  for (int d = threadIdx.x; d < HD; d += 128) {
+  if (d < HD) {
     float a = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float m = mrow[s];
-      const float w = m > -INFINITY ? __expf(m - M) : 0.f;
-      a += pa[(rh * nsplit + s) * HD + d] * w;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float m = mrow[sp];
+      a += pa[(rh * nsplit + sp) * HD + d] * (m > -INFINITY ? __expf(m - M) : 0.f);
     }
     o[rh * HD + d] = (f16)(a / den);
   }
@@ -290,9 +338,10 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
 
 int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,
                      int nsplit, void* stream) {
-  if (!pm || !pl || !pa || !o || RH <= 0 || HD <= 0 || nsplit <= 0) return ECD_EINVAL;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(RH), dim3(128), 0, (hipStream_t)stream, pm, pl, pa,
-                     (f16*)o, HD, nsplit);
+  if (!pm || !pl || !pa || !o || RH <= 0 || HD <= 0 || HD > 512 || nsplit <= 0) return ECD_EINVAL;
+  const int threads = ((HD + 63) / 64) * 64;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(RH), dim3(threads), 0, (hipStream_t)stream, pm, pl,
+                     pa, (f16*)o, HD, nsplit);
   return ecd_launch_status();
 }
 

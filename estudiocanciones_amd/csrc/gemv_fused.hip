@@ -48,6 +48,7 @@ struct GemvArgs {
   const f16* s;
   int M, N, K;
   int dense;
+  int stream_hint;  // 1: weights are streamed once (nontemporal loads), 0: keep them cacheable
   // EPI_STORE
   const f16* res;
   long ldr;
@@ -66,7 +67,121 @@ struct GemvArgs {
 
 __device__ __forceinline__ f16x8 ld8(const f16* p) { return *(const f16x8*)p; }
 
-template <int NT, int KW, int PRO, int EPI, int U>
+// Epilogue operands of tile t, lane l (rows n = nb .. nb + 3 of batch row me, the C layout of
+// v_mfma_f32_16x16x32_f16: lane l holds rows 4 (l >> 4) + r of column l & 15).  They are
+// fetched at kernel start, so the epilogue after the K reduction makes no dependent global
+// load: scales, residual, and for the RoPE epilogue the position and its cos/sin pairs.
+struct EpiPre {
+  f16 s[4];
+  f16 r[4];
+  float cs[4];
+  long p;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int n0, int m0, int t, int l) {
+  EpiPre e;
+  const int me = m0 + (l & 15);
+  const int nb = n0 + 16 * t + 4 * (l >> 4);
+  const bool ok = me < a.M && nb < a.N;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    e.s[r] = a.s[min(nb + r, a.N - 1)];
+    e.r[r] = (f16)0.0f;
+    e.cs[r] = 0.f;
+  }
+  e.p = 0;
+  if (EPI == EPI_STORE && a.res && ok) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < a.N) e.r[r] = a.res[(long)me * a.ldr + nb + r];
+  }
+  if (EPI == EPI_ROPE && ok) {
+    const int HD = a.HD;
+    const int h = nb / HD, d = nb - h * HD;
+    const long p_raw = a.pos[me];
+    e.p = p_raw;
+    if (h < a.Hq + a.Hk) {
+      const long pc = p_raw < 0 ? 0 : (p_raw >= a.L ? a.L - 1 : p_raw);
+      const float* cs = a.rope + pc * HD + d;  // (cos, sin) of pairs d/2 and d/2 + 1
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e.cs[r] = cs[r];
+    }
+  }
+  return e;
+}
+
+template <int EPI>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n0, int m0, int t, int l,
+                                              const f32x4& acc4, const EpiPre& e) {
+  const int M = a.M, N = a.N;
+  const bool dense = a.dense != 0;
+  const int me = m0 + (l & 15);
+  if (me >= M) return;
+  const int nb = n0 + 16 * t + 4 * (l >> 4);
+  if (nb >= N) return;
+  f16 yv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) yv[r] = (f16)(dense ? acc4[r] : acc4[r] * (float)e.s[r]);
+  if (EPI == EPI_STORE) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = nb + r;
+      if (n < N) {
+        f16 o = yv[r];
+        if (a.res) o = o + e.r[r];
+        a.y[(long)me * a.ldy + n] = o;
+      }
+    }
+  } else if (EPI == EPI_ROPE) {
+    // N = (Hq + 2Hk) * HD, HD % 4 == 0: the four columns sit in one head
+    const int HD = a.HD;
+    const int h = nb / HD, d = nb - h * HD;
+    const int L = a.L;
+    const long p_raw = e.p;
+    const bool pval = p_raw >= 0 && p_raw < L;
+    const long p = p_raw < 0 ? 0 : (p_raw >= L ? L - 1 : p_raw);
+    f16x4 o;
+    if (h < a.Hq + a.Hk) {
+      const float x0 = (float)yv[0], x1 = (float)yv[1], x2 = (float)yv[2], x3 = (float)yv[3];
+      o[0] = (f16)(x0 * e.cs[0] - x1 * e.cs[1]);
+      o[1] = (f16)(x1 * e.cs[0] + x0 * e.cs[1]);
+      o[2] = (f16)(x2 * e.cs[2] - x3 * e.cs[3]);
+      o[3] = (f16)(x3 * e.cs[2] + x2 * e.cs[3]);
+    } else {
+      o = (f16x4){yv[0], yv[1], yv[2], yv[3]};
+    }
+    if (h < a.Hq) {
+      *(f16x4*)(a.q + ((long)me * a.Hq + h) * HD + d) = o;
+    } else if (pval) {
+      const int b = me / a.S;
+      const int kh = h < a.Hq + a.Hk ? h - a.Hq : h - a.Hq - a.Hk;
+      f16* dst = h < a.Hq + a.Hk ? a.kc : a.vc;
+      *(f16x4*)(dst + (((long)b * a.Hk + kh) * L + p) * HD + d) = o;
+    }
+  } else {  // EPI_SILU: (a_j, b_j, a_j+1, b_j+1) with j = nb / 2
+    const int F = N >> 1;
+    const int j = nb >> 1;
+    f16x2 o;
+    const float a0 = (float)yv[0], a1 = (float)yv[2];
+    o.x = (f16)(a0 / (1.0f + expf(-a0))) * yv[1];
+    o.y = (f16)(a1 / (1.0f + expf(-a1))) * yv[3];
+    *(f16x2*)(a.mm + (long)me * F + j) = o;
+  }
+}
+
+constexpr int NW_MAX = 4096;  // RMS prologue: normalisation weights staged in LDS (K <= NW_MAX)
+
+template <bool NTL>
+__device__ __forceinline__ u32x4 ldw(const int8_t* p) {
+  if (NTL) return __builtin_nontemporal_load((const u32x4*)p);
+  return *(const u32x4*)p;
+}
+
+// One wave owns chunks [c0, c1) of every tile of its block and processes them in groups of CW:
+// all weight loads of a group are issued back to back (one memory latency per group), then the
+// x fragments, then the MFMAs.  Blocks are KW waves splitting K, NT tiles of 16 rows each.
+template <int NT, int KW, int PRO, int EPI, int CW, bool NTL>
 __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -94,14 +209,11 @@ __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
   // ---- prologue state for batch row m = m0 + row
   const int m = m0 + row;
   const bool mval = m < M;
-  __shared__ float s_inv[16];
   const f16* xp = nullptr;
-  const f16* nwp = nullptr;
   const int8_t* ep = nullptr;
   f16 esc = (f16)0.0f;
   if (PRO == PRO_PLAIN || PRO == PRO_RMS) {
-    xp = a.x + (long)(mval ? m : 0) * a.ldx + 16 * grp;
-    if (PRO == PRO_RMS) nwp = a.nw + 16 * grp;
+    if (mval) xp = a.x + (long)m * a.ldx + 16 * grp;
   } else {
     // embedding rows; with `even`, row m even comes from even[m / 2], odd from the table
     const bool from_even = a.even && ((m & 1) == 0);
@@ -118,17 +230,30 @@ __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
     }
   }
 
-  // first weight loads go out before the RMS statistics so their latency overlaps
-  u32x4 pre[U][NT];
-  const int cpre = min(c0 + U, c1);
+  f32x4 acc[NT];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // epilogue operands of this thread's (tile, lane) slot, fetched up front
+  const bool epi_thread = (int)threadIdx.x < NT * 64;
+  EpiPre pre_e;
+  if (KW > 1 && epi_thread) pre_e = epi_prefetch<EPI>(a, n0, m0, threadIdx.x >> 6, threadIdx.x & 63);
+
+  u32x4 wr[CW][NT];
+  int cb = c0;
+  int nc = min(CW, c1 - cb);
+#pragma unroll
+  for (int u = 0; u < CW; ++u)
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      if (c0 + u < cpre) pre[u][t] = __builtin_nontemporal_load((const u32x4*)(wb[t] + (long)(c0 + u) * 1024));
+      if (u < nc) wr[u][t] = ldw<NTL>(wb[t] + (long)(cb + u) * 1024);
 
+  // RMS statistics while the first weight group is in flight
+  __shared__ float s_inv[16];
+  __shared__ f16 s_nw[PRO == PRO_RMS ? NW_MAX : 8];
   float inv = 0.f;
   if (PRO == PRO_RMS) {
+    for (int k = threadIdx.x * 8; k < K; k += KW * 64 * 8) *(f16x8*)(s_nw + k) = ld8(a.nw + k);
     for (int mm = wv; mm < 16; mm += KW) {
       const int mr = m0 + mm;
       float ss = 0.f;
@@ -147,155 +272,68 @@ __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
     inv = s_inv[row];
   }
 
-  auto xfrag = [&](int c, f16x8& fa, f16x8& fb) {
-    if (PRO == PRO_EMBED) {
-      if (xp) {
-        fa = ld8(xp + (long)c * 64);
-        fb = ld8(xp + (long)c * 64 + 8);
-      } else if (ep) {
-        const u32x4 codes = *(const u32x4*)(ep + (long)c * 64);
-        i8x16_to_f16(codes, fa, fb);
-        fa = fa * esc;
-        fb = fb * esc;
-      } else {
-        fa = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        fb = fa;
-      }
-      return;
-    }
-    if (!mval) {
-      fa = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      fb = fa;
-      return;
-    }
-    fa = ld8(xp + (long)c * 64);
-    fb = ld8(xp + (long)c * 64 + 8);
-    if (PRO == PRO_RMS) {
-      const f16x8 wa = ld8(nwp + (long)c * 64);
-      const f16x8 wb2 = ld8(nwp + (long)c * 64 + 8);
+  while (nc > 0) {
+    // raw x fragments of the group
+    u32x4 xa[CW], xb[CW];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fa[e] = (f16)((float)fa[e] * inv) * wa[e];
-        fb[e] = (f16)((float)fb[e] * inv) * wb2[e];
-      }
-    }
-  };
-
-  f32x4 acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  auto step = [&](const u32x4 (&wr)[NT], const f16x8& fa, const f16x8& fb) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      f16x8 wa, wbv;
-      i8x16_to_f16(wr[t], wa, wbv);
-      if (dense) {
-        wa = wa * sw[t];
-        wbv = wbv * sw[t];
-      }
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wbv, fb, acc[t], 0, 0, 0);
-    }
-  };
-
-  // consume the prefetched chunks
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (c0 + u < cpre) {
-      f16x8 fa, fb;
-      xfrag(c0 + u, fa, fb);
-      step(pre[u], fa, fb);
-    }
-  }
-  int c = cpre;
-  for (; c + U <= c1; c += U) {
-    u32x4 wr[U][NT];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        wr[u][t] = __builtin_nontemporal_load((const u32x4*)(wb[t] + (long)(c + u) * 1024));
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      f16x8 fa, fb;
-      xfrag(c + u, fa, fb);
-      step(wr[u], fa, fb);
-    }
-  }
-  for (; c < c1; ++c) {
-    u32x4 wr[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) wr[t] = __builtin_nontemporal_load((const u32x4*)(wb[t] + (long)c * 1024));
-    f16x8 fa, fb;
-    xfrag(c, fa, fb);
-    step(wr, fa, fb);
-  }
-
-  // ---- epilogue on (tile t, lane l): rows n = nb .. nb + 3 of batch row me
-  auto epilogue = [&](int t, int l, const f32x4& acc4) {
-    const int me = m0 + (l & 15);
-    if (me >= M) return;
-    const int nb = n0 + 16 * t + 4 * (l >> 4);
-    if (nb >= N) return;
-    f16 yv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int n = min(nb + r, N - 1);
-      yv[r] = (f16)(dense ? acc4[r] : acc4[r] * (float)a.s[n]);
-    }
-    if (EPI == EPI_STORE) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = nb + r;
-        if (n < N) {
-          f16 o = yv[r];
-          if (a.res) o = o + a.res[(long)me * a.ldr + n];
-          a.y[(long)me * a.ldy + n] = o;
+    for (int u = 0; u < CW; ++u) {
+      if (u < nc) {
+        const long ko = (long)(cb + u) * 64;
+        if (PRO == PRO_EMBED && ep) {
+          xa[u] = *(const u32x4*)(ep + ko);
+        } else if (xp) {
+          xa[u] = *(const u32x4*)(xp + ko);
+          xb[u] = *(const u32x4*)(xp + ko + 8);
         }
       }
-    } else if (EPI == EPI_ROPE) {
-      // N = (Hq + 2Hk) * HD, HD % 4 == 0: the four columns sit in one head
-      const int HD = a.HD;
-      const int h = nb / HD, d = nb - h * HD;
-      const long p_raw = a.pos[me];
-      const int L = a.L;
-      const bool pval = p_raw >= 0 && p_raw < L;
-      const long p = p_raw < 0 ? 0 : (p_raw >= L ? L - 1 : p_raw);
-      f16x4 o;
-      if (h < a.Hq + a.Hk) {
-        const float* cs = a.rope + p * HD + d;  // (cos, sin) of pairs d/2 and d/2 + 1
-        const float c0f = cs[0], s0f = cs[1], c1f = cs[2], s1f = cs[3];
-        const float x0 = (float)yv[0], x1 = (float)yv[1], x2 = (float)yv[2], x3 = (float)yv[3];
-        o[0] = (f16)(x0 * c0f - x1 * s0f);
-        o[1] = (f16)(x1 * c0f + x0 * s0f);
-        o[2] = (f16)(x2 * c1f - x3 * s1f);
-        o[3] = (f16)(x3 * c1f + x2 * s1f);
-      } else {
-        o = (f16x4){yv[0], yv[1], yv[2], yv[3]};
-      }
-      if (h < a.Hq) {
-        *(f16x4*)(a.q + ((long)me * a.Hq + h) * HD + d) = o;
-      } else if (pval) {
-        const int b = me / a.S;
-        const int kh = h < a.Hq + a.Hk ? h - a.Hq : h - a.Hq - a.Hk;
-        f16* dst = h < a.Hq + a.Hk ? a.kc : a.vc;
-        *(f16x4*)(dst + (((long)b * a.Hk + kh) * L + p) * HD + d) = o;
-      }
-    } else {  // EPI_SILU: (a_j, b_j, a_j+1, b_j+1) with j = nb / 2
-      const int F = N >> 1;
-      const int j = nb >> 1;
-      f16x2 o;
-      const float a0 = (float)yv[0], a1 = (float)yv[2];
-      o.x = (f16)(a0 / (1.0f + expf(-a0))) * yv[1];
-      o.y = (f16)(a1 / (1.0f + expf(-a1))) * yv[3];
-      *(f16x2*)(a.mm + (long)me * F + j) = o;
     }
-  };
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      if (u < nc) {
+        f16x8 fa = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, fb = fa;
+        if (PRO == PRO_EMBED && ep) {
+          i8x16_to_f16(xa[u], fa, fb);
+          fa = fa * esc;
+          fb = fb * esc;
+        } else if (xp) {
+          fa = __builtin_bit_cast(f16x8, xa[u]);
+          fb = __builtin_bit_cast(f16x8, xb[u]);
+          if (PRO == PRO_RMS) {
+            const int k0 = (cb + u) * 64 + 16 * grp;
+            const f16x8 wa = *(const f16x8*)(s_nw + k0);
+            const f16x8 wb2 = *(const f16x8*)(s_nw + k0 + 8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              fa[e] = (f16)((float)fa[e] * inv) * wa[e];
+              fb[e] = (f16)((float)fb[e] * inv) * wb2[e];
+            }
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          f16x8 wa, wbv;
+          i8x16_to_f16(wr[u][t], wa, wbv);
+          if (dense) {
+            wa = wa * sw[t];
+            wbv = wbv * sw[t];
+          }
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wbv, fb, acc[t], 0, 0, 0);
+        }
+      }
+    }
+    cb += CW;
+    nc = min(CW, c1 - cb);
+#pragma unroll
+    for (int u = 0; u < CW; ++u)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (u < nc) wr[u][t] = ldw<NTL>(wb[t] + (long)(cb + u) * 1024);
+  }
 
   if constexpr (KW == 1) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) epilogue(t, lane, acc[t]);
+    for (int t = 0; t < NT; ++t) gemv_epilogue<EPI>(a, n0, m0, t, lane, acc[t], epi_prefetch<EPI>(a, n0, m0, t, lane));
   } else {
     __shared__ f32x4 red[KW][NT][64];
 #pragma unroll
@@ -306,8 +344,177 @@ __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
       f32x4 s4 = red[0][t][l];
 #pragma unroll
       for (int v = 1; v < KW; ++v) s4 += red[v][t][l];
-      epilogue(t, l, s4);
+      gemv_epilogue<EPI>(a, n0, m0, t, l, s4, pre_e);
     }
+  }
+}
+
+// LDS-staged variant: the block's x rows (after the prologue transform: RMSNorm or embedding
+// gather) are built once in LDS by one wave per row at kernel start, while the first weight
+// group is already in flight; the weight stream is then software-pipelined two groups deep and
+// the MFMA B fragments come from LDS.  Used whenever the x tile fits in LDS.
+constexpr int XPAD = 8;  // halfs of padding per LDS row (spreads rows over banks)
+
+template <int NT, int KW, int PRO, int EPI, int CW, bool NTL>
+__global__ __launch_bounds__(KW * 64) void gemv_xlds_kernel(const GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int tile0 = blockIdx.x * NT;
+  const int n0 = tile0 * 16;
+  const int m0 = blockIdx.y * 16;
+  const int K = a.K, M = a.M, N = a.N;
+  const int nch = K >> 6;
+  const int ntiles = (N + 15) >> 4;
+  const int c0 = (nch * wv) / KW;
+  const int c1 = (nch * (wv + 1)) / KW;
+  const bool dense = a.dense != 0;
+  const int mv = min(16, M - m0);
+  const int ldx = K + XPAD;
+  f16* xs = (f16*)smem;
+
+  const int8_t* wb[NT];
+  f16 sw[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int tile = min(tile0 + t, ntiles - 1);
+    wb[t] = a.wp + (long)tile * nch * 1024 + 16 * lane;
+    sw[t] = dense ? a.s[min(n0 + 16 * t + row, N - 1)] : (f16)0.0f;
+  }
+
+  const bool epi_thread = (int)threadIdx.x < NT * 64;
+  EpiPre pre_e;
+  if (epi_thread) pre_e = epi_prefetch<EPI>(a, n0, m0, threadIdx.x >> 6, threadIdx.x & 63);
+
+  u32x4 wA[CW][NT], wB[CW][NT];
+  auto issue = [&](u32x4 (&w)[CW][NT], int cb) {
+    const int nc = min(CW, c1 - cb);
+#pragma unroll
+    for (int u = 0; u < CW; ++u)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (u < nc) w[u][t] = ldw<NTL>(wb[t] + (long)(cb + u) * 1024);
+  };
+  if (c0 < c1) issue(wA, c0);
+
+  // ---- stage x rows: wave w builds rows w, w + KW, ...
+  for (int mr = wv; mr < mv; mr += KW) {
+    const int m = m0 + mr;
+    f16* dst = xs + (long)mr * ldx;
+    if (PRO == PRO_EMBED) {
+      const bool from_even = a.even && ((m & 1) == 0);
+      const int b = a.even ? (m >> 1) : m;
+      if (from_even) {
+        const f16* src = a.even + (long)b * K;
+        for (int k = lane * 8; k < K; k += 512) *(f16x8*)(dst + k) = ld8(src + k);
+      } else {
+        const long t = a.tok[(long)b * a.tok_stride];
+        const long r = t + (long)a.cb * a.vocab;
+        const bool ok = t >= 0 && t < a.vocab && r < a.erows;
+        const int8_t* src = a.etab + (ok ? r : 0) * K;
+        const f16 sc = ok ? a.escale[r] : (f16)0.0f;
+        for (int k = lane * 16; k < K; k += 1024) {
+          f16x8 lo = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, hi = lo;
+          if (ok) {
+            i8x16_to_f16(*(const u32x4*)(src + k), lo, hi);
+            lo = lo * sc;
+            hi = hi * sc;
+          }
+          *(f16x8*)(dst + k) = lo;
+          *(f16x8*)(dst + k + 8) = hi;
+        }
+      }
+    } else if (PRO == PRO_RMS) {
+      // K <= NW_MAX: the whole row stays in registers (8 halfs per lane per 512)
+      const f16* src = a.x + (long)m * a.ldx;
+      f16x8 v[NW_MAX / 512];
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NW_MAX / 512; ++i) {
+        const int k = lane * 8 + 512 * i;
+        if (k < K) {
+          v[i] = ld8(src + k);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += (float)v[i][e] * (float)v[i][e];
+        }
+      }
+      ss = wave_sum(ss);
+      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+      for (int i = 0; i < NW_MAX / 512; ++i) {
+        const int k = lane * 8 + 512 * i;
+        if (k < K) {
+          const f16x8 w = ld8(a.nw + k);
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (f16)((float)v[i][e] * inv) * w[e];
+          *(f16x8*)(dst + k) = o;
+        }
+      }
+    } else {
+      const f16* src = a.x + (long)m * a.ldx;
+      for (int k = lane * 8; k < K; k += 512) *(f16x8*)(dst + k) = ld8(src + k);
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const bool mval = row < mv;
+  const f16* xrow = xs + (long)row * ldx + 16 * grp;
+
+  auto compute = [&](const u32x4 (&w)[CW][NT], int cb) {
+    const int nc = min(CW, c1 - cb);
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      if (u < nc) {
+        f16x8 fa = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, fb = fa;
+        if (mval) {
+          fa = *(const f16x8*)(xrow + (cb + u) * 64);
+          fb = *(const f16x8*)(xrow + (cb + u) * 64 + 8);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          f16x8 wa, wbv;
+          i8x16_to_f16(w[u][t], wa, wbv);
+          if (dense) {
+            wa = wa * sw[t];
+            wbv = wbv * sw[t];
+          }
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wbv, fb, acc[t], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  for (int cb = c0; cb < c1;) {
+    int nb = cb + CW;
+    if (nb < c1) issue(wB, nb);
+    compute(wA, cb);
+    if (nb >= c1) break;
+    cb = nb;
+    nb = cb + CW;
+    if (nb < c1) issue(wA, nb);
+    compute(wB, cb);
+    cb = nb;
+  }
+
+  // ---- cross-wave reduction (LDS reused after the x tile is dead) and epilogue
+  __syncthreads();
+  f32x4* red = (f32x4*)smem;  // [KW][NT][64]
+#pragma unroll
+  for (int t = 0; t < NT; ++t) red[(wv * NT + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < NT * 64; idx += KW * 64) {
+    const int t = idx >> 6, l = idx & 63;
+    f32x4 s4 = red[t * 64 + l];
+#pragma unroll
+    for (int v = 1; v < KW; ++v) s4 += red[(v * NT + t) * 64 + l];
+    gemv_epilogue<EPI>(a, n0, m0, t, l, s4, pre_e);
   }
 }
 
@@ -336,33 +543,61 @@ struct Cfg {
   int nt, kw;
 };
 
+// Tile rule from a sweep of (tiles per block, waves per block, chunk group) over every frame
+// shape on MI355X: 16 waves splitting K with 2-chunk load groups always wins; more 16-row tiles
+// per block cut the re-read of x from L2 once there are enough tiles to keep 256 CUs busy.
 static Cfg pick(int N, int K) {
   const int ntiles = (N + 15) / 16;
-  const int nch = K / 64;
-  Cfg c{1, 8};
-  if (nch >= 128) c.kw = 16;
-  else if (nch <= 16) c.kw = 4;
-  if (ntiles >= 768 && nch >= 16) c.nt = 2;
+  (void)K;
+  Cfg c{1, 16};
+  if (ntiles >= 512) c = Cfg{4, 8};
+  else if (ntiles >= 320) c.nt = 2;
   return c;
+}
+
+constexpr int LDS_MAX = 160 * 1024;
+
+template <int NT, int KW, int PRO, int EPI, bool NTL>
+static int launch_one(const GemvArgs& a, hipStream_t st) {
+  const int ntiles = (a.N + 15) / 16;
+  dim3 grid((ntiles + NT - 1) / NT, (a.M + 15) / 16);
+  const long xbytes = (long)min(16, a.M) * (a.K + XPAD) * 2;
+  const long rbytes = (long)KW * NT * 64 * 16;
+  const long lds = xbytes > rbytes ? xbytes : rbytes;
+  if (lds <= LDS_MAX && (PRO != PRO_RMS || a.K <= NW_MAX)) {
+    static bool attr = false;  // raise the dynamic LDS limit once per instantiation
+    if (!attr) {
+      const hipError_t e = hipFuncSetAttribute((const void*)gemv_xlds_kernel<NT, KW, PRO, EPI, 2, NTL>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, LDS_MAX);
+      if (e != hipSuccess) return (int)e;
+      attr = true;
+    }
+    hipLaunchKernelGGL((gemv_xlds_kernel<NT, KW, PRO, EPI, 2, NTL>), grid, dim3(KW * 64),
+                       (unsigned)lds, st, a);
+  } else {
+    hipLaunchKernelGGL((gemv_fused_kernel<NT, KW, PRO, EPI, 2, NTL>), grid, dim3(KW * 64), 0, st, a);
+  }
+  return ecd_launch_status();
+}
+
+template <int PRO, int EPI, bool NTL>
+static int launch_ntl(const GemvArgs& a, Cfg c, hipStream_t st) {
+#define ECD_FCASE(NT_, KW_) \
+  if (c.nt == NT_ && c.kw == KW_) return launch_one<NT_, KW_, PRO, EPI, NTL>(a, st);
+  ECD_FCASE(1, 8)
+  ECD_FCASE(1, 16)
+  ECD_FCASE(2, 8)
+  ECD_FCASE(2, 16)
+  ECD_FCASE(4, 8)
+  ECD_FCASE(4, 16)
+#undef ECD_FCASE
+  return ECD_ENOTSUP;
 }
 
 template <int PRO, int EPI>
 static int launch(const GemvArgs& a, Cfg c, hipStream_t st) {
-  const int ntiles = (a.N + 15) / 16;
-#define ECD_FCASE(NT_, KW_)                                                                      \
-  if (c.nt == NT_ && c.kw == KW_) {                                                              \
-    dim3 grid((ntiles + NT_ - 1) / NT_, (a.M + 15) / 16);                                        \
-    hipLaunchKernelGGL((gemv_fused_kernel<NT_, KW_, PRO, EPI, 4>), grid, dim3(KW_ * 64), 0, st, a); \
-    return ecd_launch_status();                                                                  \
-  }
-  ECD_FCASE(1, 4)
-  ECD_FCASE(1, 8)
-  ECD_FCASE(1, 16)
-  ECD_FCASE(2, 4)
-  ECD_FCASE(2, 8)
-  ECD_FCASE(2, 16)
-#undef ECD_FCASE
-  return ECD_ENOTSUP;
+  if (PRO == PRO_RMS && a.K > NW_MAX) return ECD_ENOTSUP;
+  return a.stream_hint ? launch_ntl<PRO, EPI, true>(a, c, st) : launch_ntl<PRO, EPI, false>(a, c, st);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -392,10 +627,10 @@ static int check_common(const GemvArgs& a) {
 }
 
 int ecd_gemv_i8p(const void* x, long ldx, const void* wp, const void* s, const void* res, long ldr,
-                 void* y, long ldy, int M, int N, int K, int dense, int nt, int kw, void* stream) {
+                 void* y, long ldy, int M, int N, int K, int flags, int nt, int kw, void* stream) {
   GemvArgs a = {};
   a.x = (const f16*)x; a.ldx = ldx; a.wp = (const int8_t*)wp; a.s = (const f16*)s;
-  a.M = M; a.N = N; a.K = K; a.dense = dense;
+  a.M = M; a.N = N; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1;
   a.res = (const f16*)res; a.ldr = ldr; a.y = (f16*)y; a.ldy = ldy;
   if (check_common(a) || !x || !y || ldx < K || (ldx % 8) || !aligned16(x) || ldy < N ||
       (res && ldr < N))
@@ -407,11 +642,11 @@ int ecd_gemv_i8p(const void* x, long ldx, const void* wp, const void* s, const v
 }
 
 int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const void* wp,
-                     const void* s, void* y, long ldy, int M, int N, int K, int dense,
+                     const void* s, void* y, long ldy, int M, int N, int K, int flags,
                      void* stream) {
   GemvArgs a = {};
   a.x = (const f16*)x; a.ldx = ldx; a.nw = (const f16*)nw; a.eps = eps;
-  a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.N = N; a.K = K; a.dense = dense;
+  a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.N = N; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1;
   a.y = (f16*)y; a.ldy = ldy;
   if (check_common(a) || !x || !nw || !y || ldx < K || (ldx % 8) || !aligned16(x) ||
       !aligned16(nw) || ldy < N)
@@ -421,11 +656,11 @@ int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const v
 
 int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const void* wp,
                      const void* s, const float* rope, const int64_t* pos, void* q, void* kc,
-                     void* vc, int M, int S, int Hq, int Hk, int L, int HD, int K, int dense,
+                     void* vc, int M, int S, int Hq, int Hk, int L, int HD, int K, int flags,
                      void* stream) {
   GemvArgs a = {};
   a.x = (const f16*)x; a.ldx = ldx; a.nw = (const f16*)nw; a.eps = eps;
-  a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.K = K; a.dense = dense;
+  a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1;
   a.N = (Hq + 2 * Hk) * HD;
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
@@ -437,11 +672,11 @@ int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const v
 }
 
 int ecd_rms_w13_silu(const void* x, long ldx, const void* nw, float eps, const void* wp,
-                     const void* s, void* mm, int M, int F, int K, int dense, void* stream) {
+                     const void* s, void* mm, int M, int F, int K, int flags, void* stream) {
   GemvArgs a = {};
   a.x = (const f16*)x; a.ldx = ldx; a.nw = (const f16*)nw; a.eps = eps;
   a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.N = 2 * F; a.K = K;
-  a.dense = dense; a.mm = (f16*)mm;
+  a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1; a.mm = (f16*)mm;
   if (check_common(a) || !x || !nw || !mm || F <= 0 || (F % 2) || ldx < K || (ldx % 8) ||
       !aligned16(x) || !aligned16(nw))
     return ECD_EINVAL;
@@ -450,13 +685,13 @@ int ecd_rms_w13_silu(const void* x, long ldx, const void* nw, float eps, const v
 
 int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, const void* tscale,
                        long trows, int cb, int vocab, const void* even, const void* wp,
-                       const void* s, void* y, long ldy, int M, int N, int K, int dense,
+                       const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream) {
   GemvArgs a = {};
   a.tok = tok; a.tok_stride = tok_stride; a.etab = (const int8_t*)table;
   a.escale = (const f16*)tscale; a.erows = trows; a.cb = cb; a.vocab = vocab;
   a.even = (const f16*)even; a.wp = (const int8_t*)wp; a.s = (const f16*)s;
-  a.M = M; a.N = N; a.K = K; a.dense = dense; a.y = (f16*)y; a.ldy = ldy;
+  a.M = M; a.N = N; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1; a.y = (f16*)y; a.ldy = ldy;
   if (check_common(a) || !tok || !table || !tscale || !y || tok_stride <= 0 || trows <= 0 ||
       cb < 0 || vocab <= 0 || ldy < N || !aligned16(table) || (even && !aligned16(even)) ||
       (even && (M & 1)))

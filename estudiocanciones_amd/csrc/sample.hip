@@ -121,9 +121,28 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     if (tid < 256) hist[tid] = 0u;
     __syncthreads();
     const uint32_t prefix = sel[0];
-    for (int i = tid; i < V; i += SMP_THREADS) {
-      const uint32_t k = fkey(xs[i]);
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    for (int base = 0; base < V; base += SMP_THREADS) {
+      const int i = base + tid;
+      bool act = false;
+      uint32_t dg = 0u;
+      if (i < V) {
+        const uint32_t k = fkey(xs[i]);
+        act = (k & mask) == prefix;
+        dg = (k >> shift) & 255u;
+      }
+      // few distinct digits dominate (the top byte of the keys especially): count up to four
+      // of them per wave with one LDS atomic each, the rest with per-lane atomics
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const uint64_t pend = __ballot(act);
+        if (pend == 0) break;
+        const int leader = __ffsll((unsigned long long)pend) - 1;
+        const uint32_t d0 = __shfl(dg, leader, 64);
+        const uint64_t same = __ballot(act && dg == d0);
+        if ((tid & 63) == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
+        if (dg == d0) act = false;
+      }
+      if (act) atomicAdd(&hist[dg], 1u);
     }
     __syncthreads();
     if (tid < 64) {
@@ -173,15 +192,15 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   for (int i = tid; i < V; i += SMP_THREADS) sloc += expf(xs[i] - m1);
   const float s1 = block_reduce_sum(sloc, red);
   const float logsum = logf(s1);
-  float m2loc = -INFINITY;
-  for (int i = tid; i < V; i += SMP_THREADS) {
-    const float ls = xs[i] - m1 - logsum;
-    xs[i] = ls;
-    m2loc = fmaxf(m2loc, ls);
-  }
-  const float m2 = block_reduce_max(m2loc, red);
+  // log_softmax: ls = (x - m1) - logsum; its maximum is exactly -logsum (at x = m1, where
+  // (m1 - m1) - logsum is exact), so the second softmax needs no max reduction
+  const float m2 = 0.f - logsum;
   float s2loc = 0.f;
-  for (int i = tid; i < V; i += SMP_THREADS) s2loc += expf(xs[i] - m2);
+  for (int i = tid; i < V; i += SMP_THREADS) {
+    const float ls = (xs[i] - m1) - logsum;
+    xs[i] = ls;
+    s2loc += expf(ls - m2);
+  }
   const float s2 = block_reduce_sum(s2loc, red);
 
   // 4. exponential race

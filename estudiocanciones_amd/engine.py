@@ -28,8 +28,8 @@ import torch
 
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
-                      gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms, rms_qkv_rope,
-                      rms_w13_silu, sample_topk, stream_ptr)
+                      gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms,
+                      rms_gemv_packed, rms_qkv_rope, rms_w13_silu, sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
 N_CB = 8
@@ -66,10 +66,13 @@ class Linear:
         self.w, self.q8, self.s8 = None, q8, s8
         self.qp = self.sp = None
         self.N, self.K = q8.shape
+        self.stream = False
 
-    def pack(self, interleave=False):
+    def pack(self, interleave=False, stream=False):
         """Add the lane-ordered tile copy used by the fused GEMVs (K % 64 == 0).  With
-        ``interleave`` the w1 | w3 halves become (a_j, b_j) row pairs (scales likewise)."""
+        ``interleave`` the w1 | w3 halves become (a_j, b_j) row pairs (scales likewise).
+        ``stream``: the layer is read once per frame, so its loads bypass cache allocation."""
+        self.stream = stream
         if self.K % 64:
             return self
         self.qp = pack_i8(self.q8, interleave)
@@ -83,7 +86,7 @@ class Linear:
     def __call__(self, x, res=None):
         if self.qp is not None and self.sp is self.s8 and x.dim() == 2 and x.stride(1) == 1 \
                 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0:
-            return gemv_packed(x, self.qp, self.s8, self.N, self.K, res)
+            return gemv_packed(x, self.qp, self.s8, self.N, self.K, res, stream=self.stream)
         return int8_mm(x, self.q8, self.s8, res)
 
     @property
@@ -194,25 +197,29 @@ class Stack:
         h = self.decode(x.reshape(B * S, D), pos.reshape(B * S).to(torch.int64).contiguous(), S)
         return h.reshape(B, S, D)
 
-    def decode(self, x, pos, S):
+    def decode(self, x, pos, S, final_norm=True):
         """Fast path for few rows (app/engine.py:180-211): x [R, D] with R = B*S (row r -> batch
         r // S), pos [R] absolute positions; row r attends [0, pos[r]].
 
         Per layer: rms+qkv+RoPE/KV write (one kernel), attention (+ split combine),
-        O projection + residual, rms+w1|w3+SiLU*mul (one kernel), w2 + residual."""
+        O projection + residual, rms+w1|w3+SiLU*mul (one kernel), w2 + residual.
+        ``final_norm=False`` returns the residual stream before the stack's last RMSNorm, for a
+        consumer that fuses that norm into its own GEMV (the codebook heads)."""
         if any(b.qkv.qp is None for b in self.blocks):
-            return self.decode_reference(x, pos, S)
+            h = self.decode_reference(x, pos, S)
+            return h if final_norm else None
         R = x.shape[0]
         ns = self.nsplit
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
-            rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L, HD)
+            rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L, HD,
+                         stream=b.qkv.stream)
             o = self._attention(b, q, pos, S, ns)
             x = b.o(o, res=x)
-            mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2)
+            mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2, stream=b.w13.stream)
             x = b.w2(mm, res=x)
-        return krms(x, self.norm)
+        return krms(x, self.norm) if final_norm else x
 
     def _attention(self, b, q, pos, S, ns):
         R = q.shape[0]
@@ -311,19 +318,22 @@ class HeartMuLaLite:
         self.bb_cfg, self.dec_cfg = dict(backbone), dict(decoder)
         self.backbone = Stack(p, "backbone", backbone)
         self.decoder = Stack(p, "decoder", decoder)
-        for st in (self.backbone, self.decoder):
+        # the backbone (2.8 GB at the 3B shape) is streamed once per frame; the depth decoder is
+        # re-read by 7 passes per frame, so its loads stay cacheable (256 MB Infinity Cache)
+        for st, streamed in ((self.backbone, True), (self.decoder, False)):
             for b in st.blocks:
-                b.qkv.pack()
-                b.o.pack()
-                b.w13.pack(interleave=True)
-                b.w2.pack()
+                b.qkv.pack(stream=streamed)
+                b.o.pack(stream=streamed)
+                b.w13.pack(interleave=True, stream=streamed)
+                b.w2.pack(stream=streamed)
         self.text_emb = emb("text_embeddings.weight")
         self.audio_emb = emb("audio_embeddings.weight")
         self.uncond = f.get("unconditional_text_embedding.weight").to(dtype)
         self.projection = p("projection.weight")
         self.c0_head = p("codebook0_head.weight")
         self.audio_head = [p(f"audio_head.{i}") for i in range(N_CB - 1)]
-        for lin in [self.projection, self.c0_head, *self.audio_head]:
+        self.c0_head.pack(stream=True)
+        for lin in [self.projection, *self.audio_head]:
             lin.pack()
         self.muq_b = f.get("muq_linear.bias").to(dtype)
         self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
@@ -381,12 +391,27 @@ class HeartMuLaLite:
 
         c0 = pick(0, self.c0_head(last_h))
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
-        h = self.decoder.decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
+        h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
-            ci = pick(i, self.audio_head[i - 1](h))
+            ci = pick(i, self._head(i - 1, h))
             if i < N_CB - 1:
-                h = self.decoder.decode(self._project(ci, i), self._dpos[i], 1)
+                h = self._decode(self._project(ci, i), self._dpos[i], 1)
         return samples
+
+    def _decode(self, x, pos, S):
+        """Decoder pass; with packed heads the stack's final RMSNorm is left to the head GEMV."""
+        if self.audio_head[0].qp is not None and self.decoder.blocks and \
+                self.decoder.blocks[0].qkv.qp is not None:
+            return self.decoder.decode(x, pos, S, final_norm=False)
+        return self.decoder.decode(x, pos, S)
+
+    def _head(self, i, h):
+        """audio_head[i](decoder.norm(h)) -- norm fused into the head GEMV when packed."""
+        hd = self.audio_head[i]
+        if hd.qp is not None and self.decoder.blocks and self.decoder.blocks[0].qkv.qp is not None:
+            return rms_gemv_packed(h, self.decoder.norm, hd.qp, hd.s8, hd.N, hd.K,
+                                   stream=hd.stream)
+        return hd(h)
 
     def _project(self, tok, cb, even=None):
         """projection(_embed_audio(cb, tok)) -- with ``even`` the interleave (even[b], emb[b]) --

@@ -276,8 +276,13 @@ def _check_x(x, K, name):
         raise ValueError(f"{name}: x must be [M, {K}] fp16 with unit inner stride, 16-byte rows")
 
 
-def gemv_packed(x, wp, s, N, K, res=None, out=None):
-    """y = int8_mm(x, w, s, res) on packed weights (same numerics)."""
+def _flags(M, stream):
+    return int(M > 16) | (2 if stream else 0)
+
+
+def gemv_packed(x, wp, s, N, K, res=None, out=None, stream=False):
+    """y = int8_mm(x, w, s, res) on packed weights (same numerics).  ``stream``: the weights are
+    read once per frame (nontemporal loads)."""
     _check_x(x, K, "gemv_packed")
     M = x.shape[0]
     y = out if out is not None else torch.empty(M, N, device=x.device, dtype=torch.float16)
@@ -287,21 +292,21 @@ def gemv_packed(x, wp, s, N, K, res=None, out=None):
             raise ValueError("gemv_packed: res must be [M, N] with unit inner stride")
     _ffi.call("ecd_gemv_i8p", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(), _ptr(res),
               res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0), M, N, K,
-              int(M > 16), 0, 0, stream_ptr(x.device))
+              _flags(M, stream), 0, 0, stream_ptr(x.device))
     return y
 
 
-def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5):
+def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5, stream=False):
     """int8_mm(rms(x, nw), w, s) in one kernel."""
     _check_x(x, K, "rms_gemv_packed")
     M = x.shape[0]
     y = torch.empty(M, N, device=x.device, dtype=torch.float16)
     _ffi.call("ecd_rms_gemv_i8p", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
-              s.data_ptr(), y.data_ptr(), N, M, N, K, int(M > 16), stream_ptr(x.device))
+              s.data_ptr(), y.data_ptr(), N, M, N, K, _flags(M, stream), stream_ptr(x.device))
     return y
 
 
-def rms_qkv_rope(x, nw, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, eps=1e-5):
+def rms_qkv_rope(x, nw, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, eps=1e-5, stream=False):
     """rms -> fused q|k|v GEMV -> RoPE of q and k -> q out, k/v into the cache at pos (one kernel)."""
     K = x.shape[1]
     _check_x(x, K, "rms_qkv_rope")
@@ -316,21 +321,21 @@ def rms_qkv_rope(x, nw, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, eps=1e-5)
         raise ValueError("rms_qkv_rope: q/kc/vc must be contiguous")
     _ffi.call("ecd_rms_qkv_rope", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
               s.data_ptr(), rope.data_ptr(), pos.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-              M, S, Hq, Hk, L, HD, K, int(M > 16), stream_ptr(x.device))
+              M, S, Hq, Hk, L, HD, K, _flags(M, stream), stream_ptr(x.device))
 
 
-def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5):
+def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5, stream=False):
     """rms -> [w1 | w3] GEMV on row-interleaved packed weights -> fp16(silu(a)) * b, [M, F]."""
     K = x.shape[1]
     _check_x(x, K, "rms_w13_silu")
     M = x.shape[0]
     mm = torch.empty(M, F, device=x.device, dtype=torch.float16)
     _ffi.call("ecd_rms_w13_silu", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
-              s_il.data_ptr(), mm.data_ptr(), M, F, K, int(M > 16), stream_ptr(x.device))
+              s_il.data_ptr(), mm.data_ptr(), M, F, K, _flags(M, stream), stream_ptr(x.device))
     return mm
 
 
-def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None):
+def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False):
     """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
     interleave (even[b], emb[b]) and the output has 2B rows."""
     dev = _dev(tok, "embed_gemv_packed")
@@ -346,5 +351,5 @@ def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None):
     y = torch.empty(M, N, device=dev, dtype=torch.float16)
     _ffi.call("ecd_embed_gemv_i8p", tok.data_ptr(), tok.stride(0), table.data_ptr(), tscale.data_ptr(),
               table.shape[0], int(cb), int(vocab), _ptr(even), wp.data_ptr(), s.data_ptr(),
-              y.data_ptr(), N, M, N, K, int(M > 16), stream_ptr(dev))
+              y.data_ptr(), N, M, N, K, _flags(M, stream), stream_ptr(dev))
     return y

@@ -122,7 +122,9 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
 /* ---- packed-weight fused GEMVs (the engine's per-layer kernels) ----------------------------
  * Packed layout: [ceil(N/16)] tiles x [K/64] chunks x 1 KB, chunk bytes [16l, 16l+16) holding
  * row 16*tile + (l & 15), bytes 64c + 16(l >> 4) .. +15 (zero rows beyond N).  K % 64 == 0.
- * Every fused variant keeps the numerics of ecd_gemv_i8 (dense = 0/1 as there). */
+ * Every fused variant keeps the numerics of ecd_gemv_i8.  `flags`: bit 0 = dense numerics (the
+ * M > 16 path of ecd_gemv_i8), bit 1 = the weights are streamed once (nontemporal loads; leave
+ * it clear for weights re-read soon, e.g. the depth decoder's 7 passes, so they stay cached). */
 
 /* Size in bytes of the packed copy of an [N, K] matrix.  No reference counterpart. */
 long ecd_packed_bytes(int N, int K);
@@ -134,12 +136,12 @@ int ecd_pack_i8(const void* w, int N, int K, int interleave, void* out, void* st
 
 /* int8_mm (app/kernels.py:40-54) on packed weights; nt/kw as in ecd_gemv_i8_tuned. */
 int ecd_gemv_i8p(const void* x, long ldx, const void* wp, const void* s, const void* res, long ldr,
-                 void* y, long ldy, int M, int N, int K, int dense, int nt, int kw, void* stream);
+                 void* y, long ldy, int M, int N, int K, int flags, int nt, int kw, void* stream);
 
 /* y = int8_mm(rms(x, nw, eps), w, s): rms (app/kernels.py:58-74) fused as the GEMV prologue
  * -- the final norm + head of Stack.decode / _frame_fast (app/engine.py:211, :333, :339). */
 int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const void* wp,
-                     const void* s, void* y, long ldy, int M, int N, int K, int dense,
+                     const void* s, void* y, long ldy, int M, int N, int K, int flags,
                      void* stream);
 
 /* rms -> q|k|v GEMV -> RoPE -> q [M, Hq*HD] and k/v into kc/vc [B, Hk, L, HD] at pos[m]
@@ -147,13 +149,13 @@ int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const v
  * N = (Hq + 2Hk) * HD, HD % 4 == 0; rope [>= L, HD/2, 2] f32. */
 int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const void* wp,
                      const void* s, const float* rope, const int64_t* pos, void* q, void* kc,
-                     void* vc, int M, int S, int Hq, int Hk, int L, int HD, int K, int dense,
+                     void* vc, int M, int S, int Hq, int Hk, int L, int HD, int K, int flags,
                      void* stream);
 
 /* rms -> [w1 | w3] GEMV on interleaved packed rows (scales interleaved the same way) ->
  * mm [M, F] = f16(f16(silu(a)) * b): app/engine.py:206-209 (krms, b.w13, _silu_mul). */
 int ecd_rms_w13_silu(const void* x, long ldx, const void* nw, float eps, const void* wp,
-                     const void* s, void* mm, int M, int F, int K, int dense, void* stream);
+                     const void* s, void* mm, int M, int F, int K, int flags, void* stream);
 
 /* y = int8_mm(E, w, s) where row m of E is the int8 embedding of tok[m * tok_stride] + cb * vocab
  * (table [trows, K] int8, tscale [trows] f16); with even != NULL (M even) row 2b of E is
@@ -161,7 +163,7 @@ int ecd_rms_w13_silu(const void* x, long ldx, const void* nw, float eps, const v
  * projection(_embed_audio(...)) and the pass-0 stack of app/engine.py:336-342. */
 int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, const void* tscale,
                        long trows, int cb, int vocab, const void* even, const void* wp,
-                       const void* s, void* y, long ldy, int M, int N, int K, int dense,
+                       const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream);
 
 /* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
