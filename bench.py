@@ -50,18 +50,28 @@ def attn_bytes(R, Hq, Hk, HD, lens):
     return sum(Hk * ln * HD * 4 for ln in lens) + 4 * R * Hq * HD
 
 
-def time_launch_sequence(calls, torch):
-    """hipEvent pairs around each recorded launch, replayed eagerly on the current stream
-    behind a GPU spin so the queue never drains; returns per-launch milliseconds."""
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
+def time_graph(calls, torch, reps=20):
+    """Capture `calls` into one hipGraph, replay it `reps` times between two hipEvents on the
+    stream the kernels run on, and return the mean milliseconds per launch."""
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in calls:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        for f in calls:
+            f()
+    g.replay()
     torch.cuda.synchronize()
-    torch.cuda._sleep(50_000_000)
-    for (a, b), fn in zip(ev, calls):
-        a.record()
-        fn()
-        b.record()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
     torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in ev]
+    return e0.elapsed_time(e1) / reps / len(calls)
 
 
 def main():
@@ -168,19 +178,21 @@ def main():
     attn_calls = [(n, a) for n, a in calls if n == "ecd_decode_attn"]
     gemv_b = [b for _, _, b in gemv_calls]
     attn_b = [sum(Hk * ln * HD * 4 for ln in lens) + 4 * R * Hq * HD for lens, R, Hq, Hk, HD in attn_lens]
-    reps = 3
-    g_ms = [0.0] * len(gemv_calls)
-    a_ms = [0.0] * len(attn_calls)
-    for _ in range(reps):
-        ts = time_launch_sequence([lambda n=n, a=a: orig_call(n, *a) for n, a, _ in gemv_calls], torch)
-        g_ms = [x + t / reps for x, t in zip(g_ms, ts)]
-        ts = time_launch_sequence([lambda n=n, a=a: orig_call(n, *a) for n, a in attn_calls], torch)
-        a_ms = [x + t / reps for x, t in zip(a_ms, ts)]
-    g_avg_us = sum(g_ms) / len(g_ms) * 1e3
+    def relaunch(name, a):
+        # the recorded stream handle is replaced by the stream current at replay (capture) time
+        return lambda: orig_call(name, *a[:-1], torch.cuda.current_stream().cuda_stream)
+
+    g_ms_launch = time_graph([relaunch(n, a) for n, a, _ in gemv_calls], torch)
+    g_ms_total = g_ms_launch * len(gemv_calls)
+    bb_idx = [i for i, b in enumerate(attn_b) if b > 10e6]
+    a_ms_launch = time_graph([relaunch(*attn_calls[i]) for i in range(len(attn_calls))], torch)
+    a_ms_total = a_ms_launch * len(attn_calls)
+    bb_ms = time_graph([relaunch(*attn_calls[i]) for i in bb_idx], torch) if bb_idx else None
+    g_avg_us = g_ms_launch * 1e3
     g_bytes_avg = sum(gemv_b) / len(gemv_b)
-    g_gbps = sum(gemv_b) / (sum(g_ms) * 1e-3) / 1e9
-    a_gbps = sum(attn_b) / (sum(a_ms) * 1e-3) / 1e9
-    bb_attn = [(b, t) for b, t in zip(attn_b, a_ms) if b > 10e6]
+    g_gbps = sum(gemv_b) / (g_ms_total * 1e-3) / 1e9
+    a_gbps = sum(attn_b) / (a_ms_total * 1e-3) / 1e9
+    bb_attn_gbps = (sum(attn_b[i] for i in bb_idx) / (bb_ms * len(bb_idx) * 1e-3) / 1e9) if bb_idx else None
     frame_bytes = sum(gemv_b) + sum(attn_b)
     launches = len(calls)
 
@@ -222,16 +234,16 @@ def main():
         "decode_attn": {
             "achieved_GBps": round(a_gbps, 1),
             "frac": round(a_gbps / HBM_PEAK_GBPS, 4),
-            "backbone_layer_GBps": round(sum(b for b, _ in bb_attn) / (sum(t for _, t in bb_attn) * 1e-3) / 1e9, 1)
-            if bb_attn else None,
+            "backbone_layer_GBps": round(bb_attn_gbps, 1) if bb_attn_gbps else None,
+            "avg_launch_us": round(a_ms_launch * 1e3, 3),
             "launches_per_frame": len(attn_b),
         },
         "frame": {
             "algorithmic_bytes": int(frame_bytes),
             "effective_GBps": round(frame_bytes * fps / 1e9, 1),
             "frac_of_hbm": round(frame_bytes * fps / 1e9 / HBM_PEAK_GBPS, 4),
-            "kernel_time_gemv_ms": round(sum(g_ms), 4),
-            "kernel_time_attn_ms": round(sum(a_ms), 4),
+            "kernel_time_gemv_ms": round(g_ms_total, 4),
+            "kernel_time_attn_ms": round(a_ms_total, 4),
             "library_launches": launches,
         },
         "setup_s": round(t_build, 1),
@@ -287,7 +299,7 @@ def cpu_baseline(bb, dec, B, kv, budget_s):
     tm = dict(bb=0.0, dec=0.0, heads=0.0)
     n = 0
     t_start = time.perf_counter()
-    while n < 2 or (time.perf_counter() - t_start < budget_s and n < 50):
+    while n < 2 or (time.perf_counter() - t_start < budget_s and n < 5000):
         t = time.perf_counter()
         sb.decode(xb, pos_b)
         tm["bb"] += time.perf_counter() - t

@@ -81,133 +81,140 @@ __device__ __forceinline__ float block_reduce_sum(float v, float* red) {
   return r;
 }
 
+// Order-preserving 16-bit key of an fp16 value (-0.0 must be canonicalised to +0.0 first so
+// that key order equals float comparison).
+__device__ __forceinline__ uint32_t hkey(f16 h) {
+  const uint32_t u = __builtin_bit_cast(uint16_t, h);
+  return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+}
+
+constexpr int SMP_PER = (SMP_MAXV + SMP_THREADS - 1) / SMP_THREADS;  // values per thread
+
+// Digit d (from the top) of the radix select: the largest digit whose cumulative count from
+// the top reaches `rank`.  Run by wave 0 over 256 bins; writes (prefix | d << shift, new rank).
+__device__ __forceinline__ void radix_pick(const uint32_t* hist, uint32_t* sel, uint32_t prefix,
+                                           int shift, int lane) {
+  const uint32_t rank = sel[1];
+  uint32_t c4 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c4 += hist[255 - (lane * 4 + j)];
+  uint32_t incl = c4;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  const uint32_t excl = incl - c4;
+  if (excl < rank && incl >= rank) {
+    uint32_t acc = excl;
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t d = 255 - (lane * 4 + j);
+      const uint32_t h = hist[d];
+      if (acc + h >= rank) {
+        sel[0] = prefix | (d << shift);
+        sel[1] = rank - acc;
+        break;
+      }
+      acc += h;
+    }
+  }
+}
+
 __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
     const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
-  __shared__ float xs[SMP_MAXV];
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[2][256];
   __shared__ float red[SMP_THREADS / 64];
-  __shared__ uint32_t sel[2];  // selected prefix, remaining rank
+  __shared__ uint32_t sel[2];  // selected key prefix, remaining rank
   __shared__ float bestv[SMP_THREADS / 64];
   __shared__ int besti[SMP_THREADS / 64];
 
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const f16* lc = logits + (long)n * ld;
   const f16* lu = logits + (long)(n + N) * ld;
 
-  // 1. CFG mix in fp16, temperature in fp32
-  for (int i = tid; i < V; i += SMP_THREADS) {
-    f16 l = lc[i];
-    if (cfg_on) {
-      const f16 u = lu[i];
-      const f16 d = l - u;
-      const f16 e = (f16)((float)d * cfg);
-      l = u + e;
+  // 1. CFG mix in fp16 (values stay in registers: thread tid owns indices tid + 1024 j)
+  f16 lv[SMP_PER];
+  uint32_t key[SMP_PER];
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) {
+    const int i = tid + SMP_THREADS * j;
+    key[j] = 0u;
+    lv[j] = (f16)0.0f;
+    if (i < V) {
+      f16 l = lc[i];
+      if (cfg_on) {
+        const f16 u = lu[i];
+        const f16 d = l - u;
+        const f16 e = (f16)((float)d * cfg);
+        l = u + e;
+      }
+      l = l + (f16)0.0f;  // -0.0 -> +0.0
+      lv[j] = l;
+      key[j] = hkey(l);
     }
-    xs[i] = (float)l / temp;
   }
-  __syncthreads();
-
-  // 2. exact k-th largest value by radix select on the keys
+  if (tid < 256) {
+    hist[0][tid] = 0u;
+    hist[1][tid] = 0u;
+  }
   if (tid == 0) {
     sel[0] = 0u;
     sel[1] = (uint32_t)topk;
   }
-  uint32_t mask = 0u;
-#pragma unroll 1
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if (tid < 256) hist[tid] = 0u;
-    __syncthreads();
-    const uint32_t prefix = sel[0];
-    for (int base = 0; base < V; base += SMP_THREADS) {
-      const int i = base + tid;
-      bool act = false;
-      uint32_t dg = 0u;
-      if (i < V) {
-        const uint32_t k = fkey(xs[i]);
-        act = (k & mask) == prefix;
-        dg = (k >> shift) & 255u;
-      }
-      // few distinct digits dominate (the top byte of the keys especially): count up to four
-      // of them per wave with one LDS atomic each, the rest with per-lane atomics
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const uint64_t pend = __ballot(act);
-        if (pend == 0) break;
-        const int leader = __ffsll((unsigned long long)pend) - 1;
-        const uint32_t d0 = __shfl(dg, leader, 64);
-        const uint64_t same = __ballot(act && dg == d0);
-        if ((tid & 63) == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
-        if (dg == d0) act = false;
-      }
-      if (act) atomicAdd(&hist[dg], 1u);
-    }
-    __syncthreads();
-    if (tid < 64) {
-      // find the digit (from the top) where the cumulative count reaches the rank
-      const uint32_t rank = sel[1];
-      // each lane sums 4 bins, counting down from digit 255
-      uint32_t c4 = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c4 += hist[255 - (tid * 4 + j)];
-      // inclusive prefix over lanes (lane 0 = highest digits)
-      uint32_t incl = c4;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(incl, o, 64);
-        if (tid >= o) incl += t;
-      }
-      const uint32_t excl = incl - c4;
-      if (excl < rank && incl >= rank) {
-        uint32_t acc = excl;
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t d = 255 - (tid * 4 + j);
-          const uint32_t h = hist[d];
-          if (acc + h >= rank) {
-            sel[0] = prefix | (d << shift);
-            sel[1] = rank - acc;
-            break;
-          }
-          acc += h;
-        }
-      }
-    }
-    __syncthreads();
-    mask |= 255u << shift;
-  }
-  const float thr = keyf(sel[0]);
+  __syncthreads();
 
-  // 3. mask below the threshold; log_softmax then softmax, fp32
+  // 2. k-th largest fp16 value by a two-pass radix select on the 16-bit keys.  x = fp32(l)/temp
+  //    is strictly monotonic in l, so the threshold and the ties of the reference's fp32 topk
+  //    are those of l.
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j)
+    if (tid + SMP_THREADS * j < V) atomicAdd(&hist[0][key[j] >> 8], 1u);
+  __syncthreads();
+  if (tid < 64) radix_pick(hist[0], sel, 0u, 8, lane);
+  __syncthreads();
+  const uint32_t hi8 = sel[0];
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j)
+    if (tid + SMP_THREADS * j < V && (key[j] & 0xFF00u) == hi8) atomicAdd(&hist[1][key[j] & 255u], 1u);
+  __syncthreads();
+  if (tid < 64) radix_pick(hist[1], sel, hi8, 0, lane);
+  __syncthreads();
+  const uint32_t thr = sel[0];
+
+  // 3. masked logits / temp; log_softmax then softmax in fp32 (app/engine.py:293-296)
+  float xv[SMP_PER];
   float mloc = -INFINITY;
-  for (int i = tid; i < V; i += SMP_THREADS) {
-    float x = xs[i];
-    x = x < thr ? -INFINITY : x;
-    xs[i] = x;
-    mloc = fmaxf(mloc, x);
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) {
+    const bool in = tid + SMP_THREADS * j < V && key[j] >= thr;
+    xv[j] = in ? (float)lv[j] / temp : -INFINITY;
+    mloc = fmaxf(mloc, xv[j]);
   }
   const float m1 = block_reduce_max(mloc, red);
   float sloc = 0.f;
-  for (int i = tid; i < V; i += SMP_THREADS) sloc += expf(xs[i] - m1);
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) sloc += expf(xv[j] - m1);
   const float s1 = block_reduce_sum(sloc, red);
   const float logsum = logf(s1);
-  // log_softmax: ls = (x - m1) - logsum; its maximum is exactly -logsum (at x = m1, where
-  // (m1 - m1) - logsum is exact), so the second softmax needs no max reduction
+  // the maximum of ls = (x - m1) - logsum is exactly -logsum (at x = m1)
   const float m2 = 0.f - logsum;
   float s2loc = 0.f;
-  for (int i = tid; i < V; i += SMP_THREADS) {
-    const float ls = (xs[i] - m1) - logsum;
-    xs[i] = ls;
-    s2loc += expf(ls - m2);
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) {
+    xv[j] = (xv[j] - m1) - logsum;
+    s2loc += expf(xv[j] - m2);
   }
   const float s2 = block_reduce_sum(s2loc, red);
 
-  // 4. exponential race
-  // seed and pos are only dereferenced on the Philox path (they may be NULL with noise)
+  // 4. exponential race: argmax p / q, q ~ Exp(1); draws for index i come from Philox block
+  //    (i / 4, take, pos, salt), word i % 4 (or the injected noise)
   uint32_t k0 = 0u, k1 = 0u;
   uint64_t p64 = 0u;
-  if (!noise) {
+  if (!noise) {  // seed and pos are only dereferenced on the Philox path (NULL with noise)
     const uint64_t sd = (uint64_t)seed[0];
     k0 = (uint32_t)sd;
     k1 = (uint32_t)(sd >> 32);
@@ -215,31 +222,26 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
   float bv = -1.f;
   int bi = 0x7FFFFFFF;
-  for (int base = tid * 4; base < V; base += SMP_THREADS * 4) {
-    float q[4];
-    if (noise) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) q[j] = base + j < V ? noise[(long)n * V + base + j] : 1.f;
-    } else {
-      uint32_t c[4] = {(uint32_t)(base >> 2), (uint32_t)n, (uint32_t)p64,
-                       (uint32_t)(p64 >> 32) ^ ((uint32_t)salt << 20)};
-      philox4x32_10(c, k0, k1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float u = ((float)(c[j] >> 8) + 0.5f) * (1.0f / 16777216.0f);
-        q[j] = -logf(u);
+  for (int j = 0; j < SMP_PER; ++j) {
+    const int i = tid + SMP_THREADS * j;
+    if (i < V) {
+      float q;
+      if (noise) {
+        q = noise[(long)n * V + i];
+      } else {
+        uint32_t c[4] = {(uint32_t)(i >> 2), (uint32_t)n, (uint32_t)p64,
+                         (uint32_t)(p64 >> 32) ^ ((uint32_t)salt << 20)};
+        philox4x32_10(c, k0, k1);
+        const uint32_t w = c[i & 3];
+        const float u = ((float)(w >> 8) + 0.5f) * (1.0f / 16777216.0f);
+        q = -logf(u);
       }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = base + j;
-      if (i < V) {
-        const float p = expf(xs[i] - m2) / s2;
-        const float r = p / q[j];
-        if (r > bv || (r == bv && i < bi)) {
-          bv = r;
-          bi = i;
-        }
+      const float p = expf(xv[j] - m2) / s2;
+      const float r = p / q;
+      if (r > bv || (r == bv && i < bi)) {
+        bv = r;
+        bi = i;
       }
     }
   }
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
       bi = oi;
     }
   }
-  if ((tid & 63) == 0) {
+  if (lane == 0) {
     bestv[tid >> 6] = bv;
     besti[tid >> 6] = bi;
   }

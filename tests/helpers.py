@@ -28,8 +28,20 @@ def tiny_cfgs(ffn=512):
     return bb, dec
 
 
+_WEIGHTS_CACHE = {}
+
+
 def model_weights_np(backbone, decoder, seed=0, std=0.02, emb_std=1.0, text_vocab=64):
-    """Random-init weights in the int8 file layout, quantised by the oracle (numpy)."""
+    """Random-init weights in the int8 file layout, quantised by the oracle (numpy).
+    Memoised per configuration; callers must not modify the returned arrays."""
+    key = (tuple(sorted(backbone.items())), tuple(sorted(decoder.items())), seed, std, emb_std,
+           text_vocab)
+    if key not in _WEIGHTS_CACHE:
+        _WEIGHTS_CACHE[key] = _model_weights_np(backbone, decoder, seed, std, emb_std, text_vocab)
+    return _WEIGHTS_CACHE[key]
+
+
+def _model_weights_np(backbone, decoder, seed, std, emb_std, text_vocab):
     from estudiocanciones_amd.quant import weight_shapes  # pure-python shape table
     g = rng(seed)
     lin, dense = weight_shapes(backbone, decoder, text_vocab)
