@@ -176,6 +176,7 @@ def main():
 
     gemv_calls = [(n, a, gemv_family_bytes(n, a)) for n, a in calls if gemv_family_bytes(n, a)]
     attn_calls = [(n, a) for n, a in calls if n == "ecd_decode_attn"]
+    assert len(attn_calls) == len(attn_lens), (len(attn_calls), len(attn_lens))
     gemv_b = [b for _, _, b in gemv_calls]
     attn_b = [sum(Hk * ln * HD * 4 for ln in lens) + 4 * R * Hq * HD for lens, R, Hq, Hk, HD in attn_lens]
     def relaunch(name, a):

@@ -22,55 +22,32 @@
 
 namespace ecd {
 
+// One split of one (row, kv head) as seen by one wave: on return lanes 0..15 hold the
+// unnormalised accumulators acc[g][j][0..7] of d-chunk 8 (lane + 16 j), and lane g < G holds
+// head g's running max m and running sum l (m = -inf, l = 0 for an empty split).
 template <int HD, int G>
-__global__ __launch_bounds__(64) void decode_attn_kernel(
-    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
-    const int64_t* __restrict__ pos, f16* __restrict__ o, float* __restrict__ pm,
-    float* __restrict__ pl, float* __restrict__ pa, int S, int Hq, int Hk, int L, float scale,
-    int nsplit) {
-  static_assert(HD % 32 == 0 && HD <= 512, "head_dim must be a multiple of 32");
-  static_assert(G >= 1 && G <= 16, "query heads per kv head must be 1..16");
-  constexpr int NKC = HD / 32;
-  constexpr int NDP = (HD + 127) / 128;
+struct SplitState {
+  static constexpr int NDP = (HD + 127) / 128;
+  float m_run, l_run;
+  float acc[G][NDP][8];
+};
 
-  const int lane = threadIdx.x;
+template <int HD, int G, bool DB>
+__device__ __forceinline__ void attn_split(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                           const f16* __restrict__ kb, const f16* __restrict__ vb,
+                                           int lo, int hi, float scale, int lane) {
+  constexpr int NKC = HD / 32;
+  constexpr int NDP = SplitState<HD, G>::NDP;
   const int row = lane & 15;
   const int grp = lane >> 4;
-  const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
-  const int b = r / S;
-  const long praw = pos[r];
-  const int ln = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));
-  const int per = (ln + nsplit - 1) / nsplit;
-  const int chunk = ((per + 15) / 16) * 16;
-  const int lo = sp * chunk;
-  const int hi = min(ln, lo + chunk);
-
-  const long cbase = ((long)b * Hk + kh) * (long)L * HD;
-  const f16* kb = kc + cbase;
-  const f16* vb = vc + cbase;
-
-  f16x8 qf[NKC];
-  {
-    const bool gv = row < G;
-    const f16* qp = q + ((long)r * Hq + kh * G + (gv ? row : 0)) * HD + 8 * grp;
-#pragma unroll
-    for (int i = 0; i < NKC; ++i) {
-      if (gv)
-        qf[i] = *(const f16x8*)(qp + 32 * i);
-      else
-        qf[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    }
-  }
-
   float m_run = -INFINITY;
   float l_run = 0.f;
-  float acc[G][NDP][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < NDP; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][j][e] = 0.f;
+      for (int e = 0; e < 8; ++e) ss.acc[g][j][e] = 0.f;
 
   f16x8 kf[NKC];
   f16x8 vv[4][NDP];
@@ -96,10 +73,9 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
   if (lo < hi) load_tile(lo, kf, vv);
 
   for (int t0 = lo; t0 < hi; t0 += 16) {
-    // double buffering for the narrow heads: the next tile's loads fly during this tile's math
+    // double buffering (DB): the next tile's loads fly during this tile's math
     f16x8 kn[NKC];
     f16x8 vn[4][NDP];
-    constexpr bool DB = HD <= 128;
     if (DB && t0 + 16 < hi) load_tile(t0 + 16, kn, vn);
     f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -140,10 +116,10 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
       for (int j = 0; j < NDP; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float a = acc[g][j][e] * ag;
+          float a = ss.acc[g][j][e] * ag;
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)vv[rr][j][e];
-          acc[g][j][e] = a;
+          ss.acc[g][j][e] = a;
         }
     }
     if (t0 + 16 < hi) {
@@ -167,17 +143,71 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
     for (int j = 0; j < NDP; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float a = acc[g][j][e];
+        float a = ss.acc[g][j][e];
         a += __shfl_xor(a, 16, 64);
         a += __shfl_xor(a, 32, 64);
-        acc[g][j][e] = a;
+        ss.acc[g][j][e] = a;
       }
+  ss.m_run = m_run;
+  ss.l_run = l_run;
+}
+
+// Attended length of row r and the [lo, hi) token range of split sp (app/kernels.py:120-127).
+__device__ __forceinline__ void split_range(const int64_t* __restrict__ pos, int r, int L,
+                                            int nsplit, int sp, int& lo, int& hi) {
+  const long praw = pos[r];
+  const int ln = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));
+  const int per = (ln + nsplit - 1) / nsplit;
+  const int chunk = ((per + 15) / 16) * 16;
+  lo = sp * chunk;
+  hi = min(ln, lo + chunk);
+}
+
+// Q^T fragments of the G query heads of kv head kh (B operand: lane l holds head l & 15,
+// d-chunk 8 (l >> 4) + 32 i; zero for heads >= G).
+template <int HD, int G>
+__device__ __forceinline__ void load_q(f16x8 (&qf)[HD / 32], const f16* __restrict__ q, int r,
+                                       int Hq, int kh, int lane) {
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const bool gv = row < G;
+  const f16* qp = q + ((long)r * Hq + kh * G + (gv ? row : 0)) * HD + 8 * grp;
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i) {
+    if (gv)
+      qf[i] = *(const f16x8*)(qp + 32 * i);
+    else
+      qf[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  }
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(64) void decode_attn_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+    const int64_t* __restrict__ pos, f16* __restrict__ o, float* __restrict__ pm,
+    float* __restrict__ pl, float* __restrict__ pa, int S, int Hq, int Hk, int L, float scale,
+    int nsplit) {
+  static_assert(HD % 32 == 0 && HD <= 512, "head_dim must be a multiple of 32");
+  static_assert(G >= 1 && G <= 16, "query heads per kv head must be 1..16");
+  constexpr int NDP = SplitState<HD, G>::NDP;
+  const int lane = threadIdx.x;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
+  const int b = r / S;
+  int lo, hi;
+  split_range(pos, r, L, nsplit, sp, lo, hi);
+  const long cbase = ((long)b * Hk + kh) * (long)L * HD;
+  f16x8 qf[HD / 32];
+  load_q<HD, G>(qf, q, r, Hq, kh, lane);
+  SplitState<HD, G> ss;
+  attn_split<HD, G, (HD <= 128)>(ss, qf, kc + cbase, vc + cbase, lo, hi, scale, lane);
 
   const long hbase = (long)r * Hq + kh * G;
   if (nsplit == 1) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float lg = __shfl(l_run, g, 64);
+      const float lg = __shfl(ss.l_run, g, 64);
       if (grp == 0) {
 #pragma unroll
         for (int j = 0; j < NDP; ++j) {
@@ -185,7 +215,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
           if (d < HD) {
             f16x8 ov;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ov[e] = (f16)(acc[g][j][e] / lg);
+            for (int e = 0; e < 8; ++e) ov[e] = (f16)(ss.acc[g][j][e] / lg);
             *(f16x8*)(o + (hbase + g) * HD + d) = ov;
           }
         }
@@ -194,8 +224,8 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
   } else {
     if (lane < G) {
       const long pidx = (hbase + lane) * nsplit + sp;
-      pm[pidx] = m_run;
-      pl[pidx] = l_run;
+      pm[pidx] = ss.m_run;
+      pl[pidx] = ss.l_run;
     }
     if (grp == 0) {
 #pragma unroll
@@ -206,12 +236,78 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
           const int d = 8 * (row + 16 * j);
           if (d < HD) {
             float* dst = pa + pidx * HD + d;
-            *(f32x4*)dst = (f32x4){acc[g][j][0], acc[g][j][1], acc[g][j][2], acc[g][j][3]};
-            *(f32x4*)(dst + 4) = (f32x4){acc[g][j][4], acc[g][j][5], acc[g][j][6], acc[g][j][7]};
+            *(f32x4*)dst = (f32x4){ss.acc[g][j][0], ss.acc[g][j][1], ss.acc[g][j][2], ss.acc[g][j][3]};
+            *(f32x4*)(dst + 4) = (f32x4){ss.acc[g][j][4], ss.acc[g][j][5], ss.acc[g][j][6], ss.acc[g][j][7]};
           }
         }
       }
     }
+  }
+}
+
+// Split attention and its log-sum-exp combine in one launch: one workgroup per (kv head, row),
+// NW waves; wave w computes splits w, w + NW, ... exactly as decode_attn_kernel does and leaves
+// its partials in LDS; after one workgroup barrier every thread merges the partials of one
+// (head, d) output the way attn_combine_kernel does.  The splits never leave the CU, so the
+// partial traffic and the combine launch disappear; the cost is that only R * Hk workgroups
+// share the chip, each streaming its (row, kv head)'s K and V through one CU.
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_attn_fused_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+    const int64_t* __restrict__ pos, f16* __restrict__ o, int S, int Hq, int Hk, int L,
+    float scale, int nsplit) {
+  constexpr int NDP = SplitState<HD, G>::NDP;
+  extern __shared__ float smem[];
+  float* s_m = smem;                    // [nsplit][G]
+  float* s_l = smem + nsplit * G;       // [nsplit][G]
+  float* s_a = smem + 2 * nsplit * G;   // [nsplit][G][HD]
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int kh = blockIdx.x, r = blockIdx.y;
+  const int b = r / S;
+  const long cbase = ((long)b * Hk + kh) * (long)L * HD;
+  f16x8 qf[HD / 32];
+  load_q<HD, G>(qf, q, r, Hq, kh, lane);
+  for (int sp = wv; sp < nsplit; sp += NW) {
+    int lo, hi;
+    split_range(pos, r, L, nsplit, sp, lo, hi);
+    SplitState<HD, G> ss;
+    // double buffering only where the register budget of NW waves per CU allows it
+    attn_split<HD, G, (HD <= 128 && NW <= 8)>(ss, qf, kc + cbase, vc + cbase, lo, hi, scale, lane);
+    if (lane < G) {
+      s_m[sp * G + lane] = ss.m_run;
+      s_l[sp * G + lane] = ss.l_run;
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < NDP; ++j) {
+          const int d = 8 * (row + 16 * j);
+          if (d < HD) {
+            float* dst = s_a + (sp * G + g) * HD + d;
+            *(f32x4*)dst = (f32x4){ss.acc[g][j][0], ss.acc[g][j][1], ss.acc[g][j][2], ss.acc[g][j][3]};
+            *(f32x4*)(dst + 4) = (f32x4){ss.acc[g][j][4], ss.acc[g][j][5], ss.acc[g][j][6], ss.acc[g][j][7]};
+          }
+        }
+    }
+  }
+  __syncthreads();
+  const long hbase = (long)r * Hq + kh * G;
+  for (int t = threadIdx.x; t < G * HD; t += NW * 64) {
+    const int g = t / HD, d = t - g * HD;
+    float M = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, s_m[sp * G + g]);
+    float den = 0.f, acc = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float m = s_m[sp * G + g];
+      const float w = m > -INFINITY ? __expf(m - M) : 0.f;
+      den += s_l[sp * G + g] * w;
+      acc += s_a[(sp * G + g) * HD + d] * w;
+    }
+    o[(hbase + g) * HD + d] = (f16)(acc / den);
   }
 }
 
@@ -296,6 +392,69 @@ static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* 
 #undef ECD_ATTN_G
 }
 
+constexpr int FUSED_MAXS = 32;
+constexpr int FUSED_LDS_MAX = 160 * 1024;
+
+template <int HD, int G, int NW>
+static int launch_fused_one(dim3 grid, size_t lds, hipStream_t st, const f16* q, const f16* kc,
+                            const f16* vc, const int64_t* pos, f16* o, int S, int Hq, int Hk,
+                            int L, float scale, int nsplit) {
+  // instantiated only where the per-wave register budget of NW waves per CU holds the split
+  // state without spilling (16 waves: 128 registers per lane; 8 waves: 256)
+  constexpr bool fits = NW == 16 ? (HD <= 128 && G <= 4) : !(HD == 256 && G == 8);
+  if constexpr (!fits) {
+    return ECD_ENOTSUP;
+  } else {
+  static bool attr = false;  // raise the dynamic LDS limit once per instantiation
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)decode_attn_fused_kernel<HD, G, NW>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             FUSED_LDS_MAX);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  hipLaunchKernelGGL((decode_attn_fused_kernel<HD, G, NW>), grid, dim3(NW * 64), lds, st, q, kc,
+                     vc, pos, o, S, Hq, Hk, L, scale, nsplit);
+  return ECD_OK;
+  }
+}
+
+template <int HD, int NW>
+static int launch_fused_hd(int G, dim3 grid, size_t lds, hipStream_t st, const f16* q,
+                           const f16* kc, const f16* vc, const int64_t* pos, f16* o, int S,
+                           int Hq, int Hk, int L, float scale, int nsplit) {
+  switch (G) {
+#define ECD_FUSED_G(G_) \
+  case G_:              \
+    return launch_fused_one<HD, G_, NW>(grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
+    ECD_FUSED_G(1)
+    ECD_FUSED_G(2)
+    ECD_FUSED_G(3)
+    ECD_FUSED_G(4)
+    ECD_FUSED_G(6)
+    ECD_FUSED_G(8)
+#undef ECD_FUSED_G
+    default:
+      return ECD_ENOTSUP;
+  }
+}
+
+template <int NW>
+static int launch_fused(int HD, int G, dim3 grid, size_t lds, hipStream_t st, const f16* q,
+                        const f16* kc, const f16* vc, const int64_t* pos, f16* o, int S, int Hq,
+                        int Hk, int L, float scale, int nsplit) {
+  switch (HD) {
+    case 64:
+      return launch_fused_hd<64, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
+    case 128:
+      return launch_fused_hd<128, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
+    case 256:
+      return launch_fused_hd<256, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
+    default:
+      return ECD_ENOTSUP;
+  }
+}
+
 }  // namespace ecd
 
 using namespace ecd;
@@ -332,6 +491,27 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
     default:
       rc = ECD_ENOTSUP;
   }
+  if (rc != ECD_OK) return rc;
+  return ecd_launch_status();
+}
+
+int ecd_decode_attn_fused(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                          void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
+                          int nw, float scale, void* stream) {
+  if (!q || !kc || !vc || !pos || !o || R <= 0 || S <= 0 || Hq <= 0 || Hk <= 0 || L <= 0 ||
+      HD <= 0 || nsplit <= 0 || nsplit > FUSED_MAXS || (Hq % Hk) != 0 ||
+      (nw != 0 && nw != 8 && nw != 16))
+    return ECD_EINVAL;
+  const int G = Hq / Hk;
+  const size_t lds = (size_t)nsplit * G * (HD + 2) * sizeof(float);
+  if (lds > (size_t)FUSED_LDS_MAX) return ECD_ENOTSUP;
+  if (nw == 0) nw = (nsplit > 8 && HD <= 128 && G <= 4) ? 16 : 8;
+  dim3 grid(Hk, R);
+  hipStream_t st = (hipStream_t)stream;
+  const f16 *qh = (const f16*)q, *kh = (const f16*)kc, *vh = (const f16*)vc;
+  const int rc = nw == 16
+                     ? launch_fused<16>(HD, G, grid, lds, st, qh, kh, vh, pos, (f16*)o, S, Hq, Hk, L, scale, nsplit)
+                     : launch_fused<8>(HD, G, grid, lds, st, qh, kh, vh, pos, (f16*)o, S, Hq, Hk, L, scale, nsplit);
   if (rc != ECD_OK) return rc;
   return ecd_launch_status();
 }

@@ -428,14 +428,22 @@ __global__ __launch_bounds__(KW * 64) void gemv_xlds_kernel(const GemvArgs a) {
       }
     } else if (PRO == PRO_RMS) {
       // K <= NW_MAX: the whole row stays in registers (8 halfs per lane per 512)
+      // the norm weights are loaded together with the row (one memory round trip, not two)
       const f16* src = a.x + (long)m * a.ldx;
-      f16x8 v[NW_MAX / 512];
-      float ss = 0.f;
+      f16x8 v[NW_MAX / 512], nwv[NW_MAX / 512];
 #pragma unroll
       for (int i = 0; i < NW_MAX / 512; ++i) {
         const int k = lane * 8 + 512 * i;
         if (k < K) {
           v[i] = ld8(src + k);
+          nwv[i] = ld8(a.nw + k);
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NW_MAX / 512; ++i) {
+        const int k = lane * 8 + 512 * i;
+        if (k < K) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss += (float)v[i][e] * (float)v[i][e];
         }
@@ -446,10 +454,9 @@ __global__ __launch_bounds__(KW * 64) void gemv_xlds_kernel(const GemvArgs a) {
       for (int i = 0; i < NW_MAX / 512; ++i) {
         const int k = lane * 8 + 512 * i;
         if (k < K) {
-          const f16x8 w = ld8(a.nw + k);
           f16x8 o;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = (f16)((float)v[i][e] * inv) * w[e];
+          for (int e = 0; e < 8; ++e) o[e] = (f16)((float)v[i][e] * inv) * nwv[i][e];
           *(f16x8*)(dst + k) = o;
         }
       }
@@ -518,6 +525,197 @@ __global__ __launch_bounds__(KW * 64) void gemv_xlds_kernel(const GemvArgs a) {
   }
 }
 
+// Register-x variant: every wave loads, at kernel start, its own K-range of x (the B fragments
+// of chunks [c0, c1), straight from memory in MFMA lane order) and then the first LA chunks of
+// its weights; chunk u + LA is issued as chunk u is consumed.  No LDS tile or barrier sits
+// before the MFMAs.  PRO_RMS needs the full-row statistics: each wave reduces the sum of
+// squares over its own slice, one barrier exchanges the KW partial sums, and the norm weights
+// are staged in LDS meanwhile.  MAXC >= c1 - c0 bounds the chunks a wave holds (host-checked).
+template <int NT, int KW, int PRO, int EPI, bool NTL, int MAXC, int LA>
+__global__ __launch_bounds__(KW * 64) void gemv_xreg_kernel(const GemvArgs a) {
+  static_assert(PRO == PRO_PLAIN || PRO == PRO_RMS, "register-x prologue: plain or RMS");
+  static_assert(KW * 512 >= NW_MAX, "one norm-weight vector per thread stages K <= NW_MAX");
+  extern __shared__ __align__(16) unsigned char smem[];
+  f32x4* red = (f32x4*)smem;                               // [KW][NT][64]
+  float* s_ss = (float*)(smem + KW * NT * 64 * 16);        // [KW][16]
+  f16* s_nw = (f16*)(smem + KW * NT * 64 * 16 + KW * 64);  // [K]
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int tile0 = blockIdx.x * NT;
+  const int n0 = tile0 * 16;
+  const int m0 = blockIdx.y * 16;
+  const int K = a.K, M = a.M, N = a.N;
+  const int nch = K >> 6;
+  const int ntiles = (N + 15) >> 4;
+  const int c0 = (nch * wv) / KW;
+  const int nc = (nch * (wv + 1)) / KW - c0;
+  const bool dense = a.dense != 0;
+
+  // Issue order matters: loads complete in order for the wait counters, so the norm weights
+  // and x (needed first) go out before the weights, and the weights go out chunk by chunk (the
+  // MFMAs of chunk u wait only for chunks <= u).
+  f16x8 nwt;
+  const int kn = threadIdx.x * 8;
+  if (PRO == PRO_RMS && kn < K) nwt = ld8(a.nw + kn);
+  const bool mval = m0 + row < M;
+  const f16* xp = a.x + (long)(mval ? m0 + row : 0) * a.ldx + (long)c0 * 64 + 16 * grp;
+  f16x8 xa[MAXC], xb[MAXC];
+#pragma unroll
+  for (int u = 0; u < MAXC; ++u) {
+    if (u < nc) {
+      if (mval) {
+        xa[u] = ld8(xp + u * 64);
+        xb[u] = ld8(xp + u * 64 + 8);
+      } else {
+        xa[u] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        xb[u] = xa[u];
+      }
+    }
+  }
+
+  u32x4 w[MAXC][NT];
+  f16 sw[NT];
+  const int8_t* wb = a.wp + (long)c0 * 1024 + 16 * lane;
+  int tl[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) tl[t] = min(tile0 + t, ntiles - 1);
+  // weight chunks [0, LA) now; chunk u + LA is issued when chunk u is consumed (at most LA
+  // chunks of NT tiles in flight per wave)
+#pragma unroll
+  for (int u = 0; u < (LA < MAXC ? LA : MAXC); ++u)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if (u < nc) w[u][t] = ldw<NTL>(wb + ((long)tl[t] * nch + u) * 1024);
+
+  const bool epi_thread = (int)threadIdx.x < NT * 64;
+  EpiPre pre_e;
+  if (epi_thread) pre_e = epi_prefetch<EPI>(a, n0, m0, threadIdx.x >> 6, threadIdx.x & 63);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) sw[t] = dense ? a.s[min(n0 + 16 * t + row, N - 1)] : (f16)0.0f;
+
+  if (PRO == PRO_RMS) {
+    if (kn < K) *(f16x8*)(s_nw + kn) = nwt;
+    // sum of squares with v_dot2_f32_f16 (exact f16 products, fp32 sums): no fp32 copy of the
+    // fragments stays live across the barrier below
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u)
+      if (u < nc)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const f16x2 pa = (f16x2){xa[u][e], xa[u][e + 1]};
+          const f16x2 pb = (f16x2){xb[u][e], xb[u][e + 1]};
+          ss = __builtin_amdgcn_fdot2(pa, pa, ss, false);
+          ss = __builtin_amdgcn_fdot2(pb, pb, ss, false);
+        }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (grp == 0) s_ss[wv * 16 + row] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int v = 0; v < KW; ++v) tot += s_ss[v * 16 + row];
+    const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+      if (u < nc) {
+        const int k0 = (c0 + u) * 64 + 16 * grp;
+        const f16x8 na = *(const f16x8*)(s_nw + k0);
+        const f16x8 nb = *(const f16x8*)(s_nw + k0 + 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xa[u][e] = (f16)((float)xa[u][e] * inv) * na[e];
+          xb[u][e] = (f16)((float)xb[u][e] * inv) * nb[e];
+        }
+      }
+    }
+  }
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < MAXC; ++u) {
+    if (u < nc) {
+      if (u + LA < MAXC && u + LA < nc) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) w[u + LA][t] = ldw<NTL>(wb + ((long)tl[t] * nch + u + LA) * 1024);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f16x8 wa, wbv;
+        i8x16_to_f16(w[u][t], wa, wbv);
+        if (dense) {
+          wa = wa * sw[t];
+          wbv = wbv * sw[t];
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, xa[u], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wbv, xb[u], acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < NT; ++t) red[(wv * NT + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < NT * 64; idx += KW * 64) {
+    const int t = idx >> 6, l = idx & 63;
+    f32x4 s4 = red[t * 64 + l];
+#pragma unroll
+    for (int v = 1; v < KW; ++v) s4 += red[(v * NT + t) * 64 + l];
+    gemv_epilogue<EPI>(a, n0, m0, t, l, s4, pre_e);
+  }
+}
+
+// Chunks per wave the register-x kernel can hold for NT tiles with KW waves per block (x and
+// weight fragments stay within the per-lane register budget of KW waves per CU), 0 if none.
+constexpr int xreg_maxc(int NT, int KW, int PRO) {
+  return KW == 16 ? (NT == 1 ? 8 : NT == 2 ? 4 : 2) : (NT <= 2 || PRO == PRO_PLAIN ? 8 : 6);
+}
+
+template <int NT, int KW, int PRO, int EPI, bool NTL, int MAXC>
+static int launch_xreg_one(const GemvArgs& a, hipStream_t st) {
+  const int ntiles = (a.N + 15) / 16;
+  dim3 grid((ntiles + NT - 1) / NT, (a.M + 15) / 16);
+  const unsigned lds = KW * NT * 64 * 16 + KW * 64 + (PRO == PRO_RMS ? a.K * 2 : 0);
+  // weight chunks in flight per wave: 16 KB (NT = 4 reads four tiles per chunk)
+  constexpr int LA = NT >= 4 ? 4 : 16;
+  hipLaunchKernelGGL((gemv_xreg_kernel<NT, KW, PRO, EPI, NTL, MAXC, LA>), grid, dim3(KW * 64), lds,
+                     st, a);
+  return ecd_launch_status();
+}
+
+// Launches the register-x kernel if the shape fits it; returns 1 (not launched) otherwise.
+template <int NT, int KW, int PRO, int EPI, bool NTL>
+static int launch_xreg(const GemvArgs& a, hipStream_t st) {
+  if constexpr (PRO == PRO_EMBED || (PRO == PRO_RMS && KW != 8)) {
+    return 1;
+  } else {
+    const int nch = a.K >> 6;
+    const int cpw = (nch + KW - 1) / KW;
+    // Measured on every frame shape (MI355X): register x wins for the plain prologue at every
+    // K and for the RMS prologue with 8 waves and at most two chunks per wave (K <= 1024); the
+    // LDS tile wins for the RMS prologue over wider rows, whose partial-sum barrier waits for
+    // every wave's slice of x.
+    if (PRO == PRO_RMS && (a.K > NW_MAX || cpw > 2)) return 1;
+    constexpr int MC = PRO == PRO_RMS ? 2 : xreg_maxc(NT, KW, PRO);
+    if (cpw <= 1) return launch_xreg_one<NT, KW, PRO, EPI, NTL, 1>(a, st);
+    if (cpw <= 2) return launch_xreg_one<NT, KW, PRO, EPI, NTL, 2>(a, st);
+    if constexpr (MC >= 4) {
+      if (cpw <= 4) return launch_xreg_one<NT, KW, PRO, EPI, NTL, 4>(a, st);
+    }
+    if constexpr (MC == 6) {
+      if (cpw <= 6) return launch_xreg_one<NT, KW, PRO, EPI, NTL, 6>(a, st);
+    }
+    if constexpr (MC >= 8) {
+      if (cpw <= 8) return launch_xreg_one<NT, KW, PRO, EPI, NTL, 8>(a, st);
+    }
+    return 1;
+  }
+}
+
 // Pack w [N, K] into lane-ordered 16 x 64 tiles.  With `interleave` (N even), packed row 2j is
 // source row j and packed row 2j + 1 is source row N/2 + j (w1 | w3 -> pairs).
 __global__ __launch_bounds__(256) void pack_i8_kernel(const int8_t* __restrict__ w, int N, int K,
@@ -559,6 +757,10 @@ constexpr int LDS_MAX = 160 * 1024;
 
 template <int NT, int KW, int PRO, int EPI, bool NTL>
 static int launch_one(const GemvArgs& a, hipStream_t st) {
+  {
+    const int rc = launch_xreg<NT, KW, PRO, EPI, NTL>(a, st);
+    if (rc != 1) return rc;
+  }
   const int ntiles = (a.N + 15) / 16;
   dim3 grid((ntiles + NT - 1) / NT, (a.M + 15) / 16);
   const long xbytes = (long)min(16, a.M) * (a.K + XPAD) * 2;

@@ -5,8 +5,9 @@ method names and tensor layouts -- ``Linear``, ``fuse``, ``Emb``, ``Block``, ``S
 (``alloc``/``free``/``__call__``/``decode``) and ``HeartMuLaLite`` (``_sample``,
 ``_guided``, ``_embed_audio``, ``_frame_fast``, ``_step``, ``generate``, ``_capture``,
 ``release``) -- but every op of the per-frame step is a hand-written HIP kernel reached
-through the C ABI of ``libecdecode.so`` (see ``kernels.py``); sampling stays on PyTorch GPU
-ops exactly as in the reference.  Differences from the reference, all deliberate:
+through the C ABI of ``libecdecode.so`` (see ``kernels.py``), sampling included (one fused
+CFG + top-k + Exponential-race kernel per codebook; ``_sample``/``_guided`` keep the
+reference's PyTorch form for the slow path).  Differences from the reference, all deliberate:
 
 * stacks are shape-parametric (``dim`` per stack) instead of the global ``DIM = 3072``
   (app/engine.py:19, :116, :161), so a 1024-wide decoder can be expressed;

@@ -41,6 +41,44 @@ def test_gemv_packed(dev, M, N, K, res):
     assert_close16(N_(y), OK.gemv_i8(x, q, s, r), what=f"packed gemv M={M} N={N} K={K}")
 
 
+def test_gemv_packed_every_tile_config_and_chunk_count(dev):
+    """Every (tiles per block, waves per block) pair over K values that give each wave 0, 1, 2,
+    3-4, 5-8 and more than 8 chunks (the register-x kernel's bounds and the LDS-tile fallback),
+    both numerics (M <= 16 and M > 16) and a row count that is not a multiple of 16."""
+    import torch
+    from estudiocanciones_amd import _ffi
+    from estudiocanciones_amd.kernels import pack_i8, stream_ptr
+    for K in (64, 192, 1024, 4096, 8192, 9216):
+        for N in (100, 1000):
+            q, s = qweights(K + N, N, K)
+            wp = pack_i8(T(q, dev))
+            st = T(s, dev)
+            for M in (8, 20):
+                x = randn16(K + M, M, K)
+                r = randn16(K + M + 1, M, N)
+                want = OK.gemv_i8(x, q, s, r)
+                xt, rt = T(x, dev), T(r, dev)
+                for nt, kw in ((1, 8), (1, 16), (2, 8), (2, 16), (4, 8), (4, 16)):
+                    y = torch.empty(M, N, dtype=torch.float16, device=dev)
+                    _ffi.call("ecd_gemv_i8p", xt.data_ptr(), K, wp.data_ptr(), st.data_ptr(),
+                              rt.data_ptr(), N, y.data_ptr(), N, M, N, K, int(M > 16), nt, kw,
+                              stream_ptr(dev))
+                    assert_close16(N_(y), want, what=f"M={M} N={N} K={K} nt={nt} kw={kw}")
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 8197, 1024), (8, 8197, 512), (16, 9000, 64), (20, 8197, 1024),
+                                   (8, 300, 1024)])
+def test_rms_gemv_packed_shapes(dev, M, N, K):
+    """RMS prologue on the shapes that take the register-x kernel (8 waves, <= 2 chunks per
+    wave) and on those that stay on the LDS tile."""
+    from estudiocanciones_amd.kernels import pack_i8, rms_gemv_packed
+    q, s = qweights(7 + K, N, K)
+    x = randn16(8 + K, M, K, std=2.0)
+    nw = (1 + 0.02 * rng(9).standard_normal(K)).astype(np.float16)
+    y = rms_gemv_packed(T(x, dev), T(nw, dev), pack_i8(T(q, dev)), T(s, dev), N, K)
+    assert_close16(N_(y), OK.gemv_i8(OK.rms(x, nw), q, s), what=f"rms+gemv M={M} N={N} K={K}")
+
+
 def test_rms_gemv_packed(dev):
     from estudiocanciones_amd.kernels import pack_i8, rms_gemv_packed
     M, N, K = 8, 8197, 3072
