@@ -1,0 +1,209 @@
+// Per-wave flash-decoding core shared by the attention kernels and the attention-prologue GEMV.
+// Semantics: app/kernels.py:111-153 (see decode_attn.hip for the full description).
+#pragma once
+#include "common.h"
+
+namespace ecd {
+
+// One split of one (row, kv head) as seen by one wave: on return lanes 0..15 hold the
+// unnormalised accumulators acc[g][j][0..7] of d-chunk 8 (lane + 16 j), and lane g < G holds
+// head g's running max m and running sum l (m = -inf, l = 0 for an empty split).
+template <int HD, int G>
+struct SplitState {
+  static constexpr int NDP = (HD + 127) / 128;
+  float m_run, l_run;
+  float acc[G][NDP][8];
+};
+
+// K rows (A operand: lane l holds token t0 + (l & 15), d-chunk 8 (l >> 4) + 32 i) and V rows
+// (lane l holds token t0 + 4 (l >> 4) + rr, d-chunk 8 (l & 15) + 128 j) of one 16-token tile.
+template <int HD>
+struct KVTile {
+  static constexpr int NKC = HD / 32;
+  static constexpr int NDP = (HD + 127) / 128;
+  f16x8 k[NKC];
+  f16x8 v[4][NDP];
+};
+
+// Loads the tile at t0 with token indices clamped to `lim` (any valid slot).  Tokens past the
+// attended range are masked by attn_run, so a tile may be loaded before that range is known.
+template <int HD>
+__device__ __forceinline__ void kv_load(KVTile<HD>& t, const f16* __restrict__ kb,
+                                        const f16* __restrict__ vb, int t0, int lim, int lane) {
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const f16* kp = kb + (long)min(t0 + row, lim) * HD + 8 * grp;
+#pragma unroll
+  for (int i = 0; i < KVTile<HD>::NKC; ++i) t.k[i] = *(const f16x8*)(kp + 32 * i);
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const f16* vp = vb + (long)min(t0 + 4 * grp + rr, lim) * HD + 8 * row;
+#pragma unroll
+    for (int j = 0; j < KVTile<HD>::NDP; ++j) {
+      if (8 * (row + 16 * j) < HD)
+        t.v[rr][j] = *(const f16x8*)(vp + 128 * j);
+      else
+        t.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+}
+
+// The split [lo, hi) given its first tile `cur` already loaded at lo.
+template <int HD, int G, bool DB>
+__device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                         KVTile<HD>& cur, const f16* __restrict__ kb,
+                                         const f16* __restrict__ vb, int lo, int hi, float scale,
+                                         int lane) {
+  constexpr int NKC = HD / 32;
+  constexpr int NDP = SplitState<HD, G>::NDP;
+  const int grp = lane >> 4;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss.acc[g][j][e] = 0.f;
+
+  for (int t0 = lo; t0 < hi; t0 += 16) {
+    // double buffering (DB): the next tile's loads fly during this tile's math
+    KVTile<HD> nxt;
+    if (DB && t0 + 16 < hi) kv_load<HD>(nxt, kb, vb, t0 + 16, hi - 1, lane);
+    // V rows past the range contribute nothing (they may hold any bits, even NaN)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      if (t0 + 4 * grp + rr >= hi)
+#pragma unroll
+        for (int j = 0; j < NDP; ++j) cur.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[i], qf[i], st, 0, 0, 0);
+
+    float sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int t = t0 + 4 * grp + rr;
+      sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
+      mx = fmaxf(mx, sc[rr]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __expf(m_run - m_new);
+    float pr[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pr[rr] = __expf(sc[rr] - m_new);
+      ps += pr[rr];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int src = 16 * grp + g;
+      const float ag = __shfl(alpha, src, 64);
+      float pg[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) pg[rr] = (float)(f16)__shfl(pr[rr], src, 64);
+#pragma unroll
+      for (int j = 0; j < NDP; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float a = ss.acc[g][j][e] * ag;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)cur.v[rr][j][e];
+          ss.acc[g][j][e] = a;
+        }
+    }
+    if (t0 + 16 < hi) {
+      if (DB)
+        cur = nxt;
+      else
+        kv_load<HD>(cur, kb, vb, t0 + 16, hi - 1, lane);
+    }
+  }
+
+  // merge the four token phases (lane groups) of every d-chunk
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = ss.acc[g][j][e];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        ss.acc[g][j][e] = a;
+      }
+  ss.m_run = m_run;
+  ss.l_run = l_run;
+}
+
+template <int HD, int G, bool DB>
+__device__ __forceinline__ void attn_split(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                           const f16* __restrict__ kb, const f16* __restrict__ vb,
+                                           int lo, int hi, float scale, int lane) {
+  KVTile<HD> t;
+  if (lo < hi) kv_load<HD>(t, kb, vb, lo, hi - 1, lane);
+  attn_run<HD, G, DB>(ss, qf, t, kb, vb, lo, hi, scale, lane);
+}
+
+// Writes head g's normalised output o = acc / l as fp16 (lanes 0..15) to dst[g * HD + d].
+template <int HD, int G>
+__device__ __forceinline__ void attn_store_o(const SplitState<HD, G>& ss, f16* dst, int lane) {
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float lg = __shfl(ss.l_run, g, 64);
+    if (grp == 0) {
+#pragma unroll
+      for (int j = 0; j < SplitState<HD, G>::NDP; ++j) {
+        const int d = 8 * (row + 16 * j);
+        if (d < HD) {
+          f16x8 ov;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ov[e] = (f16)(ss.acc[g][j][e] / lg);
+          *(f16x8*)(dst + g * HD + d) = ov;
+        }
+      }
+    }
+  }
+}
+
+// Attended length of row r and the [lo, hi) token range of split sp (app/kernels.py:120-127).
+__device__ __forceinline__ void split_range(const int64_t* __restrict__ pos, int r, int L,
+                                            int nsplit, int sp, int& lo, int& hi) {
+  const long praw = pos[r];
+  const int ln = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));
+  const int per = (ln + nsplit - 1) / nsplit;
+  const int chunk = ((per + 15) / 16) * 16;
+  lo = sp * chunk;
+  hi = min(ln, lo + chunk);
+}
+
+// Q^T fragments of the G query heads of kv head kh (B operand: lane l holds head l & 15,
+// d-chunk 8 (l >> 4) + 32 i; zero for heads >= G).
+template <int HD, int G>
+__device__ __forceinline__ void load_q(f16x8 (&qf)[HD / 32], const f16* __restrict__ q, int r,
+                                       int Hq, int kh, int lane) {
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const bool gv = row < G;
+  const f16* qp = q + ((long)r * Hq + kh * G + (gv ? row : 0)) * HD + 8 * grp;
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i) {
+    if (gv)
+      qf[i] = *(const f16x8*)(qp + 32 * i);
+    else
+      qf[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  }
+}
+
+}  // namespace ecd

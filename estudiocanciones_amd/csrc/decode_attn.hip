@@ -18,168 +18,9 @@
 //                        the same 16-lane row and arrive through lane shuffles.
 // Each K and V byte of the attended range is read once per (row, kv head): the G query
 // heads of a group share it (no repeat_kv copy).
-#include "common.h"
+#include "attn_core.h"
 
 namespace ecd {
-
-// One split of one (row, kv head) as seen by one wave: on return lanes 0..15 hold the
-// unnormalised accumulators acc[g][j][0..7] of d-chunk 8 (lane + 16 j), and lane g < G holds
-// head g's running max m and running sum l (m = -inf, l = 0 for an empty split).
-template <int HD, int G>
-struct SplitState {
-  static constexpr int NDP = (HD + 127) / 128;
-  float m_run, l_run;
-  float acc[G][NDP][8];
-};
-
-template <int HD, int G, bool DB>
-__device__ __forceinline__ void attn_split(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
-                                           const f16* __restrict__ kb, const f16* __restrict__ vb,
-                                           int lo, int hi, float scale, int lane) {
-  constexpr int NKC = HD / 32;
-  constexpr int NDP = SplitState<HD, G>::NDP;
-  const int row = lane & 15;
-  const int grp = lane >> 4;
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < NDP; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss.acc[g][j][e] = 0.f;
-
-  f16x8 kf[NKC];
-  f16x8 vv[4][NDP];
-  auto load_tile = [&](int t0, f16x8 (&kd)[NKC], f16x8 (&vd)[4][NDP]) {
-    const int tk = min(t0 + row, hi - 1);
-    const f16* kp = kb + (long)tk * HD + 8 * grp;
-#pragma unroll
-    for (int i = 0; i < NKC; ++i) kd[i] = *(const f16x8*)(kp + 32 * i);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 4 * grp + rr;
-      const int tv = min(t, hi - 1);
-      const f16* vp = vb + (long)tv * HD + 8 * row;
-#pragma unroll
-      for (int j = 0; j < NDP; ++j) {
-        if (8 * (row + 16 * j) < HD && t < hi)
-          vd[rr][j] = *(const f16x8*)(vp + 128 * j);
-        else
-          vd[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-  };
-  if (lo < hi) load_tile(lo, kf, vv);
-
-  for (int t0 = lo; t0 < hi; t0 += 16) {
-    // double buffering (DB): the next tile's loads fly during this tile's math
-    f16x8 kn[NKC];
-    f16x8 vn[4][NDP];
-    if (DB && t0 + 16 < hi) load_tile(t0 + 16, kn, vn);
-    f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[i], qf[i], st, 0, 0, 0);
-
-    float sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 4 * grp + rr;
-      sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
-      mx = fmaxf(mx, sc[rr]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __expf(m_run - m_new);
-    float pr[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      pr[rr] = __expf(sc[rr] - m_new);
-      ps += pr[rr];
-    }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int src = 16 * grp + g;
-      const float ag = __shfl(alpha, src, 64);
-      float pg[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) pg[rr] = (float)(f16)__shfl(pr[rr], src, 64);
-#pragma unroll
-      for (int j = 0; j < NDP; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float a = ss.acc[g][j][e] * ag;
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)vv[rr][j][e];
-          ss.acc[g][j][e] = a;
-        }
-    }
-    if (t0 + 16 < hi) {
-      if (DB) {
-#pragma unroll
-        for (int i = 0; i < NKC; ++i) kf[i] = kn[i];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-          for (int j = 0; j < NDP; ++j) vv[rr][j] = vn[rr][j];
-      } else {
-        load_tile(t0 + 16, kf, vv);
-      }
-    }
-  }
-
-  // merge the four token phases (lane groups) of every d-chunk
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < NDP; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float a = ss.acc[g][j][e];
-        a += __shfl_xor(a, 16, 64);
-        a += __shfl_xor(a, 32, 64);
-        ss.acc[g][j][e] = a;
-      }
-  ss.m_run = m_run;
-  ss.l_run = l_run;
-}
-
-// Attended length of row r and the [lo, hi) token range of split sp (app/kernels.py:120-127).
-__device__ __forceinline__ void split_range(const int64_t* __restrict__ pos, int r, int L,
-                                            int nsplit, int sp, int& lo, int& hi) {
-  const long praw = pos[r];
-  const int ln = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));
-  const int per = (ln + nsplit - 1) / nsplit;
-  const int chunk = ((per + 15) / 16) * 16;
-  lo = sp * chunk;
-  hi = min(ln, lo + chunk);
-}
-
-// Q^T fragments of the G query heads of kv head kh (B operand: lane l holds head l & 15,
-// d-chunk 8 (l >> 4) + 32 i; zero for heads >= G).
-template <int HD, int G>
-__device__ __forceinline__ void load_q(f16x8 (&qf)[HD / 32], const f16* __restrict__ q, int r,
-                                       int Hq, int kh, int lane) {
-  const int row = lane & 15;
-  const int grp = lane >> 4;
-  const bool gv = row < G;
-  const f16* qp = q + ((long)r * Hq + kh * G + (gv ? row : 0)) * HD + 8 * grp;
-#pragma unroll
-  for (int i = 0; i < HD / 32; ++i) {
-    if (gv)
-      qf[i] = *(const f16x8*)(qp + 32 * i);
-    else
-      qf[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-  }
-}
 
 template <int HD, int G>
 __global__ __launch_bounds__(64) void decode_attn_kernel(
@@ -195,32 +36,22 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
   const int grp = lane >> 4;
   const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
   const int b = r / S;
-  int lo, hi;
-  split_range(pos, r, L, nsplit, sp, lo, hi);
   const long cbase = ((long)b * Hk + kh) * (long)L * HD;
+  // one split starts at slot 0: its first tile is loaded before the attended length is known
+  // (rows clamped to the cache, masked later), so the position read and the tile overlap
+  KVTile<HD> t;
+  if (nsplit == 1) kv_load<HD>(t, kc + cbase, vc + cbase, 0, L - 1, lane);
   f16x8 qf[HD / 32];
   load_q<HD, G>(qf, q, r, Hq, kh, lane);
+  int lo, hi;
+  split_range(pos, r, L, nsplit, sp, lo, hi);
+  if (nsplit != 1 && lo < hi) kv_load<HD>(t, kc + cbase, vc + cbase, lo, hi - 1, lane);
   SplitState<HD, G> ss;
-  attn_split<HD, G, (HD <= 128)>(ss, qf, kc + cbase, vc + cbase, lo, hi, scale, lane);
+  attn_run<HD, G, (HD <= 128)>(ss, qf, t, kc + cbase, vc + cbase, lo, hi, scale, lane);
 
   const long hbase = (long)r * Hq + kh * G;
   if (nsplit == 1) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float lg = __shfl(ss.l_run, g, 64);
-      if (grp == 0) {
-#pragma unroll
-        for (int j = 0; j < NDP; ++j) {
-          const int d = 8 * (row + 16 * j);
-          if (d < HD) {
-            f16x8 ov;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ov[e] = (f16)(ss.acc[g][j][e] / lg);
-            *(f16x8*)(o + (hbase + g) * HD + d) = ov;
-          }
-        }
-      }
-    }
+    attn_store_o<HD, G>(ss, o + hbase * HD, lane);
   } else {
     if (lane < G) {
       const long pidx = (hbase + lane) * nsplit + sp;

@@ -20,6 +20,8 @@ reference GPU default, app/engine.py:219-222) and live on a ROCm device.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _ffi

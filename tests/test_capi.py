@@ -81,3 +81,4 @@ def test_python_wrappers_refuse_cpu_tensors():
         int8_mm(x, w, s)
     with pytest.raises(RuntimeError):
         rms(x, torch.ones(64, dtype=torch.float16))
+
