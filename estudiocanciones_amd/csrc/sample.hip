@@ -8,8 +8,13 @@
 //   tok = argmax(p / q),  q ~ Exponential(1)             (first index on ties)
 //   the token is written for row n and, with CFG, for row n + N.
 //
-// One block of 1024 threads per take.  The k-th largest value is found by an exact 4-pass
-// radix select (8-bit digits) on order-preserving uint32 keys of the fp32 values in LDS.
+// One block of 1024 threads per take.  The k-th largest value comes from a two-pass radix select
+// (8-bit digits, LDS histograms) on order-preserving 16-bit keys of the fp16 logits: x =
+// fp32(l)/temp is strictly monotonic in l, so the threshold and its ties are those of l.  Only
+// the kept values (key >= threshold, k of them plus ties) reach the softmax and the race:
+// every other index has p = 0 exactly and can neither win nor change a sum.  The kept values
+// are compacted into LDS in (thread, slot) order by prefix sums, so their fp32 sums are formed
+// in a fixed order, and one wave finishes the softmax and the race without further barriers.
 // The Exponential(1) draws are q = -log(u), u = (bits >> 8 + 0.5) * 2^-24 from the
 // counter-based Philox4x32-10 generator (Salmon, Moraes, Dror, Shaw, "Parallel random
 // numbers: as easy as 1, 2, 3", SC 2011), keyed by a 64-bit seed read from device memory and
@@ -44,42 +49,8 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
   }
 }
 
-// Order-preserving key: larger float -> larger unsigned key (finite and -inf values).
-__device__ __forceinline__ uint32_t fkey(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float keyf(uint32_t k) {
-  const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
-  return __builtin_bit_cast(float, u);
-}
-
 constexpr int SMP_THREADS = 1024;
 constexpr int SMP_MAXV = 8704;  // LDS capacity in values (8197 codebook entries + slack)
-
-__device__ __forceinline__ float block_reduce_max(float v, float* red) {
-  v = wave_max(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int i = 1; i < SMP_THREADS / 64; ++i) r = fmaxf(r, red[i]);
-  return r;
-}
-
-__device__ __forceinline__ float block_reduce_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float r = 0.f;
-#pragma unroll
-  for (int i = 0; i < SMP_THREADS / 64; ++i) r += red[i];
-  return r;
-}
 
 // Order-preserving 16-bit key of an fp16 value (-0.0 must be canonicalised to +0.0 first so
 // that key order equals float comparison).
@@ -88,7 +59,8 @@ __device__ __forceinline__ uint32_t hkey(f16 h) {
   return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
 }
 
-constexpr int SMP_PER = (SMP_MAXV + SMP_THREADS - 1) / SMP_THREADS;  // values per thread
+constexpr int SMP_GRP = (SMP_MAXV + 8 * SMP_THREADS - 1) / (8 * SMP_THREADS);  // 8-value groups
+constexpr int SMP_PER = 8 * SMP_GRP;  // values per thread
 
 // Digit d (from the top) of the radix select: the largest digit whose cumulative count from
 // the top reaches `rank`.  Run by wave 0 over 256 bins; writes (prefix | d << shift, new rank).
@@ -125,36 +97,50 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
     const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
   __shared__ uint32_t hist[2][256];
-  __shared__ float red[SMP_THREADS / 64];
   __shared__ uint32_t sel[2];  // selected key prefix, remaining rank
-  __shared__ float bestv[SMP_THREADS / 64];
-  __shared__ int besti[SMP_THREADS / 64];
+  __shared__ uint32_t wtot[SMP_THREADS / 64];
+  __shared__ int kept_i[SMP_MAXV];
+  __shared__ float kept_x[SMP_MAXV];
 
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int wv = tid >> 6;
   const f16* lc = logits + (long)n * ld;
   const f16* lu = logits + (long)(n + N) * ld;
 
-  // 1. CFG mix in fp16 (values stay in registers: thread tid owns indices tid + 1024 j)
+  // 1. CFG mix in fp16.  Thread tid owns indices 8 tid + e + 8192 g (e < 8, g < SMP_GRP): the
+  //    loads are 16 bytes per lane where the row stride allows it.
   f16 lv[SMP_PER];
   uint32_t key[SMP_PER];
+  const bool vec = ((ld & 7) == 0) && ((((uintptr_t)logits) & 15) == 0);
 #pragma unroll
-  for (int j = 0; j < SMP_PER; ++j) {
-    const int i = tid + SMP_THREADS * j;
-    key[j] = 0u;
-    lv[j] = (f16)0.0f;
-    if (i < V) {
-      f16 l = lc[i];
+  for (int g = 0; g < SMP_GRP; ++g) {
+    const int i0 = 8 * tid + SMP_THREADS * 8 * g;
+    f16x8 c8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, u8 = c8;
+    if (vec && i0 + 7 < V) {
+      c8 = *(const f16x8*)(lc + i0);
+      if (cfg_on) u8 = *(const f16x8*)(lu + i0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (i0 + e < V) {
+          c8[e] = lc[i0 + e];
+          if (cfg_on) u8[e] = lu[i0 + e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = 8 * g + e;
+      f16 l = c8[e];
       if (cfg_on) {
-        const f16 u = lu[i];
-        const f16 d = l - u;
-        const f16 e = (f16)((float)d * cfg);
-        l = u + e;
+        const f16 d = l - u8[e];
+        const f16 m = (f16)((float)d * cfg);
+        l = u8[e] + m;
       }
       l = l + (f16)0.0f;  // -0.0 -> +0.0
       lv[j] = l;
-      key[j] = hkey(l);
+      key[j] = (i0 + e < V) ? hkey(l) : 0u;
     }
   }
   if (tid < 256) {
@@ -167,50 +153,70 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
   __syncthreads();
 
-  // 2. k-th largest fp16 value by a two-pass radix select on the 16-bit keys.  x = fp32(l)/temp
-  //    is strictly monotonic in l, so the threshold and the ties of the reference's fp32 topk
-  //    are those of l.
+  // 2. k-th largest fp16 value by a two-pass radix select on the 16-bit keys (key 0 marks an
+  //    index past V: hkey is nonzero for every fp16 value except the NaN pattern 0xFFFF)
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j)
-    if (tid + SMP_THREADS * j < V) atomicAdd(&hist[0][key[j] >> 8], 1u);
+    if (key[j]) atomicAdd(&hist[0][key[j] >> 8], 1u);
   __syncthreads();
   if (tid < 64) radix_pick(hist[0], sel, 0u, 8, lane);
   __syncthreads();
   const uint32_t hi8 = sel[0];
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j)
-    if (tid + SMP_THREADS * j < V && (key[j] & 0xFF00u) == hi8) atomicAdd(&hist[1][key[j] & 255u], 1u);
+    if (key[j] && (key[j] & 0xFF00u) == hi8) atomicAdd(&hist[1][key[j] & 255u], 1u);
   __syncthreads();
   if (tid < 64) radix_pick(hist[1], sel, hi8, 0, lane);
   __syncthreads();
   const uint32_t thr = sel[0];
 
-  // 3. masked logits / temp; log_softmax then softmax in fp32 (app/engine.py:293-296)
-  float xv[SMP_PER];
-  float mloc = -INFINITY;
+  // 3. compact the kept indices (key >= thr) in (thread, slot) order: a wave-level inclusive
+  //    scan of per-thread counts, then per-wave totals through LDS
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) cnt += (key[j] && key[j] >= thr) ? 1 : 0;
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) wtot[wv] = (uint32_t)incl;
+  __syncthreads();
+  int base = incl - cnt;
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) {
+    const int t = (int)wtot[w];
+    base += w < wv ? t : 0;
+    total += t;
+  }
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j) {
-    const bool in = tid + SMP_THREADS * j < V && key[j] >= thr;
-    xv[j] = in ? (float)lv[j] / temp : -INFINITY;
-    mloc = fmaxf(mloc, xv[j]);
+    if (key[j] && key[j] >= thr) {
+      kept_i[base] = 8 * tid + (j & 7) + SMP_THREADS * 8 * (j >> 3);
+      kept_x[base] = (float)lv[j] / temp;
+      ++base;
+    }
   }
-  const float m1 = block_reduce_max(mloc, red);
-  float sloc = 0.f;
-#pragma unroll
-  for (int j = 0; j < SMP_PER; ++j) sloc += expf(xv[j] - m1);
-  const float s1 = block_reduce_sum(sloc, red);
+  __syncthreads();
+  if (wv != 0) return;
+
+  // 4. wave 0: log_softmax then softmax in fp32 over the kept values (app/engine.py:293-296)
+  float m1 = -INFINITY;
+  for (int b = lane; b < total; b += 64) m1 = fmaxf(m1, kept_x[b]);
+  m1 = wave_max(m1);
+  float s1 = 0.f;
+  for (int b = lane; b < total; b += 64) s1 += expf(kept_x[b] - m1);
+  s1 = wave_sum(s1);
   const float logsum = logf(s1);
   // the maximum of ls = (x - m1) - logsum is exactly -logsum (at x = m1)
   const float m2 = 0.f - logsum;
-  float s2loc = 0.f;
-#pragma unroll
-  for (int j = 0; j < SMP_PER; ++j) {
-    xv[j] = (xv[j] - m1) - logsum;
-    s2loc += expf(xv[j] - m2);
-  }
-  const float s2 = block_reduce_sum(s2loc, red);
+  float s2 = 0.f;
+  for (int b = lane; b < total; b += 64) s2 += expf(((kept_x[b] - m1) - logsum) - m2);
+  s2 = wave_sum(s2);
 
-  // 4. exponential race: argmax p / q, q ~ Exp(1); draws for index i come from Philox block
+  // 5. exponential race: argmax p / q, q ~ Exp(1); draws for index i come from Philox block
   //    (i / 4, take, pos, salt), word i % 4 (or the injected noise)
   uint32_t k0 = 0u, k1 = 0u;
   uint64_t p64 = 0u;
@@ -222,30 +228,27 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
   float bv = -1.f;
   int bi = 0x7FFFFFFF;
-#pragma unroll
-  for (int j = 0; j < SMP_PER; ++j) {
-    const int i = tid + SMP_THREADS * j;
-    if (i < V) {
-      float q;
-      if (noise) {
-        q = noise[(long)n * V + i];
-      } else {
-        uint32_t c[4] = {(uint32_t)(i >> 2), (uint32_t)n, (uint32_t)p64,
-                         (uint32_t)(p64 >> 32) ^ ((uint32_t)salt << 20)};
-        philox4x32_10(c, k0, k1);
-        const uint32_t w = c[i & 3];
-        const float u = ((float)(w >> 8) + 0.5f) * (1.0f / 16777216.0f);
-        q = -logf(u);
-      }
-      const float p = expf(xv[j] - m2) / s2;
-      const float r = p / q;
-      if (r > bv || (r == bv && i < bi)) {
-        bv = r;
-        bi = i;
-      }
+  for (int b = lane; b < total; b += 64) {
+    const int i = kept_i[b];
+    float q;
+    if (noise) {
+      q = noise[(long)n * V + i];
+    } else {
+      uint32_t c[4] = {(uint32_t)(i >> 2), (uint32_t)n, (uint32_t)p64,
+                       (uint32_t)(p64 >> 32) ^ ((uint32_t)salt << 20)};
+      philox4x32_10(c, k0, k1);
+      const uint32_t w = c[i & 3];
+      const float u = ((float)(w >> 8) + 0.5f) * (1.0f / 16777216.0f);
+      q = -logf(u);
+    }
+    const float p = expf(((kept_x[b] - m1) - logsum) - m2) / s2;
+    const float r = p / q;
+    if (r > bv || (r == bv && i < bi)) {
+      bv = r;
+      bi = i;
     }
   }
-  // block argmax, lowest index on ties
+  // wave argmax, lowest index on ties
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, 64);
@@ -256,21 +259,8 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     }
   }
   if (lane == 0) {
-    bestv[tid >> 6] = bv;
-    besti[tid >> 6] = bi;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float v = bestv[0];
-    int ix = besti[0];
-    for (int w = 1; w < SMP_THREADS / 64; ++w) {
-      if (bestv[w] > v || (bestv[w] == v && besti[w] < ix)) {
-        v = bestv[w];
-        ix = besti[w];
-      }
-    }
-    out[(long)n * out_stride] = ix;
-    if (cfg_on) out[(long)(n + N) * out_stride] = ix;
+    out[(long)n * out_stride] = bi;
+    if (cfg_on) out[(long)(n + N) * out_stride] = bi;
   }
 }
 

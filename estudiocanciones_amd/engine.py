@@ -390,7 +390,7 @@ class HeartMuLaLite:
                             salt=i, noise=None if noise is None else noise[i])
             return samples[:, i:i + 1]
 
-        c0 = pick(0, self.c0_head(last_h))
+        c0 = pick(0, self._c0(last_h))
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
         h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
@@ -406,12 +406,24 @@ class HeartMuLaLite:
             return self.decoder.decode(x, pos, S, final_norm=False)
         return self.decoder.decode(x, pos, S)
 
+    def _logits(self, M, N):
+        """[M, N] fp16 logits whose rows start 128-byte aligned (the sampler loads 16 B/lane)."""
+        return torch.empty(M, -(-N // 64) * 64, device=self.dev, dtype=torch.float16)[:, :N]
+
+    def _c0(self, h):
+        """codebook0_head(h) into aligned logit rows."""
+        hd = self.c0_head
+        if hd.qp is not None and hd.sp is hd.s8:
+            return gemv_packed(h, hd.qp, hd.s8, hd.N, hd.K, out=self._logits(h.shape[0], hd.N),
+                               stream=hd.stream)
+        return hd(h)
+
     def _head(self, i, h):
         """audio_head[i](decoder.norm(h)) -- norm fused into the head GEMV when packed."""
         hd = self.audio_head[i]
         if hd.qp is not None and self.decoder.blocks and self.decoder.blocks[0].qkv.qp is not None:
             return rms_gemv_packed(h, self.decoder.norm, hd.qp, hd.s8, hd.N, hd.K,
-                                   stream=hd.stream)
+                                   stream=hd.stream, out=self._logits(h.shape[0], hd.N))
         return hd(h)
 
     def _project(self, tok, cb, even=None):

@@ -334,13 +334,16 @@ def gemv_packed(x, wp, s, N, K, res=None, out=None, stream=False):
     return y
 
 
-def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5, stream=False):
-    """int8_mm(rms(x, nw), w, s) in one kernel."""
+def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5, stream=False, out=None):
+    """int8_mm(rms(x, nw), w, s) in one kernel.  ``out``: optional [M, N] fp16 destination with
+    unit inner stride (any row stride)."""
     _check_x(x, K, "rms_gemv_packed")
     M = x.shape[0]
-    y = torch.empty(M, N, device=x.device, dtype=torch.float16)
+    y = out if out is not None else torch.empty(M, N, device=x.device, dtype=torch.float16)
+    if y.shape != (M, N) or y.dtype != torch.float16 or y.stride(1) != 1:
+        raise ValueError("rms_gemv_packed: out must be fp16 [M, N] with unit inner stride")
     _ffi.call("ecd_rms_gemv_i8p", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
-              s.data_ptr(), y.data_ptr(), N, M, N, K, _flags(M, stream), stream_ptr(x.device))
+              s.data_ptr(), y.data_ptr(), y.stride(0), M, N, K, _flags(M, stream), stream_ptr(x.device))
     return y
 
 

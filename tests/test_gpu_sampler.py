@@ -30,12 +30,16 @@ def test_sampler_matches_oracle_with_noise(dev, N, cfg_on, topk, temp):
         noise = g.exponential(1.0, (N, V)).astype(np.float32)
         lg = cfg_mix(logits, N, 1.5) if cfg_on else logits
         want = sample(lg.astype(np.float32), topk, temp, noise)[:, 0]
-        out = torch.full((B,), -1, dtype=torch.int64, device=dev)
-        sample_topk(T(logits, dev), N, 1.5, temp, topk, out, noise=T(noise, dev))
-        got = out.cpu().numpy()
-        assert np.array_equal(got[:N], want), (trial, got[:N], want)
-        if cfg_on:
-            assert np.array_equal(got[N:], got[:N])
+        # contiguous rows (odd stride: 2-byte loads) and 128-byte aligned rows (16-byte loads)
+        padded = torch.zeros(B, 8256, dtype=torch.float16, device=dev)
+        padded[:, :V] = T(logits, dev)
+        for lg_t in (T(logits, dev), padded[:, :V]):
+            out = torch.full((B,), -1, dtype=torch.int64, device=dev)
+            sample_topk(lg_t, N, 1.5, temp, topk, out, noise=T(noise, dev))
+            got = out.cpu().numpy()
+            assert np.array_equal(got[:N], want), (trial, lg_t.stride(0), got[:N], want)
+            if cfg_on:
+                assert np.array_equal(got[N:], got[:N])
 
 
 def test_sampler_threshold_ties_kept(dev):
