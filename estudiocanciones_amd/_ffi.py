@@ -26,8 +26,6 @@ SIGNATURES = {
     "ecd_decode_attn": [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
                         c_int, c_float, _P],
     "ecd_attn_combine": [_P, _P, _P, _P, c_int, c_int, c_int, _P],
-    "ecd_decode_attn_fused": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
-                              c_int, c_float, _P],
     "ecd_silu_mul": [_P, _P, c_int, c_int, _P],
     "ecd_embed_sum_i8": [_P, _P, _P, c_long, _P, c_int, c_int, c_int, c_int, _P],
     "ecd_embed_i8": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, c_int, c_int, _P],

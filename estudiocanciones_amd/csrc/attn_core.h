@@ -48,15 +48,76 @@ __device__ __forceinline__ void kv_load(KVTile<HD>& t, const f16* __restrict__ k
   }
 }
 
-// The split [lo, hi) given its first tile `cur` already loaded at lo.
-template <int HD, int G, bool DB>
-__device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
-                                         KVTile<HD>& cur, const f16* __restrict__ kb,
-                                         const f16* __restrict__ vb, int lo, int hi, float scale,
-                                         int lane) {
+// Online-softmax update of one 16-token tile starting at t0 (tokens >= hi masked).
+template <int HD, int G>
+__device__ __forceinline__ void attn_tile(SplitState<HD, G>& ss, float& m_run, float& l_run,
+                                          const f16x8 (&qf)[HD / 32], KVTile<HD>& cur, int t0,
+                                          int hi, float scale, int lane) {
   constexpr int NKC = HD / 32;
   constexpr int NDP = SplitState<HD, G>::NDP;
   const int grp = lane >> 4;
+  // V rows past the range contribute nothing (they may hold any bits, even NaN)
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr)
+    if (t0 + 4 * grp + rr >= hi)
+#pragma unroll
+      for (int j = 0; j < NDP; ++j) cur.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[i], qf[i], st, 0, 0, 0);
+
+  float sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int t = t0 + 4 * grp + rr;
+    sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
+    mx = fmaxf(mx, sc[rr]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = __expf(m_run - m_new);
+  float pr[4];
+  float ps = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    pr[rr] = __expf(sc[rr] - m_new);
+    ps += pr[rr];
+  }
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  l_run = l_run * alpha + ps;
+  m_run = m_new;
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int src = 16 * grp + g;
+    const float ag = __shfl(alpha, src, 64);
+    float pg[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) pg[rr] = (float)(f16)__shfl(pr[rr], src, 64);
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = ss.acc[g][j][e] * ag;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)cur.v[rr][j][e];
+        ss.acc[g][j][e] = a;
+      }
+  }
+}
+
+// The split [lo, hi) with its first tile already loaded (at lo) into ring[0].  RING tiles are
+// in flight: slot r holds tiles r, r + RING, ...; a slot is refilled as soon as its tile is
+// consumed, so the split costs about one memory round trip per RING tiles.
+template <int HD, int G, int RING>
+__device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                         KVTile<HD> (&ring)[RING], const f16* __restrict__ kb,
+                                         const f16* __restrict__ vb, int lo, int hi, float scale,
+                                         int lane) {
+  constexpr int NDP = SplitState<HD, G>::NDP;
   float m_run = -INFINITY;
   float l_run = 0.f;
 #pragma unroll
@@ -66,66 +127,18 @@ __device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss.acc[g][j][e] = 0.f;
 
-  for (int t0 = lo; t0 < hi; t0 += 16) {
-    // double buffering (DB): the next tile's loads fly during this tile's math
-    KVTile<HD> nxt;
-    if (DB && t0 + 16 < hi) kv_load<HD>(nxt, kb, vb, t0 + 16, hi - 1, lane);
-    // V rows past the range contribute nothing (they may hold any bits, even NaN)
+  const int ntiles = hi > lo ? (hi - lo + 15) / 16 : 0;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      if (t0 + 4 * grp + rr >= hi)
+  for (int r = 1; r < RING; ++r)
+    if (r < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
+  for (int base = 0; base < ntiles; base += RING) {
 #pragma unroll
-        for (int j = 0; j < NDP; ++j) cur.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[i], qf[i], st, 0, 0, 0);
-
-    float sc[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = t0 + 4 * grp + rr;
-      sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
-      mx = fmaxf(mx, sc[rr]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __expf(m_run - m_new);
-    float pr[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      pr[rr] = __expf(sc[rr] - m_new);
-      ps += pr[rr];
-    }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int src = 16 * grp + g;
-      const float ag = __shfl(alpha, src, 64);
-      float pg[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) pg[rr] = (float)(f16)__shfl(pr[rr], src, 64);
-#pragma unroll
-      for (int j = 0; j < NDP; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float a = ss.acc[g][j][e] * ag;
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) a += pg[rr] * (float)cur.v[rr][j][e];
-          ss.acc[g][j][e] = a;
-        }
-    }
-    if (t0 + 16 < hi) {
-      if (DB)
-        cur = nxt;
-      else
-        kv_load<HD>(cur, kb, vb, t0 + 16, hi - 1, lane);
+    for (int r = 0; r < RING; ++r) {
+      const int i = base + r;
+      if (i < ntiles) {
+        attn_tile<HD, G>(ss, m_run, l_run, qf, ring[r], lo + 16 * i, hi, scale, lane);
+        if (i + RING < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
+      }
     }
   }
 
@@ -145,13 +158,13 @@ __device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf
   ss.l_run = l_run;
 }
 
-template <int HD, int G, bool DB>
+template <int HD, int G, int RING>
 __device__ __forceinline__ void attn_split(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
                                            const f16* __restrict__ kb, const f16* __restrict__ vb,
                                            int lo, int hi, float scale, int lane) {
-  KVTile<HD> t;
-  if (lo < hi) kv_load<HD>(t, kb, vb, lo, hi - 1, lane);
-  attn_run<HD, G, DB>(ss, qf, t, kb, vb, lo, hi, scale, lane);
+  KVTile<HD> ring[RING];
+  if (lo < hi) kv_load<HD>(ring[0], kb, vb, lo, hi - 1, lane);
+  attn_run<HD, G, RING>(ss, qf, ring, kb, vb, lo, hi, scale, lane);
 }
 
 // Writes head g's normalised output o = acc / l as fp16 (lanes 0..15) to dst[g * HD + d].

@@ -22,6 +22,9 @@
 
 namespace ecd {
 
+// Tiles in flight per wave: four for head_dim <= 128, two for 256, one for wider heads.
+constexpr int attn_ring(int HD) { return HD <= 128 ? 4 : (HD <= 256 ? 2 : 1); }
+
 template <int HD, int G>
 __global__ __launch_bounds__(64) void decode_attn_kernel(
     const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
@@ -39,15 +42,15 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
   const long cbase = ((long)b * Hk + kh) * (long)L * HD;
   // one split starts at slot 0: its first tile is loaded before the attended length is known
   // (rows clamped to the cache, masked later), so the position read and the tile overlap
-  KVTile<HD> t;
-  if (nsplit == 1) kv_load<HD>(t, kc + cbase, vc + cbase, 0, L - 1, lane);
+  KVTile<HD> ring[attn_ring(HD)];
+  if (nsplit == 1) kv_load<HD>(ring[0], kc + cbase, vc + cbase, 0, L - 1, lane);
   f16x8 qf[HD / 32];
   load_q<HD, G>(qf, q, r, Hq, kh, lane);
   int lo, hi;
   split_range(pos, r, L, nsplit, sp, lo, hi);
-  if (nsplit != 1 && lo < hi) kv_load<HD>(t, kc + cbase, vc + cbase, lo, hi - 1, lane);
+  if (nsplit != 1 && lo < hi) kv_load<HD>(ring[0], kc + cbase, vc + cbase, lo, hi - 1, lane);
   SplitState<HD, G> ss;
-  attn_run<HD, G, (HD <= 128)>(ss, qf, t, kc + cbase, vc + cbase, lo, hi, scale, lane);
+  attn_run<HD, G, attn_ring(HD)>(ss, qf, ring, kc + cbase, vc + cbase, lo, hi, scale, lane);
 
   const long hbase = (long)r * Hq + kh * G;
   if (nsplit == 1) {
@@ -73,72 +76,6 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
         }
       }
     }
-  }
-}
-
-// Split attention and its log-sum-exp combine in one launch: one workgroup per (kv head, row),
-// NW waves; wave w computes splits w, w + NW, ... exactly as decode_attn_kernel does and leaves
-// its partials in LDS; after one workgroup barrier every thread merges the partials of one
-// (head, d) output the way attn_combine_kernel does.  The splits never leave the CU, so the
-// partial traffic and the combine launch disappear; the cost is that only R * Hk workgroups
-// share the chip, each streaming its (row, kv head)'s K and V through one CU.
-template <int HD, int G, int NW>
-__global__ __launch_bounds__(NW * 64) void decode_attn_fused_kernel(
-    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
-    const int64_t* __restrict__ pos, f16* __restrict__ o, int S, int Hq, int Hk, int L,
-    float scale, int nsplit) {
-  constexpr int NDP = SplitState<HD, G>::NDP;
-  extern __shared__ float smem[];
-  float* s_m = smem;                    // [nsplit][G]
-  float* s_l = smem + nsplit * G;       // [nsplit][G]
-  float* s_a = smem + 2 * nsplit * G;   // [nsplit][G][HD]
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int row = lane & 15;
-  const int grp = lane >> 4;
-  const int kh = blockIdx.x, r = blockIdx.y;
-  const int b = r / S;
-  const long cbase = ((long)b * Hk + kh) * (long)L * HD;
-  f16x8 qf[HD / 32];
-  load_q<HD, G>(qf, q, r, Hq, kh, lane);
-  for (int sp = wv; sp < nsplit; sp += NW) {
-    int lo, hi;
-    split_range(pos, r, L, nsplit, sp, lo, hi);
-    SplitState<HD, G> ss;
-    // double buffering only where the register budget of NW waves per CU allows it
-    attn_split<HD, G, (HD <= 128 && NW <= 8)>(ss, qf, kc + cbase, vc + cbase, lo, hi, scale, lane);
-    if (lane < G) {
-      s_m[sp * G + lane] = ss.m_run;
-      s_l[sp * G + lane] = ss.l_run;
-    }
-    if (grp == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < NDP; ++j) {
-          const int d = 8 * (row + 16 * j);
-          if (d < HD) {
-            float* dst = s_a + (sp * G + g) * HD + d;
-            *(f32x4*)dst = (f32x4){ss.acc[g][j][0], ss.acc[g][j][1], ss.acc[g][j][2], ss.acc[g][j][3]};
-            *(f32x4*)(dst + 4) = (f32x4){ss.acc[g][j][4], ss.acc[g][j][5], ss.acc[g][j][6], ss.acc[g][j][7]};
-          }
-        }
-    }
-  }
-  __syncthreads();
-  const long hbase = (long)r * Hq + kh * G;
-  for (int t = threadIdx.x; t < G * HD; t += NW * 64) {
-    const int g = t / HD, d = t - g * HD;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, s_m[sp * G + g]);
-    float den = 0.f, acc = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float m = s_m[sp * G + g];
-      const float w = m > -INFINITY ? __expf(m - M) : 0.f;
-      den += s_l[sp * G + g] * w;
-      acc += s_a[(sp * G + g) * HD + d] * w;
-    }
-    o[(hbase + g) * HD + d] = (f16)(acc / den);
   }
 }
 
@@ -223,69 +160,6 @@ static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* 
 #undef ECD_ATTN_G
 }
 
-constexpr int FUSED_MAXS = 32;
-constexpr int FUSED_LDS_MAX = 160 * 1024;
-
-template <int HD, int G, int NW>
-static int launch_fused_one(dim3 grid, size_t lds, hipStream_t st, const f16* q, const f16* kc,
-                            const f16* vc, const int64_t* pos, f16* o, int S, int Hq, int Hk,
-                            int L, float scale, int nsplit) {
-  // instantiated only where the per-wave register budget of NW waves per CU holds the split
-  // state without spilling (16 waves: 128 registers per lane; 8 waves: 256)
-  constexpr bool fits = NW == 16 ? (HD <= 128 && G <= 4) : !(HD == 256 && G == 8);
-  if constexpr (!fits) {
-    return ECD_ENOTSUP;
-  } else {
-  static bool attr = false;  // raise the dynamic LDS limit once per instantiation
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)decode_attn_fused_kernel<HD, G, NW>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             FUSED_LDS_MAX);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
-  hipLaunchKernelGGL((decode_attn_fused_kernel<HD, G, NW>), grid, dim3(NW * 64), lds, st, q, kc,
-                     vc, pos, o, S, Hq, Hk, L, scale, nsplit);
-  return ECD_OK;
-  }
-}
-
-template <int HD, int NW>
-static int launch_fused_hd(int G, dim3 grid, size_t lds, hipStream_t st, const f16* q,
-                           const f16* kc, const f16* vc, const int64_t* pos, f16* o, int S,
-                           int Hq, int Hk, int L, float scale, int nsplit) {
-  switch (G) {
-#define ECD_FUSED_G(G_) \
-  case G_:              \
-    return launch_fused_one<HD, G_, NW>(grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
-    ECD_FUSED_G(1)
-    ECD_FUSED_G(2)
-    ECD_FUSED_G(3)
-    ECD_FUSED_G(4)
-    ECD_FUSED_G(6)
-    ECD_FUSED_G(8)
-#undef ECD_FUSED_G
-    default:
-      return ECD_ENOTSUP;
-  }
-}
-
-template <int NW>
-static int launch_fused(int HD, int G, dim3 grid, size_t lds, hipStream_t st, const f16* q,
-                        const f16* kc, const f16* vc, const int64_t* pos, f16* o, int S, int Hq,
-                        int Hk, int L, float scale, int nsplit) {
-  switch (HD) {
-    case 64:
-      return launch_fused_hd<64, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
-    case 128:
-      return launch_fused_hd<128, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
-    case 256:
-      return launch_fused_hd<256, NW>(G, grid, lds, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale, nsplit);
-    default:
-      return ECD_ENOTSUP;
-  }
-}
-
 }  // namespace ecd
 
 using namespace ecd;
@@ -322,27 +196,6 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
     default:
       rc = ECD_ENOTSUP;
   }
-  if (rc != ECD_OK) return rc;
-  return ecd_launch_status();
-}
-
-int ecd_decode_attn_fused(const void* q, const void* kc, const void* vc, const int64_t* pos,
-                          void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
-                          int nw, float scale, void* stream) {
-  if (!q || !kc || !vc || !pos || !o || R <= 0 || S <= 0 || Hq <= 0 || Hk <= 0 || L <= 0 ||
-      HD <= 0 || nsplit <= 0 || nsplit > FUSED_MAXS || (Hq % Hk) != 0 ||
-      (nw != 0 && nw != 8 && nw != 16))
-    return ECD_EINVAL;
-  const int G = Hq / Hk;
-  const size_t lds = (size_t)nsplit * G * (HD + 2) * sizeof(float);
-  if (lds > (size_t)FUSED_LDS_MAX) return ECD_ENOTSUP;
-  if (nw == 0) nw = (nsplit > 8 && HD <= 128 && G <= 4) ? 16 : 8;
-  dim3 grid(Hk, R);
-  hipStream_t st = (hipStream_t)stream;
-  const f16 *qh = (const f16*)q, *kh = (const f16*)kc, *vh = (const f16*)vc;
-  const int rc = nw == 16
-                     ? launch_fused<16>(HD, G, grid, lds, st, qh, kh, vh, pos, (f16*)o, S, Hq, Hk, L, scale, nsplit)
-                     : launch_fused<8>(HD, G, grid, lds, st, qh, kh, vh, pos, (f16*)o, S, Hq, Hk, L, scale, nsplit);
   if (rc != ECD_OK) return rc;
   return ecd_launch_status();
 }

@@ -213,42 +213,6 @@ _attn_combine = _Launcher("_attn_combine", _attn_combine_impl,
                           lambda pm, pl, pa, o, HD=None, HDP=None, NSPLIT=16: (o.numel() // HD,))
 
 
-def attn_fused_waves(HD, G, nsplit, nw=0):
-    """Waves per workgroup ecd_decode_attn_fused runs (HD, G = Hq // Hk, nsplit) with, or 0 for
-    a shape it has no kernel for: 16 waves need HD <= 128 and G <= 4 (128 registers per
-    lane), 8 waves cover the rest except HD 256 with G 8; the partials must fit 160 KB of LDS."""
-    if nw == 0:
-        nw = 16 if (nsplit > 8 and HD <= 128 and G <= 4) else 8
-    ok = (HD in (64, 128, 256) and G in (1, 2, 3, 4, 6, 8) and 1 <= nsplit <= 32
-          and nsplit * G * (HD + 2) * 4 <= 160 * 1024
-          and ((HD <= 128 and G <= 4) if nw == 16 else (nw == 8 and not (HD == 256 and G == 8))))
-    return nw if ok else 0
-
-
-def attn_fused(q, kc, vc, pos, o, S, Hq, Hk, scale, nsplit=16, nw=0):
-    """_attn with NSPLIT=nsplit then _attn_combine, in one launch (one workgroup per
-    (kv head, row), the splits merged in LDS).  Returns False, launching nothing, for a shape
-    the one-launch kernel does not cover; the caller then uses the two-launch pair."""
-    dev = _dev(q, "attn_fused")
-    for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (o, "o")):
-        _f16(t, f"attn_fused {n}")
-        if not t.is_contiguous():
-            raise ValueError(f"attn_fused: {n} must be contiguous")
-    if pos.dtype != torch.int64 or not pos.is_contiguous():
-        raise TypeError("attn_fused: pos must be contiguous int64")
-    R = q.shape[0]
-    B, _, L, HD = kc.shape
-    if (q.numel() != R * Hq * HD or o.numel() != R * Hq * HD or pos.numel() != R
-            or kc.shape[1] != Hk or vc.shape != kc.shape or B * S < R or Hq % Hk):
-        raise ValueError("attn_fused: shape mismatch")
-    nw = attn_fused_waves(HD, Hq // Hk, nsplit, nw)
-    if not nw:
-        return False
-    _ffi.call("ecd_decode_attn_fused", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(),
-              o.data_ptr(), R, S, Hq, Hk, L, HD, int(nsplit), nw, float(scale), stream_ptr(dev))
-    return True
-
-
 # ---------------------------------------------------------------- SiLU(a) * b
 def _silu_mul_impl(x, y, F_, BLOCK=None):
     dev = _dev(x, "_silu_mul")

@@ -76,17 +76,6 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
 int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,
                      int nsplit, void* stream);
 
-/* ecd_decode_attn with nsplit splits followed by ecd_attn_combine, as one launch: one
- * workgroup per (kv head, row) whose waves compute the splits and merge them in LDS.  Same
- * split boundaries and merge as the two-launch pair (app/kernels.py:111-167, launched at
- * app/engine.py:194-204); writes o [R, Hq * HD] f16.
- *   nsplit in [1, 32]; nw = waves per workgroup (8 or 16, 0 = choose).  HD in {64, 128, 256}.
- *   Returns ECD_ENOTSUP for shapes it has no kernel for (nw = 16 with HD > 128 or
- *   Hq / Hk > 4; HD = 256 with Hq / Hk = 8); the two-launch pair covers those. */
-int ecd_decode_attn_fused(const void* q, const void* kc, const void* vc, const int64_t* pos,
-                          void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
-                          int nw, float scale, void* stream);
-
 /* y[r, c] = f16(f16(silu(x[r, c])) * x[r, F + c]) for x [R, 2F], y [R, F].
  * Replaces _silu_mul (app/kernels.py:171-180), launched at app/engine.py:209. */
 int ecd_silu_mul(const void* x, void* y, int R, int F, void* stream);

@@ -243,60 +243,6 @@ def test_decode_attn_split_invariance(dev):
         assert_close16(o, outs[0], what="split invariance")
 
 
-FUSED_ATTN_CASES = [
-    # R, S, Hq, Hk, HD, L, nsplit, nw
-    (8, 1, 24, 8, 128, 750, 16, 16),    # backbone shape (3 query heads per kv head)
-    (8, 1, 24, 8, 128, 750, 16, 8),
-    (2, 1, 24, 8, 128, 4096, 16, 0),
-    (4, 1, 8, 2, 128, 300, 7, 0),       # ragged split count, one wave idle
-    (3, 1, 6, 1, 64, 40, 32, 0),        # more splits than waves, empty splits
-    (4, 1, 16, 2, 128, 500, 16, 0),     # 8 query heads per kv head (8 waves)
-    (2, 1, 12, 2, 256, 333, 16, 0),
-    (4, 2, 8, 8, 64, 20, 2, 8),         # S = 2 rows per cache, G = 1
-    (2, 1, 8, 4, 128, 1, 16, 16),       # one attended slot
-]
-
-
-@pytest.mark.parametrize("R,S,Hq,Hk,HD,L,ns,nw", FUSED_ATTN_CASES)
-def test_decode_attn_fused(dev, R, S, Hq, Hk, HD, L, ns, nw):
-    """The one-launch split + combine equals the oracle's split attention and the exact softmax."""
-    import torch
-    from estudiocanciones_amd.kernels import attn_fused
-    B = R // S
-    q = randn16(60, R, Hq * HD)
-    kc = randn16(61, B, Hk, L, HD)
-    vc = randn16(62, B, Hk, L, HD)
-    g = rng(63)
-    if S == 1:
-        pos = g.integers(0, L, R).astype(np.int64)
-        pos[0] = L - 1
-    else:
-        pos = np.tile(np.arange(S, dtype=np.int64), B) + (L - S) // 2
-    want = OK.decode_attn_out(q, kc, vc, pos, S, Hq, Hk, HD, nsplit=ns)
-    o = torch.full((R, Hq * HD), float("nan"), dtype=torch.float16, device=dev)
-    assert attn_fused(T(q, dev), T(kc, dev), T(vc, dev), T(pos, dev), o, S, Hq, Hk,
-                      1.0 / math.sqrt(HD), nsplit=ns, nw=nw)
-    assert_close16(N(o), want, what=f"fused attn R={R} L={L} HD={HD} ns={ns} nw={nw}")
-    assert_close16(N(o), OK.attention_exact(q, kc, vc, pos, S, Hq, Hk, HD), what="vs exact softmax")
-
-
-def test_decode_attn_fused_unsupported_shapes_launch_nothing(dev):
-    """Shapes without a one-launch kernel return False (the caller uses the two-launch pair)."""
-    import torch
-    from estudiocanciones_amd.kernels import attn_fused, attn_fused_waves
-    assert attn_fused_waves(384, 2, 16) == 0
-    assert attn_fused_waves(256, 8, 16) == 0
-    assert attn_fused_waves(128, 8, 16, nw=16) == 0
-    assert attn_fused_waves(128, 3, 16) == 16 and attn_fused_waves(128, 6, 16) == 8
-    q = torch.zeros(2, 8 * 384, dtype=torch.float16, device=dev)
-    kc = torch.zeros(2, 4, 16, 384, dtype=torch.float16, device=dev)
-    o = torch.full_like(q, 7.0)
-    pos = torch.zeros(2, dtype=torch.int64, device=dev)
-    assert not attn_fused(q, kc, kc, pos, o, 1, 8, 4, 0.05, nsplit=16)
-    torch.cuda.synchronize()
-    assert bool((o == 7.0).all())
-
-
 # ---------------------------------------------------------------- SiLU * mul
 @pytest.mark.parametrize("R,F", [(8, 8192), (16, 8192), (2, 1000)])
 def test_silu_mul(dev, R, F):
