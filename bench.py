@@ -14,6 +14,11 @@ and a CPU baseline: the reference's CPU path (numpy float32 restatement) timed o
 sample of layers on the host cores and scaled to a frame.
 
     python bench.py [--steps K] [--warmup W] [--kv 750] [--decoder 1024|ref] [--no-cpu]
+
+HBM traffic of the GEMV family (``roofline.traffic``) comes from two rocprofv3 counter runs of
+this script with a calibration copy appended (``--copy-calib-mib``), summarised by
+``--pmc-summary FETCH_CSV WRITE_CSV`` into ``profiles/gemv_family_traffic.json``, which the
+timed run reads back.
 """
 from __future__ import annotations
 
@@ -25,6 +30,8 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "gemv_family_traffic.json")
 METRIC = "frames/s (3B backbone + 7 decoder passes) @ batch 8; decode-attn+GEMV HBM GB/s"
 
 
@@ -39,6 +46,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="append one ecd_copy_bytes of this many MiB (counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc counter_collection.csv files and exit")
     return ap.parse_args()
 
 
@@ -74,8 +85,46 @@ def time_graph(calls, torch, reps=20):
     return e0.elapsed_time(e1) / reps / len(calls)
 
 
+def pmc_summary(fetch_csv, write_csv, calib_mib):
+    """GEMV-family HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each
+    scaled by what the counter reads for the calibration copy of known size."""
+    import csv
+
+    def per_dispatch(path, counter):
+        rows = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = r["Dispatch_Id"]
+                e = rows.setdefault(key, [r["Kernel_Name"], 0.0])
+                e[1] += float(r["Counter_Value"])
+        return list(rows.values())
+
+    out = {}
+    for tag, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
+        rows = per_dispatch(path, counter)
+        gemv = [v for n, v in rows if "gemv_" in n]
+        copy = [v for n, v in rows if "copy_bytes_kernel" in n]
+        if not gemv or not copy:
+            raise SystemExit(f"{path}: no GEMV-family or calibration-copy dispatches with {counter}")
+        kib_copy = copy[-1]
+        factor = kib_copy / (calib_mib * 1024.0)
+        kib = sum(gemv) / len(gemv)
+        out[tag] = {"counter": counter, "gemv_dispatches": len(gemv),
+                    "kib_per_gemv_launch": round(kib, 1), "calib_copy_kib": round(kib_copy, 1),
+                    "calib_expected_kib": calib_mib * 1024, "factor": round(factor, 4),
+                    "bytes_per_gemv_launch": int(kib * 1024 / factor)}
+    out["traffic_bytes_per_launch"] = out["fetch"]["bytes_per_gemv_launch"] + \
+        out["write"]["bytes_per_gemv_launch"]
+    return out
+
+
 def main():
     args = parse()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calib_mib or 256), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the decode path has no "
                           "multi-GPU mode (takes would shard by data parallelism with no collectives)"}))
@@ -196,6 +245,19 @@ def main():
     bb_attn_gbps = (sum(attn_b[i] for i in bb_idx) / (bb_ms * len(bb_idx) * 1e-3) / 1e9) if bb_idx else None
     frame_bytes = sum(gemv_b) + sum(attn_b)
     launches = len(calls)
+    if args.copy_calib_mib > 0:
+        # calibration for the counter runs: one plain copy of known size, read once, written once
+        nb = args.copy_calib_mib << 20
+        src = torch.empty(nb, dtype=torch.int8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        _ffi.call("ecd_copy_bytes", src.data_ptr(), dst.data_ptr(), nb,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
 
     res = {
         "metric": METRIC,
@@ -227,7 +289,9 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(g_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per GEMV-family dispatch, "
+                               "copy-calibrated (profiles/gemv_family_traffic.json)") if traffic else None,
             "avg_launch_us": round(g_avg_us, 3),
             "algorithmic_bytes_per_launch": int(g_bytes_avg),
             "launches_per_frame": len(gemv_b),
