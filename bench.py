@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--prompt", type=int, default=256,
+                    help="prompt tokens of the timed prompt pass (0 skips it)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -254,6 +256,30 @@ def main():
         _ffi.call("ecd_copy_bytes", src.data_ptr(), dst.data_ptr(), nb,
                   torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
+    prompt = None
+    if args.prompt > 0 and args.prompt <= Lcap:
+        # prompt pass (runs after the frame measurements: it overwrites cache slots [0, P))
+        P = args.prompt
+        xp = torch.randn(B, P, bb["dim"], generator=g, device=dev).to(torch.float16)
+        pp = torch.arange(P, device=dev)[None].expand(B, P).contiguous()
+        model.backbone(xp, pp)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            model.backbone(xp, pp)
+        e1.record()
+        torch.cuda.synchronize()
+        p_ms = e0.elapsed_time(e1) / 3
+        hd = bb["dim"] // bb["heads"]
+        per_layer = 2 * B * P * sum(N * K for N, K in (
+            ((bb["heads"] + 2 * bb["kv_heads"]) * hd, bb["dim"]), (bb["dim"], bb["dim"]),
+            (2 * bb["ffn"], bb["dim"]), (bb["dim"], bb["ffn"])))
+        flops = per_layer * bb["layers"]
+        prompt = {"prompt_tokens": P, "rows": B * P, "ms": round(p_ms, 3),
+                  "gemm_flops": int(flops), "gemm_equivalent_TFLOPs": round(flops / p_ms / 1e9, 1),
+                  "frac_of_mfma_f16_peak": round(flops / p_ms / 1e9 / 2500.0, 4),
+                  "path": "MFMA GEMM (dense numerics) + decode-kernel causal attention, 28 layers"}
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -311,6 +337,7 @@ def main():
             "kernel_time_attn_ms": round(a_ms_total, 4),
             "library_launches": launches,
         },
+        "prompt_pass": prompt,
         "setup_s": round(t_build, 1),
     }
     if not args.no_cpu:

@@ -29,10 +29,12 @@ import torch
 
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
+                      gemm_packed, gemm_silu_packed,
                       gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms,
                       rms_gemv_packed, rms_qkv_rope, rms_w13_silu, sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
+PROMPT_GEMM_ROWS = 64  # prompt passes with more rows run the MFMA GEMM path
 N_CB = 8
 MUQ_DIM = 512
 DIM = 3072
@@ -195,8 +197,32 @@ class Stack:
         if mask is not None:
             raise NotImplementedError("explicit attention masks are not part of the fast path")
         B, S, D = x.shape
-        h = self.decode(x.reshape(B * S, D), pos.reshape(B * S).to(torch.int64).contiguous(), S)
+        x2 = x.reshape(B * S, D)
+        p2 = pos.reshape(B * S).to(torch.int64).contiguous()
+        if B * S > PROMPT_GEMM_ROWS and all(b.qkv.qp is not None for b in self.blocks):
+            h = self._prompt_pass(x2.contiguous(), p2, S)
+        else:
+            h = self.decode(x2, p2, S)
         return h.reshape(B, S, D)
+
+    def _prompt_pass(self, x, pos, S):
+        """Many rows (app/engine.py:123-153): every Linear runs the MFMA GEMM with the
+        reference's dense numerics (M > 16); RMSNorm, RoPE + cache write and the causal
+        attention (row r attends [0, pos[r]]) use the decode kernels."""
+        R = x.shape[0]
+        for b in self.blocks:
+            Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
+            qkv = gemm_packed(krms(x, b.n1), b.qkv.qp, b.qkv.sp, b.qkv.N, b.qkv.K)
+            q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
+            _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
+                                      HD=HD, HALF=next_power_of_2(HD // 2))
+            # one split per row: a prompt row attends at most the prompt (no empty splits, no
+            # combine pass); the rows themselves give the parallelism
+            o = self._attention(b, q, pos, S, 1)
+            x = gemm_packed(o, b.o.qp, b.o.sp, b.o.N, b.o.K, res=x)
+            mm = gemm_silu_packed(krms(x, b.n2), b.w13.qp, b.w13.sp, b.w13.N // 2, b.w13.K)
+            x = gemm_packed(mm, b.w2.qp, b.w2.sp, b.w2.N, b.w2.K, res=x)
+        return krms(x, self.norm)
 
     def decode(self, x, pos, S, final_norm=True):
         """Fast path for few rows (app/engine.py:180-211): x [R, D] with R = B*S (row r -> batch

@@ -298,6 +298,33 @@ def gemv_packed(x, wp, s, N, K, res=None, out=None, stream=False):
     return y
 
 
+def gemm_packed(x, wp, s, N, K, res=None):
+    """int8_mm(x, w, s, res) for many rows (the dense numerics, y = fp16(x @ fp16(q * s)^T))
+    on packed weights, tiled on MFMA; ``res`` is added in fp16."""
+    _check_x(x, K, "gemm_packed")
+    M = x.shape[0]
+    y = torch.empty(M, N, device=x.device, dtype=torch.float16)
+    if res is not None:
+        _f16(res, "gemm_packed res")
+        if res.shape != (M, N) or res.stride(1) != 1:
+            raise ValueError("gemm_packed: res must be [M, N] with unit inner stride")
+    _ffi.call("ecd_gemm_i8p", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(), _ptr(res),
+              res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0), M, N, K,
+              stream_ptr(x.device))
+    return y
+
+
+def gemm_silu_packed(x, wp, s, F, K):
+    """_silu_mul(int8_mm(x, w1|w3, s)) for many rows on row-interleaved packed w1|w3
+    (pack_i8(..., interleave=True)) -> [M, F]."""
+    _check_x(x, K, "gemm_silu_packed")
+    M = x.shape[0]
+    mm = torch.empty(M, F, device=x.device, dtype=torch.float16)
+    _ffi.call("ecd_gemm_i8p_silu", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(),
+              mm.data_ptr(), mm.stride(0), M, F, K, stream_ptr(x.device))
+    return mm
+
+
 def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5, stream=False, out=None):
     """int8_mm(rms(x, nw), w, s) in one kernel.  ``out``: optional [M, N] fp16 destination with
     unit inner stride (any row stride)."""

@@ -166,6 +166,20 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
                        const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream);
 
+/* Prompt-pass GEMM (many rows) on packed weights: y = fp16(x @ fp16(q * s)^T) (+ res as an
+ * fp16 add) -- the dense numerics of int8_mm for M > 16 (app/kernels.py:46-49), used by the
+ * prompt pass (app/engine.py:123-153, 174-178).  MFMA-tiled 128 x 128 per workgroup.
+ *   x [M, K] fp16 (row stride ldx, 16-byte aligned, K % 64 == 0); wp = ecd_pack_i8(w);
+ *   s [N] fp16; res [M, N] (row stride ldr) or NULL; y [M, N] (row stride ldy). */
+int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const void* res,
+                 long ldr, void* y, long ldy, int M, int N, int K, void* stream);
+
+/* The same GEMM on row-interleaved w1|w3 (ecd_pack_i8 with interleave) with the SiLU * mul
+ * epilogue: mm[m, j] = fp16(fp16(silu(a_j)) * b_j), a/b the GEMM outputs of rows 2j / 2j + 1
+ * (app/engine.py:152-153, app/kernels.py:171-180).  mm [M, F] (row stride ldm). */
+int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,
+                      long ldm, int M, int F, int K, void* stream);
+
 /* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
  * counterpart: a kernel of known HBM traffic used to calibrate hardware byte counters. */
 int ecd_copy_bytes(const void* src, void* dst, long nbytes, void* stream);

@@ -79,6 +79,35 @@ def test_rms_gemv_packed_shapes(dev, M, N, K):
     assert_close16(N_(y), OK.gemv_i8(OK.rms(x, nw), q, s), what=f"rms+gemv M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,N,K,res", [(17, 100, 64, True), (128, 1000, 1024, False),
+                                       (300, 3072, 1024, True), (512, 1536, 3072, False),
+                                       (129, 257, 192, True)])
+def test_gemm_packed_dense_numerics(dev, M, N, K, res):
+    """The prompt-pass GEMM: the dense numerics (fp16(q * s) weights, fp32 sums) of int8_mm for
+    M > 16, ragged M and N, residual added in fp16."""
+    from estudiocanciones_amd.kernels import gemm_packed, pack_i8
+    q, s = qweights(30 + K, N, K)
+    x = randn16(31 + M, M, K)
+    r = randn16(32 + M, M, N) if res else None
+    y = gemm_packed(T(x, dev), pack_i8(T(q, dev)), T(s, dev), N, K, T(r, dev) if res else None)
+    want = OK.gemv_i8(x, q, s, r)  # M > 16: the oracle's dense numerics
+    assert_close16(N_(y), want, what=f"gemm M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M,F,K", [(96, 512, 256), (2048, 8192, 1024)])
+def test_gemm_silu_packed(dev, M, F, K):
+    """GEMM on row-interleaved w1|w3 with the SiLU * mul epilogue vs silu_mul(int8_mm(...))."""
+    import torch
+    from estudiocanciones_amd.kernels import gemm_silu_packed, pack_i8
+    q, s = qweights(40 + F, 2 * F, K)
+    x = randn16(41 + M, M, K, std=0.5)
+    st = T(s, dev)
+    sp = torch.stack([st[:F], st[F:]], 1).reshape(-1).contiguous()
+    mm = gemm_silu_packed(T(x, dev), pack_i8(T(q, dev), True), sp, F, K)
+    want = OK.silu_mul(OK.gemv_i8(x, q, s))
+    assert_close16(N_(mm), want, what=f"gemm+silu M={M} F={F}")
+
+
 def test_rms_gemv_packed(dev):
     from estudiocanciones_amd.kernels import pack_i8, rms_gemv_packed
     M, N, K = 8, 8197, 3072

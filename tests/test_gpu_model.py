@@ -182,12 +182,14 @@ def test_graph_replay_matches_eager(dev):
             assert torch.equal(a, b)
 
 
-def test_prefill_matches_oracle(dev):
-    """Prompt pass (B=2, P=12) through the decode kernels vs the oracle's causal prefill."""
+@pytest.mark.parametrize("P", [12, 48])
+def test_prefill_matches_oracle(dev, P):
+    """Prompt pass (B=2) vs the oracle's causal prefill: 24 rows run the decode kernels, 96 rows
+    the MFMA GEMM path (more than 64 rows)."""
     import torch
     bb, dec = tiny_cfgs()
-    om, gm = build_pair(dev, bb, dec, 1, 32, seed=3)
-    B, P, D = gm.B, 12, bb["dim"]
+    om, gm = build_pair(dev, bb, dec, 1, 64, seed=3)
+    B, D = gm.B, bb["dim"]
     x = randn16(8, B, P, D)
     pos = np.arange(P, dtype=np.int64)
     want = om.backbone.prefill(x, pos)
