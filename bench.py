@@ -206,7 +206,8 @@ def main():
     torch.cuda.synchronize()
 
     def gemv_family_bytes(name, a):
-        if name in ("ecd_gemv_i8", "ecd_gemv_i8p"):
+        if name in ("ecd_gemv_i8", "ecd_gemv_i8p", "ecd_gemv_i8p_splitk"):
+            # (the split-K variant's fp32 partials are workspace traffic, not algorithmic bytes)
             M, N, K = a[8], a[9], a[10]
             return N * K + 2 * N + 2 * M * K + 2 * M * N + (2 * M * N if a[4] else 0)
         if name == "ecd_rms_gemv_i8p":

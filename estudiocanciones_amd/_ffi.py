@@ -34,6 +34,8 @@ SIGNATURES = {
     "ecd_sample_topk": [_P, c_long, c_int, c_int, c_float, c_float, c_int, c_int, _P, _P, _P, c_int,
                         _P, c_long, _P],
     "ecd_copy_bytes": [_P, _P, c_long, _P],
+    "ecd_gemv_i8p_splitk": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int,
+                            _P, c_int, _P],
     "ecd_gemm_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_i8p_silu": [_P, c_long, _P, _P, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_packed_bytes": [c_int, c_int],

@@ -22,12 +22,14 @@
 //              (app/kernels.py:78-107 applied to the fp16 GEMV output)
 //   EPI_SILU   rows interleaved (w1 row j at 2j, w3 row j at 2j+1): mm[j] = fp16(fp16(silu(a)) * b)
 //              (app/kernels.py:171-180 applied to the fp16 GEMV outputs)
+//   EPI_PARTIAL split K: block z writes its fp32 sums to ws[z][M][N]; splitk_reduce_kernel adds
+//              the splits in order and applies the scale and residual of EPI_STORE
 #include "common.h"
 
 namespace ecd {
 
 enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED = 2 };
-enum { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2 };
+enum { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_PARTIAL = 3 };
 
 struct GemvArgs {
   // prologue
@@ -63,6 +65,9 @@ struct GemvArgs {
   int S, Hq, Hk, L, HD;
   // EPI_SILU
   f16* mm;
+  // EPI_PARTIAL: ks K-splits (blockIdx.z), fp32 partial sums [ks][M][N]
+  float* ws;
+  int ks;
 };
 
 __device__ __forceinline__ f16x8 ld8(const f16* p) { return *(const f16x8*)p; }
@@ -120,6 +125,13 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n0, int m0,
   if (me >= M) return;
   const int nb = n0 + 16 * t + 4 * (l >> 4);
   if (nb >= N) return;
+  if constexpr (EPI == EPI_PARTIAL) {
+    float* dst = a.ws + ((long)blockIdx.z * M + me) * N + nb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (nb + r < N) dst[r] = acc4[r];
+    return;
+  }
   f16 yv[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) yv[r] = (f16)(dense ? acc4[r] : acc4[r] * (float)e.s[r]);
@@ -549,8 +561,10 @@ __global__ __launch_bounds__(KW * 64) void gemv_xreg_kernel(const GemvArgs a) {
   const int K = a.K, M = a.M, N = a.N;
   const int nch = K >> 6;
   const int ntiles = (N + 15) >> 4;
-  const int c0 = (nch * wv) / KW;
-  const int nc = (nch * (wv + 1)) / KW - c0;
+  // K-split (EPI_PARTIAL): block z covers chunks [z nchs, (z + 1) nchs); host: nch % ks == 0
+  const int nchs = EPI == EPI_PARTIAL ? nch / a.ks : nch;
+  const int c0 = (EPI == EPI_PARTIAL ? (int)blockIdx.z * nchs : 0) + (nchs * wv) / KW;
+  const int nc = (nchs * (wv + 1)) / KW - (nchs * wv) / KW;
   const bool dense = a.dense != 0;
 
   // Issue order matters: loads complete in order for the wait counters, so the norm weights
@@ -678,7 +692,7 @@ constexpr int xreg_maxc(int NT, int KW, int PRO) {
 template <int NT, int KW, int PRO, int EPI, bool NTL, int MAXC>
 static int launch_xreg_one(const GemvArgs& a, hipStream_t st) {
   const int ntiles = (a.N + 15) / 16;
-  dim3 grid((ntiles + NT - 1) / NT, (a.M + 15) / 16);
+  dim3 grid((ntiles + NT - 1) / NT, (a.M + 15) / 16, EPI == EPI_PARTIAL ? a.ks : 1);
   const unsigned lds = KW * NT * 64 * 16 + KW * 64 + (PRO == PRO_RMS ? a.K * 2 : 0);
   // weight chunks in flight per wave: 16 KB (NT = 4 reads four tiles per chunk)
   constexpr int LA = NT >= 4 ? 4 : 16;
@@ -693,7 +707,7 @@ static int launch_xreg(const GemvArgs& a, hipStream_t st) {
   if constexpr (PRO == PRO_EMBED || (PRO == PRO_RMS && KW != 8)) {
     return 1;
   } else {
-    const int nch = a.K >> 6;
+    const int nch = (a.K >> 6) / (EPI == EPI_PARTIAL ? a.ks : 1);
     const int cpw = (nch + KW - 1) / KW;
     // Measured on every frame shape (MI355X): register x wins for the plain prologue at every
     // K and for the RMS prologue with 8 waves and at most two chunks per wave (K <= 1024); the
@@ -802,6 +816,40 @@ static int launch(const GemvArgs& a, Cfg c, hipStream_t st) {
   return a.stream_hint ? launch_ntl<PRO, EPI, true>(a, c, st) : launch_ntl<PRO, EPI, false>(a, c, st);
 }
 
+// y[m, n] = fp16(sum_z ws[z][m][n] * s[n]) (dense: fp16(sum_z ws)), then + res as an fp16 add
+// (the EPI_STORE numerics of the unsplit GEMV, with the K sum formed split by split in order).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int ks,
+                                                            const f16* __restrict__ s,
+                                                            const f16* __restrict__ res, long ldr,
+                                                            f16* __restrict__ y, long ldy, int M,
+                                                            int N, int dense) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (long)m * N);
+  float acc = 0.f;
+  for (int z = 0; z < ks; ++z) acc += ws[(long)z * M * N + i];
+  f16 o = (f16)(dense ? acc : acc * (float)s[n]);
+  if (res) o = o + res[(long)m * ldr + n];
+  y[(long)m * ldy + n] = o;
+}
+
+template <bool NTL>
+static int launch_splitk(const GemvArgs& a, Cfg c, hipStream_t st) {
+  int rc = 1;
+#define ECD_SK(NT_, KW_) \
+  if (c.nt == NT_ && c.kw == KW_) rc = launch_xreg<NT_, KW_, PRO_PLAIN, EPI_PARTIAL, NTL>(a, st);
+  ECD_SK(1, 16)
+  ECD_SK(2, 16)
+  ECD_SK(4, 8)
+#undef ECD_SK
+  if (rc == 1) return ECD_ENOTSUP;
+  if (rc != ECD_OK) return rc;
+  const long n = (long)a.M * a.N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     a.ws, a.ks, a.s, a.res, a.ldr, a.y, a.ldy, a.M, a.N, a.dense);
+  return ecd_launch_status();
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace ecd
@@ -841,6 +889,21 @@ int ecd_gemv_i8p(const void* x, long ldx, const void* wp, const void* s, const v
   if (nt > 0) c.nt = nt;
   if (kw > 0) c.kw = kw;
   return launch<PRO_PLAIN, EPI_STORE>(a, c, (hipStream_t)stream);
+}
+
+int ecd_gemv_i8p_splitk(const void* x, long ldx, const void* wp, const void* s, const void* res,
+                        long ldr, void* y, long ldy, int M, int N, int K, int ks, float* ws,
+                        int flags, void* stream) {
+  GemvArgs a = {};
+  a.x = (const f16*)x; a.ldx = ldx; a.wp = (const int8_t*)wp; a.s = (const f16*)s;
+  a.M = M; a.N = N; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1;
+  a.res = (const f16*)res; a.ldr = ldr; a.y = (f16*)y; a.ldy = ldy; a.ws = ws; a.ks = ks;
+  if (check_common(a) || !x || !y || !ws || ldx < K || (ldx % 8) || !aligned16(x) || ldy < N ||
+      (res && ldr < N) || ks < 1 || ((K / 64) % ks))
+    return ECD_EINVAL;
+  const Cfg c = pick(N, K);
+  return a.stream_hint ? launch_splitk<true>(a, c, (hipStream_t)stream)
+                       : launch_splitk<false>(a, c, (hipStream_t)stream);
 }
 
 int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const void* wp,

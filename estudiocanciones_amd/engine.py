@@ -29,7 +29,7 @@ import torch
 
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
-                      gemm_packed, gemm_silu_packed,
+                      gemm_packed, gemm_silu_packed, gemv_packed_splitk,
                       gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms,
                       rms_gemv_packed, rms_qkv_rope, rms_w13_silu, sample_topk, stream_ptr)
 
@@ -70,6 +70,7 @@ class Linear:
         self.qp = self.sp = None
         self.N, self.K = q8.shape
         self.stream = False
+        self.ks = 1
 
     def pack(self, interleave=False, stream=False):
         """Add the lane-ordered tile copy used by the fused GEMVs (K % 64 == 0).  With
@@ -79,6 +80,9 @@ class Linear:
         if self.K % 64:
             return self
         self.qp = pack_i8(self.q8, interleave)
+        # few output tiles over a long K: split K over 4 workgroups per tile
+        if (self.N + 15) // 16 <= 64 and self.K >= 4096 and (self.K // 64) % 4 == 0:
+            self.ks = 4
         if interleave:
             F = self.N // 2
             self.sp = torch.stack([self.s8[:F], self.s8[F:]], 1).reshape(-1).contiguous()
@@ -89,6 +93,9 @@ class Linear:
     def __call__(self, x, res=None):
         if self.qp is not None and self.sp is self.s8 and x.dim() == 2 and x.stride(1) == 1 \
                 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0:
+            if self.ks > 1:
+                return gemv_packed_splitk(x, self.qp, self.s8, self.N, self.K, self.ks, res,
+                                          stream=self.stream)
             return gemv_packed(x, self.qp, self.s8, self.N, self.K, res, stream=self.stream)
         return int8_mm(x, self.q8, self.s8, res)
 

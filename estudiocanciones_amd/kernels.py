@@ -298,6 +298,24 @@ def gemv_packed(x, wp, s, N, K, res=None, out=None, stream=False):
     return y
 
 
+def gemv_packed_splitk(x, wp, s, N, K, ks, res=None, stream=False):
+    """gemv_packed with K split over ``ks`` workgroups per tile (fp32 partial sums added in a
+    fixed order by a second kernel): for few output tiles over a long K, where one workgroup
+    per tile leaves most CUs idle.  Same numerics up to the fp32 summation order."""
+    _check_x(x, K, "gemv_packed_splitk")
+    M = x.shape[0]
+    y = torch.empty(M, N, device=x.device, dtype=torch.float16)
+    ws = torch.empty(ks * M * N, device=x.device, dtype=torch.float32)
+    if res is not None:
+        _f16(res, "gemv_packed_splitk res")
+        if res.shape != (M, N) or res.stride(1) != 1:
+            raise ValueError("gemv_packed_splitk: res must be [M, N] with unit inner stride")
+    _ffi.call("ecd_gemv_i8p_splitk", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(),
+              _ptr(res), res.stride(0) if res is not None else 0, y.data_ptr(), y.stride(0), M, N,
+              K, int(ks), ws.data_ptr(), _flags(M, stream), stream_ptr(x.device))
+    return y
+
+
 def gemm_packed(x, wp, s, N, K, res=None):
     """int8_mm(x, w, s, res) for many rows (the dense numerics, y = fp16(x @ fp16(q * s)^T))
     on packed weights, tiled on MFMA; ``res`` is added in fp16."""

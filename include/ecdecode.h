@@ -138,6 +138,16 @@ int ecd_pack_i8(const void* w, int N, int K, int interleave, void* out, void* st
 int ecd_gemv_i8p(const void* x, long ldx, const void* wp, const void* s, const void* res, long ldr,
                  void* y, long ldy, int M, int N, int K, int flags, int nt, int kw, void* stream);
 
+/* ecd_gemv_i8p with K split over ks workgroups per 16-row tile: each writes fp32 partial sums
+ * into the caller's workspace ws [ks, M, N], and a second kernel adds them in split order and
+ * applies the scale and residual of ecd_gemv_i8p (same rounding points; the fp32 sum is formed
+ * split by split).  For shapes with few output tiles over a long K, where one workgroup per
+ * tile leaves most CUs idle (the decoder's w2: N = 1024, K = 8192).  Replaces int8_mm with
+ * residual (app/kernels.py:40-54) at app/engine.py:210.  Requires (K / 64) % ks == 0. */
+int ecd_gemv_i8p_splitk(const void* x, long ldx, const void* wp, const void* s, const void* res,
+                        long ldr, void* y, long ldy, int M, int N, int K, int ks, float* ws,
+                        int flags, void* stream);
+
 /* y = int8_mm(rms(x, nw, eps), w, s): rms (app/kernels.py:58-74) fused as the GEMV prologue
  * -- the final norm + head of Stack.decode / _frame_fast (app/engine.py:211, :333, :339). */
 int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const void* wp,

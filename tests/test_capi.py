@@ -52,6 +52,7 @@ def test_signatures_match_header_arity():
     lambda L: L.ecd_decode_attn(8, 8, 8, 8, 8, None, None, None, 1, 1, 8, 2, 8, 128, 16, 0.1, None),
     lambda L: L.ecd_decode_attn(8, 8, 8, 8, None, None, None, None, 1, 1, 8, 2, 8, 128, 1, 0.1, None),
     lambda L: L.ecd_attn_combine(None, None, None, None, 1, 128, 16, None),
+    lambda L: L.ecd_gemv_i8p_splitk(16, 64, 16, 16, None, 0, 16, 64, 1, 64, 192, 2, 16, 0, None),  # 3 chunks % 2
     lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
     lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0

@@ -79,6 +79,20 @@ def test_rms_gemv_packed_shapes(dev, M, N, K):
     assert_close16(N_(y), OK.gemv_i8(OK.rms(x, nw), q, s), what=f"rms+gemv M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,N,K,ks,res", [(8, 1024, 8192, 4, True), (16, 1024, 8192, 4, False),
+                                          (8, 100, 4096, 2, True), (20, 300, 2048, 8, True),
+                                          (3, 64, 1024, 16, False)])
+def test_gemv_packed_splitk(dev, M, N, K, ks, res):
+    """K split over ks workgroups (fp32 partials, in-order reduction) vs the oracle; M > 16 keeps
+    the dense numerics."""
+    from estudiocanciones_amd.kernels import gemv_packed_splitk, pack_i8
+    q, s = qweights(50 + ks, N, K)
+    x = randn16(51 + M, M, K)
+    r = randn16(52 + M, M, N) if res else None
+    y = gemv_packed_splitk(T(x, dev), pack_i8(T(q, dev)), T(s, dev), N, K, ks, T(r, dev) if res else None)
+    assert_close16(N_(y), OK.gemv_i8(x, q, s, r), what=f"splitk M={M} N={N} K={K} ks={ks}")
+
+
 @pytest.mark.parametrize("M,N,K,res", [(17, 100, 64, True), (128, 1000, 1024, False),
                                        (300, 3072, 1024, True), (512, 1536, 3072, False),
                                        (129, 257, 192, True)])
