@@ -64,6 +64,45 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Wave-wide scans and reductions on the VALU with DPP (no LDS crossbar round trips): row_shr
+// 1, 2, 4, 8 inside each 16-lane row, then row_bcast:15 into rows 1 and 3 and row_bcast:31 into
+// rows 2 and 3.  Lane l ends with the inclusive result over lanes 0..l; lanes whose DPP source
+// is outside the row take `fill`, the operation's identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x, uint32_t fill, Op op) {
+  x = op(x, dpp_u32<0x111, 0xF>(x, fill));
+  x = op(x, dpp_u32<0x112, 0xF>(x, fill));
+  x = op(x, dpp_u32<0x114, 0xF>(x, fill));
+  x = op(x, dpp_u32<0x118, 0xF>(x, fill));
+  x = op(x, dpp_u32<0x142, 0xA>(x, fill));
+  x = op(x, dpp_u32<0x143, 0xC>(x, fill));
+  return x;
+}
+__device__ __forceinline__ uint32_t wave_incl_add_u32(uint32_t x) {
+  return wave_incl_scan_u32(x, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+// reductions: the result in every lane (read from lane 63)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = wave_incl_scan_u32(x, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = wave_incl_scan_u32(x, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+// fp32 sum in the scan's fixed order
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  const uint32_t r = wave_incl_scan_u32(
+      __builtin_bit_cast(uint32_t, v), 0u, [](uint32_t a, uint32_t b) {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b));
+      });
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)r, 63));
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
 __device__ __host__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);

@@ -8,13 +8,19 @@
 //   tok = argmax(p / q),  q ~ Exponential(1)             (first index on ties)
 //   the token is written for row n and, with CFG, for row n + N.
 //
-// One block of 1024 threads per take.  The k-th largest value comes from a two-pass radix select
-// (8-bit digits, LDS histograms) on order-preserving 16-bit keys of the fp16 logits: x =
-// fp32(l)/temp is strictly monotonic in l, so the threshold and its ties are those of l.  Only
-// the kept values (key >= threshold, k of them plus ties) reach the softmax and the race:
-// every other index has p = 0 exactly and can neither win nor change a sum.  The kept values
-// are compacted into LDS in (thread, slot) order by prefix sums, so their fp32 sums are formed
-// in a fixed order, and one wave finishes the softmax and the race without further barriers.
+// One block of 1024 threads per take; the selection works on order-preserving 16-bit keys of the
+// fp16 logits: x = fp32(l)/temp is strictly monotonic in l, so the threshold and its ties are
+// those of l.  Only the kept values (key >= threshold, k of them plus ties) reach the softmax
+// and the race: every other index has p = 0 exactly and can neither win nor change a sum.
+//   - The k-th largest key: the block's largest key fixes a window of the 16 top-byte digits
+//     below it (about 4 octaves); one LDS bin per key of the window (4096) counts the keys that
+//     fall there (fine bins: the atomics rarely collide), and wave 0 walks the bins from the
+//     top until the count reaches k.  When fewer than k keys lie in the window, a two-pass
+//     radix select over all keys (8-bit digits) finds the threshold instead.
+//   - The kept values land in LDS in descending key order (first slot of each key from the
+//     walk, then one atomic per value).  Values with equal keys are equal, so the fp32 sums
+//     below see the same sequence of numbers whatever the order among them: results are
+//     deterministic.  One wave finishes the softmax and the race without further barriers.
 // The Exponential(1) draws are q = -log(u), u = (bits >> 8 + 0.5) * 2^-24 from the
 // counter-based Philox4x32-10 generator (Salmon, Moraes, Dror, Shaw, "Parallel random
 // numbers: as easy as 1, 2, 3", SC 2011), keyed by a 64-bit seed read from device memory and
@@ -50,17 +56,30 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
 }
 
 constexpr int SMP_THREADS = 1024;
-constexpr int SMP_MAXV = 8704;  // LDS capacity in values (8197 codebook entries + slack)
+constexpr int SMP_MAXV = 8704;  // values per take supported (8197 codebook entries + slack)
+constexpr int SMP_PER = 9;      // values per thread: 8 contiguous + one of the tail past 8192
+constexpr int SMP_WDIG = 16;    // top key bytes (digits) covered by the window below the maximum
+constexpr int SMP_WBINS = SMP_WDIG * 256;  // one bin per 16-bit key of the window
+// LDS position of window bin b: 4 words of padding after every 64 bins, so that the 64 lanes
+// reading their own 64-bin runs as 16-byte words spread over the banks
+constexpr int SMP_WBINS_LDS = SMP_WBINS + 4 * (SMP_WBINS / 64);
+__device__ __forceinline__ int wbin_at(uint32_t b) { return (int)(b + 4 * (b >> 6)); }
 
 // Order-preserving 16-bit key of an fp16 value (-0.0 must be canonicalised to +0.0 first so
-// that key order equals float comparison).
+// that key order equals float comparison), and its inverse.
 __device__ __forceinline__ uint32_t hkey(f16 h) {
   const uint32_t u = __builtin_bit_cast(uint16_t, h);
   return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
 }
+__device__ __forceinline__ f16 hkey_inv(uint32_t k) {
+  const uint16_t u = (uint16_t)((k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu));
+  return __builtin_bit_cast(f16, u);
+}
 
-constexpr int SMP_GRP = (SMP_MAXV + 8 * SMP_THREADS - 1) / (8 * SMP_THREADS);  // 8-value groups
-constexpr int SMP_PER = 8 * SMP_GRP;  // values per thread
+// vocabulary index of slot j of thread tid
+__device__ __forceinline__ int slot_index(int tid, int j) {
+  return j < 8 ? 8 * tid + j : 8 * SMP_THREADS + tid;
+}
 
 // Digit d (from the top) of the radix select: the largest digit whose cumulative count from
 // the top reaches `rank`.  Run by wave 0 over 256 bins; writes (prefix | d << shift, new rank).
@@ -92,57 +111,13 @@ __device__ __forceinline__ void radix_pick(const uint32_t* hist, uint32_t* sel, 
   }
 }
 
-__global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
-    const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
-    int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
-    const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
-  __shared__ uint32_t hist[2][256];
-  __shared__ uint32_t sel[2];  // selected key prefix, remaining rank
-  __shared__ uint32_t wtot[SMP_THREADS / 64];
-  __shared__ int kept_i[SMP_MAXV];
-  __shared__ float kept_x[SMP_MAXV];
-
-  const int n = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wv = tid >> 6;
-  const f16* lc = logits + (long)n * ld;
-  const f16* lu = logits + (long)(n + N) * ld;
-
-  // 1. CFG mix in fp16.  Thread tid owns indices 8 tid + e + 8192 g (e < 8, g < SMP_GRP): the
-  //    loads are 16 bytes per lane where the row stride allows it.
-  f16 lv[SMP_PER];
-  uint32_t key[SMP_PER];
-  const bool vec = ((ld & 7) == 0) && ((((uintptr_t)logits) & 15) == 0);
-#pragma unroll
-  for (int g = 0; g < SMP_GRP; ++g) {
-    const int i0 = 8 * tid + SMP_THREADS * 8 * g;
-    f16x8 c8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, u8 = c8;
-    if (vec && i0 + 7 < V) {
-      c8 = *(const f16x8*)(lc + i0);
-      if (cfg_on) u8 = *(const f16x8*)(lu + i0);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (i0 + e < V) {
-          c8[e] = lc[i0 + e];
-          if (cfg_on) u8[e] = lu[i0 + e];
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int j = 8 * g + e;
-      f16 l = c8[e];
-      if (cfg_on) {
-        const f16 d = l - u8[e];
-        const f16 m = (f16)((float)d * cfg);
-        l = u8[e] + m;
-      }
-      l = l + (f16)0.0f;  // -0.0 -> +0.0
-      lv[j] = l;
-      key[j] = (i0 + e < V) ? hkey(l) : 0u;
-    }
-  }
+// Fallback when fewer than k values lie in the window: the k-th largest key by a two-pass radix
+// select over all keys (8-bit digits, LDS histograms), then the kept keys (>= threshold) are
+// compacted in (thread, slot) order by prefix sums.  Returns the kept count.
+__device__ uint32_t select_full(const uint32_t (&key)[SMP_PER], const f16 (&lv)[SMP_PER],
+                                float temp, int topk, uint32_t (&hist)[2][256], uint32_t* sel,
+                                uint32_t* wtot, int* kept_i, float* kept_x) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (tid < 256) {
     hist[0][tid] = 0u;
     hist[1][tid] = 0u;
@@ -152,9 +127,6 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     sel[1] = (uint32_t)topk;
   }
   __syncthreads();
-
-  // 2. k-th largest fp16 value by a two-pass radix select on the 16-bit keys (key 0 marks an
-  //    index past V: hkey is nonzero for every fp16 value except the NaN pattern 0xFFFF)
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j)
     if (key[j]) atomicAdd(&hist[0][key[j] >> 8], 1u);
@@ -170,8 +142,6 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   __syncthreads();
   const uint32_t thr = sel[0];
 
-  // 3. compact the kept indices (key >= thr) in (thread, slot) order: a wave-level inclusive
-  //    scan of per-thread counts, then per-wave totals through LDS
   int cnt = 0;
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j) cnt += (key[j] && key[j] >= thr) ? 1 : 0;
@@ -194,41 +164,177 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
 #pragma unroll
   for (int j = 0; j < SMP_PER; ++j) {
     if (key[j] && key[j] >= thr) {
-      kept_i[base] = 8 * tid + (j & 7) + SMP_THREADS * 8 * (j >> 3);
+      kept_i[base] = slot_index(tid, j);
       kept_x[base] = (float)lv[j] / temp;
       ++base;
     }
   }
+  return (uint32_t)total;
+}
+
+__global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
+    const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
+    int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
+    const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
+  __shared__ uint32_t hist[2][256];
+  __shared__ uint32_t sel[4];  // threshold key, kept count, fallback flag; radix state
+  __shared__ uint32_t wtot[SMP_THREADS / 64];
+  __shared__ __align__(16) uint32_t wbin[SMP_WBINS_LDS];
+  __shared__ int kept_i[SMP_MAXV];
+  __shared__ float kept_x[SMP_MAXV];
+
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const f16* lc = logits + (long)n * ld;
+  const f16* lu = logits + (long)(n + N) * ld;
+
+  // 1. loads, all issued before any arithmetic: thread tid owns indices 8 tid .. 8 tid + 7
+  //    (16-byte loads where the row stride allows) and 8192 + tid of the tail.  The Philox key
+  //    and counter words are read here too, so their latency hides under the logits loads.
+  const bool vec = ((ld & 7) == 0) && ((((uintptr_t)logits) & 15) == 0);
+  const int i0 = 8 * tid;
+  f16x8 c8 = (f16x8){0, 0, 0, 0, 0, 0, 0, 0}, u8 = c8;
+  if (vec && i0 + 7 < V) {
+    c8 = *(const f16x8*)(lc + i0);
+    if (cfg_on) u8 = *(const f16x8*)(lu + i0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < V) {
+        c8[e] = lc[i0 + e];
+        if (cfg_on) u8[e] = lu[i0 + e];
+      }
+  }
+  const int it = 8 * SMP_THREADS + tid;
+  f16 ct = (f16)0.0f, ut = ct;
+  if (it < V) {
+    ct = lc[it];
+    if (cfg_on) ut = lu[it];
+  }
+  uint64_t sd = 0u, p64 = 0u;
+  if (!noise) {  // seed and pos are only dereferenced on the Philox path (NULL with noise)
+    sd = (uint64_t)seed[0];
+    p64 = (uint64_t)pos[0];
+  }
+
+  // 2. CFG mix in fp16, keys, and the block's largest key
+  f16 lv[SMP_PER];
+  uint32_t key[SMP_PER];
+  uint32_t kmx = 0u;
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j) {
+    f16 l = j < 8 ? c8[j] : ct;
+    if (cfg_on) {
+      const f16 u = j < 8 ? u8[j] : ut;
+      const f16 d = l - u;
+      const f16 m = (f16)((float)d * cfg);
+      l = u + m;
+    }
+    l = l + (f16)0.0f;  // -0.0 -> +0.0
+    lv[j] = l;
+    key[j] = (slot_index(tid, j) < V) ? hkey(l) : 0u;  // key 0: no value (hkey(x) > 0)
+    kmx = max(kmx, key[j]);
+  }
+  kmx = wave_max_u32(kmx);
+  if (lane == 0) wtot[wv] = kmx;
+  for (int b = tid; b < SMP_WBINS_LDS; b += SMP_THREADS) wbin[b] = 0u;
+  __syncthreads();
+
+  // 3. histogram of the exact keys within SMP_WDIG digits below the largest one
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int w = 0; w < SMP_THREADS / 64; ++w) kmax = max(kmax, wtot[w]);
+  const uint32_t dtop = kmax >> 8;
+  const uint32_t kbase = dtop >= SMP_WDIG - 1 ? (dtop - (SMP_WDIG - 1)) << 8 : 0u;
+#pragma unroll
+  for (int j = 0; j < SMP_PER; ++j)
+    if (key[j] && key[j] >= kbase) atomicAdd(&wbin[wbin_at(key[j] - kbase)], 1u);
+  __syncthreads();
+
+  // 4. wave 0 walks the window from the top: the threshold is the key at which the count from
+  //    the top reaches k; every bin of the lanes at or above it is replaced by the first kept
+  //    slot of its key (kept values are stored in descending key order).  Lane l holds bins
+  //    64 (63 - l) .. +63 (lane 0 the top ones) in 16-byte LDS words.
+  if (wv == 0) {
+    uint32_t* mine = wbin + wbin_at(64 * (63 - lane));
+    uint32_t c = 0u;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const u32x4 v = *(const u32x4*)(mine + 4 * q);
+      c += (v.x + v.y) + (v.z + v.w);
+    }
+    const uint32_t incl = wave_incl_add_u32(c);
+    const uint32_t wtotal = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    const uint32_t k = (uint32_t)topk;
+    if (wtotal >= k && incl - c < k) {
+      // running count from the top; it never decreases, so the crossing bin is the one after
+      // the `below` bins whose running count is still under k
+      uint32_t acc = incl - c, below = 0u, kept = 0xFFFFFFFFu;
+#pragma unroll
+      for (int q = 15; q >= 0; --q) {
+        const u32x4 v = *(const u32x4*)(mine + 4 * q);
+        const uint32_t h[4] = {v.w, v.z, v.y, v.x};  // descending bins 4q + 3 .. 4q
+        uint32_t f[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          f[r] = acc;
+          acc += h[r];
+          const uint32_t lt = (acc - k) >> 31;  // acc < k (counts < 2^31), no lane masks
+          below += lt;
+          kept = min(kept, acc | (0u - lt));
+        }
+        *(u32x4*)(mine + 4 * q) = (u32x4){f[3], f[2], f[1], f[0]};
+      }
+      if (incl >= k) {  // the lane holding the crossing
+        sel[0] = kbase + (uint32_t)(64 * (63 - lane) + 63) - below;
+        sel[1] = kept;
+      }
+    }
+    if (lane == 0) sel[2] = wtotal >= k ? 0u : 1u;
+  }
+  __syncthreads();
+
+  uint32_t total;
+  if (sel[2] == 0u) {
+    // 5. kept values (key >= threshold) to their slots; values with equal keys are equal, so
+    //    their order among themselves does not change any sum below
+    const uint32_t thr = sel[0];
+    total = sel[1];
+#pragma unroll
+    for (int j = 0; j < SMP_PER; ++j) {
+      if (key[j] && key[j] >= thr) {
+        const uint32_t slot = atomicAdd(&wbin[wbin_at(key[j] - kbase)], 1u);
+        kept_i[slot] = slot_index(tid, j);
+        kept_x[slot] = (float)lv[j] / temp;
+      }
+    }
+  } else {
+    total = select_full(key, lv, temp, topk, hist, sel, wtot, kept_i, kept_x);
+  }
   __syncthreads();
   if (wv != 0) return;
 
-  // 4. wave 0: log_softmax then softmax in fp32 over the kept values (app/engine.py:293-296)
-  float m1 = -INFINITY;
-  for (int b = lane; b < total; b += 64) m1 = fmaxf(m1, kept_x[b]);
-  m1 = wave_max(m1);
+  // 6. wave 0: log_softmax then softmax in fp32 over the kept values (app/engine.py:293-296);
+  //    the largest x is the one of the largest key
+  const float m1 = (float)hkey_inv(kmax) / temp;
   float s1 = 0.f;
-  for (int b = lane; b < total; b += 64) s1 += expf(kept_x[b] - m1);
-  s1 = wave_sum(s1);
+  for (uint32_t b = lane; b < total; b += 64) s1 += expf(kept_x[b] - m1);
+  s1 = wave_sum_dpp(s1);
   const float logsum = logf(s1);
   // the maximum of ls = (x - m1) - logsum is exactly -logsum (at x = m1)
   const float m2 = 0.f - logsum;
   float s2 = 0.f;
-  for (int b = lane; b < total; b += 64) s2 += expf(((kept_x[b] - m1) - logsum) - m2);
-  s2 = wave_sum(s2);
+  for (uint32_t b = lane; b < total; b += 64) s2 += expf(((kept_x[b] - m1) - logsum) - m2);
+  s2 = wave_sum_dpp(s2);
 
-  // 5. exponential race: argmax p / q, q ~ Exp(1); draws for index i come from Philox block
+  // 7. exponential race: argmax p / q, q ~ Exp(1); draws for index i come from Philox block
   //    (i / 4, take, pos, salt), word i % 4 (or the injected noise)
-  uint32_t k0 = 0u, k1 = 0u;
-  uint64_t p64 = 0u;
-  if (!noise) {  // seed and pos are only dereferenced on the Philox path (NULL with noise)
-    const uint64_t sd = (uint64_t)seed[0];
-    k0 = (uint32_t)sd;
-    k1 = (uint32_t)(sd >> 32);
-    p64 = (uint64_t)pos[0];
-  }
+  const uint32_t k0 = (uint32_t)sd, k1 = (uint32_t)(sd >> 32);
   float bv = -1.f;
   int bi = 0x7FFFFFFF;
-  for (int b = lane; b < total; b += 64) {
+  for (uint32_t b = lane; b < total; b += 64) {
     const int i = kept_i[b];
     float q;
     if (noise) {
@@ -248,16 +354,11 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
       bi = i;
     }
   }
-  // wave argmax, lowest index on ties
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
+  // wave argmax, lowest index on ties: r >= 0 (or no candidate in the lane), so the bit
+  // patterns order like the values
+  const uint32_t rb = bi == 0x7FFFFFFF ? 0u : __builtin_bit_cast(uint32_t, bv);
+  const uint32_t mb = wave_max_u32(rb);
+  bi = (int)wave_min_u32(rb == mb ? (uint32_t)bi : 0xFFFFFFFFu);
   if (lane == 0) {
     out[(long)n * out_stride] = bi;
     if (cfg_on) out[(long)(n + N) * out_stride] = bi;

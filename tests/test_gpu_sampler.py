@@ -42,6 +42,45 @@ def test_sampler_matches_oracle_with_noise(dev, N, cfg_on, topk, temp):
                 assert np.array_equal(got[N:], got[:N])
 
 
+def _shaped_logits(kind, g, B):
+    x = g.standard_normal((B, V), dtype=np.float32)
+    if kind == "spread":        # 11 values far above the rest: fewer than k near the maximum
+        x[:, g.choice(V, 11, replace=False)] = 30000.0
+        x[:, 5] = 60000.0
+    elif kind == "negative":    # every logit negative
+        x = -20.0 + 3.0 * x
+    elif kind == "tail":        # maximum and a tie group in the last indices (past 8192)
+        x *= 3.0
+        x[:, 8195] = 40.0
+        x[:, [8192, 8196, 100]] = 20.0
+    elif kind in ("edge_in", "edge_out"):   # 50th largest on / just below the lowest key of
+        x = 0.01 * x                        # the 16-digit window under 64.0 (digits of 2 bits)
+        x[:, :30] = 64.0
+        x[:, 30:60] = 5.0 if kind == "edge_in" else 4.996
+    return x.astype(np.float16)
+
+
+@pytest.mark.parametrize("kind", ["spread", "negative", "tail", "edge_in", "edge_out"])
+@pytest.mark.parametrize("topk", [1, 50])
+def test_sampler_window_and_fallback(dev, kind, topk):
+    """Shapes that put the k-th largest value far below the maximum (the full radix select), in
+    negative keys, in the tail slots past 8192, or on / just below the window's lowest key."""
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    g = rng(300 + topk)
+    N = 2
+    for trial in range(3):
+        logits = _shaped_logits(kind, g, 2 * N)
+        noise = g.exponential(1.0, (N, V)).astype(np.float32)
+        want = sample(cfg_mix(logits, N, 1.5).astype(np.float32), topk, 1.0, noise)[:, 0]
+        out = torch.full((2 * N,), -1, dtype=torch.int64, device=dev)
+        padded = torch.zeros(2 * N, 8256, dtype=torch.float16, device=dev)
+        padded[:, :V] = T(logits, dev)
+        sample_topk(padded[:, :V], N, 1.5, 1.0, topk, out, noise=T(noise, dev))
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:N], want), (kind, trial, got, want)
+
+
 def test_sampler_threshold_ties_kept(dev):
     """Values equal to the k-th largest stay eligible (mask is logits < thr)."""
     import torch
