@@ -10,10 +10,13 @@ with N(0, 1) values; everything resident in HBM before the timed region.
 
 Prints one JSON line: frames/s (value), the GEMV roofline (hipEvent-timed launches of one
 frame's GEMV sequence, algorithmic bytes N*K + 2N + 2MK + 2MN (+2MN residual) per launch),
-and a CPU baseline: the reference's CPU path (numpy float32 restatement) timed on a bounded
-sample of layers on the host cores and scaled to a frame.
+the same frame at a second KV length (``target_point``, default 4096: frames/s and the HBM
+fractions of the GEMV family and the decode attention there), the prompt pass, and a CPU
+baseline: the reference's CPU path (numpy float32 restatement) timed on a bounded sample of
+layers on the host cores and scaled to a frame.
 
-    python bench.py [--steps K] [--warmup W] [--kv 750] [--decoder 1024|ref] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--kv 750] [--target-kv 4096] [--decoder 1024|ref]
+                    [--no-cpu]
 
 HBM traffic of the GEMV family (``roofline.traffic``) comes from two rocprofv3 counter runs of
 this script with a calibration copy appended (``--copy-calib-mib``), summarised by
@@ -46,6 +49,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--target-kv", type=int, default=4096,
+                    help="second attended KV length, timed and reported as target_point (0 skips)")
+    ap.add_argument("--target-steps", type=int, default=100)
     ap.add_argument("--prompt", type=int, default=256,
                     help="prompt tokens of the timed prompt pass (0 skips it)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -122,57 +128,35 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
     return out
 
 
-def main():
-    args = parse()
-    if args.pmc_summary:
-        print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calib_mib or 256), indent=1))
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this benchmark runs on one GPU only: the decode path has no "
-                          "multi-GPU mode (takes would shard by data parallelism with no collectives)"}))
-        sys.exit(2)
-    import torch
-    from estudiocanciones_amd import engine as E
-    from estudiocanciones_amd import kernels as KK
-    from estudiocanciones_amd.quant import synthetic_weights
-
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    bb = dict(E.BACKBONE, ffn=8192)
-    dec = dict(E.DECODER_1024 if args.decoder == "1024" else E.DECODER, ffn=8192)
-    t_build = time.time()
-    w = synthetic_weights(bb, dec, dev, seed=args.seed)
-    model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
-    del w
-    n = args.takes
-    P, n_frames = 64, max(args.kv - 64, 1)
+def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
+    """Allocate the caches for attended length ``kv``, capture one frame as a hipGraph, time
+    ``steps`` replays, then replay the frame's GEMV-family and attention launches one by one
+    between hipEvents for their per-launch rooflines."""
+    P, n_frames = 64, max(kv - 64, 1)
     Lcap = P + n_frames + 2 + 256
-    if args.kv > Lcap:
-        Lcap = args.kv + 258
+    if kv > Lcap:
+        Lcap = kv + 258
     model.alloc(n, Lcap, cfg_scale=1.5)
     B = model.B
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed + 1)
     for blk in model.backbone.blocks:
-        blk.kc[:, :, : args.kv].copy_(torch.randn(blk.kc[:, :, : args.kv].shape, generator=g, device=dev))
-        blk.vc[:, :, : args.kv].copy_(torch.randn(blk.vc[:, :, : args.kv].shape, generator=g, device=dev))
+        blk.kc[:, :, : kv].copy_(torch.randn(blk.kc[:, :, : kv].shape, generator=g, device=dev))
+        blk.vc[:, :, : kv].copy_(torch.randn(blk.vc[:, :, : kv].shape, generator=g, device=dev))
     tok = torch.randint(0, E.AUDIO_VOCAB, (B, E.N_CB), generator=g, device=dev)
-    static = dict(tok=tok, pos=torch.full((B, 1), args.kv - 1, dtype=torch.long, device=dev))
+    static = dict(tok=tok, pos=torch.full((B, 1), kv - 1, dtype=torch.long, device=dev))
     graph, out = model._capture(static, Lcap, 1.5, 50, 1.0)
     torch.cuda.synchronize()
-    t_build = time.time() - t_build
 
     # ------------------------------------------------ timed frames (one hipGraph per frame)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         graph.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    fps = args.steps / dt
-    ms = dt / args.steps * 1e3
+    fps = steps / dt
+    ms = dt / steps * 1e3
 
     # ------------------------------------------------ per-kernel roofline of one frame
     # Record every C-ABI launch of one eager frame step, then replay the GEMV-family and the
@@ -248,6 +232,61 @@ def main():
     bb_attn_gbps = (sum(attn_b[i] for i in bb_idx) / (bb_ms * len(bb_idx) * 1e-3) / 1e9) if bb_idx else None
     frame_bytes = sum(gemv_b) + sum(attn_b)
     launches = len(calls)
+    del graph
+    return dict(Lcap=Lcap, fps=fps, ms=ms, timed_s=dt, g_gbps=g_gbps, a_gbps=a_gbps,
+                bb_attn_gbps=bb_attn_gbps, gemv_b=gemv_b, attn_b=attn_b, g_avg_us=g_avg_us,
+                g_bytes_avg=g_bytes_avg, g_ms_total=g_ms_total, a_ms_total=a_ms_total,
+                a_ms_launch=a_ms_launch, frame_bytes=frame_bytes, launches=launches)
+
+
+def main():
+    args = parse()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calib_mib or 256), indent=1))
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only: the decode path has no "
+                          "multi-GPU mode (takes would shard by data parallelism with no collectives)"}))
+        sys.exit(2)
+    import torch
+    from estudiocanciones_amd import engine as E
+    from estudiocanciones_amd import kernels as KK
+    from estudiocanciones_amd.quant import synthetic_weights
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bb = dict(E.BACKBONE, ffn=8192)
+    dec = dict(E.DECODER_1024 if args.decoder == "1024" else E.DECODER, ffn=8192)
+    t_build = time.time()
+    w = synthetic_weights(bb, dec, dev, seed=args.seed)
+    model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
+    del w
+    n = args.takes
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 1)
+    t_build = time.time() - t_build
+    main_pt = measure_point(torch, E, model, dev, n, args.kv, args.steps, args.warmup, g)
+    B, Lcap = model.B, main_pt["Lcap"]
+    target = None
+    if args.target_kv > 0 and args.target_kv != args.kv:
+        tp = measure_point(torch, E, model, dev, n, args.target_kv, args.target_steps, args.warmup, g)
+        target = {
+            "kv_len": args.target_kv, "steps": args.target_steps,
+            "value": round(tp["fps"], 2), "unit": "frames/s", "ms_per_step": round(tp["ms"], 4),
+            "gemv_frac": round(tp["g_gbps"] / HBM_PEAK_GBPS, 4),
+            "decode_attn_frac": round(tp["a_gbps"] / HBM_PEAK_GBPS, 4),
+            "backbone_attn_GBps": round(tp["bb_attn_gbps"], 1) if tp["bb_attn_gbps"] else None,
+            "backbone_attn_frac": (round(tp["bb_attn_gbps"] / HBM_PEAK_GBPS, 4)
+                                   if tp["bb_attn_gbps"] else None),
+            "frame_frac_of_hbm": round(tp["frame_bytes"] * tp["fps"] / 1e9 / HBM_PEAK_GBPS, 4),
+        }
+    fps, ms = main_pt["fps"], main_pt["ms"]
+    g_gbps, a_gbps, bb_attn_gbps = main_pt["g_gbps"], main_pt["a_gbps"], main_pt["bb_attn_gbps"]
+    gemv_b, attn_b = main_pt["gemv_b"], main_pt["attn_b"]
+    g_avg_us, g_bytes_avg = main_pt["g_avg_us"], main_pt["g_bytes_avg"]
+    g_ms_total, a_ms_total, a_ms_launch = main_pt["g_ms_total"], main_pt["a_ms_total"], main_pt["a_ms_launch"]
+    frame_bytes, launches = main_pt["frame_bytes"], main_pt["launches"]
+    from estudiocanciones_amd import _ffi
     if args.copy_calib_mib > 0:
         # calibration for the counter runs: one plain copy of known size, read once, written once
         nb = args.copy_calib_mib << 20
@@ -311,7 +350,8 @@ def main():
         "tokens_per_s": round(fps * E.N_CB * n, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_fused_kernel (int8 weight x f16 GEMV family, all launches of one frame)",
+            "kernel": ("gemv_xreg/xlds/fused kernels (int8 weight x f16 GEMV family, every GEMV "
+                       "launch of one frame)"),
             "achieved": round(g_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -338,6 +378,7 @@ def main():
             "kernel_time_attn_ms": round(a_ms_total, 4),
             "library_launches": launches,
         },
+        "target_point": target,
         "prompt_pass": prompt,
         "setup_s": round(t_build, 1),
     }
