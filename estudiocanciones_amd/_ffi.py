@@ -38,6 +38,7 @@ SIGNATURES = {
                             _P, c_int, _P],
     "ecd_gemm_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_i8p_silu": [_P, c_long, _P, _P, _P, c_long, c_int, c_int, c_int, _P],
+    "ecd_prefill_attn": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     "ecd_packed_bytes": [c_int, c_int],
     "ecd_pack_i8": [_P, c_int, c_int, c_int, _P, _P],
     "ecd_gemv_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int, c_int,

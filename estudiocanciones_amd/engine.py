@@ -29,7 +29,7 @@ import torch
 
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
-                      gemm_packed, gemm_silu_packed, gemv_packed_splitk,
+                      gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
                       gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms,
                       rms_gemv_packed, rms_qkv_rope, rms_w13_silu, sample_topk, stream_ptr)
 
@@ -223,9 +223,13 @@ class Stack:
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
             _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
                                       HD=HD, HALF=next_power_of_2(HD // 2))
-            # one split per row: a prompt row attends at most the prompt (no empty splits, no
-            # combine pass); the rows themselves give the parallelism
-            o = self._attention(b, q, pos, S, 1)
+            if HD == 128 and Hq // Hk <= 4:
+                # causal flash attention on MFMA: each K/V tile is read once per 64-row block
+                o = prefill_attn(q, b.kc, b.vc, pos, S, Hq, Hk)
+            else:
+                # one split per row: a prompt row attends at most the prompt (no empty splits,
+                # no combine pass); the rows themselves give the parallelism
+                o = self._attention(b, q, pos, S, 1)
             x = gemm_packed(o, b.o.qp, b.o.sp, b.o.N, b.o.K, res=x)
             mm = gemm_silu_packed(krms(x, b.n2), b.w13.qp, b.w13.sp, b.w13.N // 2, b.w13.K)
             x = gemm_packed(mm, b.w2.qp, b.w2.sp, b.w2.N, b.w2.K, res=x)

@@ -343,6 +343,23 @@ def gemm_silu_packed(x, wp, s, F, K):
     return mm
 
 
+def prefill_attn(q, kc, vc, pos, S, Hq, Hk, scale=None):
+    """Causal prompt-pass attention on MFMA: q [B*S, Hq*HD] fp16, kc/vc [B, Hk, L, HD] holding
+    the prompt's K/V, pos [B*S] int64 -> o [B*S, Hq*HD] (row r attends slots [0, pos[r]])."""
+    R = q.shape[0]
+    B, _, L, HD = kc.shape
+    if q.dtype != torch.float16 or not q.is_contiguous() or q.shape[1] != Hq * HD or R != B * S:
+        raise ValueError("prefill_attn: q must be contiguous fp16 [B*S, Hq*HD]")
+    if not (kc.is_contiguous() and vc.is_contiguous()) or pos.dtype != torch.int64:
+        raise ValueError("prefill_attn: contiguous caches and int64 positions required")
+    o = torch.empty_like(q)
+    pc = pos.contiguous()
+    _ffi.call("ecd_prefill_attn", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+              pc.data_ptr(), o.data_ptr(), B, S, Hq, Hk, L, HD,
+              float(scale if scale is not None else 1.0 / math.sqrt(HD)), stream_ptr(q.device))
+    return o
+
+
 def rms_gemv_packed(x, nw, wp, s, N, K, eps=1e-5, stream=False, out=None):
     """int8_mm(rms(x, nw), w, s) in one kernel.  ``out``: optional [M, N] fp16 destination with
     unit inner stride (any row stride)."""

@@ -190,6 +190,15 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
 int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,
                       long ldm, int M, int F, int K, void* stream);
 
+/* Causal attention of the prompt pass on MFMA: row r = b * S + s of q [B * S, Hq * HD] attends
+ * cache slots [0, pos[r]] of kc, vc [B, Hk, L, HD] (the prompt's K/V already written), with the
+ * decode kernel's numerics (fp32 scores, running max, fp16 probabilities into P.V, fp32 sums).
+ * Replaces the causal scaled_dot_product_attention of the prompt pass (app/engine.py:123-153,
+ * :174-178).  o [B * S, Hq * HD].  HD == 128; Hq / Hk in {1, 2, 3, 4}; q, kc, vc 16-byte and o
+ * 8-byte aligned. */
+int ecd_prefill_attn(const void* q, const void* kc, const void* vc, const int64_t* pos, void* o,
+                     int B, int S, int Hq, int Hk, int L, int HD, float scale, void* stream);
+
 /* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
  * counterpart: a kernel of known HBM traffic used to calibrate hardware byte counters. */
 int ecd_copy_bytes(const void* src, void* dst, long nbytes, void* stream);

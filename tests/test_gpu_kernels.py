@@ -243,6 +243,30 @@ def test_decode_attn_split_invariance(dev):
         assert_close16(o, outs[0], what="split invariance")
 
 
+@pytest.mark.parametrize("B,S,Hq,Hk,L,off", [(2, 100, 24, 8, 128, 0), (1, 64, 8, 2, 160, 37),
+                                              (3, 17, 4, 4, 40, 5), (1, 130, 8, 4, 256, 0)])
+def test_prefill_attn(dev, B, S, Hq, Hk, L, off):
+    """Causal prompt-pass attention on MFMA against the exact softmax and against the decode
+    kernel (one split per row) on the same inputs: row s attends [0, off + s]; S not a
+    multiple of the 64-row block, G = 1..4, a prompt placed after cached slots."""
+    import torch
+    from estudiocanciones_amd.kernels import _attn, prefill_attn
+    HD = 128
+    R = B * S
+    q = randn16(60, R, Hq * HD)
+    kc = randn16(61, B, Hk, L, HD)
+    vc = randn16(62, B, Hk, L, HD)
+    pos = np.tile(np.arange(S, dtype=np.int64) + off, B)
+    exact = OK.attention_exact(q, kc, vc, pos, S, Hq, Hk, HD)
+    qt, kt, vt, pt = T(q, dev), T(kc, dev), T(vc, dev), T(pos, dev)
+    got = prefill_attn(qt, kt, vt, pt, S, Hq, Hk)
+    assert_close16(N(got), exact, what=f"prefill attn B={B} S={S} G={Hq // Hk}")
+    o = torch.empty(R, Hq * HD, dtype=torch.float16, device=dev)
+    _attn[(R, Hk, 1)](qt, kt, vt, pt, o, o, o, o, S, Hq, Hk, L, 1 / math.sqrt(HD), HD=HD,
+                      NSPLIT=1)
+    assert_close16(N(got), N(o), what="prefill attn vs decode kernel")
+
+
 # ---------------------------------------------------------------- SiLU * mul
 @pytest.mark.parametrize("R,F", [(8, 8192), (16, 8192), (2, 1000)])
 def test_silu_mul(dev, R, F):
