@@ -58,7 +58,9 @@ def build(verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, srcs))
     out = LIBDIR / LIBNAME
     tmp = LIBDIR / (LIBNAME + ".tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o",
+           str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
