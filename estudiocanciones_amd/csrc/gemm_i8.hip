@@ -9,11 +9,21 @@
 //
 // Tiling: a block computes 128 output features x 128 rows with 4 waves; wave (wn, wm) owns
 // 64 features x 64 rows = 4 x 4 tiles of v_mfma_f32_16x16x32_f16 (weights = A operand, x = B
-// operand).  K advances in 64-wide chunks staged through LDS (weights as packed 1 KB tiles,
-// x rows padded to 72 halfs so the B-fragment reads spread over the banks), double-buffered:
-// the next chunk's global loads are in flight while the current one is multiplied.  Each
-// 16-byte weight fragment is dequantised once and used by 4 row tiles; each x fragment is
-// used by 4 feature tiles.
+// operand).  K advances in 64-wide chunks that go straight from global memory into a ring of
+// three LDS stages (global_load_lds_dwordx4: each wave instruction writes 1 KB of LDS in lane
+// order), so two chunks are in flight while one is multiplied and no registers stage the data.
+// Weights arrive as packed 1 KB tiles; the 16-byte pieces of each x row (128 bytes per chunk)
+// are XOR-swizzled by row (piece p of row r at position p ^ (r & 7)), which the loads produce
+// by choosing each lane's source and which spreads the fragment reads over the banks.  Each
+// 16-byte weight fragment is dequantised once and used by 4 row tiles; each x fragment is used
+// by 4 feature tiles.
+//
+// The LDS DMA is issued from inline asm with M0 (the instruction's LDS base) saved and restored
+// around it: with the compiler's builtin, every later LDS read waits for all DMA in flight
+// (vmcnt 0), which removes the overlap.  The kernel counts the DMA itself: before chunk c is
+// read each thread waits until only its 6 loads of chunk c + 1 are outstanding (vector memory
+// operations complete in issue order), then a barrier makes the chunk of every wave visible and
+// frees the stage read in the previous step, which the next chunk's loads then overwrite.
 //
 // Block order is XCD-aware: the row blocks that share a weight tile get block ids that are
 // equal modulo 8, so they run on one XCD and re-read the tile from its L2.
@@ -25,15 +35,33 @@ enum { GEPI_STORE = 0, GEPI_SILU = 1 };
 
 constexpr int GT_N = 128;   // output features per block
 constexpr int GT_M = 128;   // rows per block
-constexpr int GXS = 72;     // LDS row stride of the x tile, halfs (64 + 8 padding)
+constexpr int GT_NS = 3;    // LDS stages
+constexpr int GT_LPC = 6;   // LDS DMA loads per thread per chunk (2 weight, 4 x)
+
+// wait until at most N vector-memory operations of this wave are outstanding (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima, i.e. not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// one wave instruction: 16 bytes per lane from `src` into LDS at dst + 16 * lane (dst uniform)
+__device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(src), "s"(la) : "memory");
+}
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     const f16* __restrict__ x, long ldx, const int8_t* __restrict__ wp,
     const f16* __restrict__ s, const f16* __restrict__ res, long ldr, f16* __restrict__ y,
     long ldy, int M, int N, int K, int nfb, int nmb) {
-  __shared__ __align__(16) int8_t lw[2][8 * 1024];
-  __shared__ __align__(16) f16 lx[2][GT_M * GXS];
+  __shared__ __align__(16) int8_t lw[GT_NS][8 * 1024];
+  __shared__ __align__(16) f16 lx[GT_NS][GT_M * 64];
 
   // XCD-aware block order: blocks b and b + 8 run on the same XCD.  Feature block fb and row
   // block mb map to b = (fb / 8) * (8 * nmb) + mb * 8 + fb % 8.
@@ -46,37 +74,29 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wv & 1, wm = wv >> 1;
   const int n0 = fb * GT_N;
   const int m0 = mb * GT_M;
   const int nch = K >> 6;
   const int ntiles = (N + 15) >> 4;
 
-  // global -> register staging of one chunk: weights (8 tiles x 1 KB, 32 bytes per thread),
-  // x (128 rows x 128 bytes, 64 bytes per thread)
-  const int wt = tid >> 5;                       // tile of this thread's weight bytes
-  const int wo = (tid & 31) * 32;                // byte offset inside the tile's 1 KB chunk
-  const int wtile = min(n0 / 16 + wt, ntiles - 1);
-  const int8_t* wsrc = wp + (long)wtile * nch * 1024 + wo;
-  const int xr = tid >> 1;                       // x row of this thread (0..127)
-  const int xo = (tid & 1) * 32;                 // first half of the row's 64-k chunk
-  const bool xok = m0 + xr < M;
-  const f16* xsrc = x + (long)(xok ? m0 + xr : 0) * ldx + xo;
-
-  u32x4 rw[2], rx[4];
-  auto gload = [&](int c) {
-    rw[0] = *(const u32x4*)(wsrc + (long)c * 1024);
-    rw[1] = *(const u32x4*)(wsrc + (long)c * 1024 + 16);
+  // sources of this thread's loads: weight tiles wv and wv + 4 (16 bytes of each 1 KB chunk);
+  // x rows 8 (4 wv + i) + (lane >> 3), swizzled piece (lane & 7) ^ (lane >> 3).  Rows past M
+  // read row M - 1 and tiles past N the last tile (their results are never stored), so every
+  // thread issues the same number of loads.
+  const int8_t* wsrc0 = wp + (long)min(n0 / 16 + wv, ntiles - 1) * nch * 1024 + 16 * lane;
+  const int8_t* wsrc1 = wp + (long)min(n0 / 16 + 4 + wv, ntiles - 1) * nch * 1024 + 16 * lane;
+  const int xpiece = (lane & 7) ^ (lane >> 3);
+  const f16* xsrc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      rx[i] = xok ? *(const u32x4*)(xsrc + (long)c * 64 + 8 * i) : (u32x4){0u, 0u, 0u, 0u};
-  };
-  auto lstore = [&](int buf) {
-    *(u32x4*)(&lw[buf][wt * 1024 + wo]) = rw[0];
-    *(u32x4*)(&lw[buf][wt * 1024 + wo + 16]) = rw[1];
+  for (int i = 0; i < 4; ++i)
+    xsrc[i] = x + (long)min(m0 + 8 * (4 * wv + i) + (lane >> 3), M - 1) * ldx + 8 * xpiece;
+  auto issue = [&](int c, int st) {
+    lds_dma16(wsrc0 + (long)c * 1024, &lw[st][wv * 1024]);
+    lds_dma16(wsrc1 + (long)c * 1024, &lw[st][(4 + wv) * 1024]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4*)(&lx[buf][xr * GXS + xo + 8 * i]) = rx[i];
+    for (int i = 0; i < 4; ++i) lds_dma16(xsrc[i] + (long)c * 64, &lx[st][8 * (4 * wv + i) * 64]);
   };
 
   // per-lane dequantisation scales of the 4 feature tiles (row lane & 15 of each)
@@ -90,33 +110,39 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  issue(0, 0);
+  if (nch > 1) issue(1, 1);
+  const int sw = lane & 7;  // swizzle of the rows this lane reads (row & 7 == lane & 7)
   for (int c = 0; c < nch; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nch) gload(c + 1);
+    if (c + 1 < nch)
+      wait_vm<GT_LPC>();  // chunk c + 1's loads may stay in flight
+    else
+      wait_vm<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // chunk c in LDS for every wave; stage of c - 1 free
+    asm volatile("" ::: "memory");
+    if (c + 2 < nch) issue(c + 2, (c + 2) % GT_NS);
+    const int st = c % GT_NS;
     f16x8 wa[4], wb[4];
 #pragma unroll
     for (int ft = 0; ft < 4; ++ft) {
-      const u32x4 raw = *(const u32x4*)(&lw[buf][(wn * 4 + ft) * 1024 + 16 * lane]);
+      const u32x4 raw = *(const u32x4*)(&lw[st][(wn * 4 + ft) * 1024 + 16 * lane]);
       i8x16_to_f16(raw, wa[ft], wb[ft]);
       wa[ft] = wa[ft] * sc[ft];
       wb[ft] = wb[ft] * sc[ft];
     }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      const f16* xp = &lx[buf][(wm * 64 + rt * 16 + (lane & 15)) * GXS + 16 * (lane >> 4)];
-      const f16x8 fa = *(const f16x8*)xp;
-      const f16x8 fb2 = *(const f16x8*)(xp + 8);
+      const f16* xr = &lx[st][(wm * 64 + rt * 16 + (lane & 15)) * 64];
+      const int p0 = 2 * (lane >> 4);
+      const f16x8 fa = *(const f16x8*)(xr + 8 * (p0 ^ sw));
+      const f16x8 fb2 = *(const f16x8*)(xr + 8 * ((p0 + 1) ^ sw));
 #pragma unroll
       for (int ft = 0; ft < 4; ++ft) {
         acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[ft], fa, acc[ft][rt], 0, 0, 0);
         acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[ft], fb2, acc[ft][rt], 0, 0, 0);
       }
     }
-    if (c + 1 < nch) lstore(buf ^ 1);
-    __syncthreads();
   }
 
   // epilogue: lane holds features nb + r (r < 4) of row m for every (ft, rt)
