@@ -319,7 +319,7 @@ def main():
         prompt = {"prompt_tokens": P, "rows": B * P, "ms": round(p_ms, 3),
                   "gemm_flops": int(flops), "gemm_equivalent_TFLOPs": round(flops / p_ms / 1e9, 1),
                   "frac_of_mfma_f16_peak": round(flops / p_ms / 1e9 / 2500.0, 4),
-                  "path": ("MFMA GEMM (dense numerics, 3-stage LDS DMA ring) + MFMA causal flash "
+                  "path": ("MFMA GEMM (dense numerics, 2-stage LDS DMA) + MFMA causal flash "
                           "attention, 28 layers")}
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

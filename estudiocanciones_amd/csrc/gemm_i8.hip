@@ -9,9 +9,10 @@
 //
 // Tiling: a block computes 128 output features x 128 rows with 4 waves; wave (wn, wm) owns
 // 64 features x 64 rows = 4 x 4 tiles of v_mfma_f32_16x16x32_f16 (weights = A operand, x = B
-// operand).  K advances in 64-wide chunks that go straight from global memory into a ring of
-// three LDS stages (global_load_lds_dwordx4: each wave instruction writes 1 KB of LDS in lane
-// order), so two chunks are in flight while one is multiplied and no registers stage the data.
+// operand).  K advances in 64-wide chunks that go straight from global memory into two LDS
+// stages (global_load_lds_dwordx4: each wave instruction writes 1 KB of LDS in lane order): the
+// next chunk is in flight while one is multiplied, no registers stage the data, and 48 KB of
+// LDS per block leave room for three blocks per CU.
 // Weights arrive as packed 1 KB tiles; the 16-byte pieces of each x row (128 bytes per chunk)
 // are XOR-swizzled by row (piece p of row r at position p ^ (r & 7)), which the loads produce
 // by choosing each lane's source and which spreads the fragment reads over the banks.  Each
@@ -19,11 +20,11 @@
 // by 4 feature tiles.
 //
 // The LDS DMA is issued from inline asm with M0 (the instruction's LDS base) saved and restored
-// around it: with the compiler's builtin, every later LDS read waits for all DMA in flight
-// (vmcnt 0), which removes the overlap.  The kernel counts the DMA itself: before chunk c is
-// read each thread waits until only its 6 loads of chunk c + 1 are outstanding (vector memory
-// operations complete in issue order), then a barrier makes the chunk of every wave visible and
-// frees the stage read in the previous step, which the next chunk's loads then overwrite.
+// around it: with the compiler's builtin, every LDS read of the chunk being multiplied would
+// wait for the DMA of the next one too (vmcnt 0 before any LDS read), which removes the overlap.
+// The kernel orders the DMA itself: at the top of step c each thread waits for its own loads of
+// chunk c (vmcnt 0), a barrier makes the chunk of every wave visible and frees the stage read
+// in step c - 1, and only then are chunk c + 1's loads issued into that stage.
 //
 // Block order is XCD-aware: the row blocks that share a weight tile get block ids that are
 // equal modulo 8, so they run on one XCD and re-read the tile from its L2.
@@ -35,16 +36,11 @@ enum { GEPI_STORE = 0, GEPI_SILU = 1 };
 
 constexpr int GT_N = 128;   // output features per block
 constexpr int GT_M = 128;   // rows per block
-constexpr int GT_NS = 3;    // LDS stages
-constexpr int GT_LPC = 6;   // LDS DMA loads per thread per chunk (2 weight, 4 x)
+constexpr int GT_NS = 2;    // LDS stages
 
-// wait until at most N vector-memory operations of this wave are outstanding (gfx9 encoding:
-// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima, i.e. not waited for)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
+// wait until no vector-memory operation of this wave is outstanding (gfx9 encoding: vmcnt 0,
+// expcnt and lgkmcnt at their maxima, i.e. not waited for)
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
 // one wave instruction: 16 bytes per lane from `src` into LDS at dst + 16 * lane (dst uniform)
 __device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
@@ -111,18 +107,14 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     for (int rt = 0; rt < 4; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   issue(0, 0);
-  if (nch > 1) issue(1, 1);
   const int sw = lane & 7;  // swizzle of the rows this lane reads (row & 7 == lane & 7)
   for (int c = 0; c < nch; ++c) {
-    if (c + 1 < nch)
-      wait_vm<GT_LPC>();  // chunk c + 1's loads may stay in flight
-    else
-      wait_vm<0>();
+    wait_vm0();  // this thread's loads of chunk c have landed in LDS
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // chunk c in LDS for every wave; stage of c - 1 free
     asm volatile("" ::: "memory");
-    if (c + 2 < nch) issue(c + 2, (c + 2) % GT_NS);
-    const int st = c % GT_NS;
+    if (c + 1 < nch) issue(c + 1, (c + 1) & 1);
+    const int st = c & 1;
     f16x8 wa[4], wb[4];
 #pragma unroll
     for (int ft = 0; ft < 4; ++ft) {
