@@ -76,24 +76,35 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
   const int vp = 2 * (tid >> 3);
   const int vd = 16 * (tid & 7);
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int t0 = it * PA_KT;
-    // loads: V pair (4 x 16 B), this wave's K fragments (16 x 16 B); slots past the cache are
-    // clamped to its last slot (finite values, masked below)
-    f16x8 va[2][2];
+  // loads of one tile: V pair (4 x 16 B), this wave's K fragments (16 x 16 B); slots past the
+  // cache are clamped to its last slot (finite values, masked below)
+  auto load_tile = [&](int t0, f16x8 (&va)[2][2], f16x8 (&kf)[4][4]) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const f16* src = vb + (long)min(t0 + vp + u, L - 1) * HD + vd;
       va[u][0] = *(const f16x8*)src;
       va[u][1] = *(const f16x8*)(src + 8);
     }
-    f16x8 kf[4][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f16* src = kb + (long)min(t0 + 16 * j + col, L - 1) * HD + 8 * grp;
 #pragma unroll
       for (int st = 0; st < 4; ++st) kf[j][st] = *(const f16x8*)(src + 32 * st);
     }
+  };
+  // the next tile's loads are issued before this one is computed where registers allow (G <= 3:
+  // with 4 heads the second buffer would spill)
+  constexpr bool PREFETCH = G <= 3;
+  f16x8 va[2][2], kf[4][4];
+  if (PREFETCH && ntiles > 0) load_tile(0, va, kf);
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = it * PA_KT;
+    f16x8 vn[2][2], kn[4][4];
+    if (!PREFETCH)
+      load_tile(t0, va, kf);
+    else if (it + 1 < ntiles)
+      load_tile(t0 + PA_KT, vn, kn);
     // V^T into LDS: word (d, slot pair) = {V[t][d], V[t + 1][d]}
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -167,6 +178,16 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
           oacc[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, pb[g][ks], oacc[g][dt], 0, 0, 0);
       }
     __syncthreads();  // V^T consumed before the next tile overwrites it
+    if (PREFETCH && it + 1 < ntiles) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) va[u][h] = vn[u][h];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) kf[j][st] = kn[j][st];
+    }
   }
 
   // O = O^T / l: lane holds row s, d = 16 dt + 4 grp + i
