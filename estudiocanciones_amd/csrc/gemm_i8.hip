@@ -7,17 +7,18 @@
 // Weights use the lane-ordered packed layout of gemv_fused.hip: chunk (tile, c) = 16 rows x
 // 64 bytes stored so that lane l's 16 bytes are row l & 15, k = 64c + 16 (l >> 4) .. +15.
 //
-// Tiling: a block computes 128 output features x 128 rows with 4 waves; wave (wn, wm) owns
-// 64 features x 64 rows = 4 x 4 tiles of v_mfma_f32_16x16x32_f16 (weights = A operand, x = B
-// operand).  K advances in 64-wide chunks that go straight from global memory into two LDS
+// Tiling: a block computes 128 output features x 128 rows with 4 waves; wave w owns features
+// 32 w .. 32 w + 31 for all 128 rows = 2 x 8 tiles of v_mfma_f32_16x16x32_f16 (weights = A
+// operand, x = B operand), so each weight fragment is dequantised by one wave only (the
+// dequantisation is the kernel's largest VALU cost).  K advances in 64-wide chunks that go straight from global memory into two LDS
 // stages (global_load_lds_dwordx4: each wave instruction writes 1 KB of LDS in lane order): the
 // next chunk is in flight while one is multiplied, no registers stage the data, and 48 KB of
 // LDS per block leave room for three blocks per CU.
 // Weights arrive as packed 1 KB tiles; the 16-byte pieces of each x row (128 bytes per chunk)
 // are XOR-swizzled by row (piece p of row r at position p ^ (r & 7)), which the loads produce
 // by choosing each lane's source and which spreads the fragment reads over the banks.  Each
-// 16-byte weight fragment is dequantised once and used by 4 row tiles; each x fragment is used
-// by 4 feature tiles.
+// 16-byte weight fragment is dequantised once and used by 8 row tiles; each x fragment is used
+// by 2 feature tiles.
 //
 // The LDS DMA is issued from inline asm with M0 (the instruction's LDS base) saved and restored
 // around it: with the compiler's builtin, every LDS read of the chunk being multiplied would
@@ -71,7 +72,6 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wv & 1, wm = wv >> 1;
   const int n0 = fb * GT_N;
   const int m0 = mb * GT_M;
   const int nch = K >> 6;
@@ -96,15 +96,15 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   };
 
   // per-lane dequantisation scales of the 4 feature tiles (row lane & 15 of each)
-  f16 sc[4];
+  f16 sc[2];
 #pragma unroll
-  for (int ft = 0; ft < 4; ++ft) sc[ft] = s[min(n0 + (wn * 4 + ft) * 16 + (lane & 15), N - 1)];
+  for (int ft = 0; ft < 2; ++ft) sc[ft] = s[min(n0 + (wv * 2 + ft) * 16 + (lane & 15), N - 1)];
 
-  f32x4 acc[4][4];
+  f32x4 acc[2][8];
 #pragma unroll
-  for (int ft = 0; ft < 4; ++ft)
+  for (int ft = 0; ft < 2; ++ft)
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < 8; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   issue(0, 0);
   const int sw = lane & 7;  // swizzle of the rows this lane reads (row & 7 == lane & 7)
@@ -115,22 +115,22 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     asm volatile("" ::: "memory");
     if (c + 1 < nch) issue(c + 1, (c + 1) & 1);
     const int st = c & 1;
-    f16x8 wa[4], wb[4];
+    f16x8 wa[2], wb[2];
 #pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      const u32x4 raw = *(const u32x4*)(&lw[st][(wn * 4 + ft) * 1024 + 16 * lane]);
+    for (int ft = 0; ft < 2; ++ft) {
+      const u32x4 raw = *(const u32x4*)(&lw[st][(wv * 2 + ft) * 1024 + 16 * lane]);
       i8x16_to_f16(raw, wa[ft], wb[ft]);
       wa[ft] = wa[ft] * sc[ft];
       wb[ft] = wb[ft] * sc[ft];
     }
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const f16* xr = &lx[st][(wm * 64 + rt * 16 + (lane & 15)) * 64];
+    for (int rt = 0; rt < 8; ++rt) {
+      const f16* xr = &lx[st][(rt * 16 + (lane & 15)) * 64];
       const int p0 = 2 * (lane >> 4);
       const f16x8 fa = *(const f16x8*)(xr + 8 * (p0 ^ sw));
       const f16x8 fb2 = *(const f16x8*)(xr + 8 * ((p0 + 1) ^ sw));
 #pragma unroll
-      for (int ft = 0; ft < 4; ++ft) {
+      for (int ft = 0; ft < 2; ++ft) {
         acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[ft], fa, acc[ft][rt], 0, 0, 0);
         acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[ft], fb2, acc[ft][rt], 0, 0, 0);
       }
@@ -139,12 +139,12 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
 
   // epilogue: lane holds features nb + r (r < 4) of row m for every (ft, rt)
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int m = m0 + wm * 64 + rt * 16 + (lane & 15);
+  for (int rt = 0; rt < 8; ++rt) {
+    const int m = m0 + rt * 16 + (lane & 15);
     if (m >= M) continue;
 #pragma unroll
-    for (int ft = 0; ft < 4; ++ft) {
-      const int nb = n0 + (wn * 4 + ft) * 16 + 4 * (lane >> 4);
+    for (int ft = 0; ft < 2; ++ft) {
+      const int nb = n0 + (wv * 2 + ft) * 16 + 4 * (lane >> 4);
       if (nb >= N) continue;
       f16 yv[4];
 #pragma unroll
