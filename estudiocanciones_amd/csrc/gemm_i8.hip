@@ -43,13 +43,14 @@ constexpr int GT_NS = 2;    // LDS stages
 // expcnt and lgkmcnt at their maxima, i.e. not waited for)
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
-// one wave instruction: 16 bytes per lane from `src` into LDS at dst + 16 * lane (dst uniform)
-__device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
+// one wave instruction: 16 bytes per lane from base + off (base wave-uniform, off a per-lane
+// byte offset below 2^31) into LDS at dst + 16 * lane (dst uniform)
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, void* dst) {
   const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
-               "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(src), "s"(la) : "memory");
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
 }
 
 template <int EPI>
@@ -81,18 +82,23 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   // x rows 8 (4 wv + i) + (lane >> 3), swizzled piece (lane & 7) ^ (lane >> 3).  Rows past M
   // read row M - 1 and tiles past N the last tile (their results are never stored), so every
   // thread issues the same number of loads.
-  const int8_t* wsrc0 = wp + (long)min(n0 / 16 + wv, ntiles - 1) * nch * 1024 + 16 * lane;
-  const int8_t* wsrc1 = wp + (long)min(n0 / 16 + 4 + wv, ntiles - 1) * nch * 1024 + 16 * lane;
+  // The addresses are a wave-uniform base (SGPRs, advanced per chunk by scalar adds) plus a
+  // per-lane byte offset fixed for the whole loop (the host keeps the x buffer below 2 GiB).
+  const int8_t* wbase0 = wp + (long)min(n0 / 16 + wv, ntiles - 1) * nch * 1024;
+  const int8_t* wbase1 = wp + (long)min(n0 / 16 + 4 + wv, ntiles - 1) * nch * 1024;
+  const uint32_t woff = 16u * lane;
   const int xpiece = (lane & 7) ^ (lane >> 3);
-  const f16* xsrc[4];
+  uint32_t xoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    xsrc[i] = x + (long)min(m0 + 8 * (4 * wv + i) + (lane >> 3), M - 1) * ldx + 8 * xpiece;
+    xoff[i] = (uint32_t)((long)min(m0 + 8 * (4 * wv + i) + (lane >> 3), M - 1) * ldx * 2 +
+                         16 * xpiece);
   auto issue = [&](int c, int st) {
-    lds_dma16(wsrc0 + (long)c * 1024, &lw[st][wv * 1024]);
-    lds_dma16(wsrc1 + (long)c * 1024, &lw[st][(4 + wv) * 1024]);
+    lds_dma16(wbase0 + (long)c * 1024, woff, &lw[st][wv * 1024]);
+    lds_dma16(wbase1 + (long)c * 1024, woff, &lw[st][(4 + wv) * 1024]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lds_dma16(xsrc[i] + (long)c * 64, &lx[st][8 * (4 * wv + i) * 64]);
+    for (int i = 0; i < 4; ++i)
+      lds_dma16(x + (long)c * 64, xoff[i], &lx[st][8 * (4 * wv + i) * 64]);
   };
 
   // per-lane dequantisation scales of the 4 feature tiles (row lane & 15 of each)
@@ -184,6 +190,9 @@ static int launch_gemm(const f16* x, long ldx, const int8_t* wp, const f16* s, c
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// the per-lane byte offsets of the x loads are 32-bit: the x buffer must stay below 2 GiB
+static bool x_offsets_fit(int M, long ldx) { return (long)M * ldx * 2 < 0x7FFFFFFFL; }
+
 }  // namespace ecd
 
 using namespace ecd;
@@ -195,6 +204,7 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
   if (!x || !wp || !s || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
       !al16(x) || !al16(wp) || ldy < N || (res && ldr < N))
     return ECD_EINVAL;
+  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
   return launch_gemm<GEPI_STORE>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s,
                                  (const f16*)res, ldr, (f16*)y, ldy, M, N, K,
                                  (hipStream_t)stream);
@@ -205,6 +215,7 @@ int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, vo
   if (!x || !wp || !s || !mm || M <= 0 || F <= 0 || (F % 2) || K <= 0 || (K % 64) || ldx < K ||
       (ldx % 8) || !al16(x) || !al16(wp) || ldm < F || (ldm % 2) || ((uintptr_t)mm & 3))
     return ECD_EINVAL;
+  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
   return launch_gemm<GEPI_SILU>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s, nullptr, 0,
                                 (f16*)mm, ldm, M, 2 * F, K, (hipStream_t)stream);
 }

@@ -180,7 +180,8 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * fp16 add) -- the dense numerics of int8_mm for M > 16 (app/kernels.py:46-49), used by the
  * prompt pass (app/engine.py:123-153, 174-178).  MFMA-tiled 128 x 128 per workgroup.
  *   x [M, K] fp16 (row stride ldx, 16-byte aligned, K % 64 == 0); wp = ecd_pack_i8(w);
- *   s [N] fp16; res [M, N] (row stride ldr) or NULL; y [M, N] (row stride ldy). */
+ *   s [N] fp16; res [M, N] (row stride ldr) or NULL; y [M, N] (row stride ldy).
+ *   ECD_ENOTSUP when M * ldx * 2 bytes reach 2 GiB (32-bit per-lane load offsets). */
 int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const void* res,
                  long ldr, void* y, long ldy, int M, int N, int K, void* stream);
 

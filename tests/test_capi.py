@@ -83,3 +83,12 @@ def test_python_wrappers_refuse_cpu_tensors():
     with pytest.raises(RuntimeError):
         rms(x, torch.ones(64, dtype=torch.float16))
 
+
+def test_gemm_rejects_x_beyond_32bit_offsets():
+    """The prompt GEMM's per-lane load offsets are 32-bit: an x buffer of 2 GiB or more is
+    refused with ECD_ENOTSUP before any launch."""
+    from estudiocanciones_amd import _ffi
+    L = _ffi.lib()
+    # M = 2^17 rows of ldx = 2^13 halfs -> 2 GiB
+    assert L.ecd_gemm_i8p(16, 8192, 16, 16, None, 0, 16, 64, 1 << 17, 64, 8192, None) == _ffi.ECD_ENOTSUP
+    assert L.ecd_gemm_i8p_silu(16, 8192, 16, 16, 16, 64, 1 << 17, 32, 8192, None) == _ffi.ECD_ENOTSUP
