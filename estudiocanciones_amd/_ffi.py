@@ -39,7 +39,11 @@ SIGNATURES = {
     "ecd_gemm_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_i8p_silu": [_P, c_long, _P, _P, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_prefill_attn": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
+    "ecd_pack_f16": [_P, c_int, c_int, c_int, _P, _P],
+    "ecd_gemm_f16p": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
+    "ecd_gemm_f16p_silu": [_P, c_long, _P, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_packed_bytes": [c_int, c_int],
+    "ecd_packed_bytes_f16": [c_int, c_int],
     "ecd_pack_i8": [_P, c_int, c_int, c_int, _P, _P],
     "ecd_gemv_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int, c_int,
                      c_int, _P],
@@ -70,7 +74,7 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = argtypes
-            fn.restype = c_long if name == "ecd_packed_bytes" else c_int
+            fn.restype = c_long if name.startswith("ecd_packed_bytes") else c_int
         handle.ecd_version.argtypes = []
         handle.ecd_version.restype = ctypes.c_char_p
         _lib = handle

@@ -343,6 +343,43 @@ def gemm_silu_packed(x, wp, s, F, K):
     return mm
 
 
+def pack_f16(w: torch.Tensor, interleave: bool = False) -> torch.Tensor:
+    """Lane-ordered 16 x 64 tile layout (2 KB tiles) of an fp16 [N, K] matrix (K % 64 == 0) for
+    the fp16-weight GEMM; ``interleave`` row-interleaves the two halves (gate | up -> pairs)."""
+    dev = _dev(w, "pack_f16")
+    if w.dtype != torch.float16 or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("pack_f16: w must be a contiguous fp16 [N, K] matrix")
+    N, K = w.shape
+    out = torch.empty(_ffi.lib().ecd_packed_bytes_f16(N, K) // 2, device=dev, dtype=torch.float16)
+    _ffi.call("ecd_pack_f16", w.data_ptr(), N, K, int(interleave), out.data_ptr(), stream_ptr(dev))
+    return out
+
+
+def gemm_f16_packed(x, wp, N, K, bias=None, alpha=1.0, res=None, out=None):
+    """F.linear(x, w, bias) on packed fp16 weights (fp32 accumulation and bias, one fp16 rounding),
+    optionally scaled by ``alpha`` (rounded again) and plus ``res`` (fp16 add) -> [M, N]."""
+    _check_x(x, K, "gemm_f16_packed")
+    M = x.shape[0]
+    y = out if out is not None else torch.empty(M, N, device=x.device, dtype=torch.float16)
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N):
+        raise ValueError("gemm_f16_packed: bias must be fp32 [N]")
+    _ffi.call("ecd_gemm_f16p", x.data_ptr(), x.stride(0), wp.data_ptr(),
+              bias.data_ptr() if bias is not None else None, float(alpha),
+              res.data_ptr() if res is not None else None, res.stride(0) if res is not None else 0,
+              y.data_ptr(), y.stride(0), M, N, K, stream_ptr(x.device))
+    return y
+
+
+def gemm_f16_silu_packed(x, wp, F, K):
+    """silu(x @ gate^T) * (x @ up^T) on interleaved packed fp16 gate | up -> [M, F]."""
+    _check_x(x, K, "gemm_f16_silu_packed")
+    M = x.shape[0]
+    mm = torch.empty(M, F, device=x.device, dtype=torch.float16)
+    _ffi.call("ecd_gemm_f16p_silu", x.data_ptr(), x.stride(0), wp.data_ptr(), mm.data_ptr(),
+              mm.stride(0), M, F, K, stream_ptr(x.device))
+    return mm
+
+
 def prefill_attn(q, kc, vc, pos, S, Hq, Hk, scale=None):
     """Causal prompt-pass attention on MFMA: q [B*S, Hq*HD] fp16, kc/vc [B, Hk, L, HD] holding
     the prompt's K/V, pos [B*S] int64 -> o [B*S, Hq*HD] (row r attends slots [0, pos[r]])."""

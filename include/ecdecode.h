@@ -191,6 +191,24 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
 int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,
                       long ldm, int M, int F, int K, void* stream);
 
+/* fp16-weight GEMM of the codec's flow-matching estimator (the dense nn.Linear / Conv1d-as-GEMM
+ * layers of app/heartcodec/models/transformer.py; torch's F.linear numerics: fp32 accumulation,
+ * fp32 bias, one fp16 rounding).  Weights are packed once with ecd_pack_f16 into lane-ordered
+ * 16 x 64 tiles of 2 KB (ecd_packed_bytes_f16 bytes; rows beyond N zero).
+ *   ecd_gemm_f16p:      y = fp16(x @ w^T + bias); if alpha != 1, y = fp16(y * alpha); then
+ *                       y += res (fp16 add).  bias [N] fp32 or NULL, res [M, N] or NULL.
+ *   ecd_gemm_f16p_silu: w packed with interleave (gate | up), mm[m, j] =
+ *                       fp16(fp16(silu(g)) * u) with g, u the fp16 GEMM outputs (LlamaMLP,
+ *                       transformer.py:181-184).
+ * x [M, K] fp16 (row stride ldx, 16-byte aligned, K % 64 == 0); ECD_ENOTSUP when M * ldx * 2
+ * bytes reach 2 GiB. */
+long ecd_packed_bytes_f16(int N, int K);
+int ecd_pack_f16(const void* w, int N, int K, int interleave, void* out, void* stream);
+int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                  const void* res, long ldr, void* y, long ldy, int M, int N, int K, void* stream);
+int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,
+                       int K, void* stream);
+
 /* Causal attention of the prompt pass on MFMA: row r = b * S + s of q [B * S, Hq * HD] attends
  * cache slots [0, pos[r]] of kc, vc [B, Hk, L, HD] (the prompt's K/V already written), with the
  * decode kernel's numerics (fp32 scores, running max, fp16 probabilities into P.V, fp32 sums).
