@@ -243,15 +243,18 @@ def test_decode_attn_split_invariance(dev):
         assert_close16(o, outs[0], what="split invariance")
 
 
-@pytest.mark.parametrize("B,S,Hq,Hk,L,off", [(2, 100, 24, 8, 128, 0), (1, 64, 8, 2, 160, 37),
-                                              (3, 17, 4, 4, 40, 5), (1, 130, 8, 4, 256, 0)])
-def test_prefill_attn(dev, B, S, Hq, Hk, L, off):
+@pytest.mark.parametrize("B,S,Hq,Hk,L,off,HD", [(2, 100, 24, 8, 128, 0, 128),
+                                                 (1, 64, 8, 2, 160, 37, 128),
+                                                 (3, 17, 4, 4, 40, 5, 128),
+                                                 (1, 130, 8, 4, 256, 0, 128),
+                                                 (2, 100, 6, 6, 128, 0, 64),
+                                                 (1, 70, 8, 2, 100, 9, 64)])
+def test_prefill_attn(dev, B, S, Hq, Hk, L, off, HD):
     """Causal prompt-pass attention on MFMA against the exact softmax and against the decode
     kernel (one split per row) on the same inputs: row s attends [0, off + s]; S not a
     multiple of the 64-row block, G = 1..4, a prompt placed after cached slots."""
     import torch
     from estudiocanciones_amd.kernels import _attn, prefill_attn
-    HD = 128
     R = B * S
     q = randn16(60, R, Hq * HD)
     kc = randn16(61, B, Hk, L, HD)
@@ -265,6 +268,21 @@ def test_prefill_attn(dev, B, S, Hq, Hk, L, off):
     _attn[(R, Hk, 1)](qt, kt, vt, pt, o, o, o, o, S, Hq, Hk, L, 1 / math.sqrt(HD), HD=HD,
                       NSPLIT=1)
     assert_close16(N(got), N(o), what="prefill attn vs decode kernel")
+
+
+@pytest.mark.parametrize("B,Ls,H,HD", [(2, 100, 4, 64), (2, 70, 2, 128)])
+def test_prefill_attn_full_sequence(dev, B, Ls, H, HD):
+    """Every position at the last slot: non-causal attention over the whole sequence (the codec
+    estimator's SDPA without a mask), against the exact softmax."""
+    from estudiocanciones_amd.kernels import prefill_attn
+    R = B * Ls
+    q = randn16(70, R, H * HD)
+    kc = randn16(71, B, H, Ls, HD)
+    vc = randn16(72, B, H, Ls, HD)
+    pos = np.full(R, Ls - 1, np.int64)
+    exact = OK.attention_exact(q, kc, vc, pos, Ls, H, H, HD)
+    got = prefill_attn(T(q, dev), T(kc, dev), T(vc, dev), T(pos, dev), Ls, H, H)
+    assert_close16(N(got), exact, what=f"full attention T={Ls} HD={HD}")
 
 
 # ---------------------------------------------------------------- SiLU * mul
