@@ -34,6 +34,15 @@ SIGNATURES = {
     "ecd_sample_topk": [_P, c_long, c_int, c_int, c_float, c_float, c_int, c_int, _P, _P, _P, c_int,
                         _P, c_long, _P],
     "ecd_copy_bytes": [_P, _P, c_long, _P],
+    "ecd_codec_rope_table": [_P, c_int, c_int, _P],
+    "ecd_codec_rope_heads": [_P, c_long, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P],
+    "ecd_codec_norm_mod": [_P, _P, _P, _P, c_long, _P, _P, _P, _P, _P, c_long, _P, c_int, c_int,
+                           c_int, c_int, c_float, _P],
+    "ecd_codec_cols3": [_P, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P],
+    "ecd_codec_timestep": [_P, _P, c_int, _P],
+    "ecd_codec_silu": [_P, _P, c_long, _P],
+    "ecd_codec_euler": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, c_float,
+                        c_float, c_int, _P],
     "ecd_gemv_i8p_splitk": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, c_int,
                             _P, c_int, _P],
     "ecd_gemm_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],

@@ -1,0 +1,347 @@
+"""The codec's flow-matching estimator and Euler solver on gfx950.
+
+Mirrors ``LlamaTransformer`` with ``norm_type="ada_norm_single"``
+(app/heartcodec/models/transformer.py:275-396) and ``FlowMatching.solve_euler``
+(app/heartcodec/models/flow_matching.py:161-210), run in fp16 as the reference loads the codec
+(app/codec_lite.py:13,27).  Every step is a HIP kernel of ``libecdecode.so``:
+
+    ProjectLayer (k = 3 conv + Linear)   ecd_codec_cols3 + ecd_gemm_f16p (x2)
+    adaLN + RMSNorm / gated residual     ecd_codec_norm_mod
+    q | k | v projection                 ecd_gemm_f16p (one GEMM, N = 3D)
+    interleaved RoPE -> heads            ecd_codec_rope_heads
+    non-causal SDPA                      ecd_prefill_attn (every row at the last slot)
+    LlamaMLP                             ecd_gemm_f16p_silu + ecd_gemm_f16p
+    timestep path                        ecd_codec_timestep, ecd_gemm_f16p, ecd_codec_silu
+    Euler + CFG + in-context blend       ecd_codec_euler
+
+The solver computes the adaLN vectors of all steps in one batched pass before the loop (they
+depend only on t), and feeds the estimator's [x | incontext | mu] input to the first
+convolution as channel segments instead of concatenated copies.  There is no CPU fallback:
+without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _ffi
+from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_attn,
+                      stream_ptr)
+
+__all__ = ["LlamaTransformer", "solve_euler", "mlp_hidden", "euler_times"]
+
+EPS = 1e-6
+SQRT1_3 = 3 ** -0.5
+
+
+def mlp_hidden(dim: int, multiple_of: int = 256) -> int:
+    """LlamaMLP hidden width (transformer.py:170-172)."""
+    h = int(2 * (4 * dim) / 3)
+    return multiple_of * ((h + multiple_of - 1) // multiple_of)
+
+
+def euler_times(t_span) -> tuple[list[np.float32], list[np.float32]]:
+    """The fp32 (t, dt) of every Euler step as solve_euler advances them (flow_matching.py:
+    172-173, 204-207): t += dt, then dt = t_span[k + 1] - t."""
+    ts = np.asarray(t_span, dtype=np.float32)
+    t, dt = ts[0], np.float32(ts[1] - ts[0])
+    out_t, out_dt = [], []
+    for step in range(1, len(ts)):
+        out_t.append(np.float32(t))
+        out_dt.append(np.float32(dt))
+        t = np.float32(t + dt)
+        if step < len(ts) - 1:
+            dt = np.float32(ts[step + 1] - t)
+    return out_t, out_dt
+
+
+def _off(t: torch.Tensor, elems: int) -> int:
+    """Device address of element ``elems`` of a contiguous fp16 tensor."""
+    return t.data_ptr() + 2 * int(elems)
+
+
+class _Linear:
+    """One nn.Linear (or a k = 3 Conv1d as a GEMM) with packed fp16 weights, fp32 bias."""
+
+    def __init__(self, w: torch.Tensor, b: torch.Tensor | None = None, interleave=False):
+        self.N, self.K = w.shape
+        self.wp = pack_f16(w.contiguous(), interleave=interleave)
+        self.b = None if b is None else b.float().contiguous()
+
+    def __call__(self, x, out, alpha=1.0, res=None):
+        return gemm_f16_packed(x, self.wp, self.N, self.K, self.b, alpha, res, out)
+
+
+class _Block:
+    """Weights of one LlamaTransformerBlock (transformer.py:184-255)."""
+
+    def __init__(self, get, pre: str, dim: int, heads: int, head_dim: int):
+        self.D, self.H, self.HD = dim, heads, head_dim
+        self.qkv = _Linear(torch.cat([get(pre + "attn.q_proj.weight"),
+                                      get(pre + "attn.k_proj.weight"),
+                                      get(pre + "attn.v_proj.weight")], 0))
+        self.o = _Linear(get(pre + "attn.o_proj.weight"))
+        gate, up = get(pre + "mlp.gate.weight"), get(pre + "mlp.up.weight")
+        self.F = gate.shape[0]
+        self.gu = pack_f16(torch.cat([gate, up], 0).contiguous(), interleave=True)
+        self.down = _Linear(get(pre + "mlp.down.weight"))
+        self.attn_norm = get(pre + "attn_norm.weight")
+        self.mlp_norm = get(pre + "mlp_norm.weight")
+        self.table = get(pre + "scale_shift_table")        # [6, D]
+
+
+class _Ada:
+    """AdaLayerNormSingleFlow weights (transformer.py:429-458)."""
+
+    def __init__(self, get, pre: str):
+        te = pre + "emb.timestep_embedder."
+        self.l1 = _Linear(get(te + "linear_1.weight"), get(te + "linear_1.bias"))
+        self.l2 = _Linear(get(te + "linear_2.weight"), get(te + "linear_2.bias"))
+        self.lin = _Linear(get(pre + "linear.weight"), get(pre + "linear.bias"))
+
+
+class _Project:
+    """ProjectLayer(kernel_size=3) weights (transformer.py:258-272): the conv as a GEMM over
+    [t - 1 | t | t + 1] columns, W'[o, j * Cin + c] = weight[o, c, j]."""
+
+    def __init__(self, get, pre: str):
+        w = get(pre + "ffn_1.weight")                       # [Cout, Cin, 3]
+        self.cout, self.cin, k = w.shape
+        if k != 3:
+            raise ValueError(f"{pre}ffn_1: kernel size {k}, expected 3")
+        self.conv = _Linear(w.permute(0, 2, 1).reshape(self.cout, 3 * self.cin).contiguous(),
+                            get(pre + "ffn_1.bias"))
+        self.ffn_2 = _Linear(get(pre + "ffn_2.weight"), get(pre + "ffn_2.bias"))
+
+
+class LlamaTransformer:
+    """The estimator: ``forward(hidden_states, timestep)`` as in transformer.py:345-396.
+
+    ``sd`` maps the reference's parameter names relative to the estimator
+    (``proj_in.ffn_1.weight``, ``transformer_blocks.0.attn.q_proj.weight``, ...) to tensors;
+    ``from_codec_state_dict`` takes a whole HeartCodec state dict."""
+
+    def __init__(self, sd: dict, num_attention_heads=24, attention_head_dim=64, in_channels=1024,
+                 out_channels=256, num_layers=24, num_layers_2=6, device="cuda"):
+        self.dev = torch.device(device)
+        if self.dev.type != "cuda":
+            raise RuntimeError("the codec estimator runs only on a ROCm GPU")
+        self.H, self.HD = num_attention_heads, attention_head_dim
+        self.D = self.H * self.HD
+        self.D2 = 2 * self.D
+        self.cin, self.cout = in_channels, out_channels
+
+        def get(name):
+            return sd[name].to(device=self.dev, dtype=torch.float16).contiguous()
+
+        self.proj_in = _Project(get, "proj_in.")
+        self.blocks = [_Block(get, f"transformer_blocks.{i}.", self.D, self.H, self.HD)
+                       for i in range(num_layers)]
+        self.blocks_2 = [_Block(get, f"transformer_blocks_2.{i}.", self.D2, self.H, 2 * self.HD)
+                         for i in range(num_layers_2)]
+        self.connection_proj = _Project(get, "connection_proj.")
+        self.proj_out = _Project(get, "proj_out.")
+        self.table = get("scale_shift_table")               # [2, D]
+        self.table_2 = get("scale_shift_table_2")           # [2, D2]
+        self.ada = _Ada(get, "adaln_single.")
+        self.ada_2 = _Ada(get, "adaln_single_2.")
+        if (self.proj_in.cin, self.proj_in.cout) != (in_channels, self.D):
+            raise ValueError("proj_in shape does not match the configuration")
+        self._bufs = {}
+        self._rope = {}
+
+    @classmethod
+    def from_codec_state_dict(cls, sd: dict, prefix="flow_matching.estimator.", **cfg):
+        return cls({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}, **cfg)
+
+    # ------------------------------------------------------------ timestep path
+    def timestep_vectors(self, t: torch.Tensor):
+        """adaln_single / adaln_single_2 for every entry of t [n] fp32: (tmod [n, 6D],
+        emb [n, D], tmod_2 [n, 6D2], emb_2 [n, D2]) (transformer.py:354-357, :377-380)."""
+        t = t.to(device=self.dev, dtype=torch.float32).contiguous()
+        n = t.numel()
+        st = stream_ptr(self.dev)
+        sin = torch.empty(n, 512, device=self.dev, dtype=torch.float16)
+        _ffi.call("ecd_codec_timestep", t.data_ptr(), sin.data_ptr(), n, st)
+        out = []
+        for ada, D in ((self.ada, self.D), (self.ada_2, self.D2)):
+            h = ada.l1(sin, torch.empty(n, D, device=self.dev, dtype=torch.float16))
+            _ffi.call("ecd_codec_silu", h.data_ptr(), h.data_ptr(), h.numel(), st)
+            emb = ada.l2(h, torch.empty(n, D, device=self.dev, dtype=torch.float16))
+            se = torch.empty_like(emb)
+            _ffi.call("ecd_codec_silu", emb.data_ptr(), se.data_ptr(), emb.numel(), st)
+            tmod = ada.lin(se, torch.empty(n, 6 * D, device=self.dev, dtype=torch.float16))
+            out += [tmod, emb]
+        return tuple(out)
+
+    # ------------------------------------------------------------ buffers
+    def _buffers(self, B: int, T: int):
+        key = (B, T)
+        if key not in self._bufs:
+            M, D2 = B * T, self.D2
+            F2 = max(b.F for b in self.blocks + self.blocks_2)
+            cmax = max(self.cin + self.D, D2, self.cin)
+            e = lambda *s: torch.empty(*s, device=self.dev, dtype=torch.float16)
+            self._bufs[key] = dict(
+                cols=e(M * 3 * cmax), t1=e(M * D2), x=e(M * D2), y=e(M * D2), qkv=e(M * 3 * D2),
+                q=e(M * D2), k=e(M * D2), v=e(M * D2), o=e(M * D2), h=e(M * D2), m=e(M * F2),
+                out=e(M, self.cout),
+                pos=torch.full((M,), T - 1, device=self.dev, dtype=torch.int64))
+        return self._bufs[key]
+
+    def _rope_table(self, T: int, HD: int):
+        key = (T, HD)
+        if key not in self._rope:
+            tab = torch.empty(T, HD, device=self.dev, dtype=torch.float16)
+            _ffi.call("ecd_codec_rope_table", tab.data_ptr(), T, HD, stream_ptr(self.dev))
+            self._rope[key] = tab
+        return self._rope[key]
+
+    # ------------------------------------------------------------ pieces
+    def _cols(self, segs, B, T, buf):
+        """k = 3 columns of the channel concatenation of ``segs`` [(tensor, width, bmod, bzero)]."""
+        n = len(segs)
+        ptr = (ctypes.c_void_p * n)(*[s[0].data_ptr() for s in segs])
+        ld = (ctypes.c_long * n)(*[s[0].stride(-2) for s in segs])
+        w = (ctypes.c_int * n)(*[s[1] for s in segs])
+        bm = (ctypes.c_int * n)(*[s[2] for s in segs])
+        bz = (ctypes.c_int * n)(*[s[3] for s in segs])
+        C = sum(s[1] for s in segs)
+        cols = buf["cols"][:B * T * 3 * C].view(B * T, 3 * C)
+        _ffi.call("ecd_codec_cols3", ptr, ld, w, bm, bz, n, cols.data_ptr(), B, T,
+                  stream_ptr(self.dev))
+        return cols
+
+    def _project(self, p: _Project, cols, buf):
+        M = cols.shape[0]
+        t1 = p.conv(cols, buf["t1"][:M * p.cout].view(M, p.cout), alpha=SQRT1_3)
+        return t1
+
+    def _norm(self, x, h, gate, w, shift, scale, tm_ld, y, T, norm):
+        """gate/shift/scale: (table address, vector address); gate None: no residual."""
+        R, D = x.shape
+        g_tab, g_tm, g_ld = gate if gate is not None else (None, None, 0)
+        _ffi.call("ecd_codec_norm_mod", x.data_ptr(), None if h is None else h.data_ptr(),
+                  g_tab, g_tm, g_ld, None if w is None else w.data_ptr(), shift[0], shift[1],
+                  scale[0], scale[1], tm_ld, y.data_ptr(), R, T, D, norm, EPS,
+                  stream_ptr(self.dev))
+
+    def _blocks(self, blocks, x, B, T, tmod, tm_ld, buf):
+        """The LlamaTransformerBlock stack; returns the pending gated residual (h, gate) of the
+        last block's MLP, which the following norm applies."""
+        M = B * T
+        h, gate = None, None
+        st = stream_ptr(self.dev)
+        for bp in blocks:
+            D, H, HD = bp.D, bp.H, bp.HD
+            ch = lambda i: (_off(bp.table, i * D), _off(tmod, i * D))
+            y = buf["y"][:M * D].view(M, D)
+            self._norm(x, h, None if gate is None else gate + (tm_ld,), bp.attn_norm, ch(0), ch(1),
+                       tm_ld, y, T, 0)
+            qkv = bp.qkv(y, buf["qkv"][:M * 3 * D].view(M, 3 * D))
+            q = buf["q"][:M * D].view(M, D)
+            k = buf["k"][:M * D].view(B, H, T, HD)
+            v = buf["v"][:M * D].view(B, H, T, HD)
+            _ffi.call("ecd_codec_rope_heads", qkv.data_ptr(), qkv.stride(0),
+                      self._rope_table(T, HD).data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                      B, T, H, HD, st)
+            o = prefill_attn(q, k, v, buf["pos"][:M], T, H, H, out=buf["o"][:M * D].view(M, D))
+            ha = bp.o(o, buf["h"][:M * D].view(M, D))
+            g_a = ch(2) + (tm_ld,)
+            self._norm(x, ha, g_a, bp.mlp_norm, ch(3), ch(4), tm_ld, y, T, 0)
+            m = gemm_f16_silu_packed(y, bp.gu, bp.F, D, out=buf["m"][:M * bp.F].view(M, bp.F))
+            h = bp.down(m, buf["h"][:M * D].view(M, D))
+            gate = ch(5)
+        return h, gate
+
+    def _run(self, segs, B, T, tm):
+        """Estimator body over input segments; tm = (tmod, emb, tmod_2, emb_2, per_batch)."""
+        tmod, emb, tmod2, emb2, per_batch = tm
+        buf = self._buffers(B, T)
+        M, D, D2 = B * T, self.D, self.D2
+        # proj_in
+        cols = self._cols(segs, B, T, buf)
+        t1 = self._project(self.proj_in, cols, buf)
+        x = self.proj_in.ffn_2(t1, buf["x"][:M * D].view(M, D))
+        h, gate = self._blocks(self.blocks, x, B, T, tmod, 6 * D if per_batch else 0, buf)
+        # norm_out with the scale_shift_table modulation
+        s = buf["o"][:M * D].view(M, D)
+        e_ld = D if per_batch else 0
+        self._norm(x, h, gate + (6 * D if per_batch else 0,), None,
+                   (_off(self.table, 0), _off(emb, 0)), (_off(self.table, D), _off(emb, 0)),
+                   e_ld, s, T, 1)
+        # connection_proj over [hidden_states | s]
+        cols = self._cols(segs + [(s, D, B, 0)], B, T, buf)
+        t1 = self._project(self.connection_proj, cols, buf)
+        x2 = self.connection_proj.ffn_2(t1, buf["x"][:M * D2].view(M, D2))
+        h, gate = self._blocks(self.blocks_2, x2, B, T, tmod2, 6 * D2 if per_batch else 0, buf)
+        s2 = buf["o"][:M * D2].view(M, D2)
+        e_ld = D2 if per_batch else 0
+        self._norm(x2, h, gate + (6 * D2 if per_batch else 0,), None,
+                   (_off(self.table_2, 0), _off(emb2, 0)), (_off(self.table_2, D2), _off(emb2, 0)),
+                   e_ld, s2, T, 1)
+        cols = self._cols([(s2, D2, B, 0)], B, T, buf)
+        t1 = self._project(self.proj_out, cols, buf)
+        return self.proj_out.ffn_2(t1, buf["out"][:M])
+
+    # ------------------------------------------------------------ reference entry point
+    def forward(self, hidden_states: torch.Tensor, timestep: torch.Tensor) -> torch.Tensor:
+        """hidden_states [B, T, in_channels] fp16, timestep [B] -> [B, T, out_channels] fp16
+        (a new tensor)."""
+        B, T, C = hidden_states.shape
+        if C != self.cin or hidden_states.dtype != torch.float16 or not hidden_states.is_contiguous():
+            raise ValueError(f"hidden_states must be contiguous fp16 [B, T, {self.cin}]")
+        if timestep.numel() != B:
+            raise ValueError("timestep must hold one value per batch entry")
+        tm = self.timestep_vectors(timestep.reshape(-1)) + (True,)
+        out = self._run([(hidden_states.view(B * T, C), C, B, 0)], B, T, tm)
+        return out.view(B, T, self.cout).clone()
+
+    __call__ = forward
+
+
+def solve_euler(est: LlamaTransformer, x: torch.Tensor, incontext_x: torch.Tensor,
+                incontext_length: int, t_span, mu: torch.Tensor, guidance_scale: float,
+                copy_incontext: bool = False) -> torch.Tensor:
+    """FlowMatching.solve_euler (flow_matching.py:161-210) on the GPU.  x, incontext_x
+    [B, T, C] fp16, mu [B, T, Cmu] fp16, t_span the fp32 time grid.  Returns the final x (a new
+    tensor).  ``copy_incontext`` also applies inference_codes' final
+    ``latents[:, :L] = incontext_latents[:, :L]`` (flow_matching.py:156-158)."""
+    B, T, C = x.shape
+    Cmu = mu.shape[-1]
+    if C + C + Cmu != est.cin:
+        raise ValueError("x, incontext_x and mu widths must add up to the estimator's input")
+    for a in (x, incontext_x, mu):
+        if a.dtype != torch.float16 or not a.is_contiguous() or a.shape[:2] != (B, T):
+            raise ValueError("x, incontext_x, mu must be contiguous fp16 [B, T, *]")
+    L = int(incontext_length)
+    ts, dts = euler_times(t_span)
+    n = len(ts)
+    cfg = guidance_scale > 1.0
+    dev = est.dev
+    st = stream_ptr(dev)
+    tmod, emb, tmod2, emb2 = est.timestep_vectors(torch.tensor(np.array(ts, np.float32)))
+    noise = x.clone()
+    x = x.clone()
+    ic = incontext_x
+    B2 = 2 * B if cfg else B
+    # rows of the estimator input: [x | incontext | 0 (uncond) or mu (cond)] over 2B entries
+    segs = [(x.view(B * T, C), C, B, 0), (ic.view(B * T, C), C, B, 0),
+            (mu.view(B * T, Cmu), Cmu, B, B if cfg else 0)]
+    _ffi.call("ecd_codec_euler", x.data_ptr(), noise.data_ptr(), ic.data_ptr(), None, int(cfg),
+              B, T, C, L, 0.0, 0.0, float(ts[0]), 0, st)
+    D, D2 = est.D, est.D2
+    for k in range(n):
+        tm = (tmod[k], emb[k], tmod2[k], emb2[k], False)
+        d = est._run(segs, B2, T, tm)
+        last = k == n - 1
+        if last and copy_incontext:
+            mode, tb = 1, 0.0
+        else:
+            mode, tb = 0, (0.0 if last else float(ts[k + 1]))
+        _ffi.call("ecd_codec_euler", x.data_ptr(), noise.data_ptr(), ic.data_ptr(), d.data_ptr(),
+                  int(cfg), B, T, C, 0 if (last and not copy_incontext) else L, float(dts[k]),
+                  float(guidance_scale), tb, mode, st)
+    return x

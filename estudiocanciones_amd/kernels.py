@@ -370,17 +370,19 @@ def gemm_f16_packed(x, wp, N, K, bias=None, alpha=1.0, res=None, out=None):
     return y
 
 
-def gemm_f16_silu_packed(x, wp, F, K):
+def gemm_f16_silu_packed(x, wp, F, K, out=None):
     """silu(x @ gate^T) * (x @ up^T) on interleaved packed fp16 gate | up -> [M, F]."""
     _check_x(x, K, "gemm_f16_silu_packed")
     M = x.shape[0]
-    mm = torch.empty(M, F, device=x.device, dtype=torch.float16)
+    mm = out if out is not None else torch.empty(M, F, device=x.device, dtype=torch.float16)
+    if mm.shape != (M, F) or mm.dtype != torch.float16 or mm.stride(1) != 1:
+        raise ValueError("gemm_f16_silu_packed: out must be fp16 [M, F] with unit inner stride")
     _ffi.call("ecd_gemm_f16p_silu", x.data_ptr(), x.stride(0), wp.data_ptr(), mm.data_ptr(),
               mm.stride(0), M, F, K, stream_ptr(x.device))
     return mm
 
 
-def prefill_attn(q, kc, vc, pos, S, Hq, Hk, scale=None):
+def prefill_attn(q, kc, vc, pos, S, Hq, Hk, scale=None, out=None):
     """Causal prompt-pass attention on MFMA: q [B*S, Hq*HD] fp16, kc/vc [B, Hk, L, HD] holding
     the prompt's K/V, pos [B*S] int64 -> o [B*S, Hq*HD] (row r attends slots [0, pos[r]])."""
     R = q.shape[0]
@@ -389,7 +391,9 @@ def prefill_attn(q, kc, vc, pos, S, Hq, Hk, scale=None):
         raise ValueError("prefill_attn: q must be contiguous fp16 [B*S, Hq*HD]")
     if not (kc.is_contiguous() and vc.is_contiguous()) or pos.dtype != torch.int64:
         raise ValueError("prefill_attn: contiguous caches and int64 positions required")
-    o = torch.empty_like(q)
+    o = out if out is not None else torch.empty_like(q)
+    if o.shape != q.shape or o.dtype != torch.float16 or not o.is_contiguous():
+        raise ValueError("prefill_attn: out must be a contiguous fp16 tensor shaped like q")
     pc = pos.contiguous()
     _ffi.call("ecd_prefill_attn", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
               pc.data_ptr(), o.data_ptr(), B, S, Hq, Hk, L, HD,

@@ -219,6 +219,54 @@ int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long l
 int ecd_prefill_attn(const void* q, const void* kc, const void* vc, const int64_t* pos, void* o,
                      int B, int S, int Hq, int Hk, int L, int HD, float scale, void* stream);
 
+/* ---- codec flow-matching estimator glue (app/heartcodec/models/transformer.py,
+ * app/heartcodec/models/flow_matching.py).  All tensors fp16 unless stated, 16-byte aligned,
+ * rounded to fp16 at the points where the reference's eager fp16 ops round. */
+
+/* RoPE table tab [T, HD/2] of (cos, sin) fp16 pairs, computed in fp16 like
+ * RotaryEmbedding.get_sin_cos (transformer.py:28-42, base 10000). */
+int ecd_codec_rope_table(void* tab, int T, int HD, void* stream);
+
+/* Interleaved RoPE on the q and k heads of qkv [B*T, ldq] (q | k | v, H*HD columns each) ->
+ * q [B*T, H*HD], k and v [B, H, T, HD] (apply_rope_vec, transformer.py:108-122). HD % 8 == 0. */
+int ecd_codec_rope_heads(const void* qkv, long ldq, const void* tab, void* q, void* k, void* v,
+                         int B, int T, int H, int HD, void* stream);
+
+/* Row r of x [R, D] (batch r / T): with h, x = fp16(x + fp16(fp16(g_tab + g_tm[b]) * h)) in
+ * place (the gated residual, transformer.py:241-248); then norm 0 = RMSNorm with weight w
+ * (:9-18), norm 1 = LayerNorm without affine (:333-334), and
+ * y = fp16(fp16(n * fp16(1 + scale)) + shift) with shift = fp16(sh_tab + sh_tm[b]),
+ * scale = fp16(sc_tab + sc_tm[b]) (:234-239, :366-370).  g_tm of batch b starts at b * g_ld,
+ * sh_tm and sc_tm at b * tm_ld (0: shared).  D % 8 == 0, D <= 4096. */
+int ecd_codec_norm_mod(void* x, const void* h, const void* g_tab, const void* g_tm, long g_ld,
+                       const void* w, const void* sh_tab, const void* sh_tm, const void* sc_tab,
+                       const void* sc_tm, long tm_ld, void* y, int R, int T, int D, int norm,
+                       float eps, void* stream);
+
+/* Columns of nn.Conv1d(k = 3, padding = 1) (ProjectLayer, transformer.py:258-272) over the
+ * channel concatenation of up to 4 segments: out [B*T, 3*C], out[b*T + t, j*C + c] =
+ * in[b, t + j - 1, c] (zero outside [0, T)); segment i gives seg_w[i] channels from
+ * seg_ptr[i] + ((b % seg_bmod[i]) * T + s) * seg_ld[i] for b >= seg_bzero[i], zeros below
+ * (solve_euler's input, flow_matching.py:183-193; torch.cat of transformer.py:372). */
+int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* seg_w,
+                    const int* seg_bmod, const int* seg_bzero, int nseg, void* out, int B, int T,
+                    void* stream);
+
+/* Timestep sinusoid out [n, 512] fp16 from t [n] fp32 (PixArtAlphaCombinedFlowEmbeddings.
+ * timestep_embedding, transformer.py:408-426). */
+int ecd_codec_timestep(const float* t, void* out, int n, void* stream);
+
+/* y = fp16(silu(x)) over n elements (nn.SiLU, transformer.py:435, 451). */
+int ecd_codec_silu(const void* x, void* y, long n, void* stream);
+
+/* One Euler step on x [B, T, C]: with cfg 1, dphi [2B, T, C] (unconditional half first) is
+ * combined with guidance g; with cfg 0, dphi [B, T, C] is the velocity (dphi NULL: no update).
+ * Then on rows t < L: mode 0 the in-context blend at time tb for the next estimator call,
+ * mode 1 the in-context latents (FlowMatching.solve_euler, flow_matching.py:179-203, and
+ * :156-158).  C % 8 == 0. */
+int ecd_codec_euler(void* x, const void* noise, const void* ic, const void* dphi, int cfg, int B,
+                    int T, int C, int L, float dt, float g, float tb, int mode, void* stream);
+
 /* Plain device-to-device byte copy (nbytes and both pointers 16-byte aligned).  No reference
  * counterpart: a kernel of known HBM traffic used to calibrate hardware byte counters. */
 int ecd_copy_bytes(const void* src, void* dst, long nbytes, void* stream);

@@ -1,0 +1,296 @@
+"""Oracle of the codec's flow-matching estimator and Euler solver (test infrastructure only).
+
+Restates, in numpy, the fp16 forward of ``LlamaTransformer`` with ``norm_type="ada_norm_single"``
+(app/heartcodec/models/transformer.py:275-396) and ``FlowMatching.solve_euler``
+(app/heartcodec/models/flow_matching.py:161-210) as the reference runs them (weights and
+activations fp16, app/codec_lite.py:13,27).  Every eager fp16 torch op computes in fp32 and
+rounds its result to fp16; each such rounding point is an ``f16(...)`` here.  Products and sums
+inside one library call (matmul, convolution, reductions, softmax) are evaluated in float64,
+which any fp32 accumulation order of the reference lies within the fp16 output tolerance of.
+
+Weights are a dict of numpy arrays under the reference's parameter names relative to the
+estimator (``proj_in.ffn_1.weight``, ``transformer_blocks.3.attn.q_proj.weight``, ...).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .numerics import f16, f32
+
+EPS = 1e-6
+SQRT1_3 = 3 ** -0.5
+
+
+def mlp_hidden(dim: int, multiple_of: int = 256) -> int:
+    """LlamaMLP hidden width (transformer.py:170-172)."""
+    h = int(2 * (4 * dim) / 3)
+    return multiple_of * ((h + multiple_of - 1) // multiple_of)
+
+
+# ---------------------------------------------------------------- elementwise pieces
+def silu(x) -> np.ndarray:
+    """nn.SiLU on fp16: fp16(x / (1 + exp(-x))) evaluated in fp32 or better."""
+    a = np.asarray(x, dtype=np.float16).astype(np.float64)
+    return f16(a / (1.0 + np.exp(-a)))
+
+
+def linear(x, w, b=None) -> np.ndarray:
+    """F.linear on fp16: fp16(x @ w^T + b) with wide accumulation."""
+    y = np.asarray(x, np.float16).astype(np.float64) @ np.asarray(w, np.float16).astype(np.float64).T
+    if b is not None:
+        y = y + np.asarray(b, np.float16).astype(np.float64)
+    return f16(y)
+
+
+def rms_norm(x, w, eps=EPS) -> np.ndarray:
+    """RMSNorm.forward (transformer.py:15-18) on fp16: every op rounds to fp16."""
+    x = np.asarray(x, np.float16)
+    sq = f16(f32(x) * f32(x))
+    var = f16(sq.astype(np.float64).mean(-1, keepdims=True))
+    r = f16(1.0 / np.sqrt(f32(f16(f32(var) + np.float32(eps))).astype(np.float64)))
+    n = f16(f32(x) * f32(r))
+    return f16(f32(np.asarray(w, np.float16)) * f32(n))
+
+
+def layer_norm(x, eps=EPS) -> np.ndarray:
+    """nn.LayerNorm(elementwise_affine=False) on fp16: fp32 statistics, one rounding
+    (transformer.py:333-334)."""
+    a = np.asarray(x, np.float16).astype(np.float64)
+    mu = a.mean(-1, keepdims=True)
+    var = ((a - mu) ** 2).mean(-1, keepdims=True)
+    return f16((a - mu) / np.sqrt(var + eps))
+
+
+def modulate(n, shift, scale) -> np.ndarray:
+    """n * (1 + scale) + shift on fp16 tensors (transformer.py:239, :245, :370, :393)."""
+    one = f16(np.float32(1.0) + f32(scale))
+    return f16(f32(f16(f32(n) * f32(one))) + f32(shift))
+
+
+# ---------------------------------------------------------------- RoPE
+def rope_table(T: int, HD: int):
+    """RotaryEmbedding.get_sin_cos in fp16 (transformer.py:28-42): (sin, cos) [T, HD/2]."""
+    i = np.arange(0, HD, 2, dtype=np.float32)
+    ex = f16(i * np.float32(1.0 / HD))
+    p = f16(np.power(np.float32(10000.0), f32(ex)))
+    inv = f16(np.float32(1.0) / f32(p))
+    t = f16(np.arange(T, dtype=np.float32))
+    fr = f16(f32(t)[:, None] * f32(inv)[None, :])
+    return f16(np.sin(f32(fr))), f16(np.cos(f32(fr)))
+
+
+def apply_rope_vec(x, sin, cos) -> np.ndarray:
+    """apply_rope_vec (transformer.py:108-119): interleaved pairs (x[2i], x[2i+1]) of
+    x [B, H, T, HD] rotated by the fp16 table, every product and sum rounded to fp16."""
+    x = np.asarray(x, np.float16)
+    x1, x2 = f32(x[..., 0::2]), f32(x[..., 1::2])
+    s, c = f32(sin)[None, None], f32(cos)[None, None]
+    o1 = f16(f32(f16(x1 * c)) - f32(f16(x2 * s)))
+    o2 = f16(f32(f16(x1 * s)) + f32(f16(x2 * c)))
+    out = np.empty_like(x)
+    out[..., 0::2] = o1
+    out[..., 1::2] = o2
+    return out
+
+
+# ---------------------------------------------------------------- attention, MLP, blocks
+def sdpa(q, k, v) -> np.ndarray:
+    """Non-causal scaled_dot_product_attention (transformer.py:140-147): exact softmax over all
+    keys, scale 1/sqrt(HD), fp16 output.  q, k, v [B, H, T, HD]."""
+    q64, k64, v64 = (np.asarray(a, np.float16).astype(np.float64) for a in (q, k, v))
+    s = q64 @ np.swapaxes(k64, -1, -2) / math.sqrt(q.shape[-1])
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return f16((p @ v64) / p.sum(-1, keepdims=True))
+
+
+def attention(p: dict, pre: str, x, H: int, HD: int) -> np.ndarray:
+    """LlamaAttention.forward without mask (transformer.py:86-149).  x [B, T, D]."""
+    B, T, _ = x.shape
+
+    def heads(a):
+        return a.reshape(B, T, H, HD).transpose(0, 2, 1, 3)
+
+    q = heads(linear(x, p[pre + "q_proj.weight"]))
+    k = heads(linear(x, p[pre + "k_proj.weight"]))
+    v = heads(linear(x, p[pre + "v_proj.weight"]))
+    sin, cos = rope_table(T, HD)
+    q, k = apply_rope_vec(q, sin, cos), apply_rope_vec(k, sin, cos)
+    o = sdpa(q, k, v).transpose(0, 2, 1, 3).reshape(B, T, H * HD)
+    return linear(o, p[pre + "o_proj.weight"])
+
+
+def llama_mlp(p: dict, pre: str, x) -> np.ndarray:
+    """LlamaMLP.forward (transformer.py:178-181): down(fp16(silu(gate(x)) * up(x)))."""
+    g = silu(linear(x, p[pre + "gate.weight"]))
+    u = linear(x, p[pre + "up.weight"])
+    return linear(f16(f32(g) * f32(u)), p[pre + "down.weight"])
+
+
+def block(p: dict, pre: str, x, tmod, H: int, HD: int) -> np.ndarray:
+    """LlamaTransformerBlock.forward with use_ada_layer_norm_single (transformer.py:225-249).
+    tmod [B, 6 * D]."""
+    B, _, D = x.shape
+    mods = f16(f32(p[pre + "scale_shift_table"])[None] + f32(tmod).reshape(B, 6, D))
+    sh_msa, sc_msa, g_msa, sh_mlp, sc_mlp, g_mlp = (mods[:, i:i + 1] for i in range(6))
+    n = modulate(rms_norm(x, p[pre + "attn_norm.weight"]), sh_msa, sc_msa)
+    h = attention(p, pre + "attn.", n, H, HD)
+    x = f16(f32(x) + f32(f16(f32(g_msa) * f32(h))))
+    n = modulate(rms_norm(x, p[pre + "mlp_norm.weight"]), sh_mlp, sc_mlp)
+    h = llama_mlp(p, pre + "mlp.", n)
+    return f16(f32(x) + f32(f16(f32(g_mlp) * f32(h))))
+
+
+def project_layer(p: dict, pre: str, x) -> np.ndarray:
+    """ProjectLayer with kernel_size 3 (transformer.py:258-272): Conv1d(padding 1) over time on
+    x [B, T, Cin] (cross-correlation; the library call rounds, then its bias add rounds), times
+    3^-0.5 (rounded), then Linear with bias."""
+    w = np.asarray(p[pre + "ffn_1.weight"], np.float16).astype(np.float64)   # [Cout, Cin, 3]
+    a = np.asarray(x, np.float16).astype(np.float64)
+    B, T, _ = a.shape
+    pad = np.zeros((B, T + 2, a.shape[2]))
+    pad[:, 1:T + 1] = a
+    acc = sum(pad[:, j:j + T] @ w[:, :, j].T for j in range(3))
+    y = f16(f32(f16(acc)) + f32(p[pre + "ffn_1.bias"]))
+    y = f16(f32(y) * np.float32(SQRT1_3))
+    return linear(y, p[pre + "ffn_2.weight"], p[pre + "ffn_2.bias"])
+
+
+# ---------------------------------------------------------------- timestep path
+def timestep_sinusoid(t) -> np.ndarray:
+    """PixArtAlphaCombinedFlowEmbeddings.timestep_embedding (transformer.py:408-421) in fp32,
+    cast to fp16 (:425).  t [n] fp32 -> [n, 512]."""
+    i = np.arange(256, dtype=np.float32)
+    fr = np.exp((i * np.float32(-math.log(10000))) * np.float32(1 / 256)).astype(np.float32)
+    args = (f32(t)[:, None] * fr[None]).astype(np.float32) * np.float32(1000)
+    return f16(np.concatenate([np.cos(args.astype(np.float64)),
+                               np.sin(args.astype(np.float64))], -1))
+
+
+def adaln_single(p: dict, pre: str, t):
+    """AdaLayerNormSingleFlow.forward (transformer.py:438-444): (linear(silu(emb)), emb) with
+    emb = linear_2(silu(linear_1(sinusoid(t)))) (:447-458)."""
+    e = timestep_sinusoid(t)
+    e = silu(linear(e, p[pre + "emb.timestep_embedder.linear_1.weight"],
+                    p[pre + "emb.timestep_embedder.linear_1.bias"]))
+    emb = linear(e, p[pre + "emb.timestep_embedder.linear_2.weight"],
+                 p[pre + "emb.timestep_embedder.linear_2.bias"])
+    return linear(silu(emb), p[pre + "linear.weight"], p[pre + "linear.bias"]), emb
+
+
+def final_norm(x, table, emb) -> np.ndarray:
+    """norm_out / norm_out_2 with the scale_shift_table modulation (transformer.py:366-370)."""
+    m = f16(f32(table)[None] + f32(emb)[:, None])
+    return modulate(layer_norm(x), m[:, 0:1], m[:, 1:2])
+
+
+def estimator(p: dict, cfg: dict, hidden, t) -> np.ndarray:
+    """LlamaTransformer.forward (transformer.py:345-396).  hidden [B, T, in_channels] fp16,
+    t [B] fp32 -> [B, T, out_channels] fp16.  cfg: heads, head_dim, layers, layers_2."""
+    H, HD = cfg["heads"], cfg["head_dim"]
+    hidden = np.asarray(hidden, np.float16)
+    s = project_layer(p, "proj_in.", hidden)
+    tmod, emb = adaln_single(p, "adaln_single.", t)
+    for i in range(cfg["layers"]):
+        s = block(p, f"transformer_blocks.{i}.", s, tmod, H, HD)
+    s = final_norm(s, p["scale_shift_table"], emb)
+    x = project_layer(p, "connection_proj.", np.concatenate([hidden, s], -1))
+    tmod2, emb2 = adaln_single(p, "adaln_single_2.", t)
+    for i in range(cfg["layers_2"]):
+        x = block(p, f"transformer_blocks_2.{i}.", x, tmod2, H, 2 * HD)
+    x = final_norm(x, p["scale_shift_table_2"], emb2)
+    return project_layer(p, "proj_out.", x)
+
+
+# ---------------------------------------------------------------- Euler solver
+def solve_euler(est, x, incontext_x, incontext_length: int, t_span, mu, guidance_scale: float):
+    """FlowMatching.solve_euler (flow_matching.py:161-210).  ``est(hidden, t)`` is the
+    estimator; x, incontext_x [B, T, C] fp16, mu [B, T, Cmu] fp16, t_span fp32.  Scalars t and
+    dt are fp32 device tensors in the reference; their products with fp16 tensors round to fp16."""
+    x = np.array(x, np.float16)
+    ic = np.asarray(incontext_x, np.float16)
+    mu = np.asarray(mu, np.float16)
+    t_span = f32(t_span)
+    L = int(incontext_length)
+    t = t_span[0]
+    dt = np.float32(t_span[1] - t_span[0])
+    noise = x.copy()
+    n = len(t_span)
+    for step in range(1, n):
+        a = np.float32(np.float32(1) - np.float32(np.float32(1 - 1e-6) * t))
+        x[:, :L] = f16(f32(f16(a * f32(noise[:, :L]))) + f32(f16(t * f32(ic[:, :L]))))
+        if guidance_scale > 1.0:
+            inp = np.concatenate([np.concatenate([x, x], 0), np.concatenate([ic, ic], 0),
+                                  np.concatenate([np.zeros_like(mu), mu], 0)], 2)
+            d = est(inp, np.full(2 * x.shape[0], t, np.float32))
+            u, c = np.split(d, 2, 0)
+            d = f16(f32(u) + f32(f16(np.float32(guidance_scale) * f32(f16(f32(c) - f32(u))))))
+        else:
+            d = est(np.concatenate([x, ic, mu], 2), np.full(x.shape[0], t, np.float32))
+        x = f16(f32(x) + f32(f16(dt * f32(d))))
+        t = np.float32(t + dt)
+        if step < n - 1:
+            dt = np.float32(t_span[step + 1] - t)
+    return x
+
+
+def t_span(num_steps: int) -> np.ndarray:
+    """torch.linspace(0, 1, num_steps + 1) in fp32 (flow_matching.py:140-142): the first half
+    from the start, the second half from the end, as torch's linspace evaluates it."""
+    n = num_steps + 1
+    step = np.float32(1.0) / np.float32(n - 1)
+    half = n // 2
+    i = np.arange(n, dtype=np.float32)
+    lo = (step * i).astype(np.float32)
+    hi = (np.float32(1.0) - (step * (np.float32(n - 1) - i)).astype(np.float32)).astype(np.float32)
+    return np.where(np.arange(n) < half, lo, hi).astype(np.float32)
+
+
+# ---------------------------------------------------------------- synthetic weights
+def random_weights(cfg: dict, seed: int = 0) -> dict:
+    """Random fp16 estimator weights under the reference's names.  cfg: heads, head_dim,
+    in_channels, out_channels, layers, layers_2.  Scales keep activations O(1)."""
+    g = np.random.default_rng(seed)
+    H, HD = cfg["heads"], cfg["head_dim"]
+    D, D2, Cin, Cout = H * HD, 2 * H * HD, cfg["in_channels"], cfg["out_channels"]
+    p = {}
+
+    def lin(name, n, k, bias=True, gain=1.0):
+        p[name + ".weight"] = f16(g.standard_normal((n, k)) * (gain / math.sqrt(k)))
+        if bias:
+            p[name + ".bias"] = f16(g.standard_normal(n) * 0.02)
+
+    def conv(name, cout, cin):
+        p[name + ".ffn_1.weight"] = f16(g.standard_normal((cout, cin, 3)) / math.sqrt(cin))
+        p[name + ".ffn_1.bias"] = f16(g.standard_normal(cout) * 0.02)
+        lin(name + ".ffn_2", cout, cout)
+
+    def blk(pre, dim):
+        p[pre + "attn_norm.weight"] = f16(1 + 0.1 * g.standard_normal(dim))
+        p[pre + "mlp_norm.weight"] = f16(1 + 0.1 * g.standard_normal(dim))
+        for nm in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lin(pre + "attn." + nm, dim, dim, bias=False)
+        F = mlp_hidden(dim)
+        lin(pre + "mlp.gate", F, dim, bias=False)
+        lin(pre + "mlp.up", F, dim, bias=False)
+        lin(pre + "mlp.down", dim, F, bias=False)
+        p[pre + "scale_shift_table"] = f16(g.standard_normal((6, dim)) / math.sqrt(dim))
+
+    def ada(pre, dim):
+        lin(pre + "emb.timestep_embedder.linear_1", dim, 512)
+        lin(pre + "emb.timestep_embedder.linear_2", dim, dim)
+        lin(pre + "linear", 6 * dim, dim, gain=0.5)
+
+    conv("proj_in", D, Cin)
+    for i in range(cfg["layers"]):
+        blk(f"transformer_blocks.{i}.", D)
+    for i in range(cfg["layers_2"]):
+        blk(f"transformer_blocks_2.{i}.", D2)
+    conv("connection_proj", D2, Cin + D)
+    p["scale_shift_table"] = f16(g.standard_normal((2, D)) / math.sqrt(D))
+    p["scale_shift_table_2"] = f16(g.standard_normal((2, D2)) / math.sqrt(D2))
+    conv("proj_out", Cout, D2)
+    ada("adaln_single.", D)
+    ada("adaln_single_2.", D2)
+    return p

@@ -64,6 +64,21 @@ def test_signatures_match_header_arity():
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 24, 8, 64, 96, 0.1, None),    # HD 96
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 40, 8, 64, 128, 0.1, None),   # G = 5
     lambda L: L.ecd_prefill_attn(18, 16, 16, 16, 16, 1, 8, 24, 8, 64, 128, 0.1, None),   # q align
+    lambda L: L.ecd_codec_rope_table(16, 8, 63, None),                             # odd HD
+    lambda L: L.ecd_codec_rope_heads(16, 192, 16, 16, 16, 16, 1, 8, 1, 60, None),   # HD % 8
+    lambda L: L.ecd_codec_rope_heads(16, 100, 16, 16, 16, 16, 1, 8, 1, 64, None),   # ldq < 3D
+    lambda L: L.ecd_codec_norm_mod(16, None, None, None, 0, 16, 16, 16, 16, 16, 0, 16, 8, 8,
+                                   8200, 0, 1e-6, None),                            # D > 4096
+    lambda L: L.ecd_codec_norm_mod(16, 16, None, None, 0, 16, 16, 16, 16, 16, 0, 16, 8, 8, 64,
+                                   0, 1e-6, None),                                  # h, no gate
+    lambda L: L.ecd_codec_norm_mod(16, None, None, None, 0, None, 16, 16, 16, 16, 0, 16, 8, 8,
+                                   64, 0, 1e-6, None),                              # RMS, no w
+    lambda L: L.ecd_codec_cols3(None, None, None, None, None, 1, 16, 1, 8, None),
+    lambda L: L.ecd_codec_timestep(None, 16, 1, None),
+    lambda L: L.ecd_codec_silu(16, 16, 0, None),
+    lambda L: L.ecd_codec_euler(16, 16, 16, 16, 2, 1, 8, 256, 0, 0.1, 1.2, 0.0, 0, None),  # cfg 2
+    lambda L: L.ecd_codec_euler(16, None, 16, 16, 1, 1, 8, 256, 4, 0.1, 1.2, 0.0, 0, None),  # blend, no noise
+    lambda L: L.ecd_codec_euler(16, 16, 16, 16, 1, 1, 8, 252, 0, 0.1, 1.2, 0.0, 0, None),  # C % 8
 ])
 def test_host_argument_validation(call):
     """Invalid arguments return ECD_EINVAL before any HIP call (no GPU needed)."""

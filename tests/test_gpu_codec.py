@@ -1,15 +1,22 @@
-"""Kernels of the codec's flow-matching estimator (app/heartcodec/models/transformer.py) against
-fp32 numpy products with the same fp16 rounding points as torch's fp16 layers."""
+"""Kernels of the codec's flow-matching estimator (app/heartcodec/models/transformer.py) and its
+Euler solver (app/heartcodec/models/flow_matching.py) against the oracle (oracle/codec.py) and
+fp32 numpy products with the same fp16 rounding points as torch's fp16 layers.
+
+Bars: copies, RoPE rotation and the Euler update bit-exact; single kernels within
+|got - want| <= 2e-3 + 1e-2 |want|; the whole estimator and solver (many fp16 layers, fp32
+accumulation in a different order than the oracle's float64) within 2e-2 of the output's
+largest magnitude, with correlation above 0.9999."""
 import numpy as np
 import pytest
 
 from helpers import assert_close16, randn16, rng
+from oracle import codec as OC
 from oracle.numerics import f16
 
 pytestmark = pytest.mark.gpu
 
 
-def T(a, dev):
+def D_(a, dev):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
@@ -18,6 +25,24 @@ def N_(t):
     return t.detach().cpu().numpy()
 
 
+def _exact(got, want, what):
+    """Bit-exact comparison that names the first differing elements."""
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    if len(bad):
+        show = [(tuple(i), float(got[tuple(i)]), float(want[tuple(i)])) for i in bad[:6]]
+        raise AssertionError(f"{what}: {len(bad)} of {got.size} differ; first {show}")
+
+
+def _call(name, *args):
+    import torch
+    from estudiocanciones_amd import _ffi
+    from estudiocanciones_amd.kernels import stream_ptr
+    _ffi.call(name, *args, stream_ptr(torch.device("cuda")))
+
+
+# ---------------------------------------------------------------- fp16 GEMM
 @pytest.mark.parametrize("M,N,K,bias,alpha,res", [
     (17, 100, 64, True, 1.0, False),          # ragged M and N, one K chunk
     (1488, 1536, 3072, True, 3 ** -0.5, False),  # ProjectLayer conv (k = 3) as a GEMM, scaled
@@ -41,16 +66,16 @@ def test_gemm_f16_linear(dev, M, N, K, bias, alpha, res):
         want = f16(want.astype(np.float32) * np.float32(alpha))
     if res:
         want = f16(want.astype(np.float32) + r.astype(np.float32))
-    got = gemm_f16_packed(T(x, dev), pack_f16(T(w, dev)), N, K, T(b, dev) if bias else None,
-                          alpha, T(r, dev) if res else None)
+    got = gemm_f16_packed(D_(x, dev), pack_f16(D_(w, dev)), N, K, D_(b, dev) if bias else None,
+                          alpha, D_(r, dev) if res else None)
     assert_close16(N_(got), want, what=f"gemm f16 M={M} N={N} K={K}")
 
 
 @pytest.mark.parametrize("M,F,K", [(40, 256, 128), (1488, 4096, 1536)])
 def test_gemm_f16_silu(dev, M, F, K):
-    """LlamaMLP's F.silu(gate(x)) * up(x) in fp16 (transformer.py:181-184)."""
-    from estudiocanciones_amd.kernels import gemm_f16_silu_packed, pack_f16
+    """LlamaMLP's F.silu(gate(x)) * up(x) in fp16 (transformer.py:178-181)."""
     import torch
+    from estudiocanciones_amd.kernels import gemm_f16_silu_packed, pack_f16
     g = rng(410 + F)
     x = randn16(411 + M, M, K)
     gate = (g.standard_normal((F, K), dtype=np.float32) * 0.02).astype(np.float16)
@@ -58,6 +83,188 @@ def test_gemm_f16_silu(dev, M, F, K):
     a = f16(x.astype(np.float32) @ gate.astype(np.float32).T).astype(np.float32)
     u = f16(x.astype(np.float32) @ up.astype(np.float32).T).astype(np.float32)
     want = f16(f16(a / (1.0 + np.exp(-a))).astype(np.float32) * u)
-    wp = pack_f16(torch.cat([T(gate, dev), T(up, dev)], 0).contiguous(), interleave=True)
-    got = gemm_f16_silu_packed(T(x, dev), wp, F, K)
+    wp = pack_f16(torch.cat([D_(gate, dev), D_(up, dev)], 0).contiguous(), interleave=True)
+    got = gemm_f16_silu_packed(D_(x, dev), wp, F, K)
     assert_close16(N_(got), want, what=f"gemm f16 silu M={M} F={F}")
+
+
+# ---------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("L,HD", [(744, 64), (744, 128), (37, 64)])
+def test_codec_rope_table(dev, L, HD):
+    import torch
+    tab = torch.empty(L, HD, dtype=torch.float16, device=dev)
+    _call("ecd_codec_rope_table", tab.data_ptr(), L, HD)
+    sin, cos = OC.rope_table(L, HD)
+    got = N_(tab).reshape(L, HD // 2, 2)
+    # the angles are fp16 values on both sides; only last-bit differences of fp32 sin/cos can
+    # flip a rounding
+    np.testing.assert_allclose(got[..., 0], cos, atol=1e-3, rtol=0)
+    np.testing.assert_allclose(got[..., 1], sin, atol=1e-3, rtol=0)
+
+
+@pytest.mark.parametrize("B,L,H,HD", [(2, 37, 3, 64), (2, 50, 2, 128)])
+def test_codec_rope_heads_bit_exact(dev, B, L, H, HD):
+    import torch
+    D = H * HD
+    qkv = randn16(500 + HD, B * L, 3 * D)
+    sin, cos = OC.rope_table(L, HD)
+    tab = np.stack([cos, sin], -1).astype(np.float16)
+    q = torch.empty(B * L, D, dtype=torch.float16, device=dev)
+    k = torch.empty(B, H, L, HD, dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    qt, tt = D_(qkv, dev), D_(tab, dev)
+    _call("ecd_codec_rope_heads", qt.data_ptr(), 3 * D, tt.data_ptr(), q.data_ptr(),
+          k.data_ptr(), v.data_ptr(), B, L, H, HD)
+    heads = lambda a: a.reshape(B, L, H, HD).transpose(0, 2, 1, 3)
+    want_q = OC.apply_rope_vec(heads(qkv[:, :D]), sin, cos)
+    want_k = OC.apply_rope_vec(heads(qkv[:, D:2 * D]), sin, cos)
+    assert np.array_equal(N_(q), want_q.transpose(0, 2, 1, 3).reshape(B * L, D))
+    assert np.array_equal(N_(k), want_k)
+    assert np.array_equal(N_(v), heads(qkv[:, 2 * D:]))
+
+
+# ---------------------------------------------------------------- norms + adaLN
+@pytest.mark.parametrize("norm,resid,per_batch,D", [(0, False, False, 1536), (0, True, True, 3072),
+                                                    (1, True, False, 1536), (1, False, True, 128),
+                                                    (0, True, False, 4096)])
+def test_codec_norm_mod(dev, norm, resid, per_batch, D):
+    import torch
+    B, L = 2, 29
+    g = rng(600 + D + norm)
+    x = randn16(601 + D, B * L, D, std=2.0)
+    h = randn16(602 + D, B * L, D)
+    w = f16(1 + 0.1 * g.standard_normal(D))
+    tab = f16(g.standard_normal((3, D)) * 0.3)          # gate, shift, scale rows
+    tm = f16(g.standard_normal((B if per_batch else 1, 3, D)) * 0.3)
+    ld = 3 * D if per_batch else 0
+    xt, ht, wt, tabt, tmt = (D_(a, dev) for a in (x, h, w, tab, tm))
+    y = torch.empty(B * L, D, dtype=torch.float16, device=dev)
+    a = lambda t, i: t.data_ptr() + 2 * i * D
+    _call("ecd_codec_norm_mod", xt.data_ptr(), ht.data_ptr() if resid else None,
+          a(tabt, 0) if resid else None, a(tmt, 0) if resid else None, ld,
+          wt.data_ptr() if norm == 0 else None, a(tabt, 1), a(tmt, 1), a(tabt, 2), a(tmt, 2), ld,
+          y.data_ptr(), B * L, L, D, norm, 1e-6)
+    bt = lambda v: np.repeat(v, L, 0) if per_batch else v
+    m = f16(tab[None].astype(np.float32) + tm.astype(np.float32))       # [B or 1, 3, D]
+    gate, shift, scale = bt(m[:, 0]), bt(m[:, 1]), bt(m[:, 2])
+    xw = x
+    if resid:
+        xw = f16(x.astype(np.float32) + f16(gate.astype(np.float32) * h.astype(np.float32)))
+        assert np.array_equal(N_(xt), xw), "gated residual must be bit-exact"
+    n = OC.rms_norm(xw, w) if norm == 0 else OC.layer_norm(xw)
+    assert_close16(N_(y), OC.modulate(n, shift, scale), what=f"norm_mod norm={norm} D={D}")
+
+
+# ---------------------------------------------------------------- conv columns
+def test_codec_cols3_bit_exact(dev):
+    """Segments as solve_euler feeds them: x and incontext shared by both halves, mu zeroed in
+    the unconditional half, plus a per-row segment (connection_proj's s)."""
+    import ctypes
+    import torch
+    from estudiocanciones_amd import _ffi
+    from estudiocanciones_amd.kernels import stream_ptr
+    B, L = 1, 23
+    x, ic, mu = randn16(700, B * L, 16), randn16(701, B * L, 16), randn16(702, B * L, 32)
+    s = randn16(703, 2 * B * L, 24)
+    segs = [(x, 16, B, 0), (ic, 16, B, 0), (mu, 32, B, B), (s, 24, 2 * B, 0)]
+    dt = [D_(a[0], dev) for a in segs]
+    C = 88
+    out = torch.full((2 * B * L, 3 * C), 7.0, dtype=torch.float16, device=dev)
+    n = len(segs)
+    _ffi.call("ecd_codec_cols3", (ctypes.c_void_p * n)(*[t.data_ptr() for t in dt]),
+              (ctypes.c_long * n)(*[sg[1] for sg in segs]), (ctypes.c_int * n)(*[sg[1] for sg in segs]),
+              (ctypes.c_int * n)(*[sg[2] for sg in segs]), (ctypes.c_int * n)(*[sg[3] for sg in segs]),
+              n, out.data_ptr(), 2 * B, L, stream_ptr(dev))
+    inp = np.concatenate([np.concatenate([x, x]), np.concatenate([ic, ic]),
+                          np.concatenate([np.zeros_like(mu), mu]), s], 1).reshape(2 * B, L, C)
+    pad = np.zeros((2 * B, L + 2, C), np.float16)
+    pad[:, 1:-1] = inp
+    want = np.concatenate([pad[:, j:j + L] for j in range(3)], -1).reshape(2 * B * L, 3 * C)
+    assert np.array_equal(N_(out), want)
+
+
+# ---------------------------------------------------------------- timestep path pieces
+def test_codec_timestep_and_silu(dev):
+    import torch
+    t = OC.t_span(10)
+    out = torch.empty(11, 512, dtype=torch.float16, device=dev)
+    tt = D_(t, dev)
+    _call("ecd_codec_timestep", tt.data_ptr(), out.data_ptr(), 11)
+    assert_close16(N_(out), OC.timestep_sinusoid(t), what="timestep sinusoid")
+    x = randn16(710, 7, 300, std=4.0)
+    y = torch.empty(7, 300, dtype=torch.float16, device=dev)
+    xt = D_(x, dev)
+    _call("ecd_codec_silu", xt.data_ptr(), y.data_ptr(), x.size)
+    assert_close16(N_(y), OC.silu(x), what="silu")
+
+
+# ---------------------------------------------------------------- Euler update
+@pytest.mark.parametrize("cfg,mode,L", [(1, 0, 10), (0, 0, 0), (1, 1, 7), (1, 0, 0)])
+def test_codec_euler_bit_exact(dev, cfg, mode, L):
+    B, Ln, C = 1, 30, 256
+    x, nz, ic = randn16(720, B, Ln, C), randn16(721, B, Ln, C), randn16(722, B, Ln, C)
+    d = randn16(723, (2 if cfg else 1) * B, Ln, C)
+    dt, g, tb = np.float32(0.1), 1.25, np.float32(0.3)
+    xt, nzt, ict, dt_ = D_(x, dev), D_(nz, dev), D_(ic, dev), D_(d, dev)   # keep all alive
+    _call("ecd_codec_euler", xt.data_ptr(), nzt.data_ptr(), ict.data_ptr(), dt_.data_ptr(), cfg,
+          B, Ln, C, L, float(dt), g, float(tb), mode)
+    f32 = lambda a: np.asarray(a, np.float32)
+    if cfg:
+        u, c = d[:B], d[B:]
+        v = f16(f32(u) + f32(f16(np.float32(g) * f32(f16(f32(c) - f32(u))))))
+    else:
+        v = d
+    want = f16(f32(x) + f32(f16(dt * f32(v))))
+    if L:
+        if mode == 1:
+            want[:, :L] = ic[:, :L]
+        else:
+            a = np.float32(np.float32(1) - np.float32(np.float32(1 - 1e-6) * tb))
+            want[:, :L] = f16(f32(f16(a * f32(nz[:, :L]))) + f32(f16(tb * f32(ic[:, :L]))))
+    _exact(N_(xt), want, f"euler cfg={cfg} mode={mode} L={L}")
+
+
+# ---------------------------------------------------------------- estimator and solver
+TINY = dict(heads=2, head_dim=64, in_channels=192, out_channels=64, layers=2, layers_2=1)
+
+
+def _estimator(dev, p, cfg):
+    import torch
+    from estudiocanciones_amd.codec import LlamaTransformer
+    sd = {k: torch.from_numpy(v) for k, v in p.items()}
+    return LlamaTransformer(sd, num_attention_heads=cfg["heads"],
+                            attention_head_dim=cfg["head_dim"], in_channels=cfg["in_channels"],
+                            out_channels=cfg["out_channels"], num_layers=cfg["layers"],
+                            num_layers_2=cfg["layers_2"], device=dev)
+
+
+def _close_model(got, want, what):
+    got, want = got.astype(np.float64), want.astype(np.float64)
+    assert np.all(np.isfinite(got)), what
+    err = np.abs(got - want).max() / np.abs(want).max()
+    corr = np.corrcoef(got.ravel(), want.ravel())[0, 1]
+    assert err < 2e-2 and corr > 0.9999, f"{what}: rel max err {err:.3g}, corr {corr:.6f}"
+
+
+@pytest.mark.parametrize("B,L,t", [(2, 40, (0.3, 0.3)), (1, 70, (0.0,)), (3, 17, (0.1, 0.5, 0.9))])
+def test_codec_estimator_forward(dev, B, L, t):
+    p = OC.random_weights(TINY, seed=21)
+    est = _estimator(dev, p, TINY)
+    hidden = randn16(730 + L, B, L, TINY["in_channels"])
+    tt = np.array(t, np.float32)
+    got = est(D_(hidden, dev), D_(tt, dev))
+    _close_model(N_(got), OC.estimator(p, TINY, hidden, tt), f"estimator B={B} T={L}")
+
+
+@pytest.mark.parametrize("g,L_ic", [(1.25, 0), (1.25, 9), (1.0, 5)])
+def test_codec_solve_euler(dev, g, L_ic):
+    from estudiocanciones_amd.codec import solve_euler
+    p = OC.random_weights(TINY, seed=22)
+    est = _estimator(dev, p, TINY)
+    Ln, C, Cmu = 36, 64, 64
+    x0, ic, mu = randn16(740, 1, Ln, C), randn16(741, 1, Ln, C), randn16(742, 1, Ln, Cmu)
+    ic[:, L_ic:] = 0
+    ts = OC.t_span(4)
+    got = solve_euler(est, D_(x0, dev), D_(ic, dev), L_ic, ts, D_(mu, dev), g)
+    want = OC.solve_euler(lambda h, t: OC.estimator(p, TINY, h, t), x0, ic, L_ic, ts, mu, g)
+    _close_model(N_(got), want, f"solve_euler g={g} L={L_ic}")
