@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--target-kv", type=int, default=4096,
                     help="second attended KV length, timed and reported as target_point (0 skips)")
     ap.add_argument("--target-steps", type=int, default=100)
+    ap.add_argument("--codec-steps", type=int, default=10,
+                    help="Euler steps of the codec detokenize window leg (0 skips it)")
     ap.add_argument("--prompt", type=int, default=256,
                     help="prompt tokens of the timed prompt pass (0 skips it)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -321,6 +323,7 @@ def main():
                   "frac_of_mfma_f16_peak": round(flops / p_ms / 1e9 / 2500.0, 4),
                   "path": ("MFMA GEMM (dense numerics, 2-stage LDS DMA) + MFMA causal flash "
                           "attention, 28 layers")}
+    codec = measure_codec(torch, dev, args.codec_steps, args.seed) if args.codec_steps > 0 else None
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -381,11 +384,65 @@ def main():
         },
         "target_point": target,
         "prompt_pass": prompt,
+        "codec_window": codec,
         "setup_s": round(t_build, 1),
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(bb, dec, B, args.kv, args.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+
+def measure_codec(torch, dev, steps, seed):
+    """One detokenize window of the codec's flow-matching estimator: 24 + 6 layers (dim 1536 /
+    3072, 24 heads), batch 1 doubled by CFG, 744 latent frames (29.76 s), ``steps`` Euler steps
+    with guidance 1.25, random-init fp16 weights, inputs resident on the GPU."""
+    import numpy as np
+    from estudiocanciones_amd import codec as C
+    sd = C.random_state_dict(device=dev, seed=seed + 7)
+    est = C.LlamaTransformer(sd, device=dev)
+    del sd
+    B, T = 1, 744
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 8)
+    x = torch.randn(B, T, 256, generator=g, device=dev).half()
+    ic = torch.zeros(B, T, 256, device=dev, dtype=torch.float16)
+    mu = torch.randn(B, T, 512, generator=g, device=dev).half()
+    ts = np.linspace(0, 1, steps + 1).astype(np.float32)
+    C.solve_euler(est, x, ic, 0, ts, mu, 1.25)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    out = C.solve_euler(est, x, ic, 0, ts, mu, 1.25)
+    e1.record()
+    torch.cuda.synchronize()
+    win_ms = e0.elapsed_time(e1)
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError("codec window produced non-finite latents")
+    tm = est.timestep_vectors(torch.tensor([0.5], device=dev))
+    segs = [(x.view(T, 256), 256, B, 0), (ic.view(T, 256), 256, B, 0), (mu.view(T, 512), 512, B, B)]
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        est._run(segs, 2 * B, T, (tm[0][0], tm[1][0], tm[2][0], tm[3][0], False))
+    e1.record()
+    torch.cuda.synchronize()
+    call_ms = e0.elapsed_time(e1) / reps
+    fl = C.estimator_flops(est, 2 * B, T)
+    del est
+    torch.cuda.empty_cache()
+    return {
+        "workload": ("codec flow-matching estimator (24 + 6 LlamaTransformer layers, dim 1536 / "
+                     "3072, 24 heads, hd 64 / 128), batch 1 x CFG 2, 744 latent frames (one "
+                     f"29.76 s window), {steps} Euler steps, guidance 1.25, fp16"),
+        "window_ms": round(win_ms, 2),
+        "latent_frames_per_s": round(T * B / (win_ms / 1e3), 1),
+        "estimator_call_ms": round(call_ms, 3),
+        "estimator_flops": int(fl["total"]),
+        "estimator_TFLOPs": round(fl["total"] / call_ms / 1e9, 1),
+        "frac_of_mfma_f16_peak": round(fl["total"] / call_ms / 1e9 / 2500.0, 4),
+        "path": ("fp16 MFMA GEMM (packed weights, fused bias / scale / SiLU-mul epilogues), MFMA "
+                 "flash attention, fused gated-residual + adaLN norms, CFG Euler kernel"),
+    }
 
 
 def cpu_baseline(bb, dec, B, kv, budget_s):

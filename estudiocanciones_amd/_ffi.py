@@ -51,6 +51,8 @@ SIGNATURES = {
     "ecd_pack_f16": [_P, c_int, c_int, c_int, _P, _P],
     "ecd_gemm_f16p": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_f16p_silu": [_P, c_long, _P, _P, c_long, c_int, c_int, c_int, _P],
+    "ecd_gemm_f16p_tuned": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
+                            c_int, c_int, c_int, _P],
     "ecd_packed_bytes": [c_int, c_int],
     "ecd_packed_bytes_f16": [c_int, c_int],
     "ecd_pack_i8": [_P, c_int, c_int, c_int, _P, _P],

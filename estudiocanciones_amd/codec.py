@@ -30,7 +30,7 @@ from . import _ffi
 from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_attn,
                       stream_ptr)
 
-__all__ = ["LlamaTransformer", "solve_euler", "mlp_hidden", "euler_times"]
+__all__ = ["LlamaTransformer", "solve_euler", "mlp_hidden", "euler_times", "random_state_dict", "estimator_flops"]
 
 EPS = 1e-6
 SQRT1_3 = 3 ** -0.5
@@ -345,3 +345,72 @@ def solve_euler(est: LlamaTransformer, x: torch.Tensor, incontext_x: torch.Tenso
                   int(cfg), B, T, C, 0 if (last and not copy_incontext) else L, float(dts[k]),
                   float(guidance_scale), tb, mode, st)
     return x
+
+
+def random_state_dict(num_attention_heads=24, attention_head_dim=64, in_channels=1024,
+                      out_channels=256, num_layers=24, num_layers_2=6, device="cuda", seed=0):
+    """Random fp16 estimator weights under the reference's names, drawn on the device (there are
+    no checkpoints here).  Scales keep activations O(1) through the stack."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    D = num_attention_heads * attention_head_dim
+    D2 = 2 * D
+    sd = {}
+
+    def rnd(*shape, scale):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).half()
+
+    def lin(name, n, k, bias=True, gain=1.0):
+        sd[name + ".weight"] = rnd(n, k, scale=gain / k ** 0.5)
+        if bias:
+            sd[name + ".bias"] = rnd(n, scale=0.02)
+
+    def proj(name, cout, cin):
+        sd[name + ".ffn_1.weight"] = rnd(cout, cin, 3, scale=cin ** -0.5)
+        sd[name + ".ffn_1.bias"] = rnd(cout, scale=0.02)
+        lin(name + ".ffn_2", cout, cout)
+
+    def blk(pre, dim):
+        sd[pre + "attn_norm.weight"] = (1 + rnd(dim, scale=0.1).float()).half()
+        sd[pre + "mlp_norm.weight"] = (1 + rnd(dim, scale=0.1).float()).half()
+        for nm in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lin(pre + "attn." + nm, dim, dim, bias=False)
+        F = mlp_hidden(dim)
+        lin(pre + "mlp.gate", F, dim, bias=False)
+        lin(pre + "mlp.up", F, dim, bias=False)
+        lin(pre + "mlp.down", dim, F, bias=False)
+        sd[pre + "scale_shift_table"] = rnd(6, dim, scale=dim ** -0.5)
+
+    def ada(pre, dim):
+        lin(pre + "emb.timestep_embedder.linear_1", dim, 512)
+        lin(pre + "emb.timestep_embedder.linear_2", dim, dim)
+        lin(pre + "linear", 6 * dim, dim, gain=0.5)
+
+    proj("proj_in", D, in_channels)
+    for i in range(num_layers):
+        blk(f"transformer_blocks.{i}.", D)
+    for i in range(num_layers_2):
+        blk(f"transformer_blocks_2.{i}.", D2)
+    proj("connection_proj", D2, in_channels + D)
+    sd["scale_shift_table"] = rnd(2, D, scale=D ** -0.5)
+    sd["scale_shift_table_2"] = rnd(2, D2, scale=D2 ** -0.5)
+    proj("proj_out", out_channels, D2)
+    ada("adaln_single.", D)
+    ada("adaln_single_2.", D2)
+    return sd
+
+
+def estimator_flops(est: LlamaTransformer, B: int, T: int) -> dict:
+    """Algorithmic FLOPs of one estimator call on B x T rows: the dense layers (2 M N K each,
+    the k = 3 convolutions as GEMMs with K = 3 Cin) and the attention products (4 B H T^2 HD per
+    block: Q K^T and P V)."""
+    M = B * T
+    gemm = 0
+    for p in (est.proj_in, est.connection_proj, est.proj_out):
+        gemm += 2 * M * p.cout * 3 * p.cin + 2 * M * p.cout * p.cout
+    attn = 0
+    for bp in est.blocks + est.blocks_2:
+        D, F = bp.D, bp.F
+        gemm += 2 * M * (3 * D * D + D * D + 2 * F * D + D * F)
+        attn += 4 * B * bp.H * T * T * bp.HD
+    return {"gemm": gemm, "attn": attn, "total": gemm + attn}

@@ -103,6 +103,27 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)r, 63));
 }
 
+// wait until at most N vector-memory operations of this wave are outstanding (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt at their maxima, i.e. not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_vm0() { wait_vm<0>(); }
+
+// LDS DMA, one wave instruction: 16 bytes per lane from base + off (base wave-uniform, off a
+// per-lane byte offset below 2^31) into LDS at dst + 16 * lane (dst uniform).  Issued from
+// inline asm with M0 (the instruction's LDS base) saved and restored around it: with the
+// compiler's builtin every later LDS read would wait for all outstanding DMA (vmcnt 0).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, void* dst) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
 __device__ __host__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);

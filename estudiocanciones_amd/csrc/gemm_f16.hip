@@ -1,0 +1,377 @@
+// fp16-weight GEMM on gfx950 MFMA for the dense layers of the codec's flow-matching estimator
+// (the nn.Linear layers and the k = 3 Conv1d-as-GEMM of app/heartcodec/models/transformer.py),
+// with torch's F.linear numerics: fp32 accumulation, fp32 bias, one fp16 rounding.
+//   EPI_STORE: y = fp16(acc + bias); if alpha != 1, y = fp16(y * alpha); then y = fp16(y + res).
+//   EPI_SILU:  weight rows interleaved (gate row j at 2j, up row j at 2j + 1),
+//              mm[m, j] = fp16(fp16(silu(g)) * u) with g, u the fp16 GEMM outputs (LlamaMLP,
+//              transformer.py:178-181).
+//
+// Packed weights: 16-row tiles x 64-wide K chunks of 2 KB, two 1 KB halves h; lane l's 16 bytes
+// of half h hold row l & 15, k = 64c + 16 (l >> 4) + 8h .. +7 (ecd_pack_f16), so one 16-byte
+// LDS read is an MFMA A fragment.  The activations x are the B operand.
+//
+// Tiling (template): 4 waves as WN x WM; wave (wn, wm) owns FT 16-feature tiles and RT 16-row
+// tiles of v_mfma_f32_16x16x32_f16, so a block covers BN = 16 WN FT features x BM = 16 WM RT
+// rows.  K advances in 64-wide chunks that go straight from global memory into an NS-stage LDS
+// ring (LDS DMA, no register staging); x rows are stored with their 16-byte pieces XOR-swizzled
+// by row (piece p of row r at position p ^ (r & 7)) so the fragment reads spread over banks.
+// At the top of step c each wave waits until its own loads of chunk c have landed (vmcnt counts
+// the later chunks still allowed in flight), a barrier publishes the chunk and frees the stage
+// read in step c - 1, and then the loads of chunk c + NS - 1 go into that stage.
+//
+// Why the shapes: every block re-reads its weight tile and x tile from L2 once per chunk, so the
+// block tile sets the FLOPs per L2 byte (128 x 128: 64 FLOP/B; 256 x 128: 85 FLOP/B), while the
+// number of blocks must still fill 256 CUs; the host picks the tile per shape.
+//
+// Block order is XCD-aware: the row blocks that share a weight tile get block ids equal modulo 8,
+// so they run on one XCD and share its L2.
+#include "common.h"
+
+namespace ecd {
+
+enum { F16_STORE = 0, F16_SILU = 1 };
+
+// wait for every vector-memory and LDS operation of this wave (vmcnt 0, lgkmcnt 0)
+__device__ __forceinline__ void wait_vm0_lgkm0() { __builtin_amdgcn_s_waitcnt(7 << 4); }
+
+// A fragments (two k-halves) of the wave's FT weight tiles and B fragments of its RT row tiles
+// for one chunk of LDS stage (lw_st, lx_st).
+template <int FT, int RT>
+__device__ __forceinline__ void f16_frags(const f16* lw_st, const f16* lx_st, int wn, int wm,
+                                          int lane, f16x8 (&wa)[FT], f16x8 (&wb)[FT],
+                                          f16x8 (&fa)[RT], f16x8 (&fb)[RT]) {
+  const int sw = lane & 7, p0 = 2 * (lane >> 4);
+#pragma unroll
+  for (int ft = 0; ft < FT; ++ft) {
+    const f16* tp = lw_st + (wn * FT + ft) * 1024;
+    wa[ft] = *(const f16x8*)(tp + 8 * lane);
+    wb[ft] = *(const f16x8*)(tp + 512 + 8 * lane);
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const f16* xr = lx_st + ((wm * RT + rt) * 16 + (lane & 15)) * 64;
+    fa[rt] = *(const f16x8*)(xr + 8 * (p0 ^ sw));
+    fb[rt] = *(const f16x8*)(xr + 8 * ((p0 + 1) ^ sw));
+  }
+}
+
+// acc[ft][rt] += w[ft] x f[rt] over one k-half; consecutive MFMAs write different accumulators
+template <int FT, int RT>
+__device__ __forceinline__ void f16_mfma_half(f32x4 (&acc)[FT][RT], const f16x8 (&w)[FT],
+                                              const f16x8 (&f)[RT]) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+      acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[ft], f[rt], acc[ft][rt], 0, 0, 0);
+}
+
+// 128 x 128 tiles are built for two waves per SIMD (two blocks per CU); the larger ones for one
+template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL>
+__global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel(
+    const f16* __restrict__ x, long ldx, const f16* __restrict__ wp,
+    const float* __restrict__ bias, float alpha, const f16* __restrict__ res, long ldr,
+    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb) {
+  static_assert(WN * WM == 4, "four waves");
+  constexpr int BN = 16 * WN * FT;      // features per block
+  constexpr int BM = 16 * WM * RT;      // rows per block
+  constexpr int WI = BN / 16 * 2 / 4;   // weight DMA instructions per wave per chunk (1 KB each)
+  constexpr int XI = BM / 8 / 4;        // x DMA instructions per wave per chunk (8 rows each)
+  constexpr int PER_CHUNK = WI + XI;
+  static_assert(PER_CHUNK * (NS - 2) < 64, "vmcnt range");
+  __shared__ __align__(16) f16 lw[NS][BN / 16 * 1024];  // BN / 16 tiles x 2 KB
+  __shared__ __align__(16) f16 lx[NS][BM * 64];         // BM rows x 128 B
+
+  const int b = blockIdx.x;
+  const int grp8 = b / (8 * nmb);
+  const int rem = b - grp8 * 8 * nmb;
+  const int mb = rem >> 3;
+  const int fb = grp8 * 8 + (rem & 7);
+  if (fb >= nfb) return;  // padding blocks of the last group of 8 (uniform per block)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wv % WN, wm = wv / WN;
+  const int n0 = fb * BN;
+  const int m0 = mb * BM;
+  const int nch = K >> 6;
+  const int ntiles = (N + 15) >> 4;
+  const long tile_bytes = (long)nch * 2048;
+
+  // DMA sources: weight instruction j of this wave is tile t = i >> 1, half h = i & 1 with
+  // i = wv + 4 j (tiles past N re-read the last tile; their results are never stored); x
+  // instruction j covers rows 8 i .. 8 i + 7, i = wv + 4 j (rows past M re-read row M - 1).
+  const char* wsrc[WI];
+  int wdst[WI];
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int i = wv + 4 * j;
+    const int t = i >> 1, h = i & 1;
+    wsrc[j] = (const char*)wp + (long)min(n0 / 16 + t, ntiles - 1) * tile_bytes + 1024 * h;
+    wdst[j] = t * 1024 + 512 * h;  // in halfs
+  }
+  const uint32_t woff = 16u * lane;
+  const int xpiece = (lane & 7) ^ (lane >> 3);
+  uint32_t xoff[XI];
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int i = wv + 4 * j;
+    xoff[j] = (uint32_t)((long)min(m0 + 8 * i + (lane >> 3), M - 1) * ldx * 2 + 16 * xpiece);
+  }
+  auto issue = [&](int c, int st) {
+#pragma unroll
+    for (int j = 0; j < WI; ++j) lds_dma16(wsrc[j] + (long)c * 2048, woff, &lw[st][wdst[j]]);
+#pragma unroll
+    for (int j = 0; j < XI; ++j)
+      lds_dma16(x + (long)c * 64, xoff[j], &lx[st][8 * (wv + 4 * j) * 64]);
+  };
+
+  f32x4 acc[FT][RT];
+#pragma unroll
+  for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  if constexpr (PL) {
+    // Software-pipelined (2 stages): the fragments of chunk c + 1 are read from LDS while the
+    // second k-half MFMAs of chunk c run, and the wait + barrier for chunk c + 1 sit behind the
+    // first k-half MFMAs, so no MFMA waits for an LDS read at a chunk boundary.
+    static_assert(NS == 2, "pipelined loop uses two stages");
+    f16x8 wa0[FT], wb0[FT], fa0[RT], fb0[RT], wa1[FT], wb1[FT], fa1[RT], fb1[RT];
+    issue(0, 0);
+    if (nch > 1) {
+      issue(1, 1);
+      wait_vm<PER_CHUNK>();
+    } else {
+      wait_vm0();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    f16_frags<FT, RT>(lw[0], lx[0], wn, wm, lane, wa0, wb0, fa0, fb0);
+    // one chunk: MFMAs on (wa, wb, fa, fb) = chunk c, next fragments into (na, nb, nfa, nfb)
+#define F16_PL_STEP(c, wa, wb, fa, fb, na, nb, nfa, nfb)                                   \
+    do {                                                                                  \
+      f16_mfma_half<FT, RT>(acc, wa, fa);                                                 \
+      if ((c) + 1 < nch) {                                                                \
+        wait_vm0_lgkm0(); /* own DMA of c + 1 landed, own reads of c done */              \
+        asm volatile("" ::: "memory");                                                    \
+        __builtin_amdgcn_s_barrier();                                                     \
+        asm volatile("" ::: "memory");                                                    \
+        if ((c) + 2 < nch) issue((c) + 2, (c) & 1);                                       \
+        f16_frags<FT, RT>(lw[((c) + 1) & 1], lx[((c) + 1) & 1], wn, wm, lane, na, nb, nfa, \
+                          nfb);                                                           \
+      }                                                                                   \
+      f16_mfma_half<FT, RT>(acc, wb, fb);                                                 \
+    } while (0)
+    for (int c = 0; c < nch; c += 2) {
+      F16_PL_STEP(c, wa0, wb0, fa0, fb0, wa1, wb1, fa1, fb1);
+      if (c + 1 < nch) F16_PL_STEP(c + 1, wa1, wb1, fa1, fb1, wa0, wb0, fa0, fb0);
+    }
+#undef F16_PL_STEP
+  } else {
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nch) issue(s, s);
+  for (int c = 0; c < nch; ++c) {
+    // chunk c landed for this wave: later chunks c + 1 .. c + NS - 2 may still be in flight
+    if (NS == 3 && c + 1 < nch)
+      wait_vm<(NS == 3 ? PER_CHUNK : 0)>();
+    else
+      wait_vm0();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // chunk c visible to every wave; stage of c - 1 free
+    asm volatile("" ::: "memory");
+    if (c + NS - 1 < nch) issue(c + NS - 1, (c + NS - 1) % NS);
+    const int st = c % NS;
+    f16x8 wa[FT], wb[FT], fa[RT], fb[RT];
+    f16_frags<FT, RT>(lw[st], lx[st], wn, wm, lane, wa, wb, fa, fb);
+    f16_mfma_half<FT, RT>(acc, wa, fa);
+    f16_mfma_half<FT, RT>(acc, wb, fb);
+  }
+  }
+
+  // epilogue: lane holds features nb .. nb + 3 of row m for every (ft, rt).  Where the rows of
+  // y (and res) are 8-byte aligned the four values go out as one 8-byte store.
+  const bool vec = ((ldy & 3) == 0) && (((uintptr_t)y & 7) == 0) &&
+                   (!res || (((ldr & 3) == 0) && (((uintptr_t)res & 7) == 0)));
+#pragma unroll
+  for (int ft = 0; ft < FT; ++ft) {
+    const int nb = n0 + (wn * FT + ft) * 16 + 4 * (lane >> 4);
+    if (nb >= N) continue;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[r] = bias[min(nb + r, N - 1)];
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int m = m0 + (wm * RT + rt) * 16 + (lane & 15);
+      if (m >= M) continue;
+      f16x4 yv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        yv[r] = (f16)(acc[ft][rt][r] + bv[r]);
+        if (alpha != 1.0f) yv[r] = (f16)((float)yv[r] * alpha);
+      }
+      if (EPI == F16_STORE) {
+        if (vec && nb + 3 < N) {
+          if (res) yv = yv + *(const f16x4*)(res + (long)m * ldr + nb);
+          *(f16x4*)(y + (long)m * ldy + nb) = yv;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (nb + r < N) {
+              f16 o = yv[r];
+              if (res) o = o + res[(long)m * ldr + nb + r];
+              y[(long)m * ldy + nb + r] = o;
+            }
+          }
+        }
+      } else {  // (a_j, b_j, a_j+1, b_j+1) with j = nb / 2; N even
+        const int j = nb >> 1;
+        const float a0 = (float)yv[0], a1 = (float)yv[2];
+        f16x2 o;
+        o.x = (f16)(a0 / (1.0f + expf(-a0))) * yv[1];
+        o.y = (f16)(a1 / (1.0f + expf(-a1))) * yv[3];
+        *(f16x2*)(y + (long)m * ldy + j) = o;
+      }
+    }
+  }
+}
+
+// Pack fp16 w [N, K] into lane-ordered 16 x 64 tiles of 2 KB (two 1 KB halves); with
+// `interleave` (N even) packed row 2j is source row j and 2j + 1 is source row N/2 + j.
+__global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w, int N, int K,
+                                                       int interleave, f16* __restrict__ out) {
+  const int nch = K >> 6;
+  const long ntiles = (N + 15) >> 4;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= ntiles * nch * 128) return;
+  const int l = (int)(idx & 63);
+  const int h = (int)((idx >> 6) & 1);
+  const long tc = idx >> 7;
+  const int c = (int)(tc % nch);
+  const long tile = tc / nch;
+  const long r = tile * 16 + (l & 15);
+  u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+  if (r < N) {
+    const long src = interleave ? ((r & 1) ? (N >> 1) + (r >> 1) : (r >> 1)) : r;
+    v = *(const u32x4*)(w + src * K + 64L * c + 16 * (l >> 4) + 8 * h);
+  }
+  *(u32x4*)(out + (tile * nch + c) * 1024 + 512 * h + 8 * l) = v;
+}
+
+// Tile configurations: {WN, WM, FT, RT, NS}.
+//   1: 128 x 128, waves 4 x 1 (32 features x 128 rows each), 2 stages, 64 KB LDS
+//   2: 128 x 128, waves 2 x 2 (64 x 64 each), 2 stages, 64 KB
+//   3: 256 x 128, waves 4 x 1 (64 x 128 each), 2 stages, 96 KB
+//   4: 256 x 128, waves 4 x 1, 3 stages, 144 KB
+//   5: 256 x 128, waves 2 x 2 (128 x 64 each), 2 stages, 96 KB
+//   6: 128 x 256, waves 2 x 2 (64 x 128 each), 2 stages, 96 KB
+//   7: 128 x 128, waves 2 x 2, 3 stages, 96 KB
+//   8: as 2, software-pipelined (next chunk's fragments read during this chunk's MFMAs)
+//   9: as 1, software-pipelined
+//  10: 128 x 64, waves 4 x 1 (32 x 64 each), software-pipelined, 48 KB
+//  11: 128 x 64, waves 2 x 2 (64 x 32 each), software-pipelined, 48 KB
+template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
+static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
+                      const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
+                      hipStream_t st) {
+  constexpr int BN = 16 * WN * FT, BM = 16 * WM * RT;
+  const int nfb = (N + BN - 1) / BN;
+  const int nmb = (M + BM - 1) / BM;
+  const long blocks = (long)((nfb + 7) / 8) * 8 * nmb;
+  if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
+  hipLaunchKernelGGL((gemm_f16w_kernel<EPI, WN, WM, FT, RT, NS, PL>), dim3((unsigned)blocks),
+                     dim3(256), 0, st, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, nfb,
+                     nmb);
+  return ecd_launch_status();
+}
+
+// Library default per shape (N counts output features before the SiLU pairing).
+static int default_cfg(int M, int N, int K, bool silu) {
+  (void)M;
+  if (silu) return K <= 2048 ? 2 : 8;
+  return N <= 1536 ? 10 : 8;   // narrow outputs: 128 x 64 tiles for more blocks
+}
+
+template <int EPI>
+static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const float* bias,
+                      float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N,
+                      int K, hipStream_t st) {
+  if (cfg == 0) cfg = default_cfg(M, N, K, EPI == F16_SILU);
+  switch (cfg) {
+    case 1: return launch_cfg<EPI, 4, 1, 2, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 2: return launch_cfg<EPI, 2, 2, 4, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 3: return launch_cfg<EPI, 4, 1, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 4: return launch_cfg<EPI, 4, 1, 4, 8, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 5: return launch_cfg<EPI, 2, 2, 8, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 6: return launch_cfg<EPI, 2, 2, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 7: return launch_cfg<EPI, 2, 2, 4, 4, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 8: return launch_cfg<EPI, 2, 2, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    default: return ECD_EINVAL;
+  }
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// the per-lane byte offsets of the x loads are 32-bit: the x buffer must stay below 2 GiB
+static bool x_offsets_fit(int M, long ldx) { return (long)M * ldx * 2 < 0x7FFFFFFFL; }
+
+}  // namespace ecd
+
+using namespace ecd;
+
+extern "C" {
+
+long ecd_packed_bytes_f16(int N, int K) { return (long)((N + 15) / 16) * 16 * (long)K * 2; }
+
+int ecd_pack_f16(const void* w, int N, int K, int interleave, void* out, void* stream) {
+  if (!w || !out || N <= 0 || K <= 0 || (K % 64) || (interleave && (N & 1)) || !al16(w) ||
+      !al16(out))
+    return ECD_EINVAL;
+  const long total = (long)((N + 15) / 16) * (K / 64) * 128;
+  hipLaunchKernelGGL(pack_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const f16*)w, N, K, interleave, (f16*)out);
+  return ecd_launch_status();
+}
+
+int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                        const void* res, long ldr, void* y, long ldy, int M, int N, int K,
+                        int silu, int cfg, void* stream) {
+  if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 11 || (silu != 0 && silu != 1))
+    return ECD_EINVAL;
+  if (silu) {
+    if ((N % 2) || ldy < N / 2 || (ldy % 2) || ((uintptr_t)y & 3) || bias || res || alpha != 1.0f)
+      return ECD_EINVAL;
+  } else if (ldy < N || (res && ldr < N)) {
+    return ECD_EINVAL;
+  }
+  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
+  if (silu)
+    return launch_f16<F16_SILU>(cfg, (const f16*)x, ldx, (const f16*)wp, nullptr, 1.0f, nullptr,
+                                0, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
+  return launch_f16<F16_STORE>(cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha,
+                               (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
+}
+
+int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                  const void* res, long ldr, void* y, long ldy, int M, int N, int K,
+                  void* stream) {
+  return ecd_gemm_f16p_tuned(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, 0, 0, stream);
+}
+
+int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,
+                       int K, void* stream) {
+  if (F <= 0) return ECD_EINVAL;
+  return ecd_gemm_f16p_tuned(x, ldx, wp, nullptr, 1.0f, nullptr, 0, mm, ldm, M, 2 * F, K, 1, 0,
+                             stream);
+}
+
+}  // extern "C"

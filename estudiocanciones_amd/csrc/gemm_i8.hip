@@ -7,12 +7,6 @@
 // Weights use the lane-ordered packed layout of gemv_fused.hip: chunk (tile, c) = 16 rows x
 // 64 bytes stored so that lane l's 16 bytes are row l & 15, k = 64c + 16 (l >> 4) .. +15.
 //
-// The same kernel serves fp16 weights (the dense layers of the codec's flow-matching estimator,
-// app/heartcodec/models/transformer.py): chunk (tile, c) is then 2 KB, two 1 KB halves h in
-// the same lane order (lane l's 8 halfs of half h: row l & 15, k = 64c + 16 (l >> 4) + 8h ..),
-// so every lane reads its two A fragments directly; the epilogue adds an fp32 bias before the
-// fp16 rounding and can scale the rounded value by alpha (ecd_pack_f16, ecd_gemm_f16p).
-//
 // Tiling: a block computes 128 output features x 128 rows with 4 waves; wave w owns features
 // 32 w .. 32 w + 31 for all 128 rows = 2 x 8 tiles of v_mfma_f32_16x16x32_f16 (weights = A
 // operand, x = B operand), so each weight fragment is dequantised by one wave only (the
@@ -26,9 +20,6 @@
 // 16-byte weight fragment is dequantised once and used by 8 row tiles; each x fragment is used
 // by 2 feature tiles.
 //
-// The LDS DMA is issued from inline asm with M0 (the instruction's LDS base) saved and restored
-// around it: with the compiler's builtin, every LDS read of the chunk being multiplied would
-// wait for the DMA of the next one too (vmcnt 0 before any LDS read), which removes the overlap.
 // The kernel orders the DMA itself: at the top of step c each thread waits for its own loads of
 // chunk c (vmcnt 0), a barrier makes the chunk of every wave visible and frees the stage read
 // in step c - 1, and only then are chunk c + 1's loads issued into that stage.
@@ -45,27 +36,12 @@ constexpr int GT_N = 128;   // output features per block
 constexpr int GT_M = 128;   // rows per block
 constexpr int GT_NS = 2;    // LDS stages
 
-// wait until no vector-memory operation of this wave is outstanding (gfx9 encoding: vmcnt 0,
-// expcnt and lgkmcnt at their maxima, i.e. not waited for)
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
-
-// one wave instruction: 16 bytes per lane from base + off (base wave-uniform, off a per-lane
-// byte offset below 2^31) into LDS at dst + 16 * lane (dst uniform)
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, void* dst) {
-  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
-  uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-               "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
-}
-
-template <int EPI, bool FW>
+template <int EPI>
 __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     const f16* __restrict__ x, long ldx, const int8_t* __restrict__ wp,
-    const f16* __restrict__ s, const float* __restrict__ bias, float alpha,
-    const f16* __restrict__ res, long ldr, f16* __restrict__ y, long ldy, int M, int N, int K,
+    const f16* __restrict__ s, const f16* __restrict__ res, long ldr, f16* __restrict__ y, long ldy, int M, int N, int K,
     int nfb, int nmb) {
-  constexpr int WB = FW ? 2048 : 1024;  // bytes of one (tile, chunk) of packed weights
+  constexpr int WB = 1024;  // bytes of one (tile, chunk) of packed weights
   __shared__ __align__(16) int8_t lw[GT_NS][8 * WB];
   __shared__ __align__(16) f16 lx[GT_NS][GT_M * 64];
 
@@ -102,11 +78,8 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     xoff[i] = (uint32_t)((long)min(m0 + 8 * (4 * wv + i) + (lane >> 3), M - 1) * ldx * 2 +
                          16 * xpiece);
   auto issue = [&](int c, int st) {
-#pragma unroll
-    for (int h = 0; h < WB / 1024; ++h) {
-      lds_dma16(wbase0 + (long)c * WB + 1024 * h, woff, &lw[st][wv * WB + 1024 * h]);
-      lds_dma16(wbase1 + (long)c * WB + 1024 * h, woff, &lw[st][(4 + wv) * WB + 1024 * h]);
-    }
+    lds_dma16(wbase0 + (long)c * WB, woff, &lw[st][wv * WB]);
+    lds_dma16(wbase1 + (long)c * WB, woff, &lw[st][(4 + wv) * WB]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       lds_dma16(x + (long)c * 64, xoff[i], &lx[st][8 * (4 * wv + i) * 64]);
@@ -114,10 +87,8 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
 
   // per-lane dequantisation scales of the 2 feature tiles (row lane & 15 of each)
   f16 sc[2];
-  if constexpr (!FW) {
 #pragma unroll
-    for (int ft = 0; ft < 2; ++ft) sc[ft] = s[min(n0 + (wv * 2 + ft) * 16 + (lane & 15), N - 1)];
-  }
+  for (int ft = 0; ft < 2; ++ft) sc[ft] = s[min(n0 + (wv * 2 + ft) * 16 + (lane & 15), N - 1)];
 
   f32x4 acc[2][8];
 #pragma unroll
@@ -137,15 +108,10 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     f16x8 wa[2], wb[2];
 #pragma unroll
     for (int ft = 0; ft < 2; ++ft) {
-      if constexpr (FW) {
-        wa[ft] = *(const f16x8*)(&lw[st][(wv * 2 + ft) * WB + 16 * lane]);
-        wb[ft] = *(const f16x8*)(&lw[st][(wv * 2 + ft) * WB + 1024 + 16 * lane]);
-      } else {
-        const u32x4 raw = *(const u32x4*)(&lw[st][(wv * 2 + ft) * 1024 + 16 * lane]);
-        i8x16_to_f16(raw, wa[ft], wb[ft]);
-        wa[ft] = wa[ft] * sc[ft];
-        wb[ft] = wb[ft] * sc[ft];
-      }
+      const u32x4 raw = *(const u32x4*)(&lw[st][(wv * 2 + ft) * 1024 + 16 * lane]);
+      i8x16_to_f16(raw, wa[ft], wb[ft]);
+      wa[ft] = wa[ft] * sc[ft];
+      wb[ft] = wb[ft] * sc[ft];
     }
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) {
@@ -172,12 +138,7 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
       if (nb >= N) continue;
       f16 yv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float a = acc[ft][rt][r];
-        if (FW && bias) a += bias[min(nb + r, N - 1)];
-        yv[r] = (f16)a;
-        if (FW && alpha != 1.0f) yv[r] = (f16)((float)yv[r] * alpha);
-      }
+      for (int r = 0; r < 4; ++r) yv[r] = (f16)acc[ft][rt][r];
       if (EPI == GEPI_STORE) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -199,39 +160,16 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   }
 }
 
-template <int EPI, bool FW>
-static int launch_gemm(const f16* x, long ldx, const int8_t* wp, const f16* s, const float* bias,
-                       float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N,
-                       int K, hipStream_t st) {
+template <int EPI>
+static int launch_gemm(const f16* x, long ldx, const int8_t* wp, const f16* s, const f16* res,
+                       long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st) {
   const int nfb = (N + GT_N - 1) / GT_N;
   const int nmb = (M + GT_M - 1) / GT_M;
   const long blocks = (long)((nfb + 7) / 8) * 8 * nmb;
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
-  hipLaunchKernelGGL((gemm_i8p_kernel<EPI, FW>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
-                     wp, s, bias, alpha, res, ldr, y, ldy, M, N, K, nfb, nmb);
+  hipLaunchKernelGGL((gemm_i8p_kernel<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
+                     wp, s, res, ldr, y, ldy, M, N, K, nfb, nmb);
   return ecd_launch_status();
-}
-
-// Pack fp16 w [N, K] into lane-ordered 16 x 64 tiles of 2 KB (two 1 KB halves); with
-// `interleave` (N even) packed row 2j is source row j and 2j + 1 is source row N/2 + j.
-__global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w, int N, int K,
-                                                       int interleave, f16* __restrict__ out) {
-  const int nch = K >> 6;
-  const long ntiles = (N + 15) >> 4;
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= ntiles * nch * 128) return;
-  const int l = (int)(idx & 63);
-  const int h = (int)((idx >> 6) & 1);
-  const long tc = idx >> 7;
-  const int c = (int)(tc % nch);
-  const long tile = tc / nch;
-  const long r = tile * 16 + (l & 15);
-  u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-  if (r < N) {
-    const long src = interleave ? ((r & 1) ? (N >> 1) + (r >> 1) : (r >> 1)) : r;
-    v = *(const u32x4*)(w + src * K + 64L * c + 16 * (l >> 4) + 8 * h);
-  }
-  *(u32x4*)(out + (tile * nch + c) * 1024 + 512 * h + 8 * l) = v;
 }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -251,9 +189,8 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
       !al16(x) || !al16(wp) || ldy < N || (res && ldr < N))
     return ECD_EINVAL;
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  return launch_gemm<GEPI_STORE, false>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s,
-                                        nullptr, 1.0f, (const f16*)res, ldr, (f16*)y, ldy, M, N,
-                                        K, (hipStream_t)stream);
+  return launch_gemm<GEPI_STORE>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s,
+                                 (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
 }
 
 int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,
@@ -262,44 +199,8 @@ int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, vo
       (ldx % 8) || !al16(x) || !al16(wp) || ldm < F || (ldm % 2) || ((uintptr_t)mm & 3))
     return ECD_EINVAL;
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  return launch_gemm<GEPI_SILU, false>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s,
-                                       nullptr, 1.0f, nullptr, 0, (f16*)mm, ldm, M, 2 * F, K,
-                                       (hipStream_t)stream);
-}
-
-long ecd_packed_bytes_f16(int N, int K) { return (long)((N + 15) / 16) * 16 * (long)K * 2; }
-
-int ecd_pack_f16(const void* w, int N, int K, int interleave, void* out, void* stream) {
-  if (!w || !out || N <= 0 || K <= 0 || (K % 64) || (interleave && (N & 1)) || !al16(w) ||
-      !al16(out))
-    return ECD_EINVAL;
-  const long total = (long)((N + 15) / 16) * (K / 64) * 128;
-  hipLaunchKernelGGL(pack_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const f16*)w, N, K, interleave, (f16*)out);
-  return ecd_launch_status();
-}
-
-int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, float alpha,
-                  const void* res, long ldr, void* y, long ldy, int M, int N, int K,
-                  void* stream) {
-  if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || ldy < N || (res && ldr < N))
-    return ECD_EINVAL;
-  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  return launch_gemm<GEPI_STORE, true>((const f16*)x, ldx, (const int8_t*)wp, nullptr, bias,
-                                       alpha, (const f16*)res, ldr, (f16*)y, ldy, M, N, K,
-                                       (hipStream_t)stream);
-}
-
-int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,
-                       int K, void* stream) {
-  if (!x || !wp || !mm || M <= 0 || F <= 0 || (F % 2) || K <= 0 || (K % 64) || ldx < K ||
-      (ldx % 8) || !al16(x) || !al16(wp) || ldm < F || (ldm % 2) || ((uintptr_t)mm & 3))
-    return ECD_EINVAL;
-  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  return launch_gemm<GEPI_SILU, true>((const f16*)x, ldx, (const int8_t*)wp, nullptr, nullptr,
-                                      1.0f, nullptr, 0, (f16*)mm, ldm, M, 2 * F, K,
-                                      (hipStream_t)stream);
+  return launch_gemm<GEPI_SILU>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s, nullptr,
+                                0, (f16*)mm, ldm, M, 2 * F, K, (hipStream_t)stream);
 }
 
 }  // extern "C"

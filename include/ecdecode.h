@@ -209,6 +209,14 @@ int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, fl
 int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,
                        int K, void* stream);
 
+/* ecd_gemm_f16p (silu 0) or ecd_gemm_f16p_silu (silu 1, N = 2F, bias/res NULL, alpha 1) with an
+ * explicit block tile (cfg 1..11: 128x128, 256x128, 128x256 or 128x64 features x rows, 2 or 3 LDS
+ * stages; 0 = the library's choice).  Replaces nothing in the reference: the launch-shape knob
+ * of the codec GEMMs, for sweeps. */
+int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                        const void* res, long ldr, void* y, long ldy, int M, int N, int K,
+                        int silu, int cfg, void* stream);
+
 /* Causal attention of the prompt pass on MFMA: row r = b * S + s of q [B * S, Hq * HD] attends
  * cache slots [0, pos[r]] of kc, vc [B, Hk, L, HD] (the prompt's K/V already written), with the
  * decode kernel's numerics (fp32 scores, running max, fp16 probabilities into P.V, fp32 sums).

@@ -88,6 +88,35 @@ def test_gemm_f16_silu(dev, M, F, K):
     assert_close16(N_(got), want, what=f"gemm f16 silu M={M} F={F}")
 
 
+@pytest.mark.parametrize("M,N,K,silu", [(200, 1536, 1536, 0), (77, 1000, 640, 0), (300, 2048, 512, 1)])
+def test_gemm_f16_tile_configs_agree(dev, M, N, K, silu):
+    """Every block tile / pipeline variant accumulates each output in the same order: all agree
+    bit for bit with the first, and the library default with the fp32 product."""
+    import torch
+    from estudiocanciones_amd.kernels import pack_f16
+    g = rng(420 + N)
+    x = randn16(421 + M, M, K)
+    w = (g.standard_normal((N, K), dtype=np.float32) * 0.02).astype(np.float16)
+    b = None if silu else D_((g.standard_normal(N, dtype=np.float32) * 0.1), dev)
+    r = None if silu else D_(randn16(422, M, N), dev)
+    xt, wp = D_(x, dev), pack_f16(D_(w, dev), interleave=bool(silu))
+    No = N // 2 if silu else N
+    outs = []
+    for cfg in range(0, 12):
+        y = torch.empty(M, No, dtype=torch.float16, device=dev)
+        _call("ecd_gemm_f16p_tuned", xt.data_ptr(), K, wp.data_ptr(),
+              None if b is None else b.data_ptr(), 1.0 if silu else 0.75,
+              None if r is None else r.data_ptr(), N, y.data_ptr(), No, M, N, K, silu, cfg)
+        outs.append(N_(y))
+    for cfg, o in enumerate(outs[2:], 2):
+        _exact(o, outs[1], f"gemm f16 cfg {cfg} vs cfg 1 (M={M} N={N} K={K} silu={silu})")
+    _exact(outs[0], outs[1], "library default vs cfg 1")
+    if not silu:
+        want = f16(x.astype(np.float32) @ w.astype(np.float32).T + N_(b))
+        want = f16(f16(want.astype(np.float32) * np.float32(0.75)).astype(np.float32) + N_(r))
+        assert_close16(outs[0], want, what="gemm f16 default")
+
+
 # ---------------------------------------------------------------- RoPE
 @pytest.mark.parametrize("L,HD", [(744, 64), (744, 128), (37, 64)])
 def test_codec_rope_table(dev, L, HD):
