@@ -128,6 +128,8 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   }
 
   // epilogue: lane holds features nb + r (r < 4) of row m for every (ft, rt)
+  const bool vec = ((ldy & 3) == 0) && (((uintptr_t)y & 7) == 0) &&
+                   (!res || (((ldr & 3) == 0) && (((uintptr_t)res & 7) == 0)));
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
     const int m = m0 + rt * 16 + (lane & 15);
@@ -136,16 +138,21 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     for (int ft = 0; ft < 2; ++ft) {
       const int nb = n0 + (wv * 2 + ft) * 16 + 4 * (lane >> 4);
       if (nb >= N) continue;
-      f16 yv[4];
+      f16x4 yv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) yv[r] = (f16)acc[ft][rt][r];
       if (EPI == GEPI_STORE) {
+        if (vec && nb + 3 < N) {  // one 8-byte store (and residual load) per lane
+          if (res) yv = yv + *(const f16x4*)(res + (long)m * ldr + nb);
+          *(f16x4*)(y + (long)m * ldy + nb) = yv;
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (nb + r < N) {
-            f16 o = yv[r];
-            if (res) o = o + res[(long)m * ldr + nb + r];
-            y[(long)m * ldy + nb + r] = o;
+          for (int r = 0; r < 4; ++r) {
+            if (nb + r < N) {
+              f16 o = yv[r];
+              if (res) o = o + res[(long)m * ldr + nb + r];
+              y[(long)m * ldy + nb + r] = o;
+            }
           }
         }
       } else {  // (a_j, b_j, a_j+1, b_j+1) with j = nb / 2; N even
