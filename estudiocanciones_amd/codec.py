@@ -30,7 +30,8 @@ from . import _ffi
 from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_attn,
                       stream_ptr)
 
-__all__ = ["LlamaTransformer", "solve_euler", "mlp_hidden", "euler_times", "random_state_dict", "estimator_flops"]
+__all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes", "mlp_hidden",
+           "euler_times", "t_span", "random_state_dict", "estimator_flops"]
 
 EPS = 1e-6
 SQRT1_3 = 3 ** -0.5
@@ -201,8 +202,10 @@ class LlamaTransformer:
 
     # ------------------------------------------------------------ pieces
     def _cols(self, segs, B, T, buf):
-        """k = 3 columns of the channel concatenation of ``segs`` [(tensor, width, bmod, bzero)]."""
+        """k = 3 columns of the channel concatenation of ``segs`` [(tensor, width, bmod, bzero)
+        or (tensor, width, bmod, bzero, rep)]; rep 2 reads a half-rate source upsampled 2x."""
         n = len(segs)
+        rp = (ctypes.c_int * n)(*[s[4] if len(s) > 4 else 1 for s in segs])
         ptr = (ctypes.c_void_p * n)(*[s[0].data_ptr() for s in segs])
         ld = (ctypes.c_long * n)(*[s[0].stride(-2) for s in segs])
         w = (ctypes.c_int * n)(*[s[1] for s in segs])
@@ -210,7 +213,7 @@ class LlamaTransformer:
         bz = (ctypes.c_int * n)(*[s[3] for s in segs])
         C = sum(s[1] for s in segs)
         cols = buf["cols"][:B * T * 3 * C].view(B * T, 3 * C)
-        _ffi.call("ecd_codec_cols3", ptr, ld, w, bm, bz, n, cols.data_ptr(), B, T,
+        _ffi.call("ecd_codec_cols3", ptr, ld, w, bm, bz, rp, n, cols.data_ptr(), B, T,
                   stream_ptr(self.dev))
         return cols
 
@@ -304,18 +307,23 @@ class LlamaTransformer:
 
 def solve_euler(est: LlamaTransformer, x: torch.Tensor, incontext_x: torch.Tensor,
                 incontext_length: int, t_span, mu: torch.Tensor, guidance_scale: float,
-                copy_incontext: bool = False) -> torch.Tensor:
+                copy_incontext: bool = False, mu_rep: int = 1) -> torch.Tensor:
     """FlowMatching.solve_euler (flow_matching.py:161-210) on the GPU.  x, incontext_x
-    [B, T, C] fp16, mu [B, T, Cmu] fp16, t_span the fp32 time grid.  Returns the final x (a new
-    tensor).  ``copy_incontext`` also applies inference_codes' final
+    [B, T, C] fp16, mu [B, T / mu_rep, Cmu] fp16 (mu_rep 2: half-rate mu, read as its nearest
+    2x upsampling), t_span the fp32 time grid.  Returns the final x (a new tensor).
+    ``copy_incontext`` also applies inference_codes' final
     ``latents[:, :L] = incontext_latents[:, :L]`` (flow_matching.py:156-158)."""
     B, T, C = x.shape
     Cmu = mu.shape[-1]
     if C + C + Cmu != est.cin:
         raise ValueError("x, incontext_x and mu widths must add up to the estimator's input")
+    if mu_rep not in (1, 2) or T % mu_rep or mu.shape[:2] != (B, T // mu_rep):
+        raise ValueError("mu must be [B, T / mu_rep, Cmu] with mu_rep 1 or 2")
     for a in (x, incontext_x, mu):
-        if a.dtype != torch.float16 or not a.is_contiguous() or a.shape[:2] != (B, T):
+        if a.dtype != torch.float16 or not a.is_contiguous() or a.shape[0] != B:
             raise ValueError("x, incontext_x, mu must be contiguous fp16 [B, T, *]")
+    if x.shape != incontext_x.shape:
+        raise ValueError("incontext_x must be shaped like x")
     L = int(incontext_length)
     ts, dts = euler_times(t_span)
     n = len(ts)
@@ -329,7 +337,7 @@ def solve_euler(est: LlamaTransformer, x: torch.Tensor, incontext_x: torch.Tenso
     B2 = 2 * B if cfg else B
     # rows of the estimator input: [x | incontext | 0 (uncond) or mu (cond)] over 2B entries
     segs = [(x.view(B * T, C), C, B, 0), (ic.view(B * T, C), C, B, 0),
-            (mu.view(B * T, Cmu), Cmu, B, B if cfg else 0)]
+            (mu.view(B * (T // mu_rep), Cmu), Cmu, B, B if cfg else 0, mu_rep)]
     _ffi.call("ecd_codec_euler", x.data_ptr(), noise.data_ptr(), ic.data_ptr(), None, int(cfg),
               B, T, C, L, 0.0, 0.0, float(ts[0]), 0, st)
     D, D2 = est.D, est.D2
@@ -345,6 +353,81 @@ def solve_euler(est: LlamaTransformer, x: torch.Tensor, incontext_x: torch.Tenso
                   int(cfg), B, T, C, 0 if (last and not copy_incontext) else L, float(dts[k]),
                   float(guidance_scale), tb, mode, st)
     return x
+
+
+class CodeEmbedding:
+    """The conditioning of FlowMatching.inference_codes (flow_matching.py:86-108): per-quantizer
+    codebook rows summed (ResidualVQ.get_codes_from_indices + sum), ``project_out``,
+    ``cond_feature_emb``.  Returns the half-rate features [B * Tc, dim]; the estimator input
+    reads them through the nearest 2x upsampling (``solve_euler(..., mu_rep=2)``).
+
+    ``sd`` maps the reference's names relative to ``flow_matching.`` (``vq_embed.layers.{q}.
+    _codebook.embed`` [1, V, Dc], ``vq_embed.project_out.{weight,bias}``,
+    ``cond_feature_emb.{weight,bias}``)."""
+
+    def __init__(self, sd: dict, num_quantizers=8, device="cuda"):
+        self.dev = torch.device(device)
+        get = lambda n: sd[n].to(device=self.dev, dtype=torch.float16).contiguous()
+        books = [get(f"vq_embed.layers.{q}._codebook.embed") for q in range(num_quantizers)]
+        self.Q = num_quantizers
+        self.V, self.Dc = books[0].shape[-2], books[0].shape[-1]
+        self.books = torch.stack([b.reshape(self.V, self.Dc) for b in books]).contiguous()
+        self.Wp = (self.Dc + 63) // 64 * 64          # K of the projection padded to the GEMM
+        po = get("vq_embed.project_out.weight")      # [dim, Dc]
+        self.dim = po.shape[0]
+        pw = torch.zeros(self.dim, self.Wp, device=self.dev, dtype=torch.float16)
+        pw[:, :self.Dc] = po
+        self.project_out = _Linear(pw, get("vq_embed.project_out.bias"))
+        self.cond = _Linear(get("cond_feature_emb.weight"), get("cond_feature_emb.bias"))
+
+    def __call__(self, codes: torch.Tensor) -> torch.Tensor:
+        """codes [B, Q, Tc] int64 (any strides with unit stride along Tc) -> [B * Tc, dim]."""
+        B, Q, Tc = codes.shape
+        if Q != self.Q or codes.dtype != torch.int64 or codes.stride(2) != 1:
+            raise ValueError(f"codes must be int64 [B, {self.Q}, Tc] with unit stride in time")
+        codes = codes.to(self.dev)
+        st = stream_ptr(self.dev)
+        e = torch.empty(B * Tc, self.Wp, device=self.dev, dtype=torch.float16)
+        _ffi.call("ecd_codec_vq_embed", codes.data_ptr(), codes.stride(0), codes.stride(1),
+                  self.books.data_ptr(), e.data_ptr(), B, Q, Tc, self.V, self.Dc, self.Wp, st)
+        h = self.project_out(e, torch.empty(B * Tc, self.dim, device=self.dev, dtype=torch.float16))
+        return self.cond(h, torch.empty_like(h))
+
+
+def t_span(num_steps: int) -> np.ndarray:
+    """torch.linspace(0, 1, num_steps + 1) in fp32 (flow_matching.py:140-142), evaluated as
+    torch's linspace does: the first half from the start, the second half from the end."""
+    n = num_steps + 1
+    step = np.float32(1.0) / np.float32(n - 1)
+    i = np.arange(n, dtype=np.float32)
+    lo = (step * i).astype(np.float32)
+    hi = (np.float32(1.0) - (step * (np.float32(n - 1) - i)).astype(np.float32)).astype(np.float32)
+    return np.where(np.arange(n) < n // 2, lo, hi).astype(np.float32)
+
+
+def inference_codes(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.Tensor,
+                    true_latents: torch.Tensor, latent_length: int, incontext_length: int,
+                    guidance_scale: float = 2.0, num_steps: int = 20, scenario: str = "start_seg",
+                    noise: torch.Tensor | None = None) -> torch.Tensor:
+    """FlowMatching.inference_codes (flow_matching.py:72-159): codes [B, Q, Tc] -> latents
+    [B, 2 Tc, latent_dim] fp16.  ``noise`` is the initial latent sample (the reference draws it
+    with torch.randn on its global generator); drawn from torch's device generator when None.
+    Every frame must be a conditioned frame (latent_length == 2 Tc), as in detokenize."""
+    B, _, Tc = codes.shape
+    T = 2 * Tc
+    C = true_latents.shape[-1]
+    if latent_length != T:
+        raise NotImplementedError("frames past latent_length (zero_cond rows) are not built")
+    dev = est.dev
+    mu = emb(codes).view(B, Tc, emb.dim)
+    x = (noise if noise is not None else torch.randn(B, T, C, device=dev)).to(
+        device=dev, dtype=torch.float16).contiguous()
+    L = int(incontext_length) if scenario == "other_seg" else 0
+    ic = torch.zeros(B, T, C, device=dev, dtype=torch.float16)
+    if L:
+        ic[:, :L] = true_latents[:, :L].to(device=dev, dtype=torch.float16)
+    return solve_euler(est, x, ic, L, t_span(num_steps), mu, guidance_scale,
+                       copy_incontext=True, mu_rep=2)
 
 
 def random_state_dict(num_attention_heads=24, attention_head_dim=64, in_channels=1024,

@@ -198,13 +198,15 @@ __global__ __launch_bounds__(256) void codec_norm_mod_kernel(
 
 // ---------------------------------------------------------------- k = 3 convolution columns
 // Channel segments of the convolution input: segment i contributes w[i] channels read from
-// p[i] + ((b % bmod[i]) * T + s) * ld[i] for batch entries b >= bzero[i], zeros below.
+// p[i] + ((b % bmod[i]) * (T / rep[i]) + s / rep[i]) * ld[i] for batch entries b >= bzero[i],
+// zeros below (rep 2: a half-rate source repeated, nearest 2x upsampling).
 struct ColSegs {
   const f16* p[4];
   long ld[4];
   int w[4];
   int bmod[4];
   int bzero[4];
+  int rep[4];
   int n;
 };
 
@@ -229,7 +231,9 @@ __global__ __launch_bounds__(256) void codec_cols3_kernel(ColSegs sg, f16* __res
     for (int g = 0; g < 4; ++g) {
       if (g >= sg.n) break;
       const bool live = inside && b >= sg.bzero[g];
-      const f16* src = sg.p[g] + ((long)(b % sg.bmod[g]) * T + (inside ? s : 0)) * sg.ld[g];
+      const int rp = sg.rep[g];
+      const f16* src =
+          sg.p[g] + ((long)(b % sg.bmod[g]) * (T / rp) + (inside ? s : 0) / rp) * sg.ld[g];
       const int nv = sg.w[g] >> 3;
       for (int i = threadIdx.x; i < nv; i += 256) {
         u32x4 val = {0u, 0u, 0u, 0u};
@@ -238,6 +242,37 @@ __global__ __launch_bounds__(256) void codec_cols3_kernel(ColSegs sg, f16* __res
       }
       base += sg.w[g];
     }
+  }
+}
+
+// ---------------------------------------------------------------- code embedding
+// out[b * Tc + t, d] = fp16(sum_q codebooks[q, codes[b, q, t], d]) for d < Dc (fp32 sum in
+// quantizer order), zero for Dc <= d < Wp: ResidualVQ.get_codes_from_indices then the sum over
+// quantizers (flow_matching.py:98-99).  A code of -1 (the library's padding) or any code
+// outside [0, V) contributes nothing.  codes [B, Q, Tc] int64 with strides (cb, cq, 1).  One
+// thread per (row, 8 dims).
+__global__ __launch_bounds__(256) void codec_vq_embed_kernel(
+    const int64_t* __restrict__ codes, long cb, long cq, const f16* __restrict__ books,
+    f16* __restrict__ out, int B, int Q, int Tc, int V, int Dc, int Wp) {
+  const long n = (long)B * Tc * (Wp >> 3);
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const int dv = (int)(i % (Wp >> 3)) * 8;
+    const long row = i / (Wp >> 3);
+    const int b = (int)(row / Tc), t = (int)(row - (long)b * Tc);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (dv < Dc) {
+      for (int qq = 0; qq < Q; ++qq) {
+        const int64_t c = codes[b * cb + qq * cq + t];
+        if (c < 0 || c >= V) continue;
+        const f16x8 e = *(const f16x8*)(books + ((long)qq * V + c) * Dc + dv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += (float)e[j];
+      }
+    }
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (f16)acc[j];
+    *(f16x8*)(out + row * Wp + dv) = o;
   }
 }
 
@@ -367,8 +402,8 @@ int ecd_codec_norm_mod(void* x, const void* h, const void* g_tab, const void* g_
 }
 
 int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* seg_w,
-                    const int* seg_bmod, const int* seg_bzero, int nseg, void* out, int B, int T,
-                    void* stream) {
+                    const int* seg_bmod, const int* seg_bzero, const int* seg_rep, int nseg,
+                    void* out, int B, int T, void* stream) {
   if (!seg_ptr || !seg_ld || !seg_w || !seg_bmod || !seg_bzero || !out || nseg <= 0 ||
       nseg > 4 || B <= 0 || T <= 0 || !a16(out))
     return ECD_EINVAL;
@@ -376,8 +411,10 @@ int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* s
   int C = 0;
   for (int i = 0; i < nseg; ++i) {
     if (!seg_ptr[i] || !a16(seg_ptr[i]) || seg_w[i] <= 0 || (seg_w[i] & 7) ||
-        seg_ld[i] < seg_w[i] || (seg_ld[i] & 7) || seg_bmod[i] <= 0 || seg_bzero[i] < 0)
+        seg_ld[i] < seg_w[i] || (seg_ld[i] & 7) || seg_bmod[i] <= 0 || seg_bzero[i] < 0 ||
+        (seg_rep && (seg_rep[i] <= 0 || T % seg_rep[i])))
       return ECD_EINVAL;
+    sg.rep[i] = seg_rep ? seg_rep[i] : 1;
     sg.p[i] = (const f16*)seg_ptr[i];
     sg.ld[i] = seg_ld[i];
     sg.w[i] = seg_w[i];
@@ -388,6 +425,17 @@ int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* s
   sg.n = nseg;
   hipLaunchKernelGGL(codec_cols3_kernel, dim3(B * T), dim3(256), 0, (hipStream_t)stream, sg,
                      (f16*)out, T, C);
+  return ecd_launch_status();
+}
+
+int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books, void* out,
+                       int B, int Q, int Tc, int V, int Dc, int Wp, void* stream) {
+  if (!codes || !books || !out || B <= 0 || Q <= 0 || Tc <= 0 || V <= 0 || Dc <= 0 || (Dc & 7) ||
+      Wp < Dc || (Wp & 7) || cb < 0 || cq < 0 || !a16(books) || !a16(out))
+    return ECD_EINVAL;
+  hipLaunchKernelGGL(codec_vq_embed_kernel, dim3(grid_for((long)B * Tc * (Wp / 8))), dim3(256), 0,
+                     (hipStream_t)stream, codes, cb, cq, (const f16*)books, (f16*)out, B, Q, Tc,
+                     V, Dc, Wp);
   return ecd_launch_status();
 }
 

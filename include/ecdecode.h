@@ -254,11 +254,20 @@ int ecd_codec_norm_mod(void* x, const void* h, const void* g_tab, const void* g_
 /* Columns of nn.Conv1d(k = 3, padding = 1) (ProjectLayer, transformer.py:258-272) over the
  * channel concatenation of up to 4 segments: out [B*T, 3*C], out[b*T + t, j*C + c] =
  * in[b, t + j - 1, c] (zero outside [0, T)); segment i gives seg_w[i] channels from
- * seg_ptr[i] + ((b % seg_bmod[i]) * T + s) * seg_ld[i] for b >= seg_bzero[i], zeros below
- * (solve_euler's input, flow_matching.py:183-193; torch.cat of transformer.py:372). */
+ * seg_ptr[i] + ((b % seg_bmod[i]) * (T / r) + s / r) * seg_ld[i], r = seg_rep[i] (1 if
+ * seg_rep is NULL; 2 reads a half-rate source as its nearest 2x upsampling,
+ * flow_matching.py:106-108), for b >= seg_bzero[i], zeros below (solve_euler's input,
+ * flow_matching.py:183-193; torch.cat of transformer.py:372). */
 int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* seg_w,
-                    const int* seg_bmod, const int* seg_bzero, int nseg, void* out, int B, int T,
-                    void* stream);
+                    const int* seg_bmod, const int* seg_bzero, const int* seg_rep, int nseg,
+                    void* out, int B, int T, void* stream);
+
+/* Code embedding: out [B*Tc, Wp] fp16, out[b*Tc + t, d] = fp16(sum_q books[q, codes[b, q, t], d])
+ * for d < Dc, zero for Dc <= d < Wp (ResidualVQ.get_codes_from_indices and the sum over
+ * quantizers, flow_matching.py:98-99); books [Q, V, Dc] fp16; codes int64 at
+ * codes[b*cb + q*cq + t]; codes -1 or outside [0, V) contribute nothing.  Dc, Wp % 8 == 0. */
+int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books, void* out,
+                       int B, int Q, int Tc, int V, int Dc, int Wp, void* stream);
 
 /* Timestep sinusoid out [n, 512] fp16 from t [n] fp32 (PixArtAlphaCombinedFlowEmbeddings.
  * timestep_embedding, transformer.py:408-426). */

@@ -1,4 +1,5 @@
-"""Oracle of the codec's flow-matching estimator and Euler solver (test infrastructure only).
+"""Oracle of the codec's flow-matching estimator, Euler solver and code embedding (test
+infrastructure only).
 
 Restates, in numpy, the fp16 forward of ``LlamaTransformer`` with ``norm_type="ada_norm_single"``
 (app/heartcodec/models/transformer.py:275-396) and ``FlowMatching.solve_euler``
@@ -293,4 +294,62 @@ def random_weights(cfg: dict, seed: int = 0) -> dict:
     conv("proj_out", Cout, D2)
     ada("adaln_single.", D)
     ada("adaln_single_2.", D2)
+    return p
+
+
+# ---------------------------------------------------------------- code embedding
+def code_embedding(p: dict, codes, num_quantizers: int = 8) -> np.ndarray:
+    """FlowMatching.inference_codes conditioning (flow_matching.py:98-108): codebook rows of every
+    quantizer (ResidualVQ.get_codes_from_indices; a code of -1 contributes zeros), their fp16 sum,
+    project_out, cond_feature_emb, nearest 2x upsampling in time.  codes [B, Q, Tc] ->
+    [B, 2 Tc, dim].  Weights under the names relative to ``flow_matching.``."""
+    codes = np.asarray(codes, dtype=np.int64)
+    B, Q, Tc = codes.shape
+    acc = None
+    for q in range(num_quantizers):
+        book = np.asarray(p[f"vq_embed.layers.{q}._codebook.embed"], np.float16)
+        book = book.reshape(-1, book.shape[-1]).astype(np.float64)
+        idx = codes[:, q, :]
+        e = book[np.clip(idx, 0, None)] * (idx >= 0)[..., None]
+        acc = e if acc is None else acc + e
+    summed = f16(acc)                                                  # [B, Tc, Dc]
+    h = linear(summed, p["vq_embed.project_out.weight"], p["vq_embed.project_out.bias"])
+    h = linear(h, p["cond_feature_emb.weight"], p["cond_feature_emb.bias"])
+    return np.repeat(h, 2, axis=1)
+
+
+def inference_codes(p_fm: dict, p_est: dict, cfg: dict, codes, true_latents, latent_length: int,
+                    incontext_length: int, guidance_scale: float, num_steps: int, scenario: str,
+                    noise) -> np.ndarray:
+    """FlowMatching.inference_codes (flow_matching.py:72-159) with the initial sample ``noise``
+    given (the reference draws it from torch's global generator)."""
+    mu = code_embedding(p_fm, codes)
+    B, T, _ = mu.shape
+    masks = np.zeros((B, T), np.int64)
+    masks[:, :latent_length] = 2
+    if scenario == "other_seg":
+        masks[:, :incontext_length] = 1
+    zero = np.asarray(p_fm["zero_cond_embedding1"], np.float16)
+    mu = f16(f32(f16((masks > 0.5)[..., None] * f32(mu))) + f32(f16((masks < 0.5)[..., None] * f32(zero))))
+    sel = ((masks > 0.5) & (masks < 1.5))
+    ic = f16(np.asarray(true_latents, np.float16).astype(np.float32) * sel[..., None])
+    L = int(sel.sum(-1)[0])
+    x = solve_euler(lambda h, t: estimator(p_est, cfg, h, t), noise, ic, L, t_span(num_steps), mu,
+                    guidance_scale)
+    x[:, :L] = ic[:, :L]
+    return x
+
+
+def random_vq_weights(num_quantizers: int, codebook_size: int, codebook_dim: int, dim: int,
+                      seed: int = 0) -> dict:
+    """Random fp16 code-embedding weights under the reference's names (relative to
+    ``flow_matching.``)."""
+    g = np.random.default_rng(seed)
+    p = {f"vq_embed.layers.{q}._codebook.embed":
+         f16(g.standard_normal((1, codebook_size, codebook_dim)) * 0.5) for q in range(num_quantizers)}
+    p["vq_embed.project_out.weight"] = f16(g.standard_normal((dim, codebook_dim)) / math.sqrt(codebook_dim))
+    p["vq_embed.project_out.bias"] = f16(g.standard_normal(dim) * 0.02)
+    p["cond_feature_emb.weight"] = f16(g.standard_normal((dim, dim)) / math.sqrt(dim))
+    p["cond_feature_emb.bias"] = f16(g.standard_normal(dim) * 0.02)
+    p["zero_cond_embedding1"] = f16(g.standard_normal(dim))
     return p

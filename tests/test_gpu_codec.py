@@ -203,7 +203,7 @@ def test_codec_cols3_bit_exact(dev):
     _ffi.call("ecd_codec_cols3", (ctypes.c_void_p * n)(*[t.data_ptr() for t in dt]),
               (ctypes.c_long * n)(*[sg[1] for sg in segs]), (ctypes.c_int * n)(*[sg[1] for sg in segs]),
               (ctypes.c_int * n)(*[sg[2] for sg in segs]), (ctypes.c_int * n)(*[sg[3] for sg in segs]),
-              n, out.data_ptr(), 2 * B, L, stream_ptr(dev))
+              None, n, out.data_ptr(), 2 * B, L, stream_ptr(dev))
     inp = np.concatenate([np.concatenate([x, x]), np.concatenate([ic, ic]),
                           np.concatenate([np.zeros_like(mu), mu]), s], 1).reshape(2 * B, L, C)
     pad = np.zeros((2 * B, L + 2, C), np.float16)
@@ -297,3 +297,65 @@ def test_codec_solve_euler(dev, g, L_ic):
     got = solve_euler(est, D_(x0, dev), D_(ic, dev), L_ic, ts, D_(mu, dev), g)
     want = OC.solve_euler(lambda h, t: OC.estimator(p, TINY, h, t), x0, ic, L_ic, ts, mu, g)
     _close_model(N_(got), want, f"solve_euler g={g} L={L_ic}")
+
+
+# ---------------------------------------------------------------- code embedding, inference_codes
+def test_codec_vq_embed(dev):
+    """Sum of the 8 quantizers' codebook rows (-1 and out-of-range codes dropped), zero-padded to
+    the GEMM's K, from a strided [B, Q, Tc] window of a longer code tensor."""
+    import torch
+    B, Q, Tfull, Tc, V, Dc, Wp = 2, 8, 40, 29, 100, 32, 64
+    g = rng(760)
+    books = f16(g.standard_normal((Q, V, Dc)) * 0.5)
+    codes_full = g.integers(0, V, (B, Q, Tfull))
+    codes_full[0, 2, 7] = -1
+    codes_full[1, 5, 3] = V + 3
+    win = codes_full[:, :, 5:5 + Tc]
+    ct = D_(codes_full, dev)[:, :, 5:5 + Tc]
+    out = torch.full((B * Tc, Wp), 9.0, dtype=torch.float16, device=dev)
+    bt = D_(books, dev)
+    _call("ecd_codec_vq_embed", ct.data_ptr(), ct.stride(0), ct.stride(1), bt.data_ptr(),
+          out.data_ptr(), B, Q, Tc, V, Dc, Wp)
+    want = np.zeros((B, Tc, Wp))
+    for q in range(Q):
+        idx = win[:, q]
+        ok = (idx >= 0) & (idx < V)
+        want[..., :Dc] += books[q].astype(np.float64)[np.where(ok, idx, 0)] * ok[..., None]
+    assert_close16(N_(out), f16(want).reshape(B * Tc, Wp), what="vq embed")
+    assert np.all(N_(out)[:, Dc:] == 0)
+
+
+def _code_embedding(dev, p):
+    import torch
+    from estudiocanciones_amd.codec import CodeEmbedding
+    return CodeEmbedding({k: torch.from_numpy(v) for k, v in p.items()}, device=dev)
+
+
+def test_code_embedding_host(dev):
+    p = OC.random_vq_weights(8, 64, 32, 128, seed=33)
+    codes = rng(34).integers(0, 64, (2, 8, 21))
+    got = _code_embedding(dev, p)(D_(codes, dev))
+    want = OC.code_embedding(p, codes)[:, ::2].reshape(2 * 21, 128)
+    assert_close16(N_(got), want, what="code embedding")
+
+
+@pytest.mark.parametrize("scenario,L_ic", [("start_seg", 0), ("other_seg", 8)])
+def test_codec_inference_codes(dev, scenario, L_ic):
+    """codes -> latents through the embedding, the half-rate mu read as its 2x upsampling, the
+    CFG solve and the final in-context copy, against the oracle."""
+    from estudiocanciones_amd.codec import inference_codes
+    p_est = OC.random_weights(TINY, seed=35)
+    p_fm = OC.random_vq_weights(8, 64, 32, 64, seed=36)
+    est = _estimator(dev, p_est, TINY)
+    emb = _code_embedding(dev, p_fm)
+    Tc = 18
+    codes = rng(37).integers(0, 64, (1, 8, Tc))
+    true_lat = randn16(38, 1, 2 * Tc, 64)
+    noise = randn16(39, 1, 2 * Tc, 64)
+    got = inference_codes(emb, est, D_(codes, dev), D_(true_lat, dev), 2 * Tc, L_ic, 1.25, 3,
+                          scenario, noise=D_(noise, dev))
+    want = OC.inference_codes(p_fm, p_est, TINY, codes, true_lat, 2 * Tc, L_ic, 1.25, 3, scenario,
+                              noise)
+    _close_model(N_(got), want, f"inference_codes {scenario}")
+    if L_ic:
+        _exact(N_(got)[:, :L_ic], true_lat[:, :L_ic], "in-context prefix copied")

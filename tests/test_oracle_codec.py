@@ -229,3 +229,32 @@ def test_estimator_matches_float64_library_composition():
     err = np.abs(got - want).max() / np.abs(want).max()
     assert err < 2e-2, err
     assert np.corrcoef(got.ravel(), want.ravel())[0, 1] > 0.9999
+
+
+def test_code_embedding_matches_library():
+    """Per-quantizer F.embedding summed, the two linears and nearest 2x interpolation in float64
+    torch; a -1 code (the library's padding) contributes nothing."""
+    Q, V, Dc, dim = 8, 64, 32, 96
+    p = OC.random_vq_weights(Q, V, Dc, dim, seed=31)
+    g = np.random.default_rng(32)
+    codes = g.integers(0, V, (2, Q, 13))
+    codes[1, 3, 5] = -1
+    got = OC.code_embedding(p, codes).astype(np.float64)
+    t = lambda a: torch.from_numpy(np.asarray(a).astype(np.float64))
+    ci = torch.from_numpy(codes)
+    e = sum(F.embedding(ci[:, q].clamp(min=0), t(p[f"vq_embed.layers.{q}._codebook.embed"][0]))
+            * (ci[:, q] >= 0)[..., None] for q in range(Q))
+    h = F.linear(F.linear(e, t(p["vq_embed.project_out.weight"]), t(p["vq_embed.project_out.bias"])),
+                 t(p["cond_feature_emb.weight"]), t(p["cond_feature_emb.bias"]))
+    want = F.interpolate(h.permute(0, 2, 1), scale_factor=2, mode="nearest").permute(0, 2, 1).numpy()
+    assert got.shape == (2, 26, dim)
+    np.testing.assert_allclose(got, want, atol=1e-2, rtol=1e-2)
+    # a -1 code is the same as a code whose codebook row is all zeros
+    unused = next(c for c in range(V) if c not in set(codes[:, 3].ravel().tolist()))
+    p0 = dict(p)
+    book = p["vq_embed.layers.3._codebook.embed"].copy()
+    book[0, unused] = 0
+    p0["vq_embed.layers.3._codebook.embed"] = book
+    codes0 = codes.copy()
+    codes0[1, 3, 5] = unused
+    assert np.array_equal(OC.code_embedding(p0, codes0), got.astype(np.float16))
