@@ -40,7 +40,7 @@ SIGNATURES = {
                            c_int, c_int, c_float, _P],
     "ecd_codec_cols3": [_P, _P, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P],
     "ecd_codec_vq_embed": [_P, c_long, c_long, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
-                           _P],
+                           c_int, _P],
     "ecd_codec_timestep": [_P, _P, c_int, _P],
     "ecd_codec_silu": [_P, _P, c_long, _P],
     "ecd_codec_euler": [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, c_float,

@@ -22,6 +22,7 @@ without the built library every call raises.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import numpy as np
 import torch
@@ -30,7 +31,8 @@ from . import _ffi
 from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_attn,
                       stream_ptr)
 
-__all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes", "mlp_hidden",
+__all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes",
+           "detokenize_latents", "mlp_hidden",
            "euler_times", "t_span", "random_state_dict", "estimator_flops"]
 
 EPS = 1e-6
@@ -380,8 +382,10 @@ class CodeEmbedding:
         self.project_out = _Linear(pw, get("vq_embed.project_out.bias"))
         self.cond = _Linear(get("cond_feature_emb.weight"), get("cond_feature_emb.bias"))
 
-    def __call__(self, codes: torch.Tensor) -> torch.Tensor:
-        """codes [B, Q, Tc] int64 (any strides with unit stride along Tc) -> [B * Tc, dim]."""
+    def __call__(self, codes: torch.Tensor, clamp: bool = False) -> torch.Tensor:
+        """codes [B, Q, Tc] int64 (any strides with unit stride along Tc) -> [B * Tc, dim].
+        ``clamp``: codes clamped to [0, V - 1] first (codec_lite.decode); otherwise -1 and
+        out-of-range codes contribute nothing (get_codes_from_indices' padding)."""
         B, Q, Tc = codes.shape
         if Q != self.Q or codes.dtype != torch.int64 or codes.stride(2) != 1:
             raise ValueError(f"codes must be int64 [B, {self.Q}, Tc] with unit stride in time")
@@ -389,7 +393,8 @@ class CodeEmbedding:
         st = stream_ptr(self.dev)
         e = torch.empty(B * Tc, self.Wp, device=self.dev, dtype=torch.float16)
         _ffi.call("ecd_codec_vq_embed", codes.data_ptr(), codes.stride(0), codes.stride(1),
-                  self.books.data_ptr(), e.data_ptr(), B, Q, Tc, self.V, self.Dc, self.Wp, st)
+                  self.books.data_ptr(), e.data_ptr(), B, Q, Tc, self.V, self.Dc, self.Wp,
+                  int(clamp), st)
         h = self.project_out(e, torch.empty(B * Tc, self.dim, device=self.dev, dtype=torch.float16))
         return self.cond(h, torch.empty_like(h))
 
@@ -408,7 +413,7 @@ def t_span(num_steps: int) -> np.ndarray:
 def inference_codes(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.Tensor,
                     true_latents: torch.Tensor, latent_length: int, incontext_length: int,
                     guidance_scale: float = 2.0, num_steps: int = 20, scenario: str = "start_seg",
-                    noise: torch.Tensor | None = None) -> torch.Tensor:
+                    noise: torch.Tensor | None = None, clamp: bool = False) -> torch.Tensor:
     """FlowMatching.inference_codes (flow_matching.py:72-159): codes [B, Q, Tc] -> latents
     [B, 2 Tc, latent_dim] fp16.  ``noise`` is the initial latent sample (the reference draws it
     with torch.randn on its global generator); drawn from torch's device generator when None.
@@ -419,7 +424,7 @@ def inference_codes(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.Tens
     if latent_length != T:
         raise NotImplementedError("frames past latent_length (zero_cond rows) are not built")
     dev = est.dev
-    mu = emb(codes).view(B, Tc, emb.dim)
+    mu = emb(codes, clamp=clamp).view(B, Tc, emb.dim)
     x = (noise if noise is not None else torch.randn(B, T, C, device=dev)).to(
         device=dev, dtype=torch.float16).contiguous()
     L = int(incontext_length) if scenario == "other_seg" else 0
@@ -428,6 +433,51 @@ def inference_codes(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.Tens
         ic[:, :L] = true_latents[:, :L].to(device=dev, dtype=torch.float16)
     return solve_euler(est, x, ic, L, t_span(num_steps), mu, guidance_scale,
                        copy_incontext=True, mu_rep=2)
+
+
+def detokenize_latents(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.Tensor,
+                       duration: float = 29.76, num_steps: int = 10,
+                       guidance_scale: float = 1.25, randn=None) -> list:
+    """The latent half of HeartCodec.detokenize (modeling_heartcodec.py:57-167) with
+    codec_lite.decode's clamp of the codes (app/codec_lite.py:71): codes [Q, Tc] -> the latents
+    [1, 25 duration, latent_dim] of every overlapping window, each later window continuing the
+    previous one's last frames in context.  ``randn(shape)`` draws each window's initial sample
+    (the only draw that reaches the output: the reference's other draws are masked to zero).
+    The waveform decoder (ScalarModel) is not part of this build."""
+    dev = est.dev
+    if randn is None:
+        randn = lambda shape: torch.randn(*shape, device=dev)
+    codes = codes.unsqueeze(0).to(dev)
+    C = est.cout
+    min_samples = int(duration * 12.5)
+    hop = min_samples // 93 * 80
+    ovlp_samples = min_samples - hop
+    ovlp_frames = ovlp_samples * 2
+    if codes.shape[-1] < min_samples:
+        while codes.shape[-1] < min_samples:
+            codes = torch.cat([codes, codes], -1)
+        codes = codes[:, :, :min_samples]
+    codes_len = codes.shape[-1]
+    if (codes_len - ovlp_frames) % hop > 0:   # the reference tests with ovlp_frames here
+        len_codes = math.ceil((codes_len - ovlp_samples) / float(hop)) * hop + ovlp_samples
+        while codes.shape[-1] < len_codes:
+            codes = torch.cat([codes, codes], -1)
+        codes = codes[:, :, :len_codes]
+    latent_length = int(duration * 25)
+    out = []
+    for sinx in range(0, codes.shape[-1] - hop + 1, hop):
+        win = codes[:, :, sinx:sinx + min_samples].contiguous()
+        noise = randn((1, latent_length, C))
+        if sinx == 0 or ovlp_frames == 0:
+            true_latent = torch.zeros(1, latent_length, C, device=dev, dtype=torch.float16)
+            L = 0
+        else:
+            true_latent = torch.zeros(1, latent_length, C, device=dev, dtype=torch.float16)
+            true_latent[:, :ovlp_frames] = out[-1][:, -ovlp_frames:]
+            L = ovlp_frames
+        out.append(inference_codes(emb, est, win, true_latent, latent_length, L, guidance_scale,
+                                   num_steps, "other_seg", noise=noise, clamp=True))
+    return out
 
 
 def random_state_dict(num_attention_heads=24, attention_head_dim=64, in_channels=1024,

@@ -248,12 +248,13 @@ __global__ __launch_bounds__(256) void codec_cols3_kernel(ColSegs sg, f16* __res
 // ---------------------------------------------------------------- code embedding
 // out[b * Tc + t, d] = fp16(sum_q codebooks[q, codes[b, q, t], d]) for d < Dc (fp32 sum in
 // quantizer order), zero for Dc <= d < Wp: ResidualVQ.get_codes_from_indices then the sum over
-// quantizers (flow_matching.py:98-99).  A code of -1 (the library's padding) or any code
-// outside [0, V) contributes nothing.  codes [B, Q, Tc] int64 with strides (cb, cq, 1).  One
-// thread per (row, 8 dims).
+// quantizers (flow_matching.py:98-99).  clamp 0: a code of -1 (the library's padding) or any
+// code outside [0, V) contributes nothing; clamp 1: codes are first clamped to [0, V - 1], as
+// codec_lite.decode does before detokenizing (app/codec_lite.py:71).  codes [B, Q, Tc] int64
+// with strides (cb, cq, 1).  One thread per (row, 8 dims).
 __global__ __launch_bounds__(256) void codec_vq_embed_kernel(
     const int64_t* __restrict__ codes, long cb, long cq, const f16* __restrict__ books,
-    f16* __restrict__ out, int B, int Q, int Tc, int V, int Dc, int Wp) {
+    f16* __restrict__ out, int B, int Q, int Tc, int V, int Dc, int Wp, int clamp) {
   const long n = (long)B * Tc * (Wp >> 3);
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
     const int dv = (int)(i % (Wp >> 3)) * 8;
@@ -262,7 +263,8 @@ __global__ __launch_bounds__(256) void codec_vq_embed_kernel(
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (dv < Dc) {
       for (int qq = 0; qq < Q; ++qq) {
-        const int64_t c = codes[b * cb + qq * cq + t];
+        int64_t c = codes[b * cb + qq * cq + t];
+        if (clamp) c = c < 0 ? 0 : (c >= V ? V - 1 : c);
         if (c < 0 || c >= V) continue;
         const f16x8 e = *(const f16x8*)(books + ((long)qq * V + c) * Dc + dv);
 #pragma unroll
@@ -429,13 +431,14 @@ int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* s
 }
 
 int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books, void* out,
-                       int B, int Q, int Tc, int V, int Dc, int Wp, void* stream) {
+                       int B, int Q, int Tc, int V, int Dc, int Wp, int clamp, void* stream) {
   if (!codes || !books || !out || B <= 0 || Q <= 0 || Tc <= 0 || V <= 0 || Dc <= 0 || (Dc & 7) ||
+      (clamp != 0 && clamp != 1) ||
       Wp < Dc || (Wp & 7) || cb < 0 || cq < 0 || !a16(books) || !a16(out))
     return ECD_EINVAL;
   hipLaunchKernelGGL(codec_vq_embed_kernel, dim3(grid_for((long)B * Tc * (Wp / 8))), dim3(256), 0,
                      (hipStream_t)stream, codes, cb, cq, (const f16*)books, (f16*)out, B, Q, Tc,
-                     V, Dc, Wp);
+                     V, Dc, Wp, clamp);
   return ecd_launch_status();
 }
 

@@ -265,9 +265,10 @@ int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* s
 /* Code embedding: out [B*Tc, Wp] fp16, out[b*Tc + t, d] = fp16(sum_q books[q, codes[b, q, t], d])
  * for d < Dc, zero for Dc <= d < Wp (ResidualVQ.get_codes_from_indices and the sum over
  * quantizers, flow_matching.py:98-99); books [Q, V, Dc] fp16; codes int64 at
- * codes[b*cb + q*cq + t]; codes -1 or outside [0, V) contribute nothing.  Dc, Wp % 8 == 0. */
+ * codes[b*cb + q*cq + t].  clamp 0: codes -1 or outside [0, V) contribute nothing; clamp 1:
+ * codes are clamped to [0, V - 1] first (app/codec_lite.py:71).  Dc, Wp % 8 == 0. */
 int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books, void* out,
-                       int B, int Q, int Tc, int V, int Dc, int Wp, void* stream);
+                       int B, int Q, int Tc, int V, int Dc, int Wp, int clamp, void* stream);
 
 /* Timestep sinusoid out [n, 512] fp16 from t [n] fp32 (PixArtAlphaCombinedFlowEmbeddings.
  * timestep_embedding, transformer.py:408-426). */

@@ -353,3 +353,38 @@ def random_vq_weights(num_quantizers: int, codebook_size: int, codebook_dim: int
     p["cond_feature_emb.bias"] = f16(g.standard_normal(dim) * 0.02)
     p["zero_cond_embedding1"] = f16(g.standard_normal(dim))
     return p
+
+
+def detokenize_latents(p_fm: dict, p_est: dict, cfg: dict, codes, duration: float,
+                       num_steps: int, guidance_scale: float, noises) -> list:
+    """The latent half of HeartCodec.detokenize (modeling_heartcodec.py:57-167) after
+    codec_lite.decode's clamp to [0, 8191] (app/codec_lite.py:71; here [0, V - 1]): codes [Q, Tc]
+    -> one latent window per hop.  ``noises`` are the windows' initial samples in order."""
+    V = np.asarray(p_fm["vq_embed.layers.0._codebook.embed"]).shape[-2]
+    codes = np.clip(np.asarray(codes, np.int64), 0, V - 1)[None]
+    min_samples = int(duration * 12.5)
+    hop = min_samples // 93 * 80
+    ovlp_samples = min_samples - hop
+    ovlp_frames = ovlp_samples * 2
+    if codes.shape[-1] < min_samples:
+        while codes.shape[-1] < min_samples:
+            codes = np.concatenate([codes, codes], -1)
+        codes = codes[:, :, :min_samples]
+    if (codes.shape[-1] - ovlp_frames) % hop > 0:
+        len_codes = math.ceil((codes.shape[-1] - ovlp_samples) / float(hop)) * hop + ovlp_samples
+        while codes.shape[-1] < len_codes:
+            codes = np.concatenate([codes, codes], -1)
+        codes = codes[:, :, :len_codes]
+    latent_length = int(duration * 25)
+    C = cfg["out_channels"]
+    out = []
+    for w, sinx in enumerate(range(0, codes.shape[-1] - hop + 1, hop)):
+        win = codes[:, :, sinx:sinx + min_samples]
+        true_latent = np.zeros((1, latent_length, C), np.float16)
+        L = 0
+        if sinx != 0 and ovlp_frames != 0:
+            true_latent[:, :ovlp_frames] = out[-1][:, -ovlp_frames:]
+            L = ovlp_frames
+        out.append(inference_codes(p_fm, p_est, cfg, win, true_latent, latent_length, L,
+                                   guidance_scale, num_steps, "other_seg", noises[w]))
+    return out

@@ -74,8 +74,9 @@ def test_signatures_match_header_arity():
     lambda L: L.ecd_codec_norm_mod(16, None, None, None, 0, None, 16, 16, 16, 16, 0, 16, 8, 8,
                                    64, 0, 1e-6, None),                              # RMS, no w
     lambda L: L.ecd_codec_cols3(None, None, None, None, None, None, 1, 16, 1, 8, None),
-    lambda L: L.ecd_codec_vq_embed(16, 8, 1, 16, 16, 1, 8, 10, 8192, 30, 64, None),  # Dc % 8
-    lambda L: L.ecd_codec_vq_embed(16, 8, 1, 16, 16, 1, 8, 10, 8192, 32, 24, None),  # Wp < Dc
+    lambda L: L.ecd_codec_vq_embed(16, 8, 1, 16, 16, 1, 8, 10, 8192, 30, 64, 0, None),  # Dc % 8
+    lambda L: L.ecd_codec_vq_embed(16, 8, 1, 16, 16, 1, 8, 10, 8192, 32, 24, 0, None),  # Wp < Dc
+    lambda L: L.ecd_codec_vq_embed(16, 8, 1, 16, 16, 1, 8, 10, 8192, 32, 64, 2, None),  # clamp 2
     lambda L: L.ecd_codec_timestep(None, 16, 1, None),
     lambda L: L.ecd_codec_silu(16, 16, 0, None),
     lambda L: L.ecd_codec_euler(16, 16, 16, 16, 2, 1, 8, 256, 0, 0.1, 1.2, 0.0, 0, None),  # cfg 2

@@ -314,15 +314,16 @@ def test_codec_vq_embed(dev):
     ct = D_(codes_full, dev)[:, :, 5:5 + Tc]
     out = torch.full((B * Tc, Wp), 9.0, dtype=torch.float16, device=dev)
     bt = D_(books, dev)
-    _call("ecd_codec_vq_embed", ct.data_ptr(), ct.stride(0), ct.stride(1), bt.data_ptr(),
-          out.data_ptr(), B, Q, Tc, V, Dc, Wp)
-    want = np.zeros((B, Tc, Wp))
-    for q in range(Q):
-        idx = win[:, q]
-        ok = (idx >= 0) & (idx < V)
-        want[..., :Dc] += books[q].astype(np.float64)[np.where(ok, idx, 0)] * ok[..., None]
-    assert_close16(N_(out), f16(want).reshape(B * Tc, Wp), what="vq embed")
-    assert np.all(N_(out)[:, Dc:] == 0)
+    for clamp in (0, 1):
+        _call("ecd_codec_vq_embed", ct.data_ptr(), ct.stride(0), ct.stride(1), bt.data_ptr(),
+              out.data_ptr(), B, Q, Tc, V, Dc, Wp, clamp)
+        want = np.zeros((B, Tc, Wp))
+        for q in range(Q):
+            idx = np.clip(win[:, q], 0, V - 1) if clamp else win[:, q]
+            ok = (idx >= 0) & (idx < V)
+            want[..., :Dc] += books[q].astype(np.float64)[np.where(ok, idx, 0)] * ok[..., None]
+        assert_close16(N_(out), f16(want).reshape(B * Tc, Wp), what=f"vq embed clamp={clamp}")
+        assert np.all(N_(out)[:, Dc:] == 0)
 
 
 def _code_embedding(dev, p):
@@ -359,3 +360,29 @@ def test_codec_inference_codes(dev, scenario, L_ic):
     _close_model(N_(got), want, f"inference_codes {scenario}")
     if L_ic:
         _exact(N_(got)[:, :L_ic], true_lat[:, :L_ic], "in-context prefix copied")
+
+
+def test_codec_detokenize_latents(dev):
+    """The window loop of detokenize up to the latents: 250 codes at a 7.44 s window (93 codes,
+    hop 80, overlap 13 codes = 26 frames) are padded to 253 by repetition and decoded as three
+    windows, each later one continuing the previous window's last 26 frames; codes outside the
+    codebook are clamped."""
+    import torch
+    from estudiocanciones_amd.codec import detokenize_latents
+    p_est = OC.random_weights(TINY, seed=40)
+    p_fm = OC.random_vq_weights(8, 64, 32, 64, seed=41)
+    est = _estimator(dev, p_est, TINY)
+    emb = _code_embedding(dev, p_fm)
+    codes = rng(42).integers(0, 64, (8, 250))
+    codes[2, 17] = 70
+    codes[5, 100] = -4
+    duration, frames = 7.44, 186
+    noises = [randn16(43 + w, 1, frames, 64) for w in range(3)]
+    it = iter(noises)
+    got = detokenize_latents(emb, est, D_(codes, dev), duration, 2, 1.25,
+                             randn=lambda shape: D_(next(it), dev))
+    want = OC.detokenize_latents(p_fm, p_est, TINY, codes, duration, 2, 1.25, noises)
+    assert len(got) == len(want) == 3
+    for w, (g, wv) in enumerate(zip(got, want)):
+        _close_model(N_(g), wv, f"detokenize window {w}")
+    _exact(N_(got[1])[:, :26], N_(got[0])[:, -26:], "window 1 continues window 0")
