@@ -11,9 +11,11 @@ with N(0, 1) values; everything resident in HBM before the timed region.
 Prints one JSON line: frames/s (value), the GEMV roofline (hipEvent-timed launches of one
 frame's GEMV sequence, algorithmic bytes N*K + 2N + 2MK + 2MN (+2MN residual) per launch),
 the same frame at a second KV length (``target_point``, default 4096: frames/s and the HBM
-fractions of the GEMV family and the decode attention there), the prompt pass, and a CPU
-baseline: the reference's CPU path (numpy float32 restatement) timed on a bounded sample of
-layers on the host cores and scaled to a frame.
+fractions of the GEMV family and the decode attention there), the prompt pass, one codec
+detokenize window from codes to latents (``codec_window``: code embedding + 10 CFG Euler steps
+of the 30-layer flow-matching estimator at 744 frames), and a CPU baseline: the reference's CPU
+path (numpy float32 restatement) timed on a bounded sample of layers on the host cores and
+scaled to a frame.
 
     python bench.py [--steps K] [--warmup W] [--kv 750] [--target-kv 4096] [--decoder 1024|ref]
                     [--no-cpu]
@@ -393,31 +395,36 @@ def main():
 
 
 def measure_codec(torch, dev, steps, seed):
-    """One detokenize window of the codec's flow-matching estimator: 24 + 6 layers (dim 1536 /
-    3072, 24 heads), batch 1 doubled by CFG, 744 latent frames (29.76 s), ``steps`` Euler steps
-    with guidance 1.25, random-init fp16 weights, inputs resident on the GPU."""
-    import numpy as np
+    """One detokenize window of the codec, codes to latents: 372 codes x 8 quantizers -> code
+    embedding -> the flow-matching estimator (24 + 6 layers, dim 1536 / 3072, 24 heads), batch 1
+    doubled by CFG, 744 latent frames (29.76 s), ``steps`` Euler steps with guidance 1.25,
+    random-init fp16 weights, codes and noise resident on the GPU."""
     from estudiocanciones_amd import codec as C
     sd = C.random_state_dict(device=dev, seed=seed + 7)
     est = C.LlamaTransformer(sd, device=dev)
     del sd
+    emb = C.CodeEmbedding(C.random_code_embedding_state_dict(device=dev, seed=seed + 9), device=dev)
     B, T = 1, 744
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 8)
-    x = torch.randn(B, T, 256, generator=g, device=dev).half()
-    ic = torch.zeros(B, T, 256, device=dev, dtype=torch.float16)
-    mu = torch.randn(B, T, 512, generator=g, device=dev).half()
-    ts = np.linspace(0, 1, steps + 1).astype(np.float32)
-    C.solve_euler(est, x, ic, 0, ts, mu, 1.25)
+    codes = torch.randint(0, 8192, (B, 8, T // 2), generator=g, device=dev)
+    noise = torch.randn(B, T, 256, generator=g, device=dev).half()
+    true_lat = torch.zeros(B, T, 256, device=dev, dtype=torch.float16)
+    run = lambda: C.inference_codes(emb, est, codes, true_lat, T, 0, 1.25, steps, "other_seg",
+                                    noise=noise, clamp=True)
+    run()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    out = C.solve_euler(est, x, ic, 0, ts, mu, 1.25)
+    out = run()
     e1.record()
     torch.cuda.synchronize()
     win_ms = e0.elapsed_time(e1)
     if not bool(torch.isfinite(out).all()):
         raise RuntimeError("codec window produced non-finite latents")
+    x = noise
+    ic = true_lat
+    mu = torch.randn(B, T, 512, generator=g, device=dev).half()
     tm = est.timestep_vectors(torch.tensor([0.5], device=dev))
     segs = [(x.view(T, 256), 256, B, 0), (ic.view(T, 256), 256, B, 0), (mu.view(T, 512), 512, B, B)]
     reps = 10
@@ -431,17 +438,19 @@ def measure_codec(torch, dev, steps, seed):
     del est
     torch.cuda.empty_cache()
     return {
-        "workload": ("codec flow-matching estimator (24 + 6 LlamaTransformer layers, dim 1536 / "
-                     "3072, 24 heads, hd 64 / 128), batch 1 x CFG 2, 744 latent frames (one "
-                     f"29.76 s window), {steps} Euler steps, guidance 1.25, fp16"),
+        "workload": ("codec detokenize window, codes to latents: 372 x 8 codes -> ResidualVQ "
+                     "embedding -> flow-matching estimator (24 + 6 LlamaTransformer layers, dim "
+                     "1536 / 3072, 24 heads, hd 64 / 128), batch 1 x CFG 2, 744 latent frames "
+                     f"(29.76 s), {steps} Euler steps, guidance 1.25, fp16"),
         "window_ms": round(win_ms, 2),
         "latent_frames_per_s": round(T * B / (win_ms / 1e3), 1),
         "estimator_call_ms": round(call_ms, 3),
         "estimator_flops": int(fl["total"]),
         "estimator_TFLOPs": round(fl["total"] / call_ms / 1e9, 1),
         "frac_of_mfma_f16_peak": round(fl["total"] / call_ms / 1e9 / 2500.0, 4),
-        "path": ("fp16 MFMA GEMM (packed weights, fused bias / scale / SiLU-mul epilogues), MFMA "
-                 "flash attention, fused gated-residual + adaLN norms, CFG Euler kernel"),
+        "path": ("code gather-sum kernel + fp16 MFMA GEMM (packed weights, fused bias / scale / "
+                 "SiLU-mul epilogues), MFMA flash attention, fused gated-residual + adaLN norms, "
+                 "CFG Euler kernel"),
     }
 
 

@@ -32,7 +32,7 @@ from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_a
                       stream_ptr)
 
 __all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes",
-           "detokenize_latents", "mlp_hidden",
+           "detokenize_latents", "random_code_embedding_state_dict", "mlp_hidden",
            "euler_times", "t_span", "random_state_dict", "estimator_flops"]
 
 EPS = 1e-6
@@ -530,6 +530,23 @@ def random_state_dict(num_attention_heads=24, attention_head_dim=64, in_channels
     proj("proj_out", out_channels, D2)
     ada("adaln_single.", D)
     ada("adaln_single_2.", D2)
+    return sd
+
+
+def random_code_embedding_state_dict(num_quantizers=8, codebook_size=8192, codebook_dim=32,
+                                     dim=512, device="cuda", seed=0):
+    """Random fp16 code-embedding weights under the reference's names (relative to
+    ``flow_matching.``), drawn on the device."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *shape, scale: (torch.randn(*shape, generator=g, device=dev) * scale).half()
+    sd = {f"vq_embed.layers.{q}._codebook.embed": rnd(1, codebook_size, codebook_dim, scale=0.5)
+          for q in range(num_quantizers)}
+    sd["vq_embed.project_out.weight"] = rnd(dim, codebook_dim, scale=codebook_dim ** -0.5)
+    sd["vq_embed.project_out.bias"] = rnd(dim, scale=0.02)
+    sd["cond_feature_emb.weight"] = rnd(dim, dim, scale=dim ** -0.5)
+    sd["cond_feature_emb.bias"] = rnd(dim, scale=0.02)
+    sd["zero_cond_embedding1"] = rnd(dim, scale=1.0)
     return sd
 
 
