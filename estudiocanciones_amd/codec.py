@@ -32,7 +32,8 @@ from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_a
                       stream_ptr)
 
 __all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes",
-           "detokenize_latents", "random_code_embedding_state_dict", "mlp_hidden",
+           "detokenize_latents", "ScalarDecoder", "random_code_embedding_state_dict",
+           "mlp_hidden",
            "euler_times", "t_span", "random_state_dict", "estimator_flops"]
 
 EPS = 1e-6
@@ -531,6 +532,158 @@ def random_state_dict(num_attention_heads=24, attention_head_dim=64, in_channels
     ada("adaln_single.", D)
     ada("adaln_single_2.", D2)
     return sd
+
+
+class _Conv:
+    """One Conv1d (optionally weight-normed) as a GEMM over tap columns: W'[o, j*Cin + c] =
+    weight[o, c, j], taps (j - k + 1) * dilation (causal) or j - (k - 1) / 2 (centred)."""
+
+    def __init__(self, w, b, offsets, prelu=None):
+        self.cout, self.cin, k = w.shape
+        self.off = (ctypes.c_int * k)(*offsets)
+        self.k = k
+        self.lin = _Linear(w.permute(0, 2, 1).reshape(self.cout, k * self.cin).contiguous(), b)
+        self.prelu = prelu
+
+
+class _ConvT:
+    """A causal ConvTranspose1d (kernel 2s, stride s, trailing s outputs dropped) as a GEMM over
+    the tap columns [x[i], x[i - 1]]: output phase p of input step i is
+    W[:, :, p]^T x[i] + W[:, :, p + s]^T x[i - 1], so W'[p*Cout + o, c] = weight[c, o, p],
+    W'[p*Cout + o, Cin + c] = weight[c, o, p + s], and the [T, s*Cout] product is the upsampled
+    [T*s, Cout] sequence."""
+
+    def __init__(self, w, b, stride):
+        self.cin, self.cout, k = w.shape
+        if k != 2 * stride:
+            raise ValueError("causal ConvTranspose1d needs kernel 2 * stride")
+        self.s = stride
+        wt = torch.cat([w[:, :, :stride], w[:, :, stride:]], 0)      # [2 Cin, Cout, s]
+        wt = wt.permute(2, 1, 0).reshape(stride * self.cout, 2 * self.cin).contiguous()
+        self.off = (ctypes.c_int * 2)(0, -1)
+        self.k = 2
+        self.prelu = None
+        self.lin = _Linear(wt, b.repeat(stride))
+
+
+class ScalarDecoder:
+    """ScalarModel.decode (app/heartcodec/models/sq_codec.py:380-526) on the GPU, time-major:
+    round(9 x) / 9 of the latent, a centred Conv1d (kernel 5), five ResDecoderBlocks (causal
+    ConvTranspose1d upsampling, then five ResidualUnits: dilated causal conv -> PReLU -> 1x1
+    conv -> PReLU -> + x), the PostProcessor (2x repeat, causal conv, PReLU) and a causal
+    Conv1d to the waveform.  Weight-normed weights are folded once at load (ecd_codec_weight_norm).
+
+    ``sd`` maps the reference's names relative to ``scalar_model.`` (``decoder.0.parametrizations.
+    weight.original0`` / ``original1``, or ``weight_g`` / ``weight_v``; ``decoder.N.bias``, ...)."""
+
+    ROWS_BYTES = 512 << 20      # tap-column chunk per GEMM call
+
+    def __init__(self, sd: dict, latent_hidden_dim=128, init_channel=64,
+                 upsample_factors=(5, 4, 4, 4, 3), upsample_kernel_sizes=(10, 8, 8, 8, 6),
+                 default_kernel_size=7, delay_kernel_size=5, res_kernel_size=7, num_samples=2,
+                 num_bands=1, device="cuda"):
+        self.dev = torch.device(device)
+        if num_samples != 2:
+            raise NotImplementedError("the PostProcessor is built for num_samples 2")
+        get = lambda n: sd[n].to(device=self.dev, dtype=torch.float16).contiguous()
+        st = stream_ptr(self.dev)
+
+        def wn(pre):
+            """The folded weight of a weight-normed layer (or the plain weight)."""
+            if pre + "weight" in sd:
+                return get(pre + "weight")
+            g = sd.get(pre + "parametrizations.weight.original0", sd.get(pre + "weight_g"))
+            v = sd.get(pre + "parametrizations.weight.original1", sd.get(pre + "weight_v"))
+            g = g.to(device=self.dev, dtype=torch.float16).contiguous()
+            v = v.to(device=self.dev, dtype=torch.float16).contiguous()
+            w = torch.empty_like(v)
+            _ffi.call("ecd_codec_weight_norm", v.data_ptr(), g.data_ptr(), w.data_ptr(),
+                      v.shape[0], v[0].numel(), st)
+            return w
+
+        def prelu(pre):
+            return float(sd[pre + "weight"].float().reshape(-1)[0])
+
+        k0 = delay_kernel_size
+        self.latent_dim = latent_hidden_dim
+        self.conv0 = _Conv(wn("decoder.0."), get("decoder.0.bias"),
+                           [j - (k0 - 1) // 2 for j in range(k0)])
+        self.blocks = []
+        for i, s in enumerate(upsample_factors):
+            pre = f"decoder.{1 + i}."
+            up = _ConvT(wn(pre + "up_conv.layer."), get(pre + "up_conv.layer.bias"), s)
+            if upsample_kernel_sizes[i] != 2 * s:
+                raise ValueError("upsample kernel must be 2 * factor (causal)")
+            units = []
+            for u, d in enumerate((1, 3, 5, 7, 9)):
+                q = f"{pre}convs.{u}."
+                kr = res_kernel_size
+                c1 = _Conv(wn(q + "conv1."), get(q + "conv1.bias"),
+                           [(j - kr + 1) * d for j in range(kr)], prelu(q + "activation1."))
+                c2 = _Conv(wn(q + "conv2."), get(q + "conv2.bias"), [0], prelu(q + "activation2."))
+                units.append((c1, c2))
+            self.blocks.append((up, units))
+        n_post = 1 + len(upsample_factors)
+        kd = default_kernel_size
+        causal = [j - kd + 1 for j in range(kd)]
+        self.post = _Conv(get(f"decoder.{n_post}.conv.weight"), get(f"decoder.{n_post}.conv.bias"),
+                          causal, prelu(f"decoder.{n_post}.activation."))
+        self.final = _Conv(wn(f"decoder.{n_post + 1}."), get(f"decoder.{n_post + 1}.bias"), causal)
+        self.num_bands = num_bands
+
+    @classmethod
+    def from_codec_state_dict(cls, sd: dict, prefix="scalar_model.", **cfg):
+        return cls({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}, **cfg)
+
+    def _conv(self, cv, x, B, T, rep=1, res=None, out=None):
+        """cv over x [B * T / rep, Cin] (time-major) -> [B * T, N] in row chunks."""
+        st = stream_ptr(self.dev)
+        lin = cv.lin
+        K = lin.K
+        M = B * T
+        y = out if out is not None else torch.empty(M, lin.N, device=self.dev, dtype=torch.float16)
+        step = max(256, self.ROWS_BYTES // (2 * K)) // 256 * 256
+        direct = cv.k == 1 and cv.off[0] == 0 and rep == 1     # a 1x1 conv reads x itself
+        cols = None if direct else torch.empty(min(step, M) * K, device=self.dev, dtype=torch.float16)
+        for r0 in range(0, M, step):
+            n = min(step, M - r0)
+            if direct:
+                c = x[r0:r0 + n]
+            else:
+                c = cols[:n * K].view(n, K)
+                _ffi.call("ecd_codec_cols_taps", x.data_ptr(), x.stride(0), cv.off, cv.k,
+                          c.data_ptr(), B, T, lin.K // cv.k, rep, r0, n, st)
+            yr = y[r0:r0 + n]
+            rr = res[r0:r0 + n] if res is not None else None
+            if getattr(cv, "prelu", None) is not None:
+                _ffi.call("ecd_gemm_f16p_prelu", c.data_ptr(), c.stride(0), lin.wp.data_ptr(),
+                          lin.b.data_ptr() if lin.b is not None else None, cv.prelu,
+                          rr.data_ptr() if rr is not None else None, rr.stride(0) if rr is not None else 0,
+                          yr.data_ptr(), yr.stride(0), n, lin.N, K, st)
+            else:
+                lin(c, yr, res=rr)
+        return y
+
+    def decode(self, latent: torch.Tensor) -> torch.Tensor:
+        """latent [1, T, S * latent_dim] fp16 (one window) -> waveform [S, T * up, num_bands]
+        fp16, S = the channel groups (the two stereo channels), up = prod(factors) * 2."""
+        _, T, W = latent.shape
+        S = W // self.latent_dim
+        st = stream_ptr(self.dev)
+        lat = latent.to(self.dev, torch.float16).contiguous()
+        x = torch.empty(S * T, self.latent_dim, device=self.dev, dtype=torch.float16)
+        _ffi.call("ecd_codec_latent_split", lat.data_ptr(), x.data_ptr(), T, S, self.latent_dim, st)
+        x = self._conv(self.conv0, x, S, T)
+        for up, units in self.blocks:
+            x = self._conv(up, x, S, T).view(S * T * up.s, up.cout)
+            T *= up.s
+            for c1, c2 in units:
+                h = self._conv(c1, x, S, T)
+                x = self._conv(c2, h, S, T, res=x)
+        x = self._conv(self.post, x, S, 2 * T, rep=2)
+        T *= 2
+        y = self._conv(self.final, x, S, T)
+        return y.view(S, T, -1)
 
 
 def random_code_embedding_state_dict(num_quantizers=8, codebook_size=8192, codebook_dim=32,

@@ -278,6 +278,77 @@ __global__ __launch_bounds__(256) void codec_vq_embed_kernel(
   }
 }
 
+// ---------------------------------------------------------------- waveform decoder glue
+// Tap offsets of one convolution (up to 8 taps).
+struct Taps {
+  int off[8];
+  int k;
+};
+
+// Tap columns, time-major, for global rows row0 .. row0 + nrows - 1 (row = b * T + t):
+// out[row - row0, j * C + c] = src[b, (t + off[j]) / rep, c] when 0 <= t + off[j] < T, else 0.  src [B, T / rep, C] with row stride ld.  A Conv1d of kernel k
+// and dilation d is the GEMM of these columns with W'[o, j * C + c] = weight[o, c, j]:
+// causal (sq_codec.py:32-73) off[j] = (j - k + 1) d; centred off[j] = j - (k - 1) / 2; the causal
+// ConvTranspose1d (kernel 2s, stride s, sq_codec.py:76-117) uses taps {0, -1}; rep 2 is the
+// PostProcessor's nearest 2x repeat (sq_codec.py:140-146).  One thread per 16-byte piece.
+__global__ __launch_bounds__(256) void codec_cols_taps_kernel(const f16* __restrict__ src, long ld,
+                                                              Taps tp, f16* __restrict__ out,
+                                                              int T, int C, int rep, long row0,
+                                                              long nrows) {
+  const int vpr = tp.k * C >> 3;  // 16-byte pieces per output row
+  const long n = nrows * vpr;
+  const int Ts = T / rep;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const long lr = i / vpr;
+    const int v = (int)(i - lr * vpr);
+    const long row = row0 + lr;
+    const int e = v * 8, j = e / C, c = e - j * C;
+    const int b = (int)(row / T), t = (int)(row - (long)b * T);
+    const int u = t + tp.off[j];
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (u >= 0 && u < T) val = *(const u32x4*)(src + ((long)b * Ts + u / rep) * ld + c);
+    *(u32x4*)(out + lr * (long)tp.k * C + e) = val;
+  }
+}
+
+// Weight normalisation of R rows of n contiguous values (dim 0 of the parametrisation:
+// a Conv1d's output channels, a ConvTranspose1d's input channels): w = fp16(v * (g / |v|)) with
+// the norm in fp32, as the fused weight-norm kernel computes it (sq_codec.py:152-160,
+// torch.nn.utils.parametrizations.weight_norm).
+__global__ __launch_bounds__(256) void codec_weight_norm_kernel(const f16* __restrict__ v,
+                                                                const f16* __restrict__ g,
+                                                                f16* __restrict__ w, int n) {
+  __shared__ float part[4];
+  const f16* vr = v + (long)blockIdx.x * n;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float a = (float)vr[i];
+    ss += a * a;
+  }
+  ss = block_sum256(ss, part);
+  const float sc = (float)g[blockIdx.x] / sqrtf(ss);
+  for (int i = threadIdx.x; i < n; i += 256) w[(long)blockIdx.x * n + i] = (f16)((float)vr[i] * sc);
+}
+
+// The latent of one window [T, S * Cl] (one batch item) split into S channel groups and
+// quantised: out[s, t, c] = fp16(fp16(round(fp16(9 x))) * fp32(1 / 9)), x = lat[t, s * Cl + c]
+// (modeling_heartcodec.py:176-183 reshape, ScalarModel.decode's round_func9,
+// sq_codec.py:368-372, 522-523; the division by 9 is a multiply by the fp32 reciprocal).
+__global__ __launch_bounds__(256) void codec_latent_split_kernel(const f16* __restrict__ lat,
+                                                                 f16* __restrict__ out, int T,
+                                                                 int S, int Cl) {
+  const long n = (long)T * S * Cl;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const int c = (int)(i % Cl);
+    const long tsr = i / Cl;
+    const int s = (int)(tsr % S);
+    const long t = tsr / S;
+    const float x9 = rnd(9.0f * (float)lat[i]);
+    const float r = __builtin_rintf(x9);  // round half to even
+    out[((long)s * T + t) * Cl + c] = (f16)mul32(r, 1.0f / 9.0f);
+  }
+}
+
 // ---------------------------------------------------------------- timestep sinusoid
 // out[n, i] = cos(a_i), out[n, 256 + i] = sin(a_i) in fp16, a_i = fp32(fp32(t[n] * f_i) * 1000),
 // f_i = exp(fp32(i * -ln 10000) * (1 / 256))  -- PixArtAlphaCombinedFlowEmbeddings
@@ -439,6 +510,35 @@ int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books
   hipLaunchKernelGGL(codec_vq_embed_kernel, dim3(grid_for((long)B * Tc * (Wp / 8))), dim3(256), 0,
                      (hipStream_t)stream, codes, cb, cq, (const f16*)books, (f16*)out, B, Q, Tc,
                      V, Dc, Wp, clamp);
+  return ecd_launch_status();
+}
+
+int ecd_codec_cols_taps(const void* src, long ld, const int* offsets, int k, void* out, int B,
+                        int T, int C, int rep, long row0, long nrows, void* stream) {
+  if (!src || !offsets || !out || k <= 0 || k > 8 || B <= 0 || T <= 0 || C <= 0 || (C & 7) ||
+      ld < C || (ld & 7) || (rep != 1 && rep != 2) || T % rep || !a16(src) || !a16(out) ||
+      row0 < 0 || nrows <= 0 || row0 + nrows > (long)B * T)
+    return ECD_EINVAL;
+  Taps tp = {};
+  tp.k = k;
+  for (int j = 0; j < k; ++j) tp.off[j] = offsets[j];
+  hipLaunchKernelGGL(codec_cols_taps_kernel, dim3(grid_for(nrows * (k * C / 8))), dim3(256), 0,
+                     (hipStream_t)stream, (const f16*)src, ld, tp, (f16*)out, T, C, rep, row0,
+                     nrows);
+  return ecd_launch_status();
+}
+
+int ecd_codec_weight_norm(const void* v, const void* g, void* w, int rows, int n, void* stream) {
+  if (!v || !g || !w || rows <= 0 || n <= 0) return ECD_EINVAL;
+  hipLaunchKernelGGL(codec_weight_norm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream,
+                     (const f16*)v, (const f16*)g, (f16*)w, n);
+  return ecd_launch_status();
+}
+
+int ecd_codec_latent_split(const void* lat, void* out, int T, int S, int Cl, void* stream) {
+  if (!lat || !out || T <= 0 || S <= 0 || Cl <= 0) return ECD_EINVAL;
+  hipLaunchKernelGGL(codec_latent_split_kernel, dim3(grid_for((long)T * S * Cl)), dim3(256), 0,
+                     (hipStream_t)stream, (const f16*)lat, (f16*)out, T, S, Cl);
   return ecd_launch_status();
 }
 

@@ -5,6 +5,9 @@
 //   EPI_SILU:  weight rows interleaved (gate row j at 2j, up row j at 2j + 1),
 //              mm[m, j] = fp16(fp16(silu(g)) * u) with g, u the fp16 GEMM outputs (LlamaMLP,
 //              transformer.py:178-181).
+//   EPI_PRELU: y = fp16(acc + bias), then nn.PReLU with one slope a: y < 0 -> fp16(a * y), then
+//              y = fp16(y + res) (the conv -> PReLU (-> + x) steps of the codec's waveform
+//              decoder, app/heartcodec/models/sq_codec.py:149-168).
 //
 // Packed weights: 16-row tiles x 64-wide K chunks of 2 KB, two 1 KB halves h; lane l's 16 bytes
 // of half h hold row l & 15, k = 64c + 16 (l >> 4) + 8h .. +7 (ecd_pack_f16), so one 16-byte
@@ -29,7 +32,7 @@
 
 namespace ecd {
 
-enum { F16_STORE = 0, F16_SILU = 1 };
+enum { F16_STORE = 0, F16_SILU = 1, F16_PRELU = 2 };
 
 // wait for every vector-memory and LDS operation of this wave (vmcnt 0, lgkmcnt 0)
 __device__ __forceinline__ void wait_vm0_lgkm0() { __builtin_amdgcn_s_waitcnt(7 << 4); }
@@ -213,9 +216,13 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         yv[r] = (f16)(acc[ft][rt][r] + bv[r]);
-        if (alpha != 1.0f) yv[r] = (f16)((float)yv[r] * alpha);
+        if (EPI == F16_PRELU) {
+          if ((float)yv[r] < 0.f) yv[r] = (f16)((float)yv[r] * alpha);  // alpha: the slope
+        } else if (alpha != 1.0f) {
+          yv[r] = (f16)((float)yv[r] * alpha);
+        }
       }
-      if (EPI == F16_STORE) {
+      if (EPI == F16_STORE || EPI == F16_PRELU) {
         if (vec && nb + 3 < N) {
           if (res) yv = yv + *(const f16x4*)(res + (long)m * ldr + nb);
           *(f16x4*)(y + (long)m * ldy + nb) = yv;
@@ -343,10 +350,11 @@ int ecd_pack_f16(const void* w, int N, int K, int interleave, void* out, void* s
 
 int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bias, float alpha,
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
-                        int silu, int cfg, void* stream) {
+                        int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || cfg < 0 || cfg > 11 || (silu != 0 && silu != 1))
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 11 || epi < 0 || epi > 2)
     return ECD_EINVAL;
+  const bool silu = epi == F16_SILU;
   if (silu) {
     if ((N % 2) || ldy < N / 2 || (ldy % 2) || ((uintptr_t)y & 3) || bias || res || alpha != 1.0f)
       return ECD_EINVAL;
@@ -357,6 +365,9 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
   if (silu)
     return launch_f16<F16_SILU>(cfg, (const f16*)x, ldx, (const f16*)wp, nullptr, 1.0f, nullptr,
                                 0, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
+  if (epi == F16_PRELU)
+    return launch_f16<F16_PRELU>(cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha,
+                                 (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
   return launch_f16<F16_STORE>(cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha,
                                (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
 }
@@ -365,6 +376,13 @@ int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, fl
                   const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                   void* stream) {
   return ecd_gemm_f16p_tuned(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, 0, 0, stream);
+}
+
+int ecd_gemm_f16p_prelu(const void* x, long ldx, const void* wp, const float* bias, float slope,
+                        const void* res, long ldr, void* y, long ldy, int M, int N, int K,
+                        void* stream) {
+  return ecd_gemm_f16p_tuned(x, ldx, wp, bias, slope, res, ldr, y, ldy, M, N, K, F16_PRELU, 0,
+                             stream);
 }
 
 int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,

@@ -209,13 +209,22 @@ int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, fl
 int ecd_gemm_f16p_silu(const void* x, long ldx, const void* wp, void* mm, long ldm, int M, int F,
                        int K, void* stream);
 
-/* ecd_gemm_f16p (silu 0) or ecd_gemm_f16p_silu (silu 1, N = 2F, bias/res NULL, alpha 1) with an
+/* The same GEMM with nn.PReLU (one slope) after the bias and rounding, then the optional fp16
+ * residual: y = fp16(acc + bias); y < 0 -> fp16(slope * y); y = fp16(y + res).  The conv ->
+ * PReLU (-> + x) steps of the codec's waveform decoder (app/heartcodec/models/sq_codec.py:
+ * 149-168), with the convolution as a GEMM over tap columns (ecd_codec_cols_taps). */
+int ecd_gemm_f16p_prelu(const void* x, long ldx, const void* wp, const float* bias, float slope,
+                        const void* res, long ldr, void* y, long ldy, int M, int N, int K,
+                        void* stream);
+
+/* ecd_gemm_f16p (epi 0), ecd_gemm_f16p_silu (epi 1, N = 2F, bias/res NULL, alpha 1) or
+ * ecd_gemm_f16p_prelu (epi 2, alpha = the slope) with an
  * explicit block tile (cfg 1..11: 128x128, 256x128, 128x256 or 128x64 features x rows, 2 or 3 LDS
  * stages; 0 = the library's choice).  Replaces nothing in the reference: the launch-shape knob
  * of the codec GEMMs, for sweeps. */
 int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bias, float alpha,
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
-                        int silu, int cfg, void* stream);
+                        int epi, int cfg, void* stream);
 
 /* Causal attention of the prompt pass on MFMA: row r = b * S + s of q [B * S, Hq * HD] attends
  * cache slots [0, pos[r]] of kc, vc [B, Hk, L, HD] (the prompt's K/V already written), with the
@@ -269,6 +278,27 @@ int ecd_codec_cols3(const void* const* seg_ptr, const long* seg_ld, const int* s
  * codes are clamped to [0, V - 1] first (app/codec_lite.py:71).  Dc, Wp % 8 == 0. */
 int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books, void* out,
                        int B, int Q, int Tc, int V, int Dc, int Wp, int clamp, void* stream);
+
+/* ---- codec waveform decoder (app/heartcodec/models/sq_codec.py ScalarModel.decode), time-major
+ * activations [B, T, C]. */
+
+/* Tap columns of a 1-D convolution for global rows row0 .. row0 + nrows - 1 (row = b*T + t):
+ * out[row - row0, j*C + c] = src[b, (t + offsets[j]) / rep, c] for 0 <= t + offsets[j] < T,
+ * else 0 (src [B, T / rep, C], row stride ld; k <= 8 taps,
+ * rep 1 or 2).  Causal Conv1d: offsets (j - k + 1) * dilation (sq_codec.py:32-73); causal
+ * ConvTranspose1d with kernel 2s, stride s (sq_codec.py:76-117): offsets {0, -1}, the GEMM's
+ * [T, s*Cout] output being the upsampled [T*s, Cout]; rep 2: PostProcessor's 2x repeat
+ * (sq_codec.py:140-146).  C % 8 == 0. */
+int ecd_codec_cols_taps(const void* src, long ld, const int* offsets, int k, void* out, int B,
+                        int T, int C, int rep, long row0, long nrows, void* stream);
+
+/* Weight normalisation (torch.nn.utils.parametrizations.weight_norm, dim 0): w[r, :] =
+ * fp16(v[r, :] * (g[r] / |v[r, :]|)), fp32 norm, rows of n contiguous values. */
+int ecd_codec_weight_norm(const void* v, const void* g, void* w, int rows, int n, void* stream);
+
+/* One window's latent lat [T, S*Cl] -> out [S, T, Cl], out[s, t, c] = round(9 x) / 9 in fp16
+ * (modeling_heartcodec.py:176-183, ScalarModel.decode's round_func9, sq_codec.py:368-372). */
+int ecd_codec_latent_split(const void* lat, void* out, int T, int S, int Cl, void* stream);
 
 /* Timestep sinusoid out [n, 512] fp16 from t [n] fp32 (PixArtAlphaCombinedFlowEmbeddings.
  * timestep_embedding, transformer.py:408-426). */

@@ -388,3 +388,131 @@ def detokenize_latents(p_fm: dict, p_est: dict, cfg: dict, codes, duration: floa
         out.append(inference_codes(p_fm, p_est, cfg, win, true_latent, latent_length, L,
                                    guidance_scale, num_steps, "other_seg", noises[w]))
     return out
+
+
+# ---------------------------------------------------------------- waveform decoder
+def weight_norm(v, g) -> np.ndarray:
+    """torch.nn.utils.parametrizations.weight_norm, dim 0: w = fp16(v * (g / |v|)), norm over
+    all but the first axis (fused kernel: fp32 norm, one rounding)."""
+    v64 = np.asarray(v, np.float16).astype(np.float64)
+    nrm = np.sqrt((v64.reshape(v64.shape[0], -1) ** 2).sum(-1))
+    sc = np.asarray(g, np.float16).astype(np.float64).reshape(-1) / nrm
+    return f16(v64 * sc.reshape((-1,) + (1,) * (v64.ndim - 1)))
+
+
+def conv1d(x, w, b, dilation: int = 1, causal: bool = True) -> np.ndarray:
+    """Conv1d of sq_codec.py:32-73 on time-major x [B, T, Cin], w [Cout, Cin, k]: causal left
+    padding (k - 1) d, else centred padding (k - 1) d / 2; the library rounds its result, then
+    the bias add rounds."""
+    a = np.asarray(x, np.float16).astype(np.float64)
+    w64 = np.asarray(w, np.float16).astype(np.float64)
+    B, T, _ = a.shape
+    k = w64.shape[2]
+    left = (k - 1) * dilation if causal else (k - 1) * dilation // 2
+    right = 0 if causal else (k - 1) * dilation - left
+    pad = np.zeros((B, T + left + right, a.shape[2]))
+    pad[:, left:left + T] = a
+    acc = sum(pad[:, j * dilation:j * dilation + T] @ w64[:, :, j].T for j in range(k))
+    return f16(f32(f16(acc)) + f32(b))
+
+
+def conv_transpose_causal(x, w, b, stride: int) -> np.ndarray:
+    """ConvTranspose1d(kernel 2s, stride s) with the trailing s outputs dropped (sq_codec.py:
+    76-117): out[i*s + j] += x[i] @ w[:, :, j]; x [B, T, Cin], w [Cin, Cout, 2s]."""
+    a = np.asarray(x, np.float16).astype(np.float64)
+    w64 = np.asarray(w, np.float16).astype(np.float64)
+    B, T, _ = a.shape
+    k = w64.shape[2]
+    out = np.zeros((B, (T - 1) * stride + k, w64.shape[1]))
+    for j in range(k):
+        out[:, j:j + (T - 1) * stride + 1:stride] += a @ w64[:, :, j]
+    out = out[:, :T * stride]
+    return f16(f32(f16(out)) + f32(b))
+
+
+def prelu(x, a: float) -> np.ndarray:
+    """nn.PReLU with one slope on fp16."""
+    x32 = f32(x)
+    return f16(np.where(x32 < 0, np.float32(a) * x32, x32))
+
+
+def round9(x) -> np.ndarray:
+    """round_func9 (sq_codec.py:368-372) on fp16: fp16(9 x) rounded half to even, then the
+    division as a multiply by the fp32 reciprocal of 9."""
+    r = np.rint(f32(f16(np.float32(9) * f32(x))))
+    return f16((r.astype(np.float32) * np.float32(1 / 9)).astype(np.float32))
+
+
+def _wn(p, pre):
+    if pre + "weight" in p:
+        return np.asarray(p[pre + "weight"], np.float16)
+    return weight_norm(p[pre + "parametrizations.weight.original1"],
+                       p[pre + "parametrizations.weight.original0"])
+
+
+def scalar_decode(p: dict, cfg: dict, latent) -> np.ndarray:
+    """ScalarModel.decode (sq_codec.py:522-526) after detokenize's stereo split
+    (modeling_heartcodec.py:176-183), time-major: latent [1, T, S * Cl] -> [S, T * up, bands].
+    cfg: latent_hidden_dim, upsample_factors."""
+    Cl = cfg["latent_hidden_dim"]
+    lat = np.asarray(latent, np.float16)[0]
+    T = lat.shape[0]
+    S = lat.shape[1] // Cl
+    x = round9(lat.reshape(T, S, Cl).transpose(1, 0, 2))
+    x = conv1d(x, _wn(p, "decoder.0."), p["decoder.0.bias"], causal=False)
+    for i, s in enumerate(cfg["upsample_factors"]):
+        pre = f"decoder.{1 + i}."
+        x = conv_transpose_causal(x, _wn(p, pre + "up_conv.layer."), p[pre + "up_conv.layer.bias"], s)
+        for u, d in enumerate((1, 3, 5, 7, 9)):
+            q = f"{pre}convs.{u}."
+            h = prelu(conv1d(x, _wn(p, q + "conv1."), p[q + "conv1.bias"], d),
+                      float(np.asarray(p[q + "activation1.weight"]).reshape(-1)[0]))
+            h = prelu(conv1d(h, _wn(p, q + "conv2."), p[q + "conv2.bias"]),
+                      float(np.asarray(p[q + "activation2.weight"]).reshape(-1)[0]))
+            x = f16(f32(h) + f32(x))
+    n = 1 + len(cfg["upsample_factors"])
+    x = np.repeat(x, 2, axis=1)
+    x = prelu(conv1d(x, p[f"decoder.{n}.conv.weight"], p[f"decoder.{n}.conv.bias"]),
+              float(np.asarray(p[f"decoder.{n}.activation.weight"]).reshape(-1)[0]))
+    return conv1d(x, _wn(p, f"decoder.{n + 1}."), p[f"decoder.{n + 1}.bias"])
+
+
+def random_decoder_weights(cfg: dict, seed: int = 0) -> dict:
+    """Random fp16 decoder weights under the reference's names (relative to ``scalar_model.``,
+    weight-normed layers as parametrization pairs).  cfg: latent_hidden_dim, init_channel,
+    upsample_factors."""
+    g = np.random.default_rng(seed)
+    p = {}
+    ups = cfg["upsample_factors"]
+    ch = lambda i: cfg["init_channel"] * 2 ** (len(ups) - i)
+
+    def wnl(pre, shape, fan):
+        v = g.standard_normal(shape)
+        p[pre + "parametrizations.weight.original1"] = f16(v)
+        nrm = np.sqrt((v.reshape(shape[0], -1) ** 2).sum(-1))
+        p[pre + "parametrizations.weight.original0"] = f16(
+            (nrm / math.sqrt(fan) * (1 + 0.1 * g.standard_normal(shape[0]))).reshape((-1, 1, 1)))
+
+    wnl("decoder.0.", (ch(0), cfg["latent_hidden_dim"], 5), cfg["latent_hidden_dim"] * 5)
+    p["decoder.0.bias"] = f16(g.standard_normal(ch(0)) * 0.02)
+    for i, s in enumerate(ups):
+        pre = f"decoder.{1 + i}."
+        wnl(pre + "up_conv.layer.", (ch(i), ch(i + 1), 2 * s), ch(i) * 2)
+        p[pre + "up_conv.layer.bias"] = f16(g.standard_normal(ch(i + 1)) * 0.02)
+        c = ch(i + 1)
+        for u in range(5):
+            q = f"{pre}convs.{u}."
+            wnl(q + "conv1.", (c, c, 7), c * 7 * 4)
+            p[q + "conv1.bias"] = f16(g.standard_normal(c) * 0.02)
+            wnl(q + "conv2.", (c, c, 1), c * 4)
+            p[q + "conv2.bias"] = f16(g.standard_normal(c) * 0.02)
+            p[q + "activation1.weight"] = f16([0.25])
+            p[q + "activation2.weight"] = f16([0.2])
+    n = 1 + len(ups)
+    c = cfg["init_channel"]
+    p[f"decoder.{n}.conv.weight"] = f16(g.standard_normal((c, c, 7)) / math.sqrt(c * 7))
+    p[f"decoder.{n}.conv.bias"] = f16(g.standard_normal(c) * 0.02)
+    p[f"decoder.{n}.activation.weight"] = f16([0.25])
+    wnl(f"decoder.{n + 1}.", (1, c, 7), c * 7)
+    p[f"decoder.{n + 1}.bias"] = f16(g.standard_normal(1) * 0.02)
+    return p

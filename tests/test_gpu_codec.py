@@ -386,3 +386,90 @@ def test_codec_detokenize_latents(dev):
     for w, (g, wv) in enumerate(zip(got, want)):
         _close_model(N_(g), wv, f"detokenize window {w}")
     _exact(N_(got[1])[:, :26], N_(got[0])[:, -26:], "window 1 continues window 0")
+
+
+# ---------------------------------------------------------------- waveform decoder
+DEC = dict(latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3))
+
+
+@pytest.mark.parametrize("offs,rep,row0,nrows", [((-6, -5, -4, -3, -2, -1, 0), 1, 0, None),
+                                                 ((-18, -15, -12, -9, -6, -3, 0), 1, 0, None),
+                                                 ((-2, -1, 0, 1, 2), 1, 7, 40),
+                                                 ((0, -1), 1, 0, None),
+                                                 ((-6, -5, -4, -3, -2, -1, 0), 2, 33, 50)])
+def test_codec_cols_taps_bit_exact(dev, offs, rep, row0, nrows):
+    import ctypes
+    import torch
+    B, T, C = 2, 44, 24
+    src = randn16(800 + len(offs), B * (T // rep), C)
+    n = nrows or B * T
+    out = torch.full((n, len(offs) * C), 5.0, dtype=torch.float16, device=dev)
+    st = D_(src, dev)
+    _call("ecd_codec_cols_taps", st.data_ptr(), C, (ctypes.c_int * len(offs))(*offs), len(offs),
+          out.data_ptr(), B, T, C, rep, row0, n)
+    x = src.reshape(B, T // rep, C)
+    want = np.zeros((B * T, len(offs) * C), np.float16)
+    for b in range(B):
+        for t in range(T):
+            for j, o in enumerate(offs):
+                if 0 <= t + o < T:
+                    want[b * T + t, j * C:(j + 1) * C] = x[b, (t + o) // rep]
+    _exact(N_(out), want[row0:row0 + n], f"cols taps {offs} rep {rep}")
+
+
+def test_codec_weight_norm_and_latent_split(dev):
+    import torch
+    g = rng(810)
+    v = f16(g.standard_normal((24, 16, 7)))
+    gg = f16(np.abs(g.standard_normal((24, 1, 1))) + 0.5)
+    w = torch.empty(24, 16, 7, dtype=torch.float16, device=dev)
+    vt, gt = D_(v, dev), D_(gg, dev)
+    _call("ecd_codec_weight_norm", vt.data_ptr(), gt.data_ptr(), w.data_ptr(), 24, 16 * 7)
+    assert_close16(N_(w), OC.weight_norm(v, gg), what="weight norm")
+    lat = randn16(811, 1, 50, 128, std=2.0)
+    lat[0, 0, :4] = f16(np.array([0.5, 1.5, -0.5, 2.5]) / 9)     # ties of round(9 x)
+    out = torch.empty(2, 50, 64, dtype=torch.float16, device=dev)
+    lt = D_(lat, dev)
+    _call("ecd_codec_latent_split", lt.data_ptr(), out.data_ptr(), 50, 2, 64)
+    _exact(N_(out), OC.round9(lat[0].reshape(50, 2, 64).transpose(1, 0, 2)), "latent split")
+
+
+def test_gemm_f16_prelu(dev):
+    from estudiocanciones_amd import _ffi
+    from estudiocanciones_amd.kernels import pack_f16, stream_ptr
+    import torch
+    M, N, K = 300, 192, 448
+    x = randn16(820, M, K)
+    w = f16(rng(821).standard_normal((N, K)) * 0.05)
+    b = (rng(822).standard_normal(N) * 0.1).astype(np.float32)
+    r = randn16(823, M, N)
+    xt, rt, bt = D_(x, dev), D_(r, dev), D_(b, dev)
+    y = torch.empty(M, N, dtype=torch.float16, device=dev)
+    _ffi.call("ecd_gemm_f16p_prelu", xt.data_ptr(), K, pack_f16(D_(w, dev)).data_ptr(), bt.data_ptr(),
+              0.25, rt.data_ptr(), N, y.data_ptr(), N, M, N, K, stream_ptr(dev))
+    want = f16(f32_(x) @ f32_(w).T + b)
+    want = f16(f32_(OC.prelu(want, 0.25)) + f32_(r))
+    assert_close16(N_(y), want, what="gemm prelu")
+
+
+def f32_(a):
+    return np.asarray(a, np.float32)
+
+
+@pytest.mark.parametrize("T", [12, 37])
+def test_codec_scalar_decoder(dev, T):
+    """ScalarModel.decode at a small configuration (latent 64 x 2 channel groups, channels
+    256 -> 128 -> 64, upsampling 2 and 3, post 2x) against the oracle, with the tap-column GEMMs
+    split into several row chunks."""
+    import torch
+    from estudiocanciones_amd.codec import ScalarDecoder
+    p = OC.random_decoder_weights(DEC, seed=830)
+    dec = ScalarDecoder({k: torch.from_numpy(np.asarray(v)) for k, v in p.items()},
+                        latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3),
+                        upsample_kernel_sizes=(4, 6), device=dev)
+    dec.ROWS_BYTES = 64 * 1024       # force several chunks per conv
+    lat = randn16(831 + T, 1, T, 128)
+    got = dec.decode(D_(lat, dev))
+    want = OC.scalar_decode(p, DEC, lat)
+    assert got.shape == want.shape == (2, T * 12, 1)
+    _close_model(N_(got), want, f"scalar decoder T={T}")

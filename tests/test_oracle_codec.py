@@ -258,3 +258,69 @@ def test_code_embedding_matches_library():
     codes0 = codes.copy()
     codes0[1, 3, 5] = unused
     assert np.array_equal(OC.code_embedding(p0, codes0), got.astype(np.float16))
+
+
+# ---------------------------------------------------------------- waveform decoder
+DEC = dict(latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3))
+
+
+def test_decoder_pieces_match_library():
+    g = np.random.default_rng(50)
+    t = lambda a: torch.from_numpy(np.asarray(a).astype(np.float64))
+    x = f16(g.standard_normal((2, 30, 16)))
+    w = f16(g.standard_normal((24, 16, 7)) / 10)
+    b = f16(g.standard_normal(24) * 0.1)
+    for d, causal in ((1, True), (3, True), (1, False)):
+        xc = t(x).transpose(1, 2)
+        if causal:
+            want = F.conv1d(F.pad(xc, (6 * d, 0)), t(w), t(b), dilation=d)
+        else:
+            want = F.conv1d(xc, t(w), t(b), padding=3 * d, dilation=d)
+        np.testing.assert_allclose(OC.conv1d(x, w, b, d, causal), want.transpose(1, 2).numpy(),
+                                   atol=1e-2, rtol=1e-2)
+    wt = f16(g.standard_normal((16, 12, 6)) / 6)
+    bt = f16(g.standard_normal(12) * 0.1)
+    want = F.conv_transpose1d(t(x).transpose(1, 2), t(wt), t(bt), stride=3)[:, :, :-3]
+    np.testing.assert_allclose(OC.conv_transpose_causal(x, wt, bt, 3),
+                               want.transpose(1, 2).numpy(), atol=1e-2, rtol=1e-2)
+    np.testing.assert_allclose(OC.prelu(x, 0.25), F.prelu(t(x), t([0.25])).numpy(), atol=1e-3)
+    v = f16(g.standard_normal((12, 5, 3)))
+    gg = f16(np.abs(g.standard_normal((12, 1, 1))) + 0.5)
+    np.testing.assert_allclose(OC.weight_norm(v, gg), torch._weight_norm(t(v), t(gg), 0).numpy(),
+                               atol=2e-3, rtol=2e-3)
+    # round(9 x) / 9: a grid of ninths is a fixed point up to fp16 rounding, ties go to even
+    q = f16(np.arange(-18, 19) / 9.0)
+    np.testing.assert_allclose(OC.round9(q), q, atol=1e-3)
+    assert OC.round9(f16([0.5 / 9]))[0] == 0 and OC.round9(f16([1.5 / 9]))[0] == f16(2 / 9)
+
+
+def test_decoder_matches_library_composition():
+    p = OC.random_decoder_weights(DEC, seed=51)
+    lat = f16(np.random.default_rng(52).standard_normal((1, 12, 128)))
+    got = OC.scalar_decode(p, DEC, lat).astype(np.float64)
+    t = lambda a: torch.from_numpy(np.asarray(a).astype(np.float64))
+    wn = lambda pre: torch._weight_norm(t(p[pre + "parametrizations.weight.original1"]),
+                                        t(p[pre + "parametrizations.weight.original0"]), 0)
+    x = t(lat).reshape(1, 12, 2, 64).permute(0, 2, 1, 3).reshape(2, 12, 64).transpose(1, 2)
+    x = torch.round(9 * x) / 9
+    x = F.conv1d(x, wn("decoder.0."), t(p["decoder.0.bias"]), padding=2)
+    for i, s in enumerate(DEC["upsample_factors"]):
+        pre = f"decoder.{1 + i}."
+        x = F.conv_transpose1d(x, wn(pre + "up_conv.layer."), t(p[pre + "up_conv.layer.bias"]),
+                               stride=s)[:, :, :-s]
+        for u, d in enumerate((1, 3, 5, 7, 9)):
+            q = f"{pre}convs.{u}."
+            h = F.prelu(F.conv1d(F.pad(x, (6 * d, 0)), wn(q + "conv1."), t(p[q + "conv1.bias"]),
+                                 dilation=d), t(p[q + "activation1.weight"]))
+            h = F.prelu(F.conv1d(h, wn(q + "conv2."), t(p[q + "conv2.bias"])),
+                        t(p[q + "activation2.weight"]))
+            x = h + x
+    n = 1 + len(DEC["upsample_factors"])
+    x = x.transpose(1, 2).repeat(1, 1, 2).reshape(2, -1, 64).transpose(1, 2)
+    x = F.prelu(F.conv1d(F.pad(x, (6, 0)), t(p[f"decoder.{n}.conv.weight"]),
+                         t(p[f"decoder.{n}.conv.bias"])), t(p[f"decoder.{n}.activation.weight"]))
+    x = F.conv1d(F.pad(x, (6, 0)), wn(f"decoder.{n + 1}."), t(p[f"decoder.{n + 1}.bias"]))
+    want = x.transpose(1, 2).numpy()
+    assert got.shape == want.shape == (2, 12 * 6 * 2, 1)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err < 3e-2 and np.corrcoef(got.ravel(), want.ravel())[0, 1] > 0.999, err
