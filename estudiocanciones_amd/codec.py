@@ -32,7 +32,9 @@ from .kernels import (gemm_f16_packed, gemm_f16_silu_packed, pack_f16, prefill_a
                       stream_ptr)
 
 __all__ = ["LlamaTransformer", "CodeEmbedding", "solve_euler", "inference_codes",
-           "detokenize_latents", "ScalarDecoder", "random_code_embedding_state_dict",
+           "detokenize_latents", "detokenize", "crossfade_windows", "ScalarDecoder",
+           "random_code_embedding_state_dict",
+           "random_decoder_state_dict", "decoder_flops",
            "mlp_hidden",
            "euler_times", "t_span", "random_state_dict", "estimator_flops"]
 
@@ -686,6 +688,44 @@ class ScalarDecoder:
         return y.view(S, T, -1)
 
 
+def crossfade_windows(windows: list, duration: float, sample_rate: int, target_len: int) -> np.ndarray:
+    """The audio assembly of HeartCodec.detokenize (modeling_heartcodec.py:168-204), a host step in
+    the reference too (each window is moved to the CPU first): every window [S, >= duration * sr]
+    is cut to duration * sr samples, consecutive windows overlap by (min - min // 93 * 80) samples
+    blended with a linear ramp in float64 and stored back in fp16 (through fp32, as torch's CPU
+    copy rounds), the result cut to ``target_len``."""
+    min_samples = int(duration * sample_rate)
+    hop = min_samples // 93 * 80
+    ovlp = min_samples - hop
+    out = None
+    for w in windows:
+        cur = np.asarray(w, dtype=np.float16)[:, :min_samples]
+        if out is None:
+            out = cur
+        elif ovlp == 0:
+            out = np.concatenate([out, cur], -1)
+        else:
+            ramp = np.linspace(0, 1, ovlp)
+            win = np.concatenate([ramp, 1 - ramp])
+            mix = out[:, -ovlp:].astype(np.float64) * win[-ovlp:] + cur[:, :ovlp].astype(np.float64) * win[:ovlp]
+            out = out.copy()
+            out[:, -ovlp:] = mix.astype(np.float32).astype(np.float16)
+            out = np.concatenate([out, cur[:, ovlp:]], -1)
+    return out[:, :target_len]
+
+
+def detokenize(emb: CodeEmbedding, est: LlamaTransformer, dec: ScalarDecoder, codes: torch.Tensor,
+               duration: float = 29.76, num_steps: int = 10, guidance_scale: float = 1.25,
+               sample_rate: int = 48000, randn=None) -> np.ndarray:
+    """HeartCodec.detokenize (modeling_heartcodec.py:57-204) after codec_lite.decode's clamp:
+    codes [Q, Tc] -> waveform [S, Tc / 12.5 * sample_rate] (fp16 numpy, on the host as the
+    reference returns it).  Latents and waveform windows are computed on the GPU."""
+    target_len = int(codes.shape[-1] / 12.5 * sample_rate)
+    lat = detokenize_latents(emb, est, codes, duration, num_steps, guidance_scale, randn)
+    wins = [dec.decode(l)[..., 0].cpu().numpy() for l in lat]
+    return crossfade_windows(wins, duration, sample_rate, target_len)
+
+
 def random_code_embedding_state_dict(num_quantizers=8, codebook_size=8192, codebook_dim=32,
                                      dim=512, device="cuda", seed=0):
     """Random fp16 code-embedding weights under the reference's names (relative to
@@ -701,6 +741,60 @@ def random_code_embedding_state_dict(num_quantizers=8, codebook_size=8192, codeb
     sd["cond_feature_emb.bias"] = rnd(dim, scale=0.02)
     sd["zero_cond_embedding1"] = rnd(dim, scale=1.0)
     return sd
+
+
+def random_decoder_state_dict(latent_hidden_dim=128, init_channel=64,
+                              upsample_factors=(5, 4, 4, 4, 3), device="cuda", seed=0):
+    """Random fp16 waveform-decoder weights under the reference's names (relative to
+    ``scalar_model.``; weight-normed layers as parametrization pairs), drawn on the device."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *shape, scale=1.0: (torch.randn(*shape, generator=g, device=dev) * scale).half()
+    sd = {}
+    ch = lambda i: init_channel * 2 ** (len(upsample_factors) - i)
+
+    def wnl(pre, shape, fan):
+        v = rnd(*shape)
+        sd[pre + "parametrizations.weight.original1"] = v
+        nrm = v.float().reshape(shape[0], -1).norm(dim=1)
+        sd[pre + "parametrizations.weight.original0"] = (nrm / fan ** 0.5).half().reshape(-1, 1, 1)
+
+    wnl("decoder.0.", (ch(0), latent_hidden_dim, 5), latent_hidden_dim * 5)
+    sd["decoder.0.bias"] = rnd(ch(0), scale=0.02)
+    for i, s in enumerate(upsample_factors):
+        pre = f"decoder.{1 + i}."
+        wnl(pre + "up_conv.layer.", (ch(i), ch(i + 1), 2 * s), ch(i) * 2)
+        sd[pre + "up_conv.layer.bias"] = rnd(ch(i + 1), scale=0.02)
+        c = ch(i + 1)
+        for u in range(5):
+            q = f"{pre}convs.{u}."
+            wnl(q + "conv1.", (c, c, 7), c * 7 * 4)
+            sd[q + "conv1.bias"] = rnd(c, scale=0.02)
+            wnl(q + "conv2.", (c, c, 1), c * 4)
+            sd[q + "conv2.bias"] = rnd(c, scale=0.02)
+            sd[q + "activation1.weight"] = torch.full((1,), 0.25, device=dev).half()
+            sd[q + "activation2.weight"] = torch.full((1,), 0.25, device=dev).half()
+    n = 1 + len(upsample_factors)
+    sd[f"decoder.{n}.conv.weight"] = rnd(init_channel, init_channel, 7, scale=(init_channel * 7) ** -0.5)
+    sd[f"decoder.{n}.conv.bias"] = rnd(init_channel, scale=0.02)
+    sd[f"decoder.{n}.activation.weight"] = torch.full((1,), 0.25, device=dev).half()
+    wnl(f"decoder.{n + 1}.", (1, init_channel, 7), init_channel * 7)
+    sd[f"decoder.{n + 1}.bias"] = rnd(1, scale=0.02)
+    return sd
+
+
+def decoder_flops(dec: ScalarDecoder, T: int, S: int = 2) -> int:
+    """Algorithmic FLOPs of ScalarDecoder.decode on a [1, T, S * latent] window (2 M N K per
+    conv as a GEMM, M = output rows)."""
+    fl = 2 * S * T * dec.conv0.lin.N * dec.conv0.lin.K
+    for up, units in dec.blocks:
+        fl += 2 * S * T * up.lin.N * up.lin.K
+        T *= up.s
+        for c1, c2 in units:
+            fl += 2 * S * T * (c1.lin.N * c1.lin.K + c2.lin.N * c2.lin.K)
+    T *= 2
+    fl += 2 * S * T * (dec.post.lin.N * dec.post.lin.K + dec.final.lin.N * dec.final.lin.K)
+    return fl
 
 
 def estimator_flops(est: LlamaTransformer, B: int, T: int) -> dict:

@@ -282,6 +282,8 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 //   9: as 1, software-pipelined
 //  10: 128 x 64, waves 4 x 1 (32 x 64 each), software-pipelined, 48 KB
 //  11: 128 x 64, waves 2 x 2 (64 x 32 each), software-pipelined, 48 KB
+//  12: 64 x 128, waves 1 x 4 (64 x 32 each), software-pipelined, 48 KB (outputs <= 64 wide)
+//  13: 64 x 256, waves 1 x 4 (64 x 64 each), software-pipelined, 80 KB
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
@@ -301,6 +303,7 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
 static int default_cfg(int M, int N, int K, bool silu) {
   (void)M;
   if (silu) return K <= 2048 ? 2 : 8;
+  if (N <= 512) return 12;     // the waveform decoder's narrow convs: 64-feature tiles
   return N <= 1536 ? 10 : 8;   // narrow outputs: 128 x 64 tiles for more blocks
 }
 
@@ -321,6 +324,8 @@ static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const floa
     case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
     case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
     case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
     default: return ECD_EINVAL;
   }
 }
@@ -352,7 +357,7 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                         int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || cfg < 0 || cfg > 11 || epi < 0 || epi > 2)
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 13 || epi < 0 || epi > 2)
     return ECD_EINVAL;
   const bool silu = epi == F16_SILU;
   if (silu) {

@@ -516,3 +516,29 @@ def random_decoder_weights(cfg: dict, seed: int = 0) -> dict:
     wnl(f"decoder.{n + 1}.", (1, c, 7), c * 7)
     p[f"decoder.{n + 1}.bias"] = f16(g.standard_normal(1) * 0.02)
     return p
+
+
+def detokenize(p_fm: dict, p_est: dict, cfg: dict, p_dec: dict, dcfg: dict, codes,
+               duration: float, num_steps: int, guidance_scale: float, sample_rate: int,
+               noises) -> np.ndarray:
+    """HeartCodec.detokenize (modeling_heartcodec.py:57-204): latent windows, the waveform of
+    each (scalar_decode), crop, linear crossfade over the overlap in float64 stored in fp16
+    (through fp32, as torch's CPU copy rounds), cut to the codes' duration."""
+    target_len = int(np.asarray(codes).shape[-1] / 12.5 * sample_rate)
+    lats = detokenize_latents(p_fm, p_est, cfg, codes, duration, num_steps, guidance_scale, noises)
+    min_samples = int(duration * sample_rate)
+    hop = min_samples // 93 * 80
+    ovlp = min_samples - hop
+    out = None
+    for lat in lats:
+        cur = scalar_decode(p_dec, dcfg, lat)[..., 0][:, :min_samples]
+        if out is None:
+            out = cur
+        else:
+            ramp = np.linspace(0, 1, ovlp)
+            win = np.concatenate([ramp, 1 - ramp])
+            mix = out[:, -ovlp:].astype(np.float64) * win[-ovlp:] + cur[:, :ovlp].astype(np.float64) * win[:ovlp]
+            out = out.copy()
+            out[:, -ovlp:] = mix.astype(np.float32).astype(np.float16)
+            out = np.concatenate([out, cur[:, ovlp:]], -1)
+    return out[:, :target_len]

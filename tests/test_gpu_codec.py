@@ -473,3 +473,28 @@ def test_codec_scalar_decoder(dev, T):
     want = OC.scalar_decode(p, DEC, lat)
     assert got.shape == want.shape == (2, T * 12, 1)
     _close_model(N_(got), want, f"scalar decoder T={T}")
+
+
+def test_codec_detokenize_audio(dev):
+    """codes -> waveform: three 7.44 s windows (latents on the GPU), each decoded by the waveform
+    decoder (small configuration: one channel group, 12 samples per latent frame, so
+    sample_rate 300 stands in for 48 kHz) and crossfaded over the overlap, against the oracle."""
+    import torch
+    from estudiocanciones_amd.codec import ScalarDecoder, detokenize
+    p_est = OC.random_weights(TINY, seed=60)
+    p_fm = OC.random_vq_weights(8, 64, 32, 64, seed=61)
+    dcfg = dict(latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3))
+    p_dec = OC.random_decoder_weights(dcfg, seed=62)
+    est = _estimator(dev, p_est, TINY)
+    emb = _code_embedding(dev, p_fm)
+    dec = ScalarDecoder({k: torch.from_numpy(np.asarray(v)) for k, v in p_dec.items()},
+                        latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3),
+                        upsample_kernel_sizes=(4, 6), device=dev)
+    codes = rng(63).integers(0, 64, (8, 250))
+    noises = [randn16(64 + w, 1, 186, 64) for w in range(3)]
+    it = iter(noises)
+    got = detokenize(emb, est, dec, D_(codes, dev), 7.44, 2, 1.25, 300,
+                     randn=lambda shape: D_(next(it), dev))
+    want = OC.detokenize(p_fm, p_est, TINY, p_dec, dcfg, codes, 7.44, 2, 1.25, 300, noises)
+    assert got.shape == want.shape == (1, 6000)   # one 64-wide channel group
+    _close_model(got, want, "detokenize audio")
