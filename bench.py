@@ -12,8 +12,9 @@ Prints one JSON line: frames/s (value), the GEMV roofline (hipEvent-timed launch
 frame's GEMV sequence, algorithmic bytes N*K + 2N + 2MK + 2MN (+2MN residual) per launch),
 the same frame at a second KV length (``target_point``, default 4096: frames/s and the HBM
 fractions of the GEMV family and the decode attention there), the prompt pass, one codec
-detokenize window from codes to latents (``codec_window``: code embedding + 10 CFG Euler steps
-of the 30-layer flow-matching estimator at 744 frames), and a CPU baseline: the reference's CPU
+detokenize window from codes to audio (``codec_window``: code embedding + 10 CFG Euler steps
+of the 30-layer flow-matching estimator at 744 frames, then the waveform decoder to 2 x 29.76 s
+at 48 kHz), and a CPU baseline: the reference's CPU
 path (numpy float32 restatement) timed on a bounded sample of layers on the host cores and
 scaled to a frame.
 
@@ -395,10 +396,11 @@ def main():
 
 
 def measure_codec(torch, dev, steps, seed):
-    """One detokenize window of the codec, codes to latents: 372 codes x 8 quantizers -> code
+    """One detokenize window of the codec, codes to audio: 372 codes x 8 quantizers -> code
     embedding -> the flow-matching estimator (24 + 6 layers, dim 1536 / 3072, 24 heads), batch 1
-    doubled by CFG, 744 latent frames (29.76 s), ``steps`` Euler steps with guidance 1.25,
-    random-init fp16 weights, codes and noise resident on the GPU."""
+    doubled by CFG, 744 latent frames (29.76 s), ``steps`` Euler steps with guidance 1.25 ->
+    the waveform decoder (timed separately), random-init fp16 weights, codes and noise resident
+    on the GPU."""
     from estudiocanciones_amd import codec as C
     sd = C.random_state_dict(device=dev, seed=seed + 7)
     est = C.LlamaTransformer(sd, device=dev)
@@ -435,22 +437,44 @@ def measure_codec(torch, dev, steps, seed):
     torch.cuda.synchronize()
     call_ms = e0.elapsed_time(e1) / reps
     fl = C.estimator_flops(est, 2 * B, T)
-    del est
+    del est, emb
+    torch.cuda.empty_cache()
+    # the waveform of the window: latents [1, 744, 256] -> 2 x 1,428,480 samples at 48 kHz
+    dec = C.ScalarDecoder(C.random_decoder_state_dict(device=dev, seed=seed + 10), device=dev)
+    wav = dec.decode(out)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(3):
+        wav = dec.decode(out)
+    e1.record()
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / 3
+    if not bool(torch.isfinite(wav).all()):
+        raise RuntimeError("codec decoder produced non-finite samples")
+    dfl = C.decoder_flops(dec, T)
+    del dec, wav
     torch.cuda.empty_cache()
     return {
-        "workload": ("codec detokenize window, codes to latents: 372 x 8 codes -> ResidualVQ "
+        "workload": ("codec detokenize window, codes to audio: 372 x 8 codes -> ResidualVQ "
                      "embedding -> flow-matching estimator (24 + 6 LlamaTransformer layers, dim "
                      "1536 / 3072, 24 heads, hd 64 / 128), batch 1 x CFG 2, 744 latent frames "
-                     f"(29.76 s), {steps} Euler steps, guidance 1.25, fp16"),
+                     f"(29.76 s), {steps} Euler steps, guidance 1.25 -> waveform decoder "
+                     "(2048 -> 64 channels, x1920) -> 2 x 1,428,480 samples at 48 kHz, fp16"),
         "window_ms": round(win_ms, 2),
         "latent_frames_per_s": round(T * B / (win_ms / 1e3), 1),
         "estimator_call_ms": round(call_ms, 3),
         "estimator_flops": int(fl["total"]),
         "estimator_TFLOPs": round(fl["total"] / call_ms / 1e9, 1),
         "frac_of_mfma_f16_peak": round(fl["total"] / call_ms / 1e9 / 2500.0, 4),
+        "decoder_ms": round(dec_ms, 2),
+        "decoder_flops": int(dfl),
+        "decoder_TFLOPs": round(dfl / dec_ms / 1e9, 1),
+        "codes_to_audio_ms": round(win_ms + dec_ms, 2),
+        "audio_x_realtime": round(29.76 / ((win_ms + dec_ms) / 1e3), 1),
         "path": ("code gather-sum kernel + fp16 MFMA GEMM (packed weights, fused bias / scale / "
                  "SiLU-mul epilogues), MFMA flash attention, fused gated-residual + adaLN norms, "
-                 "CFG Euler kernel"),
+                 "CFG Euler kernel; waveform decoder: tap-column convs as fp16 GEMMs with "
+                 "PReLU / residual epilogues"),
     }
 
 
