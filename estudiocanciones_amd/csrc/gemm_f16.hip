@@ -27,7 +27,8 @@
 // number of blocks must still fill 256 CUs; the host picks the tile per shape.
 //
 // Block order is XCD-aware: the row blocks that share a weight tile get block ids equal modulo 8,
-// so they run on one XCD and share its L2.
+// so they run on one XCD and share its L2 (feature blocks in whole groups of 8; the grid has
+// exactly one workgroup per output tile, so narrow outputs launch no empty workgroups).
 #include "common.h"
 
 namespace ecd {
@@ -85,12 +86,22 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
   __shared__ __align__(16) f16 lw[NS][BN / 16 * 1024];  // BN / 16 tiles x 2 KB
   __shared__ __align__(16) f16 lx[NS][BM * 64];         // BM rows x 128 B
 
+  // feature blocks in full groups of 8 share XCDs with their row blocks; the remaining
+  // nfb % 8 feature blocks (all of them when nfb < 8) are laid out row-major after them
   const int b = blockIdx.x;
-  const int grp8 = b / (8 * nmb);
-  const int rem = b - grp8 * 8 * nmb;
-  const int mb = rem >> 3;
-  const int fb = grp8 * 8 + (rem & 7);
-  if (fb >= nfb) return;  // padding blocks of the last group of 8 (uniform per block)
+  const int full = nfb & ~7;
+  int fb, mb;
+  if (b < full * nmb) {
+    const int grp8 = b / (8 * nmb);
+    const int rem = b - grp8 * 8 * nmb;
+    mb = rem >> 3;
+    fb = grp8 * 8 + (rem & 7);
+  } else {
+    const int rem = b - full * nmb;
+    const int tw = nfb - full;
+    mb = rem / tw;
+    fb = full + (rem - mb * tw);
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -291,7 +302,7 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
   constexpr int BN = 16 * WN * FT, BM = 16 * WM * RT;
   const int nfb = (N + BN - 1) / BN;
   const int nmb = (M + BM - 1) / BM;
-  const long blocks = (long)((nfb + 7) / 8) * 8 * nmb;
+  const long blocks = (long)nfb * nmb;
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
   hipLaunchKernelGGL((gemm_f16w_kernel<EPI, WN, WM, FT, RT, NS, PL>), dim3((unsigned)blocks),
                      dim3(256), 0, st, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, nfb,
@@ -301,10 +312,12 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
 
 // Library default per shape (N counts output features before the SiLU pairing).
 static int default_cfg(int M, int N, int K, bool silu) {
-  (void)M;
-  if (silu) return K <= 2048 ? 2 : 8;
-  if (N <= 512) return 12;     // the waveform decoder's narrow convs: 64-feature tiles
-  return N <= 1536 ? 10 : 8;   // narrow outputs: 128 x 64 tiles for more blocks
+  (void)K;
+  if (silu) return 8;
+  if (N <= 64) return 12;                  // the decoder's 64-channel convs: 64-feature tiles
+  if (N <= 1536 && M <= 16384) return 10;  // narrow outputs, few rows: 128 x 64 for more blocks
+  if (N <= 1024) return 1;                 // the decoder's wider convs over many rows
+  return 8;
 }
 
 template <int EPI>
