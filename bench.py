@@ -473,8 +473,8 @@ def measure_codec(torch, dev, steps, seed):
         "audio_x_realtime": round(29.76 / ((win_ms + dec_ms) / 1e3), 1),
         "path": ("code gather-sum kernel + fp16 MFMA GEMM (packed weights, fused bias / scale / "
                  "SiLU-mul epilogues), MFMA flash attention, fused gated-residual + adaLN norms, "
-                 "CFG Euler kernel; waveform decoder: tap-column convs as fp16 GEMMs with "
-                 "PReLU / residual epilogues"),
+                 "CFG Euler kernel; waveform decoder: convs as fp16 GEMMs reading their taps "
+                 "from zero-padded activations, PReLU / residual epilogues"),
     }
 
 

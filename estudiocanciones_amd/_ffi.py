@@ -41,8 +41,8 @@ SIGNATURES = {
     "ecd_codec_cols3": [_P, _P, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P],
     "ecd_codec_vq_embed": [_P, c_long, c_long, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_int, _P],
-    "ecd_codec_cols_taps": [_P, c_long, _P, c_int, _P, c_int, c_int, c_int, c_int, c_long, c_long,
-                            _P],
+    "ecd_codec_cols_taps": [_P, c_long, _P, c_int, _P, c_int, c_int, c_int, c_int, c_int, c_long,
+                            c_long, _P],
     "ecd_codec_weight_norm": [_P, _P, _P, c_int, c_int, _P],
     "ecd_codec_latent_split": [_P, _P, c_int, c_int, c_int, _P],
     "ecd_codec_timestep": [_P, _P, c_int, _P],
@@ -59,6 +59,8 @@ SIGNATURES = {
     "ecd_gemm_f16p_silu": [_P, c_long, _P, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_f16p_prelu": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
                             c_int, _P],
+    "ecd_gemm_f16p_conv": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
+                           c_int, c_int, c_int, c_int, _P, c_int, c_int, _P],
     "ecd_gemm_f16p_tuned": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
                             c_int, c_int, c_int, _P],
     "ecd_packed_bytes": [c_int, c_int],

@@ -616,6 +616,8 @@ class ScalarDecoder:
             up = _ConvT(wn(pre + "up_conv.layer."), get(pre + "up_conv.layer.bias"), s)
             if upsample_kernel_sizes[i] != 2 * s:
                 raise ValueError("upsample kernel must be 2 * factor (causal)")
+            if self.PAD % s:
+                raise ValueError(f"upsampling factor {s} must divide the {self.PAD} pad rows")
             units = []
             for u, d in enumerate((1, 3, 5, 7, 9)):
                 q = f"{pre}convs.{u}."
@@ -632,39 +634,61 @@ class ScalarDecoder:
                           causal, prelu(f"decoder.{n_post}.activation."))
         self.final = _Conv(wn(f"decoder.{n_post + 1}."), get(f"decoder.{n_post + 1}.bias"), causal)
         self.num_bands = num_bands
+        self._bufs = {}
 
     @classmethod
     def from_codec_state_dict(cls, sd: dict, prefix="scalar_model.", **cfg):
         return cls({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}, **cfg)
 
-    def _conv(self, cv, x, B, T, rep=1, res=None, out=None):
-        """cv over x [B * T / rep, Cin] (time-major) -> [B * T, N] in row chunks."""
-        st = stream_ptr(self.dev)
+    # Zero rows before each sequence of a padded activation: at least the widest causal reach
+    # (6 taps at dilation 9 = 54) and divisible by every upsampling factor, so a transposed conv
+    # writing s output rows per input row lands on the padded layout of the upsampled sequence.
+    PAD = 60
+    TAIL = 8     # zero rows after the last sequence
+
+    def _pbuf(self, key, S, T, C):
+        """Cached zero-padded time-major activation [S * (PAD + T) + TAIL, C].  The convolutions
+        write only the data rows, so the padding stays zero across calls."""
+        k = (key, S, T, C)
+        if k not in self._bufs:
+            self._bufs[k] = torch.zeros(S * (self.PAD + T) + self.TAIL, C, device=self.dev,
+                                        dtype=torch.float16)
+        return self._bufs[k]
+
+    def _buf(self, key, rows, C):
+        k = (key, rows, C)
+        if k not in self._bufs:
+            self._bufs[k] = torch.empty(rows, C, device=self.dev, dtype=torch.float16)
+        return self._bufs[k]
+
+    def _gemm(self, cv, x, ldx, M, T, xpad, taps, y, ldy, ypad, res=False):
+        """One conv as ecd_gemm_f16p_conv: implicit taps over the padded x (taps) or a plain x."""
         lin = cv.lin
-        K = lin.K
-        M = B * T
-        y = out if out is not None else torch.empty(M, lin.N, device=self.dev, dtype=torch.float16)
+        prelu = getattr(cv, "prelu", None)
+        _ffi.call("ecd_gemm_f16p_conv", x.data_ptr(), ldx, lin.wp.data_ptr(),
+                  lin.b.data_ptr() if lin.b is not None else None,
+                  float(prelu) if prelu is not None else 1.0, y.data_ptr() if res else None,
+                  ldy if res else 0, y.data_ptr(), ldy, M, lin.N, lin.K, T, xpad, ypad,
+                  cv.off if taps else None, cv.k if taps else 0, 2 if prelu is not None else 0,
+                  stream_ptr(self.dev))
+
+    def _cols_conv(self, cv, src, S, T, spad, rep, y, ypad):
+        """A conv over materialised tap columns of src (padded by spad rows per sequence), its
+        output rows written per sequence into y (padded by ypad rows), in chunks."""
+        st = stream_ptr(self.dev)
+        K = cv.lin.K
+        C = K // cv.k
         step = max(256, self.ROWS_BYTES // (2 * K)) // 256 * 256
-        direct = cv.k == 1 and cv.off[0] == 0 and rep == 1     # a 1x1 conv reads x itself
-        cols = None if direct else torch.empty(min(step, M) * K, device=self.dev, dtype=torch.float16)
-        for r0 in range(0, M, step):
-            n = min(step, M - r0)
-            if direct:
-                c = x[r0:r0 + n]
-            else:
-                c = cols[:n * K].view(n, K)
-                _ffi.call("ecd_codec_cols_taps", x.data_ptr(), x.stride(0), cv.off, cv.k,
-                          c.data_ptr(), B, T, lin.K // cv.k, rep, r0, n, st)
-            yr = y[r0:r0 + n]
-            rr = res[r0:r0 + n] if res is not None else None
-            if getattr(cv, "prelu", None) is not None:
-                _ffi.call("ecd_gemm_f16p_prelu", c.data_ptr(), c.stride(0), lin.wp.data_ptr(),
-                          lin.b.data_ptr() if lin.b is not None else None, cv.prelu,
-                          rr.data_ptr() if rr is not None else None, rr.stride(0) if rr is not None else 0,
-                          yr.data_ptr(), yr.stride(0), n, lin.N, K, st)
-            else:
-                lin(c, yr, res=rr)
-        return y
+        cols = self._buf("cols", min(step, T), K)
+        ld = y.stride(0)
+        for b in range(S):
+            for t0 in range(0, T, step):
+                n = min(step, T - t0)
+                c = cols[:n]
+                _ffi.call("ecd_codec_cols_taps", src.data_ptr(), src.stride(0), cv.off, cv.k,
+                          c.data_ptr(), S, T, C, rep, spad, b * T + t0, n, st)
+                yr = y[b * (ypad + T) + ypad + t0:]
+                self._gemm(cv, c, K, n, n, 0, False, yr, ld, -1)
 
     def decode(self, latent: torch.Tensor) -> torch.Tensor:
         """latent [1, T, S * latent_dim] fp16 (one window) -> waveform [S, T * up, num_bands]
@@ -672,20 +696,29 @@ class ScalarDecoder:
         _, T, W = latent.shape
         S = W // self.latent_dim
         st = stream_ptr(self.dev)
+        P = self.PAD
         lat = latent.to(self.dev, torch.float16).contiguous()
-        x = torch.empty(S * T, self.latent_dim, device=self.dev, dtype=torch.float16)
-        _ffi.call("ecd_codec_latent_split", lat.data_ptr(), x.data_ptr(), T, S, self.latent_dim, st)
-        x = self._conv(self.conv0, x, S, T)
-        for up, units in self.blocks:
-            x = self._conv(up, x, S, T).view(S * T * up.s, up.cout)
-            T *= up.s
+        x0 = self._buf("lat", S * T, self.latent_dim)
+        _ffi.call("ecd_codec_latent_split", lat.data_ptr(), x0.data_ptr(), T, S, self.latent_dim, st)
+        a = self._pbuf("c0", S, T, self.conv0.cout)
+        self._cols_conv(self.conv0, x0, S, T, 0, 1, a, P)
+        for i, (up, units) in enumerate(self.blocks):
+            s, C = up.s, up.cout
+            bb = self._pbuf(f"b{i}", S, T * s, C)
+            # transposed conv: GEMM rows are input steps, each writing s consecutive outputs
+            self._gemm(up, a, up.cin, S * T, T, P, True, bb, s * C, P // s)
+            T *= s
+            h = self._buf(f"h{i}", S * T, C)
             for c1, c2 in units:
-                h = self._conv(c1, x, S, T)
-                x = self._conv(c2, h, S, T, res=x)
-        x = self._conv(self.post, x, S, 2 * T, rep=2)
-        T *= 2
-        y = self._conv(self.final, x, S, T)
-        return y.view(S, T, -1)
+                self._gemm(c1, bb, C, S * T, T, P, True, h, C, -1)
+                self._gemm(c2, h, C, S * T, T, 0, False, bb, C, P, res=True)
+            a = bb
+        T2 = 2 * T
+        pb = self._pbuf("post", S, T2, self.post.cout)
+        self._cols_conv(self.post, a, S, T2, P, 2, pb, P)
+        y = self._buf("out", S * T2, self.final.cout)
+        self._gemm(self.final, pb, self.post.cout, S * T2, T2, P, True, y, self.final.cout, -1)
+        return y.view(S, T2, -1).clone()
 
 
 def crossfade_windows(windows: list, duration: float, sample_rate: int, target_len: int) -> np.ndarray:

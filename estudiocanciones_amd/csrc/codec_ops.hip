@@ -286,15 +286,17 @@ struct Taps {
 };
 
 // Tap columns, time-major, for global rows row0 .. row0 + nrows - 1 (row = b * T + t):
-// out[row - row0, j * C + c] = src[b, (t + off[j]) / rep, c] when 0 <= t + off[j] < T, else 0.  src [B, T / rep, C] with row stride ld.  A Conv1d of kernel k
-// and dilation d is the GEMM of these columns with W'[o, j * C + c] = weight[o, c, j]:
+// out[row - row0, j * C + c] = src[b, (t + off[j]) / rep, c] when 0 <= t + off[j] < T, else 0.
+// src [B, spad + T / rep, C] with row stride ld (spad rows before each sequence, skipped).
+// A Conv1d of kernel k and dilation d is the GEMM of these columns with
+// W'[o, j * C + c] = weight[o, c, j]:
 // causal (sq_codec.py:32-73) off[j] = (j - k + 1) d; centred off[j] = j - (k - 1) / 2; the causal
 // ConvTranspose1d (kernel 2s, stride s, sq_codec.py:76-117) uses taps {0, -1}; rep 2 is the
 // PostProcessor's nearest 2x repeat (sq_codec.py:140-146).  One thread per 16-byte piece.
 __global__ __launch_bounds__(256) void codec_cols_taps_kernel(const f16* __restrict__ src, long ld,
                                                               Taps tp, f16* __restrict__ out,
-                                                              int T, int C, int rep, long row0,
-                                                              long nrows) {
+                                                              int T, int C, int rep, int spad,
+                                                              long row0, long nrows) {
   const int vpr = tp.k * C >> 3;  // 16-byte pieces per output row
   const long n = nrows * vpr;
   const int Ts = T / rep;
@@ -306,7 +308,8 @@ __global__ __launch_bounds__(256) void codec_cols_taps_kernel(const f16* __restr
     const int b = (int)(row / T), t = (int)(row - (long)b * T);
     const int u = t + tp.off[j];
     u32x4 val = {0u, 0u, 0u, 0u};
-    if (u >= 0 && u < T) val = *(const u32x4*)(src + ((long)b * Ts + u / rep) * ld + c);
+    if (u >= 0 && u < T)
+      val = *(const u32x4*)(src + ((long)b * (Ts + spad) + spad + u / rep) * ld + c);
     *(u32x4*)(out + lr * (long)tp.k * C + e) = val;
   }
 }
@@ -514,17 +517,17 @@ int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books
 }
 
 int ecd_codec_cols_taps(const void* src, long ld, const int* offsets, int k, void* out, int B,
-                        int T, int C, int rep, long row0, long nrows, void* stream) {
+                        int T, int C, int rep, int spad, long row0, long nrows, void* stream) {
   if (!src || !offsets || !out || k <= 0 || k > 8 || B <= 0 || T <= 0 || C <= 0 || (C & 7) ||
-      ld < C || (ld & 7) || (rep != 1 && rep != 2) || T % rep || !a16(src) || !a16(out) ||
+      spad < 0 || ld < C || (ld & 7) || (rep != 1 && rep != 2) || T % rep || !a16(src) || !a16(out) ||
       row0 < 0 || nrows <= 0 || row0 + nrows > (long)B * T)
     return ECD_EINVAL;
   Taps tp = {};
   tp.k = k;
   for (int j = 0; j < k; ++j) tp.off[j] = offsets[j];
   hipLaunchKernelGGL(codec_cols_taps_kernel, dim3(grid_for(nrows * (k * C / 8))), dim3(256), 0,
-                     (hipStream_t)stream, (const f16*)src, ld, tp, (f16*)out, T, C, rep, row0,
-                     nrows);
+                     (hipStream_t)stream, (const f16*)src, ld, tp, (f16*)out, T, C, rep, spad,
+                     row0, nrows);
   return ecd_launch_status();
 }
 

@@ -70,12 +70,27 @@ __device__ __forceinline__ void f16_mfma_half(f32x4 (&acc)[FT][RT], const f16x8 
       acc[ft][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w[ft], f[rt], acc[ft][rt], 0, 0, 0);
 }
 
+// Row layouts of a convolution as a GEMM over implicit tap columns (the waveform decoder):
+// row m = b * T + t of the GEMM.  With k > 0, x is time-major with xpad zero rows before each
+// sequence and row m's K index j * C + c (C = 64 cpt) reads x row b (T + xpad) + xpad + t + off[j]
+// (the tap offsets move the chunk's DMA base; the pad rows supply the zeros of the padding).
+// With ypad >= 0, y and res rows are b (T + ypad) + ypad + t.  T = 0: plain rows throughout.
+struct RowMap {
+  int T, xpad, ypad, cpt, k;
+  int off[8];
+};
+
+__device__ __forceinline__ long seq_row(long m, int T, int pad) {
+  const long b = m / T;
+  return b * (T + pad) + pad + (m - b * T);
+}
+
 // 128 x 128 tiles are built for two waves per SIMD (two blocks per CU); the larger ones for one
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL>
 __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel(
     const f16* __restrict__ x, long ldx, const f16* __restrict__ wp,
     const float* __restrict__ bias, float alpha, const f16* __restrict__ res, long ldr,
-    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb) {
+    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb, RowMap rm) {
   static_assert(WN * WM == 4, "four waves");
   constexpr int BN = 16 * WN * FT;      // features per block
   constexpr int BM = 16 * WM * RT;      // rows per block
@@ -131,14 +146,26 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
 #pragma unroll
   for (int j = 0; j < XI; ++j) {
     const int i = wv + 4 * j;
-    xoff[j] = (uint32_t)((long)min(m0 + 8 * i + (lane >> 3), M - 1) * ldx * 2 + 16 * xpiece);
+    long xr = min(m0 + 8 * i + (lane >> 3), M - 1);
+    if (rm.k) xr = seq_row(xr, rm.T, rm.xpad);
+    xoff[j] = (uint32_t)(xr * ldx * 2 + 16 * xpiece);
   }
+  // chunk c's x base: plain K offset 64 c, or tap j = c / cpt shifted by off[j] rows
+  auto xbase = [&](int c) -> const f16* {
+    if (!rm.k) return x + (long)c * 64;
+    const int j = c / rm.cpt;
+    int o = rm.off[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i)
+      if (j == i) o = rm.off[i];
+    return x + (long)o * ldx + (long)(c - j * rm.cpt) * 64;
+  };
   auto issue = [&](int c, int st) {
 #pragma unroll
     for (int j = 0; j < WI; ++j) lds_dma16(wsrc[j] + (long)c * 2048, woff, &lw[st][wdst[j]]);
+    const f16* xb = xbase(c);
 #pragma unroll
-    for (int j = 0; j < XI; ++j)
-      lds_dma16(x + (long)c * 64, xoff[j], &lx[st][8 * (wv + 4 * j) * 64]);
+    for (int j = 0; j < XI; ++j) lds_dma16(xb, xoff[j], &lx[st][8 * (wv + 4 * j) * 64]);
   };
 
   f32x4 acc[FT][RT];
@@ -221,8 +248,9 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int m = m0 + (wm * RT + rt) * 16 + (lane & 15);
-      if (m >= M) continue;
+      const int mm = m0 + (wm * RT + rt) * 16 + (lane & 15);
+      if (mm >= M) continue;
+      const long m = rm.ypad >= 0 ? seq_row(mm, rm.T, rm.ypad) : mm;
       f16x4 yv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -298,7 +326,7 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
-                      hipStream_t st) {
+                      const RowMap& rm, hipStream_t st) {
   constexpr int BN = 16 * WN * FT, BM = 16 * WM * RT;
   const int nfb = (N + BN - 1) / BN;
   const int nmb = (M + BM - 1) / BM;
@@ -306,7 +334,7 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
   hipLaunchKernelGGL((gemm_f16w_kernel<EPI, WN, WM, FT, RT, NS, PL>), dim3((unsigned)blocks),
                      dim3(256), 0, st, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, nfb,
-                     nmb);
+                     nmb, rm);
   return ecd_launch_status();
 }
 
@@ -323,24 +351,34 @@ static int default_cfg(int M, int N, int K, bool silu) {
 template <int EPI>
 static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const float* bias,
                       float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N,
-                      int K, hipStream_t st) {
+                      int K, const RowMap& rm, hipStream_t st) {
   if (cfg == 0) cfg = default_cfg(M, N, K, EPI == F16_SILU);
   switch (cfg) {
-    case 1: return launch_cfg<EPI, 4, 1, 2, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 2: return launch_cfg<EPI, 2, 2, 4, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 3: return launch_cfg<EPI, 4, 1, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 4: return launch_cfg<EPI, 4, 1, 4, 8, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 5: return launch_cfg<EPI, 2, 2, 8, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 6: return launch_cfg<EPI, 2, 2, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 7: return launch_cfg<EPI, 2, 2, 4, 4, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 8: return launch_cfg<EPI, 2, 2, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
-    case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, st);
+    case 1: return launch_cfg<EPI, 4, 1, 2, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 2: return launch_cfg<EPI, 2, 2, 4, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 3: return launch_cfg<EPI, 4, 1, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 4: return launch_cfg<EPI, 4, 1, 4, 8, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 5: return launch_cfg<EPI, 2, 2, 8, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 6: return launch_cfg<EPI, 2, 2, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 7: return launch_cfg<EPI, 2, 2, 4, 4, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 8: return launch_cfg<EPI, 2, 2, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     default: return ECD_EINVAL;
   }
+}
+
+static int launch_epi(int epi, int cfg, const f16* x, long ldx, const f16* wp, const float* bias,
+                      float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
+                      const RowMap& rm, hipStream_t st) {
+  if (epi == F16_SILU)
+    return launch_f16<F16_SILU>(cfg, x, ldx, wp, nullptr, 1.0f, nullptr, 0, y, ldy, M, N, K, rm, st);
+  if (epi == F16_PRELU)
+    return launch_f16<F16_PRELU>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+  return launch_f16<F16_STORE>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
 }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -380,14 +418,31 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
     return ECD_EINVAL;
   }
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  if (silu)
-    return launch_f16<F16_SILU>(cfg, (const f16*)x, ldx, (const f16*)wp, nullptr, 1.0f, nullptr,
-                                0, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
-  if (epi == F16_PRELU)
-    return launch_f16<F16_PRELU>(cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha,
-                                 (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
-  return launch_f16<F16_STORE>(cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha,
-                               (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
+  const RowMap rm = {0, 0, -1, 0, 0, {0, 0, 0, 0, 0, 0, 0, 0}};
+  return launch_epi(epi, cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
+                    ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);
+}
+
+int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                       const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
+                       int xpad, int ypad, const int* offsets, int k, int epi, void* stream) {
+  if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || (ldx % 8) || !al16(x) ||
+      !al16(wp) || epi < 0 || epi > 2 || epi == F16_SILU || T <= 0 || M % T || k < 0 || k > 8 ||
+      (k && (!offsets || K % (64 * k) || xpad < 0)) || (!k && ldx < K) || ldy < N ||
+      (res && ldr < N) || ypad < -1)
+    return ECD_EINVAL;
+  RowMap rm = {T, xpad, ypad, k ? K / (64 * k) : 0, k, {0, 0, 0, 0, 0, 0, 0, 0}};
+  if (k) {
+    if (ldx < K / k) return ECD_EINVAL;
+    for (int j = 0; j < k; ++j) {
+      if (offsets[j] < -xpad || offsets[j] > xpad) return ECD_EINVAL;  // stays in the pad rows
+      rm.off[j] = offsets[j];
+    }
+  }
+  const long xrows = k ? (long)(M / T) * (T + xpad) + xpad : M;  // + the rows after the last
+  if (!x_offsets_fit((int)min(xrows, 0x7FFFFFFFL), ldx)) return ECD_ENOTSUP;
+  return launch_epi(epi, 0, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
+                    ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);
 }
 
 int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, float alpha,

@@ -217,6 +217,18 @@ int ecd_gemm_f16p_prelu(const void* x, long ldx, const void* wp, const float* bi
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                         void* stream);
 
+/* A convolution as this GEMM over implicit tap columns, time-major rows m = b*T + t (M % T == 0):
+ * with k taps, x holds each sequence after xpad zero rows (row b*(T + xpad) + xpad + t) and
+ * K = k*C, the columns of row m being x rows + offsets[j] (|offsets| <= xpad, so they stay in
+ * the zero rows of the padding; the caller also leaves max(offsets) zero rows after the last
+ * sequence); k = 0: x is plain [M, K].  With ypad >= 0, y and res rows are b*(T + ypad) + ypad +
+ * t, else plain.  epi 0 (store, alpha the scale) or 2 (PReLU, alpha the slope).  The causal and
+ * dilated Conv1d and ConvTranspose1d of the codec's waveform decoder (sq_codec.py:32-168)
+ * without materialised columns. */
+int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                       const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
+                       int xpad, int ypad, const int* offsets, int k, int epi, void* stream);
+
 /* ecd_gemm_f16p (epi 0), ecd_gemm_f16p_silu (epi 1, N = 2F, bias/res NULL, alpha 1) or
  * ecd_gemm_f16p_prelu (epi 2, alpha = the slope) with an
  * explicit block tile (cfg 1..13: 128x128, 256x128, 128x256, 128x64, 64x128 or 64x256 features x rows, 2 or 3 LDS
@@ -284,13 +296,13 @@ int ecd_codec_vq_embed(const int64_t* codes, long cb, long cq, const void* books
 
 /* Tap columns of a 1-D convolution for global rows row0 .. row0 + nrows - 1 (row = b*T + t):
  * out[row - row0, j*C + c] = src[b, (t + offsets[j]) / rep, c] for 0 <= t + offsets[j] < T,
- * else 0 (src [B, T / rep, C], row stride ld; k <= 8 taps,
+ * else 0 (src [B, spad + T / rep, C], row stride ld, spad rows before each sequence; k <= 8 taps,
  * rep 1 or 2).  Causal Conv1d: offsets (j - k + 1) * dilation (sq_codec.py:32-73); causal
  * ConvTranspose1d with kernel 2s, stride s (sq_codec.py:76-117): offsets {0, -1}, the GEMM's
  * [T, s*Cout] output being the upsampled [T*s, Cout]; rep 2: PostProcessor's 2x repeat
  * (sq_codec.py:140-146).  C % 8 == 0. */
 int ecd_codec_cols_taps(const void* src, long ld, const int* offsets, int k, void* out, int B,
-                        int T, int C, int rep, long row0, long nrows, void* stream);
+                        int T, int C, int rep, int spad, long row0, long nrows, void* stream);
 
 /* Weight normalisation (torch.nn.utils.parametrizations.weight_norm, dim 0): w[r, :] =
  * fp16(v[r, :] * (g[r] / |v[r, :]|)), fp32 norm, rows of n contiguous values. */

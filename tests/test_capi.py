@@ -42,6 +42,10 @@ def test_signatures_match_header_arity():
         assert nargs == len(argtypes), f"{name}: header has {nargs} args, binding {len(argtypes)}"
 
 
+def _taps(*offsets):
+    return (ctypes.c_int * len(offsets))(*offsets)
+
+
 @pytest.mark.parametrize("call", [
     lambda L: L.ecd_gemv_i8(None, 64, None, None, None, 0, None, 64, 1, 64, 64, 0, None),
     lambda L: L.ecd_gemv_i8(8, 32, 8, 8, None, 0, 8, 64, 1, 64, 64, 0, None),     # ldx < K
@@ -82,6 +86,17 @@ def test_signatures_match_header_arity():
     lambda L: L.ecd_codec_euler(16, 16, 16, 16, 2, 1, 8, 256, 0, 0.1, 1.2, 0.0, 0, None),  # cfg 2
     lambda L: L.ecd_codec_euler(16, None, 16, 16, 1, 1, 8, 256, 4, 0.1, 1.2, 0.0, 0, None),  # blend, no noise
     lambda L: L.ecd_codec_euler(16, 16, 16, 16, 1, 1, 8, 252, 0, 0.1, 1.2, 0.0, 0, None),  # C % 8
+    lambda L: L.ecd_codec_cols_taps(16, 64, _taps(0, -1), 2, 16, 1, 8, 64, 1, 0, 0, 9, None),  # rows > B*T
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 100, 64, 128, 30, 60, -1,
+                                   _taps(0, -1), 2, 0, None),                    # M % T
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
+                                   _taps(-61, 0), 2, 0, None),                   # tap beyond the pad
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 192, 30, 60, -1,
+                                   _taps(0, -1), 2, 0, None),                    # K % (64 k)
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
+                                   _taps(0, -1), 2, 1, None),                    # no SiLU epilogue
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
+                                   None, 2, 0, None),                            # taps missing
 ])
 def test_host_argument_validation(call):
     """Invalid arguments return ECD_EINVAL before any HIP call (no GPU needed)."""
