@@ -35,8 +35,29 @@ namespace ecd {
 
 enum { F16_STORE = 0, F16_SILU = 1, F16_PRELU = 2 };
 
-// wait for every vector-memory and LDS operation of this wave (vmcnt 0, lgkmcnt 0)
-__device__ __forceinline__ void wait_vm0_lgkm0() { __builtin_amdgcn_s_waitcnt(7 << 4); }
+// wait until at most N vector-memory operations of this wave are outstanding and its LDS
+// operations are done (lgkmcnt 0)
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// wait for this wave's DMA of one chunk while the `later` chunks issued after it (uniform,
+// 0 .. MAXL) stay in flight; PER instructions per chunk; LGKM: also drain LDS operations
+template <int PER, int MAXL, bool LGKM>
+__device__ __forceinline__ void wait_chunk(int later) {
+  if constexpr (MAXL >= 3) {
+    if (later >= 3) { if constexpr (LGKM) wait_vm_lgkm0<3 * PER>(); else wait_vm<3 * PER>(); return; }
+  }
+  if constexpr (MAXL >= 2) {
+    if (later >= 2) { if constexpr (LGKM) wait_vm_lgkm0<2 * PER>(); else wait_vm<2 * PER>(); return; }
+  }
+  if constexpr (MAXL >= 1) {
+    if (later >= 1) { if constexpr (LGKM) wait_vm_lgkm0<PER>(); else wait_vm<PER>(); return; }
+  }
+  if constexpr (LGKM) wait_vm_lgkm0<0>(); else wait_vm0();
+}
 
 // A fragments (two k-halves) of the wave's FT weight tiles and B fragments of its RT row tiles
 // for one chunk of LDS stage (lw_st, lx_st).
@@ -97,7 +118,7 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
   constexpr int WI = BN / 16 * 2 / 4;   // weight DMA instructions per wave per chunk (1 KB each)
   constexpr int XI = BM / 8 / 4;        // x DMA instructions per wave per chunk (8 rows each)
   constexpr int PER_CHUNK = WI + XI;
-  static_assert(PER_CHUNK * (NS - 2) < 64, "vmcnt range");
+  static_assert(NS >= 2 && NS <= 4 && PER_CHUNK * (NS - 1) < 64, "vmcnt range");
   __shared__ __align__(16) f16 lw[NS][BN / 16 * 1024];  // BN / 16 tiles x 2 KB
   __shared__ __align__(16) f16 lx[NS][BM * 64];         // BM rows x 128 B
 
@@ -175,18 +196,16 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
     for (int rt = 0; rt < RT; ++rt) acc[ft][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   if constexpr (PL) {
-    // Software-pipelined (2 stages): the fragments of chunk c + 1 are read from LDS while the
-    // second k-half MFMAs of chunk c run, and the wait + barrier for chunk c + 1 sit behind the
-    // first k-half MFMAs, so no MFMA waits for an LDS read at a chunk boundary.
-    static_assert(NS == 2, "pipelined loop uses two stages");
+    // Software-pipelined: the fragments of chunk c + 1 are read from LDS while the second
+    // k-half MFMAs of chunk c run, and the wait + barrier for chunk c + 1 sit behind the first
+    // k-half MFMAs, so no MFMA waits for an LDS read at a chunk boundary.  Chunk c + NS goes
+    // into the stage of chunk c (its fragments are in registers by then), so NS - 1 chunks of
+    // DMA stay in flight behind the one being computed.
     f16x8 wa0[FT], wb0[FT], fa0[RT], fb0[RT], wa1[FT], wb1[FT], fa1[RT], fb1[RT];
-    issue(0, 0);
-    if (nch > 1) {
-      issue(1, 1);
-      wait_vm<PER_CHUNK>();
-    } else {
-      wait_vm0();
-    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      if (s < nch) issue(s, s);
+    wait_chunk<PER_CHUNK, NS - 1, false>(min(NS - 1, nch - 1));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -196,13 +215,14 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
     do {                                                                                  \
       f16_mfma_half<FT, RT>(acc, wa, fa);                                                 \
       if ((c) + 1 < nch) {                                                                \
-        wait_vm0_lgkm0(); /* own DMA of c + 1 landed, own reads of c done */              \
+        /* own DMA of c + 1 landed (later chunks may fly), own reads of c done */         \
+        wait_chunk<PER_CHUNK, NS - 2, true>(min(NS - 2, nch - 2 - (c)));                  \
         asm volatile("" ::: "memory");                                                    \
         __builtin_amdgcn_s_barrier();                                                     \
         asm volatile("" ::: "memory");                                                    \
-        if ((c) + 2 < nch) issue((c) + 2, (c) & 1);                                       \
-        f16_frags<FT, RT>(lw[((c) + 1) & 1], lx[((c) + 1) & 1], wn, wm, lane, na, nb, nfa, \
-                          nfb);                                                           \
+        if ((c) + NS < nch) issue((c) + NS, (c) % NS);                                    \
+        const int sn = ((c) + 1) % NS;                                                    \
+        f16_frags<FT, RT>(lw[sn], lx[sn], wn, wm, lane, na, nb, nfa, nfb);                \
       }                                                                                   \
       f16_mfma_half<FT, RT>(acc, wb, fb);                                                 \
     } while (0)
@@ -217,10 +237,7 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
     if (s < nch) issue(s, s);
   for (int c = 0; c < nch; ++c) {
     // chunk c landed for this wave: later chunks c + 1 .. c + NS - 2 may still be in flight
-    if (NS == 3 && c + 1 < nch)
-      wait_vm<(NS == 3 ? PER_CHUNK : 0)>();
-    else
-      wait_vm0();
+    wait_chunk<PER_CHUNK, NS - 2, false>(min(NS - 2, nch - 1 - c));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // chunk c visible to every wave; stage of c - 1 free
     asm volatile("" ::: "memory");
@@ -323,6 +340,8 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 //  11: 128 x 64, waves 2 x 2 (64 x 32 each), software-pipelined, 48 KB
 //  12: 64 x 128, waves 1 x 4 (64 x 32 each), software-pipelined, 48 KB (outputs <= 64 wide)
 //  13: 64 x 256, waves 1 x 4 (64 x 64 each), software-pipelined, 80 KB
+//  14: as 11 with 4 stages, 96 KB (narrow outputs over long K: 256 x 9216 74 -> 60 us at
+//      M = 1488; 3 or 4 stages lose 10-50% on every wider estimator shape)
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
@@ -340,9 +359,9 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
 
 // Library default per shape (N counts output features before the SiLU pairing).
 static int default_cfg(int M, int N, int K, bool silu) {
-  (void)K;
   if (silu) return 8;
   if (N <= 64) return 12;                  // the decoder's 64-channel convs: 64-feature tiles
+  if (N <= 256 && K >= 4096 && M <= 16384) return 14;  // few blocks, long K: 4 stages in flight
   if (N <= 1536 && M <= 16384) return 10;  // narrow outputs, few rows: 128 x 64 for more blocks
   if (N <= 1024) return 1;                 // the decoder's wider convs over many rows
   return 8;
@@ -367,6 +386,7 @@ static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const floa
     case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 14: return launch_cfg<EPI, 2, 2, 4, 2, 4, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     default: return ECD_EINVAL;
   }
 }
@@ -408,7 +428,7 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                         int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || cfg < 0 || cfg > 13 || epi < 0 || epi > 2)
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 14 || epi < 0 || epi > 2)
     return ECD_EINVAL;
   const bool silu = epi == F16_SILU;
   if (silu) {
