@@ -340,8 +340,8 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 //  11: 128 x 64, waves 2 x 2 (64 x 32 each), software-pipelined, 48 KB
 //  12: 64 x 128, waves 1 x 4 (64 x 32 each), software-pipelined, 48 KB (outputs <= 64 wide)
 //  13: 64 x 256, waves 1 x 4 (64 x 64 each), software-pipelined, 80 KB
-//  14: as 11 with 4 stages, 96 KB (narrow outputs over long K: 256 x 9216 74 -> 60 us at
-//      M = 1488; 3 or 4 stages lose 10-50% on every wider estimator shape)
+//  14: 64 x 64, waves 2 x 2 (32 x 32 each), software-pipelined, 32 KB
+//  15: as 14 with 3 stages, 48 KB
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
@@ -361,8 +361,8 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
 static int default_cfg(int M, int N, int K, bool silu) {
   if (silu) return 8;
   if (N <= 64) return 12;                  // the decoder's 64-channel convs: 64-feature tiles
-  if (N <= 256 && K >= 4096 && M <= 16384) return 14;  // few blocks, long K: 4 stages in flight
-  if (N <= 1536 && M <= 16384) return 10;  // narrow outputs, few rows: 128 x 64 for more blocks
+  if (N <= 256 && K >= 4096 && M <= 16384) return 15;  // few blocks, long K: 3 stages in flight
+  if (N <= 1536 && M <= 16384) return 14;  // narrow outputs, few rows: 64 x 64 for more blocks
   if (N <= 1024) return 1;                 // the decoder's wider convs over many rows
   return 8;
 }
@@ -386,7 +386,8 @@ static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const floa
     case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 14: return launch_cfg<EPI, 2, 2, 4, 2, 4, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 14: return launch_cfg<EPI, 2, 2, 2, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 15: return launch_cfg<EPI, 2, 2, 2, 2, 3, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
     default: return ECD_EINVAL;
   }
 }
@@ -428,7 +429,7 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                         int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || cfg < 0 || cfg > 14 || epi < 0 || epi > 2)
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 15 || epi < 0 || epi > 2)
     return ECD_EINVAL;
   const bool silu = epi == F16_SILU;
   if (silu) {
