@@ -184,8 +184,11 @@ class LlamaTransformer:
 
     # ------------------------------------------------------------ buffers
     def _buffers(self, B: int, T: int):
+        """Work buffers for B sequences of T frames, cached for the latest shape only (a new
+        shape releases the old buffers to torch's stream-ordered allocator)."""
         key = (B, T)
         if key not in self._bufs:
+            self._bufs.clear()
             M, D2 = B * T, self.D2
             F2 = max(b.F for b in self.blocks + self.blocks_2)
             cmax = max(self.cin + self.D, D2, self.cin)
@@ -635,6 +638,7 @@ class ScalarDecoder:
         self.final = _Conv(wn(f"decoder.{n_post + 1}."), get(f"decoder.{n_post + 1}.bias"), causal)
         self.num_bands = num_bands
         self._bufs = {}
+        self._shape = None
 
     @classmethod
     def from_codec_state_dict(cls, sd: dict, prefix="scalar_model.", **cfg):
@@ -695,6 +699,9 @@ class ScalarDecoder:
         fp16, S = the channel groups (the two stereo channels), up = prod(factors) * 2."""
         _, T, W = latent.shape
         S = W // self.latent_dim
+        if self._shape != (S, T):  # buffers are cached for the latest window shape only
+            self._bufs.clear()
+            self._shape = (S, T)
         st = stream_ptr(self.dev)
         P = self.PAD
         lat = latent.to(self.dev, torch.float16).contiguous()

@@ -242,8 +242,8 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
  * cache slots [0, pos[r]] of kc, vc [B, Hk, L, HD] (the prompt's K/V already written), with the
  * decode kernel's numerics (fp32 scores, running max, fp16 probabilities into P.V, fp32 sums).
  * Replaces the causal scaled_dot_product_attention of the prompt pass (app/engine.py:123-153,
- * :174-178).  o [B * S, Hq * HD].  HD in {64, 128}; Hq / Hk in {1, 2, 3, 4}; q, kc, vc 16-byte and
- * o 8-byte aligned.  With pos[r] = S - 1 for every row and L = S it is non-causal attention over
+ * :174-178).  o [B * S, Hq * HD].  HD in {64, 128}; Hq / Hk in {1, 2, 3, 4}; scale > 0; q, kc,
+ * vc 16-byte and o 8-byte aligned.  With pos[r] = S - 1 for every row and L = S it is non-causal attention over
  * the sequence (the codec estimator, app/heartcodec/models/transformer.py:117-125). */
 int ecd_prefill_attn(const void* q, const void* kc, const void* vc, const int64_t* pos, void* o,
                      int B, int S, int Hq, int Hk, int L, int HD, float scale, void* stream);

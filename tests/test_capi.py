@@ -68,6 +68,7 @@ def _taps(*offsets):
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 24, 8, 64, 96, 0.1, None),    # HD 96
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 40, 8, 64, 128, 0.1, None),   # G = 5
     lambda L: L.ecd_prefill_attn(18, 16, 16, 16, 16, 1, 8, 24, 8, 64, 128, 0.1, None),   # q align
+    lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 24, 8, 64, 128, 0.0, None),   # scale <= 0
     lambda L: L.ecd_codec_rope_table(16, 8, 63, None),                             # odd HD
     lambda L: L.ecd_codec_rope_heads(16, 192, 16, 16, 16, 16, 1, 8, 1, 60, None),   # HD % 8
     lambda L: L.ecd_codec_rope_heads(16, 100, 16, 16, 16, 16, 1, 8, 1, 64, None),   # ldq < 3D
