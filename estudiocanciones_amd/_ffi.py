@@ -36,6 +36,8 @@ SIGNATURES = {
     "ecd_copy_bytes": [_P, _P, c_long, _P],
     "ecd_codec_rope_table": [_P, c_int, c_int, _P],
     "ecd_codec_rope_heads": [_P, c_long, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P],
+    "ecd_gemm_f16p_rope": [_P, c_long, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
+                           _P],
     "ecd_codec_norm_mod": [_P, _P, _P, _P, c_long, _P, _P, _P, _P, _P, c_long, _P, c_int, c_int,
                            c_int, c_int, c_float, _P],
     "ecd_codec_cols3": [_P, _P, _P, _P, _P, _P, c_int, _P, c_int, c_int, _P],

@@ -8,7 +8,7 @@ Mirrors ``LlamaTransformer`` with ``norm_type="ada_norm_single"``
     ProjectLayer (k = 3 conv + Linear)   ecd_codec_cols3 + ecd_gemm_f16p (x2)
     adaLN + RMSNorm / gated residual     ecd_codec_norm_mod
     q | k | v projection                 ecd_gemm_f16p (one GEMM, N = 3D)
-    interleaved RoPE -> heads            ecd_codec_rope_heads
+    q | k | v linear + interleaved RoPE  ecd_gemm_f16p_rope (ecd_codec_rope_heads standalone)
     non-causal SDPA                      ecd_prefill_attn (every row at the last slot)
     LlamaMLP                             ecd_gemm_f16p_silu + ecd_gemm_f16p
     timestep path                        ecd_codec_timestep, ecd_gemm_f16p, ecd_codec_silu
@@ -194,7 +194,7 @@ class LlamaTransformer:
             cmax = max(self.cin + self.D, D2, self.cin)
             e = lambda *s: torch.empty(*s, device=self.dev, dtype=torch.float16)
             self._bufs[key] = dict(
-                cols=e(M * 3 * cmax), t1=e(M * D2), x=e(M * D2), y=e(M * D2), qkv=e(M * 3 * D2),
+                cols=e(M * 3 * cmax), t1=e(M * D2), x=e(M * D2), y=e(M * D2),
                 q=e(M * D2), k=e(M * D2), v=e(M * D2), o=e(M * D2), h=e(M * D2), m=e(M * F2),
                 out=e(M, self.cout),
                 pos=torch.full((M,), T - 1, device=self.dev, dtype=torch.int64))
@@ -251,13 +251,13 @@ class LlamaTransformer:
             y = buf["y"][:M * D].view(M, D)
             self._norm(x, h, None if gate is None else gate + (tm_ld,), bp.attn_norm, ch(0), ch(1),
                        tm_ld, y, T, 0)
-            qkv = bp.qkv(y, buf["qkv"][:M * 3 * D].view(M, 3 * D))
             q = buf["q"][:M * D].view(M, D)
             k = buf["k"][:M * D].view(B, H, T, HD)
             v = buf["v"][:M * D].view(B, H, T, HD)
-            _ffi.call("ecd_codec_rope_heads", qkv.data_ptr(), qkv.stride(0),
+            # q | k | v projection with RoPE and the head layout in the GEMM epilogue
+            _ffi.call("ecd_gemm_f16p_rope", y.data_ptr(), D, bp.qkv.wp.data_ptr(), None,
                       self._rope_table(T, HD).data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                      B, T, H, HD, st)
+                      M, T, H, HD, D, st)
             o = prefill_attn(q, k, v, buf["pos"][:M], T, H, H, out=buf["o"][:M * D].view(M, D))
             ha = bp.o(o, buf["h"][:M * D].view(M, D))
             g_a = ch(2) + (tm_ld,)

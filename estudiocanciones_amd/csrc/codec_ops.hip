@@ -81,10 +81,11 @@ __global__ __launch_bounds__(256) void codec_rope_heads_kernel(
     f16x8 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float co = (float)cs[2 * j], si = (float)cs[2 * j + 1];
-      const float x1 = (float)xv[2 * j], x2 = (float)xv[2 * j + 1];
-      o[2 * j] = (f16)(rnd(x1 * co) - rnd(x2 * si));
-      o[2 * j + 1] = (f16)(rnd(x1 * si) + rnd(x2 * co));
+      f16 a, c;
+      rope_pair_f16((float)xv[2 * j], (float)xv[2 * j + 1], (float)cs[2 * j], (float)cs[2 * j + 1],
+                    a, c);
+      o[2 * j] = a;
+      o[2 * j + 1] = c;
     }
     if (!is_k)
       *(f16x8*)(q + (long)r * D + c) = o;

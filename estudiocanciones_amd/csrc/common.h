@@ -124,6 +124,16 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, void* 
                : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
 }
 
+// RoPE on one interleaved pair with the rounding of eager fp16 ops: each product rounded to
+// fp16, then the difference / sum in fp32 rounded to fp16; contraction off, so no product
+// fuses into the sum (the codec estimator's apply_rope_vec).
+__device__ __forceinline__ void rope_pair_f16(float x1, float x2, float co, float si, f16& o1,
+                                              f16& o2) {
+#pragma clang fp contract(off)
+  o1 = (f16)((float)(f16)(x1 * co) - (float)(f16)(x2 * si));
+  o2 = (f16)((float)(f16)(x1 * si) + (float)(f16)(x2 * co));
+}
+
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
 __device__ __host__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);

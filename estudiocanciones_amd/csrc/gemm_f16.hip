@@ -33,7 +33,7 @@
 
 namespace ecd {
 
-enum { F16_STORE = 0, F16_SILU = 1, F16_PRELU = 2 };
+enum { F16_STORE = 0, F16_SILU = 1, F16_PRELU = 2, F16_ROPE = 3 };
 
 // wait until at most N vector-memory operations of this wave are outstanding and its LDS
 // operations are done (lgkmcnt 0)
@@ -101,6 +101,15 @@ struct RowMap {
   int off[8];
 };
 
+// Output of the q | k | v projection with RoPE (F16_ROPE): features [0, D) are q, [D, 2D) k,
+// [2D, 3D) v, D = H * HD, rows m = b * T + t.  q and k pairs (2i, 2i + 1) are rotated by
+// tab[t, i] = (cos, sin) (fp16); q goes to rows [M, D], k and v to [B, H, T, HD].
+struct RopeOut {
+  const f16* tab;
+  f16 *q, *k, *v;
+  int T, H, HD;
+};
+
 __device__ __forceinline__ long seq_row(long m, int T, int pad) {
   const long b = m / T;
   return b * (T + pad) + pad + (m - b * T);
@@ -111,7 +120,8 @@ template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL>
 __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel(
     const f16* __restrict__ x, long ldx, const f16* __restrict__ wp,
     const float* __restrict__ bias, float alpha, const f16* __restrict__ res, long ldr,
-    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb, RowMap rm) {
+    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb, RowMap rm,
+    RopeOut ro) {
   static_assert(WN * WM == 4, "four waves");
   constexpr int BN = 16 * WN * FT;      // features per block
   constexpr int BM = 16 * WM * RT;      // rows per block
@@ -254,10 +264,29 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
   // y (and res) are 8-byte aligned the four values go out as one 8-byte store.
   const bool vec = ((ldy & 3) == 0) && (((uintptr_t)y & 7) == 0) &&
                    (!res || (((ldr & 3) == 0) && (((uintptr_t)res & 7) == 0)));
+  // F16_ROPE: the batch item and time step of each of this lane's row tiles
+  int rb[RT], rtm[RT];
+  if constexpr (EPI == F16_ROPE) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int mm = min(m0 + (wm * RT + rt) * 16 + (lane & 15), M - 1);
+      rb[rt] = mm / ro.T;
+      rtm[rt] = mm - rb[rt] * ro.T;
+    }
+  }
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft) {
     const int nb = n0 + (wn * FT + ft) * 16 + 4 * (lane >> 4);
     if (nb >= N) continue;
+    // F16_ROPE: section (q, k, v), head and offset of this lane's 4 features
+    int sec = 0, hc = 0, hh = 0, d = 0;
+    if constexpr (EPI == F16_ROPE) {
+      const int D = ro.H * ro.HD;
+      sec = nb >= 2 * D ? 2 : (nb >= D ? 1 : 0);
+      hc = nb - sec * D;
+      hh = hc / ro.HD;
+      d = hc - hh * ro.HD;
+    }
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
     if (bias) {
 #pragma unroll
@@ -292,6 +321,19 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
             }
           }
         }
+      } else if (EPI == F16_ROPE) {  // 4 features never straddle a head (HD % 4 == 0)
+        const int t = rtm[rt];
+        if (sec < 2) {
+          const f16x4 cs = *(const f16x4*)(ro.tab + (long)t * ro.HD + d);  // pairs d/2, d/2 + 1
+          f16 o0, o1, o2, o3;
+          rope_pair_f16((float)yv[0], (float)yv[1], (float)cs[0], (float)cs[1], o0, o1);
+          rope_pair_f16((float)yv[2], (float)yv[3], (float)cs[2], (float)cs[3], o2, o3);
+          yv = (f16x4){o0, o1, o2, o3};
+        }
+        f16* dst = sec == 0 ? ro.q + m * (ro.H * ro.HD) + hc
+                            : (sec == 1 ? ro.k : ro.v) +
+                                  (((long)rb[rt] * ro.H + hh) * ro.T + t) * ro.HD + d;
+        *(f16x4*)dst = yv;
       } else {  // (a_j, b_j, a_j+1, b_j+1) with j = nb / 2; N even
         const int j = nb >> 1;
         const float a0 = (float)yv[0], a1 = (float)yv[2];
@@ -345,7 +387,7 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
-                      const RowMap& rm, hipStream_t st) {
+                      const RowMap& rm, const RopeOut& ro, hipStream_t st) {
   constexpr int BN = 16 * WN * FT, BM = 16 * WM * RT;
   const int nfb = (N + BN - 1) / BN;
   const int nmb = (M + BM - 1) / BM;
@@ -353,7 +395,7 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
   hipLaunchKernelGGL((gemm_f16w_kernel<EPI, WN, WM, FT, RT, NS, PL>), dim3((unsigned)blocks),
                      dim3(256), 0, st, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, nfb,
-                     nmb, rm);
+                     nmb, rm, ro);
   return ecd_launch_status();
 }
 
@@ -370,24 +412,24 @@ static int default_cfg(int M, int N, int K, bool silu) {
 template <int EPI>
 static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const float* bias,
                       float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N,
-                      int K, const RowMap& rm, hipStream_t st) {
+                      int K, const RowMap& rm, const RopeOut& ro, hipStream_t st) {
   if (cfg == 0) cfg = default_cfg(M, N, K, EPI == F16_SILU);
   switch (cfg) {
-    case 1: return launch_cfg<EPI, 4, 1, 2, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 2: return launch_cfg<EPI, 2, 2, 4, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 3: return launch_cfg<EPI, 4, 1, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 4: return launch_cfg<EPI, 4, 1, 4, 8, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 5: return launch_cfg<EPI, 2, 2, 8, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 6: return launch_cfg<EPI, 2, 2, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 7: return launch_cfg<EPI, 2, 2, 4, 4, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 8: return launch_cfg<EPI, 2, 2, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 14: return launch_cfg<EPI, 2, 2, 2, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-    case 15: return launch_cfg<EPI, 2, 2, 2, 2, 3, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    case 1: return launch_cfg<EPI, 4, 1, 2, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 2: return launch_cfg<EPI, 2, 2, 4, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 3: return launch_cfg<EPI, 4, 1, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 4: return launch_cfg<EPI, 4, 1, 4, 8, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 5: return launch_cfg<EPI, 2, 2, 8, 4, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 6: return launch_cfg<EPI, 2, 2, 4, 8, 2>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 7: return launch_cfg<EPI, 2, 2, 4, 4, 3>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 8: return launch_cfg<EPI, 2, 2, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 9: return launch_cfg<EPI, 4, 1, 2, 8, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 10: return launch_cfg<EPI, 4, 1, 2, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 11: return launch_cfg<EPI, 2, 2, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 12: return launch_cfg<EPI, 1, 4, 4, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 14: return launch_cfg<EPI, 2, 2, 2, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 15: return launch_cfg<EPI, 2, 2, 2, 2, 3, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
     default: return ECD_EINVAL;
   }
 }
@@ -395,11 +437,15 @@ static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const floa
 static int launch_epi(int epi, int cfg, const f16* x, long ldx, const f16* wp, const float* bias,
                       float alpha, const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
                       const RowMap& rm, hipStream_t st) {
+  const RopeOut ro = {nullptr, nullptr, nullptr, nullptr, 1, 1, 4};
   if (epi == F16_SILU)
-    return launch_f16<F16_SILU>(cfg, x, ldx, wp, nullptr, 1.0f, nullptr, 0, y, ldy, M, N, K, rm, st);
+    return launch_f16<F16_SILU>(cfg, x, ldx, wp, nullptr, 1.0f, nullptr, 0, y, ldy, M, N, K, rm,
+                                ro, st);
   if (epi == F16_PRELU)
-    return launch_f16<F16_PRELU>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
-  return launch_f16<F16_STORE>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, st);
+    return launch_f16<F16_PRELU>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro,
+                                 st);
+  return launch_f16<F16_STORE>(cfg, x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro,
+                               st);
 }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -442,6 +488,22 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
   const RowMap rm = {0, 0, -1, 0, 0, {0, 0, 0, 0, 0, 0, 0, 0}};
   return launch_epi(epi, cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
                     ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);
+}
+
+int ecd_gemm_f16p_rope(const void* x, long ldx, const void* wp, const float* bias,
+                       const void* tab, void* q, void* k, void* v, int M, int T, int H, int HD,
+                       int K, void* stream) {
+  const long N = 3L * H * HD;
+  if (!x || !wp || !tab || !q || !k || !v || M <= 0 || T <= 0 || M % T || H <= 0 || HD <= 0 ||
+      (HD % 4) || N > 0x7FFFFFFFL || K <= 0 || (K % 64) || ldx < K || (ldx % 8) || !al16(x) ||
+      !al16(wp) || ((uintptr_t)tab & 7) || ((uintptr_t)q & 7) || ((uintptr_t)k & 7) ||
+      ((uintptr_t)v & 7))
+    return ECD_EINVAL;
+  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
+  const RowMap rm = {0, 0, -1, 0, 0, {0, 0, 0, 0, 0, 0, 0, 0}};
+  const RopeOut ro = {(const f16*)tab, (f16*)q, (f16*)k, (f16*)v, T, H, HD};
+  return launch_f16<F16_ROPE>(0, (const f16*)x, ldx, (const f16*)wp, bias, 1.0f, nullptr, 0,
+                              nullptr, 0, M, (int)N, K, rm, ro, (hipStream_t)stream);
 }
 
 int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,

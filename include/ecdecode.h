@@ -261,6 +261,16 @@ int ecd_codec_rope_table(void* tab, int T, int HD, void* stream);
 int ecd_codec_rope_heads(const void* qkv, long ldq, const void* tab, void* q, void* k, void* v,
                          int B, int T, int H, int HD, void* stream);
 
+/* The q | k | v projection with the RoPE above fused into the GEMM epilogue:
+ * qkv = fp16(x @ w^T + bias) (ecd_gemm_f16p, w packed [3 H HD, K]), then q, k, v as
+ * ecd_codec_rope_heads writes them (same rounding, bit for bit), without the qkv buffer.
+ * x [M, K] (M = B T rows b T + t), tab as above, q [M, H HD], k and v [B, H, T, HD], 8-byte
+ * aligned; HD % 4 == 0.  Replaces to_q / to_k / to_v + apply_rope_vec (transformer.py:108-122,
+ * 219-226) in one launch. */
+int ecd_gemm_f16p_rope(const void* x, long ldx, const void* wp, const float* bias,
+                       const void* tab, void* q, void* k, void* v, int M, int T, int H, int HD,
+                       int K, void* stream);
+
 /* Row r of x [R, D] (batch r / T): with h, x = fp16(x + fp16(fp16(g_tab + g_tm[b]) * h)) in
  * place (the gated residual, transformer.py:241-248); then norm 0 = RMSNorm with weight w
  * (:9-18), norm 1 = LayerNorm without affine (:333-334), and

@@ -98,6 +98,9 @@ def _taps(*offsets):
                                    _taps(0, -1), 2, 1, None),                    # no SiLU epilogue
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
                                    None, 2, 0, None),                            # taps missing
+    lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 90, 30, 2, 62, 64, None),  # HD % 4
+    lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 100, 30, 2, 64, 64, None),  # M % T
+    lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 12, 16, 90, 30, 2, 64, 64, None),  # k align
 ])
 def test_host_argument_validation(call):
     """Invalid arguments return ECD_EINVAL before any HIP call (no GPU needed)."""

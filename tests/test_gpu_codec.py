@@ -154,6 +154,40 @@ def test_codec_rope_heads_bit_exact(dev, B, L, H, HD):
     assert np.array_equal(N_(v), heads(qkv[:, 2 * D:]))
 
 
+@pytest.mark.parametrize("B,L,H,HD,K", [(2, 37, 3, 64, 192), (1, 130, 2, 128, 256), (2, 9, 5, 64, 64)])
+def test_gemm_f16_rope_fused(dev, B, L, H, HD, K):
+    """The q | k | v GEMM with RoPE in its epilogue equals the GEMM followed by the standalone
+    RoPE kernel bit for bit (q rows, k and v heads), with and without a bias."""
+    import torch
+    from estudiocanciones_amd.kernels import pack_f16
+    D, M = H * HD, B * L
+    g = rng(560 + HD + L)
+    x = randn16(561 + L, M, K)
+    w = f16(g.standard_normal((3 * D, K)) * 0.05)
+    sin, cos = OC.rope_table(L, HD)
+    tab = D_(np.stack([cos, sin], -1).astype(np.float16), dev)
+    xt, wp = D_(x, dev), pack_f16(D_(w, dev))
+    for bias in (None, D_((g.standard_normal(3 * D) * 0.1).astype(np.float32), dev)):
+        bp = None if bias is None else bias.data_ptr()
+        qkv = torch.empty(M, 3 * D, dtype=torch.float16, device=dev)
+        _call("ecd_gemm_f16p", xt.data_ptr(), K, wp.data_ptr(), bp, 1.0, None, 0, qkv.data_ptr(),
+              3 * D, M, 3 * D, K)
+        outs = []
+        for fused in (False, True):
+            q = torch.empty(M, D, dtype=torch.float16, device=dev)
+            k = torch.empty(B, H, L, HD, dtype=torch.float16, device=dev)
+            v = torch.empty_like(k)
+            if fused:
+                _call("ecd_gemm_f16p_rope", xt.data_ptr(), K, wp.data_ptr(), bp, tab.data_ptr(),
+                      q.data_ptr(), k.data_ptr(), v.data_ptr(), M, L, H, HD, K)
+            else:
+                _call("ecd_codec_rope_heads", qkv.data_ptr(), 3 * D, tab.data_ptr(), q.data_ptr(),
+                      k.data_ptr(), v.data_ptr(), B, L, H, HD)
+            outs.append((N_(q), N_(k), N_(v)))
+        for name, a, b in zip("qkv", outs[0], outs[1]):
+            _exact(b, a, f"fused rope {name} (H={H} HD={HD} bias={bias is not None})")
+
+
 # ---------------------------------------------------------------- norms + adaLN
 @pytest.mark.parametrize("norm,resid,per_batch,D", [(0, False, False, 1536), (0, True, True, 3072),
                                                     (1, True, False, 1536), (1, False, True, 128),
