@@ -384,6 +384,7 @@ __global__ __launch_bounds__(256) void pack_f16_kernel(const f16* __restrict__ w
 //  13: 64 x 256, waves 1 x 4 (64 x 64 each), software-pipelined, 80 KB
 //  14: 64 x 64, waves 2 x 2 (32 x 32 each), software-pipelined, 32 KB
 //  15: as 14 with 3 stages, 48 KB
+//  16: 128 x 96, waves 2 x 2 (64 x 48 each), software-pipelined, 56 KB
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL = false>
 static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, float alpha,
                       const f16* res, long ldr, f16* y, long ldy, int M, int N, int K,
@@ -401,11 +402,15 @@ static int launch_cfg(const f16* x, long ldx, const f16* wp, const float* bias, 
 
 // Library default per shape (N counts output features before the SiLU pairing).
 static int default_cfg(int M, int N, int K, bool silu) {
+  // blocks of 128 x 128: below 256 (one per CU) or 512 (the two that fit per CU) a smaller block
+  // fills the resident slots that 128 x 128 leaves empty
+  const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
   if (silu) return 8;
-  if (N <= 64) return 12;                  // the decoder's 64-channel convs: 64-feature tiles
-  if (N <= 256 && K >= 4096 && M <= 16384) return 15;  // few blocks, long K: 3 stages in flight
-  if (N <= 1536 && M <= 16384) return 14;  // narrow outputs, few rows: 64 x 64 for more blocks
-  if (N <= 1024) return 1;                 // the decoder's wider convs over many rows
+  if (N <= 64) return 12;                            // the decoder's 64-channel convs
+  if (N <= 256 && K >= 4096 && t128 < 256) return 15;  // few blocks, long K: 3 stages in flight
+  if (N <= 1536 && t128 < 256) return 14;            // 64 x 64
+  if (N <= 3072 && t128 < 512) return 16;            // 128 x 96
+  if (N <= 1024) return 1;                           // the decoder's wider convs over many rows
   return 8;
 }
 
@@ -430,6 +435,7 @@ static int launch_f16(int cfg, const f16* x, long ldx, const f16* wp, const floa
     case 13: return launch_cfg<EPI, 1, 4, 4, 4, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
     case 14: return launch_cfg<EPI, 2, 2, 2, 2, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
     case 15: return launch_cfg<EPI, 2, 2, 2, 2, 3, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
+    case 16: return launch_cfg<EPI, 2, 2, 4, 3, 2, true>(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, rm, ro, st);
     default: return ECD_EINVAL;
   }
 }
@@ -475,7 +481,7 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
                         const void* res, long ldr, void* y, long ldy, int M, int N, int K,
                         int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || ldx < K || (ldx % 8) ||
-      !al16(x) || !al16(wp) || cfg < 0 || cfg > 15 || epi < 0 || epi > 2)
+      !al16(x) || !al16(wp) || cfg < 0 || cfg > 16 || epi < 0 || epi > 2)
     return ECD_EINVAL;
   const bool silu = epi == F16_SILU;
   if (silu) {

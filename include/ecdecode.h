@@ -231,7 +231,7 @@ int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bia
 
 /* ecd_gemm_f16p (epi 0), ecd_gemm_f16p_silu (epi 1, N = 2F, bias/res NULL, alpha 1) or
  * ecd_gemm_f16p_prelu (epi 2, alpha = the slope) with an
- * explicit block tile (cfg 1..15: 128x128, 256x128, 128x256, 128x64, 64x128, 64x256 or 64x64 features x rows,
+ * explicit block tile (cfg 1..16: 128x128, 256x128, 128x256, 128x64, 64x128, 64x256, 64x64 or 128x96 features x rows,
  * 2 to 4 LDS stages; 0 = the library's choice).  Replaces nothing in the reference: the launch-shape knob
  * of the codec GEMMs, for sweeps. */
 int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bias, float alpha,

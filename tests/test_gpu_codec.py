@@ -104,7 +104,7 @@ def test_gemm_f16_tile_configs_agree(dev, M, N, K, silu):
     xt, wp = D_(x, dev), pack_f16(D_(w, dev), interleave=bool(silu))
     No = N // 2 if silu else N
     outs = []
-    for cfg in range(0, 16):
+    for cfg in range(0, 17):
         y = torch.empty(M, No, dtype=torch.float16, device=dev)
         _call("ecd_gemm_f16p_tuned", xt.data_ptr(), K, wp.data_ptr(),
               None if b is None else b.data_ptr(), 1.0 if silu else 0.75,
