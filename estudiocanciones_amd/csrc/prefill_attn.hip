@@ -35,8 +35,8 @@ constexpr int PA_QB = 64;            // rows per workgroup (4 waves x 16)
 constexpr int PA_KT = 64;            // cache slots per tile
 
 // V^T word (d, slot pair w) lives at d * 32 + (w ^ vt_swz(d)): the swizzle keeps word pairs
-// together (8-byte fragment reads) and spreads both the fragment reads (16 d rows x 4 lane
-// groups per half-wave) and the staging writes over the banks
+// together (8-byte fragment reads), puts the fragment reads of a half-wave (16 d rows x 2 lane
+// groups) on distinct banks and keeps the staging writes at most 2-way conflicted
 __device__ __forceinline__ int vt_swz(int d) { return 4 * (((d >> 1) ^ (d >> 3)) & 7); }
 
 template <int HD, int G>
@@ -61,7 +61,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(
   const int s = blockIdx.x * PA_QB + 16 * wv + col;   // this lane's row within the batch item
   const bool rowok = s < S;
   const long r = (long)b * S + (rowok ? s : 0);
-  const int p = rowok ? min((int)pos[r], L - 1) : -1;  // attends [0, p]; -1: no row
+  // attends [0, p] with p clamped to [-1, L - 1]; -1: nothing (no row, or a negative position)
+  const long praw = rowok ? pos[r] : -1;
+  const int p = praw < 0 ? -1 : (int)min(praw, (long)L - 1);
 
   // tiles needed by the workgroup: up to the largest attended slot of its rows
   const int pw = (int)wave_max_u32((uint32_t)(p + 1));

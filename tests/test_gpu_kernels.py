@@ -270,6 +270,23 @@ def test_prefill_attn(dev, B, S, Hq, Hk, L, off, HD):
     assert_close16(N(got), N(o), what="prefill attn vs decode kernel")
 
 
+def test_prefill_attn_positions_clamped(dev):
+    """Positions outside the cache: a negative one attends nothing (zero output), one past the
+    cache attends the whole cache, like the decode kernel's clamp; other rows are unaffected."""
+    from estudiocanciones_amd.kernels import prefill_attn
+    B, S, Hq, Hk, L, HD = 1, 70, 4, 2, 96, 128
+    q = randn16(80, B * S, Hq * HD)
+    kc = randn16(81, B, Hk, L, HD)
+    vc = randn16(82, B, Hk, L, HD)
+    pos = np.arange(S, dtype=np.int64) + 10
+    pos[3], pos[40] = -5, 1 << 40
+    got = N(prefill_attn(T(q, dev), T(kc, dev), T(vc, dev), T(pos, dev), S, Hq, Hk))
+    assert not np.any(got[3]), "a negative position attends nothing"
+    ok = pos >= 0
+    want = OK.attention_exact(q[ok], kc, vc, np.minimum(pos[ok], L - 1), int(ok.sum()), Hq, Hk, HD)
+    assert_close16(got[ok], want, what="clamped positions")
+
+
 @pytest.mark.parametrize("B,Ls,H,HD", [(2, 100, 4, 64), (2, 70, 2, 128)])
 def test_prefill_attn_full_sequence(dev, B, Ls, H, HD):
     """Every position at the last slot: non-causal attention over the whole sequence (the codec
