@@ -409,6 +409,7 @@ static int default_cfg(int M, int N, int K, bool silu) {
   if (N <= 64) return 12;                            // the decoder's 64-channel convs
   if (N <= 256 && K >= 4096 && t128 < 256) return 15;  // few blocks, long K: 3 stages in flight
   if (N <= 1536 && t128 < 256) return 14;            // 64 x 64
+  if (N <= 1536 && t128 < 512) return 10;            // 128 x 64
   if (N <= 3072 && t128 < 512) return 16;            // 128 x 96
   if (N <= 1024) return 1;                           // the decoder's wider convs over many rows
   return 8;
