@@ -553,6 +553,24 @@ def test_codec_scalar_decoder(dev, T):
     _close_model(N_(got), want, f"scalar decoder T={T}")
 
 
+def test_codec_scalar_decoder_reuse(dev):
+    """One decoder over windows of changing length (20, 9, 20 frames): its padded buffers are
+    rebuilt per shape, and every output equals a fresh decoder's bit for bit (the padding rows
+    stay zero across calls)."""
+    import torch
+    from estudiocanciones_amd.codec import ScalarDecoder
+    p = OC.random_decoder_weights(DEC, seed=840)
+    sd = {k: torch.from_numpy(np.asarray(v)) for k, v in p.items()}
+    cfg = dict(latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3),
+               upsample_kernel_sizes=(4, 6), device=dev)
+    dec = ScalarDecoder(sd, **cfg)
+    for i, T in enumerate((20, 9, 20)):
+        lat = D_(randn16(841 + i, 1, T, 128), dev)
+        got = N_(dec.decode(lat))
+        want = N_(ScalarDecoder(sd, **cfg).decode(lat))
+        _exact(got, want, f"reused decoder, window {i} (T={T})")
+
+
 def test_codec_detokenize_audio(dev):
     """codes -> waveform: three 7.44 s windows (latents on the GPU), each decoded by the waveform
     decoder (small configuration: one channel group, 12 samples per latent frame, so
