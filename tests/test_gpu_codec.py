@@ -456,11 +456,13 @@ def test_codec_cols_taps_bit_exact(dev, offs, rep, row0, nrows):
 @pytest.mark.parametrize("offs,C,N,ypad,prelu", [((-18, -15, -12, -9, -6, -3, 0), 64, 64, 60, True),
                                                   ((0, -1), 128, 192, 20, False),
                                                   ((-6, -5, -4, -3, -2, -1, 0), 128, 1, -1, False),
-                                                  ((0,), 64, 64, 60, True)])
+                                                  ((0,), 64, 64, 60, True),
+                                                  ((-2, -1, 0, 1, 2), 64, 96, 60, False)])
 def test_gemm_f16_conv_implicit_taps(dev, offs, C, N, ypad, prelu):
     """A convolution over implicit tap columns of a zero-padded activation equals the GEMM over
     materialised columns bit for bit (same accumulation order), with padded or plain output and
-    the residual read through the same row map."""
+    the residual read through the same row map; centred taps read the next sequence's pad rows
+    and, after the last sequence, the trailing zero rows."""
     import ctypes
     import torch
     from estudiocanciones_amd import _ffi
