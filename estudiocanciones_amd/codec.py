@@ -665,15 +665,16 @@ class ScalarDecoder:
             self._bufs[k] = torch.empty(rows, C, device=self.dev, dtype=torch.float16)
         return self._bufs[k]
 
-    def _gemm(self, cv, x, ldx, M, T, xpad, taps, y, ldy, ypad, res=False):
-        """One conv as ecd_gemm_f16p_conv: implicit taps over the padded x (taps) or a plain x."""
+    def _gemm(self, cv, x, ldx, M, T, xpad, taps, y, ldy, ypad, res=False, rep=1):
+        """One conv as ecd_gemm_f16p_conv: implicit taps over the padded x (taps) or a plain x;
+        rep = 2: x holds T / 2 rows per sequence, upsampled 2x by row repeat."""
         lin = cv.lin
         prelu = getattr(cv, "prelu", None)
         _ffi.call("ecd_gemm_f16p_conv", x.data_ptr(), ldx, lin.wp.data_ptr(),
                   lin.b.data_ptr() if lin.b is not None else None,
                   float(prelu) if prelu is not None else 1.0, y.data_ptr() if res else None,
                   ldy if res else 0, y.data_ptr(), ldy, M, lin.N, lin.K, T, xpad, ypad,
-                  cv.off if taps else None, cv.k if taps else 0, 2 if prelu is not None else 0,
+                  cv.off if taps else None, cv.k if taps else 0, rep, 2 if prelu is not None else 0,
                   stream_ptr(self.dev))
 
     def _cols_conv(self, cv, src, S, T, spad, rep, y, ypad):
@@ -722,7 +723,8 @@ class ScalarDecoder:
             a = bb
         T2 = 2 * T
         pb = self._pbuf("post", S, T2, self.post.cout)
-        self._cols_conv(self.post, a, S, T2, P, 2, pb, P)
+        # PostProcessor: 2x row repeat + causal conv, read straight from the padded activation
+        self._gemm(self.post, a, self.post.cin, S * T2, T2, P, True, pb, self.post.cout, P, rep=2)
         y = self._buf("out", S * T2, self.final.cout)
         self._gemm(self.final, pb, self.post.cout, S * T2, T2, P, True, y, self.final.cout, -1)
         return y.view(S, T2, -1).clone()

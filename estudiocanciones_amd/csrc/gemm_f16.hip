@@ -97,7 +97,7 @@ __device__ __forceinline__ void f16_mfma_half(f32x4 (&acc)[FT][RT], const f16x8 
 // (the tap offsets move the chunk's DMA base; the pad rows supply the zeros of the padding).
 // With ypad >= 0, y and res rows are b (T + ypad) + ypad + t.  T = 0: plain rows throughout.
 struct RowMap {
-  int T, xpad, ypad, cpt, k;
+  int T, xpad, ypad, cpt, k, rep;
   int off[8];
 };
 
@@ -173,30 +173,43 @@ __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel
   }
   const uint32_t woff = 16u * lane;
   const int xpiece = (lane & 7) ^ (lane >> 3);
-  uint32_t xoff[XI];
+  // with a 2x row-repeat (rm.rep == 2) output step t reads source row (t + o) >> 1 for tap o:
+  // (t >> 1) + (o >> 1) for even o, ((t + 1) >> 1) + (o >> 1) for odd o -- two lane rows
+  uint32_t xoff[XI], xoff1[XI];
 #pragma unroll
   for (int j = 0; j < XI; ++j) {
     const int i = wv + 4 * j;
-    long xr = min(m0 + 8 * i + (lane >> 3), M - 1);
-    if (rm.k) xr = seq_row(xr, rm.T, rm.xpad);
+    long xr = min(m0 + 8 * i + (lane >> 3), M - 1), xr1 = xr;
+    if (rm.k && rm.rep == 2) {
+      const long b = xr / rm.T, t = xr - b * rm.T;
+      const long base = b * (rm.T / 2 + rm.xpad) + rm.xpad;
+      xr = base + (t >> 1);
+      xr1 = base + ((t + 1) >> 1);
+    } else if (rm.k) {
+      xr = xr1 = seq_row(xr, rm.T, rm.xpad);
+    }
     xoff[j] = (uint32_t)(xr * ldx * 2 + 16 * xpiece);
+    xoff1[j] = (uint32_t)(xr1 * ldx * 2 + 16 * xpiece);
   }
-  // chunk c's x base: plain K offset 64 c, or tap j = c / cpt shifted by off[j] rows
-  auto xbase = [&](int c) -> const f16* {
-    if (!rm.k) return x + (long)c * 64;
-    const int j = c / rm.cpt;
-    int o = rm.off[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i)
-      if (j == i) o = rm.off[i];
-    return x + (long)o * ldx + (long)(c - j * rm.cpt) * 64;
-  };
+  // chunk c's x base: plain K offset 64 c, or tap j = c / cpt shifted by off[j] rows (by
+  // off[j] >> 1 with a 2x row-repeat, odd taps reading the second set of lane rows)
   auto issue = [&](int c, int st) {
 #pragma unroll
     for (int j = 0; j < WI; ++j) lds_dma16(wsrc[j] + (long)c * 2048, woff, &lw[st][wdst[j]]);
-    const f16* xb = xbase(c);
+    const f16* xb = x + (long)c * 64;
+    bool odd = false;
+    if (rm.k) {
+      const int tj = c / rm.cpt;
+      int o = rm.off[0];
 #pragma unroll
-    for (int j = 0; j < XI; ++j) lds_dma16(xb, xoff[j], &lx[st][8 * (wv + 4 * j) * 64]);
+      for (int i = 1; i < 8; ++i)
+        if (tj == i) o = rm.off[i];
+      odd = rm.rep == 2 && (o & 1);
+      xb = x + (long)(rm.rep == 2 ? (o >> 1) : o) * ldx + (long)(c - tj * rm.cpt) * 64;
+    }
+#pragma unroll
+    for (int j = 0; j < XI; ++j)
+      lds_dma16(xb, odd ? xoff1[j] : xoff[j], &lx[st][8 * (wv + 4 * j) * 64]);
   };
 
   f32x4 acc[FT][RT];
@@ -492,7 +505,7 @@ int ecd_gemm_f16p_tuned(const void* x, long ldx, const void* wp, const float* bi
     return ECD_EINVAL;
   }
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  const RowMap rm = {0, 0, -1, 0, 0, {0, 0, 0, 0, 0, 0, 0, 0}};
+  const RowMap rm = {0, 0, -1, 0, 0, 1, {0, 0, 0, 0, 0, 0, 0, 0}};
   return launch_epi(epi, cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
                     ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);
 }
@@ -507,7 +520,7 @@ int ecd_gemm_f16p_rope(const void* x, long ldx, const void* wp, const float* bia
       ((uintptr_t)v & 7))
     return ECD_EINVAL;
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
-  const RowMap rm = {0, 0, -1, 0, 0, {0, 0, 0, 0, 0, 0, 0, 0}};
+  const RowMap rm = {0, 0, -1, 0, 0, 1, {0, 0, 0, 0, 0, 0, 0, 0}};
   const RopeOut ro = {(const f16*)tab, (f16*)q, (f16*)k, (f16*)v, T, H, HD};
   return launch_f16<F16_ROPE>(0, (const f16*)x, ldx, (const f16*)wp, bias, 1.0f, nullptr, 0,
                               nullptr, 0, M, (int)N, K, rm, ro, (hipStream_t)stream);
@@ -515,21 +528,26 @@ int ecd_gemm_f16p_rope(const void* x, long ldx, const void* wp, const float* bia
 
 int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
                        const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
-                       int xpad, int ypad, const int* offsets, int k, int epi, void* stream) {
+                       int xpad, int ypad, const int* offsets, int k, int rep, int epi,
+                       void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || (ldx % 8) || !al16(x) ||
       !al16(wp) || epi < 0 || epi > 2 || epi == F16_SILU || T <= 0 || M % T || k < 0 || k > 8 ||
       (k && (!offsets || K % (64 * k) || xpad < 0)) || (!k && ldx < K) || ldy < N ||
-      (res && ldr < N) || ypad < -1)
+      (res && ldr < N) || ypad < -1 || (rep != 1 && rep != 2) || (rep == 2 && (!k || T % 2)))
     return ECD_EINVAL;
-  RowMap rm = {T, xpad, ypad, k ? K / (64 * k) : 0, k, {0, 0, 0, 0, 0, 0, 0, 0}};
+  RowMap rm = {T, xpad, ypad, k ? K / (64 * k) : 0, k, rep, {0, 0, 0, 0, 0, 0, 0, 0}};
   if (k) {
     if (ldx < K / k) return ECD_EINVAL;
     for (int j = 0; j < k; ++j) {
-      if (offsets[j] < -xpad || offsets[j] > xpad) return ECD_EINVAL;  // stays in the pad rows
+      // source rows stay in the pad rows: shift o (or o >> 1 and (o + 1) >> 1 with a repeat)
+      const int lo = rep == 2 ? offsets[j] >> 1 : offsets[j];
+      const int hi = rep == 2 ? (offsets[j] + 1) >> 1 : offsets[j];
+      if (lo < -xpad || hi > xpad) return ECD_EINVAL;
       rm.off[j] = offsets[j];
     }
   }
-  const long xrows = k ? (long)(M / T) * (T + xpad) + xpad : M;  // + the rows after the last
+  const long tin = rep == 2 ? T / 2 : T;  // source rows per sequence
+  const long xrows = k ? (long)(M / T) * (tin + xpad) + xpad : M;  // + the rows after the last
   if (!x_offsets_fit((int)min(xrows, 0x7FFFFFFFL), ldx)) return ECD_ENOTSUP;
   return launch_epi(epi, 0, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
                     ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);

@@ -218,16 +218,19 @@ int ecd_gemm_f16p_prelu(const void* x, long ldx, const void* wp, const float* bi
                         void* stream);
 
 /* A convolution as this GEMM over implicit tap columns, time-major rows m = b*T + t (M % T == 0):
- * with k taps, x holds each sequence after xpad zero rows (row b*(T + xpad) + xpad + t) and
- * K = k*C, the columns of row m being x rows + offsets[j] (|offsets| <= xpad, so they stay in
- * the zero rows of the padding; the caller also leaves max(offsets) zero rows after the last
- * sequence); k = 0: x is plain [M, K].  With ypad >= 0, y and res rows are b*(T + ypad) + ypad +
- * t, else plain.  epi 0 (store, alpha the scale) or 2 (PReLU, alpha the slope).  The causal and
- * dilated Conv1d and ConvTranspose1d of the codec's waveform decoder (sq_codec.py:32-168)
- * without materialised columns. */
+ * with k taps, x holds each sequence after xpad zero rows and K = k*C, the columns of row m being
+ * the source rows at offsets[j] from it; k = 0: x is plain [M, K].  rep = 1: source sequences of T
+ * rows (row b*(T + xpad) + xpad + t); rep = 2: the source is upsampled 2x by row repeat (nearest),
+ * so it holds T/2 rows per sequence and output step t, tap o reads source row (t + o) >> 1 (T even).
+ * Every source row read stays within the zero padding (|offsets| <= xpad, halved with rep 2); the
+ * caller also leaves that many zero rows after the last sequence.  With ypad >= 0, y and res rows
+ * are b*(T + ypad) + ypad + t, else plain.  epi 0 (store, alpha the scale) or 2 (PReLU, alpha the
+ * slope).  The causal and dilated Conv1d, ConvTranspose1d and the PostProcessor's upsample + conv
+ * of the codec's waveform decoder (sq_codec.py:32-287) without materialised columns. */
 int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
                        const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
-                       int xpad, int ypad, const int* offsets, int k, int epi, void* stream);
+                       int xpad, int ypad, const int* offsets, int k, int rep, int epi,
+                       void* stream);
 
 /* ecd_gemm_f16p (epi 0), ecd_gemm_f16p_silu (epi 1, N = 2F, bias/res NULL, alpha 1) or
  * ecd_gemm_f16p_prelu (epi 2, alpha = the slope) with an

@@ -89,15 +89,21 @@ def _taps(*offsets):
     lambda L: L.ecd_codec_euler(16, 16, 16, 16, 1, 1, 8, 252, 0, 0.1, 1.2, 0.0, 0, None),  # C % 8
     lambda L: L.ecd_codec_cols_taps(16, 64, _taps(0, -1), 2, 16, 1, 8, 64, 1, 0, 0, 9, None),  # rows > B*T
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 100, 64, 128, 30, 60, -1,
-                                   _taps(0, -1), 2, 0, None),                    # M % T
+                                   _taps(0, -1), 2, 1, 0, None),                    # M % T
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
-                                   _taps(-61, 0), 2, 0, None),                   # tap beyond the pad
+                                   _taps(-61, 0), 2, 1, 0, None),                   # tap beyond the pad
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 192, 30, 60, -1,
-                                   _taps(0, -1), 2, 0, None),                    # K % (64 k)
+                                   _taps(0, -1), 2, 1, 0, None),                    # K % (64 k)
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
-                                   _taps(0, -1), 2, 1, None),                    # no SiLU epilogue
+                                   _taps(0, -1), 2, 1, 1, None),                    # no SiLU epilogue
     lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
-                                   None, 2, 0, None),                            # taps missing
+                                   None, 2, 1, 0, None),                         # taps missing
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 60, -1,
+                                   _taps(0, -1), 2, 3, 0, None),                 # rep 3
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 93, 64, 128, 31, 60, -1,
+                                   _taps(0, -1), 2, 2, 0, None),                 # rep 2, odd T
+    lambda L: L.ecd_gemm_f16p_conv(16, 64, 16, None, 1.0, None, 0, 16, 64, 90, 64, 128, 30, 4, -1,
+                                   _taps(-10, 0), 2, 2, 0, None),                # rep 2, tap past pad
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 90, 30, 2, 62, 64, None),  # HD % 4
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 100, 30, 2, 64, 64, None),  # M % T
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 12, 16, 90, 30, 2, 64, 64, None),  # k align

@@ -453,36 +453,40 @@ def test_codec_cols_taps_bit_exact(dev, offs, rep, row0, nrows):
     _exact(N_(out), want[row0:row0 + n], f"cols taps {offs} rep {rep}")
 
 
-@pytest.mark.parametrize("offs,C,N,ypad,prelu", [((-18, -15, -12, -9, -6, -3, 0), 64, 64, 60, True),
-                                                  ((0, -1), 128, 192, 20, False),
-                                                  ((-6, -5, -4, -3, -2, -1, 0), 128, 1, -1, False),
-                                                  ((0,), 64, 64, 60, True),
-                                                  ((-2, -1, 0, 1, 2), 64, 96, 60, False)])
-def test_gemm_f16_conv_implicit_taps(dev, offs, C, N, ypad, prelu):
+@pytest.mark.parametrize("offs,C,N,ypad,prelu,rep", [((-18, -15, -12, -9, -6, -3, 0), 64, 64, 60, True, 1),
+                                                      ((0, -1), 128, 192, 20, False, 1),
+                                                      ((-6, -5, -4, -3, -2, -1, 0), 128, 1, -1, False, 1),
+                                                      ((0,), 64, 64, 60, True, 1),
+                                                      ((-2, -1, 0, 1, 2), 64, 96, 60, False, 1),
+                                                      ((-6, -5, -4, -3, -2, -1, 0), 64, 64, 60, True, 2),
+                                                      ((-3, -1, 0, 1, 3), 64, 96, -1, False, 2)])
+def test_gemm_f16_conv_implicit_taps(dev, offs, C, N, ypad, prelu, rep):
     """A convolution over implicit tap columns of a zero-padded activation equals the GEMM over
     materialised columns bit for bit (same accumulation order), with padded or plain output and
     the residual read through the same row map; centred taps read the next sequence's pad rows
-    and, after the last sequence, the trailing zero rows."""
+    and, after the last sequence, the trailing zero rows; rep = 2 reads a source upsampled 2x by
+    row repeat (the PostProcessor), odd taps from the second set of lane rows."""
     import ctypes
     import torch
     from estudiocanciones_amd import _ffi
     from estudiocanciones_amd.kernels import pack_f16, stream_ptr
-    B, T, P = 2, 203, 60
+    B, T, P = 2, 204 if rep == 2 else 203, 60
+    Tin = T // rep
     k = len(offs)
     K = k * C
-    g = rng(840 + C + N)
-    x = randn16(841, B, T, C)
-    xp = np.zeros((B * (P + T) + 8, C), np.float16)
+    g = rng(840 + C + N + rep)
+    x = randn16(841 + rep, B, Tin, C)
+    xp = np.zeros((B * (P + Tin) + 8, C), np.float16)
     for b in range(B):
-        xp[b * (P + T) + P:b * (P + T) + P + T] = x[b]
+        xp[b * (P + Tin) + P:b * (P + Tin) + P + Tin] = x[b]
     w = f16(g.standard_normal((N, K)) * 0.05)
     bias = (g.standard_normal(N) * 0.1).astype(np.float32)
     wp, bt = pack_f16(D_(w, dev)), D_(bias, dev)
     st = stream_ptr(dev)
     off = (ctypes.c_int * k)(*offs)
+    xpt = D_(xp, dev)
     cols = torch.empty(B * T, K, dtype=torch.float16, device=dev)
-    xt = D_(x.reshape(B * T, C), dev)
-    _ffi.call("ecd_codec_cols_taps", xt.data_ptr(), C, off, k, cols.data_ptr(), B, T, C, 1, 0, 0,
+    _ffi.call("ecd_codec_cols_taps", xpt.data_ptr(), C, off, k, cols.data_ptr(), B, T, C, rep, P, 0,
               B * T, st)
     yrows = B * (ypad + T) + 8 if ypad >= 0 else B * T
     r = randn16(842, yrows, N)
@@ -490,11 +494,10 @@ def test_gemm_f16_conv_implicit_taps(dev, offs, C, N, ypad, prelu):
     y_imp = D_(r, dev)
     epi = 2 if prelu else 0
     _ffi.call("ecd_gemm_f16p_conv", cols.data_ptr(), K, wp.data_ptr(), bt.data_ptr(), 0.25,
-              y_ref.data_ptr(), N, y_ref.data_ptr(), N, B * T, N, K, T, 0, ypad, None, 0, epi, st)
-    xpt = D_(xp, dev)
+              y_ref.data_ptr(), N, y_ref.data_ptr(), N, B * T, N, K, T, 0, ypad, None, 0, 1, epi, st)
     _ffi.call("ecd_gemm_f16p_conv", xpt.data_ptr(), C, wp.data_ptr(), bt.data_ptr(), 0.25,
-              y_imp.data_ptr(), N, y_imp.data_ptr(), N, B * T, N, K, T, P, ypad, off, k, epi, st)
-    _exact(N_(y_imp), N_(y_ref), f"implicit taps {offs} C={C} N={N} ypad={ypad}")
+              y_imp.data_ptr(), N, y_imp.data_ptr(), N, B * T, N, K, T, P, ypad, off, k, rep, epi, st)
+    _exact(N_(y_imp), N_(y_ref), f"implicit taps {offs} C={C} N={N} ypad={ypad} rep={rep}")
 
 
 def test_codec_weight_norm_and_latent_split(dev):
