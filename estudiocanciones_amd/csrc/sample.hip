@@ -365,9 +365,48 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
 }
 
+// ---------------------------------------------------------------- end of a frame
+// Frame bookkeeping of the song loop kept on the device, so a captured frame needs no host
+// work between replays (the host only reads first_eos every few frames): the frame's tokens
+// become the next frame's input, rows 0..N-1 are stored as frame f = pos - P + 1 of the song,
+// each take's first frame holding a token >= eos is recorded (frames 1..F only: the frame of
+// the prompt pass is never scanned, as in app/engine.py:433-437), and the position advances.
+// One block; thread i handles token (i / 8, i % 8) of the B x 8 frame.
+__global__ __launch_bounds__(512) void frame_advance_kernel(
+    const int64_t* __restrict__ samples, long lds, int64_t* __restrict__ tok, long ldt,
+    int64_t* __restrict__ pos, long ldp, int64_t* __restrict__ out,
+    int64_t* __restrict__ first_eos, int B, int N, int P, int F, int64_t eos) {
+  __shared__ int hit[64];
+  const int i = threadIdx.x;
+  const int b = i >> 3, c = i & 7;
+  const long f = pos[0] - (long)P + 1;  // every row holds the same position
+  if (i < 64) hit[i] = 0;
+  __syncthreads();
+  if (b < B) {
+    const int64_t t = samples[(long)b * lds + c];
+    tok[(long)b * ldt + c] = t;
+    if (b < N && f >= 0 && f <= F) out[(f * N + b) * 8 + c] = t;
+    if (b < N && t >= eos) hit[b] = 1;
+  }
+  __syncthreads();  // every thread has read pos before it moves
+  if (i < N && hit[i] && f >= 1 && f <= F && first_eos[i] < 0) first_eos[i] = f;
+  if (i < B) pos[(long)i * ldp] += 1;
+}
+
 }  // namespace ecd
 
 using namespace ecd;
+
+extern "C" int ecd_frame_advance(const int64_t* samples, long lds, int64_t* tok, long ldt,
+                                 int64_t* pos, long ldp, int64_t* out, int64_t* first_eos, int B,
+                                 int N, int P, int F, int64_t eos, void* stream) {
+  if (!samples || !tok || !pos || !out || !first_eos || B <= 0 || B > 64 || N <= 0 || N > B ||
+      lds < 8 || ldt < 8 || ldp < 1 || F < 0 || P < 0)
+    return ECD_EINVAL;
+  hipLaunchKernelGGL(frame_advance_kernel, dim3(1), dim3(B * 8), 0, (hipStream_t)stream, samples,
+                     lds, tok, ldt, pos, ldp, out, first_eos, B, N, P, F, eos);
+  return ecd_launch_status();
+}
 
 extern "C" int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float temp,
                                int topk, int V, const float* noise, const int64_t* seed,

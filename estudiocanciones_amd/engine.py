@@ -2,22 +2,26 @@
 
 Mirrors the fast path of the reference engine (app/engine.py) with the same classes,
 method names and tensor layouts -- ``Linear``, ``fuse``, ``Emb``, ``Block``, ``Stack``
-(``alloc``/``free``/``__call__``/``decode``) and ``HeartMuLaLite`` (``_sample``,
-``_guided``, ``_embed_audio``, ``_frame_fast``, ``_step``, ``generate``, ``_capture``,
-``release``) -- but every op of the per-frame step is a hand-written HIP kernel reached
-through the C ABI of ``libecdecode.so`` (see ``kernels.py``), sampling included (one fused
-CFG + top-k + Exponential-race kernel per codebook; ``_sample``/``_guided`` keep the
-reference's PyTorch form for the slow path).  Differences from the reference, all deliberate:
+(``alloc``/``free``/``__call__``/``decode``) and ``HeartMuLaLite`` (``_embed_audio``,
+``_frame_fast``, ``_step``, ``generate``, ``_capture``, ``release``) -- but every op of the
+per-frame step is a hand-written HIP kernel reached through the C ABI of ``libecdecode.so``
+(see ``kernels.py``), sampling included: one fused CFG + top-k + Exponential-race kernel per
+codebook replaces the reference's ``_sample``/``_guided`` torch ops.  Differences from the
+reference, all deliberate:
 
 * stacks are shape-parametric (``dim`` per stack) instead of the global ``DIM = 3072``
   (app/engine.py:19, :116, :161), so a 1024-wide decoder can be expressed;
-* the prompt pass (``Stack.__call__``) runs through the same decode kernels with one row
-  per prompt position (row r attends [0, pos[r]] == causal attention), instead of SDPA with
-  ``repeat_interleave``; ``int8_mm`` keeps the reference's dense numerics for M > 16 rows;
+* the prompt pass (``Stack.__call__``) runs the MFMA GEMM and causal flash-attention kernels
+  (more than 64 rows) or the decode kernels with one row per prompt position, instead of
+  SDPA with ``repeat_interleave``; ``int8_mm`` keeps the reference's dense numerics for
+  M > 16 rows;
 * the prompt arrives as token ids (tokenisation is host string work, out of scope);
 * the text-embedding table lives on the GPU (one gather per song);
 * decode attention over caches of at most 128 slots uses one split (direct output,
-  no combine pass); longer caches use the reference's 16 splits.
+  no combine pass); longer caches use the reference's 16 splits;
+* the song loop keeps its bookkeeping on the device: the captured frame ends with a kernel
+  that feeds the tokens back, stores the frame and records each take's first EOS frame, so
+  the host only replays the graph and reads N integers every 25 frames.
 """
 from __future__ import annotations
 
@@ -378,24 +382,6 @@ class HeartMuLaLite:
         self.graphs = {}
         self.N = self.B = None
 
-    # -------------------------------------------------- sampling (as in the reference)
-    @staticmethod
-    def _sample(logits, topk, temp, noise=None):
-        """app/engine.py:291-298; ``noise`` replaces the Exponential(1) draws (tests)."""
-        logits = logits / temp
-        thr = torch.topk(logits, topk)[0][..., -1, None]
-        logits = logits.masked_fill(logits < thr, -float("inf"))
-        probs = torch.softmax(torch.log_softmax(logits, -1), -1)
-        qe = torch.empty_like(probs).exponential_(1) if noise is None else noise
-        return torch.argmax(probs / qe, -1, keepdim=True)
-
-    def _guided(self, logits, cfg, topk, temp, noise=None):
-        N = self.N
-        if self.B == 2 * N:
-            logits = logits[N:] + (logits[:N] - logits[N:]) * cfg
-        s = self._sample(logits.float(), topk, temp, noise)
-        return torch.cat([s, s], 0) if self.B == 2 * N else s
-
     def _embed_audio(self, cb, tok):
         """Embedding of codebook ``cb`` for tokens tok [B, 1] -> [B, D] (app/engine.py:307-308)."""
         return self.audio_emb.gather(tok, cb, AUDIO_VOCAB)
@@ -495,84 +481,97 @@ class HeartMuLaLite:
     # -------------------------------------------------- generation
     @torch.inference_mode()
     def generate(self, text, muq_idx, *, max_ms=60_000, temperature=1.0, topk=50, cfg_scale=1.5,
-                 seed=None, use_graphs=True, progress=None, abort=None, n=1):
-        """app/engine.py:374-448 with the prompt given as token ids ``text`` [P] (int64) and the
-        muq slot index.  Returns [8, T] if n == 1, else a list of n such tensors."""
+                 seed=None, use_graphs=True, progress=None, abort=None, n=1, forced=None):
+        """A song of up to ``max_ms`` for n takes (app/engine.py:374-448) with the prompt given as
+        token ids ``text`` [P] (int64) and the muq slot index.  Returns [8, T] if n == 1, else a
+        list of n such tensors, each take cut before its first frame holding an EOS token.
+        ``forced`` [max_ms // 80 + 1, B, 8] int64 on the device replaces the sampled tokens of
+        every frame (teacher forcing a whole song)."""
         if seed is not None and seed >= 0:
             torch.manual_seed(seed)
         text = torch.as_tensor(text, dtype=torch.int64)
         P = int(text.numel())
         n_frames = max_ms // FRAME_MS
-        L = P + n_frames + 2
-        self.alloc(n, L + 256, cfg_scale)
-        self._pos_prompt.fill_(P - 1)
+        cap = P + n_frames + 2 + 256
+        self.alloc(n, cap, cfg_scale)
         N, B = self.N, self.B
-        te = self.text_emb(text.to(self.dev))                                  # [P, D]
-        h = te.unsqueeze(0).repeat(B, 1, 1)
+        if forced is not None and tuple(forced.shape) != (n_frames + 1, B, N_CB):
+            raise ValueError(f"generate: forced must be [{n_frames + 1}, {B}, {N_CB}]")
+
+        # prompt pass (text rows, the muq slot's bias, unconditional rows for CFG)
+        h = self.text_emb(text.to(self.dev)).unsqueeze(0).repeat(B, 1, 1)
         h[:N, muq_idx] = self.muq_b
         if B == 2 * N:
             h[N:] = self.uncond[0]
-        pos = torch.arange(P, device=self.dev).unsqueeze(0).expand(B, P)
-        hb = self.backbone(h, pos, P, None)
-        tok = self._frame_fast(hb[:, -1].contiguous(), cfg_scale, topk, temperature)
+        hb = self.backbone(h, torch.arange(P, device=self.dev).unsqueeze(0).expand(B, P), P, None)
 
-        out = torch.empty(n_frames + 1, N, N_CB, dtype=torch.long, device=self.dev)
-        out[0] = tok[:N]
-        cur_pos = P
-        ends = [None] * N
-        static = None
-        CHECK = 25
-        last = n_frames
-        bucket = L + 256
+        # song state on the device: next input tokens and position, the frames so far, and
+        # each take's first EOS frame (-1 while it runs)
+        st = dict(tok=torch.empty(B, N_CB, dtype=torch.long, device=self.dev),
+                  pos=torch.full((B, 1), P - 1, dtype=torch.long, device=self.dev),
+                  out=torch.empty(n_frames + 1, N, N_CB, dtype=torch.long, device=self.dev),
+                  eos=torch.full((N,), -1, dtype=torch.long, device=self.dev),
+                  forced=None if forced is None else forced[0].clone())
+        kw = {} if forced is None else {"forced": st["forced"]}
+        first = self._frame_fast(hb[:, -1].contiguous(), cfg_scale, topk, temperature,
+                                 pos=st["pos"], **kw)
+        self._advance(first, st, P, n_frames)
+
+        key = (B, cap, topk, float(temperature), float(cfg_scale))
+        ends = st["eos"]
+        done = n_frames
         for i in range(n_frames):
             if abort and abort():
                 self.release()
                 return None
+            if forced is not None:
+                st["forced"].copy_(forced[i + 1])
             if use_graphs:
-                key = (B, bucket, topk, float(temperature), float(cfg_scale))
-                if static is None:
-                    static = dict(tok=tok.clone(), pos=torch.zeros(B, 1, dtype=torch.long, device=self.dev))
-                static["tok"].copy_(tok)
-                static["pos"].fill_(cur_pos)
                 g = self.graphs.get(key)
                 if g is None:
-                    g = self._capture(static, bucket, cfg_scale, topk, temperature)
-                    self.graphs[key] = g
+                    g = self.graphs[key] = self._capture(st, cap, cfg_scale, topk, temperature,
+                                                         song=(P, n_frames))
                 g[0].replay()
-                tok = g[1]
             else:
-                p_t = torch.full((B, 1), cur_pos, dtype=torch.long, device=self.dev)
-                tok = self._step(tok, p_t, bucket, cfg_scale, topk, temperature)
-            out[i + 1] = tok[:N]
-            cur_pos += 1
-            if (i + 1) % CHECK == 0 or i == n_frames - 1:
-                a = max(1, i + 2 - CHECK)
-                eos = (out[a: i + 2] >= AUDIO_EOS).any(-1).cpu()
-                for c in range(N):
-                    if ends[c] is None and eos[:, c].any():
-                        ends[c] = a + int(eos[:, c].nonzero()[0, 0])
-                if all(e is not None for e in ends):
-                    last = i + 1
+                self._advance(self._step(st["tok"], st["pos"], cap, cfg_scale, topk, temperature,
+                                         **kw), st, P, n_frames)
+            if (i + 1) % 25 == 0 or i == n_frames - 1:
+                ends = st["eos"].tolist()          # the loop's only device -> host read
+                if min(ends) >= 0:
+                    done = i + 1
                     break
                 if progress:
                     progress((i + 1) * FRAME_MS / 1000, max_ms / 1000)
-        res = []
-        for c in range(N):
-            T = ends[c] if ends[c] is not None else last + 1
-            res.append(out[:T, c].t().clone())
+        if torch.is_tensor(ends):
+            ends = ends.tolist()
+        self.frames_run = done
+        res = [st["out"][: (e if e >= 0 else done + 1), c].t().clone() for c, e in enumerate(ends)]
         self.release()
         return res[0] if n == 1 else res
 
-    def _capture(self, static, bucket, cfg, topk, temp):
-        """One eager warm-up then capture of ``_step`` into a hipGraph (app/engine.py:450-461)."""
+    def _advance(self, samples, st, P, n_frames):
+        """Frame bookkeeping on the device: samples -> next input, frame stored, first EOS frame
+        per take recorded, position + 1 (one kernel, capturable)."""
+        _ffi.call("ecd_frame_advance", samples.data_ptr(), samples.stride(0), st["tok"].data_ptr(),
+                  st["tok"].stride(0), st["pos"].data_ptr(), st["pos"].stride(0),
+                  st["out"].data_ptr(), st["eos"].data_ptr(), self.B, self.N, P, n_frames,
+                  AUDIO_EOS, stream_ptr(self.dev))
+
+    def _capture(self, static, bucket, cfg, topk, temp, song=None):
+        """One eager warm-up, then ``_step`` captured into a hipGraph (app/engine.py:450-461).
+        With ``song`` = (P, n_frames) the graph ends with the frame bookkeeping (``_advance``),
+        so consecutive replays make consecutive frames with no host work in between."""
+        kw = {"forced": static["forced"]} if static.get("forced") is not None else {}
         s = torch.cuda.Stream(device=self.dev)
         s.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(s):
-            self._step(static["tok"], static["pos"], bucket, cfg, topk, temp)
+            self._step(static["tok"], static["pos"], bucket, cfg, topk, temp, **kw)
         torch.cuda.current_stream(self.dev).wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, pool=getattr(self, "_pool", None)):
-            out = self._step(static["tok"], static["pos"], bucket, cfg, topk, temp)
+            out = self._step(static["tok"], static["pos"], bucket, cfg, topk, temp, **kw)
+            if song is not None:
+                self._advance(out, static, *song)
         self._pool = g.pool()
         return g, out
 

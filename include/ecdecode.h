@@ -119,6 +119,17 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
                     int V, const float* noise, const int64_t* seed, const int64_t* pos, int salt,
                     int64_t* out, long out_stride, void* stream);
 
+/* End of one frame of the song loop, on the device (app/engine.py:419-440: the host's
+ * tok/pos copies, out[i + 1] = tok[:N] and the EOS scan, moved inside the captured frame).
+ *   samples [B, 8] int64 (row stride lds): the frame's tokens; copied into tok [B, 8] (stride
+ *   ldt), the next frame's input.  f = pos[0] - P + 1 (every pos row holds the same value);
+ *   for 0 <= f <= F rows 0..N-1 are stored in out [F + 1, N, 8] at frame f; for 1 <= f <= F a
+ *   take n whose frame holds a token >= eos and whose first_eos[n] is still negative gets
+ *   first_eos[n] = f.  Then every pos[b * ldp] (int64 [B]) increases by one.  B <= 64. */
+int ecd_frame_advance(const int64_t* samples, long lds, int64_t* tok, long ldt, int64_t* pos,
+                      long ldp, int64_t* out, int64_t* first_eos, int B, int N, int P, int F,
+                      int64_t eos, void* stream);
+
 /* ---- packed-weight fused GEMVs (the engine's per-layer kernels) ----------------------------
  * Packed layout: [ceil(N/16)] tiles x [K/64] chunks x 1 KB, chunk bytes [16l, 16l+16) holding
  * row 16*tile + (l & 15), bytes 64c + 16(l >> 4) .. +15 (zero rows beyond N).  K % 64 == 0.

@@ -28,14 +28,42 @@ def gemv_i8(x, q, s, res=None) -> np.ndarray:
     s = np.asarray(s, dtype=np.float16)
     M = x2.shape[0]
     if M > 16:
-        wd = hmul(q.astype(np.float16), s[:, None]).astype(np.float64)
-        y = f16((x2 @ wd.T).astype(np.float32))
+        y = f16(_dot_rows_f64(x2, q, s).astype(np.float32))
     else:
-        acc = (x2 @ q.astype(np.float64).T).astype(np.float32)
+        acc = _dot_rows_f64(x2, q).astype(np.float32)
         y = f16(acc * s.astype(np.float32)[None, :])
     if res is not None:
         y = hadd(y, np.asarray(res, dtype=np.float16).reshape(M, -1))
     return y.reshape(*shp[:-1], q.shape[0])
+
+
+_F64_BUF = [np.empty(0)]
+# Accumulation type of the GEMV sums.  float64 is the oracle; tests switch it to float32 (the
+# blocked fp32 sums of a BLAS GEMM, another valid summation order) to measure how far a model
+# output moves under fp32 re-association alone -- the noise floor of a deep composite.
+GEMV_ACC = [np.float64]
+
+
+def _dot_rows_f64(x2, q, s=None) -> np.ndarray:
+    """x2 [M, K] @ w[N, K]^T summed in GEMV_ACC (float64) with w = q, or with ``s`` the
+    dequantised w = fp16(fp16(q) * s) of the dense path.  w is formed in row chunks inside one
+    reused buffer (large weights: no per-call float64 copy of the whole matrix)."""
+    acc = GEMV_ACC[0]
+    N, Kd = q.shape
+    rows = N if N * Kd <= (1 << 22) else max(1, (1 << 22) // Kd)
+    if _F64_BUF[0].size < rows * Kd:
+        _F64_BUF[0] = np.empty(rows * Kd, np.float64)
+    x2 = x2.astype(acc, copy=False)
+    out = np.empty((x2.shape[0], N), acc)
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        b = _F64_BUF[0][: (r1 - r0) * Kd].view(acc)[: (r1 - r0) * Kd].reshape(r1 - r0, Kd)
+        if s is None:
+            np.copyto(b, q[r0:r1], casting="unsafe")
+        else:
+            np.copyto(b, hmul(q[r0:r1].astype(np.float16), s[r0:r1, None]), casting="unsafe")
+        out[:, r0:r1] = x2 @ b.T
+    return out
 
 
 # ---------------------------------------------------------------- RMSNorm

@@ -193,17 +193,64 @@ class OModel:
         samples = [c0]
         x = np.stack([last_h, self.embed_audio(0, c0)[:, 0]], 1).reshape(2 * B, -1)
         dpos0 = np.tile(np.arange(2, dtype=np.int64), B)
-        h = self.decoder.decode(self.projection(x), dpos0, 2)[1::2]
+        h = self._pair_last(self.decoder.decode(self.projection(x), dpos0, 2))
         for i in range(1, N_CB):
-            ci = pick(i, self.audio_head[i - 1](h))
+            ci = pick(i, self._audio_head(i)(h))
             samples.append(ci)
             if i < N_CB - 1:
                 e = self.embed_audio(i, ci)[:, 0]
-                h = self.decoder.decode(self.projection(e), np.full(B, i + 1, np.int64), 1)
+                h = self.decoder.decode(self.projection(e), np.full(B, self._dec_pos(i), np.int64), 1)
         return np.concatenate(samples, 1), logits
+
+    # the three composition choices of _frame_fast, kept as methods so the pins in
+    # tests/test_oracle_frame.py can show that a slip in any of them is caught
+    @staticmethod
+    def _pair_last(h):
+        """Pass 0 runs rows (backbone state, codebook-0 embedding) per batch entry; the
+        codebook-1 head reads the second row of each pair (app/engine.py:337, [1::2])."""
+        return h[1::2]
+
+    def _audio_head(self, i):
+        """Codebook i (1..7) is read by audio_head[i - 1] (app/engine.py:339)."""
+        return self.audio_head[i - 1]
+
+    @staticmethod
+    def _dec_pos(i):
+        """Decoder position of the pass that embeds codebook i (app/engine.py:332, :342)."""
+        return i + 1
 
     def step(self, tok, pos, **kw):
         """_step (app/engine.py:345-349): tok [B, 8] previous frame, pos scalar position."""
         h = K.embed_sum(self.audio_q8, self.audio_s, tok, AUDIO_VOCAB)
         last_h = self.backbone.decode(h, np.full(self.B, pos, np.int64), 1)
         return self.frame(last_h, **kw)
+
+
+def frame_loop_trim(frames, n_frames, check=25, eos=8193):
+    """The frame loop's EOS scan and per-take trim (app/engine.py:401-446) applied to a token
+    sequence: frames [n_frames + 1, N, 8] (frame 0 from the prompt pass, frame i + 1 made by
+    loop iteration i).  Every ``check`` iterations, and after the last, the frames since the
+    previous check (never frame 0) are scanned for a token >= ``eos``; a take's end is its first
+    such frame; the loop stops at the first check where every take has ended.  A take is
+    trimmed to the frames before its end (all frames up to the last one made if it never
+    ended).  Returns (list of N int64 arrays [8, T], loop iterations run)."""
+    frames = np.asarray(frames, np.int64)
+    N = frames.shape[1]
+    ends = [None] * N
+    last = n_frames
+    ran = n_frames
+    for i in range(n_frames):
+        if (i + 1) % check == 0 or i == n_frames - 1:
+            a = max(1, i + 2 - check)
+            hit = (frames[a:i + 2] >= eos).any(-1)                    # [t, N]
+            for c in range(N):
+                if ends[c] is None and hit[:, c].any():
+                    ends[c] = a + int(np.flatnonzero(hit[:, c])[0])
+            if all(e is not None for e in ends):
+                last = ran = i + 1
+                break
+    out = []
+    for c in range(N):
+        T = ends[c] if ends[c] is not None else last + 1
+        out.append(frames[:T, c].T.copy())
+    return out, ran

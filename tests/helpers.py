@@ -83,3 +83,23 @@ def assert_close16(got, want, atol=ATOL, rtol=RTOL, what=""):
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{bad.size} elements outside atol={atol} rtol={rtol}; "
             f"worst at {i}: got {got[i]} want {want[i]} (max abs err {err.max():.3e})")
+
+
+def assert_within_noise(got, want, want_alt, what="", factor=3.0, atol=ATOL, rtol=RTOL):
+    """Bar for deep composites (a 28-layer frame, a whole prompt pass), whose outputs move under
+    fp32 re-association alone by more than the per-kernel bar: ``want_alt`` is the oracle
+    evaluated with float32 instead of float64 sums.  The GPU's largest error against ``want``,
+    and its share of elements outside atol + rtol |want|, must stay within ``factor`` times the
+    oracle's own (plus one fp16 ulp at the output scale / 0.1%)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    alt = np.asarray(want_alt, np.float64)
+    assert got.shape == want.shape == alt.shape, (got.shape, want.shape, alt.shape)
+    eg, en = np.abs(got - want), np.abs(alt - want)
+    bound = atol + rtol * np.abs(want)
+    ulp = float(np.abs(want).max()) * 2.0 ** -10
+    fg, fn = float((eg > bound).mean()), float((en > bound).mean())
+    assert eg.max() <= factor * en.max() + ulp, \
+        f"{what}: max error {eg.max():.3e} vs oracle re-association {en.max():.3e}"
+    assert fg <= factor * fn + 1e-3, \
+        f"{what}: {fg:.4%} outside the kernel bar vs oracle re-association {fn:.4%}"

@@ -65,6 +65,9 @@ def _taps(*offsets):
     lambda L: L.ecd_rope_table(None, 8, 128, 5e5, 32.0, 1.0, 4.0, 8192.0, None),
     lambda L: L.ecd_rope_table(8, 8, 127, 5e5, 32.0, 1.0, 4.0, 8192.0, None),
     lambda L: L.ecd_copy_bytes(8, 8, 15, None),
+    lambda L: L.ecd_frame_advance(8, 8, 8, 8, 8, 1, 8, 8, 65, 4, 10, 60, 8193, None),  # B > 64
+    lambda L: L.ecd_frame_advance(8, 8, 8, 8, 8, 1, 8, 8, 8, 9, 10, 60, 8193, None),   # N > B
+    lambda L: L.ecd_frame_advance(8, 4, 8, 8, 8, 1, 8, 8, 8, 4, 10, 60, 8193, None),   # lds < 8
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 24, 8, 64, 96, 0.1, None),    # HD 96
     lambda L: L.ecd_prefill_attn(16, 16, 16, 16, 16, 1, 8, 40, 8, 64, 128, 0.1, None),   # G = 5
     lambda L: L.ecd_prefill_attn(18, 16, 16, 16, 16, 1, 8, 24, 8, 64, 128, 0.1, None),   # q align

@@ -1,0 +1,285 @@
+"""Parity at the benchmarked sizes, against the oracle.
+
+* frame step of the 28-layer 3B backbone (3072 wide, 24q/8kv, head_dim 128, FFN 8192) plus the
+  7 passes of the 4-layer 1024-wide depth decoder (8q/2kv, FFN 8192), batch 8 (4 takes x CFG),
+  teacher forced, at attended KV length 750 (eager, then the same frame replayed as a hipGraph)
+  and at 3256 (a 256-token prompt plus 3000 frames);
+* the same frame with the reference's own depth decoder (3 layers, 3072 wide, 8q/4kv, head_dim
+  384; app/engine.py:24, :116, :161);
+* the prompt pass at the 3B layer shape, batch 8 x 256 tokens, cache capacity 3514;
+* the isolated kernels at the backbone shapes: GEMV 3072 <-> 8192 at 1/2/4/8 rows, and decode
+  attention over 512 ... 8192 cached tokens at batch 1 and 8.
+
+Weights are random, quantised per row on the GPU by the converter's kernel (bit-exact with the
+oracle's quantiser, test_gpu_kernels) and handed to the oracle as codes and bf16 scales.
+
+Bars.  A 28-layer frame is too deep for the per-kernel bar (2e-3 + 1e-2 |want|): evaluated
+with float32 instead of float64 sums, the oracle itself moves ~7% of the codebook-0 logits
+outside it (max error 1.4e-2 at logit std 1.1, KL 5e-6).  Composites are therefore held to
+KL(oracle || gpu) < 1e-4 per row on every head and to errors within 3x the oracle's own
+float32-vs-float64 difference (helpers.assert_within_noise); tensors one kernel deep (the
+first layer's cache slot, the isolated kernels) keep the per-kernel bar.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import assert_close16, assert_within_noise, randn16, rng
+from oracle import kernels as OK
+from oracle.model import OModel, OStack
+
+pytestmark = pytest.mark.gpu
+
+AUDIO_VOCAB, N_CB = 8197, 8
+BB = dict(layers=28, heads=24, kv_heads=8, max_seq=8192, dim=3072, ffn=8192)
+DEC_1024 = dict(layers=4, heads=8, kv_heads=2, max_seq=2048, dim=1024, ffn=8192)
+DEC_REF = dict(layers=3, heads=8, kv_heads=4, max_seq=2048, dim=3072, ffn=8192)
+
+
+def N(t):
+    return t.detach().cpu().numpy()
+
+
+def kl_rows_max(p_logits, q_logits):
+    p = np.asarray(p_logits, np.float64)
+    q = np.asarray(q_logits, np.float64)
+    lp = p - p.max(-1, keepdims=True)
+    lp -= np.log(np.exp(lp).sum(-1, keepdims=True))
+    lq = q - q.max(-1, keepdims=True)
+    lq -= np.log(np.exp(lq).sum(-1, keepdims=True))
+    return float((np.exp(lp) * (lp - lq)).sum(-1).max())
+
+
+def _host(t):
+    """Device tensor of the file layout -> numpy (bf16 as its uint16 bit pattern)."""
+    import torch
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def _pair(dev, bb, dec, seed):
+    from estudiocanciones_amd.engine import HeartMuLaLite
+    from estudiocanciones_amd.quant import synthetic_weights
+    wt = synthetic_weights(bb, dec, device=dev, seed=seed, text_vocab=64)
+    om = OModel({k: _host(v) for k, v in wt.items()}, bb, dec)
+    gm = HeartMuLaLite(wt, device=dev, backbone=bb, decoder=dec)
+    return om, gm
+
+
+@pytest.fixture(scope="module")
+def c3(dev):
+    return _pair(dev, BB, DEC_1024, seed=21)
+
+
+def _fill_caches(om, gm, att, seed):
+    """Backbone caches hold N(0, 1) keys/values in slots [0, att - 1) (both sides)."""
+    import torch
+    g = torch.Generator(device=gm.dev)
+    g.manual_seed(seed)
+    for ob, gb in zip(om.backbone.blocks, gm.backbone.blocks):
+        for oc, gc in ((ob.kc, gb.kc), (ob.vc, gb.vc)):
+            t = torch.randn(gc[:, :, : att - 1].shape, generator=g, device=gm.dev).half()
+            gc[:, :, : att - 1] = t
+            oc[:, :, : att - 1] = N(t)
+
+
+def _oracle_twice(fn):
+    """fn() with the oracle's float64 sums, then again with float32 sums (the re-association
+    noise floor; see helpers.assert_within_noise)."""
+    want = fn()
+    OK.GEMV_ACC[0] = np.float32
+    try:
+        alt = fn()
+    finally:
+        OK.GEMV_ACC[0] = np.float64
+    return want, alt
+
+
+def _frame(om, gm, att, seed, graph=False):
+    """One teacher-forced frame at position att - 1, checked against the oracle: KL < 1e-4 per
+    row on every head, errors within the oracle's own re-association noise; the cache slot the
+    frame writes likewise (layer 0 to the kernel bar)."""
+    import torch
+    n = 4
+    cap = att + 258            # the reference's capacity P + frames + 2 + 256 with P + frames = att
+    om.alloc(n, cap)
+    gm.alloc(n, cap)
+    B = gm.B
+    _fill_caches(om, gm, att, seed)
+    g = rng(seed)
+    tok = g.integers(0, AUDIO_VOCAB, (B, N_CB)).astype(np.int64)
+    forced = g.integers(0, AUDIO_VOCAB, (B, N_CB)).astype(np.int64)
+    forced[n:] = forced[:n]
+    pos = att - 1
+    last = len(om.backbone.blocks) - 1
+
+    def run_oracle():
+        _, lg = om.step(tok, pos, forced=forced)
+        return lg, [(om.backbone.blocks[i].kc[:, :, pos].copy(), om.backbone.blocks[i].vc[:, :, pos].copy())
+                    for i in (0, last)]
+
+    print(f"[frame] oracle (float64 and float32 sums), kv {att}", flush=True)
+    (want, wslot), (alt, aslot) = _oracle_twice(run_oracle)
+    print(f"[frame] gpu eager, kv {att}", flush=True)
+    tt = torch.from_numpy(tok).to(gm.dev)
+    pt = torch.full((B, 1), pos, dtype=torch.long, device=gm.dev)
+    ft = torch.from_numpy(forced).to(gm.dev)
+    got = []
+    gm._step(tt, pt, None, 1.5, 50, 1.0, forced=ft, logits_out=got)
+    torch.cuda.synchronize()
+    for i in range(N_CB):
+        gi = N(got[i]).astype(np.float32)
+        kl = kl_rows_max(want[i], gi)
+        assert kl < 1e-4, (att, i, kl)
+        assert_within_noise(gi, want[i], alt[i], what=f"kv {att} head {i} logits")
+    gk0, gv0 = N(gm.backbone.blocks[0].kc[:, :, pos]), N(gm.backbone.blocks[0].vc[:, :, pos])
+    assert_close16(gk0, wslot[0][0], what=f"layer 0 k slot {pos}")
+    assert_close16(gv0, wslot[0][1], what=f"layer 0 v slot {pos}")
+    gkl, gvl = N(gm.backbone.blocks[last].kc[:, :, pos]), N(gm.backbone.blocks[last].vc[:, :, pos])
+    assert_within_noise(gkl, wslot[1][0], aslot[1][0], what=f"layer {last} k slot {pos}")
+    assert_within_noise(gvl, wslot[1][1], aslot[1][1], what=f"layer {last} v slot {pos}")
+    if not graph:
+        return
+    print(f"[frame] gpu hipGraph replay, kv {att}", flush=True)
+    eager = [x.clone() for x in got]
+    static = dict(tok=tt.clone(), pos=pt.clone(), forced=ft.clone())
+    s = torch.cuda.Stream(device=gm.dev)
+    s.wait_stream(torch.cuda.current_stream(gm.dev))
+    with torch.cuda.stream(s):
+        gm._step(static["tok"], static["pos"], None, 1.5, 50, 1.0, forced=static["forced"])
+    torch.cuda.current_stream(gm.dev).wait_stream(s)
+    glog = []
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        gm._step(static["tok"], static["pos"], None, 1.5, 50, 1.0, forced=static["forced"],
+                 logits_out=glog)
+    for _ in range(2):
+        gr.replay()
+        torch.cuda.synchronize()
+        for i in range(N_CB):
+            assert torch.equal(glog[i], eager[i]), f"graph replay head {i} differs from eager"
+
+
+def test_c3_frame_kv750_eager_and_graph(dev, c3):
+    """The benchmarked frame (3B backbone + 7 passes of the 1024-wide decoder, B = 8, KV 750)."""
+    om, gm = c3
+    _frame(om, gm, 750, seed=31, graph=True)
+
+
+def test_c3_frame_kv3256(dev, c3):
+    """The same frame at the end of a 4-minute song: 256-token prompt + 3000 frames."""
+    om, gm = c3
+    _frame(om, gm, 3256, seed=32)
+
+
+def test_reference_decoder_frame_kv750(dev):
+    """The frame with the reference's depth decoder: 3 layers, 3072 wide, 8q/4kv, head_dim 384."""
+    om, gm = _pair(dev, BB, DEC_REF, seed=22)
+    _frame(om, gm, 750, seed=33)
+
+
+def test_c4_prompt_pass_3b_layers(dev):
+    """Prompt pass at the 3B layer shape (2 of its 28 layers): B = 8 rows x 256 tokens through
+    the MFMA GEMMs and the causal flash attention, cache capacity 3514 (app/engine.py:123-178)."""
+    import torch
+    from estudiocanciones_amd.engine import Linear, Stack
+    from estudiocanciones_amd.quant import q8_rows
+    cfg = dict(BB, layers=2)
+    B, P, L = 8, 256, 3514
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    w = {}
+    from estudiocanciones_amd.quant import _stack_norms, _stack_shapes
+    for name, (Nn, K) in _stack_shapes("backbone", cfg):
+        w[name + ".q8"], w[name + ".s8"] = q8_rows(torch.randn(Nn, K, generator=g, device=dev) * 0.02)
+    for name, d in _stack_norms("backbone", cfg):
+        w[name] = (1.0 + 0.02 * torch.randn(d, generator=g, device=dev)).to(torch.bfloat16)
+    wn = {k: _host(v) for k, v in w.items()}
+
+    def op(name, norm=False):
+        from oracle.model import OLinear
+        from oracle.numerics import bf16_to_f32, f16
+        from oracle.quant import scale_f16
+        if norm:
+            return f16(bf16_to_f32(wn[name]))
+        return OLinear(wn[name + ".q8"], scale_f16(wn[name + ".s8"]))
+
+    def gp(name, norm=False):
+        if norm:
+            return w[name].to(torch.float16)
+        return Linear(q8=w[name + ".q8"], s8=w[name + ".s8"].to(torch.float16))
+
+    ost = OStack(op, "backbone", cfg)
+    ost.alloc(B, L)
+    st = Stack(gp, "backbone", cfg)
+    st.alloc(B, L, dev, torch.float16)
+    for b in st.blocks:
+        b.qkv.pack(stream=True)
+        b.o.pack(stream=True)
+        b.w13.pack(interleave=True, stream=True)
+        b.w2.pack(stream=True)
+    x = randn16(42, B, P, 3072)
+    pos = np.arange(P, dtype=np.int64)
+    print("[prompt] oracle (float64 and float32 sums)", flush=True)
+
+    def run_oracle():
+        out = ost.prefill(x, pos)
+        return out, [(b.kc[:, :, :P].copy(), b.vc[:, :, :P].copy()) for b in ost.blocks]
+
+    (want, wc), (alt, ac) = _oracle_twice(run_oracle)
+    print("[prompt] gpu", flush=True)
+    got = st(torch.from_numpy(x).to(dev), torch.from_numpy(pos).to(dev)[None].expand(B, P))
+    torch.cuda.synchronize()
+    assert_within_noise(N(got), want, alt, what="3B prompt pass output")
+    # layer 0's cache is one GEMM deep: the kernel bar
+    assert_close16(N(st.blocks[0].kc[:, :, :P]), wc[0][0], what="prompt k cache, layer 0")
+    assert_close16(N(st.blocks[0].vc[:, :, :P]), wc[0][1], what="prompt v cache, layer 0")
+    assert_within_noise(N(st.blocks[1].kc[:, :, :P]), wc[1][0], ac[1][0], what="prompt k cache, layer 1")
+    assert_within_noise(N(st.blocks[1].vc[:, :, :P]), wc[1][1], ac[1][1], what="prompt v cache, layer 1")
+
+
+# ---------------------------------------------------------------- isolated kernels (C1)
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("Nn,K", [(8192, 3072), (3072, 8192)])
+def test_gemv_backbone_shapes(dev, M, Nn, K):
+    """int8_mm (row-major weights) and the packed GEMV at the C1 shapes."""
+    import torch
+    from estudiocanciones_amd.kernels import gemv_packed, int8_mm, pack_i8
+    from estudiocanciones_amd.quant import q8_rows
+    g = torch.Generator(device=dev)
+    g.manual_seed(M * 7 + K)
+    q, sb = q8_rows(torch.randn(Nn, K, generator=g, device=dev) * 0.02)
+    s = sb.to(torch.float16)
+    x = randn16(50 + M, M, K)
+    r = randn16(60 + M, M, Nn)
+    want = OK.gemv_i8(x, N(q), N(s), r)
+    xt, rt = torch.from_numpy(x).to(dev), torch.from_numpy(r).to(dev)
+    assert_close16(N(int8_mm(xt, q, s, rt)), want, what=f"int8_mm M={M} {K}->{Nn}")
+    assert_close16(N(gemv_packed(xt, pack_i8(q), s, Nn, K, rt, stream=True)), want,
+                   what=f"packed M={M} {K}->{Nn}")
+
+
+@pytest.mark.parametrize("R,L", [(1, 512), (8, 512), (1, 2048), (8, 2048), (1, 8192), (8, 8192)])
+def test_decode_attn_backbone_lengths(dev, R, L):
+    """GQA decode attention (24q/8kv, head_dim 128, 16 splits) with the last row at L - 1."""
+    import torch
+    from estudiocanciones_amd.kernels import _attn, _attn_combine
+    Hq, Hk, HD, ns = 24, 8, 128, 16
+    q = randn16(70, R, Hq * HD)
+    kc = randn16(71, R, Hk, L, HD)
+    vc = randn16(72, R, Hk, L, HD)
+    pos = rng(73).integers(0, L, R).astype(np.int64)
+    pos[-1] = L - 1
+    want = OK.decode_attn_out(q, kc, vc, pos, 1, Hq, Hk, HD, nsplit=ns)
+    o = torch.empty(R, Hq * HD, dtype=torch.float16, device=dev)
+    pm = torch.empty(R * Hq * ns, device=dev)
+    pl = torch.empty_like(pm)
+    pa = torch.empty(R * Hq * ns, HD, device=dev)
+    T = lambda a: torch.from_numpy(a).to(dev)
+    _attn[(R, Hk, ns)](T(q), T(kc), T(vc), T(pos), o, pm, pl, pa, 1, Hq, Hk, L, 1 / math.sqrt(HD),
+                       HD=HD, G=Hq // Hk, NSPLIT=ns)
+    _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, NSPLIT=ns)
+    assert_close16(N(o), want, what=f"attn R={R} L={L}")
+    assert_close16(N(o), OK.attention_exact(q, kc, vc, pos, 1, Hq, Hk, HD), what="vs exact softmax")

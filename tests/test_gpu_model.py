@@ -11,7 +11,7 @@ import pytest
 
 from helpers import (AUDIO_VOCAB, N_CB, assert_close16, model_weights_np, randn16, rng,
                      tiny_cfgs, to_torch)
-from oracle.model import OModel, OStack
+from oracle.model import OModel, OStack, frame_loop_trim
 
 pytestmark = pytest.mark.gpu
 
@@ -216,3 +216,47 @@ def test_generate_small_song(dev):
     one = gm.generate(text, 3, max_ms=80 * 5, seed=1, use_graphs=False)
     assert one.shape[0] == N_CB
     assert gm.generate(text, 3, max_ms=800, abort=lambda: True) is None
+
+
+@pytest.mark.parametrize("use_graphs", [True, False])
+@pytest.mark.parametrize("ends", [(3, 26, 51, None), (3, 26, 40, 12)], ids=["one-never", "all-end"])
+def test_generate_forced_eos_trim(dev, use_graphs, ends):
+    """The song loop (app/engine.py:401-446) with every frame's tokens forced: EOS first appears
+    at the given frames (None: never); later EOS tokens and one in the prompt frame change
+    nothing.  The returned takes and the frames run equal the oracle's restatement of the EOS
+    scan (every 25 frames) and the per-take trim."""
+    import torch
+    from estudiocanciones_amd.engine import HeartMuLaLite
+    bb, dec = tiny_cfgs()
+    wn = model_weights_np(bb, dec, seed=4)
+    gm = HeartMuLaLite(to_torch(wn, dev), device=dev, backbone=bb, decoder=dec)
+    n, n_frames = 4, 60
+    g = rng(12)
+    frames = g.integers(0, 8193, (n_frames + 1, 2 * n, N_CB)).astype(np.int64)
+    for c, t in enumerate(ends):
+        if t is not None:
+            frames[t, c, 5] = 8193 + c
+            frames[min(t + 2, n_frames), c, 0] = 8196
+    frames[0, 3, 1] = 8193
+    frames[:, n:] = frames[:, :n]
+    want, ran = frame_loop_trim(frames[:, :n], n_frames)
+    got = gm.generate(rng(9).integers(0, 64, 10), 3, max_ms=80 * n_frames, seed=1, n=n,
+                      use_graphs=use_graphs, forced=torch.from_numpy(frames).to(dev))
+    assert gm.frames_run == ran
+    for c in range(n):
+        assert np.array_equal(N(got[c]), want[c]), c
+
+
+def test_generate_graph_equals_eager(dev):
+    """Sampled songs (no forcing): the captured loop and the eager loop give the same tokens for
+    the same seed, and a second run repeats them."""
+    from estudiocanciones_amd.engine import HeartMuLaLite
+    bb, dec = tiny_cfgs()
+    wn = model_weights_np(bb, dec, seed=4)
+    gm = HeartMuLaLite(to_torch(wn, dev), device=dev, backbone=bb, decoder=dec)
+    text = rng(9).integers(0, 64, 10)
+    a = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=2)
+    b = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=2, use_graphs=False)
+    c = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=2)
+    for x, y, z in zip(a, b, c):
+        assert np.array_equal(N(x), N(y)) and np.array_equal(N(x), N(z))
