@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libecdecode.so"
 ECD_OK = 0
 ECD_EINVAL = -22
 ECD_ENOTSUP = -95
+ECD_ENOMEM = -12
 
 _P = c_void_p
 # name -> argtypes, in the order of include/ecdecode.h
@@ -26,6 +27,8 @@ SIGNATURES = {
     "ecd_decode_attn": [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
                         c_int, c_float, _P],
     "ecd_attn_combine": [_P, _P, _P, _P, c_int, c_int, c_int, _P],
+    "ecd_decode_attn_noalloc": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                c_float, _P],
     "ecd_silu_mul": [_P, _P, c_int, c_int, _P],
     "ecd_embed_sum_i8": [_P, _P, _P, c_long, _P, c_int, c_int, c_int, c_int, _P],
     "ecd_embed_i8": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, c_int, c_int, _P],
@@ -113,6 +116,8 @@ def check(rc: int, name: str) -> None:
         raise ValueError(f"{name}: invalid argument")
     if rc == ECD_ENOTSUP:
         raise NotImplementedError(f"{name}: shape not supported by the gfx950 kernels")
+    if rc == ECD_ENOMEM:
+        raise MemoryError(f"{name}: the call needs more than the library's static workspace")
     raise ECDError(f"{name}: HIP launch failed (hipError_t {rc})")
 
 

@@ -18,6 +18,8 @@
 //                        the same 16-lane row and arrive through lane shuffles.
 // Each K and V byte of the attended range is read once per (row, kv head): the G query
 // heads of a group share it (no repeat_kv copy).
+#include <mutex>
+
 #include "attn_core.h"
 
 namespace ecd {
@@ -160,6 +162,37 @@ static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* 
 #undef ECD_ATTN_G
 }
 
+// Split partials of ecd_decode_attn_noalloc, for callers that cannot allocate: one static
+// array per GPU (each device holds its own copy at its own address), laid out as the
+// caller-supplied pm | pl | pa of ecd_decode_attn.  Every used slot is written by the attention
+// kernel before the combine reads it (empty splits write m = -inf, l = 0, acc = 0), so nothing
+// is cleared between calls; calls that overlap on one GPU share the array and race.
+constexpr long ATTN_SCRATCH_BYTES = 8l << 20;
+static __device__ __align__(256) unsigned char attn_scratch[ATTN_SCRATCH_BYTES];
+
+// Device address of attn_scratch on the current device, looked up once per device with that
+// device current (host code must never pass the array's name itself to a kernel).
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static int attn_scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return ECD_ENOTSUP;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(attn_scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return ECD_ENOTSUP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ECD_OK;
+}
+
 }  // namespace ecd
 
 using namespace ecd;
@@ -198,6 +231,32 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
   }
   if (rc != ECD_OK) return rc;
   return ecd_launch_status();
+}
+
+int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                            void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
+                            float scale, void* stream) {
+  if (!q || !kc || !vc || !pos || !o || R <= 0 || S <= 0 || Hq <= 0 || Hk <= 0 || L <= 0 ||
+      HD <= 0 || HD > 512 || nsplit <= 0 || (Hq % Hk) != 0)
+    return ECD_EINVAL;
+  if (nsplit == 1)
+    return ecd_decode_attn(q, kc, vc, pos, o, nullptr, nullptr, nullptr, R, S, Hq, Hk, L, HD, 1,
+                           scale, stream);
+  // pm [RHs] | pl [RHs] | pa [RHs, HD] fp32, RHs = R * Hq * nsplit, each part 256-byte aligned
+  const long rhs = (long)R * Hq * nsplit;
+  const long part = ((rhs * 4 + 255) / 256) * 256;
+  const long need = 2 * part + rhs * HD * 4;
+  if (need > ATTN_SCRATCH_BYTES) return ECD_ENOMEM;
+  void* base = nullptr;
+  const int rc = attn_scratch_ptr(&base);
+  if (rc != ECD_OK) return rc;
+  float* pm = (float*)base;
+  float* pl = (float*)((char*)base + part);
+  float* pa = (float*)((char*)base + 2 * part);
+  const int r1 = ecd_decode_attn(q, kc, vc, pos, o, pm, pl, pa, R, S, Hq, Hk, L, HD, nsplit, scale,
+                                 stream);
+  if (r1 != ECD_OK) return r1;
+  return ecd_attn_combine(pm, pl, pa, o, R * Hq, HD, nsplit, stream);
 }
 
 int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,

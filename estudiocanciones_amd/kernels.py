@@ -213,6 +213,31 @@ _attn_combine = _Launcher("_attn_combine", _attn_combine_impl,
                           lambda pm, pl, pa, o, HD=None, HDP=None, NSPLIT=16: (o.numel() // HD,))
 
 
+def decode_attn_noalloc(q, kc, vc, pos, S, Hq, Hk, L, scale, nsplit=16, out=None):
+    """_attn + _attn_combine in one call whose split partials live in the library's static
+    device workspace (8 MiB per GPU): nothing is allocated when ``out`` is given, so it can run
+    under hipGraph capture without a memory pool.  Raises MemoryError when R * Hq * nsplit
+    partials do not fit.  Calls overlapping on one GPU share the workspace."""
+    dev = _dev(q, "decode_attn_noalloc")
+    for t, n in ((q, "q"), (kc, "kc"), (vc, "vc")):
+        _f16(t, f"decode_attn_noalloc {n}")
+        if not t.is_contiguous():
+            raise ValueError(f"decode_attn_noalloc: {n} must be contiguous")
+    if pos.dtype != torch.int64 or not pos.is_contiguous():
+        raise TypeError("decode_attn_noalloc: pos must be contiguous int64")
+    R = q.shape[0]
+    HD = kc.shape[-1]
+    if q.numel() != R * Hq * HD or pos.numel() != R or kc.shape[1] != Hk or kc.shape[-2] != L \
+            or kc.shape[0] * S < R or vc.shape != kc.shape:
+        raise ValueError("decode_attn_noalloc: shape mismatch")
+    o = out if out is not None else torch.empty_like(q)
+    if o.shape != q.shape or o.dtype != torch.float16 or not o.is_contiguous():
+        raise ValueError("decode_attn_noalloc: out must be a contiguous fp16 tensor shaped like q")
+    _ffi.call("ecd_decode_attn_noalloc", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(),
+              o.data_ptr(), R, S, Hq, Hk, L, HD, int(nsplit), float(scale), stream_ptr(dev))
+    return o
+
+
 # ---------------------------------------------------------------- SiLU(a) * b
 def _silu_mul_impl(x, y, F_, BLOCK=None):
     dev = _dev(x, "_silu_mul")

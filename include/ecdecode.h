@@ -27,6 +27,7 @@ extern "C" {
 #define ECD_OK 0
 #define ECD_EINVAL (-22)
 #define ECD_ENOTSUP (-95)
+#define ECD_ENOMEM (-12) /* the call needs more than a fixed-size static workspace */
 
 /* int8 per-output-channel GEMV / skinny GEMM with optional residual.
  * Replaces int8_mm + _gemv8 (app/kernels.py:40-54, :20-37) and its dense fallback for
@@ -75,6 +76,18 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
  * Replaces _attn_combine (app/kernels.py:156-167), launched at app/engine.py:204. */
 int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,
                      int nsplit, void* stream);
+
+/* ecd_decode_attn followed by ecd_attn_combine into o, with the split partials kept in a
+ * static device array of 8 MiB (one per GPU) instead of caller buffers: nothing is allocated
+ * on any call.  No counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under hipGraph capture that may not call hipMalloc, tight serving loops).
+ * Same arguments and results as the two calls it replaces (bit for bit).  Returns ECD_ENOMEM
+ * when 2 * ceil256(4 * R * Hq * nsplit) + 4 * R * Hq * nsplit * HD bytes exceed 8 MiB (e.g.
+ * R = 16, Hq = 24, nsplit = 16, HD = 128 needs 3.2 MB).  The array keeps the last call's
+ * contents; calls that overlap on one GPU (two streams at once) race on it. */
+int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                            void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
+                            float scale, void* stream);
 
 /* y[r, c] = f16(f16(silu(x[r, c])) * x[r, F + c]) for x [R, 2F], y [R, F].
  * Replaces _silu_mul (app/kernels.py:171-180), launched at app/engine.py:209. */

@@ -56,6 +56,8 @@ def _taps(*offsets):
     lambda L: L.ecd_decode_attn(8, 8, 8, 8, 8, None, None, None, 1, 1, 8, 2, 8, 128, 16, 0.1, None),
     lambda L: L.ecd_decode_attn(8, 8, 8, 8, None, None, None, None, 1, 1, 8, 2, 8, 128, 1, 0.1, None),
     lambda L: L.ecd_attn_combine(None, None, None, None, 1, 128, 16, None),
+    lambda L: L.ecd_decode_attn_noalloc(8, 8, 8, 8, None, 1, 1, 8, 2, 8, 128, 16, 0.1, None),   # no o
+    lambda L: L.ecd_decode_attn_noalloc(8, 8, 8, 8, 8, 1, 1, 8, 3, 8, 128, 16, 0.1, None),      # Hq % Hk
     lambda L: L.ecd_gemv_i8p_splitk(16, 64, 16, 16, None, 0, 16, 64, 1, 64, 192, 2, 16, 0, None),  # 3 chunks % 2
     lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
@@ -138,3 +140,12 @@ def test_gemm_rejects_x_beyond_32bit_offsets():
     # M = 2^17 rows of ldx = 2^13 halfs -> 2 GiB
     assert L.ecd_gemm_i8p(16, 8192, 16, 16, None, 0, 16, 64, 1 << 17, 64, 8192, None) == _ffi.ECD_ENOTSUP
     assert L.ecd_gemm_i8p_silu(16, 8192, 16, 16, 16, 64, 1 << 17, 32, 8192, None) == _ffi.ECD_ENOTSUP
+
+
+def test_noalloc_attention_refuses_oversized_workspace():
+    """The static-workspace attention returns ECD_ENOMEM on the host, before any HIP call, when
+    its split partials exceed the 8 MiB array (64 rows x 32 heads x 32 splits x head_dim 512)."""
+    from estudiocanciones_amd import _ffi
+    L = _ffi.lib()
+    assert L.ecd_decode_attn_noalloc(16, 16, 16, 16, 16, 64, 1, 32, 8, 8192, 512, 32, 0.1,
+                                     None) == _ffi.ECD_ENOMEM
