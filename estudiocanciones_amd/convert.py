@@ -7,9 +7,12 @@ unrounded fp32 scale max|w|/127, round half to even, clamp to +-127).  The stack
 ``audio_head`` [7, D, V] is stored as 7 transposed [V, D] heads ``audio_head.{i}``.  The rotary
 ``pos_embeddings`` (recomputed at load) and ``muq_linear.weight`` (its input is always zero, only
 the bias matters) are dropped; ``unconditional_text_embedding.weight`` and every 1-D tensor are
-kept in bf16.  The file metadata carries ``{"lite": "{\\"mode\\": \\"int8\\"}"}``.
+kept in bf16, and with ``--keep-emb-bf16`` the ``text_embeddings`` / ``audio_embeddings`` tables
+too (app/convert_final.py:43, :66).  The file metadata carries
+``{"lite": "{\\"mode\\": \\"int8\\"}"}``.
 
     python -m estudiocanciones_amd.convert <HeartMuLa dir | model.safetensors> <out.safetensors>
+        [--keep-emb-bf16]
 """
 from __future__ import annotations
 
@@ -34,8 +37,9 @@ def _quantise(t: torch.Tensor, device) -> tuple[torch.Tensor, torch.Tensor]:
     return q.cpu(), s.cpu()
 
 
-def convert_tensors(items, device="cuda") -> dict:
-    """(name, tensor) pairs of the official checkpoint -> {name: tensor} of the int8 format."""
+def convert_tensors(items, device="cuda", keep_emb=False) -> dict:
+    """(name, tensor) pairs of the official checkpoint -> {name: tensor} of the int8 format;
+    ``keep_emb`` keeps the embedding tables in bf16."""
     dev = torch.device(device)
     out = {}
     for name, t in items:
@@ -44,7 +48,7 @@ def convert_tensors(items, device="cuda") -> dict:
         if name == "audio_head":
             for i in range(t.shape[0]):
                 out[f"audio_head.{i}.q8"], out[f"audio_head.{i}.s8"] = _quantise(t[i].t(), dev)
-        elif t.dim() == 2 and name not in KEPT_DENSE:
+        elif t.dim() == 2 and name not in KEPT_DENSE and not (keep_emb and "embeddings" in name):
             out[name + ".q8"], out[name + ".s8"] = _quantise(t, dev)
         else:
             out[name] = t.to(torch.bfloat16).contiguous().cpu()
@@ -63,7 +67,7 @@ def checkpoint_files(src) -> list[Path]:
     return [src / "model.safetensors"]
 
 
-def convert_file(src, dst, device="cuda") -> Path:
+def convert_file(src, dst, device="cuda", keep_emb=False) -> Path:
     """Convert an official checkpoint (directory or file) into ``dst``."""
     from safetensors import safe_open
     from safetensors.torch import save_file
@@ -74,14 +78,15 @@ def convert_file(src, dst, device="cuda") -> Path:
                 for k in f.keys():
                     yield k, f.get_tensor(k)
 
-    out = convert_tensors(items(), device)
+    out = convert_tensors(items(), device, keep_emb)
     dst = Path(dst)
     save_file(out, str(dst), metadata={"lite": json.dumps({"mode": "int8"})})
     return dst
 
 
 if __name__ == "__main__":
-    if len(sys.argv) != 3:
+    args = [a for a in sys.argv[1:] if a != "--keep-emb-bf16"]
+    if len(args) != 2:
         raise SystemExit(__doc__)
-    path = convert_file(sys.argv[1], sys.argv[2])
+    path = convert_file(args[0], args[1], keep_emb="--keep-emb-bf16" in sys.argv)
     print(path.name, round(path.stat().st_size / 1e9, 3), "GB")

@@ -141,6 +141,11 @@ __device__ __host__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Dense-numerics MFMA GEMM on a row-major [N, K] int8 weight (gemm_i8.hip); returns 1 without
+// launching when the operands do not fit it.
+int gemm_i8_rowmajor(const f16* x, long ldx, const int8_t* w, const f16* s, const f16* res,
+                     long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st);
+
 }  // namespace ecd
 
 // Launch-error plumbing shared by the entry points.

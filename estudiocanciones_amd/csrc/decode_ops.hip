@@ -1,5 +1,5 @@
 // Row-wise and element-wise kernels of the per-frame decode step (gfx950):
-// RMSNorm, RoPE + KV-cache write, SiLU(a)*b, int8 embedding gathers, the per-row
+// RMSNorm, RoPE + KV-cache write, SiLU(a)*b, embedding gathers, the per-row
 // int8 quantiser and the Llama-3-scaled RoPE table.  All fp16 rounding points follow
 // the reference kernels (app/kernels.py) exactly; accumulation is fp32.
 #include "common.h"
@@ -111,12 +111,21 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const f16* __restrict__ x
   }
 }
 
-// ---------------------------------------------------------------- int8 embeddings
-// Backbone input (app/engine.py:98, :348): out[b, :] = fp16( sum_c fp16(fp16(q[row]) * s[row]) ),
-// row = tok[b, c] + c * vocab, accumulated in fp32 over the C codebooks.
-// A token outside [0, vocab) (or a row beyond the table) contributes nothing.
+// ---------------------------------------------------------------- embeddings
+// Tables are int8 rows with per-row fp16 scales (e = fp16(fp16(q[row]) * s[row]),
+// app/engine.py:98) or, when no scales are given, dense fp16 rows (the bf16 tables of files
+// written with --keep-emb-bf16, loaded as fp16: e = w[row], app/engine.py:95-97, :244-247).
+__device__ __forceinline__ f16 emb_at(const void* table, const f16* scales, long rowi, long D,
+                                      int d) {
+  if (scales) return (f16)(float)((const int8_t*)table)[rowi * D + d] * scales[rowi];
+  return ((const f16*)table)[rowi * D + d];
+}
+
+// Backbone input (app/engine.py:98, :348): out[b, :] = fp16( sum_c e(row) ), row = tok[b, c] +
+// c * vocab, accumulated in fp32 over the C codebooks.  A token outside [0, vocab) (or a row
+// beyond the table) contributes nothing.
 __global__ __launch_bounds__(256) void embed_sum_kernel(const int64_t* __restrict__ tok,
-                                                        const int8_t* __restrict__ table,
+                                                        const void* __restrict__ table,
                                                         const f16* __restrict__ scales,
                                                         f16* __restrict__ out, int C, int D,
                                                         int vocab, long rows) {
@@ -128,18 +137,17 @@ __global__ __launch_bounds__(256) void embed_sum_kernel(const int64_t* __restric
     const long t = tok[(long)b * C + c];
     const long rowi = t + (long)c * vocab;
     if (t < 0 || t >= vocab || rowi >= rows) continue;
-    const f16 e = (f16)(float)table[rowi * D + d] * scales[rowi];
-    acc += (float)e;
+    acc += (float)emb_at(table, scales, rowi, D, d);
   }
   out[(long)b * D + d] = (f16)acc;
 }
 
-// Decoder input (app/engine.py:307-308, :336, :342): out[b] = fp16(fp16(q[row]) * s[row]) with
+// Decoder input (app/engine.py:307-308, :336, :342): out[b] = e(row) with
 // row = tok[b * tok_stride] + cb * vocab.  With `even` set, row 2b of out receives even[b]
 // and row 2b+1 the embedding (the two-row interleave of the first decoder pass).
 __global__ __launch_bounds__(256) void embed_one_kernel(const int64_t* __restrict__ tok,
                                                         long tok_stride,
-                                                        const int8_t* __restrict__ table,
+                                                        const void* __restrict__ table,
                                                         const f16* __restrict__ scales, int cb,
                                                         int vocab, long rows,
                                                         const f16* __restrict__ even,
@@ -150,9 +158,7 @@ __global__ __launch_bounds__(256) void embed_one_kernel(const int64_t* __restric
   const long t = tok[(long)b * tok_stride];
   f16 e = (f16)0.0f;
   const long rowi = t + (long)cb * vocab;
-  if (t >= 0 && t < vocab && rowi < rows) {
-    e = (f16)(float)table[rowi * D + d] * scales[rowi];
-  }
+  if (t >= 0 && t < vocab && rowi < rows) e = emb_at(table, scales, rowi, D, d);
   if (even) {
     out[(2L * b) * D + d] = even[(long)b * D + d];
     out[(2L * b + 1) * D + d] = e;
@@ -269,24 +275,23 @@ int ecd_silu_mul(const void* x, void* y, int R, int F, void* stream) {
 
 int ecd_embed_sum_i8(const int64_t* tok, const void* table, const void* scales, long rows,
                      void* out, int B, int C, int D, int vocab, void* stream) {
-  if (!tok || !table || !scales || !out || B <= 0 || C <= 0 || D <= 0 || vocab <= 0 || rows <= 0)
+  if (!tok || !table || !out || B <= 0 || C <= 0 || D <= 0 || vocab <= 0 || rows <= 0)
     return ECD_EINVAL;
   dim3 grid((D + 255) / 256, B);
-  hipLaunchKernelGGL(embed_sum_kernel, grid, dim3(256), 0, (hipStream_t)stream, tok,
-                     (const int8_t*)table, (const f16*)scales, (f16*)out, C, D, vocab, rows);
+  hipLaunchKernelGGL(embed_sum_kernel, grid, dim3(256), 0, (hipStream_t)stream, tok, table,
+                     (const f16*)scales, (f16*)out, C, D, vocab, rows);
   return ecd_launch_status();
 }
 
 int ecd_embed_i8(const int64_t* tok, long tok_stride, const void* table, const void* scales,
                  long rows, int cb, int vocab, const void* even, void* out, int B, int D,
                  void* stream) {
-  if (!tok || !table || !scales || !out || B <= 0 || D <= 0 || vocab <= 0 || cb < 0 ||
-      tok_stride <= 0 || rows <= 0)
+  if (!tok || !table || !out || B <= 0 || D <= 0 || vocab <= 0 || cb < 0 || tok_stride <= 0 ||
+      rows <= 0)
     return ECD_EINVAL;
   dim3 grid((D + 255) / 256, B);
   hipLaunchKernelGGL(embed_one_kernel, grid, dim3(256), 0, (hipStream_t)stream, tok, tok_stride,
-                     (const int8_t*)table, (const f16*)scales, cb, vocab, rows, (const f16*)even,
-                     (f16*)out, D);
+                     table, (const f16*)scales, cb, vocab, rows, (const f16*)even, (f16*)out, D);
   return ecd_launch_status();
 }
 

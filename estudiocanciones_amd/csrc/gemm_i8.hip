@@ -5,7 +5,10 @@
 //   at 2j + 1), mm[m, j] = fp16(fp16(silu(y[m, 2j])) * y[m, 2j + 1]) (app/kernels.py:171-180).
 //
 // Weights use the lane-ordered packed layout of gemv_fused.hip: chunk (tile, c) = 16 rows x
-// 64 bytes stored so that lane l's 16 bytes are row l & 15, k = 64c + 16 (l >> 4) .. +15.
+// 64 bytes stored so that lane l's 16 bytes are row l & 15, k = 64c + 16 (l >> 4) .. +15.  The
+// row-major variant (RM) reads the same 16 bytes straight from an [N, K] int8 matrix (the
+// layout int8_mm receives, app/kernels.py:40-49): the DMA lands them in LDS in the same lane
+// order, so everything after the load is shared.
 //
 // Tiling: a block computes 128 output features x 128 rows with 4 waves; wave w owns features
 // 32 w .. 32 w + 31 for all 128 rows = 2 x 8 tiles of v_mfma_f32_16x16x32_f16 (weights = A
@@ -36,7 +39,7 @@ constexpr int GT_N = 128;   // output features per block
 constexpr int GT_M = 128;   // rows per block
 constexpr int GT_NS = 2;    // LDS stages
 
-template <int EPI>
+template <int EPI, bool RM>
 __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     const f16* __restrict__ x, long ldx, const int8_t* __restrict__ wp,
     const f16* __restrict__ s, const f16* __restrict__ res, long ldr, f16* __restrict__ y, long ldy, int M, int N, int K,
@@ -68,9 +71,18 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   // thread issues the same number of loads.
   // The addresses are a wave-uniform base (SGPRs, advanced per chunk by scalar adds) plus a
   // per-lane byte offset fixed for the whole loop (the host keeps the x buffer below 2 GiB).
-  const int8_t* wbase0 = wp + (long)min(n0 / 16 + wv, ntiles - 1) * nch * WB;
-  const int8_t* wbase1 = wp + (long)min(n0 / 16 + 4 + wv, ntiles - 1) * nch * WB;
-  const uint32_t woff = 16u * lane;
+  const int t0 = min(n0 / 16 + wv, ntiles - 1), t1 = min(n0 / 16 + 4 + wv, ntiles - 1);
+  const int8_t* wbase0 = wp + (RM ? (long)t0 * 16 * K : (long)t0 * nch * WB);
+  const int8_t* wbase1 = wp + (RM ? (long)t1 * 16 * K : (long)t1 * nch * WB);
+  // row-major: row 16 t + (lane & 15) (the last row for rows past N), bytes 16 (lane >> 4) of
+  // each 64-byte chunk; the per-lane offsets stay below 16 K bytes
+  const uint32_t woff0 = RM ? (uint32_t)((min(16 * t0 + (lane & 15), N - 1) - 16 * t0) * K +
+                                         16 * (lane >> 4))
+                            : 16u * lane;
+  const uint32_t woff1 = RM ? (uint32_t)((min(16 * t1 + (lane & 15), N - 1) - 16 * t1) * K +
+                                         16 * (lane >> 4))
+                            : 16u * lane;
+  constexpr long WSTEP = RM ? 64 : WB;  // bytes between consecutive chunks of a tile
   const int xpiece = (lane & 7) ^ (lane >> 3);
   uint32_t xoff[4];
 #pragma unroll
@@ -78,8 +90,8 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     xoff[i] = (uint32_t)((long)min(m0 + 8 * (4 * wv + i) + (lane >> 3), M - 1) * ldx * 2 +
                          16 * xpiece);
   auto issue = [&](int c, int st) {
-    lds_dma16(wbase0 + (long)c * WB, woff, &lw[st][wv * WB]);
-    lds_dma16(wbase1 + (long)c * WB, woff, &lw[st][(4 + wv) * WB]);
+    lds_dma16(wbase0 + (long)c * WSTEP, woff0, &lw[st][wv * WB]);
+    lds_dma16(wbase1 + (long)c * WSTEP, woff1, &lw[st][(4 + wv) * WB]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       lds_dma16(x + (long)c * 64, xoff[i], &lx[st][8 * (4 * wv + i) * 64]);
@@ -167,14 +179,14 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   }
 }
 
-template <int EPI>
+template <int EPI, bool RM = false>
 static int launch_gemm(const f16* x, long ldx, const int8_t* wp, const f16* s, const f16* res,
                        long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st) {
   const int nfb = (N + GT_N - 1) / GT_N;
   const int nmb = (M + GT_M - 1) / GT_M;
   const long blocks = (long)((nfb + 7) / 8) * 8 * nmb;
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
-  hipLaunchKernelGGL((gemm_i8p_kernel<EPI>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
+  hipLaunchKernelGGL((gemm_i8p_kernel<EPI, RM>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
                      wp, s, res, ldr, y, ldy, M, N, K, nfb, nmb);
   return ecd_launch_status();
 }
@@ -183,6 +195,17 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // the per-lane byte offsets of the x loads are 32-bit: the x buffer must stay below 2 GiB
 static bool x_offsets_fit(int M, long ldx) { return (long)M * ldx * 2 < 0x7FFFFFFFL; }
+
+// The dense-numerics GEMM on a row-major [N, K] int8 weight (int8_mm with more than 16 rows).
+// Returns 1 without launching when the operands do not fit the kernel (the caller then runs
+// its own path).
+int gemm_i8_rowmajor(const f16* x, long ldx, const int8_t* w, const f16* s, const f16* res,
+                     long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st) {
+  if ((K % 64) || (ldx % 8) || !al16(x) || !al16(w) || !x_offsets_fit(M, ldx) ||
+      16L * K >= 0x7FFFFFFFL)
+    return 1;
+  return launch_gemm<GEPI_STORE, true>(x, ldx, w, s, res, ldr, y, ldy, M, N, K, st);
+}
 
 }  // namespace ecd
 

@@ -14,8 +14,9 @@
 //   PRO_PLAIN  x from memory
 //   PRO_RMS    x = fp16(fp16(xr * inv[m]) * nw[k]), inv[m] = 1/sqrt(sum(xr[m]^2)/K + eps)
 //              computed per block from the full rows (RMSNorm of app/kernels.py:58-67)
-//   PRO_EMBED  x = fp16(fp16(q[row]) * s[row]) of an int8 embedding table, row = tok + cb * V,
-//              with optional even rows taken from another tensor (app/engine.py:307-308, :336)
+//   PRO_EMBED  x = fp16(fp16(q[row]) * s[row]) of an int8 embedding table (or the row of a dense
+//              fp16 table), row = tok + cb * V, with optional even rows taken from another
+//              tensor (app/engine.py:307-308, :336)
 // Epilogues:
 //   EPI_STORE  y = fp16(acc * s) (+ res)
 //   EPI_ROPE   fused q|k|v output: interleaved RoPE of q and k, q -> q_out, k/v -> cache slot
@@ -41,6 +42,7 @@ struct GemvArgs {
   long tok_stride;
   const int8_t* etab;
   const f16* escale;
+  const f16* etab16;  // dense fp16 embedding table (etab/escale unused when set)
   long erows;
   int cb;
   int vocab;
@@ -236,8 +238,12 @@ __global__ __launch_bounds__(KW * 64) void gemv_fused_kernel(const GemvArgs a) {
       const long t = a.tok[(long)b * a.tok_stride];
       const long r = t + (long)a.cb * a.vocab;
       if (t >= 0 && t < a.vocab && r < a.erows) {
-        ep = a.etab + r * K + 16 * grp;
-        esc = a.escale[r];
+        if (a.etab16) {
+          xp = a.etab16 + r * K + 16 * grp;  // a dense row reads like x
+        } else {
+          ep = a.etab + r * K + 16 * grp;
+          esc = a.escale[r];
+        }
       }
     }
   }
@@ -425,6 +431,12 @@ __global__ __launch_bounds__(KW * 64) void gemv_xlds_kernel(const GemvArgs a) {
         const long t = a.tok[(long)b * a.tok_stride];
         const long r = t + (long)a.cb * a.vocab;
         const bool ok = t >= 0 && t < a.vocab && r < a.erows;
+        if (a.etab16) {
+          const f16* src = a.etab16 + (ok ? r : 0) * K;
+          const f16x8 z = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+          for (int k = lane * 8; k < K; k += 512) *(f16x8*)(dst + k) = ok ? ld8(src + k) : z;
+          continue;
+        }
         const int8_t* src = a.etab + (ok ? r : 0) * K;
         const f16 sc = ok ? a.escale[r] : (f16)0.0f;
         for (int k = lane * 16; k < K; k += 1024) {
@@ -953,11 +965,16 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
                        const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream) {
   GemvArgs a = {};
-  a.tok = tok; a.tok_stride = tok_stride; a.etab = (const int8_t*)table;
-  a.escale = (const f16*)tscale; a.erows = trows; a.cb = cb; a.vocab = vocab;
+  a.tok = tok; a.tok_stride = tok_stride; a.erows = trows; a.cb = cb; a.vocab = vocab;
+  if (tscale) {
+    a.etab = (const int8_t*)table;
+    a.escale = (const f16*)tscale;
+  } else {
+    a.etab16 = (const f16*)table;
+  }
   a.even = (const f16*)even; a.wp = (const int8_t*)wp; a.s = (const f16*)s;
   a.M = M; a.N = N; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1; a.y = (f16*)y; a.ldy = ldy;
-  if (check_common(a) || !tok || !table || !tscale || !y || tok_stride <= 0 || trows <= 0 ||
+  if (check_common(a) || !tok || !table || !y || tok_stride <= 0 || trows <= 0 ||
       cb < 0 || vocab <= 0 || ldy < N || !aligned16(table) || (even && !aligned16(even)) ||
       (even && (M & 1)))
     return ECD_EINVAL;

@@ -275,6 +275,15 @@ extern "C" {
 
 int ecd_gemv_i8(const void* x, long ldx, const void* w, const void* s, const void* res, long ldr,
                 void* y, long ldy, int M, int N, int K, int dense, void* stream) {
+  // many rows with the dense numerics (the reference's M > 16 path): the MFMA GEMM reads the
+  // weights once per XCD instead of once per 16-row tile
+  if (dense && M > 16 && x && w && s && y && N > 0 && K > 0 && ldx >= K && ldy >= N &&
+      (!res || ldr >= N)) {
+    const int rc = gemm_i8_rowmajor((const f16*)x, ldx, (const int8_t*)w, (const f16*)s,
+                                    (const f16*)res, ldr, (f16*)y, ldy, M, N, K,
+                                    (hipStream_t)stream);
+    if (rc != 1) return rc;
+  }
   return gemv_entry(x, ldx, w, s, res, ldr, y, ldy, M, N, K, dense, 0, 0, stream);
 }
 

@@ -115,34 +115,53 @@ def fuse(parts):
 
 
 class Emb:
-    """int8 per-row embedding table (app/engine.py:89-104)."""
+    """Embedding table (app/engine.py:89-104): int8 rows with per-row fp16 scales, or dense fp16
+    rows (the bf16 tables of a file written with --keep-emb-bf16, app/convert_final.py:43)."""
 
     def __init__(self, w=None, q8=None, s8=None):
-        if q8 is None:
-            raise NotImplementedError("the gfx950 decode path runs int8 embedding tables only")
-        self.w, self.q8, self.s8 = None, q8.contiguous(), s8.contiguous()
+        if w is None and q8 is None:
+            raise ValueError("Emb needs a dense table w or int8 rows q8 with scales s8")
+        if w is not None:
+            if w.dtype != torch.float16:
+                raise TypeError("Emb: the dense table must be float16 (the engine's dtype)")
+            self.w, self.q8, self.s8 = w.contiguous(), None, None
+        else:
+            self.w, self.q8, self.s8 = None, q8.contiguous(), s8.contiguous()
+
+    @property
+    def table(self):
+        return self.w if self.w is not None else self.q8
+
+    @property
+    def scales(self):
+        """Per-row scales, or None for a dense fp16 table (the kernels' convention)."""
+        return self.s8
+
+    def _args(self):
+        t = self.table
+        return t.data_ptr(), (self.s8.data_ptr() if self.s8 is not None else None), t.shape[0]
 
     def __call__(self, idx):
-        """fp16(q8[idx]) * s8[idx] -> [*idx.shape, D]."""
+        """The rows idx -> [*idx.shape, D] fp16."""
         idx = idx.to(torch.int64).contiguous()
-        D = self.q8.shape[1]
-        out = torch.empty(*idx.shape, D, device=self.q8.device, dtype=torch.float16)
+        D = self.table.shape[1]
+        out = torch.empty(*idx.shape, D, device=self.table.device, dtype=torch.float16)
         n = idx.numel()
         if n:
-            rows = self.q8.shape[0]
-            _ffi.call("ecd_embed_i8", idx.data_ptr(), 1, self.q8.data_ptr(), self.s8.data_ptr(),
-                      rows, 0, rows, None, out.data_ptr(), n, D, stream_ptr(out.device))
+            tab, sc, rows = self._args()
+            _ffi.call("ecd_embed_i8", idx.data_ptr(), 1, tab, sc, rows, 0, rows, None,
+                      out.data_ptr(), n, D, stream_ptr(out.device))
         return out
 
     def gather(self, tok, cb, vocab, even=None):
         """One codebook: rows tok[:, 0] + cb * vocab -> [B, D]; with ``even`` [B, D] the result
         is the interleave [2B, D] (even rows = even, odd rows = embeddings)."""
         B = tok.shape[0]
-        D = self.q8.shape[1]
-        out = torch.empty((2 * B if even is not None else B), D, device=self.q8.device,
+        D = self.table.shape[1]
+        out = torch.empty((2 * B if even is not None else B), D, device=self.table.device,
                           dtype=torch.float16)
-        _ffi.call("ecd_embed_i8", tok.data_ptr(), tok.stride(0), self.q8.data_ptr(),
-                  self.s8.data_ptr(), self.q8.shape[0], int(cb), int(vocab),
+        tab, sc, rows = self._args()
+        _ffi.call("ecd_embed_i8", tok.data_ptr(), tok.stride(0), tab, sc, rows, int(cb), int(vocab),
                   even.data_ptr() if even is not None else None, out.data_ptr(), B, D,
                   stream_ptr(out.device))
         return out
@@ -151,14 +170,17 @@ class Emb:
         """sum_c Emb(tok[:, c] + c * vocab) accumulated in fp32, one fp16 rounding (:348)."""
         tok = tok.contiguous()
         B, C = tok.shape
-        D = self.q8.shape[1]
-        out = torch.empty(B, D, device=self.q8.device, dtype=torch.float16)
-        _ffi.call("ecd_embed_sum_i8", tok.data_ptr(), self.q8.data_ptr(), self.s8.data_ptr(),
-                  self.q8.shape[0], out.data_ptr(), B, C, D, int(vocab), stream_ptr(out.device))
+        D = self.table.shape[1]
+        out = torch.empty(B, D, device=self.table.device, dtype=torch.float16)
+        tab, sc, rows = self._args()
+        _ffi.call("ecd_embed_sum_i8", tok.data_ptr(), tab, sc, rows, out.data_ptr(), B, C, D,
+                  int(vocab), stream_ptr(out.device))
         return out
 
     @property
     def nbytes(self):
+        if self.w is not None:
+            return self.w.numel() * 2
         return self.q8.numel() + self.s8.numel() * 2
 
 
@@ -457,7 +479,7 @@ class HeartMuLaLite:
             x = e.gather(tok, cb, AUDIO_VOCAB, even=even)
             return pr(x)
         ev = None if even is None else even.contiguous()
-        return embed_gemv_packed(tok, e.q8, e.s8, cb, AUDIO_VOCAB, pr.qp, pr.s8, pr.N, even=ev)
+        return embed_gemv_packed(tok, e.table, e.scales, cb, AUDIO_VOCAB, pr.qp, pr.s8, pr.N, even=ev)
 
     def _step(self, tok, pos, bucket, cfg, topk, temp, **kw):
         """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349)."""

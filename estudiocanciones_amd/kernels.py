@@ -470,10 +470,13 @@ def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5, stream=False):
 
 def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False):
     """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
-    interleave (even[b], emb[b]) and the output has 2B rows."""
+    interleave (even[b], emb[b]) and the output has 2B rows.  ``table`` holds int8 rows scaled by
+    ``tscale``, or dense fp16 rows when ``tscale`` is None."""
     dev = _dev(tok, "embed_gemv_packed")
     if tok.dtype != torch.int64:
         raise TypeError("embed_gemv_packed: tok must be int64")
+    if (tscale is None) != (table.dtype == torch.float16) or table.dtype not in (torch.int8, torch.float16):
+        raise TypeError("embed_gemv_packed: int8 table with scales, or fp16 table without")
     B = tok.shape[0]
     K = table.shape[1]
     M = 2 * B if even is not None else B
@@ -482,7 +485,7 @@ def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream
         if even.shape != (B, K) or not even.is_contiguous() or even.data_ptr() % 16:
             raise ValueError("embed_gemv_packed: even must be contiguous [B, K]")
     y = torch.empty(M, N, device=dev, dtype=torch.float16)
-    _ffi.call("ecd_embed_gemv_i8p", tok.data_ptr(), tok.stride(0), table.data_ptr(), tscale.data_ptr(),
+    _ffi.call("ecd_embed_gemv_i8p", tok.data_ptr(), tok.stride(0), table.data_ptr(), _ptr(tscale),
               table.shape[0], int(cb), int(vocab), _ptr(even), wp.data_ptr(), s.data_ptr(),
               y.data_ptr(), N, M, N, K, _flags(M, stream), stream_ptr(dev))
     return y

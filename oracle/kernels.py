@@ -212,8 +212,13 @@ def embed_sum(q8, s16, tok, vocab) -> np.ndarray:
     tok = np.asarray(tok, dtype=np.int64)
     C = tok.shape[1]
     rows = tok + np.arange(C, dtype=np.int64)[None, :] * vocab
-    e = embed_rows(q8, s16, rows).astype(np.float32)                  # [B, C, D]
-    acc = np.zeros(e.shape[::2], np.float32)
-    for c in range(C):
+    return sum_rows(embed_rows(q8, s16, rows))
+
+
+def sum_rows(e) -> np.ndarray:
+    """[B, C, D] fp16 -> fp16(sum over C in fp32) (the .sum(1, dtype=fp16) of app/engine.py:348)."""
+    e = np.asarray(e, np.float16).astype(np.float32)
+    acc = np.zeros((e.shape[0], e.shape[2]), np.float32)
+    for c in range(e.shape[1]):
         acc = (acc + e[:, c]).astype(np.float32)
     return f16(acc)

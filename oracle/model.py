@@ -154,8 +154,13 @@ class OModel:
 
         self.backbone = OStack(p, "backbone", backbone_cfg)
         self.decoder = OStack(p, "decoder", decoder_cfg)
-        self.audio_q8 = weights["audio_embeddings.weight.q8"]
-        self.audio_s = scale_f16(weights["audio_embeddings.weight.s8"])
+        if "audio_embeddings.weight" in weights:     # dense table (--keep-emb-bf16 files)
+            self.audio_dense = f16(bf16_to_f32(weights["audio_embeddings.weight"]))
+            self.audio_q8 = self.audio_s = None
+        else:
+            self.audio_dense = None
+            self.audio_q8 = weights["audio_embeddings.weight.q8"]
+            self.audio_s = scale_f16(weights["audio_embeddings.weight.s8"])
         self.projection = p("projection.weight")
         self.c0_head = p("codebook0_head.weight")
         self.audio_head = [p(f"audio_head.{i}") for i in range(N_CB - 1)]
@@ -168,7 +173,10 @@ class OModel:
         self.decoder.alloc(self.B, N_CB)
 
     def embed_audio(self, cb, tok):
-        return K.embed_rows(self.audio_q8, self.audio_s, np.asarray(tok, np.int64) + cb * AUDIO_VOCAB)
+        rows = np.asarray(tok, np.int64) + cb * AUDIO_VOCAB
+        if self.audio_dense is not None:
+            return self.audio_dense[rows]                    # F.embedding (app/engine.py:97)
+        return K.embed_rows(self.audio_q8, self.audio_s, rows)
 
     def guided(self, logits, cfg, topk, temp, noise):
         N, B = self.N, self.B
@@ -221,7 +229,11 @@ class OModel:
 
     def step(self, tok, pos, **kw):
         """_step (app/engine.py:345-349): tok [B, 8] previous frame, pos scalar position."""
-        h = K.embed_sum(self.audio_q8, self.audio_s, tok, AUDIO_VOCAB)
+        if self.audio_dense is not None:
+            rows = np.asarray(tok, np.int64) + np.arange(N_CB)[None] * AUDIO_VOCAB
+            h = K.sum_rows(self.audio_dense[rows])
+        else:
+            h = K.embed_sum(self.audio_q8, self.audio_s, tok, AUDIO_VOCAB)
         last_h = self.backbone.decode(h, np.full(self.B, pos, np.int64), 1)
         return self.frame(last_h, **kw)
 

@@ -8,7 +8,7 @@ import json
 import numpy as np
 import pytest
 
-from helpers import AUDIO_VOCAB, N_CB, rng, tiny_cfgs, to_torch
+from helpers import AUDIO_VOCAB, N_CB, assert_close16, rng, tiny_cfgs, to_torch
 from oracle.numerics import bf16_bits
 from oracle.quant import q8_rows
 
@@ -103,3 +103,65 @@ def test_engine_loads_written_file(dev, converted):
     b._step(tok, pos, None, 1.5, 50, 1.0, forced=forced, logits_out=lb)
     for i in range(N_CB):
         assert torch.equal(la[i], lb[i]), f"head {i}"
+
+
+@pytest.fixture(scope="module")
+def converted_dense_emb(tmp_path_factory):
+    """The same checkpoint written with --keep-emb-bf16 (app/convert_final.py:43, :66)."""
+    import torch
+    from safetensors.torch import save_file
+    from estudiocanciones_amd.convert import convert_file
+    bb, dec = tiny_cfgs()
+    ck, heads = official_checkpoint(bb, dec)
+    d = tmp_path_factory.mktemp("ckpt_emb")
+    save_file({k: torch.from_numpy(v) for k, v in ck.items()}, str(d / "model.safetensors"))
+    out = convert_file(d, d / "mula_int8.safetensors", keep_emb=True)
+    want = oracle_format(ck, heads)
+    for name in ("text_embeddings.weight", "audio_embeddings.weight"):
+        del want[name + ".q8"], want[name + ".s8"]
+        want[name] = bf16_bits(ck[name])
+    return bb, dec, out, want
+
+
+def test_keep_emb_file_matches_oracle(converted_dense_emb):
+    """Embedding tables stay bf16 (bit patterns of the fp32 rounded to nearest even)."""
+    import torch
+    from safetensors import safe_open
+    _, _, path, want = converted_dense_emb
+    with safe_open(str(path), "pt") as f:
+        assert set(f.keys()) == set(want)
+        for k in ("text_embeddings.weight", "audio_embeddings.weight"):
+            got = f.get_tensor(k)
+            assert got.dtype == torch.bfloat16
+            assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), want[k]), k
+
+
+def test_engine_runs_dense_embedding_file(dev, converted_dense_emb):
+    """HeartMuLaLite on a --keep-emb-bf16 file: the backbone's codebook sum, the projection
+    prologue and the prompt's text rows read the dense tables; teacher-forced frames match the
+    oracle's dense-embedding frame (per-kernel bar)."""
+    import torch
+    from estudiocanciones_amd.engine import HeartMuLaLite
+    from oracle.model import OModel
+    bb, dec, path, want = converted_dense_emb
+    gm = HeartMuLaLite(str(path), device=dev, backbone=bb, decoder=dec)
+    assert gm.audio_emb.w is not None and gm.text_emb.w is not None
+    om = OModel(want, bb, dec)
+    om.alloc(2, 24)
+    gm.alloc(2, 24)
+    B = gm.B
+    g = rng(23)
+    tok = g.integers(0, AUDIO_VOCAB, (B, N_CB)).astype(np.int64)
+    for f in range(3):
+        forced = g.integers(0, AUDIO_VOCAB, (B, N_CB)).astype(np.int64)
+        _, olog = om.step(tok, f, forced=forced)
+        glog = []
+        gm._step(torch.from_numpy(tok).to(dev), torch.full((B, 1), f, dtype=torch.long, device=dev),
+                 None, 1.5, 50, 1.0, forced=torch.from_numpy(forced).to(dev), logits_out=glog)
+        for i in range(N_CB):
+            assert_close16(glog[i].float().cpu().numpy(), olog[i], what=f"dense emb frame {f} head {i}")
+        tok = forced
+    text = torch.arange(5, device=dev)
+    rows = gm.text_emb(text).cpu().numpy()
+    from oracle.numerics import bf16_to_f32, f16
+    assert np.array_equal(rows, f16(bf16_to_f32(want["text_embeddings.weight"]))[:5])

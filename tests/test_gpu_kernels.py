@@ -334,3 +334,18 @@ def test_embed_sum_and_gather(dev):
     assert np.array_equal(N(x)[1::2], N(e))
     idx = T(np.array([[0, 5], [AUDIO_VOCAB * 8 - 1, 2]], np.int64), dev)
     assert np.array_equal(N(emb(idx)), OK.embed_rows(q, s, N(idx)))
+
+
+@pytest.mark.parametrize("M,Nn,K,res", [(2048, 3072, 3072, True), (300, 8197, 1024, False),
+                                        (40, 100, 192, True)])
+def test_int8_mm_many_rows_runs_the_mfma_gemm(dev, M, Nn, K, res):
+    """int8_mm with more than 16 rows (the reference's dense fallback, app/kernels.py:46-49) on
+    the row-major [N, K] weights: the MFMA GEMM, dense numerics, partial feature tiles."""
+    from estudiocanciones_amd.kernels import int8_mm
+    x = randn16(90, M, K)
+    w = rng(91).standard_normal((Nn, K), dtype=np.float32) * np.float32(0.02)
+    q, sb = o_q8_rows(w)
+    s = f16(bf16_to_f32(sb))
+    r = randn16(92, M, Nn) if res else None
+    y = int8_mm(T(x, dev), T(q, dev), T(s, dev), T(r, dev) if res else None)
+    assert_close16(N(y), OK.gemv_i8(x, q, s, r), what=f"int8_mm M={M} N={Nn} K={K}")
