@@ -59,6 +59,11 @@ def parse():
                     help="Euler steps of the codec detokenize window leg (0 skips it)")
     ap.add_argument("--prompt", type=int, default=256,
                     help="prompt tokens of the timed prompt pass (0 skips it)")
+    ap.add_argument("--no-isolated", dest="isolated", action="store_false",
+                    help="skip the isolated-kernel sweep (GEMV 3072<->8192 at 1/2/4/8 rows, "
+                         "attention over 512..8192 tokens at batch 1 and 8)")
+    ap.add_argument("--no-ref-decoder", dest="ref_decoder", action="store_false",
+                    help="skip the frame with the reference's own depth decoder")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -265,6 +270,7 @@ def main():
     t_build = time.time()
     w = synthetic_weights(bb, dec, dev, seed=args.seed)
     model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
+    wcpu = None if args.no_cpu else {k: v.cpu() for k, v in w.items()}
     del w
     n = args.takes
     g = torch.Generator(device=dev)
@@ -390,8 +396,15 @@ def main():
         "codec_window": codec,
         "setup_s": round(t_build, 1),
     }
+    if args.isolated:
+        res["isolated"] = measure_isolated(torch, dev)
+    res["drop_in"] = measure_drop_in(torch, E, KK, model, dev, n, args.kv, g)
+    del model
+    torch.cuda.empty_cache()
+    if args.ref_decoder and args.decoder == "1024":
+        res["ref_decoder"] = measure_ref_decoder(torch, E, bb, dev, n, args, g)
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(bb, dec, B, args.kv, args.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(wcpu, bb, dec, n, args.kv, args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 
@@ -478,82 +491,185 @@ def measure_codec(torch, dev, steps, seed):
     }
 
 
-def cpu_baseline(bb, dec, B, kv, budget_s):
-    """The reference's CPU path (numpy float32 restatement, dequantised weights) timed on a
-    bounded sample: one backbone layer step and one decoder layer step at batch B, plus the
-    c0 head and one audio head, repeated within ~budget_s, scaled to one frame
-    (28 backbone layers + 7 passes x decoder layers + 8 heads)."""
-    import numpy as np
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.cpu_path import CpuStack
-    from oracle.quant import q8_rows
-    from oracle.numerics import bf16_bits
-    from estudiocanciones_amd.quant import weight_shapes
+def _rotated_time(torch, launches, reps=10):
+    """Mean milliseconds per launch of ``launches`` (one per rotated buffer set) captured into one
+    hipGraph and replayed ``reps`` times between hipEvents on the capturing stream."""
+    return time_graph(launches, torch, reps=reps)
 
-    one_bb = dict(bb, layers=1)
-    one_dec = dict(dec, layers=1)
-    lin, dense = weight_shapes(one_bb, one_dec)
-    g = np.random.default_rng(0)
-    w = {}
-    for name, (N, K) in lin.items():
-        if name.startswith(("backbone.", "decoder.", "codebook0_head", "audio_head.0")):
-            w[name + ".q8"], w[name + ".s8"] = q8_rows(g.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
-    for name, shp in dense.items():
-        if name.endswith(".scale"):
-            w[name] = bf16_bits(1.0 + 0.02 * g.standard_normal(shp, dtype=np.float32))
-    sb = CpuStack(w, "backbone", one_bb)
-    sd = CpuStack(w, "decoder", one_dec)
-    sb.alloc(B, kv + 16)
-    sd.alloc(B, 8)
-    for blk in sb.blocks:
-        blk.kc[:, :, :kv] = g.standard_normal(blk.kc[:, :, :kv].shape, dtype=np.float32)
-        blk.vc[:, :, :kv] = g.standard_normal(blk.vc[:, :, :kv].shape, dtype=np.float32)
-    from oracle.cpu_path import dequant
-    h0 = dequant(w["codebook0_head.weight.q8"], w["codebook0_head.weight.s8"])
-    h1 = dequant(w["audio_head.0.q8"], w["audio_head.0.s8"])
-    proj = g.standard_normal((dec["dim"], bb["dim"]), dtype=np.float32) * np.float32(0.02)
-    xb = g.standard_normal((B, bb["dim"]), dtype=np.float32)
-    xd = g.standard_normal((B, dec["dim"]), dtype=np.float32)
-    pos_b = np.full(B, kv - 1)
-    pos_d = np.full(B, 1)
-    tm = dict(bb=0.0, dec=0.0, heads=0.0)
-    n = 0
+
+def measure_isolated(torch, dev, min_bytes=768 << 20):
+    """Isolated kernels at the backbone shapes (the C1 sweep).  Each point cycles through enough
+    independent buffer sets (>= 16, and > 768 MB in total) that the 256 MB Infinity Cache cannot
+    serve the repeated reads: GEMV 3072 -> 8192 and 8192 -> 3072 at 1/2/4/8 rows (packed weights
+    with streaming loads, the engine's path, and the drop-in int8_mm on row-major weights), and
+    GQA decode attention 24q / 8kv, head_dim 128, 16 splits + combine over 512 ... 8192 cached
+    tokens at batch 1 and 8 (every row at position L - 1)."""
+    from estudiocanciones_amd import kernels as KK
+    out = {"gemv": [], "attention": []}
+    for N, K in ((8192, 3072), (3072, 8192)):
+        wb = N * K
+        sets = max(16, -(-min_bytes // wb))
+        ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev) for _ in range(sets)]
+        wps = [KK.pack_i8(w) for w in ws]
+        s = (torch.rand(N, device=dev) * 1e-3 + 1e-4).half()
+        for M in (1, 2, 4, 8):
+            x = torch.randn(M, K, device=dev).half()
+            ys = [torch.empty(M, N, device=dev, dtype=torch.float16) for _ in range(sets)]
+            alg = gemv_bytes(M, N, K, False)
+            ms_p = _rotated_time(torch, [lambda w=wp, y=y: KK.gemv_packed(x, w, s, N, K, out=y, stream=True)
+                                         for wp, y in zip(wps, ys)])
+            ms_r = _rotated_time(torch, [lambda w=w: KK.int8_mm(x, w, s) for w in ws])
+            out["gemv"].append({"N": N, "K": K, "M": M, "sets": sets,
+                                "algorithmic_bytes": alg,
+                                "packed_us": round(ms_p * 1e3, 2),
+                                "packed_GBps": round(alg / ms_p / 1e6, 1),
+                                "packed_frac": round(alg / ms_p / 1e6 / HBM_PEAK_GBPS, 4),
+                                "int8_mm_us": round(ms_r * 1e3, 2),
+                                "int8_mm_GBps": round(alg / ms_r / 1e6, 1)})
+        del ws, wps
+        torch.cuda.empty_cache()
+    Hq, Hk, HD, ns = 24, 8, 128, 16
+    for B in (1, 8):
+        for L in (512, 1024, 2048, 4096, 8192):
+            cache_b = 2 * B * Hk * L * HD * 2
+            sets = max(16, -(-min_bytes // cache_b))
+            kcs = [torch.randn(B, Hk, L, HD, device=dev).half() for _ in range(sets)]
+            vcs = [torch.randn(B, Hk, L, HD, device=dev).half() for _ in range(sets)]
+            q = torch.randn(B, Hq * HD, device=dev).half()
+            pos = torch.full((B,), L - 1, dtype=torch.long, device=dev)
+            o = torch.empty_like(q)
+            pm = torch.empty(B * Hq * ns, device=dev)
+            pl = torch.empty_like(pm)
+            pa = torch.empty(B * Hq * ns, HD, device=dev)
+            sc = 1.0 / math.sqrt(HD)
+
+            def one(kc, vc):
+                KK._attn[(B, Hk, ns)](q, kc, vc, pos, o, pm, pl, pa, 1, Hq, Hk, L, sc, HD=HD,
+                                      G=Hq // Hk, NSPLIT=ns)
+                KK._attn_combine[(B * Hq,)](pm, pl, pa, o, HD=HD, NSPLIT=ns)
+            ms = _rotated_time(torch, [lambda kc=kc, vc=vc: one(kc, vc) for kc, vc in zip(kcs, vcs)])
+            alg = attn_bytes(B, Hq, Hk, HD, [L] * B)
+            out["attention"].append({"B": B, "L": L, "sets": sets, "algorithmic_bytes": alg,
+                                     "us": round(ms * 1e3, 2),
+                                     "GBps": round(alg / ms / 1e6, 1),
+                                     "frac": round(alg / ms / 1e6 / HBM_PEAK_GBPS, 4)})
+            del kcs, vcs
+            torch.cuda.empty_cache()
+    return out
+
+
+def measure_drop_in(torch, E, KK, model, dev, n, kv, g):
+    """The kernel-level drop-in path: the backbone step through the entry points named as in
+    app/kernels.py (Stack.decode_reference: int8_mm on the row-major weights, rms, _rope_cache,
+    _attn, _attn_combine, _silu_mul -- the reference's launch sequence), against the engine's
+    fused step, both as one hipGraph at batch 2 n, KV ``kv``; and the reference's unchanged
+    prompt-pass Linear (int8_mm at 2048 rows) on the backbone shapes."""
+    model.alloc(n, kv + 258, cfg_scale=1.5)
+    B = model.B
+    st = model.backbone
+    x = torch.randn(B, st.dim, generator=g, device=dev).half()
+    pos = torch.full((B,), kv - 1, dtype=torch.long, device=dev)
+    ms_ref = time_graph([lambda: st.decode_reference(x, pos, 1)], torch)
+    ms_fused = time_graph([lambda: st.decode(x, pos, 1)], torch)
+    blk = st.blocks[0]
+    xp = torch.randn(2048, st.dim, generator=g, device=dev).half()
+    mm = torch.randn(2048, blk.w2.K, generator=g, device=dev).half()
+    calls = [lambda: KK.int8_mm(xp, blk.qkv.q8, blk.qkv.s8), lambda: KK.int8_mm(xp, blk.o.q8, blk.o.s8),
+             lambda: KK.int8_mm(xp, blk.w13.q8, blk.w13.s8), lambda: KK.int8_mm(mm, blk.w2.q8, blk.w2.s8)]
+    ms_pre = time_graph(calls, torch) * len(calls)
+    fl = 2 * 2048 * sum(l.N * l.K for l in (blk.qkv, blk.o, blk.w13, blk.w2))
+    return {"backbone_step_ms_reference_sequence": round(ms_ref, 4),
+            "backbone_step_ms_fused": round(ms_fused, 4),
+            "workload": f"28-layer backbone step, batch {B}, KV {kv}",
+            "prompt_linear_ms_per_layer_int8_mm_2048_rows": round(ms_pre, 4),
+            "prompt_linear_TFLOPs": round(fl / ms_pre / 1e9, 1)}
+
+
+def measure_ref_decoder(torch, E, bb, dev, n, args, g):
+    """The frame with the reference's own depth decoder (3 layers, 3072 wide, 8q/4kv, head_dim
+    384; app/engine.py:24, :116, :161) at the benchmarked batch and KV length."""
+    from estudiocanciones_amd.quant import synthetic_weights
+    dec = dict(E.DECODER, ffn=8192)
+    w = synthetic_weights(bb, dec, dev, seed=args.seed + 3)
+    model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
+    del w
+    pt = measure_point(torch, E, model, dev, n, args.kv, max(20, args.steps // 2), args.warmup, g)
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": ("frame step: 28-layer 3B backbone + 7 passes of the reference depth "
+                         f"decoder (3 layers, 3072, 8q/4kv, hd384, FFN 8192), batch {2 * n}, "
+                         f"KV {args.kv}, one hipGraph"),
+            "value": round(pt["fps"], 2), "unit": "frames/s", "ms_per_step": round(pt["ms"], 4),
+            "frame_bytes": int(pt["frame_bytes"]),
+            "frame_frac_of_hbm": round(pt["frame_bytes"] * pt["fps"] / 1e9 / HBM_PEAK_GBPS, 4),
+            "gemv_frac": round(pt["g_gbps"] / HBM_PEAK_GBPS, 4)}
+
+
+def cpu_baseline(wcpu, bb, dec, n, kv, budget_s):
+    """The reference's CPU path (oracle/cpu_torch.py: dequantised F.linear, SDPA, the masked
+    decoder and the sampler of app/engine.py with fast = False) on the host cores, with
+    os.cpu_count() threads as the reference sets them (app/studio.py:63-64): medians of >= 5
+    timed repetitions after a warm-up of (a) one 3B layer decode step at B = 2, KV 1024 and (b)
+    whole frames at B = 2 n, KV ``kv``, in bf16 (the reference's CPU dtype, the reported value)
+    and fp16.  ``wcpu`` holds the benchmark's own int8 weights copied to the host."""
+    import statistics
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.cpu_torch import CpuTorchModel, _Stack
+
+    ncpu = os.cpu_count() or 1
+    torch.set_num_threads(ncpu)
     t_start = time.perf_counter()
-    while n < 2 or (time.perf_counter() - t_start < budget_s and n < 5000):
-        t = time.perf_counter()
-        sb.decode(xb, pos_b)
-        tm["bb"] += time.perf_counter() - t
-        t = time.perf_counter()
-        sd.decode(xd, pos_d)
-        tm["dec"] += time.perf_counter() - t
-        t = time.perf_counter()
-        _ = xb @ h0.T
-        _ = xd @ h1.T
-        _ = xb @ proj.T
-        tm["heads"] += time.perf_counter() - t
-        n += 1
-    t_bb, t_dec, t_hp = (tm[k] / n for k in ("bb", "dec", "heads"))
-    # per frame: 28 backbone layers, 7 passes x decoder layers, c0 head + 7 audio heads and
-    # 7 projections (~ 7 x the measured head + projection group)
-    frame_s = 28 * t_bb + 7 * dec["layers"] * t_dec + 7 * t_hp
-    return {
-        "value": round(1.0 / frame_s, 4),
-        "unit": "frames/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"reference CPU path restated in numpy float32 (dequantised weights, exact softmax "
-                   f"attention): 1 backbone layer step (batch {B}, KV {kv}) + 1 decoder layer step + "
-                   f"heads, {n} reps in {time.perf_counter() - t_start:.1f} s, scaled to "
-                   f"28 + 7x{dec['layers']} layers + 8 heads per frame"),
-        "backbone_layer_ms": round(t_bb * 1e3, 2),
-        "decoder_layer_ms": round(t_dec * 1e3, 2),
-        "cpu_model": _cpu_model(),
-    }
+
+    def med(fn, reps, warm=1):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    out = {"unit": "frames/s", "cores": ncpu, "kind": "port", "torch_threads": torch.get_num_threads(),
+           "cpu_model": _cpu_model()}
+    gen = torch.Generator().manual_seed(0)
+    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        # (a) config[0]: one backbone layer step, B = 2, KV 1024 (cache N(0, 1), position 1023)
+        one = dict(bb, layers=1)
+        st = _Stack(wcpu, "backbone", one, dt)
+        st.alloc(2, 1024, dt)
+        for layer in st.layers:
+            layer.kc.normal_(generator=gen)
+            layer.vc.normal_(generator=gen)
+        x = torch.randn(2, 1, bb["dim"], generator=gen).to(dt)
+        pos = torch.full((2, 1), 1023)
+        mask = torch.ones(2, 1, 1, 1024, dtype=torch.bool)
+        with torch.inference_mode():
+            out[f"c0_layer_ms_{tag}"] = round(med(lambda: st(x, pos, 1024, mask), 7) * 1e3, 2)
+        del st
+        # (b) frames of the benchmarked configuration
+        m = CpuTorchModel(wcpu, bb, dec, dtype=dt)
+        m.alloc(n, kv + 258)
+        for st_ in (m.backbone,):
+            for layer in st_.layers:
+                layer.kc[:, :, : kv - 1].normal_(generator=gen)
+                layer.vc[:, :, : kv - 1].normal_(generator=gen)
+        tok = torch.randint(0, 8197, (m.B, 8), generator=gen)
+        reps = 5 if tag == "bf16" else 5
+        f_s = med(lambda: m.step(tok, kv - 1, gen=gen), reps)
+        out[f"frame_ms_{tag}"] = round(f_s * 1e3, 1)
+        out[f"frames_per_s_{tag}"] = round(1.0 / f_s, 3)
+        del m
+        if time.perf_counter() - t_start > budget_s * 4:
+            break
+    out["value"] = out["frames_per_s_bf16"]
+    out["sample"] = (f"reference CPU path restated on torch (dequantised F.linear, SDPA, masked "
+                     f"decoder, sampler; oracle/cpu_torch.py) on {ncpu} host threads: whole frames "
+                     f"at batch {2 * n}, KV {kv}, median of 5 after one warm-up, bf16 (value) and "
+                     f"fp16; plus one 3B layer step at batch 2, KV 1024, median of 7")
+    out["wall_s"] = round(time.perf_counter() - t_start, 1)
+    return out
 
 
 def _cpu_model():

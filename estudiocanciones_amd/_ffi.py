@@ -68,6 +68,8 @@ SIGNATURES = {
                             c_int, _P],
     "ecd_gemm_f16p_conv": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
                            c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int, _P],
+    "ecd_gemm_f16p_conv_tuned": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
+                                 c_int, c_int, c_int, c_int, _P, c_int, c_int, c_int, c_int, _P],
     "ecd_gemm_f16p_tuned": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int,
                             c_int, c_int, c_int, _P],
     "ecd_packed_bytes": [c_int, c_int],

@@ -449,7 +449,8 @@ def detokenize_latents(emb: CodeEmbedding, est: LlamaTransformer, codes: torch.T
     [1, 25 duration, latent_dim] of every overlapping window, each later window continuing the
     previous one's last frames in context.  ``randn(shape)`` draws each window's initial sample
     (the only draw that reaches the output: the reference's other draws are masked to zero).
-    The waveform decoder (ScalarModel) is not part of this build."""
+    The waveform decoder that turns these latents into audio is ``ScalarDecoder`` (see
+    ``detokenize``)."""
     dev = est.dev
     if randn is None:
         randn = lambda shape: torch.randn(*shape, device=dev)

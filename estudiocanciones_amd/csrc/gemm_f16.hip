@@ -119,8 +119,8 @@ __device__ __forceinline__ long seq_row(long m, int T, int pad) {
 template <int EPI, int WN, int WM, int FT, int RT, int NS, bool PL>
 __global__ __launch_bounds__(256, (FT * RT <= 16 ? 2 : 1)) void gemm_f16w_kernel(
     const f16* __restrict__ x, long ldx, const f16* __restrict__ wp,
-    const float* __restrict__ bias, float alpha, const f16* __restrict__ res, long ldr,
-    f16* __restrict__ y, long ldy, int M, int N, int K, int nfb, int nmb, RowMap rm,
+    const float* __restrict__ bias, float alpha, const f16* res, long ldr,
+    f16* y, long ldy, int M, int N, int K, int nfb, int nmb, RowMap rm,
     RopeOut ro) {
   static_assert(WN * WM == 4, "four waves");
   constexpr int BN = 16 * WN * FT;      // features per block
@@ -526,12 +526,13 @@ int ecd_gemm_f16p_rope(const void* x, long ldx, const void* wp, const float* bia
                               nullptr, 0, M, (int)N, K, rm, ro, (hipStream_t)stream);
 }
 
-int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
-                       const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
-                       int xpad, int ypad, const int* offsets, int k, int rep, int epi,
-                       void* stream) {
+int ecd_gemm_f16p_conv_tuned(const void* x, long ldx, const void* wp, const float* bias,
+                             float alpha, const void* res, long ldr, void* y, long ldy, int M,
+                             int N, int K, int T, int xpad, int ypad, const int* offsets, int k,
+                             int rep, int epi, int cfg, void* stream) {
   if (!x || !wp || !y || M <= 0 || N <= 0 || K <= 0 || (K % 64) || (ldx % 8) || !al16(x) ||
-      !al16(wp) || epi < 0 || epi > 2 || epi == F16_SILU || T <= 0 || M % T || k < 0 || k > 8 ||
+      !al16(wp) || epi < 0 || epi > 2 || epi == F16_SILU || cfg < 0 || cfg > 16 || T <= 0 ||
+      M % T || k < 0 || k > 8 ||
       (k && (!offsets || K % (64 * k) || xpad < 0)) || (!k && ldx < K) || ldy < N ||
       (res && ldr < N) || ypad < -1 || (rep != 1 && rep != 2) || (rep == 2 && (!k || T % 2)))
     return ECD_EINVAL;
@@ -549,8 +550,16 @@ int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bia
   const long tin = rep == 2 ? T / 2 : T;  // source rows per sequence
   const long xrows = k ? (long)(M / T) * (tin + xpad) + xpad : M;  // + the rows after the last
   if (!x_offsets_fit((int)min(xrows, 0x7FFFFFFFL), ldx)) return ECD_ENOTSUP;
-  return launch_epi(epi, 0, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
+  return launch_epi(epi, cfg, (const f16*)x, ldx, (const f16*)wp, bias, alpha, (const f16*)res,
                     ldr, (f16*)y, ldy, M, N, K, rm, (hipStream_t)stream);
+}
+
+int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bias, float alpha,
+                       const void* res, long ldr, void* y, long ldy, int M, int N, int K, int T,
+                       int xpad, int ypad, const int* offsets, int k, int rep, int epi,
+                       void* stream) {
+  return ecd_gemm_f16p_conv_tuned(x, ldx, wp, bias, alpha, res, ldr, y, ldy, M, N, K, T, xpad,
+                                  ypad, offsets, k, rep, epi, 0, stream);
 }
 
 int ecd_gemm_f16p(const void* x, long ldx, const void* wp, const float* bias, float alpha,

@@ -256,6 +256,14 @@ int ecd_gemm_f16p_conv(const void* x, long ldx, const void* wp, const float* bia
                        int xpad, int ypad, const int* offsets, int k, int rep, int epi,
                        void* stream);
 
+/* ecd_gemm_f16p_conv with an explicit block tile (cfg as in ecd_gemm_f16p_tuned; 0 = the
+ * library's choice).  Replaces nothing in the reference: the launch-shape knob of the waveform
+ * decoder's convolutions, for sweeps and for the tests that hold every tile to the same bits. */
+int ecd_gemm_f16p_conv_tuned(const void* x, long ldx, const void* wp, const float* bias,
+                             float alpha, const void* res, long ldr, void* y, long ldy, int M,
+                             int N, int K, int T, int xpad, int ypad, const int* offsets, int k,
+                             int rep, int epi, int cfg, void* stream);
+
 /* ecd_gemm_f16p (epi 0), ecd_gemm_f16p_silu (epi 1, N = 2F, bias/res NULL, alpha 1) or
  * ecd_gemm_f16p_prelu (epi 2, alpha = the slope) with an
  * explicit block tile (cfg 1..16: 128x128, 256x128, 128x256, 128x64, 64x128, 64x256, 64x64 or 128x96 features x rows,

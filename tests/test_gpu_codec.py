@@ -498,6 +498,13 @@ def test_gemm_f16_conv_implicit_taps(dev, offs, C, N, ypad, prelu, rep):
     _ffi.call("ecd_gemm_f16p_conv", xpt.data_ptr(), C, wp.data_ptr(), bt.data_ptr(), 0.25,
               y_imp.data_ptr(), N, y_imp.data_ptr(), N, B * T, N, K, T, P, ypad, off, k, rep, epi, st)
     _exact(N_(y_imp), N_(y_ref), f"implicit taps {offs} C={C} N={N} ypad={ypad} rep={rep}")
+    # every block tile (sizes, LDS stages, pipelined or not) reads the implicit taps identically
+    for cfg in range(1, 17):
+        y_cfg = D_(r, dev)
+        _ffi.call("ecd_gemm_f16p_conv_tuned", xpt.data_ptr(), C, wp.data_ptr(), bt.data_ptr(), 0.25,
+                  y_cfg.data_ptr(), N, y_cfg.data_ptr(), N, B * T, N, K, T, P, ypad, off, k, rep,
+                  epi, cfg, st)
+        _exact(N_(y_cfg), N_(y_ref), f"implicit taps {offs} rep {rep}, tile cfg {cfg}")
 
 
 def test_codec_weight_norm_and_latent_split(dev):
@@ -539,18 +546,36 @@ def f32_(a):
     return np.asarray(a, np.float32)
 
 
-@pytest.mark.parametrize("T", [12, 37])
-def test_codec_scalar_decoder(dev, T):
+def test_codec_scalar_decoder_real_widths(dev):
+    """ScalarModel.decode at the real configuration (latent 256 split into 2 groups of 128,
+    channels 2048 -> 1024 -> ... -> 64, upsampling 5, 4, 4, 4, 3, post 2x: x1920) over a short
+    window of 6 latent frames, against the oracle."""
+    import torch
+    from estudiocanciones_amd.codec import ScalarDecoder
+    cfg = dict(latent_hidden_dim=128, init_channel=64, upsample_factors=(5, 4, 4, 4, 3))
+    p = OC.random_decoder_weights(cfg, seed=850)
+    dec = ScalarDecoder({k: torch.from_numpy(np.asarray(v)) for k, v in p.items()}, device=dev)
+    T = 6
+    lat = randn16(851, 1, T, 256)
+    got = dec.decode(D_(lat, dev))
+    want = OC.scalar_decode(p, cfg, lat)
+    assert got.shape == want.shape == (2, T * 1920, 1)
+    _close_model(N_(got), want, "scalar decoder, real widths")
+
+
+@pytest.mark.parametrize("T,rows_bytes", [(12, 64 * 1024), (37, 64 * 1024), (300, 4096)])
+def test_codec_scalar_decoder(dev, T, rows_bytes):
     """ScalarModel.decode at a small configuration (latent 64 x 2 channel groups, channels
-    256 -> 128 -> 64, upsampling 2 and 3, post 2x) against the oracle, with the tap-column GEMMs
-    split into several row chunks."""
+    256 -> 128 -> 64, upsampling 2 and 3, post 2x) against the oracle.  The first conv's tap
+    columns are cut into row chunks of at least 256 rows; at T = 300 with a small chunk budget
+    each sequence's 300 rows run as two chunks, so a chunk starting past row 0 runs too."""
     import torch
     from estudiocanciones_amd.codec import ScalarDecoder
     p = OC.random_decoder_weights(DEC, seed=830)
     dec = ScalarDecoder({k: torch.from_numpy(np.asarray(v)) for k, v in p.items()},
                         latent_hidden_dim=64, init_channel=64, upsample_factors=(2, 3),
                         upsample_kernel_sizes=(4, 6), device=dev)
-    dec.ROWS_BYTES = 64 * 1024       # force several chunks per conv
+    dec.ROWS_BYTES = rows_bytes
     lat = randn16(831 + T, 1, T, 128)
     got = dec.decode(D_(lat, dev))
     want = OC.scalar_decode(p, DEC, lat)

@@ -157,3 +157,42 @@ def test_frame_loop_trim_boundaries():
     assert [o.shape[1] for o in out] == [1, 25, 26, n + 1] and ran == n
     out, ran = frame_loop_trim(frames[:, :3], n)
     assert [o.shape[1] for o in out] == [1, 25, 26] and ran == 50
+
+
+def test_torch_cpu_path_agrees_with_numpy_slow_path():
+    """The torch restatement of the reference's CPU path (the bench's CPU baseline), run in
+    float32, agrees with the numpy slow-path restatement under teacher forcing."""
+    torch = pytest.importorskip("torch")
+    from oracle.cpu_torch import CpuTorchModel
+    from helpers import to_torch
+    bb, dec = tiny_cfgs()
+    w = model_weights_np(bb, dec, seed=11)
+    cm = CpuModel(w, bb, dec)
+    tm = CpuTorchModel(to_torch(w, "cpu"), bb, dec, dtype=torch.float32)
+    tm.alloc(2, 24)
+    cm.alloc(tm.B, 24)
+    g = np.random.default_rng(5)
+    tok = g.integers(0, V, (tm.B, N_CB))
+    for f in range(3):
+        forced = g.integers(0, V, (tm.B, N_CB))
+        want = cm.step(tok, f, forced)
+        got = []
+        tm.step(torch.from_numpy(tok), f, forced=torch.from_numpy(forced), logits=got)
+        for i in range(N_CB):
+            np.testing.assert_allclose(got[i].numpy(), want[i], atol=2e-4, rtol=2e-4)
+        tok = forced
+
+
+def test_torch_cpu_path_samples_in_range():
+    """Sampling on the torch CPU path (bf16): tokens inside the vocabulary, cond and uncond rows
+    of a take equal."""
+    torch = pytest.importorskip("torch")
+    from oracle.cpu_torch import CpuTorchModel
+    from helpers import to_torch
+    bb, dec = tiny_cfgs()
+    tm = CpuTorchModel(to_torch(model_weights_np(bb, dec, seed=11), "cpu"), bb, dec)
+    tm.alloc(2, 24)
+    gen = torch.Generator().manual_seed(0)
+    t = tm.step(torch.zeros(tm.B, N_CB, dtype=torch.long), 0, gen=gen)
+    assert t.shape == (4, N_CB) and int(t.min()) >= 0 and int(t.max()) < V
+    assert torch.equal(t[:2], t[2:])
