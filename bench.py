@@ -64,6 +64,9 @@ def parse():
                          "attention over 512..8192 tokens at batch 1 and 8)")
     ap.add_argument("--no-ref-decoder", dest="ref_decoder", action="store_false",
                     help="skip the frame with the reference's own depth decoder")
+    ap.add_argument("--no-tail", dest="tail", action="store_false",
+                    help="run each layer's O / MLP / next q|k|v as separate GEMV launches instead "
+                         "of one layer-tail launch")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -214,6 +217,15 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
         if name == "ecd_rms_w13_silu":
             M, F, K = a[7], a[8], a[9]
             return 2 * F * K + 4 * F + 2 * M * K + 2 * K + 2 * M * F
+        if name == "ecd_layer_tail":
+            # O (+res), rms -> w1|w3 -> SiLU, w2 (+res), and the next layer's rms -> q|k|v
+            M, D, F, Hq, Hk, HD = a[22], a[23], a[24], a[26], a[27], a[29]
+            b = (D * D + 2 * D + 6 * M * D) + (2 * F * D + 4 * F + 2 * M * D + 2 * D + 2 * M * F) \
+                + (D * F + 2 * D + 2 * M * F + 4 * M * D)
+            if a[10]:
+                Nq = (Hq + 2 * Hk) * HD
+                b += Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD
+            return b
         if name == "ecd_embed_gemv_i8p":
             M, N, K = a[12], a[13], a[14]
             ev = 2 * (M // 2) * K if a[7] else 0
@@ -270,6 +282,7 @@ def main():
     t_build = time.time()
     w = synthetic_weights(bb, dec, dev, seed=args.seed)
     model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
+    model.backbone.use_tail = model.decoder.use_tail = args.tail
     wcpu = None if args.no_cpu else {k: v.cpu() for k, v in w.items()}
     del w
     n = args.takes
@@ -592,6 +605,7 @@ def measure_ref_decoder(torch, E, bb, dev, n, args, g):
     dec = dict(E.DECODER, ffn=8192)
     w = synthetic_weights(bb, dec, dev, seed=args.seed + 3)
     model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
+    model.backbone.use_tail = model.decoder.use_tail = args.tail
     del w
     pt = measure_point(torch, E, model, dev, n, args.kv, max(20, args.steps // 2), args.warmup, g)
     del model

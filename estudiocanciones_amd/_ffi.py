@@ -83,6 +83,10 @@ SIGNATURES = {
     "ecd_rms_w13_silu": [_P, c_long, _P, c_float, _P, _P, _P, c_int, c_int, c_int, c_int, _P],
     "ecd_embed_gemv_i8p": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, _P, _P, c_long, c_int,
                            c_int, c_int, c_int, _P],
+    "ecd_layer_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                       _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
+                       c_int, _P],
+    "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int],
 }
 
 _lib = None

@@ -1,0 +1,691 @@
+// Layer tail of a decode stack as one persistent launch per layer (gfx950).
+//
+// One launch computes, for a few rows (M <= 8), what the reference runs as five launches plus
+// the next layer's first one (app/engine.py:189-192, 206-209; kernels app/kernels.py:11-107,
+// 170-180):
+//
+//   phase O    x1   = x + fp16(s_o * (W_o o))                      o-projection + residual
+//   phase W13  mm   = fp16(silu(a)) * b,  a | b = fp16(s * (W1|W3 rms(x1, n2)))
+//   phase W2   xout = x1 + fp16(s_2 * (W2 mm))                      down-projection + residual
+//   phase QKV  q|k|v = fp16(s_q * (Wqkv rms(xout, n1'))), RoPE of q and k, q -> q_out,
+//              k / v -> cache slot pos (the next layer's first step; skipped for the last layer)
+//
+// with the numerics of the per-op kernels (int8 codes x fp16 in fp32, fp16(acc * s), fp16
+// residual add, the RMSNorm rounding points of app/kernels.py:58-67).
+//
+// Why one launch: at these row counts every GEMV is a weight stream of 2-50 MB, and a graph
+// boundary between dependent launches costs ~3.5 us (dispatch gap, first-byte latency, store
+// drain), more than the streaming time of the smaller matrices.  Here the grid is one
+// workgroup per CU for the whole tail, and the phase boundaries are gates inside the kernel.
+// A gate costs about as much as a launch boundary, but the weight stream does not stop at it:
+// each compute wave holds its share of the next phase's weights in registers, loaded while
+// the current phase computes and while the gate resolves, so HBM stays busy across phases.
+//
+// Workgroup: 8 compute waves + 1 loader wave.
+//   * compute wave w owns K-chunks [w * C, (w + 1) * C) of every tile the workgroup has in a
+//     phase (C = K / 512), keeps those weights in registers (packed lane-ordered 1 KB chunks,
+//     int8 -> fp16 in registers, v_mfma_f32_16x16x32_f16 with the weights as A), reads the x
+//     fragments from LDS and leaves its partial sums in LDS.  It never stores to global memory,
+//     so waiting for its weights never waits for a store.
+//   * after a gate has opened, each compute wave copies its own K-slice of the phase's
+//     activation rows into LDS (global_load_lds); those copies queue behind the wave's weight
+//     loads, which the phase needs next anyway.
+//   * the loader wave polls the gates, adds up the eight partial sums in wave order, runs the
+//     epilogue and stores the outputs.  Its queue holds only epilogue operands and stores, so
+//     its wait for the stores before arriving at a gate never waits for a weight load.
+// Tiles per workgroup (256 workgroups, 3B shapes): O 1 tile on 192 workgroups, W13 4 tiles,
+// W2 1 tile (K = 8192) on 192 workgroups, QKV 1 or 2 tiles; the workgroups without an O or W2
+// tile take the second QKV tiles, so every CU streams 336-416 KB per layer.
+//
+// Cross-workgroup visibility (CDNA3/4: one L2 per XCD, not coherent across XCDs).  Outputs
+// read by other workgroups in the same launch (x1, mm, xout) are written with agent-scope
+// relaxed atomic stores (global_store ... sc1: written through to memory); after its stores
+// are acknowledged (s_waitcnt vmcnt(0)) the loader arrives at the gate with an atomic add.
+// The gate is two-level: the last of the 32 workgroups of a group (blockIdx % 8) adds to the
+// gate's global count, and the last group writes the go flags, which each workgroup polls
+// with agent-scope loads.  No workgroup reads x1 / mm / xout before its gate has opened, and
+// those lines are not in any L2 from earlier in the launch, so plain loads after the gate
+// fetch them from memory.  The gate counters only ever grow, in step with the go value, so
+// one 4 KB sync region serves every launch (each launch reads the go value at start).
+// All workgroups are resident at once (grid = CU count, one workgroup per CU by LDS use);
+// every wait on a gate is bounded, and a timeout sets *err and lets the kernel finish.
+#include "common.h"
+
+namespace ecd {
+namespace tail {
+
+constexpr int CW = 8;                // compute waves per workgroup
+constexpr int NTHR = (CW + 1) * 64;  // plus the loader wave
+constexpr int MR = 8;                // rows held in the x tile (M <= MR)
+constexpr int CHB = 128 * MR;        // LDS bytes per 64-column chunk of the x tile
+
+struct Args {
+  const f16* o;    // [M, D] attention output of this layer
+  const f16* xin;  // [M, D] layer input (residual of the O projection)
+  const int8_t* wo;
+  const f16* so;
+  const f16* n2;
+  const int8_t* w13;  // row-interleaved w1 | w3
+  const f16* s13;
+  const int8_t* w2;
+  const f16* s2;
+  // next layer's q|k|v step (wq == nullptr: last layer)
+  const f16* n1;
+  const int8_t* wq;
+  const f16* sq;
+  const float* rope;
+  const int64_t* pos;
+  f16* q;
+  f16* kc;
+  f16* vc;
+  int S, Hq, Hk, L, HD;
+  // outputs
+  f16* x1;    // [M, D]
+  f16* mm;    // [M, F]
+  f16* xout;  // [M, D]
+  uint32_t* sync;  // 4 KB gate region, zero before the first launch
+  uint32_t* err;   // set to 1 when a gate wait times out
+  int M, D, F;
+  float eps;
+  int spin_max;
+};
+
+__device__ __forceinline__ void bar() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// LDS writes of this wave complete (vmcnt and expcnt not waited for)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+__device__ __forceinline__ void st_sc1_u64(f16* p, f16x4 v) {
+  __hip_atomic_store((uint64_t*)p, __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_sc1_u32(f16* p, f16x2 v) {
+  __hip_atomic_store((uint32_t*)p, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
+  return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_agent(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Gate words: [0] arrivals of group leaders, [64 (1 + g)] arrivals of group g's workgroups,
+// [64 (1 + g) + 32] go flag of group g (the eight go flags always hold the same value).  The
+// counters are never reset: every use of a gate adds exactly `per` to each group count and 8 to
+// the leader count and moves the go value by one, so the last arrivers are recognised from the
+// go value the workgroup holds (all modulo 2^32; `per` divides 2^32).  Called by one lane after
+// this workgroup's output stores have been acknowledged.
+__device__ __forceinline__ void gate_arrive(uint32_t* sync, int grp, uint32_t per, uint32_t go) {
+  if (add_agent(sync + 64 * (1 + grp)) == (go + 1u) * per - 1u) {
+    if (add_agent(sync) == (go + 1u) * 8u - 1u) {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) store_agent(sync + 64 * (1 + g) + 32, go + 1u);
+    }
+  }
+}
+
+__device__ __forceinline__ bool gate_wait(const uint32_t* sync, int grp, uint32_t go,
+                                          int spin_max) {
+  const uint32_t* f = sync + 64 * (1 + grp) + 32;
+  for (int it = 0; ld_sc1(f) == go; ++it) {
+    if (it >= spin_max) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
+
+// LDS DMA as lds_dma16, with agent scope (sc1): the read bypasses the L2, whose miss queue the
+// weight stream keeps full, and sees the other workgroups' agent-scope stores.
+__device__ __forceinline__ void lds_dma16_sc1(const void* base, uint32_t off, void* dst) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2 sc1\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
+}
+
+// Activation rows [M, K] (row stride ld halfs) -> LDS x tile: chunk c (columns 64c .. 64c + 63)
+// occupies CHB bytes as [grp 4][row MR][16 halfs], grp = the 16-column group, i.e. exactly the
+// B fragments of the two MFMAs of the chunk.  Each compute wave copies its own chunks
+// [c0, c0 + C), one DMA instruction per chunk; lane l moves 16 bytes: grp = l >> 4,
+// row = (l >> 1) & 7, half h = l & 1.  Rows past M repeat row M - 1 (their products land in
+// output rows that are never stored).
+template <int C>
+__device__ __forceinline__ void dma_rows(const f16* x, long ld, int M, int c0, unsigned char* xs,
+                                         int lane) {
+  const int grp = lane >> 4, row = (lane >> 1) & 7, h = lane & 1;
+  const int rs = row < M ? row : M - 1;
+  const uint32_t off0 = (uint32_t)(((long)rs * ld + 64 * c0 + 16 * grp + 8 * h) * 2);
+#pragma unroll
+  for (int u = 0; u < C; ++u) {
+    lds_dma16_sc1(x, off0 + (uint32_t)u * 128u, xs + (c0 + u) * CHB);
+    if ((u & 15) == 15) wait_vm<32>();  // at most ~48 DMA instructions in flight
+  }
+}
+
+// The norm-weight columns of chunks [c0, c0 + C) -> LDS at the same offsets (C * 128 bytes:
+// lanes past 8 C idle, so no lane reads past the vector)
+template <int C>
+__device__ __forceinline__ void dma_nw(const f16* v, int c0, unsigned char* dst, int lane) {
+  static_assert(C * 8 <= 64, "one DMA instruction per wave");
+  if (lane < C * 8) lds_dma16_sc1(v + 64 * c0, (uint32_t)(16 * lane), dst + 128 * c0);
+}
+
+// B fragments of chunk c for this lane (row lane & 15; zero for rows >= MR)
+__device__ __forceinline__ void xfrag(const unsigned char* xs, int c, int lane, f16x8& fa,
+                                      f16x8& fb) {
+  const int row = lane & 15, grp = lane >> 4;
+  if (row < MR) {
+    const unsigned char* p = xs + c * CHB + (grp * MR + row) * 32;
+    fa = *(const f16x8*)p;
+    fb = *(const f16x8*)(p + 16);
+  } else {
+    fa = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    fb = fa;
+  }
+}
+
+// RMSNorm of the fragments: fp16(fp16(x * inv) * nw)
+__device__ __forceinline__ void rms_frag(f16x8& fa, f16x8& fb, const unsigned char* nws, int c,
+                                         int lane, float inv) {
+  const f16* nw = (const f16*)nws + 64 * c + 16 * (lane >> 4);
+  const f16x8 na = *(const f16x8*)nw;
+  const f16x8 nb = *(const f16x8*)(nw + 8);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    fa[e] = (f16)((float)fa[e] * inv) * na[e];
+    fb[e] = (f16)((float)fb[e] * inv) * nb[e];
+  }
+}
+
+// Sum of squares of this wave's chunks [c0, c0 + C) per row, reduced over the wave's four
+// column groups; the per-wave sums go to ss[wave][row] in LDS.
+template <int C>
+__device__ __forceinline__ void rms_partial(const unsigned char* xs, int c0, int lane, int wv,
+                                            float* ss) {
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < C; ++u) {
+    f16x8 fa, fb;
+    xfrag(xs, c0 + u, lane, fa, fb);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const f16x2 pa = (f16x2){fa[e], fa[e + 1]};
+      const f16x2 pb = (f16x2){fb[e], fb[e + 1]};
+      acc = __builtin_amdgcn_fdot2(pa, pa, acc, false);
+      acc = __builtin_amdgcn_fdot2(pb, pb, acc, false);
+    }
+  }
+  acc += __shfl_xor(acc, 16, 64);
+  acc += __shfl_xor(acc, 32, 64);
+  if (lane < MR) ss[wv * 16 + lane] = acc;
+}
+
+__device__ __forceinline__ float rms_inv(const float* ss, int lane, int K, float eps) {
+  const int row = lane & 15;
+  if (row >= MR) return 0.f;
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < CW; ++w) t += ss[w * 16 + row];
+  return 1.0f / sqrtf(t / (float)K + eps);
+}
+
+// 16 int8 codes -> two f16x8 holding q + 1152 exactly: the magic-number conversion of
+// i8x16_to_f16 (q ^ 0x80 under the exponent byte 0x64 is the half 1024 + q + 128) without its
+// final subtraction.  The GEMV then forms sum_k (q_k + 1152) x_k and removes 1152 sum_k x_k
+// once per output.
+__device__ __forceinline__ void i8x16_to_f16_biased(const u32x4& v, f16x8& lo, f16x8& hi) {
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = v[i] ^ 0x80808080u;
+    h[2 * i] = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);      // bytes u0, u1
+    h[2 * i + 1] = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, u3
+  }
+  lo = __builtin_bit_cast(f16x8, (u32x4){h[0], h[1], h[2], h[3]});
+  hi = __builtin_bit_cast(f16x8, (u32x4){h[4], h[5], h[6], h[7]});
+}
+
+// acc[t] += W_t x over chunks [c0, c0 + C) of this wave.  The weights enter the MFMAs as
+// q + 1152 (two v_perm per four codes, no subtraction); the bias is removed at the end with
+// 1152 sum_k x[m][k], formed by one extra MFMA per half-chunk whose A operand is the constant
+// 1152 (its result is the same for every tile: lane l holds the sum of column l & 15).  Every
+// product is exact in fp32; only the accumulation order of the fp32 sums differs from the
+// unbiased form.
+template <int NT, int C>
+__device__ __forceinline__ void mfma_chunks(f32x4 (&acc)[NT], const u32x4 (&w)[NT][C],
+                                            const unsigned char* xs, const unsigned char* nws,
+                                            int c0, int lane, float inv, bool rms) {
+  const f16 kb = (f16)1152.0f;
+  const f16x8 bias = (f16x8){kb, kb, kb, kb, kb, kb, kb, kb};
+  f32x4 corr = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < C; ++u) {
+    f16x8 fa, fb;
+    xfrag(xs, c0 + u, lane, fa, fb);
+    if (rms) rms_frag(fa, fb, nws, c0 + u, lane, inv);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fa, corr, 0, 0, 0);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fb, corr, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f16x8 wa, wb;
+      i8x16_to_f16_biased(w[t][u], wa, wb);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, fb, acc[t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] -= corr;
+}
+
+template <bool NTL>
+__device__ __forceinline__ u32x4 ldw(const int8_t* p) {
+  if (NTL) return __builtin_nontemporal_load((const u32x4*)p);
+  return *(const u32x4*)p;
+}
+
+template <int NT, int C, bool NTL>
+__device__ __forceinline__ void load_w(u32x4 (&w)[NT][C], const int8_t* wp, const int (&tiles)[NT],
+                                       int nch, int c0, int lane) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int u = 0; u < C; ++u)
+      w[t][u] = ldw<NTL>(wp + ((long)tiles[t] * nch + c0 + u) * 1024 + 16 * lane);
+}
+
+template <int NT>
+__device__ __forceinline__ void put_partials(unsigned char* ps, const f32x4 (&acc)[NT], int wv,
+                                             int lane) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) *(f32x4*)(ps + ((wv * NT + t) * 64 + lane) * 16) = acc[t];
+}
+
+// sum of the eight waves' partials of tile t (wave order: the same sum in every launch); all
+// eight LDS reads are issued before the first add
+template <int NT>
+__device__ __forceinline__ f32x4 sum_partials(const unsigned char* ps, int t, int lane) {
+  f32x4 p[CW];
+#pragma unroll
+  for (int w = 0; w < CW; ++w) p[w] = *(const f32x4*)(ps + ((w * NT + t) * 64 + lane) * 16);
+  f32x4 s = p[0];
+#pragma unroll
+  for (int w = 1; w < CW; ++w) s += p[w];
+  return s;
+}
+
+__device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
+  f16x4 y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = (f16)(acc[r] * (float)s[r]);
+  return y;
+}
+
+// LDS map (bytes), per phase, for K = D columns: x tile [0, XD), norm weights [XD, XD + 2D),
+// row sums [XD + 2D, + 512), partials after that; for the W2 phase (K = F): x tile [0, XF),
+// partials [XF, XF + 8 KB).  A phase's partials never overlap its own x tile or norm weights
+// (some waves still read those while others store partials); the next phase's x tile may
+// overlap them (the loader has read the partials before it releases the next phase).
+//
+// Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
+// start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
+// MFMAs, so the weight stream does not wait for the gates.
+template <int CD, int CF, int NT13, bool NTL>
+__global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  // the 1024-wide shapes issue all of W2 at the start; the 3072-wide ones after the W13 MFMAs
+  // (their W13 share alone takes 96 registers)
+  constexpr bool W2_EARLY = CD < 6;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int NB = gridDim.x, b = blockIdx.x;
+  const int D = a.D, F = a.F, M = a.M;
+  const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
+  const bool has_next = a.wq != nullptr;
+
+  // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
+  const int TO = D >> 4;
+  const int tO = b - (NB - TO);    // >= 0: one O tile
+  const int t2 = b < TO ? b : -1;  // one W2 tile (W2 has D / 16 tiles too)
+  const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
+  const int xtra = TQ - NB;
+  const int tq0 = b < TQ ? b : -1;
+  const int tq1 = (xtra > 0 && b >= NB - xtra) ? NB + (b - (NB - xtra)) : -1;
+
+  const int XD = nchD * CHB;
+  unsigned char* xs = smem;
+  unsigned char* nws = smem + XD;
+  float* ss = (float*)(smem + XD + 2 * D);
+  unsigned char* psD = smem + XD + 2 * D + 512;  // partials of the K = D phases
+  unsigned char* psF = smem + nchF * CHB;        // partials of the W2 phase
+
+  if (wv < CW) {
+    // ------------------------------------------------------------------ compute waves
+    const int c0D = wv * CD, c0F = wv * CF;
+    // this wave's slice of the attention output first (the inputs of this launch are final)
+    dma_rows<CD>(a.o, D, M, c0D, xs, lane);
+    u32x4 wo[1][CD];
+    u32x4 w13[NT13][CD];
+    const int to_t[1] = {tO < 0 ? 0 : tO};
+    int t13[NT13];
+#pragma unroll
+    for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
+    if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
+    load_w<NT13, CD, NTL>(w13, a.w13, t13, nchD, c0D, lane);
+    u32x4 w2[1][CF];
+    const int t2_t[1] = {t2 < 0 ? 0 : t2};
+    if (W2_EARLY && t2 >= 0) load_w<1, CF, NTL>(w2, a.w2, t2_t, nchF, c0F, lane);
+
+    // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
+    // wait until this wave's o slice has landed (the loads issued after it: W_O, W13, early W2)
+    {
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      if (tO >= 0) {
+        if (W2_EARLY && t2 >= 0) wait_vm<CD + NT13 * CD + (W2_EARLY ? CF : 0)>();
+        else wait_vm<CD + NT13 * CD>();
+        mfma_chunks<1, CD>(acc, wo, xs, nws, c0D, lane, 0.f, false);
+      }
+      put_partials<1>(psD, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(O)
+
+    // phase W13 (x = rms(x1, n2))
+    bar();  // X(W13): x1 is complete
+    dma_rows<CD>(a.x1, D, M, c0D, xs, lane);
+    dma_nw<CD>(a.n2, c0D, nws, lane);
+    wait_vm0();
+    rms_partial<CD>(xs, c0D, lane, wv, ss);
+    wait_lgkm0();
+    bar();  // S(W13)
+    u32x4 wq[2][CD];
+    const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
+    {
+      const float inv = rms_inv(ss, lane, D, a.eps);
+      f32x4 acc[NT13];
+#pragma unroll
+      for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      mfma_chunks<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true);
+      // the W13 registers are dead past this point: the loads below reuse them
+#pragma unroll
+      for (int t = 0; t < NT13; ++t) asm volatile("" : "+v"(acc[t])::"memory");
+      if (!W2_EARLY && t2 >= 0) load_w<1, CF, NTL>(w2, a.w2, t2_t, nchF, c0F, lane);
+      if (tq1 >= 0) load_w<2, CD, NTL>(wq, a.wq, tq_t, nchD, c0D, lane);
+      else if (tq0 >= 0)
+        load_w<1, CD, NTL>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t, nchD, c0D, lane);
+      put_partials<NT13>(psD, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(W13)
+
+    // phase W2 (x = mm)
+    bar();  // X(W2): mm is complete
+    dma_rows<CF>(a.mm, F, M, c0F, xs, lane);
+    wait_vm0();
+    {
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      if (t2 >= 0) mfma_chunks<1, CF>(acc, w2, xs, nws, c0F, lane, 0.f, false);
+      put_partials<1>(psF, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(W2)
+
+    if (has_next) {
+      // phase QKV (x = rms(xout, n1'))
+      bar();  // X(QKV): xout is complete
+      dma_rows<CD>(a.xout, D, M, c0D, xs, lane);
+      dma_nw<CD>(a.n1, c0D, nws, lane);
+      wait_vm0();
+      rms_partial<CD>(xs, c0D, lane, wv, ss);
+      wait_lgkm0();
+      bar();  // S(QKV)
+      const float inv = rms_inv(ss, lane, D, a.eps);
+      f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
+      if (tq1 >= 0) mfma_chunks<2, CD>(acc, wq, xs, nws, c0D, lane, inv, true);
+      else if (tq0 >= 0)
+        mfma_chunks<1, CD>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv, true);
+      put_partials<2>(psD, acc, wv, lane);
+      wait_lgkm0();
+      bar();  // P(QKV)
+    }
+    return;
+  }
+
+  // -------------------------------------------------------------------- loader wave
+  const int me = lane & 15;        // output row of this lane's epilogue slot
+  const int cg = 4 * (lane >> 4);  // its first column inside the tile
+  const bool mrow = me < M;
+  const int grp = b & 7;
+  const uint32_t per = (uint32_t)(NB >> 3);
+  bool ok = true;
+  uint32_t go = 0;
+  if (lane == 0) go = ld_sc1(a.sync + 64 * (1 + grp) + 32);
+
+  // epilogue operands that do not depend on this launch's phases
+  f16x4 so4 = {}, xr4 = {}, s2v = {};
+  f16x4 s13v[NT13];
+  if (tO >= 0) {
+    so4 = *(const f16x4*)(a.so + 16 * tO + cg);
+    if (mrow) xr4 = *(const f16x4*)(a.xin + (long)me * D + 16 * tO + cg);
+  }
+#pragma unroll
+  for (int t = 0; t < NT13; ++t) s13v[t] = *(const f16x4*)(a.s13 + 16 * (b * NT13 + t) + cg);
+  if (t2 >= 0) s2v = *(const f16x4*)(a.s2 + 16 * t2 + cg);
+  const int HD = a.HD, L = a.L;
+  const int tq[2] = {tq0, tq1};
+  f16x4 sqv[2] = {};
+  float cs[2][4] = {};
+  long p_raw = 0;
+  if (has_next) {
+    if (mrow) p_raw = a.pos[me];
+    const long pc = p_raw < 0 ? 0 : (p_raw >= L ? L - 1 : p_raw);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (tq[i] < 0) continue;
+      const int nb = 16 * tq[i] + cg;
+      sqv[i] = *(const f16x4*)(a.sq + nb);
+      const int h = nb / HD, d = nb - h * HD;
+      if (h < a.Hq + a.Hk) {
+        const float* c = a.rope + pc * HD + d;  // (cos, sin) of pairs d/2 and d/2 + 1
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cs[i][r] = c[r];
+      }
+    }
+  }
+
+  // phase O
+  bar();  // P(O)
+  if (tO >= 0) {
+    const f16x4 y = scale4(sum_partials<1>(psD, 0, lane), so4);
+    if (mrow) st_sc1_u64(a.x1 + (long)me * D + 16 * tO + cg, y + xr4);
+  }
+  wait_vm0();
+  if (lane == 0) {
+    gate_arrive(a.sync, grp, per, go);
+    ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+    ++go;
+  }
+
+  // phase W13 (the W2 epilogue's residual x1 is final now: read it before the weight stream of
+  // the next phases is in flight)
+  f16x4 r2 = {};
+  if (t2 >= 0 && mrow)
+    r2 = __builtin_bit_cast(f16x4, __hip_atomic_load((const uint64_t*)(a.x1 + (long)me * D + 16 * t2 + cg),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  bar();  // X(W13)
+  bar();  // S(W13)
+  bar();  // P(W13)
+  {
+    f16x2 o[NT13];
+#pragma unroll
+    for (int t = 0; t < NT13; ++t) {
+      // interleaved w1 | w3 rows: (a_j, b_j, a_j+1, b_j+1), j = column / 2
+      const f16x4 y = scale4(sum_partials<NT13>(psD, t, lane), s13v[t]);
+      const float a0 = (float)y[0], a1 = (float)y[2];
+      o[t].x = (f16)(a0 / (1.0f + expf(-a0))) * y[1];
+      o[t].y = (f16)(a1 / (1.0f + expf(-a1))) * y[3];
+    }
+    if (mrow)
+#pragma unroll
+      for (int t = 0; t < NT13; ++t)
+        st_sc1_u32(a.mm + (long)me * F + ((16 * (b * NT13 + t) + cg) >> 1), o[t]);
+  }
+  wait_vm0();
+  if (lane == 0) {
+    gate_arrive(a.sync, grp, per, go);
+    ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+    ++go;
+  }
+
+  // phase W2
+  bar();  // X(W2)
+  bar();  // P(W2)
+  if (t2 >= 0) {
+    const f16x4 y = scale4(sum_partials<1>(psF, 0, lane), s2v) + r2;
+    if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+  }
+
+  if (has_next) {
+    wait_vm0();
+    if (lane == 0) {
+      gate_arrive(a.sync, grp, per, go);
+      ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+      ++go;
+    }
+    bar();  // X(QKV)
+    bar();  // S(QKV)
+    bar();  // P(QKV)
+    const bool pval = p_raw >= 0 && p_raw < L;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (tq[i] < 0) continue;
+      const f16x4 y = scale4(sum_partials<2>(psD, i, lane), sqv[i]);
+      if (!mrow) continue;
+      const int nb = 16 * tq[i] + cg;
+      const int h = nb / HD, d = nb - h * HD;
+      f16x4 o;
+      if (h < a.Hq + a.Hk) {
+        const float x0 = (float)y[0], x1 = (float)y[1], x2 = (float)y[2], x3 = (float)y[3];
+        o[0] = (f16)(x0 * cs[i][0] - x1 * cs[i][1]);
+        o[1] = (f16)(x1 * cs[i][0] + x0 * cs[i][1]);
+        o[2] = (f16)(x2 * cs[i][2] - x3 * cs[i][3]);
+        o[3] = (f16)(x3 * cs[i][2] + x2 * cs[i][3]);
+      } else {
+        o = y;
+      }
+      if (h < a.Hq) {
+        *(f16x4*)(a.q + ((long)me * a.Hq + h) * HD + d) = o;
+      } else if (pval) {
+        const int bb = me / a.S;
+        const int kh = h < a.Hq + a.Hk ? h - a.Hq : h - a.Hq - a.Hk;
+        f16* dst = h < a.Hq + a.Hk ? a.kc : a.vc;
+        *(f16x4*)(dst + (((long)bb * a.Hk + kh) * L + p_raw) * HD + d) = o;
+      }
+    }
+  }
+  if (lane == 0 && !ok) store_agent(a.err, 1u);
+}
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev]) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+    cus[dev] = p.multiProcessorCount;
+  }
+  return cus[dev];
+}
+
+template <int CD, int CF, int NT13, bool NTL>
+int launch(const Args& a, int nb, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, NTL>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             160 * 1024);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  const int xd = CD * CW * CHB, xf = CF * CW * CHB;
+  const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
+  const int ldsF = xf + CW * 1024;
+  const int lds = ldsD > ldsF ? ldsD : ldsF;
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
+  return ecd_launch_status();
+}
+
+}  // namespace tail
+}  // namespace ecd
+
+using namespace ecd;
+
+extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
+                              const void* n2, const void* w13, const void* s13, const void* w2,
+                              const void* s2, const void* n1, const void* wq, const void* sq,
+                              const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
+                              void* x1, void* mm, void* xout, void* sync, void* err, int M, int D,
+                              int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
+                              void* stream) {
+  tail::Args a = {};
+  a.o = (const f16*)o; a.xin = (const f16*)xin;
+  a.wo = (const int8_t*)wo; a.so = (const f16*)so; a.n2 = (const f16*)n2;
+  a.w13 = (const int8_t*)w13; a.s13 = (const f16*)s13;
+  a.w2 = (const int8_t*)w2; a.s2 = (const f16*)s2;
+  a.n1 = (const f16*)n1; a.wq = (const int8_t*)wq; a.sq = (const f16*)sq;
+  a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
+  a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
+  a.x1 = (f16*)x1; a.mm = (f16*)mm; a.xout = (f16*)xout;
+  a.sync = (uint32_t*)sync; a.err = (uint32_t*)err;
+  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!o || !xin || !wo || !so || !n2 || !w13 || !s13 || !w2 || !s2 || !x1 || !mm || !xout ||
+      !sync || !err || M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) ||
+      !al(o) || !al(xin) || !al(x1) || !al(mm) || !al(xout) || !al(n2) || !al(wo) ||
+      !al(w13) || !al(w2) || ((uintptr_t)sync & 255))
+    return ECD_EINVAL;
+  if (wq && (!n1 || !sq || !rope || !pos || !q || !kc || !vc || !al(n1) || !al(wq) || S <= 0 ||
+             Hq <= 0 || Hk <= 0 || (Hq % Hk) || L <= 0 || HD <= 0 || (HD % 4) ||
+             (Hq + 2 * Hk) * HD % 16))
+    return ECD_EINVAL;
+  const int nb = tail::device_cus();
+  const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
+  const int t13 = 2 * F / 16;
+  if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb)
+    return ECD_ENOTSUP;
+  if (wq && (Hq + 2 * Hk) * HD / 16 > 2 * nb) return ECD_ENOTSUP;
+  const int nt13 = t13 / nb;
+  const bool ntl = (flags >> 1) & 1;
+  hipStream_t st = (hipStream_t)stream;
+#define ECD_TAIL(CD_, CF_, NT_)                                                          \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_)                                             \
+    return ntl ? tail::launch<CD_, CF_, NT_, true>(a, nb, st)                            \
+               : tail::launch<CD_, CF_, NT_, false>(a, nb, st);
+  ECD_TAIL(6, 16, 4)  // 3072 -> 2 x 8192 -> 3072 (backbone; the reference's depth decoder)
+  ECD_TAIL(2, 16, 4)  // 1024 -> 2 x 8192 -> 1024 (the 1024-wide depth decoder)
+#undef ECD_TAIL
+  return ECD_ENOTSUP;
+}
+
+// ECD_OK when ecd_layer_tail runs these shapes on the current device, ECD_ENOTSUP otherwise
+// (the caller then runs the per-op kernels).
+extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD) {
+  const int nb = tail::device_cus();
+  if (M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) || nb <= 0 || (nb % 8))
+    return ECD_ENOTSUP;
+  const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW, t13 = 2 * F / 16;
+  if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 || (cd != 6 && cd != 2))
+    return ECD_ENOTSUP;
+  if (Hq <= 0 || Hk <= 0 || (Hq % Hk) || HD <= 0 || (HD % 4) || (Hq + 2 * Hk) * HD % 16 ||
+      (Hq + 2 * Hk) * HD / 16 > 2 * nb)
+    return ECD_ENOTSUP;
+  return ECD_OK;
+}

@@ -34,8 +34,9 @@ import torch
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
                       gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
-                      gemv_packed, int8_mm, next_power_of_2, pack_i8, rms as krms,
-                      rms_gemv_packed, rms_qkv_rope, rms_w13_silu, sample_topk, stream_ptr)
+                      gemv_packed, int8_mm, layer_tail, layer_tail_supported, next_power_of_2,
+                      pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_w13_silu,
+                      sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
 PROMPT_GEMM_ROWS = 64  # prompt passes with more rows run the MFMA GEMM path
@@ -212,16 +213,41 @@ class Stack:
         self.hd = dim // cfg["heads"]
         self.max_seq = cfg["max_seq"]
         self.nsplit = 16
+        self.tail = None
+        self.use_tail = True
 
     def alloc(self, B, L, dev, dtype):
         self.rope = rope_cache(self.hd, max(L, 16), device=dev)
         self.nsplit = 1 if L <= 128 else 16
         for b in self.blocks:
             b.alloc(B, L, dev, dtype)
+        self.tail = self._tail_buffers(B, dev, dtype)
+
+    def _tail_buffers(self, M, dev, dtype):
+        """Static buffers of the one-launch layer tail (ecd_layer_tail) for M-row decode steps,
+        or None when the shapes or weights do not fit it: x1, mm, two layer outputs used in
+        turn (a launch's output never aliases its input), q, the gate region and the error
+        word (both kept across launches)."""
+        if not self.blocks or any(b.qkv.qp is None or b.o.qp is None or b.w13.qp is None or
+                                  b.w2.qp is None for b in self.blocks):
+            return None
+        b0 = self.blocks[0]
+        F = b0.w2.K
+        if dtype != torch.float16 or not layer_tail_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd):
+            return None
+        e = lambda n: torch.empty(M, n, device=dev, dtype=dtype)  # noqa: E731
+        return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
+                    q=e(b0.h * b0.hd), sync=torch.zeros(1024, device=dev, dtype=torch.int32),
+                    err=torch.zeros(1, device=dev, dtype=torch.int32))
+
+    def tail_error(self):
+        """True if a layer-tail launch of this stack timed out waiting at a gate (host sync)."""
+        return self.tail is not None and int(self.tail["err"].item()) != 0
 
     def free(self):
         for b in self.blocks:
             b.kc = b.vc = None
+        self.tail = None
 
     def __call__(self, x, pos, attn_len=None, mask=None):
         """Prompt pass (app/engine.py:174-178): x [B, S, D], pos [B, S] absolute positions
@@ -274,6 +300,9 @@ class Stack:
             return h if final_norm else None
         R = x.shape[0]
         ns = self.nsplit
+        if self.use_tail and self.tail is not None and R == self.tail["M"]:
+            x = self._decode_tail(x, pos, S, ns)
+            return krms(x, self.norm) if final_norm else x
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
@@ -284,6 +313,27 @@ class Stack:
             mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2, stream=b.w13.stream)
             x = b.w2(mm, res=x)
         return krms(x, self.norm) if final_norm else x
+
+    def _decode_tail(self, x, pos, S, ns):
+        """Per layer: attention (+ split combine), then one ecd_layer_tail launch for the O
+        projection, the MLP and the next layer's rms + q|k|v + RoPE + cache write; layer 0's
+        q|k|v step runs first on its own.  Returns the last layer's output (a buffer of the
+        stack, valid until the next decode call)."""
+        t = self.tail
+        q = t["q"]
+        b0 = self.blocks[0]
+        rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
+                     b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
+        for i, b in enumerate(self.blocks):
+            o = self._attention(b, q, pos, S, ns)
+            nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
+            nxt = None if nb is None else dict(
+                n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, rope=self.rope, pos=pos, q=q, kc=nb.kc,
+                vc=nb.vc, S=S, Hq=nb.h, Hk=nb.kvh, L=nb.kc.shape[2], HD=nb.hd)
+            x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
+                           t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], nxt=nxt,
+                           stream=b.w13.stream)
+        return x
 
     def _attention(self, b, q, pos, S, ns):
         R = q.shape[0]

@@ -468,6 +468,61 @@ def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5, stream=False):
     return mm
 
 
+def layer_tail_supported(M, D, F, Hq, Hk, HD):
+    """True when ``layer_tail`` runs these shapes on the current device."""
+    return _ffi.lib().ecd_layer_tail_supported(int(M), int(D), int(F), int(Hq), int(Hk),
+                                               int(HD)) == _ffi.ECD_OK
+
+
+def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, nxt=None,
+               eps=1e-5, stream=False):
+    """One launch for the tail of a decode layer (app/engine.py:206-210: O projection +
+    residual, rms -> w1|w3 -> SiLU * mul, w2 + residual) and, with ``nxt``, the next layer's
+    rms -> q|k|v -> RoPE -> q, cache slot (:189-192).  Writes x1 [M, D], mm [M, F] and the layer
+    output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq (packed),
+    sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 1024], zero before first
+    use) and ``err`` (int32 [1]) persist between calls."""
+    dev = _dev(o, "layer_tail")
+    M, D = o.shape
+    F = mm.shape[1]
+    for t, n in ((o, "o"), (xin, "xin"), (x1, "x1"), (mm, "mm"), (xout, "xout")):
+        _f16(t, f"layer_tail {n}")
+        if not t.is_contiguous() or t.data_ptr() % 16:
+            raise ValueError(f"layer_tail: {n} must be contiguous and 16-byte aligned")
+    if xin.shape != (M, D) or x1.shape != (M, D) or xout.shape != (M, D) or mm.shape[0] != M:
+        raise ValueError("layer_tail: o, xin, x1, xout must be [M, D] and mm [M, F]")
+    lo, hi = xout.data_ptr(), xout.data_ptr() + xout.numel() * 2
+    for t in (o, xin, x1, mm):
+        if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * 2:
+            raise ValueError("layer_tail: xout must not alias o, xin, x1 or mm")
+    if sync.dtype != torch.int32 or sync.numel() < 1024 or sync.data_ptr() % 256:
+        raise ValueError("layer_tail: sync must be int32 [>= 1024], 256-byte aligned")
+    if err.dtype != torch.int32 or err.numel() < 1:
+        raise ValueError("layer_tail: err must be int32 [1]")
+    if nxt is None:
+        nargs = [None] * 8
+        S = Hq = Hk = L = HD = 1
+    else:
+        n = nxt
+        pos, kc = n["pos"], n["kc"]
+        S, Hq, Hk, L, HD = n["S"], n["Hq"], n["Hk"], n["L"], n["HD"]
+        if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+            raise ValueError("layer_tail: pos must be contiguous int64 [M]")
+        if kc.shape != (kc.shape[0], Hk, L, HD) or kc.shape[0] * S < M or n["vc"].shape != kc.shape:
+            raise ValueError("layer_tail: caches must be [B, Hk, L, HD] with B * S >= M")
+        if n["q"].numel() != M * Hq * HD or not n["q"].is_contiguous():
+            raise ValueError("layer_tail: q must be contiguous [M, Hq * HD]")
+        if n["rope"].shape[0] < L or n["rope"].shape[1] != HD // 2:
+            raise ValueError("layer_tail: rope table must be float32 [>= L, HD/2, 2]")
+        nargs = [n["n1"].data_ptr(), n["wq"].data_ptr(), n["sq"].data_ptr(), n["rope"].data_ptr(),
+                 pos.data_ptr(), n["q"].data_ptr(), kc.data_ptr(), n["vc"].data_ptr()]
+    _ffi.call("ecd_layer_tail", o.data_ptr(), xin.data_ptr(), wo.data_ptr(), so.data_ptr(),
+              n2.data_ptr(), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *nargs,
+              x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(), err.data_ptr(),
+              M, D, F, S, Hq, Hk, L, HD, float(eps), _flags(M, stream), stream_ptr(dev))
+    return xout
+
+
 def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False):
     """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
     interleave (even[b], emb[b]) and the output has 2B rows.  ``table`` holds int8 rows scaled by
