@@ -51,6 +51,8 @@
 // every wait on a gate is bounded, and a timeout sets *err and lets the kernel finish.
 #include "common.h"
 
+#include <utility>
+
 namespace ecd {
 namespace tail {
 
@@ -285,6 +287,47 @@ __device__ __forceinline__ void mfma_chunks(f32x4 (&acc)[NT], const u32x4 (&w)[N
   for (int t = 0; t < NT; ++t) acc[t] -= corr;
 }
 
+// Calls f(std::integral_constant<int, I>()) for I = 0 .. N - 1 (a loop with a constant index).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>());
+}
+
+// mfma_chunks with a hook after each chunk: after(integral_constant u) issues the next phase's
+// weight loads into registers the finished chunks leave free, so the stream keeps going during
+// the MFMAs.
+template <int NT, int C, typename After>
+__device__ __forceinline__ void mfma_chunks_then(f32x4 (&acc)[NT], const u32x4 (&w)[NT][C],
+                                                 const unsigned char* xs, const unsigned char* nws,
+                                                 int c0, int lane, float inv, bool rms,
+                                                 After after) {
+  const f16 kb = (f16)1152.0f;
+  const f16x8 bias = (f16x8){kb, kb, kb, kb, kb, kb, kb, kb};
+  f32x4 corr = (f32x4){0.f, 0.f, 0.f, 0.f};
+  static_for<C>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    f16x8 fa, fb;
+    xfrag(xs, c0 + u, lane, fa, fb);
+    if (rms) rms_frag(fa, fb, nws, c0 + u, lane, inv);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fa, corr, 0, 0, 0);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fb, corr, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f16x8 wa, wb;
+      i8x16_to_f16_biased(w[t][u], wa, wb);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, fb, acc[t], 0, 0, 0);
+    }
+    after(uc);
+  });
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] -= corr;
+}
+
 template <bool NTL>
 __device__ __forceinline__ u32x4 ldw(const int8_t* p) {
   if (NTL) return __builtin_nontemporal_load((const u32x4*)p);
@@ -299,6 +342,26 @@ __device__ __forceinline__ void load_w(u32x4 (&w)[NT][C], const int8_t* wp, cons
 #pragma unroll
     for (int u = 0; u < C; ++u)
       w[t][u] = ldw<NTL>(wp + ((long)tiles[t] * nch + c0 + u) * 1024 + 16 * lane);
+}
+
+// Chunks [u0, u1) of every tile, chunk-major.  LA > 0: paced -- before each load, wait until
+// at most LA - 1 vector-memory operations of this wave are in flight.  A CU's outstanding reads
+// queue in the memory system ahead of everything issued after them (the gate's atomics and
+// polls, the activation copies, the epilogue stores), so the weight stream is kept at the depth
+// HBM needs (LA KB per wave) instead of a whole phase ahead.
+template <int NT, int C, bool NTL, int U0, int U1, int LA>
+__device__ __forceinline__ void load_w_chunks(u32x4 (&w)[NT][C], const int8_t* wp,
+                                              const int (&tiles)[NT], int nch, int c0, int lane) {
+#pragma unroll
+  for (int u = U0; u < U1; ++u)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (LA > 0) {
+        wait_vm<(LA > 0 ? LA - 1 : 0)>();
+        asm volatile("" ::: "memory");
+      }
+      w[t][u] = ldw<NTL>(wp + ((long)tiles[t] * nch + c0 + u) * 1024 + 16 * lane);
+    }
 }
 
 template <int NT>
@@ -343,6 +406,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   // the 1024-wide shapes issue all of W2 at the start; the 3072-wide ones after the W13 MFMAs
   // (their W13 share alone takes 96 registers)
   constexpr bool W2_EARLY = CD < 6;
+  constexpr int LA = 8;  // weight loads in flight per compute wave (paced issue)
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NB = gridDim.x, b = blockIdx.x;
@@ -378,24 +442,24 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 #pragma unroll
     for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
     if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
-    load_w<NT13, CD, NTL>(w13, a.w13, t13, nchD, c0D, lane);
-    u32x4 w2[1][CF];
-    const int t2_t[1] = {t2 < 0 ? 0 : t2};
-    if (W2_EARLY && t2 >= 0) load_w<1, CF, NTL>(w2, a.w2, t2_t, nchF, c0F, lane);
+    load_w_chunks<NT13, CD, NTL, 0, 1, 0>(w13, a.w13, t13, nchD, c0D, lane);
 
     // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
-    // wait until this wave's o slice has landed (the loads issued after it: W_O, W13, early W2)
+    // wait for this wave's o slice and W_O (the NT13 W13 loads issued after them may fly on)
     {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
       if (tO >= 0) {
-        if (W2_EARLY && t2 >= 0) wait_vm<CD + NT13 * CD + (W2_EARLY ? CF : 0)>();
-        else wait_vm<CD + NT13 * CD>();
+        wait_vm<NT13>();
         mfma_chunks<1, CD>(acc, wo, xs, nws, c0D, lane, 0.f, false);
       }
       put_partials<1>(psD, acc, wv, lane);
     }
     wait_lgkm0();
     bar();  // P(O)
+    load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
+    u32x4 w2[1][CF];
+    const int t2_t[1] = {t2 < 0 ? 0 : t2};
+    if (W2_EARLY && t2 >= 0) load_w_chunks<1, CF, NTL, 0, CF, LA>(w2, a.w2, t2_t, nchF, c0F, lane);
 
     // phase W13 (x = rms(x1, n2))
     bar();  // X(W13): x1 is complete
@@ -405,25 +469,26 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     rms_partial<CD>(xs, c0D, lane, wv, ss);
     wait_lgkm0();
     bar();  // S(W13)
-    u32x4 wq[2][CD];
-    const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
     {
       const float inv = rms_inv(ss, lane, D, a.eps);
       f32x4 acc[NT13];
 #pragma unroll
       for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      mfma_chunks<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true);
-      // the W13 registers are dead past this point: the loads below reuse them
-#pragma unroll
-      for (int t = 0; t < NT13; ++t) asm volatile("" : "+v"(acc[t])::"memory");
-      if (!W2_EARLY && t2 >= 0) load_w<1, CF, NTL>(w2, a.w2, t2_t, nchF, c0F, lane);
-      if (tq1 >= 0) load_w<2, CD, NTL>(wq, a.wq, tq_t, nchD, c0D, lane);
-      else if (tq0 >= 0)
-        load_w<1, CD, NTL>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t, nchD, c0D, lane);
+      // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
+      const bool ld2 = !W2_EARLY && t2 >= 0;
+      mfma_chunks_then<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (ld2)
+          load_w_chunks<1, CF, NTL, (u * CF) / CD, ((u + 1) * CF) / CD, LA>(w2, a.w2, t2_t, nchF,
+                                                                            c0F, lane);
+      });
       put_partials<NT13>(psD, acc, wv, lane);
     }
     wait_lgkm0();
     bar();  // P(W13)
+
+    u32x4 wq[2][CD];
+    const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
 
     // phase W2 (x = mm)
     bar();  // X(W2): mm is complete
@@ -431,7 +496,20 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     wait_vm0();
     {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-      if (t2 >= 0) mfma_chunks<1, CF>(acc, w2, xs, nws, c0F, lane, 0.f, false);
+      // the next layer's q|k|v weights go out during the W2 MFMAs
+      auto ldq = [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        constexpr int q0 = (u * CD) / CF, q1 = ((u + 1) * CD) / CF;
+        if (tq1 >= 0) load_w_chunks<2, CD, NTL, q0, q1, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+        else if (tq0 >= 0)
+          load_w_chunks<1, CD, NTL, q0, q1, LA>(*(u32x4(*)[1][CD])wq, a.wq,
+                                                *(const int(*)[1])tq_t, nchD, c0D, lane);
+      };
+      if (t2 >= 0) {
+        mfma_chunks_then<1, CF>(acc, w2, xs, nws, c0F, lane, 0.f, false, ldq);
+      } else {
+        static_for<CF>(ldq);
+      }
       put_partials<1>(psF, acc, wv, lane);
     }
     wait_lgkm0();
