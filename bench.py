@@ -219,7 +219,7 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
             return 2 * F * K + 4 * F + 2 * M * K + 2 * K + 2 * M * F
         if name == "ecd_layer_tail":
             # O (+res), rms -> w1|w3 -> SiLU, w2 (+res), and the next layer's rms -> q|k|v
-            M, D, F, Hq, Hk, HD = a[22], a[23], a[24], a[26], a[27], a[29]
+            M, D, F, Hq, Hk, HD = a[23], a[24], a[25], a[27], a[28], a[30]
             b = (D * D + 2 * D + 6 * M * D) + (2 * F * D + 4 * F + 2 * M * D + 2 * D + 2 * M * F) \
                 + (D * F + 2 * D + 2 * M * F + 4 * M * D)
             if a[10]:

@@ -84,8 +84,8 @@ SIGNATURES = {
     "ecd_embed_gemv_i8p": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, _P, _P, c_long, c_int,
                            c_int, c_int, c_int, _P],
     "ecd_layer_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                       _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
-                       c_int, _P],
+                       _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                       c_float, c_int, _P],
     "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int],
 }
 

@@ -60,6 +60,8 @@ constexpr int CW = 8;                // compute waves per workgroup
 constexpr int NTHR = (CW + 1) * 64;  // plus the loader wave
 constexpr int MR = 8;                // rows held in the x tile (M <= MR)
 constexpr int CHB = 128 * MR;        // LDS bytes per 64-column chunk of the x tile
+constexpr int CNT2 = 640;            // sync words [640, 1024): split-W2 arrival counters per tile
+constexpr int MAX_T2_SPLIT = 384;    // tiles a split W2 can have (sync region words)
 
 struct Args {
   const f16* o;    // [M, D] attention output of this layer
@@ -87,6 +89,7 @@ struct Args {
   f16* xout;  // [M, D]
   uint32_t* sync;  // 4 KB gate region, zero before the first launch
   uint32_t* err;   // set to 1 when a gate wait times out
+  float* ws;       // split-W2 partial sums: [D / 16 tiles][KS2][64 lanes][4] (KS2 > 1 only)
   int M, D, F;
   float eps;
   int spin_max;
@@ -107,6 +110,19 @@ __device__ __forceinline__ void st_sc1_u64(f16* p, f16x4 v) {
 __device__ __forceinline__ void st_sc1_u32(f16* p, f16x2 v) {
   __hip_atomic_store((uint32_t*)p, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_sc1_f32x4(float* p, f32x4 v) {
+  const u32x4 u = __builtin_bit_cast(u32x4, v);
+  __hip_atomic_store((uint64_t*)p, (uint64_t)u.x | ((uint64_t)u.y << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((uint64_t*)p + 1, (uint64_t)u.z | ((uint64_t)u.w << 32), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 ld_sc1_f32x4(const float* p) {
+  const uint64_t a = __hip_atomic_load((uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load((uint64_t*)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(f32x4, (u32x4){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b,
+                                           (uint32_t)(b >> 32)});
 }
 __device__ __forceinline__ uint32_t ld_sc1(const uint32_t* p) {
   return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -400,13 +416,11 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, bool NTL>
+template <int CD, int CF, int NT13, int KS2, bool NTL>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // the 1024-wide shapes issue all of W2 at the start; the 3072-wide ones after the W13 MFMAs
-  // (their W13 share alone takes 96 registers)
-  constexpr bool W2_EARLY = CD < 6;
-  constexpr int LA = 8;  // weight loads in flight per compute wave (paced issue)
+  constexpr int LA = 8;        // weight loads in flight per compute wave (paced issue)
+  constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NB = gridDim.x, b = blockIdx.x;
@@ -417,7 +431,10 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
   const int TO = D >> 4;
   const int tO = b - (NB - TO);    // >= 0: one O tile
-  const int t2 = b < TO ? b : -1;  // one W2 tile (W2 has D / 16 tiles too)
+  // W2 (D / 16 tiles too): tile b (KS2 == 1), or tile b / KS2, K-part b % KS2 (host: D / 16 *
+  // KS2 == NB), whose partial sums the last of the KS2 workgroups adds up
+  const int t2 = KS2 == 1 ? (b < TO ? b : -1) : b / KS2;
+  const int ks2 = KS2 == 1 ? 0 : b % KS2;
   const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
   const int xtra = TQ - NB;
   const int tq0 = b < TQ ? b : -1;
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
   if (wv < CW) {
     // ------------------------------------------------------------------ compute waves
-    const int c0D = wv * CD, c0F = wv * CF;
+    const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
     // this wave's slice of the attention output first (the inputs of this launch are final)
     dma_rows<CD>(a.o, D, M, c0D, xs, lane);
     u32x4 wo[1][CD];
@@ -457,9 +474,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     wait_lgkm0();
     bar();  // P(O)
     load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
-    u32x4 w2[1][CF];
+    u32x4 w2[1][C2];
     const int t2_t[1] = {t2 < 0 ? 0 : t2};
-    if (W2_EARLY && t2 >= 0) load_w_chunks<1, CF, NTL, 0, CF, LA>(w2, a.w2, t2_t, nchF, c0F, lane);
 
     // phase W13 (x = rms(x1, n2))
     bar();  // X(W13): x1 is complete
@@ -475,11 +491,10 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 #pragma unroll
       for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
       // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
-      const bool ld2 = !W2_EARLY && t2 >= 0;
       mfma_chunks_then<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        if (ld2)
-          load_w_chunks<1, CF, NTL, (u * CF) / CD, ((u + 1) * CF) / CD, LA>(w2, a.w2, t2_t, nchF,
+        if (t2 >= 0)
+          load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
                                                                             c0F, lane);
       });
       put_partials<NT13>(psD, acc, wv, lane);
@@ -492,23 +507,23 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
     // phase W2 (x = mm)
     bar();  // X(W2): mm is complete
-    dma_rows<CF>(a.mm, F, M, c0F, xs, lane);
+    dma_rows<C2>(a.mm, F, M, c0F, xs, lane);
     wait_vm0();
     {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
       // the next layer's q|k|v weights go out during the W2 MFMAs
       auto ldq = [&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        constexpr int q0 = (u * CD) / CF, q1 = ((u + 1) * CD) / CF;
+        constexpr int q0 = (u * CD) / C2, q1 = ((u + 1) * CD) / C2;
         if (tq1 >= 0) load_w_chunks<2, CD, NTL, q0, q1, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
         else if (tq0 >= 0)
           load_w_chunks<1, CD, NTL, q0, q1, LA>(*(u32x4(*)[1][CD])wq, a.wq,
                                                 *(const int(*)[1])tq_t, nchD, c0D, lane);
       };
       if (t2 >= 0) {
-        mfma_chunks_then<1, CF>(acc, w2, xs, nws, c0F, lane, 0.f, false, ldq);
+        mfma_chunks_then<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false, ldq);
       } else {
-        static_for<CF>(ldq);
+        static_for<C2>(ldq);
       }
       put_partials<1>(psF, acc, wv, lane);
     }
@@ -625,9 +640,27 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   // phase W2
   bar();  // X(W2)
   bar();  // P(W2)
-  if (t2 >= 0) {
-    const f16x4 y = scale4(sum_partials<1>(psF, 0, lane), s2v) + r2;
-    if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+  if (KS2 == 1) {
+    if (t2 >= 0) {
+      const f16x4 y = scale4(sum_partials<1>(psF, 0, lane), s2v) + r2;
+      if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+    }
+  } else {
+    // this workgroup's K-part -> workspace; the last of the tile's KS2 workgroups (its count
+    // modulo KS2; the counters only grow) adds the KS2 parts in K order and stores xout
+    float* wp = a.ws + ((long)(t2 * KS2 + ks2) * 64 + lane) * 4;
+    st_sc1_f32x4(wp, sum_partials<1>(psF, 0, lane));
+    wait_vm0();
+    uint32_t old = 0;
+    if (lane == 0) old = add_agent(a.sync + CNT2 + t2);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old % KS2 == KS2 - 1) {
+      f32x4 acc = ld_sc1_f32x4(a.ws + ((long)(t2 * KS2) * 64 + lane) * 4);
+#pragma unroll
+      for (int k = 1; k < KS2; ++k) acc += ld_sc1_f32x4(a.ws + ((long)(t2 * KS2 + k) * 64 + lane) * 4);
+      const f16x4 y = scale4(acc, s2v) + r2;
+      if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+    }
   }
 
   if (has_next) {
@@ -683,11 +716,11 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, bool NTL>
+template <int CD, int CF, int NT13, int KS2, bool NTL>
 int launch(const Args& a, int nb, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, NTL>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, NTL>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              160 * 1024);
     if (e != hipSuccess) return (int)e;
@@ -697,7 +730,7 @@ int launch(const Args& a, int nb, hipStream_t st) {
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   const int lds = ldsD > ldsF ? ldsD : ldsF;
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -710,9 +743,9 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
                               const void* n2, const void* w13, const void* s13, const void* w2,
                               const void* s2, const void* n1, const void* wq, const void* sq,
                               const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
-                              void* x1, void* mm, void* xout, void* sync, void* err, int M, int D,
-                              int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
-                              void* stream) {
+                              void* x1, void* mm, void* xout, void* sync, void* err, void* ws,
+                              int M, int D, int F, int S, int Hq, int Hk, int L, int HD, float eps,
+                              int flags, void* stream) {
   tail::Args a = {};
   a.o = (const f16*)o; a.xin = (const f16*)xin;
   a.wo = (const int8_t*)wo; a.so = (const f16*)so; a.n2 = (const f16*)n2;
@@ -722,7 +755,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
   a.x1 = (f16*)x1; a.mm = (f16*)mm; a.xout = (f16*)xout;
-  a.sync = (uint32_t*)sync; a.err = (uint32_t*)err;
+  a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
   a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   if (!o || !xin || !wo || !so || !n2 || !w13 || !s13 || !w2 || !s2 || !x1 || !mm || !xout ||
@@ -741,14 +774,17 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
     return ECD_ENOTSUP;
   if (wq && (Hq + 2 * Hk) * HD / 16 > 2 * nb) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
+  // W2 has D / 16 tiles: with four times as many CUs, K is split over 4 workgroups per tile
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
+  if (ks2 > 1 && (!ws || !al(ws))) return ECD_EINVAL;
   const bool ntl = (flags >> 1) & 1;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_TAIL(CD_, CF_, NT_)                                                          \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_)                                             \
-    return ntl ? tail::launch<CD_, CF_, NT_, true>(a, nb, st)                            \
-               : tail::launch<CD_, CF_, NT_, false>(a, nb, st);
-  ECD_TAIL(6, 16, 4)  // 3072 -> 2 x 8192 -> 3072 (backbone; the reference's depth decoder)
-  ECD_TAIL(2, 16, 4)  // 1024 -> 2 x 8192 -> 1024 (the 1024-wide depth decoder)
+#define ECD_TAIL(CD_, CF_, NT_, KS_)                                                     \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_)                               \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, true>(a, nb, st)                       \
+               : tail::launch<CD_, CF_, NT_, KS_, false>(a, nb, st);
+  ECD_TAIL(6, 16, 4, 1)  // 3072 -> 2 x 8192 -> 3072 (backbone; the reference's depth decoder)
+  ECD_TAIL(2, 16, 4, 4)  // 1024 -> 2 x 8192 -> 1024 (the 1024-wide depth decoder)
 #undef ECD_TAIL
   return ECD_ENOTSUP;
 }
@@ -760,7 +796,9 @@ extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int
   if (M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) || nb <= 0 || (nb % 8))
     return ECD_ENOTSUP;
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW, t13 = 2 * F / 16;
-  if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 || (cd != 6 && cd != 2))
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
+  if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 || !((cd == 6 && ks2 == 1) ||
+                                                               (cd == 2 && ks2 == 4)))
     return ECD_ENOTSUP;
   if (Hq <= 0 || Hk <= 0 || (Hq % Hk) || HD <= 0 || (HD % 4) || (Hq + 2 * Hk) * HD % 16 ||
       (Hq + 2 * Hk) * HD / 16 > 2 * nb)

@@ -227,7 +227,7 @@ class Stack:
         """Static buffers of the one-launch layer tail (ecd_layer_tail) for M-row decode steps,
         or None when the shapes or weights do not fit it: x1, mm, two layer outputs used in
         turn (a launch's output never aliases its input), q, the gate region and the error
-        word (both kept across launches)."""
+        word (both kept across launches) and the split-w2 workspace."""
         if not self.blocks or any(b.qkv.qp is None or b.o.qp is None or b.w13.qp is None or
                                   b.w2.qp is None for b in self.blocks):
             return None
@@ -238,7 +238,8 @@ class Stack:
         e = lambda n: torch.empty(M, n, device=dev, dtype=dtype)  # noqa: E731
         return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
                     q=e(b0.h * b0.hd), sync=torch.zeros(1024, device=dev, dtype=torch.int32),
-                    err=torch.zeros(1, device=dev, dtype=torch.int32))
+                    err=torch.zeros(1, device=dev, dtype=torch.int32),
+                    ws=torch.empty(self.dim * 64, device=dev, dtype=torch.float32))
 
     def tail_error(self):
         """True if a layer-tail launch of this stack timed out waiting at a gate (host sync)."""
@@ -331,8 +332,8 @@ class Stack:
                 n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, rope=self.rope, pos=pos, q=q, kc=nb.kc,
                 vc=nb.vc, S=S, Hq=nb.h, Hk=nb.kvh, L=nb.kc.shape[2], HD=nb.hd)
             x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
-                           t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], nxt=nxt,
-                           stream=b.w13.stream)
+                           t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], t["ws"],
+                           nxt=nxt, stream=b.w13.stream)
         return x
 
     def _attention(self, b, q, pos, S, ns):

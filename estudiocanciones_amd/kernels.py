@@ -474,14 +474,15 @@ def layer_tail_supported(M, D, F, Hq, Hk, HD):
                                                int(HD)) == _ffi.ECD_OK
 
 
-def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, nxt=None,
+def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws, nxt=None,
                eps=1e-5, stream=False):
     """One launch for the tail of a decode layer (app/engine.py:206-210: O projection +
     residual, rms -> w1|w3 -> SiLU * mul, w2 + residual) and, with ``nxt``, the next layer's
     rms -> q|k|v -> RoPE -> q, cache slot (:189-192).  Writes x1 [M, D], mm [M, F] and the layer
     output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq (packed),
     sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 1024], zero before first
-    use) and ``err`` (int32 [1]) persist between calls."""
+    use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of >= D * 64
+    elements."""
     dev = _dev(o, "layer_tail")
     M, D = o.shape
     F = mm.shape[1]
@@ -499,6 +500,8 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, nx
         raise ValueError("layer_tail: sync must be int32 [>= 1024], 256-byte aligned")
     if err.dtype != torch.int32 or err.numel() < 1:
         raise ValueError("layer_tail: err must be int32 [1]")
+    if ws.dtype != torch.float32 or ws.numel() < D * 64 or ws.data_ptr() % 16:
+        raise ValueError("layer_tail: ws must be float32 [>= D * 64], 16-byte aligned")
     if nxt is None:
         nargs = [None] * 8
         S = Hq = Hk = L = HD = 1
@@ -519,7 +522,8 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, nx
     _ffi.call("ecd_layer_tail", o.data_ptr(), xin.data_ptr(), wo.data_ptr(), so.data_ptr(),
               n2.data_ptr(), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *nargs,
               x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(), err.data_ptr(),
-              M, D, F, S, Hq, Hk, L, HD, float(eps), _flags(M, stream), stream_ptr(dev))
+              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps), _flags(M, stream),
+              stream_ptr(dev))
     return xout
 
 

@@ -212,7 +212,9 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * D (mm: F).  xout must not alias xin, o, x1 or mm.  sync: a 4 KB, 256-byte aligned region,
  * zero before the first call, kept for later calls (the kernel leaves it reusable); calls
  * sharing a sync region must not overlap in time.  err: a 4-byte word set to 1 if a
- * workgroup waited longer than its bound for the others (results then undefined).  The grid
+ * workgroup waited longer than its bound for the others (results then undefined).  ws: a
+ * 16-byte aligned workspace of D * 256 bytes (the K-split partial sums of w2 when the device has
+ * four CUs per w2 tile; contents need not persist).  The grid
  * is one workgroup per CU with all workgroups resident; shapes are those accepted by
  * ecd_layer_tail_supported (ECD_ENOTSUP otherwise).  flags bit 1: nontemporal weight loads.
  * No reference counterpart as one call: it replaces five reference launches plus one. */
@@ -220,8 +222,9 @@ int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* s
                    const void* n2, const void* w13, const void* s13, const void* w2,
                    const void* s2, const void* n1, const void* wq, const void* sq,
                    const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
-                   void* x1, void* mm, void* xout, void* sync, void* err, int M, int D, int F,
-                   int S, int Hq, int Hk, int L, int HD, float eps, int flags, void* stream);
+                   void* x1, void* mm, void* xout, void* sync, void* err, void* ws, int M,
+                   int D, int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
+                   void* stream);
 
 /* ECD_OK when ecd_layer_tail accepts these shapes on the current device (M rows, model width
  * D, FFN width F, heads), ECD_ENOTSUP otherwise.  No reference counterpart. */

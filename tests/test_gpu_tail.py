@@ -130,14 +130,16 @@ def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream):
             assert_within_noise(gv, wslot[i][1], aslot[i][1], what=f"layer {i} v slot")
 
 
-def test_tail_matches_per_op_kernels_and_repeats(dev):
+@pytest.mark.parametrize("cfg,L,stream", [(dict(BB3, layers=2), 512, True),
+                                          (dict(DEC3, layers=2), 8, False)])
+def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
     """The tail path against the per-op fused kernels on the same stack (same numerics up to
     the fp32 summation order), then five more launches from identical state give identical
-    bits (the gate region is reused), and a captured graph of the decode replays bit-equal."""
+    bits (the gate region and, for the 1024-wide shape, the split-w2 counters are reused), and
+    a captured graph of the decode replays bit-equal."""
     import torch
-    cfg = dict(BB3, layers=2)
-    B, L = 8, 512
-    ost, st = _stacks(dev, cfg, seed=11, B=B, L=L, stream=True)
+    B = 8
+    ost, st = _stacks(dev, cfg, seed=11, B=B, L=L, stream=stream)
     _fill(ost, st, seed=12, upto=L)
     kv0 = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
 
