@@ -37,7 +37,7 @@ import time
 
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "gemv_family_traffic.json")
+                            "layer_tail_backbone_traffic.json")
 METRIC = "frames/s (3B backbone + 7 decoder passes) @ batch 8; decode-attn+GEMV HBM GB/s"
 
 
@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--no-tail", dest="tail", action="store_false",
                     help="run each layer's O / MLP / next q|k|v as separate GEMV launches instead "
                          "of one layer-tail launch")
+    ap.add_argument("--tail-attn", choices=("on", "off", "backbone", "decoder"), default="on",
+                    help="which stacks run the next layer's attention inside the layer-tail "
+                         "launch (the others launch attention on its own)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -106,9 +109,14 @@ def time_graph(calls, torch, reps=20):
     return e0.elapsed_time(e1) / reps / len(calls)
 
 
+def is_backbone_tail(name):
+    """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6)."""
+    return "layer_tail_kernel<6," in name or "layer_tail_kernelILi6E" in name
+
+
 def pmc_summary(fetch_csv, write_csv, calib_mib):
-    """GEMV-family HBM bytes per launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each
-    scaled by what the counter reads for the calibration copy of known size."""
+    """HBM bytes per backbone layer-tail launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
+    each scaled by what the counter reads for the calibration copy of known size."""
     import csv
 
     def per_dispatch(path, counter):
@@ -125,19 +133,20 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
     out = {}
     for tag, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
         rows = per_dispatch(path, counter)
-        gemv = [v for n, v in rows if "gemv_" in n]
+        tail = [v for n, v in rows if is_backbone_tail(n)]
         copy = [v for n, v in rows if "copy_bytes_kernel" in n]
-        if not gemv or not copy:
-            raise SystemExit(f"{path}: no GEMV-family or calibration-copy dispatches with {counter}")
+        if not tail or not copy:
+            raise SystemExit(f"{path}: no backbone layer-tail or calibration-copy dispatches with "
+                             f"{counter}")
         kib_copy = copy[-1]
         factor = kib_copy / (calib_mib * 1024.0)
-        kib = sum(gemv) / len(gemv)
-        out[tag] = {"counter": counter, "gemv_dispatches": len(gemv),
-                    "kib_per_gemv_launch": round(kib, 1), "calib_copy_kib": round(kib_copy, 1),
+        kib = sum(tail) / len(tail)
+        out[tag] = {"counter": counter, "tail_dispatches": len(tail),
+                    "kib_per_tail_launch": round(kib, 1), "calib_copy_kib": round(kib_copy, 1),
                     "calib_expected_kib": calib_mib * 1024, "factor": round(factor, 4),
-                    "bytes_per_gemv_launch": int(kib * 1024 / factor)}
-    out["traffic_bytes_per_launch"] = out["fetch"]["bytes_per_gemv_launch"] + \
-        out["write"]["bytes_per_gemv_launch"]
+                    "bytes_per_tail_launch": int(kib * 1024 / factor)}
+    out["traffic_bytes_per_launch"] = out["fetch"]["bytes_per_tail_launch"] + \
+        out["write"]["bytes_per_tail_launch"]
     return out
 
 
@@ -219,7 +228,8 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
             return 2 * F * K + 4 * F + 2 * M * K + 2 * K + 2 * M * F
         if name == "ecd_layer_tail":
             # O (+res), rms -> w1|w3 -> SiLU, w2 (+res), and the next layer's rms -> q|k|v
-            M, D, F, Hq, Hk, HD = a[23], a[24], a[25], a[27], a[28], a[30]
+            # (the next layer's attention, when it runs in the launch, is counted by tail_attn_bytes)
+            M, D, F, Hq, Hk, HD = a[24], a[25], a[26], a[28], a[29], a[31]
             b = (D * D + 2 * D + 6 * M * D) + (2 * F * D + 4 * F + 2 * M * D + 2 * D + 2 * M * F) \
                 + (D * F + 2 * D + 2 * M * F + 4 * M * D)
             if a[10]:
@@ -232,7 +242,19 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
             return N * K + 2 * N + M * K + ev + 2 * M * N
         return None
 
-    gemv_calls = [(n, a, gemv_family_bytes(n, a)) for n, a in calls if gemv_family_bytes(n, a)]
+    # a layer-tail launch with o_next (argument 17) also runs the next layer's decode attention:
+    # its cache lengths are those of the stack's layer-0 attention launch, the latest before it
+    tail_att = {}
+    k_att, last = -1, None
+    for i, (n, a) in enumerate(calls):
+        if n == "ecd_decode_attn":
+            k_att += 1
+            last = attn_lens[k_att]
+        elif n == "ecd_layer_tail" and a[17]:
+            lens, R, Hq, Hk, HD = last
+            tail_att[i] = attn_bytes(R, Hq, Hk, HD, lens)
+    gemv_calls = [(n, a, gemv_family_bytes(n, a) + tail_att.get(i, 0))
+                  for i, (n, a) in enumerate(calls) if gemv_family_bytes(n, a)]
     attn_calls = [(n, a) for n, a in calls if n == "ecd_decode_attn"]
     assert len(attn_calls) == len(attn_lens), (len(attn_calls), len(attn_lens))
     gemv_b = [b for _, _, b in gemv_calls]
@@ -243,6 +265,11 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
 
     g_ms_launch = time_graph([relaunch(n, a) for n, a, _ in gemv_calls], torch)
     g_ms_total = g_ms_launch * len(gemv_calls)
+    # the dominant kernel: the backbone's layer-tail launches (width 3072), all of one shape
+    bt = [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_tail" and a[25] == 3072]
+    bt_ms = time_graph([relaunch(n, a) for n, a, _ in bt], torch) if bt else None
+    bt_bytes = sum(b for _, _, b in bt) / len(bt) if bt else None
+    bt_att = bool(bt) and bool(bt[0][1][17])
     bb_idx = [i for i, b in enumerate(attn_b) if b > 10e6]
     a_ms_launch = time_graph([relaunch(*attn_calls[i]) for i in range(len(attn_calls))], torch)
     a_ms_total = a_ms_launch * len(attn_calls)
@@ -258,7 +285,35 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     return dict(Lcap=Lcap, fps=fps, ms=ms, timed_s=dt, g_gbps=g_gbps, a_gbps=a_gbps,
                 bb_attn_gbps=bb_attn_gbps, gemv_b=gemv_b, attn_b=attn_b, g_avg_us=g_avg_us,
                 g_bytes_avg=g_bytes_avg, g_ms_total=g_ms_total, a_ms_total=a_ms_total,
-                a_ms_launch=a_ms_launch, frame_bytes=frame_bytes, launches=launches)
+                a_ms_launch=a_ms_launch, frame_bytes=frame_bytes, launches=launches,
+                bt_ms=bt_ms, bt_bytes=bt_bytes, bt_n=len(bt), bt_att=bt_att)
+
+
+def roofline_entry(pt, traffic):
+    """The dominant kernel of the frame: the backbone's layer-tail launch (28 per frame, one
+    shape).  achieved = its algorithmic bytes per launch / its mean launch time (graph replay of
+    the frame's 28 launches between hipEvents on their stream)."""
+    if not pt["bt_ms"]:
+        return {"bound": "hbm", "kernel": "layer tail not in use", "achieved": None,
+                "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": None, "traffic": None}
+    ach = pt["bt_bytes"] / (pt["bt_ms"] * 1e-3) / 1e9
+    what = "O + MLP + next layer's rms+q|k|v+RoPE" + (" + its decode attention"
+                                                      if pt["bt_att"] else "")
+    return {
+        "bound": "hbm",
+        "kernel": f"layer_tail_kernel, backbone width 3072 ({what})",
+        "achieved": round(ach, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBPS, 4),
+        "traffic": traffic,
+        "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per backbone layer-tail dispatch, "
+                           "copy-calibrated (profiles/layer_tail_backbone_traffic.json)")
+                          if traffic else None,
+        "avg_launch_us": round(pt["bt_ms"] * 1e3, 3),
+        "algorithmic_bytes_per_launch": int(pt["bt_bytes"]),
+        "launches_per_frame": pt["bt_n"],
+    }
 
 
 def main():
@@ -283,6 +338,8 @@ def main():
     w = synthetic_weights(bb, dec, dev, seed=args.seed)
     model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
     model.backbone.use_tail = model.decoder.use_tail = args.tail
+    model.backbone.tail_attention = args.tail_attn in ("on", "backbone")
+    model.decoder.tail_attention = args.tail_attn in ("on", "decoder")
     wcpu = None if args.no_cpu else {k: v.cpu() for k, v in w.items()}
     del w
     n = args.takes
@@ -374,17 +431,12 @@ def main():
             "batch": B, "takes": n, "kv_len": args.kv, "kv_capacity": Lcap,
         },
         "tokens_per_s": round(fps * E.N_CB * n, 1),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": ("gemv_xreg/xlds/fused kernels (int8 weight x f16 GEMV family, every GEMV "
-                       "launch of one frame)"),
-            "achieved": round(g_gbps, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
+        "roofline": roofline_entry(main_pt, traffic),
+        "gemv_family": {
+            "kernels": ("every int8-weight GEMV launch of one frame: layer tails, rms+q|k|v+RoPE, "
+                        "rms+w1|w3+SiLU, plain / split-K GEMVs, codebook heads"),
+            "achieved_GBps": round(g_gbps, 1),
             "frac": round(g_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
-            "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per GEMV-family dispatch, "
-                               "copy-calibrated (profiles/gemv_family_traffic.json)") if traffic else None,
             "avg_launch_us": round(g_avg_us, 3),
             "algorithmic_bytes_per_launch": int(g_bytes_avg),
             "launches_per_frame": len(gemv_b),
@@ -606,6 +658,8 @@ def measure_ref_decoder(torch, E, bb, dev, n, args, g):
     w = synthetic_weights(bb, dec, dev, seed=args.seed + 3)
     model = E.HeartMuLaLite(w, device=dev, backbone=bb, decoder=dec)
     model.backbone.use_tail = model.decoder.use_tail = args.tail
+    model.backbone.tail_attention = args.tail_attn in ("on", "backbone")
+    model.decoder.tail_attention = args.tail_attn in ("on", "decoder")
     del w
     pt = measure_point(torch, E, model, dev, n, args.kv, max(20, args.steps // 2), args.warmup, g)
     del model

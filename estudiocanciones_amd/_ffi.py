@@ -84,9 +84,10 @@ SIGNATURES = {
     "ecd_embed_gemv_i8p": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, _P, _P, c_long, c_int,
                            c_int, c_int, c_int, _P],
     "ecd_layer_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                       _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                       _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                        c_float, c_int, _P],
-    "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int],
+    "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    "ecd_layer_tail_ws_bytes": [c_int, c_int, c_int, c_int],
 }
 
 _lib = None
@@ -108,7 +109,8 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = argtypes
-            fn.restype = c_long if name.startswith("ecd_packed_bytes") else c_int
+            fn.restype = c_long if name.startswith("ecd_packed_bytes") or \
+                name == "ecd_layer_tail_ws_bytes" else c_int
         handle.ecd_version.argtypes = []
         handle.ecd_version.restype = ctypes.c_char_p
         _lib = handle

@@ -49,7 +49,7 @@
 // one 4 KB sync region serves every launch (each launch reads the go value at start).
 // All workgroups are resident at once (grid = CU count, one workgroup per CU by LDS use);
 // every wait on a gate is bounded, and a timeout sets *err and lets the kernel finish.
-#include "common.h"
+#include "attn_core.h"
 
 #include <utility>
 
@@ -62,6 +62,10 @@ constexpr int MR = 8;                // rows held in the x tile (M <= MR)
 constexpr int CHB = 128 * MR;        // LDS bytes per 64-column chunk of the x tile
 constexpr int CNT2 = 640;            // sync words [640, 1024): split-W2 arrival counters per tile
 constexpr int MAX_T2_SPLIT = 384;    // tiles a split W2 can have (sync region words)
+constexpr int CNTA = 1024;           // sync words [1024, 2048): attention arrival counters per pair
+constexpr int SYNC_WORDS = 2048;
+constexpr int ATT_SHORT = 128;       // caches of at most this many slots: one split per pair
+constexpr int ATT_KB_MAX = 16;       // workgroups per (row, kv head) pair, long caches
 
 struct Args {
   const f16* o;    // [M, D] attention output of this layer
@@ -87,9 +91,13 @@ struct Args {
   f16* x1;    // [M, D]
   f16* mm;    // [M, F]
   f16* xout;  // [M, D]
-  uint32_t* sync;  // 4 KB gate region, zero before the first launch
+  // next layer's attention (ATT kernels): o_next [M, Hq * HD] from q and the caches
+  f16* o_next;
+  float scale;
+  uint32_t* sync;  // 8 KB gate region, zero before the first launch
   uint32_t* err;   // set to 1 when a gate wait times out
-  float* ws;       // split-W2 partial sums: [D / 16 tiles][KS2][64 lanes][4] (KS2 > 1 only)
+  float* ws;       // workspace: split-W2 partial sums [D / 16][KS2][64][4] (KS2 > 1), and the
+                   // attention's per-workgroup partials [NB][G][2 + HD] (long caches)
   int M, D, F;
   float eps;
   int spin_max;
@@ -407,6 +415,166 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
   return y;
 }
 
+// ------------------------------------------------------------- next layer's attention phase
+// Decode attention of app/kernels.py:111-167 for the M rows, their kv heads and the query heads
+// of each (G = Hq / Hk), over cache slots [0, pos[r]], with the per-split core of the decode
+// kernel (attn_core.h).  Short caches: one wave per (row, kv head) pair writes o directly.  Long
+// caches: pair p = blockIdx / KB (KB = NB / pairs workgroups per pair), its split s =
+// (blockIdx % KB) * 8 + wave of S = 8 KB splits (the split rule of app/kernels.py:120-127 with
+// S splits); the loader merges its 8 waves' partials (log-sum-exp) into one per workgroup, and
+// the last of the pair's KB workgroups merges those and writes o.  Same arithmetic as the
+// split-combine kernel, summed in two levels.
+template <int HD, int G>
+__device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int NB, int b,
+                                                int wv, int lane) {
+  constexpr int NDP = SplitState<HD, G>::NDP;
+  constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
+  const int M = a.M, Hq = a.Hq, Hk = a.Hk, L = a.L;
+  const int pairs = M * Hk;
+  bar();  // X(ATT): q and the new cache slots are complete
+  if (L <= ATT_SHORT) {
+    const int p = b + NB * wv;
+    if (p < pairs) {
+      const int r = p / Hk, kh = p - r * Hk;
+      const long cbase = ((long)(r / a.S) * Hk + kh) * (long)L * HD;
+      f16x8 qf[HD / 32];
+      load_q<HD, G>(qf, a.q, r, Hq, kh, lane);
+      int lo, hi;
+      split_range(a.pos, r, L, 1, 0, lo, hi);
+      SplitState<HD, G> ss;
+      attn_split<HD, G, 1>(ss, qf, a.kc + cbase, a.vc + cbase, lo, hi, a.scale, lane);
+      attn_store_o<HD, G>(ss, a.o_next + ((long)r * Hq + kh * G) * HD, lane);
+    }
+    bar();  // P(ATT)
+    return;
+  }
+  const int KB = NB / pairs;
+  const int p = b / KB, kq = b - p * KB;
+  const int r = p / Hk, kh = p - r * Hk;
+  const long cbase = ((long)(r / a.S) * Hk + kh) * (long)L * HD;
+  f16x8 qf[HD / 32];
+  load_q<HD, G>(qf, a.q, r, Hq, kh, lane);
+  int lo, hi;
+  split_range(a.pos, r, L, KB * CW, kq * CW + wv, lo, hi);
+  SplitState<HD, G> ss;
+  // two K/V tiles in flight where the register budget of the 9-wave workgroup allows it
+  attn_split<HD, G, (G <= 3 ? 2 : 1)>(ss, qf, a.kc + cbase, a.vc + cbase, lo, hi, a.scale, lane);
+  // this wave's partial -> LDS [wave][g][m, l, acc]
+  float* pp = (float*)smem + wv * G * PW;
+  if (lane < G) {
+    pp[lane * PW] = ss.m_run;
+    pp[lane * PW + 1] = ss.l_run;
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < NDP; ++j) {
+        const int d = 8 * (lane + 16 * j);
+        if (d < HD)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pp[g * PW + 2 + d + e] = ss.acc[g][j][e];
+      }
+  }
+  wait_lgkm0();
+  bar();  // P(ATT)
+}
+
+// Log-sum-exp merge of n <= NMAX partials [i][g][m, l, acc[HD]] (stride `str` floats between
+// partials) for head g and the columns d = lane + 64 k: the weights exp(m_i - max m) (0 for an
+// empty part) and the sums in part order.  Every read is issued before the first use (one
+// memory round trip).
+template <int HD, int NMAX>
+__device__ __forceinline__ void lse_merge(const float* src, int n, int str, int g, int lane,
+                                          float& mo, float& lo, float (&ao)[(HD + 63) / 64],
+                                          bool agent_scope) {
+  constexpr int PW = 2 + HD;
+  constexpr int NK = (HD + 63) / 64;
+  auto rd = [&](const float* q) {
+    return agent_scope ? __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)q,
+                                                                     __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT))
+                       : *q;
+  };
+  float m[NMAX], l[NMAX], v[NMAX][NK];
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) v[i][k] = 0.f;
+    if (i < n) {
+      const float* q = src + i * str + g * PW;
+      m[i] = rd(q);
+      l[i] = rd(q + 1);
+#pragma unroll
+      for (int k = 0; k < NK; ++k)
+        if (lane + 64 * k < HD) v[i][k] = rd(q + 2 + lane + 64 * k);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) mx = fmaxf(mx, m[i]);
+  float ls = 0.f;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) ao[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) {
+    const float w = m[i] > -INFINITY ? __expf(m[i] - mx) : 0.f;
+    ls += l[i] * w;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) ao[k] += v[i][k] * w;
+  }
+  mo = mx;
+  lo = ls;
+}
+
+template <int HD, int G>
+__device__ __forceinline__ void attention_merge(const Args& a, unsigned char* smem, int NB, int b,
+                                                int lane) {
+  constexpr int PW = 2 + HD;
+  constexpr int NK = (HD + 63) / 64;
+  const int pairs = a.M * a.Hk;
+  if (a.L <= ATT_SHORT) return;  // the waves wrote o
+  const int KB = NB / pairs;
+  const int p = b / KB, kq = b - p * KB;
+  const int r = p / a.Hk, kh = p - r * a.Hk;
+  // the 8 waves -> this workgroup's partial in the workspace (agent scope)
+  float* part = a.ws + (long)(p * KB + kq) * G * PW;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mo, lo, ao[NK];
+    lse_merge<HD, CW>((const float*)smem, CW, G * PW, g, lane, mo, lo, ao, false);
+    if (lane == 0) {
+      store_agent((uint32_t*)part + g * PW, __builtin_bit_cast(uint32_t, mo));
+      store_agent((uint32_t*)part + g * PW + 1, __builtin_bit_cast(uint32_t, lo));
+    }
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int d = lane + 64 * k;
+      if (d < HD) store_agent((uint32_t*)part + g * PW + 2 + d, __builtin_bit_cast(uint32_t, ao[k]));
+    }
+  }
+  wait_vm0();
+  uint32_t old = 0;
+  if (lane == 0) old = add_agent(a.sync + CNTA + p);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old % (uint32_t)KB != (uint32_t)(KB - 1)) return;
+  // last of the pair's workgroups: merge the KB parts in order and write o
+  const float* base = a.ws + (long)p * KB * G * PW;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mo, lo, ao[NK];
+    lse_merge<HD, ATT_KB_MAX>(base, KB, G * PW, g, lane, mo, lo, ao, true);
+    f16* dst = a.o_next + ((long)r * a.Hq + kh * G + g) * HD;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int d = lane + 64 * k;
+      if (d < HD) dst[d] = (f16)(ao[k] / lo);
+    }
+  }
+}
+
 // LDS map (bytes), per phase, for K = D columns: x tile [0, XD), norm weights [XD, XD + 2D),
 // row sums [XD + 2D, + 512), partials after that; for the W2 phase (K = F): x tile [0, XF),
 // partials [XF, XF + 8 KB).  A phase's partials never overlap its own x tile or norm weights
@@ -416,7 +584,7 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, int KS2, bool NTL>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int LA = 8;        // weight loads in flight per compute wave (paced issue)
@@ -427,6 +595,10 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int D = a.D, F = a.F, M = a.M;
   const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
   const bool has_next = a.wq != nullptr;
+  // the next layer's attention runs in this launch (AHD > 0: its head_dim; AG query heads per
+  // kv head), after a fourth gate; caches longer than ATT_SHORT slots are split over the KB
+  // workgroups of each (row, kv head) pair and their 8 compute waves
+  const bool att = AHD > 0 && has_next;
 
   // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
   const int TO = D >> 4;
@@ -547,6 +719,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       put_partials<2>(psD, acc, wv, lane);
       wait_lgkm0();
       bar();  // P(QKV)
+    }
+    if constexpr (AHD > 0) {
+      if (att) attention_phase<AHD, AG>(a, smem, NB, b, wv, lane);
     }
     return;
   }
@@ -691,16 +866,34 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       } else {
         o = y;
       }
+      f16* dst = nullptr;
       if (h < a.Hq) {
-        *(f16x4*)(a.q + ((long)me * a.Hq + h) * HD + d) = o;
+        dst = a.q + ((long)me * a.Hq + h) * HD + d;
       } else if (pval) {
         const int bb = me / a.S;
         const int kh = h < a.Hq + a.Hk ? h - a.Hq : h - a.Hq - a.Hk;
-        f16* dst = h < a.Hq + a.Hk ? a.kc : a.vc;
-        *(f16x4*)(dst + (((long)bb * a.Hk + kh) * L + p_raw) * HD + d) = o;
+        dst = (h < a.Hq + a.Hk ? a.kc : a.vc) + (((long)bb * a.Hk + kh) * L + p_raw) * HD + d;
+      }
+      // read in this launch by the attention phase: agent scope
+      if (dst) {
+        if (att) st_sc1_u64(dst, o);
+        else *(f16x4*)dst = o;
       }
     }
+    if constexpr (AHD > 0) {
+      if (!att) goto done;
+      wait_vm0();
+      if (lane == 0) {
+        gate_arrive(a.sync, grp, per, go);
+        ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+        ++go;
+      }
+      bar();  // X(ATT)
+      bar();  // P(ATT)
+      attention_merge<AHD, AG>(a, smem, NB, b, lane);
+    }
   }
+done:
   if (lane == 0 && !ok) store_agent(a.err, 1u);
 }
 
@@ -716,11 +909,11 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, bool NTL>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
 int launch(const Args& a, int nb, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, NTL>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              160 * 1024);
     if (e != hipSuccess) return (int)e;
@@ -730,7 +923,7 @@ int launch(const Args& a, int nb, hipStream_t st) {
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   const int lds = ldsD > ldsF ? ldsD : ldsF;
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -739,13 +932,34 @@ int launch(const Args& a, int nb, hipStream_t st) {
 
 using namespace ecd;
 
+// Attention in the launch: (head_dim, query heads per kv head) instantiated, and the work split
+// fits the grid (long caches: NB / pairs workgroups per (row, kv head) pair).
+static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
+  if (Hk <= 0 || Hq % Hk) return false;
+  const int G = Hq / Hk, pairs = M * Hk;
+  if (!(HD == 128 && (G == 3 || G == 4))) return false;
+  if (L <= tail::ATT_SHORT) return pairs <= nb * tail::CW;
+  // KB = nb / pairs workgroups per pair; a power of two, so that the arrival counters (modulo
+  // KB, never reset) stay consistent across their 2^32 wrap
+  const int kb = nb / pairs;
+  return nb % pairs == 0 && (kb & (kb - 1)) == 0 && kb <= tail::ATT_KB_MAX &&
+         pairs <= tail::SYNC_WORDS - tail::CNTA;
+}
+
+extern "C" long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD) {
+  const int nb = tail::device_cus();
+  const long w2 = (long)D * 256;
+  const long at = Hk > 0 ? (long)nb * (Hq / Hk) * (HD + 2) * 4 : 0;
+  return w2 > at ? w2 : at;
+}
+
 extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
                               const void* n2, const void* w13, const void* s13, const void* w2,
                               const void* s2, const void* n1, const void* wq, const void* sq,
                               const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
-                              void* x1, void* mm, void* xout, void* sync, void* err, void* ws,
-                              int M, int D, int F, int S, int Hq, int Hk, int L, int HD, float eps,
-                              int flags, void* stream) {
+                              void* o_next, void* x1, void* mm, void* xout, void* sync, void* err,
+                              void* ws, int M, int D, int F, int S, int Hq, int Hk, int L, int HD,
+                              float eps, int flags, void* stream) {
   tail::Args a = {};
   a.o = (const f16*)o; a.xin = (const f16*)xin;
   a.wo = (const int8_t*)wo; a.so = (const f16*)so; a.n2 = (const f16*)n2;
@@ -754,6 +968,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   a.n1 = (const f16*)n1; a.wq = (const int8_t*)wq; a.sq = (const f16*)sq;
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
+  a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
   a.x1 = (f16*)x1; a.mm = (f16*)mm; a.xout = (f16*)xout;
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
   a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
@@ -767,31 +982,42 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
              Hq <= 0 || Hk <= 0 || (Hq % Hk) || L <= 0 || HD <= 0 || (HD % 4) ||
              (Hq + 2 * Hk) * HD % 16))
     return ECD_EINVAL;
+  if (o_next && (!wq || !al(o_next) || !ws)) return ECD_EINVAL;
   const int nb = tail::device_cus();
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
   const int t13 = 2 * F / 16;
   if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb)
     return ECD_ENOTSUP;
   if (wq && (Hq + 2 * Hk) * HD / 16 > 2 * nb) return ECD_ENOTSUP;
+  if (o_next && !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
   // W2 has D / 16 tiles: with four times as many CUs, K is split over 4 workgroups per tile
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
   if (ks2 > 1 && (!ws || !al(ws))) return ECD_EINVAL;
+  const int ag = o_next ? Hq / Hk : 0;
   const bool ntl = (flags >> 1) & 1;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_TAIL(CD_, CF_, NT_, KS_)                                                     \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_)                               \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, true>(a, nb, st)                       \
-               : tail::launch<CD_, CF_, NT_, KS_, false>(a, nb, st);
-  ECD_TAIL(6, 16, 4, 1)  // 3072 -> 2 x 8192 -> 3072 (backbone; the reference's depth decoder)
-  ECD_TAIL(2, 16, 4, 4)  // 1024 -> 2 x 8192 -> 1024 (the 1024-wide depth decoder)
+#define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_)                                          \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ && \
+      ag == AG_)                                                                         \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true>(a, nb, st)            \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false>(a, nb, st);
+  // 3072 -> 2 x 8192 -> 3072: the backbone (with its attention: 24q / 8kv, head_dim 128) and
+  // the reference's depth decoder (head_dim 384: attention launched on its own)
+  ECD_TAIL(6, 16, 4, 1, 128, 3)
+  ECD_TAIL(6, 16, 4, 1, 0, 0)
+  // 1024 -> 2 x 8192 -> 1024: the 1024-wide depth decoder (8q / 2kv, head_dim 128)
+  ECD_TAIL(2, 16, 4, 4, 128, 4)
+  ECD_TAIL(2, 16, 4, 4, 0, 0)
 #undef ECD_TAIL
   return ECD_ENOTSUP;
 }
 
-// ECD_OK when ecd_layer_tail runs these shapes on the current device, ECD_ENOTSUP otherwise
+// ECD_OK when ecd_layer_tail runs these shapes on the current device (with the next layer's
+// attention in the launch when `attention` is set; L = cache slots), ECD_ENOTSUP otherwise
 // (the caller then runs the per-op kernels).
-extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD) {
+extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD, int L,
+                                        int attention) {
   const int nb = tail::device_cus();
   if (M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) || nb <= 0 || (nb % 8))
     return ECD_ENOTSUP;
@@ -803,5 +1029,6 @@ extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int
   if (Hq <= 0 || Hk <= 0 || (Hq % Hk) || HD <= 0 || (HD % 4) || (Hq + 2 * Hk) * HD % 16 ||
       (Hq + 2 * Hk) * HD / 16 > 2 * nb)
     return ECD_ENOTSUP;
+  if (attention && !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   return ECD_OK;
 }

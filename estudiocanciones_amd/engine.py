@@ -34,7 +34,8 @@ import torch
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
                       gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
-                      gemv_packed, int8_mm, layer_tail, layer_tail_supported, next_power_of_2,
+                      gemv_packed, int8_mm, layer_tail, layer_tail_supported,
+                      layer_tail_ws_bytes, next_power_of_2,
                       pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_w13_silu,
                       sample_topk, stream_ptr)
 
@@ -215,15 +216,16 @@ class Stack:
         self.nsplit = 16
         self.tail = None
         self.use_tail = True
+        self.tail_attention = True  # the next layer's attention inside the tail launch
 
     def alloc(self, B, L, dev, dtype):
         self.rope = rope_cache(self.hd, max(L, 16), device=dev)
         self.nsplit = 1 if L <= 128 else 16
         for b in self.blocks:
             b.alloc(B, L, dev, dtype)
-        self.tail = self._tail_buffers(B, dev, dtype)
+        self.tail = self._tail_buffers(B, dev, dtype, L)
 
-    def _tail_buffers(self, M, dev, dtype):
+    def _tail_buffers(self, M, dev, dtype, L):
         """Static buffers of the one-launch layer tail (ecd_layer_tail) for M-row decode steps,
         or None when the shapes or weights do not fit it: x1, mm, two layer outputs used in
         turn (a launch's output never aliases its input), q, the gate region and the error
@@ -236,10 +238,14 @@ class Stack:
         if dtype != torch.float16 or not layer_tail_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd):
             return None
         e = lambda n: torch.empty(M, n, device=dev, dtype=dtype)  # noqa: E731
+        wsb = layer_tail_ws_bytes(self.dim, b0.h, b0.kvh, b0.hd)
+        # the next layer's attention inside the launch (its output in one of two buffers)
+        att = layer_tail_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd, L, attention=True)
         return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
-                    q=e(b0.h * b0.hd), sync=torch.zeros(1024, device=dev, dtype=torch.int32),
+                    q=e(b0.h * b0.hd), sync=torch.zeros(2048, device=dev, dtype=torch.int32),
                     err=torch.zeros(1, device=dev, dtype=torch.int32),
-                    ws=torch.empty(self.dim * 64, device=dev, dtype=torch.float32))
+                    ws=torch.empty(-(-wsb // 4), device=dev, dtype=torch.float32),
+                    att=att, ob=[e(b0.h * b0.hd), e(b0.h * b0.hd)] if att else None)
 
     def tail_error(self):
         """True if a layer-tail launch of this stack timed out waiting at a gate (host sync)."""
@@ -316,24 +322,29 @@ class Stack:
         return krms(x, self.norm) if final_norm else x
 
     def _decode_tail(self, x, pos, S, ns):
-        """Per layer: attention (+ split combine), then one ecd_layer_tail launch for the O
-        projection, the MLP and the next layer's rms + q|k|v + RoPE + cache write; layer 0's
-        q|k|v step runs first on its own.  Returns the last layer's output (a buffer of the
-        stack, valid until the next decode call)."""
+        """Layer 0's rms + q|k|v + RoPE + cache write and attention run first on their own; then
+        one ecd_layer_tail launch per layer: the O projection, the MLP, the next layer's rms +
+        q|k|v + RoPE + cache write and (where the shapes allow) that layer's attention, else
+        attention (+ split combine) as its own launches.  Returns the last layer's output (a
+        buffer of the stack, valid until the next decode call)."""
         t = self.tail
         q = t["q"]
         b0 = self.blocks[0]
         rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
                      b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
+        o = self._attention(b0, q, pos, S, ns)
         for i, b in enumerate(self.blocks):
-            o = self._attention(b, q, pos, S, ns)
             nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
             nxt = None if nb is None else dict(
                 n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, rope=self.rope, pos=pos, q=q, kc=nb.kc,
                 vc=nb.vc, S=S, Hq=nb.h, Hk=nb.kvh, L=nb.kc.shape[2], HD=nb.hd)
+            o_next = t["ob"][i % 2] if (t["att"] and self.tail_attention and nb is not None) \
+                else None
             x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
                            t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], t["ws"],
-                           nxt=nxt, stream=b.w13.stream)
+                           nxt=nxt, o_next=o_next, stream=b.w13.stream)
+            if nb is not None:
+                o = o_next if o_next is not None else self._attention(nb, q, pos, S, ns)
         return x
 
     def _attention(self, b, q, pos, S, ns):

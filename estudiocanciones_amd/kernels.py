@@ -468,21 +468,28 @@ def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5, stream=False):
     return mm
 
 
-def layer_tail_supported(M, D, F, Hq, Hk, HD):
-    """True when ``layer_tail`` runs these shapes on the current device."""
-    return _ffi.lib().ecd_layer_tail_supported(int(M), int(D), int(F), int(Hq), int(Hk),
-                                               int(HD)) == _ffi.ECD_OK
+def layer_tail_supported(M, D, F, Hq, Hk, HD, L=1, attention=False):
+    """True when ``layer_tail`` runs these shapes on the current device (with ``attention``: the
+    next layer's attention over an L-slot cache inside the same launch)."""
+    return _ffi.lib().ecd_layer_tail_supported(int(M), int(D), int(F), int(Hq), int(Hk), int(HD),
+                                               int(L), int(bool(attention))) == _ffi.ECD_OK
+
+
+def layer_tail_ws_bytes(D, Hq, Hk, HD):
+    """Bytes of the layer-tail workspace for these shapes on the current device."""
+    return int(_ffi.lib().ecd_layer_tail_ws_bytes(int(D), int(Hq), int(Hk), int(HD)))
 
 
 def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws, nxt=None,
-               eps=1e-5, stream=False):
+               o_next=None, eps=1e-5, stream=False):
     """One launch for the tail of a decode layer (app/engine.py:206-210: O projection +
     residual, rms -> w1|w3 -> SiLU * mul, w2 + residual) and, with ``nxt``, the next layer's
-    rms -> q|k|v -> RoPE -> q, cache slot (:189-192).  Writes x1 [M, D], mm [M, F] and the layer
-    output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq (packed),
-    sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 1024], zero before first
-    use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of >= D * 64
-    elements."""
+    rms -> q|k|v -> RoPE -> q, cache slot (:189-192) and, with ``o_next`` [M, Hq * HD], that
+    layer's decode attention (:194-204) into o_next.  Writes x1 [M, D], mm [M, F] and the layer
+    output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq
+    (packed), sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 2048], zero before
+    first use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of
+    layer_tail_ws_bytes bytes."""
     dev = _dev(o, "layer_tail")
     M, D = o.shape
     F = mm.shape[1]
@@ -496,12 +503,12 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     for t in (o, xin, x1, mm):
         if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * 2:
             raise ValueError("layer_tail: xout must not alias o, xin, x1 or mm")
-    if sync.dtype != torch.int32 or sync.numel() < 1024 or sync.data_ptr() % 256:
-        raise ValueError("layer_tail: sync must be int32 [>= 1024], 256-byte aligned")
+    if sync.dtype != torch.int32 or sync.numel() < 2048 or sync.data_ptr() % 256:
+        raise ValueError("layer_tail: sync must be int32 [>= 2048], 256-byte aligned")
     if err.dtype != torch.int32 or err.numel() < 1:
         raise ValueError("layer_tail: err must be int32 [1]")
-    if ws.dtype != torch.float32 or ws.numel() < D * 64 or ws.data_ptr() % 16:
-        raise ValueError("layer_tail: ws must be float32 [>= D * 64], 16-byte aligned")
+    if ws.dtype != torch.float32 or ws.data_ptr() % 16:
+        raise ValueError("layer_tail: ws must be float32, 16-byte aligned")
     if nxt is None:
         nargs = [None] * 8
         S = Hq = Hk = L = HD = 1
@@ -519,9 +526,18 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
             raise ValueError("layer_tail: rope table must be float32 [>= L, HD/2, 2]")
         nargs = [n["n1"].data_ptr(), n["wq"].data_ptr(), n["sq"].data_ptr(), n["rope"].data_ptr(),
                  pos.data_ptr(), n["q"].data_ptr(), kc.data_ptr(), n["vc"].data_ptr()]
+    if ws.numel() * 4 < layer_tail_ws_bytes(D, Hq, Hk, HD):
+        raise ValueError("layer_tail: ws is smaller than layer_tail_ws_bytes")
+    if o_next is not None:
+        if nxt is None:
+            raise ValueError("layer_tail: o_next needs the next layer (nxt)")
+        _f16(o_next, "layer_tail o_next")
+        if o_next.numel() != M * Hq * HD or not o_next.is_contiguous() or o_next.data_ptr() % 16:
+            raise ValueError("layer_tail: o_next must be contiguous [M, Hq * HD]")
     _ffi.call("ecd_layer_tail", o.data_ptr(), xin.data_ptr(), wo.data_ptr(), so.data_ptr(),
               n2.data_ptr(), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *nargs,
-              x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(), err.data_ptr(),
+              _ptr(o_next), x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(),
+              err.data_ptr(),
               ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps), _flags(M, stream),
               stream_ptr(dev))
     return xout

@@ -200,35 +200,42 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
                        const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream);
 
-/* The tail of one decode layer plus the next layer's first step, as ONE launch (M <= 8 rows):
+/* The tail of one decode layer plus the next layer's first steps, as ONE launch (M <= 8 rows):
  *   x1 = xin + int8_mm(o, wo, so)                      app/engine.py:206 (b.o with residual)
  *   mm = fp16(silu(a)) * b, a|b = int8_mm(rms(x1, n2), w13, s13)     :207-208 (krms, b.w13,
  *                                                                      _silu_mul)
  *   xout = x1 + int8_mm(mm, w2, s2)                    :209-210 (b.w2 with residual)
- *   and, unless wq is NULL (last layer), the next layer's ecd_rms_qkv_rope on xout with n1 /
- *   wq / sq (:189-192): q [M, Hq*HD], k/v into kc/vc [B, Hk, L, HD] at pos (row m -> m / S).
- * Same numerics as the per-op entry points.  wo / w13 / w2 / wq are ecd_pack_i8 copies (w13
- * interleaved, s13 interleaved the same way); o, xin, x1, mm, xout 16-byte aligned, row stride
- * D (mm: F).  xout must not alias xin, o, x1 or mm.  sync: a 4 KB, 256-byte aligned region,
- * zero before the first call, kept for later calls (the kernel leaves it reusable); calls
- * sharing a sync region must not overlap in time.  err: a 4-byte word set to 1 if a
- * workgroup waited longer than its bound for the others (results then undefined).  ws: a
- * 16-byte aligned workspace of D * 256 bytes (the K-split partial sums of w2 when the device has
- * four CUs per w2 tile; contents need not persist).  The grid
- * is one workgroup per CU with all workgroups resident; shapes are those accepted by
- * ecd_layer_tail_supported (ECD_ENOTSUP otherwise).  flags bit 1: nontemporal weight loads.
- * No reference counterpart as one call: it replaces five reference launches plus one. */
+ *   unless wq is NULL (last layer): the next layer's ecd_rms_qkv_rope on xout with n1 / wq / sq
+ *   (:189-192): q [M, Hq*HD], k/v into kc/vc [B, Hk, L, HD] at pos (row m -> m / S); and, when
+ *   o_next is not NULL, that layer's decode attention (ecd_decode_attn + ecd_attn_combine,
+ *   :194-204, scale 1/sqrt(HD)) into o_next [M, Hq * HD] -- for head_dim 128 with 3 or 4 query
+ *   heads per kv head (ecd_layer_tail_supported tells).
+ * Same numerics as the per-op entry points up to the fp32 summation order.  wo / w13 / w2 / wq
+ * are ecd_pack_i8 copies (w13 interleaved, s13 interleaved the same way); o, xin, x1, mm,
+ * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.
+ * sync: an 8 KB, 256-byte aligned region, zero before the first call, kept for later calls (the
+ * kernel leaves it reusable); calls sharing a sync region must not overlap in time.  err: a
+ * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results then
+ * undefined).  ws: a 16-byte aligned workspace of ecd_layer_tail_ws_bytes bytes (contents need
+ * not persist).  The grid is one workgroup per CU with all workgroups resident.  flags bit 1:
+ * nontemporal weight loads.  No reference counterpart as one call: it replaces up to seven
+ * reference launches. */
 int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
                    const void* n2, const void* w13, const void* s13, const void* w2,
                    const void* s2, const void* n1, const void* wq, const void* sq,
                    const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
-                   void* x1, void* mm, void* xout, void* sync, void* err, void* ws, int M,
-                   int D, int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
-                   void* stream);
+                   void* o_next, void* x1, void* mm, void* xout, void* sync, void* err,
+                   void* ws, int M, int D, int F, int S, int Hq, int Hk, int L, int HD,
+                   float eps, int flags, void* stream);
 
 /* ECD_OK when ecd_layer_tail accepts these shapes on the current device (M rows, model width
- * D, FFN width F, heads), ECD_ENOTSUP otherwise.  No reference counterpart. */
-int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD);
+ * D, FFN width F, heads, L cache slots; attention != 0: with the next layer's attention in the
+ * launch), ECD_ENOTSUP otherwise.  No reference counterpart. */
+int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD, int L, int attention);
+
+/* Bytes of the ecd_layer_tail workspace for these shapes on the current device.  No reference
+ * counterpart. */
+long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD);
 
 /* Prompt-pass GEMM (many rows) on packed weights: y = fp16(x @ fp16(q * s)^T) (+ res as an
  * fp16 add) -- the dense numerics of int8_mm for M > 16 (app/kernels.py:46-49), used by the

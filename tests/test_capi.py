@@ -112,14 +112,16 @@ def _taps(*offsets):
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 90, 30, 2, 62, 64, None),  # HD % 4
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 100, 30, 2, 64, 64, None),  # M % T
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 12, 16, 90, 30, 2, 64, 64, None),  # k align
-    lambda L: L.ecd_layer_tail(*([256] * 23), 9, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0,
+    lambda L: L.ecd_layer_tail(*([256] * 24), 9, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0,
                                None),                                           # M > 8
-    lambda L: L.ecd_layer_tail(*([256] * 21), None, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5,
+    lambda L: L.ecd_layer_tail(*([256] * 22), None, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5,
                                0, None),                                        # no err word
-    lambda L: L.ecd_layer_tail(*([256] * 20), 16, 256, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128,
+    lambda L: L.ecd_layer_tail(*([256] * 21), 16, 256, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128,
                                1e-5, 0, None),                                  # sync not 256-aligned
-    lambda L: L.ecd_layer_tail(*([256] * 23), 8, 3072, 8192, 1, 24, 7, 1024, 128, 1e-5, 0,
+    lambda L: L.ecd_layer_tail(*([256] * 24), 8, 3072, 8192, 1, 24, 7, 1024, 128, 1e-5, 0,
                                None),                                           # Hq % Hk
+    lambda L: L.ecd_layer_tail(*([256] * 10), None, *([256] * 6), 256, *([256] * 6), 8, 3072,
+                               8192, 1, 24, 8, 1024, 128, 1e-5, 0, None),       # o_next, no wq
 ])
 def test_host_argument_validation(call):
     """Invalid arguments return ECD_EINVAL before any HIP call (no GPU needed)."""
