@@ -109,10 +109,11 @@ __device__ __forceinline__ void attn_tile(SplitState<HD, G>& ss, float& m_run, f
   }
 }
 
-// The split [lo, hi) with its first tile already loaded (at lo) into ring[0].  RING tiles are
-// in flight: slot r holds tiles r, r + RING, ...; a slot is refilled as soon as its tile is
-// consumed, so the split costs about one memory round trip per RING tiles.
-template <int HD, int G, int RING>
+// The split [lo, hi) with its first tile already loaded (at lo) into ring[0] (PRE: the first
+// RING tiles already in ring[0 .. RING - 1]).  RING tiles are in flight: slot r holds tiles r,
+// r + RING, ...; a slot is refilled as soon as its tile is consumed, so the split costs about
+// one memory round trip per RING tiles.
+template <int HD, int G, int RING, bool PRE = false>
 __device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf)[HD / 32],
                                          KVTile<HD> (&ring)[RING], const f16* __restrict__ kb,
                                          const f16* __restrict__ vb, int lo, int hi, float scale,
@@ -130,7 +131,7 @@ __device__ __forceinline__ void attn_run(SplitState<HD, G>& ss, const f16x8 (&qf
   const int ntiles = hi > lo ? (hi - lo + 15) / 16 : 0;
 #pragma unroll
   for (int r = 1; r < RING; ++r)
-    if (r < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
+    if (!PRE && r < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
   for (int base = 0; base < ntiles; base += RING) {
 #pragma unroll
     for (int r = 0; r < RING; ++r) {
@@ -188,6 +189,145 @@ __device__ __forceinline__ void attn_store_o(const SplitState<HD, G>& ss, f16* d
       }
     }
   }
+}
+
+// ---- The same split with the P V product on MFMA.  The score MFMA leaves lane l holding
+// P[token 4 (l >> 4) + i][head l & 15], i = 0..3 -- the B operand of a 16x16x16 MFMA as it
+// stands -- and the V tile gives lane l the rows d = 128 j + 8 (l & 15) + b (b = 0..7) of tokens
+// 4 (l >> 4) + i, i.e. the A operand of V^T for the block of rows {128 j + 8 m + b : m < 16}.
+// So P V is 8 NDP MFMAs per tile with no lane exchange, and the sum over the tile's tokens
+// happens inside them.  acc[j][b] is that block's output: lane l holds rows
+// m = 4 (l >> 4) + i of head l & 15, i.e. d = 128 j + 8 (4 (l >> 4) + i) + b.
+template <int HD, int G>
+struct SplitStateM {
+  static constexpr int NDP = (HD + 127) / 128;
+  float m_run, l_run;  // head l & 15's running max and sum (equal in the four lane groups)
+  f32x4 acc[NDP][8];
+};
+
+template <int HD, int G>
+__device__ __forceinline__ void attn_tile_m(SplitStateM<HD, G>& ss, float& m_run, float& l_run,
+                                            const f16x8 (&qf)[HD / 32], KVTile<HD>& cur, int t0,
+                                            int hi, float scale, int lane) {
+  constexpr int NKC = HD / 32;
+  constexpr int NDP = KVTile<HD>::NDP;
+  const int grp = lane >> 4;
+  // V rows past the range contribute nothing (they may hold any bits, even NaN)
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr)
+    if (t0 + 4 * grp + rr >= hi)
+#pragma unroll
+      for (int j = 0; j < NDP; ++j) cur.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  f32x4 st = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NKC; ++i) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[i], qf[i], st, 0, 0, 0);
+
+  float sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int t = t0 + 4 * grp + rr;
+    sc[rr] = (t < hi) ? st[rr] * scale : -INFINITY;
+    mx = fmaxf(mx, sc[rr]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx);
+  const float alpha = __expf(m_run - m_new);
+  float pr[4];
+  float ps = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    pr[rr] = __expf(sc[rr] - m_new);
+    ps += pr[rr];
+  }
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  l_run = l_run * alpha + ps;
+  m_run = m_new;
+
+  const f16x4 pb = (f16x4){(f16)pr[0], (f16)pr[1], (f16)pr[2], (f16)pr[3]};
+#pragma unroll
+  for (int j = 0; j < NDP; ++j)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const f16x4 va = (f16x4){cur.v[0][j][b], cur.v[1][j][b], cur.v[2][j][b], cur.v[3][j][b]};
+      ss.acc[j][b] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, ss.acc[j][b] * alpha, 0, 0, 0);
+    }
+}
+
+// attn_run with the MFMA P V product (same ring of tiles; PRE: the first RING tiles already in
+// ring[0 .. RING - 1], else only ring[0]).
+template <int HD, int G, int RING, bool PRE = false>
+__device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                           KVTile<HD> (&ring)[RING], const f16* __restrict__ kb,
+                                           const f16* __restrict__ vb, int lo, int hi, float scale,
+                                           int lane) {
+  constexpr int NDP = SplitStateM<HD, G>::NDP;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+#pragma unroll
+  for (int j = 0; j < NDP; ++j)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) ss.acc[j][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int ntiles = hi > lo ? (hi - lo + 15) / 16 : 0;
+#pragma unroll
+  for (int r = 1; r < RING; ++r)
+    if (!PRE && r < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
+  for (int base = 0; base < ntiles; base += RING) {
+#pragma unroll
+    for (int r = 0; r < RING; ++r) {
+      const int i = base + r;
+      if (i < ntiles) {
+        attn_tile_m<HD, G>(ss, m_run, l_run, qf, ring[r], lo + 16 * i, hi, scale, lane);
+        if (i + RING < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
+      }
+    }
+  }
+  ss.m_run = m_run;
+  ss.l_run = l_run;
+}
+
+// Head g's normalised output o = acc / l as fp16 to dst[g * HD + d] (lanes of heads < G).
+template <int HD, int G>
+__device__ __forceinline__ void attn_store_o_m(const SplitStateM<HD, G>& ss, f16* dst, int lane) {
+  const int n = lane & 15, grp = lane >> 4;
+  if (n >= G) return;
+#pragma unroll
+  for (int j = 0; j < SplitStateM<HD, G>::NDP; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 128 * j + 8 * (4 * grp + i);
+      if (d0 < HD) {
+        f16x8 ov;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) ov[b] = (f16)(ss.acc[j][b][i] / ss.l_run);
+        *(f16x8*)(dst + n * HD + d0) = ov;
+      }
+    }
+}
+
+// Head g's unnormalised partial [m, l, acc[HD]] to p[g * PW ...] (PW >= HD + 2, even).
+template <int HD, int G>
+__device__ __forceinline__ void attn_store_partial_m(const SplitStateM<HD, G>& ss, float* p,
+                                                     int PW, int lane) {
+  const int n = lane & 15, grp = lane >> 4;
+  if (n >= G) return;
+  float* q = p + n * PW;
+  if (grp == 0) {
+    q[0] = ss.m_run;
+    q[1] = ss.l_run;
+  }
+#pragma unroll
+  for (int j = 0; j < SplitStateM<HD, G>::NDP; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 128 * j + 8 * (4 * grp + i);
+      if (d0 < HD)
+#pragma unroll
+        for (int b = 0; b < 8; b += 2)
+          *(float2*)(q + 2 + d0 + b) = make_float2(ss.acc[j][b][i], ss.acc[j][b + 1][i]);
+    }
 }
 
 // Attended length of row r and the [lo, hi) token range of split sp (app/kernels.py:120-127).

@@ -424,58 +424,116 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // S splits); the loader merges its 8 waves' partials (log-sum-exp) into one per workgroup, and
 // the last of the pair's KB workgroups merges those and writes o.  Same arithmetic as the
 // split-combine kernel, summed in two levels.
-template <int HD, int G>
-__device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int NB, int b,
-                                                int wv, int lane) {
-  constexpr int NDP = SplitState<HD, G>::NDP;
-  constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
-  const int M = a.M, Hq = a.Hq, Hk = a.Hk, L = a.L;
-  const int pairs = M * Hk;
-  bar();  // X(ATT): q and the new cache slots are complete
+// One wave's attention split; ring[0] holds its first K/V tile, read before the launch's new
+// cache slots exist (the other RING - 1 tiles go out after the gate: the registers of the
+// 9-wave workgroup hold one tile across the gate).
+template <int HD, int RING>
+struct AttPre {
+  KVTile<HD> ring[RING];
+  long cbase;    // this pair's cache [L, HD] (K and V alike)
+  int r, kh;     // row and kv head of the pair
+  int lo, hi;    // the split's tokens
+  int lim;       // last token the early reads touched (lo - 1: none)
+  bool on;       // this wave runs a split
+};
+
+// Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair
+// blockIdx / KB, split (blockIdx % KB) * 8 + wave of 8 KB -- and its first tile.  With one
+// row per cache (S == 1) every slot below pos[r] is final before the launch, so token indices
+// clamp to min(hi - 1, pos[r] - 1) and no line of the slot this launch writes is read; with
+// several rows per cache (their new slots fall inside each other's ranges) nothing is read early.
+template <int HD, int RING>
+__device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int wv, int lane,
+                                             AttPre<HD, RING>& pf) {
+  const int Hk = a.Hk, L = a.L;
+  const int pairs = a.M * Hk;
+  int p, ns, sp;
   if (L <= ATT_SHORT) {
-    const int p = b + NB * wv;
-    if (p < pairs) {
-      const int r = p / Hk, kh = p - r * Hk;
-      const long cbase = ((long)(r / a.S) * Hk + kh) * (long)L * HD;
-      f16x8 qf[HD / 32];
-      load_q<HD, G>(qf, a.q, r, Hq, kh, lane);
-      int lo, hi;
-      split_range(a.pos, r, L, 1, 0, lo, hi);
-      SplitState<HD, G> ss;
-      attn_split<HD, G, 1>(ss, qf, a.kc + cbase, a.vc + cbase, lo, hi, a.scale, lane);
-      attn_store_o<HD, G>(ss, a.o_next + ((long)r * Hq + kh * G) * HD, lane);
+    p = b + NB * wv;
+    ns = 1;
+    sp = 0;
+  } else {
+    const int KB = NB / pairs;
+    p = b / KB;
+    ns = KB * CW;
+    sp = (b - p * KB) * CW + wv;
+  }
+  pf.on = p < pairs;
+  pf.lo = pf.hi = 0;
+  pf.lim = -1;
+  if (!pf.on) return;
+  pf.r = p / Hk;
+  pf.kh = p - pf.r * Hk;
+  pf.cbase = ((long)(pf.r / a.S) * Hk + pf.kh) * (long)L * HD;
+  split_range(a.pos, pf.r, L, ns, sp, pf.lo, pf.hi);
+  const long praw = a.pos[pf.r];
+  const int pn = (praw >= 0 && praw < L) ? (int)praw : L;  // the slot written here (L: none)
+  pf.lim = a.S == 1 ? min(pf.hi - 1, pn - 1) : pf.lo - 1;
+  if (pf.lo <= pf.lim) kv_load<HD>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.lim, lane);
+}
+
+// After the gate: a first tile not read early is loaded now; otherwise the lanes holding its
+// tokens in (lim, hi - 1] load those (plain loads: no line of theirs was read in this launch).
+template <int HD, int RING>
+__device__ __forceinline__ void att_complete(AttPre<HD, RING>& pf, const f16* kb, const f16* vb,
+                                             int lane) {
+  constexpr int NKC = KVTile<HD>::NKC, NDP = KVTile<HD>::NDP;
+  const int row = lane & 15, grp = lane >> 4;
+  const int t0 = pf.lo;
+  if (pf.hi <= t0) return;
+  if (t0 > pf.lim) {
+    kv_load<HD>(pf.ring[0], kb, vb, t0, pf.hi - 1, lane);
+    return;
+  }
+  if (pf.lim >= pf.hi - 1 || t0 + 15 <= pf.lim) return;
+  const int tk = t0 + row;
+  if (tk > pf.lim && tk < pf.hi) {
+    const f16* kp = kb + (long)tk * HD + 8 * grp;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) pf.ring[0].k[c] = *(const f16x8*)(kp + 32 * c);
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int tv = t0 + 4 * grp + rr;
+    if (tv > pf.lim && tv < pf.hi) {
+      const f16* vp = vb + (long)tv * HD + 8 * row;
+#pragma unroll
+      for (int j = 0; j < NDP; ++j)
+        if (8 * (row + 16 * j) < HD) pf.ring[0].v[rr][j] = *(const f16x8*)(vp + 128 * j);
     }
+  }
+}
+
+// Decode attention of app/kernels.py:111-167 for the M rows, their kv heads and the query heads
+// of each (G = Hq / Hk), over cache slots [0, pos[r]], with the per-split core of the decode
+// kernel (attn_core.h), on the splits att_prefetch assigned.  Short caches: the pair's one wave
+// writes o directly.  Long caches: the loader merges its 8 waves' partials (log-sum-exp) into
+// one per workgroup, and the last of the pair's KB workgroups merges those and writes o.  Same
+// arithmetic as the split-combine kernel, summed in two levels.
+template <int HD, int G, int RING>
+__device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
+                                                int lane, AttPre<HD, RING>& pf) {
+  constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
+  const int Hq = a.Hq;
+  bar();  // X(ATT): q and the new cache slots are complete
+  if (!pf.on) {
     bar();  // P(ATT)
     return;
   }
-  const int KB = NB / pairs;
-  const int p = b / KB, kq = b - p * KB;
-  const int r = p / Hk, kh = p - r * Hk;
-  const long cbase = ((long)(r / a.S) * Hk + kh) * (long)L * HD;
+  const f16* kb = a.kc + pf.cbase;
+  const f16* vb = a.vc + pf.cbase;
   f16x8 qf[HD / 32];
-  load_q<HD, G>(qf, a.q, r, Hq, kh, lane);
-  int lo, hi;
-  split_range(a.pos, r, L, KB * CW, kq * CW + wv, lo, hi);
-  SplitState<HD, G> ss;
-  // two K/V tiles in flight where the register budget of the 9-wave workgroup allows it
-  attn_split<HD, G, (G <= 3 ? 2 : 1)>(ss, qf, a.kc + cbase, a.vc + cbase, lo, hi, a.scale, lane);
+  load_q<HD, G>(qf, a.q, pf.r, Hq, pf.kh, lane);
+  att_complete<HD, RING>(pf, kb, vb, lane);
+  SplitStateM<HD, G> ss;
+  attn_run_m<HD, G, RING>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
+  if (a.L <= ATT_SHORT) {
+    attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
+    bar();  // P(ATT)
+    return;
+  }
   // this wave's partial -> LDS [wave][g][m, l, acc]
-  float* pp = (float*)smem + wv * G * PW;
-  if (lane < G) {
-    pp[lane * PW] = ss.m_run;
-    pp[lane * PW + 1] = ss.l_run;
-  }
-  if (lane < 16) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < NDP; ++j) {
-        const int d = 8 * (lane + 16 * j);
-        if (d < HD)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pp[g * PW + 2 + d + e] = ss.acc[g][j][e];
-      }
-  }
+  attn_store_partial_m<HD, G>(ss, (float*)smem + wv * G * PW, PW, lane);
   wait_lgkm0();
   bar();  // P(ATT)
 }
@@ -621,6 +679,10 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
   if (wv < CW) {
     // ------------------------------------------------------------------ compute waves
+    // attention splits: two K/V tiles in flight after the gate where the register budget
+    // allows it (G <= 3)
+    constexpr int ARING = AG <= 3 ? 2 : 1;
+    AttPre<(AHD > 0 ? AHD : 32), ARING> pf;
     const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
     // this wave's slice of the attention output first (the inputs of this launch are final)
     dma_rows<CD>(a.o, D, M, c0D, xs, lane);
@@ -719,9 +781,14 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       put_partials<2>(psD, acc, wv, lane);
       wait_lgkm0();
       bar();  // P(QKV)
+      // the next layer's first K/V tiles go out into the registers the q|k|v phase leaves
+      // free, while the epilogue and the last gate run
+      if constexpr (AHD > 0) {
+        if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+      }
     }
     if constexpr (AHD > 0) {
-      if (att) attention_phase<AHD, AG>(a, smem, NB, b, wv, lane);
+      if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf);
     }
     return;
   }
