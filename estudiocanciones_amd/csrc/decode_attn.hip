@@ -13,9 +13,11 @@
 //                        loads 16 contiguous bytes of token t0 + (l & 15)), Q^T the B operand
 //                        (query head g = l & 15, zero for g >= G), so lane l ends holding
 //                        scores of tokens t0 + 4 (l >> 4) + r, r = 0..3, for head l & 15;
-//   P.V on the VALU:     lane l owns the d-chunk 8 (l & 15) .. +8 (plus 128-wide repeats)
-//                        and the token phase l >> 4; the probabilities it needs live in
-//                        the same 16-lane row and arrive through lane shuffles.
+//   O^T += V^T . P       on v_mfma_f32_16x16x16_f16: the scores' lane layout is the B operand
+//                        as it stands, and lane l's V rows (d-chunk 8 (l & 15) .. +8 of tokens
+//                        t0 + 4 (l >> 4) + r) are the A operand of V^T for the output rows
+//                        d = 8 m + b, one MFMA per b (plus 128-wide repeats): no lane exchange,
+//                        the tile's 16 tokens are summed inside the MFMA.
 // Each K and V byte of the attended range is read once per (row, kv head): the G query
 // heads of a group share it (no repeat_kv copy).
 #include <mutex>
@@ -35,9 +37,9 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
     int nsplit) {
   static_assert(HD % 32 == 0 && HD <= 512, "head_dim must be a multiple of 32");
   static_assert(G >= 1 && G <= 16, "query heads per kv head must be 1..16");
-  constexpr int NDP = SplitState<HD, G>::NDP;
+  constexpr int NDP = SplitStateM<HD, G>::NDP;
   const int lane = threadIdx.x;
-  const int row = lane & 15;
+  const int n = lane & 15;  // query head of this lane's outputs
   const int grp = lane >> 4;
   const int sp = blockIdx.x, kh = blockIdx.y, r = blockIdx.z;
   const int b = r / S;
@@ -51,33 +53,30 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
   int lo, hi;
   split_range(pos, r, L, nsplit, sp, lo, hi);
   if (nsplit != 1 && lo < hi) kv_load<HD>(ring[0], kc + cbase, vc + cbase, lo, hi - 1, lane);
-  SplitState<HD, G> ss;
-  attn_run<HD, G, attn_ring(HD)>(ss, qf, ring, kc + cbase, vc + cbase, lo, hi, scale, lane);
+  SplitStateM<HD, G> ss;
+  attn_run_m<HD, G, attn_ring(HD)>(ss, qf, ring, kc + cbase, vc + cbase, lo, hi, scale, lane);
 
   const long hbase = (long)r * Hq + kh * G;
   if (nsplit == 1) {
-    attn_store_o<HD, G>(ss, o + hbase * HD, lane);
-  } else {
-    if (lane < G) {
-      const long pidx = (hbase + lane) * nsplit + sp;
+    attn_store_o_m<HD, G>(ss, o + hbase * HD, lane);
+  } else if (n < G) {
+    // head n's partial: lane (n, grp) holds d = 128 j + 8 (4 grp + i) + b, b = 0..7
+    const long pidx = (hbase + n) * nsplit + sp;
+    if (grp == 0) {
       pm[pidx] = ss.m_run;
       pl[pidx] = ss.l_run;
     }
-    if (grp == 0) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const long pidx = (hbase + g) * nsplit + sp;
+    for (int j = 0; j < NDP; ++j)
 #pragma unroll
-        for (int j = 0; j < NDP; ++j) {
-          const int d = 8 * (row + 16 * j);
-          if (d < HD) {
-            float* dst = pa + pidx * HD + d;
-            *(f32x4*)dst = (f32x4){ss.acc[g][j][0], ss.acc[g][j][1], ss.acc[g][j][2], ss.acc[g][j][3]};
-            *(f32x4*)(dst + 4) = (f32x4){ss.acc[g][j][4], ss.acc[g][j][5], ss.acc[g][j][6], ss.acc[g][j][7]};
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 128 * j + 8 * (4 * grp + i);
+        if (d0 < HD) {
+          float* dst = pa + pidx * HD + d0;
+          *(f32x4*)dst = (f32x4){ss.acc[j][0][i], ss.acc[j][1][i], ss.acc[j][2][i], ss.acc[j][3][i]};
+          *(f32x4*)(dst + 4) = (f32x4){ss.acc[j][4][i], ss.acc[j][5][i], ss.acc[j][6][i], ss.acc[j][7][i]};
         }
       }
-    }
   }
 }
 
