@@ -645,7 +645,7 @@ __device__ __forceinline__ void attention_merge(const Args& a, unsigned char* sm
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  constexpr int LA = 8;        // weight loads in flight per compute wave (paced issue)
+  constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
   constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
