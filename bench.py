@@ -74,6 +74,9 @@ def parse():
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter_collection.csv files and exit")
+    ap.add_argument("--pmc-gemm-summary", metavar="CSV",
+                    help="summarise the prompt GEMM's MFMA / VALU counters of one rocprofv3 --pmc "
+                         "counter_collection.csv and exit")
     return ap.parse_args()
 
 
@@ -147,6 +150,43 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
                     "bytes_per_tail_launch": int(kib * 1024 / factor)}
     out["traffic_bytes_per_launch"] = out["fetch"]["bytes_per_tail_launch"] + \
         out["write"]["bytes_per_tail_launch"]
+    return out
+
+
+def pmc_gemm_summary(path):
+    """Per prompt-GEMM variant (gemm_i8p_kernel, by kernel name and grid): dispatches, MFMA and
+    VALU instructions per dispatch, VALU per MFMA, LDS instructions, f16 MFMA FLOP, and the
+    derived MfmaUtil (MFMA-busy cycles over GPU-active cycles x SIMDs, %) and VALUBusy (%)."""
+    import csv
+    disp = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if "gemm_i8p_kernel" not in r["Kernel_Name"]:
+                continue
+            d = disp.setdefault(r["Dispatch_Id"], {"name": r["Kernel_Name"],
+                                                   "grid": r.get("Grid_Size", "")})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    if not disp:
+        raise SystemExit(f"{path}: no gemm_i8p_kernel dispatches")
+    groups = {}
+    for d in disp.values():
+        groups.setdefault((d["name"], d["grid"]), []).append(d)
+    out = []
+    for (name, grid), ds in sorted(groups.items(), key=lambda kv: -len(kv[1])):
+        def avg(c):
+            v = [d[c] for d in ds if c in d]
+            return sum(v) / len(v) if v else None
+        mfma, valu = avg("SQ_INSTS_MFMA"), avg("SQ_INSTS_VALU")
+        mops = avg("SQ_INSTS_VALU_MFMA_MOPS_F16")
+        out.append({
+            "kernel": name.split("(")[0], "grid": grid, "dispatches": len(ds),
+            "mfma_insts": mfma, "valu_insts": valu,
+            "valu_per_mfma": round(valu / mfma, 2) if mfma and valu else None,
+            "lds_insts": avg("SQ_INSTS_LDS"),
+            "mfma_f16_flop": mops * 512 if mops is not None else None,
+            "MfmaUtil_pct": round(avg("MfmaUtil"), 2) if avg("MfmaUtil") is not None else None,
+            "VALUBusy_pct": round(avg("VALUBusy"), 2) if avg("VALUBusy") is not None else None,
+        })
     return out
 
 
@@ -320,6 +360,9 @@ def main():
     args = parse()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calib_mib or 256), indent=1))
+        return
+    if args.pmc_gemm_summary:
+        print(json.dumps(pmc_gemm_summary(args.pmc_gemm_summary), indent=1))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the decode path has no "

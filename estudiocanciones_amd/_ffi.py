@@ -60,6 +60,8 @@ SIGNATURES = {
                             _P, c_int, _P],
     "ecd_gemm_i8p": [_P, c_long, _P, _P, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],
     "ecd_gemm_i8p_silu": [_P, c_long, _P, _P, _P, c_long, c_int, c_int, c_int, _P],
+    "ecd_gemm_i8p_rope": [_P, c_long, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int,
+                          c_int, c_int, c_int, _P],
     "ecd_prefill_attn": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P],
     "ecd_pack_f16": [_P, c_int, c_int, c_int, _P, _P],
     "ecd_gemm_f16p": [_P, c_long, _P, _P, c_float, _P, c_long, _P, c_long, c_int, c_int, c_int, _P],

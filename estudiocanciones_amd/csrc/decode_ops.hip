@@ -34,6 +34,43 @@ __global__ __launch_bounds__(BLOCK) void rmsnorm_kernel(const f16* __restrict__ 
   }
 }
 
+// The same RMSNorm, one wave per row for D = 512 NV: each lane holds 8 NV elements (NV 16-byte
+// loads), so the row is read once, and the sum of squares is one wave reduction (the fp32
+// summation order differs from rmsnorm_kernel's; the rounding points do not).
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const f16* __restrict__ x, long ldx,
+                                                           const f16* __restrict__ w,
+                                                           f16* __restrict__ y, long ldy, int R,
+                                                           float eps) {
+  const int lane = threadIdx.x & 63;
+  const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const f16x8* xr = (const f16x8*)(x + r * ldx);
+  f16x8 v[NV], wv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = xr[lane + 64 * i];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) wv[i] = ((const f16x8*)w)[lane + 64 * i];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = (float)v[i][e];
+      ss += f * f;
+    }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)(512 * NV) + eps);
+  f16x8* yr = (f16x8*)(y + r * ldy);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (f16)((float)v[i][e] * inv);
+    yr[lane + 64 * i] = h * wv[i];
+  }
+}
+
 // ---------------------------------------------------------------- RoPE + KV-cache write
 // One block per row r (batch b = r / S, position p = pos[r]).  Interleaved pairs
 // (x[2i], x[2i+1]) are rotated by the table entry rope[p, i] = (cos, sin); q heads go to
@@ -250,8 +287,22 @@ extern "C" {
 int ecd_rmsnorm(const void* x, long ldx, const void* w, void* y, long ldy, int R, int D,
                 float eps, void* stream) {
   if (!x || !w || !y || R <= 0 || D <= 0 || ldx < D || ldy < D) return ECD_EINVAL;
-  hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(R), dim3(256), 0, (hipStream_t)stream,
-                     (const f16*)x, ldx, (const f16*)w, (f16*)y, ldy, D, eps);
+  const bool vec = (D % 512) == 0 && (ldx % 8) == 0 && (ldy % 8) == 0 &&
+                   (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w) & 15) == 0;
+  const dim3 g4((unsigned)((R + 3) / 4));
+  hipStream_t st = (hipStream_t)stream;
+  const f16 *xh = (const f16*)x, *wh = (const f16*)w;
+  f16* yh = (f16*)y;
+  switch (vec ? D / 512 : 0) {
+    case 1: hipLaunchKernelGGL(rmsnorm_wave_kernel<1>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    case 2: hipLaunchKernelGGL(rmsnorm_wave_kernel<2>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    case 3: hipLaunchKernelGGL(rmsnorm_wave_kernel<3>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    case 4: hipLaunchKernelGGL(rmsnorm_wave_kernel<4>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    case 6: hipLaunchKernelGGL(rmsnorm_wave_kernel<6>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    case 8: hipLaunchKernelGGL(rmsnorm_wave_kernel<8>, g4, dim3(256), 0, st, xh, ldx, wh, yh, ldy, R, eps); break;
+    default:
+      hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(R), dim3(256), 0, st, xh, ldx, wh, yh, ldy, D, eps);
+  }
   return ecd_launch_status();
 }
 

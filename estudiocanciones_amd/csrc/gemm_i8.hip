@@ -2,7 +2,11 @@
 // many rows (app/kernels.py:46-49: dequantise, then GEMM):
 //   y[m, n] = fp16( sum_k x[m, k] * fp16(q[n, k] * s[n]) )      fp32 accumulation
 //   EPI_STORE: y (+ res as an fp16 add);  EPI_SILU: rows interleaved (w1 row j at 2j, w3 row j
-//   at 2j + 1), mm[m, j] = fp16(fp16(silu(y[m, 2j])) * y[m, 2j + 1]) (app/kernels.py:171-180).
+//   at 2j + 1), mm[m, j] = fp16(fp16(silu(y[m, 2j])) * y[m, 2j + 1]) (app/kernels.py:171-180);
+//   EPI_ROPE: y is the q | k | v projection; the interleaved pairs of the q and k heads are
+//   rotated by the RoPE table at the row's position and q goes to its buffer, k and v into the
+//   cache slot (app/kernels.py:78-107: the same fp16 input, fp32 rotation and rounding as the
+//   rope_kv kernel).
 //
 // Weights use the lane-ordered packed layout of gemv_fused.hip: chunk (tile, c) = 16 rows x
 // 64 bytes stored so that lane l's 16 bytes are row l & 15, k = 64c + 16 (l >> 4) .. +15.  The
@@ -33,7 +37,18 @@
 
 namespace ecd {
 
-enum { GEPI_STORE = 0, GEPI_SILU = 1 };
+enum { GEPI_STORE = 0, GEPI_SILU = 1, GEPI_ROPE = 2 };
+
+// Operands of the RoPE + cache-write epilogue: row m is batch item m / S at position pos[m];
+// rope [L, HD] fp32 holds (cos, sin) of pair i at columns 2i, 2i + 1.
+struct RopeOut {
+  const float* rope;
+  const int64_t* pos;
+  f16* q;   // [M, Hq * HD]
+  f16* kc;  // [B, Hk, L, HD]
+  f16* vc;
+  int S, Hq, Hk, L, HD;
+};
 
 constexpr int GT_N = 128;   // output features per block
 constexpr int GT_M = 128;   // rows per block
@@ -43,7 +58,7 @@ template <int EPI, bool RM>
 __global__ __launch_bounds__(256) void gemm_i8p_kernel(
     const f16* __restrict__ x, long ldx, const int8_t* __restrict__ wp,
     const f16* __restrict__ s, const f16* __restrict__ res, long ldr, f16* __restrict__ y, long ldy, int M, int N, int K,
-    int nfb, int nmb) {
+    int nfb, int nmb, RopeOut ro) {
   constexpr int WB = 1024;  // bytes of one (tile, chunk) of packed weights
   __shared__ __align__(16) int8_t lw[GT_NS][8 * WB];
   __shared__ __align__(16) f16 lx[GT_NS][GT_M * 64];
@@ -146,6 +161,8 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
   for (int rt = 0; rt < 8; ++rt) {
     const int m = m0 + rt * 16 + (lane & 15);
     if (m >= M) continue;
+    long p_raw = 0;
+    if (EPI == GEPI_ROPE) p_raw = ro.pos[m];
 #pragma unroll
     for (int ft = 0; ft < 2; ++ft) {
       const int nb = n0 + (wv * 2 + ft) * 16 + 4 * (lane >> 4);
@@ -167,6 +184,27 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
             }
           }
         }
+      } else if (EPI == GEPI_ROPE) {  // HD % 4 == 0: the 4 features lie in one head
+        const int h = nb / ro.HD, d = nb - h * ro.HD;
+        const bool pval = p_raw >= 0 && p_raw < ro.L;
+        const long p = p_raw < 0 ? 0 : (p_raw >= ro.L ? ro.L - 1 : p_raw);
+        f16x4 o = yv;
+        if (h < ro.Hq + ro.Hk) {
+          const f32x4 cs = *(const f32x4*)(ro.rope + p * ro.HD + d);
+          const float x0 = (float)yv[0], x1 = (float)yv[1], x2 = (float)yv[2], x3 = (float)yv[3];
+          o[0] = (f16)(x0 * cs[0] - x1 * cs[1]);
+          o[1] = (f16)(x1 * cs[0] + x0 * cs[1]);
+          o[2] = (f16)(x2 * cs[2] - x3 * cs[3]);
+          o[3] = (f16)(x3 * cs[2] + x2 * cs[3]);
+        }
+        if (h < ro.Hq) {
+          *(f16x4*)(ro.q + ((long)m * ro.Hq + h) * ro.HD + d) = o;
+        } else if (pval) {
+          const int b = m / ro.S;
+          const int kh = h < ro.Hq + ro.Hk ? h - ro.Hq : h - ro.Hq - ro.Hk;
+          f16* dst = h < ro.Hq + ro.Hk ? ro.kc : ro.vc;
+          *(f16x4*)(dst + (((long)b * ro.Hk + kh) * ro.L + p) * ro.HD + d) = o;
+        }
       } else {  // (a_j, b_j, a_j+1, b_j+1) with j = nb / 2; N even
         const int j = nb >> 1;
         const float a0 = (float)yv[0], a1 = (float)yv[2];
@@ -181,13 +219,14 @@ __global__ __launch_bounds__(256) void gemm_i8p_kernel(
 
 template <int EPI, bool RM = false>
 static int launch_gemm(const f16* x, long ldx, const int8_t* wp, const f16* s, const f16* res,
-                       long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st) {
+                       long ldr, f16* y, long ldy, int M, int N, int K, hipStream_t st,
+                       RopeOut ro = RopeOut{}) {
   const int nfb = (N + GT_N - 1) / GT_N;
   const int nmb = (M + GT_M - 1) / GT_M;
   const long blocks = (long)((nfb + 7) / 8) * 8 * nmb;
   if (blocks > 0x7FFFFFFFL) return ECD_ENOTSUP;
   hipLaunchKernelGGL((gemm_i8p_kernel<EPI, RM>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
-                     wp, s, res, ldr, y, ldy, M, N, K, nfb, nmb);
+                     wp, s, res, ldr, y, ldy, M, N, K, nfb, nmb, ro);
   return ecd_launch_status();
 }
 
@@ -221,6 +260,20 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
   if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
   return launch_gemm<GEPI_STORE>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s,
                                  (const f16*)res, ldr, (f16*)y, ldy, M, N, K, (hipStream_t)stream);
+}
+
+int ecd_gemm_i8p_rope(const void* x, long ldx, const void* wp, const void* s, const float* rope,
+                      const int64_t* pos, void* q, void* kc, void* vc, int M, int S, int Hq,
+                      int Hk, int L, int HD, int K, void* stream) {
+  if (!x || !wp || !s || !rope || !pos || !q || !kc || !vc || M <= 0 || S <= 0 || Hq <= 0 ||
+      Hk <= 0 || (Hq % Hk) || L <= 0 || HD <= 0 || (HD % 4) || K <= 0 || (K % 64) || ldx < K ||
+      (ldx % 8) || !al16(x) || !al16(wp) || ((uintptr_t)q & 7) || ((uintptr_t)kc & 7) ||
+      ((uintptr_t)vc & 7) || ((uintptr_t)rope & 15))
+    return ECD_EINVAL;
+  if (!x_offsets_fit(M, ldx)) return ECD_ENOTSUP;
+  const RopeOut ro{rope, pos, (f16*)q, (f16*)kc, (f16*)vc, S, Hq, Hk, L, HD};
+  return launch_gemm<GEPI_ROPE>((const f16*)x, ldx, (const int8_t*)wp, (const f16*)s, nullptr, 0,
+                                nullptr, 0, M, (Hq + 2 * Hk) * HD, K, (hipStream_t)stream, ro);
 }
 
 int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,

@@ -34,7 +34,7 @@ import torch
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
                       gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
-                      gemv_packed, int8_mm, layer_tail, layer_tail_supported,
+                      gemm_rope_packed, gemv_packed, int8_mm, layer_tail, layer_tail_supported,
                       layer_tail_ws_bytes, next_power_of_2,
                       pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_w13_silu,
                       sample_topk, stream_ptr)
@@ -278,10 +278,15 @@ class Stack:
         R = x.shape[0]
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
-            qkv = gemm_packed(krms(x, b.n1), b.qkv.qp, b.qkv.sp, b.qkv.N, b.qkv.K)
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
-            _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
-                                      HD=HD, HALF=next_power_of_2(HD // 2))
+            if HD % 4 == 0:
+                # q | k | v GEMM with RoPE and the cache write in its epilogue
+                gemm_rope_packed(krms(x, b.n1), b.qkv.qp, b.qkv.sp, self.rope, pos, q, b.kc,
+                                 b.vc, S, Hq, Hk, L, HD, b.qkv.K)
+            else:
+                qkv = gemm_packed(krms(x, b.n1), b.qkv.qp, b.qkv.sp, b.qkv.N, b.qkv.K)
+                _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
+                                          HD=HD, HALF=next_power_of_2(HD // 2))
             if HD == 128 and Hq // Hk <= 4:
                 # causal flash attention on MFMA: each K/V tile is read once per 64-row block
                 o = prefill_attn(q, b.kc, b.vc, pos, S, Hq, Hk)

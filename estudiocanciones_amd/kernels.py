@@ -368,6 +368,30 @@ def gemm_silu_packed(x, wp, s, F, K):
     return mm
 
 
+def gemm_rope_packed(x, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, K):
+    """int8_mm(x, wq|wk|wv, s) followed by _rope_cache (app/kernels.py:78-107) in one launch:
+    the q | k | v GEMM of many rows with RoPE and the cache write in its epilogue.  pos [M] int64
+    (row m -> batch item m // S); writes q [M, Hq * HD] and the cache slots of kc / vc."""
+    _check_x(x, K, "gemm_rope_packed")
+    M = x.shape[0]
+    for t, nm in ((q, "q"), (kc, "kc"), (vc, "vc")):
+        _f16(t, f"gemm_rope_packed {nm}")
+        if not t.is_contiguous():
+            raise ValueError(f"gemm_rope_packed: {nm} must be contiguous")
+    if q.shape != (M, Hq * HD):
+        raise ValueError("gemm_rope_packed: q must be [M, Hq * HD]")
+    if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+        raise ValueError("gemm_rope_packed: pos must be a contiguous int64 vector of M rows")
+    if rope.dtype != torch.float32 or not rope.is_contiguous() or rope.numel() < L * HD:
+        raise ValueError("gemm_rope_packed: rope must be a contiguous fp32 [L, HD] table")
+    if kc.shape[1:] != (Hk, L, HD) or vc.shape != kc.shape or kc.shape[0] * S < M:
+        raise ValueError("gemm_rope_packed: kc / vc must be [B, Hk, L, HD] with B * S >= M")
+    _ffi.call("ecd_gemm_i8p_rope", x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(),
+              rope.data_ptr(), pos.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), M, S,
+              Hq, Hk, L, HD, K, stream_ptr(x.device))
+    return q
+
+
 def pack_f16(w: torch.Tensor, interleave: bool = False) -> torch.Tensor:
     """Lane-ordered 16 x 64 tile layout (2 KB tiles) of an fp16 [N, K] matrix (K % 64 == 0) for
     the fp16-weight GEMM; ``interleave`` row-interleaves the two halves (gate | up -> pairs)."""

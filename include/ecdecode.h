@@ -252,6 +252,18 @@ int ecd_gemm_i8p(const void* x, long ldx, const void* wp, const void* s, const v
 int ecd_gemm_i8p_silu(const void* x, long ldx, const void* wp, const void* s, void* mm,
                       long ldm, int M, int F, int K, void* stream);
 
+/* The same GEMM on the packed q | k | v projection (N = (Hq + 2 Hk) * HD) with the RoPE +
+ * KV-cache write of app/kernels.py:78-107 in its epilogue (replaces int8_mm + _rope_cache in
+ * the prompt pass, app/engine.py:123-153): y = fp16(x @ fp16(q * s)^T) as ecd_gemm_i8p, then
+ * row m (batch item m / S, position pos[m]) rotates the interleaved pairs of its q and k heads
+ * by rope[p] (fp32, rounded to fp16; p = pos[m] clamped into [0, L)) and writes q [M, Hq * HD],
+ * and k, v into kc / vc [B, Hk, L, HD] at slot pos[m] when 0 <= pos[m] < L -- the outputs of
+ * ecd_rope_kv_write on the GEMM's output.  HD % 4 == 0; rope 16-byte aligned; q, kc, vc 8-byte
+ * aligned. */
+int ecd_gemm_i8p_rope(const void* x, long ldx, const void* wp, const void* s, const float* rope,
+                      const int64_t* pos, void* q, void* kc, void* vc, int M, int S, int Hq,
+                      int Hk, int L, int HD, int K, void* stream);
+
 /* fp16-weight GEMM of the codec's flow-matching estimator (the dense nn.Linear / Conv1d-as-GEMM
  * layers of app/heartcodec/models/transformer.py; torch's F.linear numerics: fp32 accumulation,
  * fp32 bias, one fp16 rounding).  Weights are packed once with ecd_pack_f16 into lane-ordered

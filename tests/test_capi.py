@@ -150,6 +150,31 @@ def test_gemm_rejects_x_beyond_32bit_offsets():
     # M = 2^17 rows of ldx = 2^13 halfs -> 2 GiB
     assert L.ecd_gemm_i8p(16, 8192, 16, 16, None, 0, 16, 64, 1 << 17, 64, 8192, None) == _ffi.ECD_ENOTSUP
     assert L.ecd_gemm_i8p_silu(16, 8192, 16, 16, 16, 64, 1 << 17, 32, 8192, None) == _ffi.ECD_ENOTSUP
+    assert L.ecd_gemm_i8p_rope(16, 8192, 16, 16, 16, 16, 16, 16, 16, 1 << 17, 1, 8, 2, 64, 128,
+                               8192, None) == _ffi.ECD_ENOTSUP
+
+
+def test_gemm_rope_validates_before_launch():
+    """The q|k|v GEMM with the RoPE epilogue rejects bad shapes on the host (ECD_EINVAL, nothing
+    launched): head_dim not a multiple of 4, Hq not a multiple of Hk, K not a multiple of 64,
+    a missing position vector, a misaligned rope table."""
+    from estudiocanciones_amd import _ffi
+    L = _ffi.lib()
+    E = _ffi.ECD_EINVAL
+    ok = dict(x=16, ldx=1024, wp=16, s=16, rope=16, pos=16, q=16, kc=16, vc=16, M=64, S=1, Hq=8,
+              Hk=2, L=64, HD=128, K=1024)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.ecd_gemm_i8p_rope(a["x"], a["ldx"], a["wp"], a["s"], a["rope"], a["pos"], a["q"],
+                                   a["kc"], a["vc"], a["M"], a["S"], a["Hq"], a["Hk"], a["L"],
+                                   a["HD"], a["K"], None)
+    assert call(HD=126) == E
+    assert call(Hq=7) == E
+    assert call(K=1000, ldx=1000) == E
+    assert call(pos=None) == E
+    assert call(rope=8) == E
+    assert call(M=0) == E
 
 
 def test_noalloc_attention_refuses_oversized_workspace():

@@ -161,6 +161,52 @@ def test_rms_qkv_rope(dev, M, S, Hq, Hk, HD, D, L):
     assert_close16(N_(vct), vc, what="fused v cache")
 
 
+@pytest.mark.parametrize("M,S,Hq,Hk,HD,D,L,bad", [
+    (300, 1, 24, 8, 128, 3072, 64, False),   # the backbone's q|k|v, ragged rows, one row per cache
+    (256, 128, 8, 2, 128, 1024, 160, False),  # two prompts of 128 positions sharing their caches
+    (64, 32, 8, 4, 384, 3072, 40, False),    # head_dim 384
+    (96, 1, 2, 1, 64, 256, 64, True),        # positions outside [0, L): no slot, q at the clamp
+])
+def test_gemm_rope_packed(dev, M, S, Hq, Hk, HD, D, L, bad):
+    """The prompt pass's q|k|v GEMM with RoPE and the cache write in its epilogue: bit-equal to
+    the GEMM followed by the RoPE kernel (q and both caches, untouched slots included), and
+    within the fp16 bar of the oracle's dense GEMM + rope_kv_write."""
+    import torch
+    from estudiocanciones_amd.kernels import (_rope_cache, gemm_packed, gemm_rope_packed,
+                                              next_power_of_2, pack_i8)
+    B = M // S
+    Nq = (Hq + 2 * Hk) * HD
+    q8, s = qweights(50 + HD, Nq, D)
+    x = randn16(51 + M, M, D, std=0.5)
+    if S == 1:
+        pos = rng(52).integers(0, L, M).astype(np.int64)
+    else:
+        pos = np.tile(np.arange(S, dtype=np.int64), B)
+    if bad:
+        pos[::7] = -1
+        pos[3::7] = L + 5
+    rope = rope_cache(HD, L)
+    kc0 = randn16(53, B, Hk, L, HD)
+    vc0 = randn16(54, B, Hk, L, HD)
+    wp, st, rt, pt = pack_i8(T(q8, dev)), T(s, dev), T(rope, dev), T(pos, dev)
+    kc, vc = T(kc0, dev), T(vc0, dev)
+    q = torch.empty(M, Hq * HD, dtype=torch.float16, device=dev)
+    gemm_rope_packed(T(x, dev), wp, st, rt, pt, q, kc, vc, S, Hq, Hk, L, HD, D)
+    kc2, vc2 = T(kc0, dev), T(vc0, dev)
+    q2 = torch.empty_like(q)
+    qkv = gemm_packed(T(x, dev), wp, st, Nq, D)
+    _rope_cache[(M, Hq + Hk)](qkv, rt, pt, q2, kc2, vc2, S, Hq, Hk, L, HD=HD,
+                              HALF=next_power_of_2(HD // 2))
+    assert torch.equal(q, q2), "q differs from GEMM + RoPE kernel"
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2), "cache differs from GEMM + RoPE kernel"
+    if not bad:
+        kw, vw = kc0.copy(), vc0.copy()
+        q_want = OK.rope_kv_write(OK.gemv_i8(x, q8, s), rope, pos, kw, vw, S, Hq, Hk, HD)
+        assert_close16(N_(q), q_want, what="gemm+rope q")
+        assert_close16(N_(kc), kw, what="gemm+rope k cache")
+        assert_close16(N_(vc), vw, what="gemm+rope v cache")
+
+
 @pytest.mark.parametrize("M,D,F", [(8, 3072, 8192), (16, 1024, 8192), (40, 256, 512)])
 def test_rms_w13_silu(dev, M, D, F):
     import torch
