@@ -30,25 +30,60 @@ def _counter_csv(path, counter, rows):
 
 
 def test_pmc_summary_copy_calibration(tmp_path):
-    """GEMV-family KiB per dispatch are averaged, then divided by the factor the calibration
-    copy gives (its counter reading over its known size): a counter that reads 2x the true
-    bytes on the copy reads 2x on the GEMVs too."""
+    """Backbone layer-tail KiB per dispatch (demangled or mangled names; the decoder's tail and
+    other kernels excluded) are averaged, then divided by the factor the calibration copy gives
+    (its counter reading over its known size): a counter that reads 2x the true bytes on the
+    copy reads 2x on the tail too."""
     sys.path.insert(0, str(ROOT))
     import bench
     calib_mib = 4
     fetch, write = tmp_path / "fetch.csv", tmp_path / "write.csv"
-    # fetch counter over-reads 2x: copy of 4 MiB reads 8192 KiB; GEMVs read 300 and 500 KiB
-    _counter_csv(fetch, "FETCH_SIZE", [("gemv_xreg_kernel<...>", [100.0, 200.0]),
-                                       ("gemv_xlds_kernel<...>", [500.0]),
-                                       ("other_kernel", [9999.0]),
+    bb = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true>(ecd::tail::Args)"
+    bb_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1EEEvNS0_4ArgsE"
+    dec = "void ecd::tail::layer_tail_kernel<2, 16, 4, 4, 128, 4, false>(ecd::tail::Args)"
+    # fetch counter over-reads 2x: copy of 4 MiB reads 8192 KiB; the tails read 300 and 500 KiB
+    _counter_csv(fetch, "FETCH_SIZE", [(bb, [100.0, 200.0]), (bb_mangled, [500.0]),
+                                       (dec, [7777.0]), ("other_kernel", [9999.0]),
                                        ("copy_bytes_kernel", [4096.0, 4096.0])])
-    # write counter exact: copy reads 4096 KiB; GEMVs write 16 and 48 KiB
-    _counter_csv(write, "WRITE_SIZE", [("gemv_xreg_kernel<...>", [16.0]),
-                                       ("gemv_fused_kernel<...>", [48.0]),
+    # write counter exact: copy reads 4096 KiB; the tails write 16 and 48 KiB
+    _counter_csv(write, "WRITE_SIZE", [(bb, [16.0]), (bb_mangled, [48.0]), (dec, [1.0]),
                                        ("copy_bytes_kernel", [4096.0])])
     out = bench.pmc_summary(str(fetch), str(write), calib_mib)
-    assert out["fetch"]["gemv_dispatches"] == 2 and out["write"]["gemv_dispatches"] == 2
+    assert out["fetch"]["tail_dispatches"] == 2 and out["write"]["tail_dispatches"] == 2
     assert out["fetch"]["factor"] == 2.0 and out["write"]["factor"] == 1.0
-    assert out["fetch"]["bytes_per_gemv_launch"] == 400 * 1024 // 2
-    assert out["write"]["bytes_per_gemv_launch"] == 32 * 1024
+    assert out["fetch"]["bytes_per_tail_launch"] == 400 * 1024 // 2
+    assert out["write"]["bytes_per_tail_launch"] == 32 * 1024
     assert out["traffic_bytes_per_launch"] == 200 * 1024 + 32 * 1024
+
+
+def test_pmc_gemm_summary_groups_variants(tmp_path):
+    """The prompt-GEMM counter summary groups dispatches by kernel and grid, averages each
+    counter over them and forms VALU per MFMA and the f16 FLOP (MOPS x 512)."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    path = tmp_path / "c.csv"
+    rows = [(1, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_MFMA", 100.0),
+            (1, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_VALU", 300.0),
+            (1, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_VALU_MFMA_MOPS_F16", 2.0),
+            (1, "gemm_i8p_kernel<0>", 98304, "MfmaUtil", 30.0),
+            (2, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_MFMA", 100.0),
+            (2, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_VALU", 500.0),
+            (2, "gemm_i8p_kernel<0>", 98304, "SQ_INSTS_VALU_MFMA_MOPS_F16", 2.0),
+            (2, "gemm_i8p_kernel<0>", 98304, "MfmaUtil", 40.0),
+            (3, "gemm_i8p_kernel<1>", 524288, "SQ_INSTS_MFMA", 50.0),
+            (3, "gemm_i8p_kernel<1>", 524288, "SQ_INSTS_VALU", 100.0),
+            (4, "decode_attn_kernel", 64, "SQ_INSTS_MFMA", 7.0)]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Grid_Size",
+                                          "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for d, n, g, c, v in rows:
+            w.writerow({"Dispatch_Id": d, "Kernel_Name": n, "Grid_Size": g, "Counter_Name": c,
+                        "Counter_Value": v})
+    out = bench.pmc_gemm_summary(str(path))
+    assert [(e["kernel"], e["dispatches"]) for e in out] == [("gemm_i8p_kernel<0>", 2),
+                                                             ("gemm_i8p_kernel<1>", 1)]
+    e = out[0]
+    assert e["mfma_insts"] == 100.0 and e["valu_insts"] == 400.0 and e["valu_per_mfma"] == 4.0
+    assert e["mfma_f16_flop"] == 1024.0 and e["MfmaUtil_pct"] == 35.0
+    assert out[1]["valu_per_mfma"] == 2.0 and out[1]["mfma_f16_flop"] is None
