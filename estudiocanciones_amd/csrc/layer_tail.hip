@@ -62,8 +62,6 @@ constexpr int MR = 8;                // rows held in the x tile (M <= MR)
 constexpr int CHB = 128 * MR;        // LDS bytes per 64-column chunk of the x tile
 constexpr int CNT2 = 640;            // sync words [640, 1024): split-W2 arrival counters per tile
 constexpr int MAX_T2_SPLIT = 384;    // tiles a split W2 can have (sync region words)
-constexpr int CNTA = 1024;           // sync words [1024, 2048): attention arrival counters per pair
-constexpr int SYNC_WORDS = 2048;
 constexpr int ATT_SHORT = 128;       // caches of at most this many slots: one split per pair
 constexpr int ATT_KB_MAX = 16;       // workgroups per (row, kv head) pair, long caches
 
@@ -587,50 +585,108 @@ __device__ __forceinline__ void lse_merge(const float* src, int n, int str, int 
   lo = ls;
 }
 
+// Workspace float offset of the attention partials: after the split-W2 sums of a D-wide layer.
+__device__ __forceinline__ long ws_att_offset(int D) { return (long)D * 64; }
+
+// Long caches: the 8 waves' partials (LDS) -> this workgroup's partial [G][m, l, acc[HD]] in the
+// workspace as 8-byte words (fp32 value, epoch), epoch = the gate count this launch reached
+// after its fourth gate (the same in every workgroup, different in every launch on one sync
+// region).  Then each of the pair's KB workgroups merges the KB partials for its HD / KB
+// columns of every head as soon as all the words it needs carry the epoch (polls bounded by
+// spin_max; lanes spread over parts x columns, G * HD / 64 value words and one (m, l) pair each,
+// exchanged through LDS): the log-sum-exp sums of the per-op combine, parts in order, with no
+// counter and no wait for this workgroup's own stores.  Returns false if a poll gave up.
 template <int HD, int G>
-__device__ __forceinline__ void attention_merge(const Args& a, unsigned char* smem, int NB, int b,
-                                                int lane) {
+__device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* smem, int NB, int b,
+                                                int lane, uint32_t epoch) {
+  static_assert(HD % 64 == 0, "value words spread evenly over the lanes");
+  static_assert(G * ATT_KB_MAX <= 64, "one (m, l) pair per lane");
   constexpr int PW = 2 + HD;
-  constexpr int NK = (HD + 63) / 64;
+  constexpr int NK = HD / 64;
+  constexpr int NV = G * HD / 64;  // value words per lane
   const int pairs = a.M * a.Hk;
-  if (a.L <= ATT_SHORT) return;  // the waves wrote o
+  if (a.L <= ATT_SHORT) return true;  // the waves wrote o
   const int KB = NB / pairs;
   const int p = b / KB, kq = b - p * KB;
   const int r = p / a.Hk, kh = p - r * a.Hk;
-  // the 8 waves -> this workgroup's partial in the workspace (agent scope)
-  float* part = a.ws + (long)(p * KB + kq) * G * PW;
+  uint64_t* base = (uint64_t*)(a.ws + ws_att_offset(a.D)) + (long)p * KB * G * PW;
+  uint64_t* part = base + (long)kq * G * PW;
+  const uint64_t tag = (uint64_t)epoch << 32;
+  auto put = [&](uint64_t* q, float v) {
+    __hip_atomic_store(q, tag | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto get = [&](const uint64_t* q) {
+    return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mo, lo, ao[NK];
     lse_merge<HD, CW>((const float*)smem, CW, G * PW, g, lane, mo, lo, ao, false);
     if (lane == 0) {
-      store_agent((uint32_t*)part + g * PW, __builtin_bit_cast(uint32_t, mo));
-      store_agent((uint32_t*)part + g * PW + 1, __builtin_bit_cast(uint32_t, lo));
+      put(part + g * PW, mo);
+      put(part + g * PW + 1, lo);
     }
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int d = lane + 64 * k;
-      if (d < HD) store_agent((uint32_t*)part + g * PW + 2 + d, __builtin_bit_cast(uint32_t, ao[k]));
-    }
+    for (int k = 0; k < NK; ++k) put(part + g * PW + 2 + lane + 64 * k, ao[k]);
   }
-  wait_vm0();
-  uint32_t old = 0;
-  if (lane == 0) old = add_agent(a.sync + CNTA + p);
-  old = __builtin_amdgcn_readfirstlane(old);
-  if (old % (uint32_t)KB != (uint32_t)(KB - 1)) return;
-  // last of the pair's workgroups: merge the KB parts in order and write o
-  const float* base = a.ws + (long)p * KB * G * PW;
+  // word t = (part i, head g, column c) of this workgroup's columns d = kq * cw + c
+  const int cw = HD / KB;  // KB divides HD
+  const int gc = G * cw;
+  const uint64_t* qv[NV];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float mo, lo, ao[NK];
-    lse_merge<HD, ATT_KB_MAX>(base, KB, G * PW, g, lane, mo, lo, ao, true);
-    f16* dst = a.o_next + ((long)r * a.Hq + kh * G + g) * HD;
-#pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int d = lane + 64 * k;
-      if (d < HD) dst[d] = (f16)(ao[k] / lo);
-    }
+  for (int j = 0; j < NV; ++j) {
+    const int t = lane + 64 * j;
+    const int i = t / gc, u = t - i * gc, g = u / cw;
+    qv[j] = base + (long)i * G * PW + g * PW + 2 + kq * cw + (u - g * cw);
   }
+  const bool hml = lane < KB * G;  // lane -> (part lane / G, head lane % G)
+  const uint64_t* qm = base + (long)(lane / G) * G * PW + (lane % G) * PW;
+  uint64_t wv[NV], wm = 0, wl = 0;
+  bool ok = true;
+  for (int it = 0;; ++it) {
+    bool ready = true;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      wv[j] = get(qv[j]);
+      ready = ready && (uint32_t)(wv[j] >> 32) == epoch;
+    }
+    if (hml) {
+      wm = get(qm);
+      wl = get(qm + 1);
+      ready = ready && (uint32_t)(wm >> 32) == epoch && (uint32_t)(wl >> 32) == epoch;
+    }
+    if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+    if (it >= a.spin_max) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // exchange through LDS after the waves' partials (one wave: LDS accesses stay in order)
+  float* sv = (float*)smem + CW * G * PW;  // [KB][G][cw]
+  float* sml = sv + G * HD;                // [KB][G][m, l]
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sv[lane + 64 * j] = __builtin_bit_cast(float, (uint32_t)wv[j]);
+  if (hml) {
+    sml[2 * lane] = __builtin_bit_cast(float, (uint32_t)wm);
+    sml[2 * lane + 1] = __builtin_bit_cast(float, (uint32_t)wl);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  for (int u = lane; u < gc; u += 64) {
+    const int g = u / cw;
+    float mx = -INFINITY;
+    for (int i = 0; i < KB; ++i) mx = fmaxf(mx, sml[2 * (i * G + g)]);
+    float ls = 0.f, acc = 0.f;
+    for (int i = 0; i < KB; ++i) {
+      const float m = sml[2 * (i * G + g)];
+      const float w = m > -INFINITY ? __expf(m - mx) : 0.f;
+      ls += sml[2 * (i * G + g) + 1] * w;
+      acc += sv[i * gc + u] * w;
+    }
+    a.o_next[((long)r * a.Hq + kh * G + g) * HD + kq * cw + (u - g * cw)] = (f16)(acc / ls);
+  }
+  return ok;
 }
 
 // LDS map (bytes), per phase, for K = D columns: x tile [0, XD), norm weights [XD, XD + 2D),
@@ -957,7 +1013,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       }
       bar();  // X(ATT)
       bar();  // P(ATT)
-      attention_merge<AHD, AG>(a, smem, NB, b, lane);
+      ok = attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)) &&
+           ok;
     }
   }
 done:
@@ -989,7 +1046,10 @@ int launch(const Args& a, int nb, hipStream_t st) {
   const int xd = CD * CW * CHB, xf = CF * CW * CHB;
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
-  const int lds = ldsD > ldsF ? ldsD : ldsF;
+  // attention: the waves' partials, then the merge's exchange
+  const int ldsA = AHD > 0 ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
+  int lds = ldsD > ldsF ? ldsD : ldsF;
+  if (lds < ldsA) lds = ldsA;
   hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
@@ -1006,18 +1066,18 @@ static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
   const int G = Hq / Hk, pairs = M * Hk;
   if (!(HD == 128 && (G == 3 || G == 4))) return false;
   if (L <= tail::ATT_SHORT) return pairs <= nb * tail::CW;
-  // KB = nb / pairs workgroups per pair; a power of two, so that the arrival counters (modulo
-  // KB, never reset) stay consistent across their 2^32 wrap
+  // KB = nb / pairs workgroups per pair, each merging HD / KB columns
   const int kb = nb / pairs;
-  return nb % pairs == 0 && (kb & (kb - 1)) == 0 && kb <= tail::ATT_KB_MAX &&
-         pairs <= tail::SYNC_WORDS - tail::CNTA;
+  return nb % pairs == 0 && kb <= tail::ATT_KB_MAX && HD % kb == 0;
 }
 
 extern "C" long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD) {
   const int nb = tail::device_cus();
+  // the split-W2 sums (D * 64 fp32), then the attention partials [NB][G][2 + HD] as 8-byte
+  // (value, epoch) words
   const long w2 = (long)D * 256;
-  const long at = Hk > 0 ? (long)nb * (Hq / Hk) * (HD + 2) * 4 : 0;
-  return w2 > at ? w2 : at;
+  const long at = Hk > 0 ? (long)nb * (Hq / Hk) * (HD + 2) * 8 : 0;
+  return w2 + at;
 }
 
 extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,

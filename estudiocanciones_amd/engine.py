@@ -228,8 +228,8 @@ class Stack:
     def _tail_buffers(self, M, dev, dtype, L):
         """Static buffers of the one-launch layer tail (ecd_layer_tail) for M-row decode steps,
         or None when the shapes or weights do not fit it: x1, mm, two layer outputs used in
-        turn (a launch's output never aliases its input), q, the gate region and the error
-        word (both kept across launches) and the split-w2 workspace."""
+        turn (a launch's output never aliases its input), q, the gate region, the error
+        word and the workspace (all three kept across launches)."""
         if not self.blocks or any(b.qkv.qp is None or b.o.qp is None or b.w13.qp is None or
                                   b.w2.qp is None for b in self.blocks):
             return None
@@ -244,7 +244,7 @@ class Stack:
         return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
                     q=e(b0.h * b0.hd), sync=torch.zeros(2048, device=dev, dtype=torch.int32),
                     err=torch.zeros(1, device=dev, dtype=torch.int32),
-                    ws=torch.empty(-(-wsb // 4), device=dev, dtype=torch.float32),
+                    ws=torch.zeros(-(-wsb // 4), device=dev, dtype=torch.float32),
                     att=att, ob=[e(b0.h * b0.hd), e(b0.h * b0.hd)] if att else None)
 
     def tail_error(self):

@@ -513,7 +513,8 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq
     (packed), sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 2048], zero before
     first use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of
-    layer_tail_ws_bytes bytes."""
+    layer_tail_ws_bytes bytes, zero before first use and kept with its ``sync`` (partials are
+    recognised by the sync region's gate count)."""
     dev = _dev(o, "layer_tail")
     M, D = o.shape
     F = mm.shape[1]
