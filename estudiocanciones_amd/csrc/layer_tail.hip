@@ -94,8 +94,10 @@ struct Args {
   float scale;
   uint32_t* sync;  // 8 KB gate region, zero before the first launch
   uint32_t* err;   // set to 1 when a gate wait times out
-  float* ws;       // workspace: split-W2 partial sums [D / 16][KS2][64][4] (KS2 > 1), and the
-                   // attention's per-workgroup partials [NB][G][2 + HD] (long caches)
+  float* ws;       // workspace, zero before the first launch on `sync`: split-W2 partial sums
+                   // [D / 16][KS2][64][4] (KS2 > 1), the attention's per-workgroup partials
+                   // [NB][G][2 + HD] (long caches) and the q|k|v hand-off [MR][Hq + 2 Hk][HD],
+                   // both as tagged words
   int M, D, F;
   float eps;
   int spin_max;
@@ -138,6 +140,26 @@ __device__ __forceinline__ uint32_t add_agent(uint32_t* p) {
 }
 __device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged words: 32 bits of data (one fp32, or two fp16) and the launch's epoch in one 8-byte
+// word, stored and read whole at agent scope.  A reader that sees its epoch in a word sees that
+// word's data of this launch, with no acknowledgement or flag between writer and reader.
+__device__ __forceinline__ void put_tagged(uint64_t* p, uint32_t v, uint32_t epoch) {
+  __hip_atomic_store(p, ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get_tagged(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t epoch) {
+  return (uint32_t)(w >> 32) == epoch;
+}
+
+// Workspace float offsets: the attention partials after the split-W2 sums of a D-wide layer,
+// the q|k|v hand-off after the partials of NB workgroups.
+__device__ __forceinline__ long ws_att_offset(int D) { return (long)D * 64; }
+__device__ __forceinline__ long ws_hand_offset(const Args& a, int NB) {
+  return ws_att_offset(a.D) + (long)NB * (a.Hq / a.Hk) * (2 + a.HD) * 2;
 }
 
 // Gate words: [0] arrivals of group leaders, [64 (1 + g)] arrivals of group g's workgroups,
@@ -420,26 +442,25 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // caches: pair p = blockIdx / KB (KB = NB / pairs workgroups per pair), its split s =
 // (blockIdx % KB) * 8 + wave of S = 8 KB splits (the split rule of app/kernels.py:120-127 with
 // S splits); the loader merges its 8 waves' partials (log-sum-exp) into one per workgroup, and
-// the last of the pair's KB workgroups merges those and writes o.  Same arithmetic as the
-// split-combine kernel, summed in two levels.
-// One wave's attention split; ring[0] holds its first K/V tile, read before the launch's new
-// cache slots exist (the other RING - 1 tiles go out after the gate: the registers of the
-// 9-wave workgroup hold one tile across the gate).
+// the pair's KB workgroups merge those and write o.  Same arithmetic as the split-combine
+// kernel, summed in two levels.
+// One wave's attention split; ring[0] holds its first K/V tile, read while the loader's q|k|v
+// epilogue runs.
 template <int HD, int RING>
 struct AttPre {
   KVTile<HD> ring[RING];
   long cbase;    // this pair's cache [L, HD] (K and V alike)
   int r, kh;     // row and kv head of the pair
-  int lo, hi;    // the split's tokens
-  int lim;       // last token the early reads touched (lo - 1: none)
+  int lo, hi;    // the split's tokens held in the cache before the launch
+  int pn;        // the slot this launch writes (L: none)
+  bool nw;       // the split ends with slot pn, taken from the hand-off
   bool on;       // this wave runs a split
 };
 
 // Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair
 // blockIdx / KB, split (blockIdx % KB) * 8 + wave of 8 KB -- and its first tile.  With one
-// row per cache (S == 1) every slot below pos[r] is final before the launch, so token indices
-// clamp to min(hi - 1, pos[r] - 1) and no line of the slot this launch writes is read; with
-// several rows per cache (their new slots fall inside each other's ranges) nothing is read early.
+// row per cache every slot below pos[r] is final before the launch; the split's cache part
+// stops below slot pos[r], which comes from the hand-off, so no line of that slot is read.
 template <int HD, int RING>
 __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int wv, int lane,
                                              AttPre<HD, RING>& pf) {
@@ -458,7 +479,7 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
   }
   pf.on = p < pairs;
   pf.lo = pf.hi = 0;
-  pf.lim = -1;
+  pf.nw = false;
   if (!pf.on) return;
   pf.r = p / Hk;
   pf.kh = p - pf.r * Hk;
@@ -466,65 +487,123 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
   split_range(a.pos, pf.r, L, ns, sp, pf.lo, pf.hi);
   const long praw = a.pos[pf.r];
   const int pn = (praw >= 0 && praw < L) ? (int)praw : L;  // the slot written here (L: none)
-  pf.lim = a.S == 1 ? min(pf.hi - 1, pn - 1) : pf.lo - 1;
-  if (pf.lo <= pf.lim) kv_load<HD>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.lim, lane);
+  pf.pn = pn;
+  pf.nw = pf.lo <= pn && pn < pf.hi;
+  pf.hi = min(pf.hi, pn);
+  if (pf.lo < pf.hi) kv_load<HD>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.hi - 1, lane);
 }
 
-// After the gate: a first tile not read early is loaded now; otherwise the lanes holding its
-// tokens in (lim, hi - 1] load those (plain loads: no line of theirs was read in this launch).
-template <int HD, int RING>
-__device__ __forceinline__ void att_complete(AttPre<HD, RING>& pf, const f16* kb, const f16* vb,
-                                             int lane) {
-  constexpr int NKC = KVTile<HD>::NKC, NDP = KVTile<HD>::NDP;
-  const int row = lane & 15, grp = lane >> 4;
-  const int t0 = pf.lo;
-  if (pf.hi <= t0) return;
-  if (t0 > pf.lim) {
-    kv_load<HD>(pf.ring[0], kb, vb, t0, pf.hi - 1, lane);
-    return;
-  }
-  if (pf.lim >= pf.hi - 1 || t0 + 15 <= pf.lim) return;
-  const int tk = t0 + row;
-  if (tk > pf.lim && tk < pf.hi) {
-    const f16* kp = kb + (long)tk * HD + 8 * grp;
+// load_q from the hand-off words (row r's q at ((r * NQ + head * HD + d) / 2), two fp16 each),
+// polled until every word this lane needs carries the epoch (bounded by spin_max).
+template <int HD, int G>
+__device__ __forceinline__ bool load_q_hand(f16x8 (&qf)[HD / 32], const uint64_t* hand, int r,
+                                            int NQ, int kh, uint32_t ep, int lane, int spin_max) {
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const bool gv = row < G;
+  const uint64_t* qp = hand + (((long)r * NQ + (long)(kh * G + (gv ? row : 0)) * HD + 8 * grp) >> 1);
+  uint64_t w[HD / 32][4] = {};
+  bool ok = true;
+  for (int it = 0;; ++it) {
+    bool ready = true;
+    if (gv) {
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) pf.ring[0].k[c] = *(const f16x8*)(kp + 32 * c);
-  }
+      for (int i = 0; i < HD / 32; ++i)
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int tv = t0 + 4 * grp + rr;
-    if (tv > pf.lim && tv < pf.hi) {
-      const f16* vp = vb + (long)tv * HD + 8 * row;
-#pragma unroll
-      for (int j = 0; j < NDP; ++j)
-        if (8 * (row + 16 * j) < HD) pf.ring[0].v[rr][j] = *(const f16x8*)(vp + 128 * j);
+        for (int u = 0; u < 4; ++u) {
+          w[i][u] = get_tagged(qp + 16 * i + u);
+          ready = ready && tag_is(w[i][u], ep);
+        }
     }
+    if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+    if (it >= spin_max) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
+#pragma unroll
+  for (int i = 0; i < HD / 32; ++i)
+    qf[i] = __builtin_bit_cast(f16x8, (u32x4){(uint32_t)w[i][0], (uint32_t)w[i][1],
+                                              (uint32_t)w[i][2], (uint32_t)w[i][3]});
+  return ok;
+}
+
+// The split's last token, slot pn, as one more tile (token pn alone) from the hand-off: every
+// lane polls one K word and one V word (HD / 2 words each, bounded by spin_max), then the lanes
+// holding token 0 of the tile in the K and V registers gather their fp16 octets across lanes,
+// and the tile updates the split state (the online softmax of attn_run_m, one more step).
+template <int HD, int G>
+__device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x8 (&qf)[HD / 32],
+                                              const uint64_t* hk, const uint64_t* hv, uint32_t ep,
+                                              int pn, float scale, int lane, int spin_max) {
+  static_assert(HD == 128, "one K word and one V word per lane");
+  uint64_t wk = 0, wv = 0;
+  bool ok = true;
+  for (int it = 0;; ++it) {
+    wk = get_tagged(hk + lane);
+    wv = get_tagged(hv + lane);
+    if (__builtin_amdgcn_ballot_w64(!tag_is(wk, ep) || !tag_is(wv, ep)) == 0) break;
+    if (it >= spin_max) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const int k32 = (int)(uint32_t)wk, v32 = (int)(uint32_t)wv;
+  const int row = lane & 15, grp = lane >> 4;
+  KVTile<HD> t;
+  // K: lane (0, grp) holds d = 8 grp + 32 c + e, i.e. words 4 grp + 16 c + e / 2
+#pragma unroll
+  for (int c = 0; c < KVTile<HD>::NKC; ++c) {
+    u32x4 x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      x[u] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * grp + 16 * c + u), k32);
+    t.k[c] = row == 0 ? __builtin_bit_cast(f16x8, x) : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  // V: lane (row, 0) holds token 0 at rr = 0, d = 8 row + e, i.e. words 4 row + e / 2
+  u32x4 y;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) y[u] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * row + u), v32);
+  t.v[0][0] = grp == 0 ? __builtin_bit_cast(f16x8, y) : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int rr = 1; rr < 4; ++rr) t.v[rr][0] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  attn_tile_m<HD, G>(ss, ss.m_run, ss.l_run, qf, t, pn, pn + 1, scale, lane);
+  return ok;
 }
 
 // Decode attention of app/kernels.py:111-167 for the M rows, their kv heads and the query heads
 // of each (G = Hq / Hk), over cache slots [0, pos[r]], with the per-split core of the decode
 // kernel (attn_core.h), on the splits att_prefetch assigned.  Short caches: the pair's one wave
 // writes o directly.  Long caches: the loader merges its 8 waves' partials (log-sum-exp) into
-// one per workgroup, and the last of the pair's KB workgroups merges those and writes o.  Same
-// arithmetic as the split-combine kernel, summed in two levels.
+// one per workgroup, and the pair's KB workgroups merge those (attention_merge).  Same
+// arithmetic as the split-combine kernel, summed in two levels.  One row per cache: q and the
+// new K/V slot come from the hand-off words of epoch `ep`, with no fourth gate.
 template <int HD, int G, int RING>
 __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
-                                                int lane, AttPre<HD, RING>& pf) {
+                                                int lane, AttPre<HD, RING>& pf, uint32_t ep) {
   constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
   const int Hq = a.Hq;
-  bar();  // X(ATT): q and the new cache slots are complete
+  bar();  // X(ATT): the loader has read the q|k|v partials (LDS is free)
   if (!pf.on) {
     bar();  // P(ATT)
     return;
   }
   const f16* kb = a.kc + pf.cbase;
   const f16* vb = a.vc + pf.cbase;
+  const int NQ = (Hq + 2 * a.Hk) * HD;
+  const uint64_t* hw = (const uint64_t*)(a.ws + ws_hand_offset(a, gridDim.x));
   f16x8 qf[HD / 32];
-  load_q<HD, G>(qf, a.q, pf.r, Hq, pf.kh, lane);
-  att_complete<HD, RING>(pf, kb, vb, lane);
+  bool ok = load_q_hand<HD, G>(qf, hw, pf.r, NQ, pf.kh, ep, lane, a.spin_max);
   SplitStateM<HD, G> ss;
   attn_run_m<HD, G, RING>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
+  if (pf.nw) {
+    const uint64_t* hk = hw + (((long)pf.r * NQ + (long)(Hq + pf.kh) * HD) >> 1);
+    const uint64_t* hv = hw + (((long)pf.r * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
+    ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, pf.pn, a.scale, lane, a.spin_max) && ok;
+  }
+  if (!ok && lane == 0) store_agent(a.err, 1u);
   if (a.L <= ATT_SHORT) {
     attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
     bar();  // P(ATT)
@@ -585,9 +664,6 @@ __device__ __forceinline__ void lse_merge(const float* src, int n, int str, int 
   lo = ls;
 }
 
-// Workspace float offset of the attention partials: after the split-W2 sums of a D-wide layer.
-__device__ __forceinline__ long ws_att_offset(int D) { return (long)D * 64; }
-
 // Long caches: the 8 waves' partials (LDS) -> this workgroup's partial [G][m, l, acc[HD]] in the
 // workspace as 8-byte words (fp32 value, epoch), epoch = the gate count this launch reached
 // after its fourth gate (the same in every workgroup, different in every launch on one sync
@@ -611,14 +687,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
   const int r = p / a.Hk, kh = p - r * a.Hk;
   uint64_t* base = (uint64_t*)(a.ws + ws_att_offset(a.D)) + (long)p * KB * G * PW;
   uint64_t* part = base + (long)kq * G * PW;
-  const uint64_t tag = (uint64_t)epoch << 32;
-  auto put = [&](uint64_t* q, float v) {
-    __hip_atomic_store(q, tag | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  };
-  auto get = [&](const uint64_t* q) {
-    return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
+  auto put = [&](uint64_t* q, float v) { put_tagged(q, __builtin_bit_cast(uint32_t, v), epoch); };
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mo, lo, ao[NK];
@@ -648,13 +717,13 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
     bool ready = true;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      wv[j] = get(qv[j]);
-      ready = ready && (uint32_t)(wv[j] >> 32) == epoch;
+      wv[j] = get_tagged(qv[j]);
+      ready = ready && tag_is(wv[j], epoch);
     }
     if (hml) {
-      wm = get(qm);
-      wl = get(qm + 1);
-      ready = ready && (uint32_t)(wm >> 32) == epoch && (uint32_t)(wl >> 32) == epoch;
+      wm = get_tagged(qm);
+      wl = get_tagged(qm + 1);
+      ready = ready && tag_is(wm, epoch) && tag_is(wl, epoch);
     }
     if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
     if (it >= a.spin_max) {
@@ -701,6 +770,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ uint32_t s_epoch;  // the gate count after the third gate (loader -> compute waves)
   constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
   constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
   const int lane = threadIdx.x & 63;
@@ -710,8 +780,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
   const bool has_next = a.wq != nullptr;
   // the next layer's attention runs in this launch (AHD > 0: its head_dim; AG query heads per
-  // kv head), after a fourth gate; caches longer than ATT_SHORT slots are split over the KB
-  // workgroups of each (row, kv head) pair and their 8 compute waves
+  // kv head; one row per cache), on q and the new K/V slot handed off in tagged words; caches
+  // longer than ATT_SHORT slots are split over the KB workgroups of each (row, kv head) pair and
+  // their 8 compute waves
   const bool att = AHD > 0 && has_next;
 
   // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
@@ -735,8 +806,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
   if (wv < CW) {
     // ------------------------------------------------------------------ compute waves
-    // attention splits: two K/V tiles in flight after the gate where the register budget
-    // allows it (G <= 3)
+    // attention splits: two K/V tiles in flight where the register budget allows it (G <= 3)
     constexpr int ARING = AG <= 3 ? 2 : 1;
     AttPre<(AHD > 0 ? AHD : 32), ARING> pf;
     const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
@@ -838,13 +908,13 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       wait_lgkm0();
       bar();  // P(QKV)
       // the next layer's first K/V tiles go out into the registers the q|k|v phase leaves
-      // free, while the epilogue and the last gate run
+      // free, while the loader's epilogue runs
       if constexpr (AHD > 0) {
         if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
       }
     }
     if constexpr (AHD > 0) {
-      if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf);
+      if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf, s_epoch);
     }
     return;
   }
@@ -967,11 +1037,17 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       gate_arrive(a.sync, grp, per, go);
       ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
       ++go;
+      s_epoch = go;
     }
+    wait_lgkm0();
     bar();  // X(QKV)
     bar();  // S(QKV)
     bar();  // P(QKV)
     const bool pval = p_raw >= 0 && p_raw < L;
+    // hand-off words of this launch's epoch: [row][q heads | k heads | v heads][HD] in pairs
+    const uint32_t ep = __builtin_amdgcn_readfirstlane(go);
+    const int NQ = (a.Hq + 2 * a.Hk) * HD;
+    uint64_t* hw = (uint64_t*)(a.ws + ws_hand_offset(a, NB));
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       if (tq[i] < 0) continue;
@@ -997,20 +1073,16 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         const int kh = h < a.Hq + a.Hk ? h - a.Hq : h - a.Hq - a.Hk;
         dst = (h < a.Hq + a.Hk ? a.kc : a.vc) + (((long)bb * a.Hk + kh) * L + p_raw) * HD + d;
       }
-      // read in this launch by the attention phase: agent scope
-      if (dst) {
-        if (att) st_sc1_u64(dst, o);
-        else *(f16x4*)dst = o;
+      if (att) {  // this launch's attention reads the hand-off words, not q or the caches
+        const uint64_t ov = __builtin_bit_cast(uint64_t, o);
+        uint64_t* hp = hw + (((long)me * NQ + nb) >> 1);
+        put_tagged(hp, (uint32_t)ov, ep);
+        put_tagged(hp + 1, (uint32_t)(ov >> 32), ep);
       }
+      if (dst) *(f16x4*)dst = o;
     }
     if constexpr (AHD > 0) {
       if (!att) goto done;
-      wait_vm0();
-      if (lane == 0) {
-        gate_arrive(a.sync, grp, per, go);
-        ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-        ++go;
-      }
       bar();  // X(ATT)
       bar();  // P(ATT)
       ok = attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)) &&
@@ -1035,14 +1107,6 @@ int device_cus() {
 
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
 int launch(const Args& a, int nb, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             160 * 1024);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
   const int xd = CD * CW * CHB, xf = CF * CW * CHB;
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
@@ -1050,6 +1114,14 @@ int launch(const Args& a, int nb, hipStream_t st) {
   const int ldsA = AHD > 0 ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
   int lds = ldsD > ldsF ? ldsD : ldsF;
   if (lds < ldsA) lds = ldsA;
+  // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
+  static int attr = 0;
+  if (lds > attr) {
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return (int)e;
+    attr = lds;
+  }
   hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
@@ -1073,11 +1145,12 @@ static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
 
 extern "C" long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD) {
   const int nb = tail::device_cus();
-  // the split-W2 sums (D * 64 fp32), then the attention partials [NB][G][2 + HD] as 8-byte
-  // (value, epoch) words
+  // the split-W2 sums (D * 64 fp32), the attention partials [NB][G][2 + HD] as 8-byte (fp32,
+  // epoch) words, then the q|k|v hand-off [MR][Hq + 2 Hk][HD] as 8-byte (2 fp16, epoch) words
   const long w2 = (long)D * 256;
   const long at = Hk > 0 ? (long)nb * (Hq / Hk) * (HD + 2) * 8 : 0;
-  return w2 + at;
+  const long hd = Hk > 0 ? (long)tail::MR * (Hq + 2 * Hk) * HD * 4 : 0;
+  return w2 + at + hd;
 }
 
 extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
@@ -1110,6 +1183,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
              (Hq + 2 * Hk) * HD % 16))
     return ECD_EINVAL;
   if (o_next && (!wq || !al(o_next) || !ws)) return ECD_EINVAL;
+  if (o_next && S != 1) return ECD_ENOTSUP;  // the hand-off holds one new slot per cache
   const int nb = tail::device_cus();
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
   const int t13 = 2 * F / 16;

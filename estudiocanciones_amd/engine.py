@@ -343,8 +343,8 @@ class Stack:
             nxt = None if nb is None else dict(
                 n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, rope=self.rope, pos=pos, q=q, kc=nb.kc,
                 vc=nb.vc, S=S, Hq=nb.h, Hk=nb.kvh, L=nb.kc.shape[2], HD=nb.hd)
-            o_next = t["ob"][i % 2] if (t["att"] and self.tail_attention and nb is not None) \
-                else None
+            o_next = t["ob"][i % 2] if (t["att"] and self.tail_attention and nb is not None and
+                                        S == 1) else None
             x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
                            t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], t["ws"],
                            nxt=nxt, o_next=o_next, stream=b.w13.stream)

@@ -209,7 +209,8 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  *   (:189-192): q [M, Hq*HD], k/v into kc/vc [B, Hk, L, HD] at pos (row m -> m / S); and, when
  *   o_next is not NULL, that layer's decode attention (ecd_decode_attn + ecd_attn_combine,
  *   :194-204, scale 1/sqrt(HD)) into o_next [M, Hq * HD] -- for head_dim 128 with 3 or 4 query
- *   heads per kv head (ecd_layer_tail_supported tells).
+ *   heads per kv head (ecd_layer_tail_supported tells) and one row per cache (S = 1, else
+ *   ECD_ENOTSUP).
  * Same numerics as the per-op entry points up to the fp32 summation order.  wo / w13 / w2 / wq
  * are ecd_pack_i8 copies (w13 interleaved, s13 interleaved the same way); o, xin, x1, mm,
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.

@@ -90,7 +90,8 @@ def assert_within_noise(got, want, want_alt, what="", factor=3.0, atol=ATOL, rto
     fp32 re-association alone by more than the per-kernel bar: ``want_alt`` is the oracle
     evaluated with float32 instead of float64 sums.  The GPU's largest error against ``want``,
     and its share of elements outside atol + rtol |want|, must stay within ``factor`` times the
-    oracle's own (plus one fp16 ulp at the output scale / 0.1%)."""
+    oracle's own (plus one fp16 ulp at the output scale / 0.1% of the elements, at least 4: on
+    a 2048-element cache slot one fp16 rounding step across the bar is 0.05%)."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     alt = np.asarray(want_alt, np.float64)
@@ -101,5 +102,5 @@ def assert_within_noise(got, want, want_alt, what="", factor=3.0, atol=ATOL, rto
     fg, fn = float((eg > bound).mean()), float((en > bound).mean())
     assert eg.max() <= factor * en.max() + ulp, \
         f"{what}: max error {eg.max():.3e} vs oracle re-association {en.max():.3e}"
-    assert fg <= factor * fn + 1e-3, \
+    assert fg <= factor * fn + max(1e-3, 4.0 / eg.size), \
         f"{what}: {fg:.4%} outside the kernel bar vs oracle re-association {fn:.4%}"

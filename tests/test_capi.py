@@ -154,6 +154,16 @@ def test_gemm_rejects_x_beyond_32bit_offsets():
                                8192, None) == _ffi.ECD_ENOTSUP
 
 
+def test_layer_tail_attention_needs_one_row_per_cache():
+    """The layer tail's in-launch attention takes q and the new cache slot from per-launch
+    hand-off words, one slot per cache: several rows per cache (S > 1) with o_next is refused
+    with ECD_ENOTSUP before any HIP call."""
+    from estudiocanciones_amd import _ffi
+    L = _ffi.lib()
+    assert L.ecd_layer_tail(*([256] * 24), 8, 3072, 8192, 2, 24, 8, 1024, 128, 1e-5, 0,
+                            None) == _ffi.ECD_ENOTSUP
+
+
 def test_gemm_rope_validates_before_launch():
     """The q|k|v GEMM with the RoPE epilogue rejects bad shapes on the host (ECD_EINVAL, nothing
     launched): head_dim not a multiple of 4, Hq not a multiple of Hk, K not a multiple of 64,

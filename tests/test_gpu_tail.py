@@ -84,6 +84,7 @@ DEC_REF2 = dict(layers=2, heads=8, kv_heads=4, max_seq=2048, dim=3072, ffn=8192)
 @pytest.mark.parametrize("cfg,B,L,pos_kind,stream", [
     (BB3, 8, 1024, "spread", True),    # backbone shape, 8 rows, positions 0 .. L - 1
     (BB3, 2, 1024, "last", True),      # the C0 rows
+    (BB3, 8, 4096, "last", True),      # long splits: the new slot in a split's ninth tile
     (DEC3, 8, 8, "spread", False),     # 1024-wide decoder, per-frame cache of 8 slots
     (DEC_REF2, 8, 8, "last", False),   # the reference's decoder: 3072 wide, head_dim 384
 ])
