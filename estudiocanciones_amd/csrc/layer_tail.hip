@@ -444,8 +444,7 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // S splits); the loader merges its 8 waves' partials (log-sum-exp) into one per workgroup, and
 // the pair's KB workgroups merge those and write o.  Same arithmetic as the split-combine
 // kernel, summed in two levels.
-// One wave's attention split; ring[0] holds its first K/V tile, read while the loader's q|k|v
-// epilogue runs.
+// One wave's attention split; ring[0] holds its first K/V tile, read during the third gate.
 template <int HD, int RING>
 struct AttPre {
   KVTile<HD> ring[RING];
@@ -594,10 +593,23 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   const f16* vb = a.vc + pf.cbase;
   const int NQ = (Hq + 2 * a.Hk) * HD;
   const uint64_t* hw = (const uint64_t*)(a.ws + ws_hand_offset(a, gridDim.x));
+  // splits of more than two tiles: the ring's other tiles go out before the q polls (the
+  // polls then wait behind them in the CU's queue, which pays only when the stream is long)
+  const int ntiles = pf.hi > pf.lo ? (pf.hi - pf.lo + 15) / 16 : 0;
+  const bool early = ntiles > 2;
+  if (early) {
+#pragma unroll
+    for (int r = 1; r < RING; ++r) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
+  }
   f16x8 qf[HD / 32];
   bool ok = load_q_hand<HD, G>(qf, hw, pf.r, NQ, pf.kh, ep, lane, a.spin_max);
+  if (!early) {
+#pragma unroll
+    for (int r = 1; r < RING; ++r)
+      if (r < ntiles) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
+  }
   SplitStateM<HD, G> ss;
-  attn_run_m<HD, G, RING>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
+  attn_run_m<HD, G, RING, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
   if (pf.nw) {
     const uint64_t* hk = hw + (((long)pf.r * NQ + (long)(Hq + pf.kh) * HD) >> 1);
     const uint64_t* hv = hw + (((long)pf.r * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
@@ -891,6 +903,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     bar();  // P(W2)
 
     if (has_next) {
+      // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
+      // they stream during the third gate, and the loader's hand-off stores after the q|k|v
+      // phase do not queue behind them
+      if constexpr (AHD > 0) {
+        if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+      }
       // phase QKV (x = rms(xout, n1'))
       bar();  // X(QKV): xout is complete
       dma_rows<CD>(a.xout, D, M, c0D, xs, lane);
@@ -907,11 +925,6 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       put_partials<2>(psD, acc, wv, lane);
       wait_lgkm0();
       bar();  // P(QKV)
-      // the next layer's first K/V tiles go out into the registers the q|k|v phase leaves
-      // free, while the loader's epilogue runs
-      if constexpr (AHD > 0) {
-        if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
-      }
     }
     if constexpr (AHD > 0) {
       if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf, s_epoch);
