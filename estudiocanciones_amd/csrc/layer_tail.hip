@@ -529,25 +529,26 @@ __device__ __forceinline__ bool load_q_hand(f16x8 (&qf)[HD / 32], const uint64_t
 }
 
 // The split's last token, slot pn, as one more tile (token pn alone) from the hand-off: every
-// lane polls one K word and one V word (HD / 2 words each, bounded by spin_max), then the lanes
-// holding token 0 of the tile in the K and V registers gather their fp16 octets across lanes,
-// and the tile updates the split state (the online softmax of attn_run_m, one more step).
+// lane holds one K word and one V word (HD / 2 words each; wk, wv as read with q, polled again
+// until they carry the epoch, bounded by spin_max), then the lanes holding token 0 of the tile
+// in the K and V registers gather their fp16 octets across lanes, and the tile updates the
+// split state (the online softmax of attn_run_m, one more step).
 template <int HD, int G>
 __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x8 (&qf)[HD / 32],
                                               const uint64_t* hk, const uint64_t* hv, uint32_t ep,
-                                              int pn, float scale, int lane, int spin_max) {
+                                              int pn, float scale, int lane, int spin_max,
+                                              uint64_t wk, uint64_t wv) {
   static_assert(HD == 128, "one K word and one V word per lane");
-  uint64_t wk = 0, wv = 0;
   bool ok = true;
   for (int it = 0;; ++it) {
-    wk = get_tagged(hk + lane);
-    wv = get_tagged(hv + lane);
     if (__builtin_amdgcn_ballot_w64(!tag_is(wk, ep) || !tag_is(wv, ep)) == 0) break;
     if (it >= spin_max) {
       ok = false;
       break;
     }
     __builtin_amdgcn_s_sleep(1);
+    wk = get_tagged(hk + lane);
+    wv = get_tagged(hv + lane);
   }
   const int k32 = (int)(uint32_t)wk, v32 = (int)(uint32_t)wv;
   const int row = lane & 15, grp = lane >> 4;
@@ -601,6 +602,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
 #pragma unroll
     for (int r = 1; r < RING; ++r) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
   }
+  // the new slot's K and V words go out with the q polls (one round trip)
+  const uint64_t* hk = hw + (((long)pf.r * NQ + (long)(Hq + pf.kh) * HD) >> 1);
+  const uint64_t* hv = hw + (((long)pf.r * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
+  uint64_t nk = 0, nv = 0;
+  if (pf.nw) {
+    nk = get_tagged(hk + lane);
+    nv = get_tagged(hv + lane);
+  }
   f16x8 qf[HD / 32];
   bool ok = load_q_hand<HD, G>(qf, hw, pf.r, NQ, pf.kh, ep, lane, a.spin_max);
   if (!early) {
@@ -610,11 +619,7 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   }
   SplitStateM<HD, G> ss;
   attn_run_m<HD, G, RING, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
-  if (pf.nw) {
-    const uint64_t* hk = hw + (((long)pf.r * NQ + (long)(Hq + pf.kh) * HD) >> 1);
-    const uint64_t* hv = hw + (((long)pf.r * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
-    ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, pf.pn, a.scale, lane, a.spin_max) && ok;
-  }
+  if (pf.nw) ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, pf.pn, a.scale, lane, a.spin_max, nk, nv) && ok;
   if (!ok && lane == 0) store_agent(a.err, 1u);
   if (a.L <= ATT_SHORT) {
     attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
@@ -876,6 +881,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
     u32x4 wq[2][CD];
     const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
+    // the next layer's q|k|v weights go out during the second gate, into the registers the
+    // W13 phase freed (HBM would idle there otherwise)
+    if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+    else if (tq0 >= 0)
+      load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
+                                           nchD, c0D, lane);
 
     // phase W2 (x = mm)
     bar();  // X(W2): mm is complete
@@ -883,20 +894,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     wait_vm0();
     {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-      // the next layer's q|k|v weights go out during the W2 MFMAs
-      auto ldq = [&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        constexpr int q0 = (u * CD) / C2, q1 = ((u + 1) * CD) / C2;
-        if (tq1 >= 0) load_w_chunks<2, CD, NTL, q0, q1, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
-        else if (tq0 >= 0)
-          load_w_chunks<1, CD, NTL, q0, q1, LA>(*(u32x4(*)[1][CD])wq, a.wq,
-                                                *(const int(*)[1])tq_t, nchD, c0D, lane);
-      };
-      if (t2 >= 0) {
-        mfma_chunks_then<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false, ldq);
-      } else {
-        static_for<C2>(ldq);
-      }
+      if (t2 >= 0) mfma_chunks<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false);
       put_partials<1>(psF, acc, wv, lane);
     }
     wait_lgkm0();
