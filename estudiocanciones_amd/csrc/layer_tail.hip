@@ -439,11 +439,26 @@ __device__ __forceinline__ f16x4 scale4(const f32x4& acc, const f16x4& s) {
 // Decode attention of app/kernels.py:111-167 for the M rows, their kv heads and the query heads
 // of each (G = Hq / Hk), over cache slots [0, pos[r]], with the per-split core of the decode
 // kernel (attn_core.h).  Short caches: one wave per (row, kv head) pair writes o directly.  Long
-// caches: pair p = blockIdx / KB (KB = NB / pairs workgroups per pair), its split s =
-// (blockIdx % KB) * 8 + wave of S = 8 KB splits (the split rule of app/kernels.py:120-127 with
+// caches: KB = NB / pairs workgroups per pair (att_pair gives a workgroup's pair p and part kq),
+// split s = kq * 8 + wave of S = 8 KB splits (the split rule of app/kernels.py:120-127 with
 // S splits); the loader merges its 8 waves' partials (log-sum-exp) into one per workgroup, and
 // the pair's KB workgroups merge those and write o.  Same arithmetic as the split-combine
 // kernel, summed in two levels.
+// Long caches: pair p and part kq (of KB) of workgroup b.  Workgroups go to the XCDs round-robin
+// (b % 8), so where each XCD's NB / 8 workgroups split into whole pairs, a pair's KB workgroups
+// are taken from one XCD (their merge then stays within one L2); otherwise KB consecutive ids.
+__device__ __forceinline__ void att_pair(int b, int NB, int KB, int& p, int& kq) {
+  const int per = NB >> 3;
+  if (per % KB == 0) {
+    const int x = b & 7, i = b >> 3;
+    p = x * (per / KB) + i / KB;
+    kq = i % KB;
+  } else {
+    p = b / KB;
+    kq = b - p * KB;
+  }
+}
+
 // One wave's attention split; ring[0] holds its first K/V tile, read during the third gate.
 template <int HD, int RING>
 struct AttPre {
@@ -456,8 +471,8 @@ struct AttPre {
   bool on;       // this wave runs a split
 };
 
-// Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair
-// blockIdx / KB, split (blockIdx % KB) * 8 + wave of 8 KB -- and its first tile.  With one
+// Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair and part
+// kq of att_pair, split kq * 8 + wave of 8 KB -- and its first tile.  With one
 // row per cache every slot below pos[r] is final before the launch; the split's cache part
 // stops below slot pos[r], which comes from the hand-off, so no line of that slot is read.
 template <int HD, int RING>
@@ -472,9 +487,10 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
     sp = 0;
   } else {
     const int KB = NB / pairs;
-    p = b / KB;
+    int kq;
+    att_pair(b, NB, KB, p, kq);
     ns = KB * CW;
-    sp = (b - p * KB) * CW + wv;
+    sp = kq * CW + wv;
   }
   pf.on = p < pairs;
   pf.lo = pf.hi = 0;
@@ -700,7 +716,8 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
   const int pairs = a.M * a.Hk;
   if (a.L <= ATT_SHORT) return true;  // the waves wrote o
   const int KB = NB / pairs;
-  const int p = b / KB, kq = b - p * KB;
+  int p, kq;
+  att_pair(b, NB, KB, p, kq);
   const int r = p / a.Hk, kh = p - r * a.Hk;
   uint64_t* base = (uint64_t*)(a.ws + ws_att_offset(a.D)) + (long)p * KB * G * PW;
   uint64_t* part = base + (long)kq * G * PW;
