@@ -244,11 +244,21 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
                 return launch(q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale, **kw)
             return f
 
-    _ffi.call, E._attn = rec_call, RecAttn()
+    # a stack's layer-0 head launch runs that layer's attention: its cache lengths
+    head_lens = []
+    orig_head = E.layer_head
+
+    def rec_head(x, nxt, o_next, F, *a, **kw):
+        L = nxt["L"]
+        head_lens.append(((nxt["pos"].cpu() + 1).clamp(0, L).tolist(), x.shape[0], nxt["Hq"],
+                          nxt["Hk"], nxt["HD"]))
+        return orig_head(x, nxt, o_next, F, *a, **kw)
+
+    _ffi.call, E._attn, E.layer_head = rec_call, RecAttn(), rec_head
     try:
         model._step(static["tok"], static["pos"], Lcap, 1.5, 50, 1.0)
     finally:
-        _ffi.call, E._attn = orig_call, orig_attn
+        _ffi.call, E._attn, E.layer_head = orig_call, orig_attn, orig_head
     torch.cuda.synchronize()
 
     def gemv_family_bytes(name, a):
@@ -276,6 +286,11 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
                 Nq = (Hq + 2 * Hk) * HD
                 b += Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD
             return b
+        if name == "ecd_layer_head":
+            # rms -> q|k|v of layer 0 (its attention is counted by tail_attn_bytes)
+            M, D, Hq, Hk, HD = a[13], a[14], a[17], a[18], a[20]
+            Nq = (Hq + 2 * Hk) * HD
+            return Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD
         if name == "ecd_embed_gemv_i8p":
             M, N, K = a[12], a[13], a[14]
             ev = 2 * (M // 2) * K if a[7] else 0
@@ -283,13 +298,19 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
         return None
 
     # a layer-tail launch with o_next (argument 17) also runs the next layer's decode attention:
-    # its cache lengths are those of the stack's layer-0 attention launch, the latest before it
+    # its cache lengths are those of the stack's layer-0 attention (a decode-attention launch or
+    # the head launch), the latest before it
     tail_att = {}
-    k_att, last = -1, None
+    k_att, k_head, last = -1, -1, None
     for i, (n, a) in enumerate(calls):
         if n == "ecd_decode_attn":
             k_att += 1
             last = attn_lens[k_att]
+        elif n == "ecd_layer_head":
+            k_head += 1
+            last = head_lens[k_head]
+            lens, R, Hq, Hk, HD = last
+            tail_att[i] = attn_bytes(R, Hq, Hk, HD, lens)
         elif n == "ecd_layer_tail" and a[17]:
             lens, R, Hq, Hk, HD = last
             tail_att[i] = attn_bytes(R, Hq, Hk, HD, lens)

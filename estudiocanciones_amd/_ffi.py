@@ -88,6 +88,8 @@ SIGNATURES = {
     "ecd_layer_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                        _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                        c_float, c_int, _P],
+    "ecd_layer_head": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int,
+                       c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P],
     "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "ecd_layer_tail_ws_bytes": [c_int, c_int, c_int, c_int],
 }

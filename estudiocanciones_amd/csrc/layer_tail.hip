@@ -801,7 +801,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ uint32_t s_epoch;  // the gate count after the third gate (loader -> compute waves)
@@ -844,93 +844,118 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     constexpr int ARING = AG <= 3 ? 2 : 1;
     AttPre<(AHD > 0 ? AHD : 32), ARING> pf;
     const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
-    // this wave's slice of the attention output first (the inputs of this launch are final)
-    dma_rows<CD>(a.o, D, M, c0D, xs, lane);
-    u32x4 wo[1][CD];
-    u32x4 w13[NT13][CD];
-    const int to_t[1] = {tO < 0 ? 0 : tO};
-    int t13[NT13];
-#pragma unroll
-    for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
-    if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
-    load_w_chunks<NT13, CD, NTL, 0, 1, 0>(w13, a.w13, t13, nchD, c0D, lane);
-
-    // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
-    // wait for this wave's o slice and W_O (the NT13 W13 loads issued after them may fly on)
-    {
-      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-      if (tO >= 0) {
-        wait_vm<NT13>();
-        mfma_chunks<1, CD>(acc, wo, xs, nws, c0D, lane, 0.f, false);
-      }
-      put_partials<1>(psD, acc, wv, lane);
-    }
-    wait_lgkm0();
-    bar();  // P(O)
-    load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
-    u32x4 w2[1][C2];
-    const int t2_t[1] = {t2 < 0 ? 0 : t2};
-
-    // phase W13 (x = rms(x1, n2))
-    bar();  // X(W13): x1 is complete
-    dma_rows<CD>(a.x1, D, M, c0D, xs, lane);
-    dma_nw<CD>(a.n2, c0D, nws, lane);
-    wait_vm0();
-    rms_partial<CD>(xs, c0D, lane, wv, ss);
-    wait_lgkm0();
-    bar();  // S(W13)
-    {
-      const float inv = rms_inv(ss, lane, D, a.eps);
-      f32x4 acc[NT13];
-#pragma unroll
-      for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
-      mfma_chunks_then<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        if (t2 >= 0)
-          load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
-                                                                            c0F, lane);
-      });
-      put_partials<NT13>(psD, acc, wv, lane);
-    }
-    wait_lgkm0();
-    bar();  // P(W13)
-
     u32x4 wq[2][CD];
     const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
-    // the next layer's q|k|v weights go out during the second gate, into the registers the
-    // W13 phase freed (HBM would idle there otherwise)
-    if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
-    else if (tq0 >= 0)
-      load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
-                                           nchD, c0D, lane);
+    if constexpr (!HEAD) {
+      // this wave's slice of the attention output first (the inputs of this launch are final)
+      dma_rows<CD>(a.o, D, M, c0D, xs, lane);
+      u32x4 wo[1][CD];
+      u32x4 w13[NT13][CD];
+      const int to_t[1] = {tO < 0 ? 0 : tO};
+      int t13[NT13];
+#pragma unroll
+      for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
+      if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
+      load_w_chunks<NT13, CD, NTL, 0, 1, 0>(w13, a.w13, t13, nchD, c0D, lane);
 
-    // phase W2 (x = mm)
-    bar();  // X(W2): mm is complete
-    dma_rows<C2>(a.mm, F, M, c0F, xs, lane);
-    wait_vm0();
-    {
-      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-      if (t2 >= 0) mfma_chunks<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false);
-      put_partials<1>(psF, acc, wv, lane);
-    }
-    wait_lgkm0();
-    bar();  // P(W2)
-
-    if (has_next) {
-      // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
-      // they stream during the third gate, and the loader's hand-off stores after the q|k|v
-      // phase do not queue behind them
-      if constexpr (AHD > 0) {
-        if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+      // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
+      // wait for this wave's o slice and W_O (the NT13 W13 loads issued after them may fly on)
+      {
+        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+        if (tO >= 0) {
+          wait_vm<NT13>();
+          mfma_chunks<1, CD>(acc, wo, xs, nws, c0D, lane, 0.f, false);
+        }
+        put_partials<1>(psD, acc, wv, lane);
       }
-      // phase QKV (x = rms(xout, n1'))
-      bar();  // X(QKV): xout is complete
-      dma_rows<CD>(a.xout, D, M, c0D, xs, lane);
-      dma_nw<CD>(a.n1, c0D, nws, lane);
+      wait_lgkm0();
+      bar();  // P(O)
+      load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
+      u32x4 w2[1][C2];
+      const int t2_t[1] = {t2 < 0 ? 0 : t2};
+
+      // phase W13 (x = rms(x1, n2))
+      bar();  // X(W13): x1 is complete
+      dma_rows<CD>(a.x1, D, M, c0D, xs, lane);
+      dma_nw<CD>(a.n2, c0D, nws, lane);
       wait_vm0();
       rms_partial<CD>(xs, c0D, lane, wv, ss);
       wait_lgkm0();
+      bar();  // S(W13)
+      {
+        const float inv = rms_inv(ss, lane, D, a.eps);
+        f32x4 acc[NT13];
+#pragma unroll
+        for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
+        mfma_chunks_then<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          if (t2 >= 0)
+            load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
+                                                                              c0F, lane);
+        });
+        put_partials<NT13>(psD, acc, wv, lane);
+      }
+      wait_lgkm0();
+      bar();  // P(W13)
+
+      // the next layer's q|k|v weights go out during the second gate, into the registers the
+      // W13 phase freed (HBM would idle there otherwise)
+      if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+      else if (tq0 >= 0)
+        load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
+                                             nchD, c0D, lane);
+
+      // phase W2 (x = mm)
+      bar();  // X(W2): mm is complete
+      dma_rows<C2>(a.mm, F, M, c0F, xs, lane);
+      wait_vm0();
+      {
+        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+        if (t2 >= 0) mfma_chunks<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false);
+        put_partials<1>(psF, acc, wv, lane);
+      }
+      wait_lgkm0();
+      bar();  // P(W2)
+    }
+
+    if (has_next) {
+      if constexpr (HEAD) {
+        // head launch (x = xin, final at launch start): x slice, then the layer's q|k|v
+        // weights, the only weights (all at once); the RMS waits for the x slice only
+        dma_rows<CD>(a.xin, D, M, c0D, xs, lane);
+        dma_nw<CD>(a.n1, c0D, nws, lane);
+        if (tq1 >= 0) {
+          load_w_chunks<2, CD, NTL, 0, CD, 0>(wq, a.wq, tq_t, nchD, c0D, lane);
+          wait_vm<2 * CD>();
+        } else if (tq0 >= 0) {
+          load_w_chunks<1, CD, NTL, 0, CD, 0>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
+                                              nchD, c0D, lane);
+          wait_vm<CD>();
+        } else {
+          wait_vm0();
+        }
+        rms_partial<CD>(xs, c0D, lane, wv, ss);
+        if constexpr (AHD > 0) {
+          if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+        }
+        wait_lgkm0();
+        bar();  // X(QKV)
+      } else {
+        // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
+        // they stream during the third gate, and the loader's hand-off stores after the q|k|v
+        // phase do not queue behind them
+        if constexpr (AHD > 0) {
+          if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+        }
+        // phase QKV (x = rms(xout, n1'))
+        bar();  // X(QKV): xout is complete
+        dma_rows<CD>(a.xout, D, M, c0D, xs, lane);
+        dma_nw<CD>(a.n1, c0D, nws, lane);
+        wait_vm0();
+        rms_partial<CD>(xs, c0D, lane, wv, ss);
+        wait_lgkm0();
+      }
       bar();  // S(QKV)
       const float inv = rms_inv(ss, lane, D, a.eps);
       f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
@@ -959,14 +984,16 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
   // epilogue operands that do not depend on this launch's phases
   f16x4 so4 = {}, xr4 = {}, s2v = {};
-  f16x4 s13v[NT13];
-  if (tO >= 0) {
-    so4 = *(const f16x4*)(a.so + 16 * tO + cg);
-    if (mrow) xr4 = *(const f16x4*)(a.xin + (long)me * D + 16 * tO + cg);
-  }
+  f16x4 s13v[NT13] = {};
+  if constexpr (!HEAD) {
+    if (tO >= 0) {
+      so4 = *(const f16x4*)(a.so + 16 * tO + cg);
+      if (mrow) xr4 = *(const f16x4*)(a.xin + (long)me * D + 16 * tO + cg);
+    }
 #pragma unroll
-  for (int t = 0; t < NT13; ++t) s13v[t] = *(const f16x4*)(a.s13 + 16 * (b * NT13 + t) + cg);
-  if (t2 >= 0) s2v = *(const f16x4*)(a.s2 + 16 * t2 + cg);
+    for (int t = 0; t < NT13; ++t) s13v[t] = *(const f16x4*)(a.s13 + 16 * (b * NT13 + t) + cg);
+    if (t2 >= 0) s2v = *(const f16x4*)(a.s2 + 16 * t2 + cg);
+  }
   const int HD = a.HD, L = a.L;
   const int tq[2] = {tq0, tq1};
   f16x4 sqv[2] = {};
@@ -989,86 +1016,100 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     }
   }
 
-  // phase O
-  bar();  // P(O)
-  if (tO >= 0) {
-    const f16x4 y = scale4(sum_partials<1>(psD, 0, lane), so4);
-    if (mrow) st_sc1_u64(a.x1 + (long)me * D + 16 * tO + cg, y + xr4);
-  }
-  wait_vm0();
-  if (lane == 0) {
-    gate_arrive(a.sync, grp, per, go);
-    ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-    ++go;
-  }
-
-  // phase W13 (the W2 epilogue's residual x1 is final now: read it before the weight stream of
-  // the next phases is in flight)
-  f16x4 r2 = {};
-  if (t2 >= 0 && mrow)
-    r2 = __builtin_bit_cast(f16x4, __hip_atomic_load((const uint64_t*)(a.x1 + (long)me * D + 16 * t2 + cg),
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  bar();  // X(W13)
-  bar();  // S(W13)
-  bar();  // P(W13)
-  {
-    f16x2 o[NT13];
-#pragma unroll
-    for (int t = 0; t < NT13; ++t) {
-      // interleaved w1 | w3 rows: (a_j, b_j, a_j+1, b_j+1), j = column / 2
-      const f16x4 y = scale4(sum_partials<NT13>(psD, t, lane), s13v[t]);
-      const float a0 = (float)y[0], a1 = (float)y[2];
-      o[t].x = (f16)(a0 / (1.0f + expf(-a0))) * y[1];
-      o[t].y = (f16)(a1 / (1.0f + expf(-a1))) * y[3];
+  if constexpr (!HEAD) {
+    // phase O
+    bar();  // P(O)
+    if (tO >= 0) {
+      const f16x4 y = scale4(sum_partials<1>(psD, 0, lane), so4);
+      if (mrow) st_sc1_u64(a.x1 + (long)me * D + 16 * tO + cg, y + xr4);
     }
-    if (mrow)
-#pragma unroll
-      for (int t = 0; t < NT13; ++t)
-        st_sc1_u32(a.mm + (long)me * F + ((16 * (b * NT13 + t) + cg) >> 1), o[t]);
-  }
-  wait_vm0();
-  if (lane == 0) {
-    gate_arrive(a.sync, grp, per, go);
-    ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-    ++go;
-  }
-
-  // phase W2
-  bar();  // X(W2)
-  bar();  // P(W2)
-  if (KS2 == 1) {
-    if (t2 >= 0) {
-      const f16x4 y = scale4(sum_partials<1>(psF, 0, lane), s2v) + r2;
-      if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
-    }
-  } else {
-    // this workgroup's K-part -> workspace; the last of the tile's KS2 workgroups (its count
-    // modulo KS2; the counters only grow) adds the KS2 parts in K order and stores xout
-    float* wp = a.ws + ((long)(t2 * KS2 + ks2) * 64 + lane) * 4;
-    st_sc1_f32x4(wp, sum_partials<1>(psF, 0, lane));
-    wait_vm0();
-    uint32_t old = 0;
-    if (lane == 0) old = add_agent(a.sync + CNT2 + t2);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old % KS2 == KS2 - 1) {
-      f32x4 acc = ld_sc1_f32x4(a.ws + ((long)(t2 * KS2) * 64 + lane) * 4);
-#pragma unroll
-      for (int k = 1; k < KS2; ++k) acc += ld_sc1_f32x4(a.ws + ((long)(t2 * KS2 + k) * 64 + lane) * 4);
-      const f16x4 y = scale4(acc, s2v) + r2;
-      if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
-    }
-  }
-
-  if (has_next) {
     wait_vm0();
     if (lane == 0) {
       gate_arrive(a.sync, grp, per, go);
       ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
       ++go;
-      s_epoch = go;
+    }
+
+    // phase W13 (the W2 epilogue's residual x1 is final now: read it before the weight stream of
+    // the next phases is in flight)
+    f16x4 r2 = {};
+    if (t2 >= 0 && mrow)
+      r2 = __builtin_bit_cast(f16x4, __hip_atomic_load((const uint64_t*)(a.x1 + (long)me * D + 16 * t2 + cg),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    bar();  // X(W13)
+    bar();  // S(W13)
+    bar();  // P(W13)
+    {
+      f16x2 o[NT13];
+#pragma unroll
+      for (int t = 0; t < NT13; ++t) {
+        // interleaved w1 | w3 rows: (a_j, b_j, a_j+1, b_j+1), j = column / 2
+        const f16x4 y = scale4(sum_partials<NT13>(psD, t, lane), s13v[t]);
+        const float a0 = (float)y[0], a1 = (float)y[2];
+        o[t].x = (f16)(a0 / (1.0f + expf(-a0))) * y[1];
+        o[t].y = (f16)(a1 / (1.0f + expf(-a1))) * y[3];
+      }
+      if (mrow)
+#pragma unroll
+        for (int t = 0; t < NT13; ++t)
+          st_sc1_u32(a.mm + (long)me * F + ((16 * (b * NT13 + t) + cg) >> 1), o[t]);
+    }
+    wait_vm0();
+    if (lane == 0) {
+      gate_arrive(a.sync, grp, per, go);
+      ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+      ++go;
+    }
+
+    // phase W2
+    bar();  // X(W2)
+    bar();  // P(W2)
+    if (KS2 == 1) {
+      if (t2 >= 0) {
+        const f16x4 y = scale4(sum_partials<1>(psF, 0, lane), s2v) + r2;
+        if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+      }
+    } else {
+      // this workgroup's K-part -> workspace; the last of the tile's KS2 workgroups (its count
+      // modulo KS2; the counters only grow) adds the KS2 parts in K order and stores xout
+      float* wp = a.ws + ((long)(t2 * KS2 + ks2) * 64 + lane) * 4;
+      st_sc1_f32x4(wp, sum_partials<1>(psF, 0, lane));
+      wait_vm0();
+      uint32_t old = 0;
+      if (lane == 0) old = add_agent(a.sync + CNT2 + t2);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old % KS2 == KS2 - 1) {
+        f32x4 acc = ld_sc1_f32x4(a.ws + ((long)(t2 * KS2) * 64 + lane) * 4);
+#pragma unroll
+        for (int k = 1; k < KS2; ++k) acc += ld_sc1_f32x4(a.ws + ((long)(t2 * KS2 + k) * 64 + lane) * 4);
+        const f16x4 y = scale4(acc, s2v) + r2;
+        if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
+      }
+    }
+  }
+
+  if (has_next) {
+    if constexpr (!HEAD) {
+      wait_vm0();
+      if (lane == 0) {
+        gate_arrive(a.sync, grp, per, go);
+        ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
+        ++go;
+        s_epoch = go;
+      }
+    } else {
+      if (lane == 0) s_epoch = go + 1;
     }
     wait_lgkm0();
     bar();  // X(QKV)
+    if constexpr (HEAD) {
+      // the gate count moves on by one, arrivals only (every workgroup read it at launch
+      // start), so that the next launch's epoch differs from this one's
+      if (lane == 0) {
+        gate_arrive(a.sync, grp, per, go);
+        ++go;
+      }
+    }
     bar();  // S(QKV)
     bar();  // P(QKV)
     const bool pval = p_raw >= 0 && p_raw < L;
@@ -1133,7 +1174,7 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD>
 int launch(const Args& a, int nb, hipStream_t st) {
   const int xd = CD * CW * CHB, xf = CF * CW * CHB;
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
@@ -1145,12 +1186,12 @@ int launch(const Args& a, int nb, hipStream_t st) {
   // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
   static int attr = 0;
   if (lds > attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return (int)e;
     attr = lds;
   }
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -1169,6 +1210,47 @@ static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
   // KB = nb / pairs workgroups per pair, each merging HD / KB columns
   const int kb = nb / pairs;
   return nb % pairs == 0 && kb <= tail::ATT_KB_MAX && HD % kb == 0;
+}
+
+extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, const void* sq,
+                              const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
+                              void* o_next, void* sync, void* err, void* ws, int M, int D, int F,
+                              int S, int Hq, int Hk, int L, int HD, float eps, int flags,
+                              void* stream) {
+  tail::Args a = {};
+  a.xin = (const f16*)xin;
+  a.n1 = (const f16*)n1; a.wq = (const int8_t*)wq; a.sq = (const f16*)sq;
+  a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
+  a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
+  a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
+  a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
+  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!xin || !n1 || !wq || !sq || !rope || !pos || !q || !kc || !vc || !o_next || !sync ||
+      !err || !ws || M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) ||
+      S <= 0 || Hq <= 0 || Hk <= 0 || (Hq % Hk) || L <= 0 || HD <= 0 || (HD % 4) ||
+      (Hq + 2 * Hk) * HD % 16 || !al(xin) || !al(n1) || !al(wq) || !al(o_next) || !al(ws) ||
+      ((uintptr_t)sync & 255))
+    return ECD_EINVAL;
+  if (S != 1) return ECD_ENOTSUP;  // the hand-off holds one new slot per cache
+  const int nb = tail::device_cus();
+  const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
+  const int t13 = 2 * F / 16;
+  if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb) return ECD_ENOTSUP;
+  if ((Hq + 2 * Hk) * HD / 16 > 2 * nb || !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
+  const int nt13 = t13 / nb;
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
+  const int ag = Hq / Hk;
+  const bool ntl = (flags >> 1) & 1;
+  hipStream_t st = (hipStream_t)stream;
+#define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_)                                           \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_)      \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true>(a, nb, st)       \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true>(a, nb, st);
+  ECD_HEAD(6, 16, 4, 1, 128, 3)
+  ECD_HEAD(2, 16, 4, 4, 128, 4)
+#undef ECD_HEAD
+  return ECD_ENOTSUP;
 }
 
 extern "C" long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD) {
@@ -1229,8 +1311,8 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
 #define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_)                                          \
   if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ && \
       ag == AG_)                                                                         \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true>(a, nb, st)            \
-               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false>(a, nb, st);
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false>(a, nb, st)     \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false>(a, nb, st);
   // 3072 -> 2 x 8192 -> 3072: the backbone (with its attention: 24q / 8kv, head_dim 128) and
   // the reference's depth decoder (head_dim 384: attention launched on its own)
   ECD_TAIL(6, 16, 4, 1, 128, 3)

@@ -34,7 +34,8 @@ import torch
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
                       gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
-                      gemm_rope_packed, gemv_packed, int8_mm, layer_tail, layer_tail_supported,
+                      gemm_rope_packed, gemv_packed, int8_mm, layer_head, layer_tail,
+                      layer_tail_supported,
                       layer_tail_ws_bytes, next_power_of_2,
                       pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_w13_silu,
                       sample_topk, stream_ptr)
@@ -327,24 +328,32 @@ class Stack:
         return krms(x, self.norm) if final_norm else x
 
     def _decode_tail(self, x, pos, S, ns):
-        """Layer 0's rms + q|k|v + RoPE + cache write and attention run first on their own; then
-        one ecd_layer_tail launch per layer: the O projection, the MLP, the next layer's rms +
-        q|k|v + RoPE + cache write and (where the shapes allow) that layer's attention, else
-        attention (+ split combine) as its own launches.  Returns the last layer's output (a
-        buffer of the stack, valid until the next decode call)."""
+        """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
+        ecd_layer_head launch where the shapes allow attention in the launch, else on their
+        own; then one ecd_layer_tail launch per layer: the O projection, the MLP, the next
+        layer's rms + q|k|v + RoPE + cache write and (where the shapes allow) that layer's
+        attention, else attention (+ split combine) as its own launches.  Returns the last
+        layer's output (a buffer of the stack, valid until the next decode call)."""
         t = self.tail
         q = t["q"]
+        att = t["att"] and self.tail_attention and S == 1
+
+        def nxt_of(b):
+            return dict(n1=b.n1, wq=b.qkv.qp, sq=b.qkv.s8, rope=self.rope, pos=pos, q=q, kc=b.kc,
+                        vc=b.vc, S=S, Hq=b.h, Hk=b.kvh, L=b.kc.shape[2], HD=b.hd)
+
         b0 = self.blocks[0]
-        rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
-                     b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
-        o = self._attention(b0, q, pos, S, ns)
+        if att:
+            o = layer_head(x, nxt_of(b0), t["ob"][1], b0.w2.K, t["sync"], t["err"], t["ws"],
+                           stream=b0.qkv.stream)
+        else:
+            rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
+                         b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
+            o = self._attention(b0, q, pos, S, ns)
         for i, b in enumerate(self.blocks):
             nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
-            nxt = None if nb is None else dict(
-                n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, rope=self.rope, pos=pos, q=q, kc=nb.kc,
-                vc=nb.vc, S=S, Hq=nb.h, Hk=nb.kvh, L=nb.kc.shape[2], HD=nb.hd)
-            o_next = t["ob"][i % 2] if (t["att"] and self.tail_attention and nb is not None and
-                                        S == 1) else None
+            nxt = None if nb is None else nxt_of(nb)
+            o_next = t["ob"][i % 2] if (att and nb is not None) else None
             x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
                            t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], t["ws"],
                            nxt=nxt, o_next=o_next, stream=b.w13.stream)

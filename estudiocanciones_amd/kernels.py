@@ -568,6 +568,45 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     return xout
 
 
+def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False):
+    """A stack's first layer up to its attention as one launch (app/engine.py:189-204 for layer
+    0): rms(x, n1) -> q|k|v -> RoPE -> q and the cache slot, and the decode attention into
+    o_next [M, Hq * HD].  ``nxt`` as for layer_tail (that layer's n1, wq, ..., S = 1); F: the
+    stack's FFN width; sync, err, ws: the stack's layer_tail buffers."""
+    dev = _dev(x, "layer_head")
+    M, D = x.shape
+    _f16(x, "layer_head x")
+    _f16(o_next, "layer_head o_next")
+    n = nxt
+    pos, kc = n["pos"], n["kc"]
+    S, Hq, Hk, L, HD = n["S"], n["Hq"], n["Hk"], n["L"], n["HD"]
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        raise ValueError("layer_head: x must be contiguous and 16-byte aligned")
+    if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+        raise ValueError("layer_head: pos must be contiguous int64 [M]")
+    if kc.shape != (kc.shape[0], Hk, L, HD) or kc.shape[0] * S < M or n["vc"].shape != kc.shape:
+        raise ValueError("layer_head: caches must be [B, Hk, L, HD] with B * S >= M")
+    if n["q"].numel() != M * Hq * HD or not n["q"].is_contiguous():
+        raise ValueError("layer_head: q must be contiguous [M, Hq * HD]")
+    if n["rope"].shape[0] < L or n["rope"].shape[1] != HD // 2:
+        raise ValueError("layer_head: rope table must be float32 [>= L, HD/2, 2]")
+    if o_next.numel() != M * Hq * HD or not o_next.is_contiguous() or o_next.data_ptr() % 16:
+        raise ValueError("layer_head: o_next must be contiguous [M, Hq * HD]")
+    if sync.dtype != torch.int32 or sync.numel() < 2048 or sync.data_ptr() % 256:
+        raise ValueError("layer_head: sync must be int32 [>= 2048], 256-byte aligned")
+    if err.dtype != torch.int32 or err.numel() < 1:
+        raise ValueError("layer_head: err must be int32 [1]")
+    if ws.dtype != torch.float32 or ws.data_ptr() % 16 or \
+            ws.numel() * 4 < layer_tail_ws_bytes(D, Hq, Hk, HD):
+        raise ValueError("layer_head: ws must be float32, 16-byte aligned, layer_tail_ws_bytes")
+    _ffi.call("ecd_layer_head", x.data_ptr(), n["n1"].data_ptr(), n["wq"].data_ptr(),
+              n["sq"].data_ptr(), n["rope"].data_ptr(), pos.data_ptr(), n["q"].data_ptr(),
+              kc.data_ptr(), n["vc"].data_ptr(), o_next.data_ptr(), sync.data_ptr(),
+              err.data_ptr(), ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
+              _flags(M, stream), stream_ptr(dev))
+    return o_next
+
+
 def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False):
     """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
     interleave (even[b], emb[b]) and the output has 2B rows.  ``table`` holds int8 rows scaled by

@@ -230,6 +230,20 @@ int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* s
                    void* ws, int M, int D, int F, int S, int Hq, int Hk, int L, int HD,
                    float eps, int flags, void* stream);
 
+/* A stack's first layer up to its attention, as one launch of the ecd_layer_tail kernel without
+ * the O projection and the MLP (app/engine.py:189-204 for layer 0): rms(xin, n1) -> q|k|v (wq
+ * packed, sq) -> RoPE -> q and the cache slot at pos, and the decode attention into o_next
+ * [M, Hq * HD], with q and the new slot handed to the attention as tagged words.  Replaces
+ * ecd_rms_qkv_rope + ecd_decode_attn (+ ecd_attn_combine) for one row per cache (S = 1, else
+ * ECD_ENOTSUP) and the shapes ecd_layer_tail_supported(M, D, F, Hq, Hk, HD, L, 1) accepts; F is
+ * the stack's FFN width (the launch shape).  sync, err and ws as for ecd_layer_tail, shared
+ * with the stack's ecd_layer_tail calls (the launch moves the gate count on by one).  No
+ * reference counterpart as one call. */
+int ecd_layer_head(const void* xin, const void* n1, const void* wq, const void* sq,
+                   const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
+                   void* o_next, void* sync, void* err, void* ws, int M, int D, int F, int S,
+                   int Hq, int Hk, int L, int HD, float eps, int flags, void* stream);
+
 /* ECD_OK when ecd_layer_tail accepts these shapes on the current device (M rows, model width
  * D, FFN width F, heads, L cache slots; attention != 0: with the next layer's attention in the
  * launch), ECD_ENOTSUP otherwise.  No reference counterpart. */

@@ -8,7 +8,7 @@ handed to the oracle as codes and bf16 scales."""
 import numpy as np
 import pytest
 
-from helpers import assert_close16, assert_within_noise, randn16, rng
+from helpers import ATOL, RTOL, assert_close16, assert_within_noise, randn16, rng
 from oracle import kernels as OK
 from oracle.model import OLinear, OStack
 
@@ -134,10 +134,10 @@ def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream):
 @pytest.mark.parametrize("cfg,L,stream", [(dict(BB3, layers=2), 512, True),
                                           (dict(DEC3, layers=2), 8, False)])
 def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
-    """The tail path against the per-op fused kernels on the same stack (same numerics up to
-    the fp32 summation order), then five more launches from identical state give identical
-    bits (the gate region and, for the 1024-wide shape, the split-w2 counters are reused), and
-    a captured graph of the decode replays bit-equal."""
+    """The tail path (head launch + tails) against the per-op fused kernels on the same stack
+    (same numerics up to the fp32 summation order), then five more launches from identical
+    state give identical bits (the gate region and, for the 1024-wide shape, the split-w2
+    counters are reused), and a captured graph of the decode replays bit-equal."""
     import torch
     B = 8
     ost, st = _stacks(dev, cfg, seed=11, B=B, L=L, stream=stream)
@@ -160,7 +160,13 @@ def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
         outs.append(st.decode(x, pos, 1).clone())
     torch.cuda.synchronize()
     assert not st.tail_error()
-    assert_close16(N(outs[0]), N(ref), what="tail vs per-op kernels")
+    # the attention splits differ (the launches split a pair's cache over their own waves, the
+    # decode kernel over its split count), layer 0 included: the same function up to the fp32
+    # summation order, so the fp16 kernel bar holds for all but a few elements, and 3x it for all
+    got, want = N(outs[0]).astype(np.float32), N(ref).astype(np.float32)
+    err, bound = np.abs(got - want), ATOL + RTOL * np.abs(want)
+    assert (err > bound).mean() <= 1e-3, f"tail vs per-op kernels: {(err > bound).sum()} past the bar"
+    assert (err <= 3 * bound).all(), f"tail vs per-op kernels: max abs err {err.max():.3e}"
     for o in outs[1:]:
         assert torch.equal(o, outs[0]), "repeated tail launches differ"
     # graph capture and replay
