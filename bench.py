@@ -113,8 +113,11 @@ def time_graph(calls, torch, reps=20):
 
 
 def is_backbone_tail(name):
-    """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6)."""
-    return "layer_tail_kernel<6," in name or "layer_tail_kernelILi6E" in name
+    """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6: the
+    frame's 28 tail launches), not its head launch (last template argument true)."""
+    import re
+    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false>", name)
+                or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0E", name))
 
 
 def pmc_summary(fetch_csv, write_csv, calib_mib):

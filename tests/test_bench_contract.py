@@ -30,26 +30,32 @@ def _counter_csv(path, counter, rows):
 
 
 def test_pmc_summary_copy_calibration(tmp_path):
-    """Backbone layer-tail KiB per dispatch (demangled or mangled names; the decoder's tail and
-    other kernels excluded) are averaged, then divided by the factor the calibration copy gives
+    """Backbone layer-tail KiB per dispatch (demangled or mangled names; the decoder's tail, the
+    head launch, the last layer's tail and other kernels excluded) are averaged, then divided by the factor the calibration copy gives
     (its counter reading over its known size): a counter that reads 2x the true bytes on the
     copy reads 2x on the tail too."""
     sys.path.insert(0, str(ROOT))
     import bench
     calib_mib = 4
     fetch, write = tmp_path / "fetch.csv", tmp_path / "write.csv"
-    bb = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true>(ecd::tail::Args)"
-    bb_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1EEEvNS0_4ArgsE"
-    dec = "void ecd::tail::layer_tail_kernel<2, 16, 4, 4, 128, 4, false>(ecd::tail::Args)"
-    # fetch counter over-reads 2x: copy of 4 MiB reads 8192 KiB; the tails read 300 and 500 KiB
+    bb = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, false>(ecd::tail::Args)"
+    bb_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb0EEEvNS0_4ArgsE"
+    dec = "void ecd::tail::layer_tail_kernel<2, 16, 4, 4, 128, 4, false, false>(ecd::tail::Args)"
+    head = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, true>(ecd::tail::Args)"
+    head_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb1EEEvNS0_4ArgsE"
+    last = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 0, 0, true, false>(ecd::tail::Args)"
+    # fetch counter over-reads 2x: copy of 4 MiB reads 8192 KiB; the tails read 300, 500 and
+    # 400 KiB (the decoder's tail and the backbone's head launch are not counted)
     _counter_csv(fetch, "FETCH_SIZE", [(bb, [100.0, 200.0]), (bb_mangled, [500.0]),
-                                       (dec, [7777.0]), ("other_kernel", [9999.0]),
+                                       (dec, [7777.0]), (head, [55.0]), (head_mangled, [66.0]),
+                                       (last, [400.0]), ("other_kernel", [9999.0]),
                                        ("copy_bytes_kernel", [4096.0, 4096.0])])
     # write counter exact: copy reads 4096 KiB; the tails write 16 and 48 KiB
-    _counter_csv(write, "WRITE_SIZE", [(bb, [16.0]), (bb_mangled, [48.0]), (dec, [1.0]),
+    _counter_csv(write, "WRITE_SIZE", [(bb, [16.0]), (bb_mangled, [48.0]), (last, [32.0]),
+                                       (dec, [1.0]), (head, [5.0]),
                                        ("copy_bytes_kernel", [4096.0])])
     out = bench.pmc_summary(str(fetch), str(write), calib_mib)
-    assert out["fetch"]["tail_dispatches"] == 2 and out["write"]["tail_dispatches"] == 2
+    assert out["fetch"]["tail_dispatches"] == 3 and out["write"]["tail_dispatches"] == 3
     assert out["fetch"]["factor"] == 2.0 and out["write"]["factor"] == 1.0
     assert out["fetch"]["bytes_per_tail_launch"] == 400 * 1024 // 2
     assert out["write"]["bytes_per_tail_launch"] == 32 * 1024
