@@ -1224,7 +1224,7 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
   a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
-  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
+  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   if (!xin || !n1 || !wq || !sq || !rope || !pos || !q || !kc || !vc || !o_next || !sync ||
       !err || !ws || M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) ||
@@ -1281,7 +1281,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
   a.x1 = (f16*)x1; a.mm = (f16*)mm; a.xout = (f16*)xout;
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
-  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = 1 << 17;
+  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   if (!o || !xin || !wo || !so || !n2 || !w13 || !s13 || !w2 || !s2 || !x1 || !mm || !xout ||
       !sync || !err || M < 1 || M > tail::MR || D <= 0 || F <= 0 || (D % 512) || (F % 512) ||

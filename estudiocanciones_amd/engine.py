@@ -218,6 +218,7 @@ class Stack:
         self.tail = None
         self.use_tail = True
         self.tail_attention = True  # the next layer's attention inside the tail launch
+        self.tail_no_wait = False   # tests of the error path: every wait in the launches gives up
 
     def alloc(self, B, L, dev, dtype):
         self.rope = rope_cache(self.hd, max(L, 16), device=dev)
@@ -251,6 +252,13 @@ class Stack:
     def tail_error(self):
         """True if a layer-tail launch of this stack timed out waiting at a gate (host sync)."""
         return self.tail is not None and int(self.tail["err"].item()) != 0
+
+    def tail_reset(self):
+        """Zero the launches' gate region, workspace and error word (after a timeout their
+        contents are undefined)."""
+        if self.tail is not None:
+            for k in ("sync", "ws", "err"):
+                self.tail[k].zero_()
 
     def free(self):
         for b in self.blocks:
@@ -345,7 +353,7 @@ class Stack:
         b0 = self.blocks[0]
         if att:
             o = layer_head(x, nxt_of(b0), t["ob"][1], b0.w2.K, t["sync"], t["err"], t["ws"],
-                           stream=b0.qkv.stream)
+                           stream=b0.qkv.stream, no_wait=self.tail_no_wait)
         else:
             rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
                          b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
@@ -356,7 +364,8 @@ class Stack:
             o_next = t["ob"][i % 2] if (att and nb is not None) else None
             x = layer_tail(o, x, b.o.qp, b.o.s8, b.n2, b.w13.qp, b.w13.sp, b.w2.qp, b.w2.s8,
                            t["x1"], t["mm"], t["xb"][i % 2], t["sync"], t["err"], t["ws"],
-                           nxt=nxt, o_next=o_next, stream=b.w13.stream)
+                           nxt=nxt, o_next=o_next, stream=b.w13.stream,
+                           no_wait=self.tail_no_wait)
             if nb is not None:
                 o = o_next if o_next is not None else self._attention(nb, q, pos, S, ns)
         return x

@@ -505,7 +505,7 @@ def layer_tail_ws_bytes(D, Hq, Hk, HD):
 
 
 def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws, nxt=None,
-               o_next=None, eps=1e-5, stream=False):
+               o_next=None, eps=1e-5, stream=False, no_wait=False):
     """One launch for the tail of a decode layer (app/engine.py:206-210: O projection +
     residual, rms -> w1|w3 -> SiLU * mul, w2 + residual) and, with ``nxt``, the next layer's
     rms -> q|k|v -> RoPE -> q, cache slot (:189-192) and, with ``o_next`` [M, Hq * HD], that
@@ -514,7 +514,8 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     (packed), sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 2048], zero before
     first use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of
     layer_tail_ws_bytes bytes, zero before first use and kept with its ``sync`` (partials are
-    recognised by the sync region's gate count)."""
+    recognised by the sync region's gate count).  ``no_wait``: every wait gives up at once (tests
+    of the error path: err becomes 1 and sync, ws and err must be zeroed before the next call)."""
     dev = _dev(o, "layer_tail")
     M, D = o.shape
     F = mm.shape[1]
@@ -563,16 +564,17 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
               n2.data_ptr(), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *nargs,
               _ptr(o_next), x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(),
               err.data_ptr(),
-              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps), _flags(M, stream),
-              stream_ptr(dev))
+              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
+              _flags(M, stream) | (4 if no_wait else 0), stream_ptr(dev))
     return xout
 
 
-def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False):
+def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait=False):
     """A stack's first layer up to its attention as one launch (app/engine.py:189-204 for layer
     0): rms(x, n1) -> q|k|v -> RoPE -> q and the cache slot, and the decode attention into
     o_next [M, Hq * HD].  ``nxt`` as for layer_tail (that layer's n1, wq, ..., S = 1); F: the
-    stack's FFN width; sync, err, ws: the stack's layer_tail buffers."""
+    stack's FFN width; sync, err, ws: the stack's layer_tail buffers; ``no_wait`` as for
+    layer_tail."""
     dev = _dev(x, "layer_head")
     M, D = x.shape
     _f16(x, "layer_head x")
@@ -603,7 +605,7 @@ def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False):
               n["sq"].data_ptr(), n["rope"].data_ptr(), pos.data_ptr(), n["q"].data_ptr(),
               kc.data_ptr(), n["vc"].data_ptr(), o_next.data_ptr(), sync.data_ptr(),
               err.data_ptr(), ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
-              _flags(M, stream), stream_ptr(dev))
+              _flags(M, stream) | (4 if no_wait else 0), stream_ptr(dev))
     return o_next
 
 

@@ -216,12 +216,14 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.
  * sync: an 8 KB, 256-byte aligned region, zero before the first call, kept for later calls (the
  * kernel leaves it reusable); calls sharing a sync region must not overlap in time.  err: a
- * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results then
- * undefined).  ws: a 16-byte aligned workspace of ecd_layer_tail_ws_bytes bytes, zero before the
- * first call and kept with its sync region (a launch recognises its attention partials by the
- * region's gate count; calls on another sync region must use another ws).  The grid is one workgroup per CU with all workgroups resident.  flags bit 1:
- * nontemporal weight loads.  No reference counterpart as one call: it replaces up to seven
- * reference launches. */
+ * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results, sync
+ * and ws then undefined: zero sync, ws and err before the next call).  ws: a 16-byte aligned
+ * workspace of ecd_layer_tail_ws_bytes bytes, zero before the first call and kept with its sync
+ * region (a launch recognises its attention partials by the region's gate count; calls on
+ * another sync region must use another ws).  The grid is one workgroup per CU with all
+ * workgroups resident.  flags bit 1: nontemporal weight loads; bit 2: no waiting at all (every
+ * wait gives up at its first look: tests of the error path).  No reference counterpart as one
+ * call: it replaces up to seven reference launches. */
 int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
                    const void* n2, const void* w13, const void* s13, const void* w2,
                    const void* s2, const void* n1, const void* wq, const void* sq,

@@ -185,3 +185,40 @@ def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
         torch.cuda.synchronize()
         assert torch.equal(gout, outs[0]), "graph replay of the tail path differs from eager"
     assert not st.tail_error()
+
+
+@pytest.mark.parametrize("cfg,L", [(dict(BB3, layers=2), 512), (dict(DEC3, layers=2), 8)])
+def test_tail_timeout_sets_err_and_reset_recovers(dev, cfg, L):
+    """The error path, forced from the host: with every wait of the launches giving up at its
+    first look (gates, hand-off and merge polls), the launches still end and the error word
+    reports it; after Stack.tail_reset the same decode matches the per-op path again."""
+    import torch
+    B = 8
+    ost, st = _stacks(dev, cfg, seed=21, B=B, L=L, stream=False)
+    _fill(ost, st, seed=22, upto=L)
+    kv0 = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
+
+    def reset():
+        for b, (k, v) in zip(st.blocks, kv0):
+            b.kc.copy_(k)
+            b.vc.copy_(v)
+
+    x = torch.from_numpy(randn16(23, B, cfg["dim"])).to(dev)
+    pos = torch.from_numpy(rng(24).integers(0, L, B).astype(np.int64)).to(dev)
+    st.use_tail = False
+    ref = st.decode(x, pos, 1).clone()
+    st.use_tail = True
+    reset()
+    st.tail_no_wait = True
+    st.decode(x, pos, 1)
+    torch.cuda.synchronize()
+    assert st.tail_error()
+    st.tail_no_wait = False
+    st.tail_reset()
+    reset()
+    got = N(st.decode(x, pos, 1)).astype(np.float32)
+    torch.cuda.synchronize()
+    assert not st.tail_error()
+    want = N(ref).astype(np.float32)
+    err, bound = np.abs(got - want), ATOL + RTOL * np.abs(want)
+    assert (err > bound).mean() <= 1e-3 and (err <= 3 * bound).all()
