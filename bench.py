@@ -116,8 +116,8 @@ def is_backbone_tail(name):
     """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6: the
     frame's 28 tail launches), not its head launch (last template argument true)."""
     import re
-    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false>", name)
-                or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0E", name))
+    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false, \d+>", name)
+                or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0ELi\d+E", name))
 
 
 def pmc_summary(fetch_csv, write_csv, calib_mib):
@@ -335,13 +335,14 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     bt_bytes = sum(b for _, _, b in bt) / len(bt) if bt else None
     bt_att = bool(bt) and bool(bt[0][1][17])
     bb_idx = [i for i, b in enumerate(attn_b) if b > 10e6]
-    a_ms_launch = time_graph([relaunch(*attn_calls[i]) for i in range(len(attn_calls))], torch)
+    # (no standalone attention launch is left when every layer's attention runs in a launch)
+    a_ms_launch = time_graph([relaunch(*c) for c in attn_calls], torch) if attn_calls else 0.0
     a_ms_total = a_ms_launch * len(attn_calls)
     bb_ms = time_graph([relaunch(*attn_calls[i]) for i in bb_idx], torch) if bb_idx else None
     g_avg_us = g_ms_launch * 1e3
     g_bytes_avg = sum(gemv_b) / len(gemv_b)
     g_gbps = sum(gemv_b) / (g_ms_total * 1e-3) / 1e9
-    a_gbps = sum(attn_b) / (a_ms_total * 1e-3) / 1e9
+    a_gbps = sum(attn_b) / (a_ms_total * 1e-3) / 1e9 if attn_calls else None
     bb_attn_gbps = (sum(attn_b[i] for i in bb_idx) / (bb_ms * len(bb_idx) * 1e-3) / 1e9) if bb_idx else None
     frame_bytes = sum(gemv_b) + sum(attn_b)
     launches = len(calls)
@@ -422,7 +423,8 @@ def main():
             "kv_len": args.target_kv, "steps": args.target_steps,
             "value": round(tp["fps"], 2), "unit": "frames/s", "ms_per_step": round(tp["ms"], 4),
             "gemv_frac": round(tp["g_gbps"] / HBM_PEAK_GBPS, 4),
-            "decode_attn_frac": round(tp["a_gbps"] / HBM_PEAK_GBPS, 4),
+            "decode_attn_frac": (round(tp["a_gbps"] / HBM_PEAK_GBPS, 4) if tp["a_gbps"]
+                                 else None),
             "backbone_attn_GBps": round(tp["bb_attn_gbps"], 1) if tp["bb_attn_gbps"] else None,
             "backbone_attn_frac": (round(tp["bb_attn_gbps"] / HBM_PEAK_GBPS, 4)
                                    if tp["bb_attn_gbps"] else None),
@@ -509,10 +511,10 @@ def main():
             "launches_per_frame": len(gemv_b),
         },
         "decode_attn": {
-            "achieved_GBps": round(a_gbps, 1),
-            "frac": round(a_gbps / HBM_PEAK_GBPS, 4),
+            "achieved_GBps": round(a_gbps, 1) if a_gbps else None,
+            "frac": round(a_gbps / HBM_PEAK_GBPS, 4) if a_gbps else None,
             "backbone_layer_GBps": round(bb_attn_gbps, 1) if bb_attn_gbps else None,
-            "avg_launch_us": round(a_ms_launch * 1e3, 3),
+            "avg_launch_us": round(a_ms_launch * 1e3, 3) if attn_b else None,
             "launches_per_frame": len(attn_b),
         },
         "frame": {

@@ -58,8 +58,9 @@ namespace tail {
 
 constexpr int CW = 8;                // compute waves per workgroup
 constexpr int NTHR = (CW + 1) * 64;  // plus the loader wave
-constexpr int MR = 8;                // rows held in the x tile (M <= MR)
-constexpr int CHB = 128 * MR;        // LDS bytes per 64-column chunk of the x tile
+constexpr int MR = 16;               // rows a launch takes (M <= MR; x tiles of R = 8 or 16 rows)
+// LDS bytes per 64-column chunk of an x tile of R rows
+__host__ __device__ constexpr int chb(int R) { return 128 * R; }
 constexpr int CNT2 = 640;            // sync words [640, 1024): split-W2 arrival counters per tile
 constexpr int MAX_T2_SPLIT = 384;    // tiles a split W2 can have (sync region words)
 constexpr int ATT_SHORT = 128;       // caches of at most this many slots: one split per pair
@@ -197,23 +198,28 @@ __device__ __forceinline__ void lds_dma16_sc1(const void* base, uint32_t off, vo
                : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
 }
 
-// Activation rows [M, K] (row stride ld halfs) -> LDS x tile: chunk c (columns 64c .. 64c + 63)
-// occupies CHB bytes as [grp 4][row MR][16 halfs], grp = the 16-column group, i.e. exactly the
-// B fragments of the two MFMAs of the chunk.  Each compute wave copies its own chunks
-// [c0, c0 + C), one DMA instruction per chunk; lane l moves 16 bytes: grp = l >> 4,
-// row = (l >> 1) & 7, half h = l & 1.  Rows past M repeat row M - 1 (their products land in
-// output rows that are never stored).
-template <int C>
-__device__ __forceinline__ void dma_rows(const f16* x, long ld, int M, int c0, unsigned char* xs,
+// Activation rows [M, K] (row stride ld halfs) -> LDS x tile of R rows: chunk c (columns 64c ..
+// 64c + 63) occupies chb(R) bytes as [grp 4][row R][16 halfs], grp = the 16-column group, i.e.
+// exactly the B fragments of the two MFMAs of the chunk.  Each compute wave copies its own
+// chunks [c0, c0 + C) to dst (the LDS address of chunk c0), R / 8 DMA instructions per chunk;
+// in instruction i lane l moves 16 bytes: grp = i * 8 / R + l / 2R, row = (l >> 1) % R, half
+// h = l & 1.  Rows past M repeat row M - 1 (their products land in output rows that are never
+// stored).
+template <int C, int R>
+__device__ __forceinline__ void dma_rows(const f16* x, long ld, int M, int c0, unsigned char* dst,
                                          int lane) {
-  const int grp = lane >> 4, row = (lane >> 1) & 7, h = lane & 1;
+  constexpr int NI = R / 8;  // DMA instructions per chunk, 4 / NI column groups each
+  const int row = (lane >> 1) % R, h = lane & 1, gl = lane / (2 * R);
   const int rs = row < M ? row : M - 1;
-  const uint32_t off0 = (uint32_t)(((long)rs * ld + 64 * c0 + 16 * grp + 8 * h) * 2);
 #pragma unroll
-  for (int u = 0; u < C; ++u) {
-    lds_dma16_sc1(x, off0 + (uint32_t)u * 128u, xs + (c0 + u) * CHB);
-    if ((u & 15) == 15) wait_vm<32>();  // at most ~48 DMA instructions in flight
-  }
+  for (int u = 0; u < C; ++u)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int grp = i * (4 / NI) + gl;
+      lds_dma16_sc1(x, (uint32_t)(((long)rs * ld + 64 * (c0 + u) + 16 * grp + 8 * h) * 2),
+                    dst + u * chb(R) + i * 1024);
+      if (((u * NI + i) & 15) == 15) wait_vm<32>();  // at most ~48 DMA instructions in flight
+    }
 }
 
 // The norm-weight columns of chunks [c0, c0 + C) -> LDS at the same offsets (C * 128 bytes:
@@ -224,12 +230,13 @@ __device__ __forceinline__ void dma_nw(const f16* v, int c0, unsigned char* dst,
   if (lane < C * 8) lds_dma16_sc1(v + 64 * c0, (uint32_t)(16 * lane), dst + 128 * c0);
 }
 
-// B fragments of chunk c for this lane (row lane & 15; zero for rows >= MR)
+// B fragments of chunk c of an R-row tile for this lane (row lane & 15; zero for rows >= R)
+template <int R>
 __device__ __forceinline__ void xfrag(const unsigned char* xs, int c, int lane, f16x8& fa,
                                       f16x8& fb) {
   const int row = lane & 15, grp = lane >> 4;
-  if (row < MR) {
-    const unsigned char* p = xs + c * CHB + (grp * MR + row) * 32;
+  if (row < R) {
+    const unsigned char* p = xs + c * chb(R) + (grp * R + row) * 32;
     fa = *(const f16x8*)p;
     fb = *(const f16x8*)(p + 16);
   } else {
@@ -253,14 +260,14 @@ __device__ __forceinline__ void rms_frag(f16x8& fa, f16x8& fb, const unsigned ch
 
 // Sum of squares of this wave's chunks [c0, c0 + C) per row, reduced over the wave's four
 // column groups; the per-wave sums go to ss[wave][row] in LDS.
-template <int C>
+template <int C, int R>
 __device__ __forceinline__ void rms_partial(const unsigned char* xs, int c0, int lane, int wv,
                                             float* ss) {
   float acc = 0.f;
 #pragma unroll
   for (int u = 0; u < C; ++u) {
     f16x8 fa, fb;
-    xfrag(xs, c0 + u, lane, fa, fb);
+    xfrag<R>(xs, c0 + u, lane, fa, fb);
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
       const f16x2 pa = (f16x2){fa[e], fa[e + 1]};
@@ -271,12 +278,13 @@ __device__ __forceinline__ void rms_partial(const unsigned char* xs, int c0, int
   }
   acc += __shfl_xor(acc, 16, 64);
   acc += __shfl_xor(acc, 32, 64);
-  if (lane < MR) ss[wv * 16 + lane] = acc;
+  if (lane < R) ss[wv * 16 + lane] = acc;
 }
 
+template <int R>
 __device__ __forceinline__ float rms_inv(const float* ss, int lane, int K, float eps) {
   const int row = lane & 15;
-  if (row >= MR) return 0.f;
+  if (row >= R) return 0.f;
   float t = 0.f;
 #pragma unroll
   for (int w = 0; w < CW; ++w) t += ss[w * 16 + row];
@@ -305,7 +313,7 @@ __device__ __forceinline__ void i8x16_to_f16_biased(const u32x4& v, f16x8& lo, f
 // 1152 (its result is the same for every tile: lane l holds the sum of column l & 15).  Every
 // product is exact in fp32; only the accumulation order of the fp32 sums differs from the
 // unbiased form.
-template <int NT, int C>
+template <int NT, int C, int R>
 __device__ __forceinline__ void mfma_chunks(f32x4 (&acc)[NT], const u32x4 (&w)[NT][C],
                                             const unsigned char* xs, const unsigned char* nws,
                                             int c0, int lane, float inv, bool rms) {
@@ -315,7 +323,7 @@ __device__ __forceinline__ void mfma_chunks(f32x4 (&acc)[NT], const u32x4 (&w)[N
 #pragma unroll
   for (int u = 0; u < C; ++u) {
     f16x8 fa, fb;
-    xfrag(xs, c0 + u, lane, fa, fb);
+    xfrag<R>(xs, c0 + u, lane, fa, fb);
     if (rms) rms_frag(fa, fb, nws, c0 + u, lane, inv);
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fa, corr, 0, 0, 0);
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fb, corr, 0, 0, 0);
@@ -344,7 +352,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // mfma_chunks with a hook after each chunk: after(integral_constant u) issues the next phase's
 // weight loads into registers the finished chunks leave free, so the stream keeps going during
 // the MFMAs.
-template <int NT, int C, typename After>
+template <int NT, int C, int R, typename After>
 __device__ __forceinline__ void mfma_chunks_then(f32x4 (&acc)[NT], const u32x4 (&w)[NT][C],
                                                  const unsigned char* xs, const unsigned char* nws,
                                                  int c0, int lane, float inv, bool rms,
@@ -355,7 +363,7 @@ __device__ __forceinline__ void mfma_chunks_then(f32x4 (&acc)[NT], const u32x4 (
   static_for<C>([&](auto uc) {
     constexpr int u = decltype(uc)::value;
     f16x8 fa, fb;
-    xfrag(xs, c0 + u, lane, fa, fb);
+    xfrag<R>(xs, c0 + u, lane, fa, fb);
     if (rms) rms_frag(fa, fb, nws, c0 + u, lane, inv);
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fa, corr, 0, 0, 0);
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fb, corr, 0, 0, 0);
@@ -466,15 +474,16 @@ struct AttPre {
   long cbase;    // this pair's cache [L, HD] (K and V alike)
   int r, kh;     // row and kv head of the pair
   int lo, hi;    // the split's tokens held in the cache before the launch
-  int pn;        // the slot this launch writes (L: none)
-  bool nw;       // the split ends with slot pn, taken from the hand-off
+  int p0;        // the cache's first slot written in this launch (L: none)
+  int nlo, nhi;  // the split's tokens written in this launch, taken from the hand-off
   bool on;       // this wave runs a split
 };
 
 // Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair and part
-// kq of att_pair, split kq * 8 + wave of 8 KB -- and its first tile.  With one
-// row per cache every slot below pos[r] is final before the launch; the split's cache part
-// stops below slot pos[r], which comes from the hand-off, so no line of that slot is read.
+// kq of att_pair, split kq * 8 + wave of 8 KB -- and its first tile.  The S rows of a cache
+// write consecutive slots p0 .. p0 + S - 1 (p0 = the position of its first row), and every slot
+// below p0 is final before the launch: the split's cache part stops below p0, and its tokens
+// from p0 on come from the hand-off, so no line of a slot written here is read.
 template <int HD, int RING>
 __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int wv, int lane,
                                              AttPre<HD, RING>& pf) {
@@ -493,18 +502,18 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
     sp = kq * CW + wv;
   }
   pf.on = p < pairs;
-  pf.lo = pf.hi = 0;
-  pf.nw = false;
+  pf.lo = pf.hi = pf.nlo = pf.nhi = 0;
   if (!pf.on) return;
   pf.r = p / Hk;
   pf.kh = p - pf.r * Hk;
-  pf.cbase = ((long)(pf.r / a.S) * Hk + pf.kh) * (long)L * HD;
+  const int c = pf.r / a.S;  // the row's cache
+  pf.cbase = ((long)c * Hk + pf.kh) * (long)L * HD;
   split_range(a.pos, pf.r, L, ns, sp, pf.lo, pf.hi);
-  const long praw = a.pos[pf.r];
-  const int pn = (praw >= 0 && praw < L) ? (int)praw : L;  // the slot written here (L: none)
-  pf.pn = pn;
-  pf.nw = pf.lo <= pn && pn < pf.hi;
-  pf.hi = min(pf.hi, pn);
+  const long praw = a.pos[c * a.S];
+  pf.p0 = (praw >= 0 && praw < L) ? (int)praw : L;
+  pf.nlo = max(pf.lo, pf.p0);
+  pf.nhi = pf.hi;
+  pf.hi = min(pf.hi, pf.p0);
   if (pf.lo < pf.hi) kv_load<HD>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.hi - 1, lane);
 }
 
@@ -618,11 +627,17 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
 #pragma unroll
     for (int r = 1; r < RING; ++r) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
   }
-  // the new slot's K and V words go out with the q polls (one round trip)
-  const uint64_t* hk = hw + (((long)pf.r * NQ + (long)(Hq + pf.kh) * HD) >> 1);
-  const uint64_t* hv = hw + (((long)pf.r * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
+  // the split's new slots: slot t from row (cache's first row + t - p0); the first one's K and
+  // V words go out with the q polls (one round trip)
+  auto hkv = [&](int t, const uint64_t*& hk, const uint64_t*& hv) {
+    const long j = (long)(pf.r / a.S) * a.S + (t - pf.p0);
+    hk = hw + ((j * NQ + (long)(Hq + pf.kh) * HD) >> 1);
+    hv = hw + ((j * NQ + (long)(Hq + a.Hk + pf.kh) * HD) >> 1);
+  };
+  const uint64_t *hk = hw, *hv = hw;
   uint64_t nk = 0, nv = 0;
-  if (pf.nw) {
+  if (pf.nlo < pf.nhi) {
+    hkv(pf.nlo, hk, hv);
     nk = get_tagged(hk + lane);
     nv = get_tagged(hv + lane);
   }
@@ -635,7 +650,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   }
   SplitStateM<HD, G> ss;
   attn_run_m<HD, G, RING, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
-  if (pf.nw) ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, pf.pn, a.scale, lane, a.spin_max, nk, nv) && ok;
+  for (int t = pf.nlo; t < pf.nhi; ++t) {
+    if (t > pf.nlo) {
+      hkv(t, hk, hv);
+      nk = get_tagged(hk + lane);
+      nv = get_tagged(hv + lane);
+    }
+    ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, t, a.scale, lane, a.spin_max, nk, nv) && ok;
+  }
   if (!ok && lane == 0) store_agent(a.err, 1u);
   if (a.L <= ATT_SHORT) {
     attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
@@ -801,7 +823,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ uint32_t s_epoch;  // the gate count after the third gate (loader -> compute waves)
@@ -831,12 +853,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int tq0 = b < TQ ? b : -1;
   const int tq1 = (xtra > 0 && b >= NB - xtra) ? NB + (b - (NB - xtra)) : -1;
 
-  const int XD = nchD * CHB;
+  const int XD = nchD * chb(R);
   unsigned char* xs = smem;
   unsigned char* nws = smem + XD;
   float* ss = (float*)(smem + XD + 2 * D);
   unsigned char* psD = smem + XD + 2 * D + 512;  // partials of the K = D phases
-  unsigned char* psF = smem + nchF * CHB;        // partials of the W2 phase
+  unsigned char* psF = smem + C2 * CW * chb(R);  // partials of the W2 phase
 
   if (wv < CW) {
     // ------------------------------------------------------------------ compute waves
@@ -848,7 +870,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
     if constexpr (!HEAD) {
       // this wave's slice of the attention output first (the inputs of this launch are final)
-      dma_rows<CD>(a.o, D, M, c0D, xs, lane);
+      dma_rows<CD, R>(a.o, D, M, c0D, xs + c0D * chb(R), lane);
       u32x4 wo[1][CD];
       u32x4 w13[NT13][CD];
       const int to_t[1] = {tO < 0 ? 0 : tO};
@@ -864,7 +886,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
         if (tO >= 0) {
           wait_vm<NT13>();
-          mfma_chunks<1, CD>(acc, wo, xs, nws, c0D, lane, 0.f, false);
+          mfma_chunks<1, CD, R>(acc, wo, xs, nws, c0D, lane, 0.f, false);
         }
         put_partials<1>(psD, acc, wv, lane);
       }
@@ -876,19 +898,19 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
       // phase W13 (x = rms(x1, n2))
       bar();  // X(W13): x1 is complete
-      dma_rows<CD>(a.x1, D, M, c0D, xs, lane);
+      dma_rows<CD, R>(a.x1, D, M, c0D, xs + c0D * chb(R), lane);
       dma_nw<CD>(a.n2, c0D, nws, lane);
       wait_vm0();
-      rms_partial<CD>(xs, c0D, lane, wv, ss);
+      rms_partial<CD, R>(xs, c0D, lane, wv, ss);
       wait_lgkm0();
       bar();  // S(W13)
       {
-        const float inv = rms_inv(ss, lane, D, a.eps);
+        const float inv = rms_inv<R>(ss, lane, D, a.eps);
         f32x4 acc[NT13];
 #pragma unroll
         for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
         // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
-        mfma_chunks_then<NT13, CD>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
+        mfma_chunks_then<NT13, CD, R>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
           constexpr int u = decltype(uc)::value;
           if (t2 >= 0)
             load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
@@ -908,11 +930,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
       // phase W2 (x = mm)
       bar();  // X(W2): mm is complete
-      dma_rows<C2>(a.mm, F, M, c0F, xs, lane);
+      // the workgroup's K part of mm: chunks c0F .. of F, at LDS chunks wv * C2 ..
+      dma_rows<C2, R>(a.mm, F, M, c0F, xs + wv * C2 * chb(R), lane);
       wait_vm0();
       {
         f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-        if (t2 >= 0) mfma_chunks<1, C2>(acc, w2, xs, nws, c0F, lane, 0.f, false);
+        if (t2 >= 0) mfma_chunks<1, C2, R>(acc, w2, xs, nws, wv * C2, lane, 0.f, false);
         put_partials<1>(psF, acc, wv, lane);
       }
       wait_lgkm0();
@@ -923,7 +946,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       if constexpr (HEAD) {
         // head launch (x = xin, final at launch start): x slice, then the layer's q|k|v
         // weights, the only weights (all at once); the RMS waits for the x slice only
-        dma_rows<CD>(a.xin, D, M, c0D, xs, lane);
+        dma_rows<CD, R>(a.xin, D, M, c0D, xs + c0D * chb(R), lane);
         dma_nw<CD>(a.n1, c0D, nws, lane);
         if (tq1 >= 0) {
           load_w_chunks<2, CD, NTL, 0, CD, 0>(wq, a.wq, tq_t, nchD, c0D, lane);
@@ -935,7 +958,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         } else {
           wait_vm0();
         }
-        rms_partial<CD>(xs, c0D, lane, wv, ss);
+        rms_partial<CD, R>(xs, c0D, lane, wv, ss);
         if constexpr (AHD > 0) {
           if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
         }
@@ -950,18 +973,19 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         }
         // phase QKV (x = rms(xout, n1'))
         bar();  // X(QKV): xout is complete
-        dma_rows<CD>(a.xout, D, M, c0D, xs, lane);
+        dma_rows<CD, R>(a.xout, D, M, c0D, xs + c0D * chb(R), lane);
         dma_nw<CD>(a.n1, c0D, nws, lane);
         wait_vm0();
-        rms_partial<CD>(xs, c0D, lane, wv, ss);
+        rms_partial<CD, R>(xs, c0D, lane, wv, ss);
         wait_lgkm0();
       }
       bar();  // S(QKV)
-      const float inv = rms_inv(ss, lane, D, a.eps);
+      const float inv = rms_inv<R>(ss, lane, D, a.eps);
       f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
-      if (tq1 >= 0) mfma_chunks<2, CD>(acc, wq, xs, nws, c0D, lane, inv, true);
+      if (tq1 >= 0) mfma_chunks<2, CD, R>(acc, wq, xs, nws, c0D, lane, inv, true);
       else if (tq0 >= 0)
-        mfma_chunks<1, CD>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv, true);
+        mfma_chunks<1, CD, R>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv,
+                              true);
       put_partials<2>(psD, acc, wv, lane);
       wait_lgkm0();
       bar();  // P(QKV)
@@ -1174,9 +1198,9 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R>
 int launch(const Args& a, int nb, hipStream_t st) {
-  const int xd = CD * CW * CHB, xf = CF * CW * CHB;
+  const int xd = CD * CW * chb(R), xf = CF / KS2 * CW * chb(R);
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   // attention: the waves' partials, then the merge's exchange
@@ -1186,12 +1210,12 @@ int launch(const Args& a, int nb, hipStream_t st) {
   // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
   static int attr = 0;
   if (lds > attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return (int)e;
     attr = lds;
   }
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -1232,7 +1256,6 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
       (Hq + 2 * Hk) * HD % 16 || !al(xin) || !al(n1) || !al(wq) || !al(o_next) || !al(ws) ||
       ((uintptr_t)sync & 255))
     return ECD_EINVAL;
-  if (S != 1) return ECD_ENOTSUP;  // the hand-off holds one new slot per cache
   const int nb = tail::device_cus();
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
   const int t13 = 2 * F / 16;
@@ -1241,14 +1264,17 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   const int nt13 = t13 / nb;
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
   const int ag = Hq / Hk;
+  const int rt = M > 8 ? 16 : 8;  // rows of the x tile
   const bool ntl = (flags >> 1) & 1;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_)                                           \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_)      \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true>(a, nb, st)       \
-               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true>(a, nb, st);
-  ECD_HEAD(6, 16, 4, 1, 128, 3)
-  ECD_HEAD(2, 16, 4, 4, 128, 4)
+#define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_, R_)                                          \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_ &&      \
+      rt == R_)                                                                              \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true, R_>(a, nb, st)      \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true, R_>(a, nb, st);
+  ECD_HEAD(6, 16, 4, 1, 128, 3, 8)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 8)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 16)
 #undef ECD_HEAD
   return ECD_ENOTSUP;
 }
@@ -1293,7 +1319,6 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
              (Hq + 2 * Hk) * HD % 16))
     return ECD_EINVAL;
   if (o_next && (!wq || !al(o_next) || !ws)) return ECD_EINVAL;
-  if (o_next && S != 1) return ECD_ENOTSUP;  // the hand-off holds one new slot per cache
   const int nb = tail::device_cus();
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
   const int t13 = 2 * F / 16;
@@ -1306,20 +1331,24 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
   if (ks2 > 1 && (!ws || !al(ws))) return ECD_EINVAL;
   const int ag = o_next ? Hq / Hk : 0;
+  const int rt = M > 8 ? 16 : 8;  // rows of the x tile
   const bool ntl = (flags >> 1) & 1;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_)                                          \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ && \
-      ag == AG_)                                                                         \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false>(a, nb, st)     \
-               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false>(a, nb, st);
+#define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_, R_)                                          \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ &&     \
+      ag == AG_ && rt == R_)                                                                 \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false, R_>(a, nb, st)     \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false, R_>(a, nb, st);
   // 3072 -> 2 x 8192 -> 3072: the backbone (with its attention: 24q / 8kv, head_dim 128) and
-  // the reference's depth decoder (head_dim 384: attention launched on its own)
-  ECD_TAIL(6, 16, 4, 1, 128, 3)
-  ECD_TAIL(6, 16, 4, 1, 0, 0)
-  // 1024 -> 2 x 8192 -> 1024: the 1024-wide depth decoder (8q / 2kv, head_dim 128)
-  ECD_TAIL(2, 16, 4, 4, 128, 4)
-  ECD_TAIL(2, 16, 4, 4, 0, 0)
+  // the reference's depth decoder (head_dim 384: attention launched on its own), up to 8 rows
+  ECD_TAIL(6, 16, 4, 1, 128, 3, 8)
+  ECD_TAIL(6, 16, 4, 1, 0, 0, 8)
+  // 1024 -> 2 x 8192 -> 1024: the 1024-wide depth decoder (8q / 2kv, head_dim 128), up to 16
+  // rows (its first pass: two rows per cache)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 8)
+  ECD_TAIL(2, 16, 4, 4, 0, 0, 8)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 16)
+  ECD_TAIL(2, 16, 4, 4, 0, 0, 16)
 #undef ECD_TAIL
   return ECD_ENOTSUP;
 }
@@ -1334,8 +1363,8 @@ extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int
     return ECD_ENOTSUP;
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW, t13 = 2 * F / 16;
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
-  if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 || !((cd == 6 && ks2 == 1) ||
-                                                               (cd == 2 && ks2 == 4)))
+  if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 ||
+      !((cd == 6 && ks2 == 1 && M <= 8) || (cd == 2 && ks2 == 4)))
     return ECD_ENOTSUP;
   if (Hq <= 0 || Hk <= 0 || (Hq % Hk) || HD <= 0 || (HD % 4) || (Hq + 2 * Hk) * HD % 16 ||
       (Hq + 2 * Hk) * HD / 16 > 2 * nb)

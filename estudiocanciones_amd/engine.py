@@ -215,7 +215,8 @@ class Stack:
         self.hd = dim // cfg["heads"]
         self.max_seq = cfg["max_seq"]
         self.nsplit = 16
-        self.tail = None
+        self.tail = None   # layer-tail buffers for B-row decode steps
+        self.tail2 = None  # the same for 2B rows (two rows per cache), sharing sync, ws and err
         self.use_tail = True
         self.tail_attention = True  # the next layer's attention inside the tail launch
         self.tail_no_wait = False   # tests of the error path: every wait in the launches gives up
@@ -226,8 +227,10 @@ class Stack:
         for b in self.blocks:
             b.alloc(B, L, dev, dtype)
         self.tail = self._tail_buffers(B, dev, dtype, L)
+        self.tail2 = None if self.tail is None else \
+            self._tail_buffers(2 * B, dev, dtype, L, share=self.tail)
 
-    def _tail_buffers(self, M, dev, dtype, L):
+    def _tail_buffers(self, M, dev, dtype, L, share=None):
         """Static buffers of the one-launch layer tail (ecd_layer_tail) for M-row decode steps,
         or None when the shapes or weights do not fit it: x1, mm, two layer outputs used in
         turn (a launch's output never aliases its input), q, the gate region, the error
@@ -243,10 +246,14 @@ class Stack:
         wsb = layer_tail_ws_bytes(self.dim, b0.h, b0.kvh, b0.hd)
         # the next layer's attention inside the launch (its output in one of two buffers)
         att = layer_tail_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd, L, attention=True)
+        if share is not None:  # launches in turn on one stream: one gate region and workspace
+            sync, err, ws = share["sync"], share["err"], share["ws"]
+        else:
+            sync = torch.zeros(2048, device=dev, dtype=torch.int32)
+            err = torch.zeros(1, device=dev, dtype=torch.int32)
+            ws = torch.zeros(-(-wsb // 4), device=dev, dtype=torch.float32)
         return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
-                    q=e(b0.h * b0.hd), sync=torch.zeros(2048, device=dev, dtype=torch.int32),
-                    err=torch.zeros(1, device=dev, dtype=torch.int32),
-                    ws=torch.zeros(-(-wsb // 4), device=dev, dtype=torch.float32),
+                    q=e(b0.h * b0.hd), sync=sync, err=err, ws=ws,
                     att=att, ob=[e(b0.h * b0.hd), e(b0.h * b0.hd)] if att else None)
 
     def tail_error(self):
@@ -263,7 +270,7 @@ class Stack:
     def free(self):
         for b in self.blocks:
             b.kc = b.vc = None
-        self.tail = None
+        self.tail = self.tail2 = None
 
     def __call__(self, x, pos, attn_len=None, mask=None):
         """Prompt pass (app/engine.py:174-178): x [B, S, D], pos [B, S] absolute positions
@@ -321,8 +328,9 @@ class Stack:
             return h if final_norm else None
         R = x.shape[0]
         ns = self.nsplit
-        if self.use_tail and self.tail is not None and R == self.tail["M"]:
-            x = self._decode_tail(x, pos, S, ns)
+        t = next((t for t in (self.tail, self.tail2) if t is not None and R == t["M"]), None)
+        if self.use_tail and t is not None:
+            x = self._decode_tail(x, pos, S, ns, t)
             return krms(x, self.norm) if final_norm else x
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
@@ -335,16 +343,17 @@ class Stack:
             x = b.w2(mm, res=x)
         return krms(x, self.norm) if final_norm else x
 
-    def _decode_tail(self, x, pos, S, ns):
+    def _decode_tail(self, x, pos, S, ns, t):
         """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
         ecd_layer_head launch where the shapes allow attention in the launch, else on their
         own; then one ecd_layer_tail launch per layer: the O projection, the MLP, the next
         layer's rms + q|k|v + RoPE + cache write and (where the shapes allow) that layer's
         attention, else attention (+ split combine) as its own launches.  Returns the last
-        layer's output (a buffer of the stack, valid until the next decode call)."""
-        t = self.tail
+        layer's output (a buffer of the stack, valid until the next decode call).  With several
+        rows per cache (S > 1) the rows of a cache hold consecutive positions.  ``t``: the
+        buffers for R rows."""
         q = t["q"]
-        att = t["att"] and self.tail_attention and S == 1
+        att = t["att"] and self.tail_attention
 
         def nxt_of(b):
             return dict(n1=b.n1, wq=b.qkv.qp, sq=b.qkv.s8, rope=self.rope, pos=pos, q=q, kc=b.kc,

@@ -209,8 +209,9 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  *   (:189-192): q [M, Hq*HD], k/v into kc/vc [B, Hk, L, HD] at pos (row m -> m / S); and, when
  *   o_next is not NULL, that layer's decode attention (ecd_decode_attn + ecd_attn_combine,
  *   :194-204, scale 1/sqrt(HD)) into o_next [M, Hq * HD] -- for head_dim 128 with 3 or 4 query
- *   heads per kv head (ecd_layer_tail_supported tells) and one row per cache (S = 1, else
- *   ECD_ENOTSUP).
+ *   heads per kv head (ecd_layer_tail_supported tells); with several rows per cache (S > 1)
+ *   the rows of a cache hold consecutive positions p .. p + S - 1.  M <= 8 rows for the
+ *   3072-wide shape, M <= 16 for the 1024-wide one (ecd_layer_tail_supported tells).
  * Same numerics as the per-op entry points up to the fp32 summation order.  wo / w13 / w2 / wq
  * are ecd_pack_i8 copies (w13 interleaved, s13 interleaved the same way); o, xin, x1, mm,
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.
@@ -236,8 +237,9 @@ int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* s
  * the O projection and the MLP (app/engine.py:189-204 for layer 0): rms(xin, n1) -> q|k|v (wq
  * packed, sq) -> RoPE -> q and the cache slot at pos, and the decode attention into o_next
  * [M, Hq * HD], with q and the new slot handed to the attention as tagged words.  Replaces
- * ecd_rms_qkv_rope + ecd_decode_attn (+ ecd_attn_combine) for one row per cache (S = 1, else
- * ECD_ENOTSUP) and the shapes ecd_layer_tail_supported(M, D, F, Hq, Hk, HD, L, 1) accepts; F is
+ * ecd_rms_qkv_rope + ecd_decode_attn (+ ecd_attn_combine) for the shapes
+ * ecd_layer_tail_supported(M, D, F, Hq, Hk, HD, L, 1) accepts (S > 1: the rows of a cache hold
+ * consecutive positions, as for ecd_layer_tail); F is
  * the stack's FFN width (the launch shape).  sync, err and ws as for ecd_layer_tail, shared
  * with the stack's ecd_layer_tail calls (the launch moves the gate count on by one).  No
  * reference counterpart as one call. */

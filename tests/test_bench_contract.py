@@ -38,12 +38,12 @@ def test_pmc_summary_copy_calibration(tmp_path):
     import bench
     calib_mib = 4
     fetch, write = tmp_path / "fetch.csv", tmp_path / "write.csv"
-    bb = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, false>(ecd::tail::Args)"
-    bb_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb0EEEvNS0_4ArgsE"
-    dec = "void ecd::tail::layer_tail_kernel<2, 16, 4, 4, 128, 4, false, false>(ecd::tail::Args)"
-    head = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, true>(ecd::tail::Args)"
-    head_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb1EEEvNS0_4ArgsE"
-    last = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 0, 0, true, false>(ecd::tail::Args)"
+    bb = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, false, 8>(ecd::tail::Args)"
+    bb_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb0ELi8EEEvNS0_4ArgsE"
+    dec = "void ecd::tail::layer_tail_kernel<2, 16, 4, 4, 128, 4, false, false, 16>(ecd::tail::Args)"
+    head = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 128, 3, true, true, 8>(ecd::tail::Args)"
+    head_mangled = "_ZN3ecd4tail17layer_tail_kernelILi6ELi16ELi4ELi1ELi128ELi3ELb1ELb1ELi8EEEvNS0_4ArgsE"
+    last = "void ecd::tail::layer_tail_kernel<6, 16, 4, 1, 0, 0, true, false, 8>(ecd::tail::Args)"
     # fetch counter over-reads 2x: copy of 4 MiB reads 8192 KiB; the tails read 300, 500 and
     # 400 KiB (the decoder's tail and the backbone's head launch are not counted)
     _counter_csv(fetch, "FETCH_SIZE", [(bb, [100.0, 200.0]), (bb_mangled, [500.0]),

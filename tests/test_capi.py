@@ -112,8 +112,8 @@ def _taps(*offsets):
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 90, 30, 2, 62, 64, None),  # HD % 4
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 16, 16, 100, 30, 2, 64, 64, None),  # M % T
     lambda L: L.ecd_gemm_f16p_rope(16, 64, 16, None, 16, 16, 12, 16, 90, 30, 2, 64, 64, None),  # k align
-    lambda L: L.ecd_layer_tail(*([256] * 24), 9, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0,
-                               None),                                           # M > 8
+    lambda L: L.ecd_layer_tail(*([256] * 24), 17, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0,
+                               None),                                           # M > 16
     lambda L: L.ecd_layer_tail(*([256] * 22), None, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5,
                                0, None),                                        # no err word
     lambda L: L.ecd_layer_tail(*([256] * 21), 16, 256, 256, 8, 3072, 8192, 1, 24, 8, 1024, 128,
@@ -155,27 +155,16 @@ def test_gemm_rejects_x_beyond_32bit_offsets():
 
 
 def test_layer_head_validates_before_launch():
-    """The head launch (a stack's layer 0 rms + q|k|v + attention) rejects missing buffers and a
-    misaligned sync region with ECD_EINVAL, and several rows per cache with ECD_ENOTSUP, before
-    any HIP call."""
+    """The head launch (a stack's layer 0 rms + q|k|v + attention) rejects missing buffers, a
+    misaligned sync region and more than 16 rows with ECD_EINVAL before any HIP call."""
     from estudiocanciones_amd import _ffi
     L = _ffi.lib()
     shape = (8, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0, None)
     assert L.ecd_layer_head(*([256] * 9), None, *([256] * 3), *shape) == _ffi.ECD_EINVAL  # no o_next
     assert L.ecd_layer_head(*([256] * 10), 16, 256, 256, *shape) == _ffi.ECD_EINVAL  # sync 16-aligned
     assert L.ecd_layer_head(*([256] * 12), None, *shape) == _ffi.ECD_EINVAL  # no workspace
-    assert L.ecd_layer_head(*([256] * 13), 8, 3072, 8192, 2, 24, 8, 1024, 128, 1e-5, 0,
-                            None) == _ffi.ECD_ENOTSUP
-
-
-def test_layer_tail_attention_needs_one_row_per_cache():
-    """The layer tail's in-launch attention takes q and the new cache slot from per-launch
-    hand-off words, one slot per cache: several rows per cache (S > 1) with o_next is refused
-    with ECD_ENOTSUP before any HIP call."""
-    from estudiocanciones_amd import _ffi
-    L = _ffi.lib()
-    assert L.ecd_layer_tail(*([256] * 24), 8, 3072, 8192, 2, 24, 8, 1024, 128, 1e-5, 0,
-                            None) == _ffi.ECD_ENOTSUP
+    assert L.ecd_layer_head(*([256] * 13), 17, 3072, 8192, 1, 24, 8, 1024, 128, 1e-5, 0,
+                            None) == _ffi.ECD_EINVAL  # M > 16
 
 
 def test_gemm_rope_validates_before_launch():

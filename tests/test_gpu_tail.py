@@ -222,3 +222,51 @@ def test_tail_timeout_sets_err_and_reset_recovers(dev, cfg, L):
     want = N(ref).astype(np.float32)
     err, bound = np.abs(got - want), ATOL + RTOL * np.abs(want)
     assert (err > bound).mean() <= 1e-3 and (err <= 3 * bound).all()
+
+
+@pytest.mark.parametrize("first", [True, False])
+def test_tail_two_rows_per_cache_vs_oracle(dev, first):
+    """Two rows per cache (the depth decoder's first pass: S = 2, 2B rows at consecutive
+    positions p, p + 1 of each cache) through the head launch and the 16-row tails: the output
+    against the oracle's per-op composition and against the per-op kernels, and the slots each
+    layer's launch wrote."""
+    import torch
+    cfg, B, L = DEC3, 8, 8
+    ost, st = _stacks(dev, cfg, seed=31 + int(first), B=B, L=L, stream=False)
+    assert st.tail2 is not None and st.tail2["att"]
+    _fill(ost, st, seed=32, upto=L)
+    kv0 = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
+    p = np.zeros(B, np.int64) if first else rng(33).integers(0, L - 1, B)
+    pos = np.stack([p, p + 1], 1).reshape(-1).astype(np.int64)
+    x = randn16(34, 2 * B, cfg["dim"])
+    rows = np.arange(2 * B) // 2
+
+    def run_oracle():
+        out = ost.decode(x, pos, 2)
+        return out, [(b.kc[rows, :, pos].copy(), b.vc[rows, :, pos].copy()) for b in ost.blocks]
+
+    want, wslot = run_oracle()
+    OK.GEMV_ACC[0] = np.float32
+    try:
+        alt, aslot = run_oracle()
+    finally:
+        OK.GEMV_ACC[0] = np.float64
+    xt, pt = torch.from_numpy(x).to(dev), torch.from_numpy(pos).to(dev)
+    st.use_tail = False
+    ref = N(st.decode(xt, pt, 2)).astype(np.float32)
+    for b, (k, v) in zip(st.blocks, kv0):
+        b.kc.copy_(k)
+        b.vc.copy_(v)
+    st.use_tail = True
+    got = st.decode(xt, pt, 2)
+    torch.cuda.synchronize()
+    assert not st.tail_error()
+    assert_within_noise(N(got), want, alt, what=f"two rows per cache, first={first}")
+    g = N(got).astype(np.float32)
+    err, bound = np.abs(g - ref), ATOL + RTOL * np.abs(ref)
+    assert (err > bound).mean() <= 1e-3 and (err <= 3 * bound).all()
+    ri, pi = torch.from_numpy(rows).to(dev), pt
+    for i, b in enumerate(st.blocks):
+        gk, gv = N(b.kc[ri, :, pi]), N(b.vc[ri, :, pi])
+        assert_within_noise(gk, wslot[i][0], aslot[i][0], what=f"layer {i} k slots")
+        assert_within_noise(gv, wslot[i][1], aslot[i][1], what=f"layer {i} v slots")
