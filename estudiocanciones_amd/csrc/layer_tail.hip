@@ -1,14 +1,18 @@
 // Layer tail of a decode stack as one persistent launch per layer (gfx950).
 //
-// One launch computes, for a few rows (M <= 8), what the reference runs as five launches plus
-// the next layer's first one (app/engine.py:189-192, 206-209; kernels app/kernels.py:11-107,
-// 170-180):
+// One launch computes, for a few rows (M <= 8, or 16 on 1024-wide layers), what the reference
+// runs as five launches plus the next layer's first ones (app/engine.py:189-209; kernels
+// app/kernels.py:11-180):
 //
 //   phase O    x1   = x + fp16(s_o * (W_o o))                      o-projection + residual
 //   phase W13  mm   = fp16(silu(a)) * b,  a | b = fp16(s * (W1|W3 rms(x1, n2)))
 //   phase W2   xout = x1 + fp16(s_2 * (W2 mm))                      down-projection + residual
 //   phase QKV  q|k|v = fp16(s_q * (Wqkv rms(xout, n1'))), RoPE of q and k, q -> q_out,
 //              k / v -> cache slot pos (the next layer's first step; skipped for the last layer)
+//   phase ATT  the next layer's decode attention into o_next, q and the new K/V slots handed
+//              over in tagged words (no gate)
+//
+// A head launch (HEAD) runs only phases QKV and ATT, on x = xin: a stack's layer 0.
 //
 // with the numerics of the per-op kernels (int8 codes x fp16 in fp32, fp16(acc * s), fp16
 // residual add, the RMSNorm rounding points of app/kernels.py:58-67).
@@ -603,8 +607,8 @@ __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x
 // kernel (attn_core.h), on the splits att_prefetch assigned.  Short caches: the pair's one wave
 // writes o directly.  Long caches: the loader merges its 8 waves' partials (log-sum-exp) into
 // one per workgroup, and the pair's KB workgroups merge those (attention_merge).  Same
-// arithmetic as the split-combine kernel, summed in two levels.  One row per cache: q and the
-// new K/V slot come from the hand-off words of epoch `ep`, with no fourth gate.
+// arithmetic as the split-combine kernel, summed in two levels.  q and the new K/V slots come
+// from the hand-off words of epoch `ep` (no gate after the q|k|v phase).
 template <int HD, int G, int RING>
 __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
                                                 int lane, AttPre<HD, RING>& pf, uint32_t ep) {
@@ -721,7 +725,7 @@ __device__ __forceinline__ void lse_merge(const float* src, int n, int str, int 
 
 // Long caches: the 8 waves' partials (LDS) -> this workgroup's partial [G][m, l, acc[HD]] in the
 // workspace as 8-byte words (fp32 value, epoch), epoch = the gate count this launch reached
-// after its fourth gate (the same in every workgroup, different in every launch on one sync
+// after its last gate (the same in every workgroup, different in every launch on one sync
 // region).  Then each of the pair's KB workgroups merges the KB partials for its HD / KB
 // columns of every head as soon as all the words it needs carry the epoch (polls bounded by
 // spin_max; lanes spread over parts x columns, G * HD / 64 value words and one (m, l) pair each,
@@ -826,7 +830,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ uint32_t s_epoch;  // the gate count after the third gate (loader -> compute waves)
+  __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
   constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
   constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
   const int lane = threadIdx.x & 63;
@@ -836,7 +840,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
   const bool has_next = a.wq != nullptr;
   // the next layer's attention runs in this launch (AHD > 0: its head_dim; AG query heads per
-  // kv head; one row per cache), on q and the new K/V slot handed off in tagged words; caches
+  // kv head), on q and the new K/V slots handed off in tagged words; caches
   // longer than ATT_SHORT slots are split over the KB workgroups of each (row, kv head) pair and
   // their 8 compute waves
   const bool att = AHD > 0 && has_next;
