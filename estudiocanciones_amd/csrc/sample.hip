@@ -14,9 +14,10 @@
 // and the race: every other index has p = 0 exactly and can neither win nor change a sum.
 //   - The k-th largest key: the block's largest key fixes a window of the 16 top-byte digits
 //     below it (about 4 octaves); one LDS bin per key of the window (4096) counts the keys that
-//     fall there (fine bins: the atomics rarely collide), and wave 0 walks the bins from the
-//     top until the count reaches k.  When fewer than k keys lie in the window, a two-pass
-//     radix select over all keys (8-bit digits) finds the threshold instead.
+//     fall there (fine bins: the atomics rarely collide), and a block-wide scan of the bin
+//     counts from the top (4 bins per thread) finds where the count reaches k.  When fewer
+//     than k keys lie in the window, a two-pass radix select over all keys (8-bit digits)
+//     finds the threshold instead.
 //   - The kept values land in LDS in descending key order (first slot of each key from the
 //     walk, then one atomic per value).  Values with equal keys are equal, so the fp32 sums
 //     below see the same sequence of numbers whatever the order among them: results are
@@ -177,8 +178,8 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
     const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
   __shared__ uint32_t hist[2][256];
-  __shared__ uint32_t sel[4];  // threshold key, kept count, fallback flag; radix state
-  __shared__ uint32_t wtot[SMP_THREADS / 64];
+  __shared__ uint32_t sel[4];  // threshold key, kept count; radix state
+  __shared__ __align__(16) uint32_t wtot[SMP_THREADS / 64];
   __shared__ __align__(16) uint32_t wbin[SMP_WBINS_LDS];
   __shared__ int kept_i[SMP_MAXV];
   __shared__ float kept_x[SMP_MAXV];
@@ -239,7 +240,8 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
   kmx = wave_max_u32(kmx);
   if (lane == 0) wtot[wv] = kmx;
-  for (int b = tid; b < SMP_WBINS_LDS; b += SMP_THREADS) wbin[b] = 0u;
+  for (int b = tid; b < SMP_WBINS_LDS / 4; b += SMP_THREADS)
+    ((u32x4*)wbin)[b] = (u32x4){0u, 0u, 0u, 0u};
   __syncthreads();
 
   // 3. histogram of the exact keys within SMP_WDIG digits below the largest one
@@ -253,61 +255,61 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     if (key[j] && key[j] >= kbase) atomicAdd(&wbin[wbin_at(key[j] - kbase)], 1u);
   __syncthreads();
 
-  // 4. wave 0 walks the window from the top: the threshold is the key at which the count from
-  //    the top reaches k; every bin of the lanes at or above it is replaced by the first kept
-  //    slot of its key (kept values are stored in descending key order).  Lane l holds bins
-  //    64 (63 - l) .. +63 (lane 0 the top ones) in 16-byte LDS words.
-  if (wv == 0) {
-    uint32_t* mine = wbin + wbin_at(64 * (63 - lane));
-    uint32_t c = 0u;
+  // 4. the walk from the top, by all threads: thread t owns the 4 window bins 4 (1023 - t) .. +3
+  //    (thread 0 the top ones) as one 16-byte LDS word, and a block-wide scan of their counts
+  //    from the top gives every bin's running count.  The threshold is the key at which the
+  //    running count reaches k; every bin at or above it is replaced by the first kept slot of
+  //    its key (kept values are stored in descending key order).
+  static_assert(SMP_WBINS == 4 * SMP_THREADS, "four window bins per thread");
+  const int b4 = 4 * (SMP_THREADS - 1 - tid);
+  u32x4* const mine = (u32x4*)(wbin + wbin_at((uint32_t)b4));
+  const u32x4 v = *mine;
+  const uint32_t c = (v.x + v.y) + (v.z + v.w);
+  const uint32_t winc = wave_incl_add_u32(c);
+  if (lane == 63) wtot[wv] = winc;  // every thread read kmax from wtot before the last barrier
+  __syncthreads();
+  uint32_t before = 0u, wtotal = 0u;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const u32x4 v = *(const u32x4*)(mine + 4 * q);
-      c += (v.x + v.y) + (v.z + v.w);
+  for (int w4 = 0; w4 < SMP_THREADS / 256; ++w4) {
+    const u32x4 t = ((const u32x4*)wtot)[w4];
+    const uint32_t tw[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      before += 4 * w4 + r < wv ? tw[r] : 0u;
+      wtotal += tw[r];
     }
-    const uint32_t incl = wave_incl_add_u32(c);
-    const uint32_t wtotal = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-    const uint32_t k = (uint32_t)topk;
-    if (wtotal >= k && incl - c < k) {
-      // running count from the top; it never decreases, so the crossing bin is the one after
-      // the `below` bins whose running count is still under k
-      uint32_t acc = incl - c, below = 0u, kept = 0xFFFFFFFFu;
-#pragma unroll
-      for (int q = 15; q >= 0; --q) {
-        const u32x4 v = *(const u32x4*)(mine + 4 * q);
-        const uint32_t h[4] = {v.w, v.z, v.y, v.x};  // descending bins 4q + 3 .. 4q
-        uint32_t f[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          f[r] = acc;
-          acc += h[r];
-          const uint32_t lt = (acc - k) >> 31;  // acc < k (counts < 2^31), no lane masks
-          below += lt;
-          kept = min(kept, acc | (0u - lt));
-        }
-        *(u32x4*)(mine + 4 * q) = (u32x4){f[3], f[2], f[1], f[0]};
-      }
-      if (incl >= k) {  // the lane holding the crossing
-        sel[0] = kbase + (uint32_t)(64 * (63 - lane) + 63) - below;
-        sel[1] = kept;
-      }
+  }
+  const uint32_t k = (uint32_t)topk;
+  const bool window = wtotal >= k;  // otherwise the radix select over all keys
+  const uint32_t excl = before + winc - c;
+  if (window && excl < k) {
+    // running counts after each bin, from the top one (w) down
+    const uint32_t a1 = excl + v.w, a2 = a1 + v.z, a3 = a2 + v.y, a4 = a3 + v.x;
+    *mine = (u32x4){a3, a2, a1, excl};
+    if (a4 >= k) {  // the thread holding the crossing
+      const uint32_t below = (a1 < k ? 1u : 0u) + (a2 < k ? 1u : 0u) + (a3 < k ? 1u : 0u);
+      sel[0] = kbase + (uint32_t)(b4 + 3) - below;
+      sel[1] = below == 0u ? a1 : below == 1u ? a2 : below == 2u ? a3 : a4;
     }
-    if (lane == 0) sel[2] = wtotal >= k ? 0u : 1u;
   }
   __syncthreads();
 
   uint32_t total;
-  if (sel[2] == 0u) {
+  if (window) {
     // 5. kept values (key >= threshold) to their slots; values with equal keys are equal, so
-    //    their order among themselves does not change any sum below
+    //    their order among themselves does not change any sum below.  All the slot atomics are
+    //    issued before the first store waits for one.
     const uint32_t thr = sel[0];
     total = sel[1];
+    uint32_t slot[SMP_PER];
+#pragma unroll
+    for (int j = 0; j < SMP_PER; ++j)
+      if (key[j] && key[j] >= thr) slot[j] = atomicAdd(&wbin[wbin_at(key[j] - kbase)], 1u);
 #pragma unroll
     for (int j = 0; j < SMP_PER; ++j) {
       if (key[j] && key[j] >= thr) {
-        const uint32_t slot = atomicAdd(&wbin[wbin_at(key[j] - kbase)], 1u);
-        kept_i[slot] = slot_index(tid, j);
-        kept_x[slot] = (float)lv[j] / temp;
+        kept_i[slot[j]] = slot_index(tid, j);
+        kept_x[slot[j]] = (float)lv[j] / temp;
       }
     }
   } else {
