@@ -65,8 +65,6 @@ constexpr int NTHR = (CW + 1) * 64;  // plus the loader wave
 constexpr int MR = 16;               // rows a launch takes (M <= MR; x tiles of R = 8 or 16 rows)
 // LDS bytes per 64-column chunk of an x tile of R rows
 __host__ __device__ constexpr int chb(int R) { return 128 * R; }
-constexpr int CNT2 = 640;            // sync words [640, 1024): split-W2 arrival counters per tile
-constexpr int MAX_T2_SPLIT = 384;    // tiles a split W2 can have (sync region words)
 constexpr int ATT_SHORT = 128;       // caches of at most this many slots: one split per pair
 constexpr int ATT_KB_MAX = 16;       // workgroups per (row, kv head) pair, long caches
 
@@ -102,7 +100,7 @@ struct Args {
   float* ws;       // workspace, zero before the first launch on `sync`: split-W2 partial sums
                    // [D / 16][KS2][64][4] (KS2 > 1), the attention's per-workgroup partials
                    // [NB][G][2 + HD] (long caches) and the q|k|v hand-off [MR][Hq + 2 Hk][HD],
-                   // both as tagged words
+                   // all as tagged words
   int M, D, F;
   float eps;
   int spin_max;
@@ -162,7 +160,7 @@ __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t epoch) {
 
 // Workspace float offsets: the attention partials after the split-W2 sums of a D-wide layer,
 // the q|k|v hand-off after the partials of NB workgroups.
-__device__ __forceinline__ long ws_att_offset(int D) { return (long)D * 64; }
+__device__ __forceinline__ long ws_att_offset(int D) { return (long)D * 128; }
 __device__ __forceinline__ long ws_hand_offset(const Args& a, int NB) {
   return ws_att_offset(a.D) + (long)NB * (a.Hq / a.Hk) * (2 + a.HD) * 2;
 }
@@ -849,7 +847,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int TO = D >> 4;
   const int tO = b - (NB - TO);    // >= 0: one O tile
   // W2 (D / 16 tiles too): tile b (KS2 == 1), or tile b / KS2, K-part b % KS2 (host: D / 16 *
-  // KS2 == NB), whose partial sums the last of the KS2 workgroups adds up
+  // KS2 == NB), whose partial sums the K-part 0 workgroup adds up
   const int t2 = KS2 == 1 ? (b < TO ? b : -1) : b / KS2;
   const int ks2 = KS2 == 1 ? 0 : b % KS2;
   const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
@@ -1098,18 +1096,34 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
       }
     } else {
-      // this workgroup's K-part -> workspace; the last of the tile's KS2 workgroups (its count
-      // modulo KS2; the counters only grow) adds the KS2 parts in K order and stores xout
-      float* wp = a.ws + ((long)(t2 * KS2 + ks2) * 64 + lane) * 4;
-      st_sc1_f32x4(wp, sum_partials<1>(psF, 0, lane));
-      wait_vm0();
-      uint32_t old = 0;
-      if (lane == 0) old = add_agent(a.sync + CNT2 + t2);
-      old = __builtin_amdgcn_readfirstlane(old);
-      if (old % KS2 == KS2 - 1) {
-        f32x4 acc = ld_sc1_f32x4(a.ws + ((long)(t2 * KS2) * 64 + lane) * 4);
+      // K-parts 1 .. KS2 - 1 -> workspace as tagged words (epoch: the gate count after the
+      // second gate, new in every launch), and on to the third gate without waiting for them;
+      // the K-part 0 workgroup polls them, adds the KS2 parts in K order and stores xout
+      uint64_t* wt = (uint64_t*)a.ws + ((long)t2 * KS2 * 64 + lane) * 4;
+      const f32x4 part = sum_partials<1>(psF, 0, lane);
+      const uint32_t ep2 = __builtin_amdgcn_readfirstlane(go);
+      if (ks2 != 0) {
+        // (a bit_cast of a vector element directly compiles to one element for every e)
+        const float pe[4] = {part[0], part[1], part[2], part[3]};
 #pragma unroll
-        for (int k = 1; k < KS2; ++k) acc += ld_sc1_f32x4(a.ws + ((long)(t2 * KS2 + k) * 64 + lane) * 4);
+        for (int e = 0; e < 4; ++e) put_tagged(wt + ks2 * 256 + e, __builtin_bit_cast(uint32_t, pe[e]), ep2);
+      } else {
+        f32x4 acc = part;
+#pragma unroll
+        for (int k = 1; k < KS2; ++k) {
+          uint64_t w[4];
+          bool got = false;
+          for (int it = 0;; ++it) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = get_tagged(wt + k * 256 + e);
+            got = tag_is(w[0], ep2) && tag_is(w[1], ep2) && tag_is(w[2], ep2) && tag_is(w[3], ep2);
+            if (__builtin_amdgcn_ballot_w64(!got) == 0 || it >= a.spin_max) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+          ok = ok && __builtin_amdgcn_ballot_w64(!got) == 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] += __builtin_bit_cast(float, (uint32_t)w[e]);
+        }
         const f16x4 y = scale4(acc, s2v) + r2;
         if (mrow) st_sc1_u64(a.xout + (long)me * D + 16 * t2 + cg, y);
       }
@@ -1118,7 +1132,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
   if (has_next) {
     if constexpr (!HEAD) {
-      wait_vm0();
+      // xout stores acknowledged (the split W2's K-parts 1 .. KS2 - 1 stored only tagged words,
+      // which need no acknowledgement)
+      if (KS2 == 1 || ks2 == 0) wait_vm0();
       if (lane == 0) {
         gate_arrive(a.sync, grp, per, go);
         ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
@@ -1266,7 +1282,7 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb) return ECD_ENOTSUP;
   if ((Hq + 2 * Hk) * HD / 16 > 2 * nb || !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
-  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
   const int ag = Hq / Hk;
   const int rt = M > 8 ? 16 : 8;  // rows of the x tile
   const bool ntl = (flags >> 1) & 1;
@@ -1285,9 +1301,10 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
 
 extern "C" long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD) {
   const int nb = tail::device_cus();
-  // the split-W2 sums (D * 64 fp32), the attention partials [NB][G][2 + HD] as 8-byte (fp32,
-  // epoch) words, then the q|k|v hand-off [MR][Hq + 2 Hk][HD] as 8-byte (2 fp16, epoch) words
-  const long w2 = (long)D * 256;
+  // the split-W2 sums (D * 64 fp32), the attention partials [NB][G][2 + HD], all as 8-byte
+  // (fp32, epoch) words, then the q|k|v hand-off [MR][Hq + 2 Hk][HD] as 8-byte (2 fp16, epoch)
+  // words
+  const long w2 = (long)D * 512;
   const long at = Hk > 0 ? (long)nb * (Hq / Hk) * (HD + 2) * 8 : 0;
   const long hd = Hk > 0 ? (long)tail::MR * (Hq + 2 * Hk) * HD * 4 : 0;
   return w2 + at + hd;
@@ -1332,7 +1349,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   if (o_next && !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
   // W2 has D / 16 tiles: with four times as many CUs, K is split over 4 workgroups per tile
-  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4 && D / 16 <= tail::MAX_T2_SPLIT) ? 4 : 1;
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
   if (ks2 > 1 && (!ws || !al(ws))) return ECD_EINVAL;
   const int ag = o_next ? Hq / Hk : 0;
   const int rt = M > 8 ? 16 : 8;  // rows of the x tile

@@ -220,7 +220,8 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results, sync
  * and ws then undefined: zero sync, ws and err before the next call).  ws: a 16-byte aligned
  * workspace of ecd_layer_tail_ws_bytes bytes, zero before the first call and kept with its sync
- * region (a launch recognises its attention partials by the region's gate count; calls on
+ * region (a launch recognises its split-W2 parts and attention partials by the region's gate
+ * count; calls on
  * another sync region must use another ws).  The grid is one workgroup per CU with all
  * workgroups resident.  flags bit 1: nontemporal weight loads; bit 2: no waiting at all (every
  * wait gives up at its first look: tests of the error path).  No reference counterpart as one
