@@ -176,7 +176,8 @@ __device__ uint32_t select_full(const uint32_t (&key)[SMP_PER], const f16 (&lv)[
 __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
-    const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride) {
+    const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride,
+    const f16* __restrict__ rows, long rows_ld, f16* __restrict__ xo, long x_ld, int D) {
   __shared__ uint32_t hist[2][256];
   __shared__ uint32_t sel[4];  // threshold key, kept count; radix state
   __shared__ __align__(16) uint32_t wtot[SMP_THREADS / 64];
@@ -365,6 +366,20 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     out[(long)n * out_stride] = bi;
     if (cfg_on) out[(long)(n + N) * out_stride] = bi;
   }
+  // 8. the next pass's input row of the sampled token (rows [V, D] precomputed from it) into
+  //    x rows n and n + N; zeros if no index won (NaN logits)
+  if (rows) {
+    const bool valid = (uint32_t)bi < (uint32_t)V;
+    const f16* src = rows + (long)(valid ? bi : 0) * rows_ld;
+    f16* d0 = xo + (long)n * x_ld;
+    f16* d1 = xo + (long)(n + N) * x_ld;
+    for (int c = 8 * lane; c < D; c += 512) {
+      f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (valid) v = *(const f16x8*)(src + c);
+      *(f16x8*)(d0 + c) = v;
+      if (cfg_on) *(f16x8*)(d1 + c) = v;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- end of a frame
@@ -421,6 +436,26 @@ extern "C" int ecd_sample_topk(const void* logits, long ld, int B, int N, float 
   const int cfg_on = (B == 2 * N) ? 1 : 0;
   hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
                      (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
-                     out, out_stride);
+                     out, out_stride, (const f16*)nullptr, 0L, (f16*)nullptr, 0L, 0);
+  return ecd_launch_status();
+}
+
+extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, float cfg,
+                                    float temp, int topk, int V, const float* noise,
+                                    const int64_t* seed, const int64_t* pos, int salt,
+                                    int64_t* out, long out_stride, const void* rows, long rows_ld,
+                                    int rows_n, void* x, long x_ld, int D, void* stream) {
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!rows || !x || rows_n < V || D <= 0 || (D % 8) || rows_ld < D || (rows_ld % 8) ||
+      x_ld < D || (x_ld % 8) || !al(rows) || !al(x))
+    return ECD_EINVAL;
+  if (!logits || !out || N <= 0 || V <= 0 || V > SMP_MAXV || ld < V || topk <= 0 || topk > V ||
+      !(temp > 0.f) || out_stride <= 0 || (B != N && B != 2 * N) ||
+      (!noise && (!seed || !pos)))
+    return ECD_EINVAL;
+  const int cfg_on = B == 2 * N ? 1 : 0;
+  hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
+                     (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
+                     out, out_stride, (const f16*)rows, rows_ld, (f16*)x, x_ld, D);
   return ecd_launch_status();
 }

@@ -497,6 +497,7 @@ class HeartMuLaLite:
         self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
         self.graphs = {}
         self.N = self.B = None
+        self._next_rows = self._xnext = None
 
     def _embed_audio(self, cb, tok):
         """Embedding of codebook ``cb`` for tokens tok [B, 1] -> [B, D] (app/engine.py:307-308)."""
@@ -521,21 +522,28 @@ class HeartMuLaLite:
         else:
             samples = forced
 
-        def pick(i, lg):
+        # sampled codebooks 1..6: the sampler also writes the next pass's input row (the
+        # precomputed projection of the token's embedding)
+        nxt = self._next_rows if forced is None else None
+
+        def pick(i, lg, rows=None):
             if logits_out is not None:
                 logits_out.append(lg)
             if forced is None:
                 sample_topk(lg, self.N, cfg, temp, topk, samples[:, i], seed=self._seed, pos=pos,
-                            salt=i, noise=None if noise is None else noise[i])
+                            salt=i, noise=None if noise is None else noise[i], rows=rows,
+                            x=None if rows is None else self._xnext)
             return samples[:, i:i + 1]
 
         c0 = pick(0, self._c0(last_h))
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
         h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
-            ci = pick(i, self._head(i - 1, h))
+            rows = nxt[i - 1] if nxt is not None and i < N_CB - 1 else None
+            ci = pick(i, self._head(i - 1, h), rows)
             if i < N_CB - 1:
-                h = self._decode(self._project(ci, i), self._dpos[i], 1)
+                x = self._xnext if rows is not None else self._project(ci, i)
+                h = self._decode(x, self._dpos[i], 1)
         return samples
 
     def _decode(self, x, pos, S):
@@ -593,6 +601,35 @@ class HeartMuLaLite:
         self._pos_prompt = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self.backbone.alloc(self.B, L, self.dev, self.dt)
         self.decoder.alloc(self.B, N_CB, self.dev, self.dt)
+        self._alloc_next_rows()
+
+    @torch.no_grad()
+    def _alloc_next_rows(self):
+        """The decoder input of passes 1..6 is projection(_embed_audio(i, ci)) (app/engine.py:343),
+        a function of (codebook, token) and the weights only: rows[i - 1][t] holds it for every
+        token t of codebooks i = 1..6 (weight preprocessing, like the packing), and the frame's
+        sampler copies the sampled token's row into the [B, D] buffer ``_xnext``.  Each row comes
+        from the frame's own projection launch with B rows (the rows of a launch do not
+        interact), so it is bit-equal to the per-frame projection it replaces.  Kept across
+        allocations with the same B."""
+        pr, e = self.projection, self.audio_emb
+        B = self.B
+        if pr.qp is None or self.dt != torch.float16:
+            self._next_rows = self._xnext = None
+            return
+        if getattr(self, "_next_rows", None) is not None and self._xnext.shape[0] == B:
+            return
+        self._next_rows = self._xnext = None
+        V = AUDIO_VOCAB
+        rows = torch.empty(N_CB - 2, V, pr.N, device=self.dev, dtype=torch.float16)
+        tok = torch.arange(V + B, device=self.dev).clamp_(max=V - 1).view(-1, 1)
+        for cb in range(1, N_CB - 1):
+            for t0 in range(0, V, B):
+                n = min(B, V - t0)
+                y = embed_gemv_packed(tok[t0:t0 + B], e.table, e.scales, cb, V, pr.qp, pr.s8, pr.N)
+                rows[cb - 1, t0:t0 + n] = y[:n]
+        self._next_rows = rows
+        self._xnext = torch.empty(B, pr.N, device=self.dev, dtype=torch.float16)
 
     # -------------------------------------------------- generation
     @torch.inference_mode()

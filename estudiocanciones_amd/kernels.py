@@ -256,14 +256,19 @@ _silu_mul = _Launcher("_silu_mul", _silu_mul_impl,
 
 
 # ---------------------------------------------------------------- fused sampler
-def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, noise=None):
+def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, noise=None,
+                rows=None, x=None):
     """CFG mix + temperature + top-k + softmax(log_softmax) + Exponential race in one kernel
     (the math of _sample/_guided, app/engine.py:291-305).
 
     logits [B, V] fp16 (B = 2N: cond rows then uncond rows; B = N: no CFG); out: int64 view
     with out[b] the token slot of row b (any row stride).  The Exponential(1) draws come from
     a counter-based Philox keyed by seed (int64 device scalar) at frame position pos (int64
-    device scalar) and ``salt``, or from ``noise`` [N, V] float32 when given."""
+    device scalar) and ``salt``, or from ``noise`` [N, V] float32 when given.
+
+    With ``rows`` [>= V, D] fp16 and ``x`` [B, D] fp16, row b of x also receives rows[token of
+    row b] (zeros where the race had no winner): the next decoder pass's input when rows[t]
+    holds projection(embedding of token t) (app/engine.py:343)."""
     dev = _dev(logits, "sample_topk")
     _f16(logits, "sample_topk logits")
     B, V = logits.shape
@@ -276,9 +281,23 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
             raise ValueError("sample_topk: noise must be contiguous float32 [N, V]")
     elif seed is None or pos is None:
         raise ValueError("sample_topk: seed and pos device scalars are required without noise")
-    _ffi.call("ecd_sample_topk", logits.data_ptr(), logits.stride(0), B, N, float(cfg), float(temp),
-              int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt), out.data_ptr(),
-              out.stride(0), stream_ptr(dev))
+    if (rows is None) != (x is None):
+        raise ValueError("sample_topk: rows and x go together")
+    if rows is None:
+        _ffi.call("ecd_sample_topk", logits.data_ptr(), logits.stride(0), B, N, float(cfg),
+                  float(temp), int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt),
+                  out.data_ptr(), out.stride(0), stream_ptr(dev))
+        return
+    _f16(rows, "sample_topk rows")
+    _f16(x, "sample_topk x")
+    D = x.shape[1]
+    if rows.dim() != 2 or rows.shape[0] < V or rows.shape[1] != D or rows.stride(1) != 1 or \
+            x.dim() != 2 or x.shape[0] < B or x.stride(1) != 1:
+        raise ValueError("sample_topk: rows must be [>= V, D] and x [>= B, D] with contiguous rows")
+    _ffi.call("ecd_sample_topk_next", logits.data_ptr(), logits.stride(0), B, N, float(cfg),
+              float(temp), int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt),
+              out.data_ptr(), out.stride(0), rows.data_ptr(), rows.stride(0), rows.shape[0],
+              x.data_ptr(), x.stride(0), D, stream_ptr(dev))
 
 
 # ---------------------------------------------------------------- packed weights + fused GEMVs

@@ -132,6 +132,18 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
                     int V, const float* noise, const int64_t* seed, const int64_t* pos, int salt,
                     int64_t* out, long out_stride, void* stream);
 
+/* ecd_sample_topk, then the next depth-decoder pass's input row of each sampled token copied
+ * from rows [rows_n >= V, D] f16 (row stride rows_ld) into x row n (and row n + N with CFG),
+ * row stride x_ld; rows and x 16-byte aligned, D, rows_ld and x_ld multiples of 8; a take whose
+ * race has no winner (NaN logits) gets a zero row.  With rows[t] = projection(audio embedding
+ * of codebook i, token t), precomputed by the projection kernel itself, this replaces _guided +
+ * projection(_embed_audio(i, ci)) of one decoder pass (app/engine.py:291-305, 343). */
+int ecd_sample_topk_next(const void* logits, long ld, int B, int N, float cfg, float temp,
+                         int topk, int V, const float* noise, const int64_t* seed,
+                         const int64_t* pos, int salt, int64_t* out, long out_stride,
+                         const void* rows, long rows_ld, int rows_n, void* x, long x_ld, int D,
+                         void* stream);
+
 /* End of one frame of the song loop, on the device (app/engine.py:419-440: the host's
  * tok/pos copies, out[i + 1] = tok[:N] and the EOS scan, moved inside the captured frame).
  *   samples [B, 8] int64 (row stride lds): the frame's tokens; copied into tok [B, 8] (stride

@@ -60,6 +60,16 @@ def _taps(*offsets):
     lambda L: L.ecd_decode_attn_noalloc(8, 8, 8, 8, 8, 1, 1, 8, 3, 8, 128, 16, 0.1, None),      # Hq % Hk
     lambda L: L.ecd_gemv_i8p_splitk(16, 64, 16, 16, None, 0, 16, 64, 1, 64, 192, 2, 16, 0, None),  # 3 chunks % 2
     lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8196, 16, 1024, 1024, None),      # rows_n < V
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1020, None),      # D % 8
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     24, 1024, 8197, 16, 1024, 1024, None),      # rows not 16-aligned
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, None, 1024, 1024, None),    # no x
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 3, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1024, None),      # B != N, 2N
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
     lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0
     lambda L: L.ecd_embed_i8(8, 1, 8, 8, 0, 0, 8197, None, 8, 1, 8, None),        # rows 0

@@ -142,3 +142,29 @@ def test_sampler_seed_and_position_change_draws(dev):
     assert np.array_equal(a, draw(1, 5))           # reproducible
     assert not np.array_equal(a, draw(2, 5))       # seed matters
     assert not np.array_equal(a, draw(1, 6))       # frame position matters
+
+
+@pytest.mark.parametrize("N,cfg_on,philox", [(4, True, True), (4, True, False), (3, False, True)])
+def test_sampler_next_rows(dev, N, cfg_on, philox):
+    """ecd_sample_topk_next: the same tokens as ecd_sample_topk, and row b of x = rows[token of
+    row b], bit for bit (cond and uncond rows alike), other rows of x untouched."""
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    g = rng(300 + N)
+    B = 2 * N if cfg_on else N
+    D = 1024
+    rows = T((g.standard_normal((V + 3, D), dtype=np.float32)).astype(np.float16), dev)
+    seed = torch.tensor([12345], dtype=torch.int64, device=dev)
+    pos = torch.tensor([77], dtype=torch.int64, device=dev)
+    for trial in range(4):
+        logits = T((g.standard_normal((B, V), dtype=np.float32) * 3).astype(np.float16), dev)
+        noise = None if philox else T(g.exponential(1.0, (N, V)).astype(np.float32), dev)
+        kw = dict(seed=seed, pos=pos, salt=trial) if philox else dict(noise=noise)
+        want = torch.full((B,), -1, dtype=torch.int64, device=dev)
+        sample_topk(logits, N, 1.5, 1.0, 50, want, **kw)
+        got = torch.full((B,), -1, dtype=torch.int64, device=dev)
+        x = torch.full((B + 2, D), 7.0, dtype=torch.float16, device=dev)
+        sample_topk(logits, N, 1.5, 1.0, 50, got, rows=rows, x=x, **kw)
+        assert torch.equal(got, want), (trial, got, want)
+        assert torch.equal(x[:B], rows[got]), trial
+        assert bool((x[B:] == 7.0).all())
