@@ -173,22 +173,124 @@ __device__ uint32_t select_full(const uint32_t (&key)[SMP_PER], const f16 (&lv)[
   return (uint32_t)total;
 }
 
+// What the sampler of a depth-decoder pass also does for the next pass, with the sampled token
+// t of take n (rows n and n + N with CFG):
+//  * rows != NULL: x rows <- rows[t] (the next pass's input, precomputed per token);
+//  * qkv != NULL: that pass's layer 0 up to its attention output: q | k | v of the token at
+//    slot p (precomputed per token, RoPE applied) -> the cache slot p of kc / vc, and the
+//    decode attention over slots 0 .. p (app/kernels.py:110-153: fp32 scores, exp, fp16 P,
+//    fp32 P V, o = acc / l) -> o rows, head_dim 128.  One wave per (row, kv head) pair; the
+//    pair's cached slots 0 .. p - 1 go to LDS at kernel start, while the sampler runs.
+constexpr int NXA_HD = 128;   // head_dim of the folded attention
+constexpr int NXA_SLOTS = 16; // cache slots it reads at most (p < 16)
+constexpr int NXA_PAIRS = 4;  // (row, kv head) pairs per take at most
+constexpr int NXA_G = 4;      // query heads per kv head at most
+struct NextPass {
+  const f16* rows;
+  long rows_ld;
+  f16* x;
+  long x_ld;
+  int D;
+  const f16* qkv;  // [>= V, (Hq + 2 Hk) * 128]: q heads | k heads | v heads per token
+  long qkv_ld;
+  f16* kc;         // [B, Hk, L, 128]
+  f16* vc;
+  int L, p;
+  f16* o;          // [B, Hq * 128]
+  long o_ld;
+  int Hq, Hk;
+  float scale;
+};
+
+// Pair (row, kv head) of the next pass's layer-0 attention for the sampled token tok, one wave:
+// q | k | v of the token from its precomputed row (zeros if no index won), k and v into cache
+// slot p and LDS slot p (slots 0 .. p - 1 are in LDS already), then scores (lane: head
+// lane / 16, slot lane % 16), softmax over the slots of each head, P V (lane: head lane / 16,
+// columns 8 (lane % 16) .. + 7) and o.
+__device__ __forceinline__ void next_attention(const NextPass& nx, int tok, int V, int aj,
+                                               int row, int kh, long cache, int lane,
+                                               f16 (*ak)[NXA_HD], f16 (*av)[NXA_HD],
+                                               f16 (*aq)[NXA_HD], float (*ape)[NXA_SLOTS]) {
+  const int G = nx.Hq / nx.Hk, p = nx.p;
+  const bool valid = (uint32_t)tok < (uint32_t)V;
+  const f16* src = nx.qkv + (long)(valid ? tok : 0) * nx.qkv_ld;
+  const int nq = G * (NXA_HD / 8);  // 16-byte chunks of the pair's q heads
+  for (int c = lane; c < nq + NXA_HD / 4; c += 64) {
+    const bool isq = c < nq, isk = !isq && c < nq + NXA_HD / 8;
+    const int d = isq ? 0 : 8 * (c - nq - (isk ? 0 : NXA_HD / 8));
+    const long so = isq ? (long)kh * G * NXA_HD + 8 * c
+                        : (long)(nx.Hq + (isk ? 0 : nx.Hk) + kh) * NXA_HD + d;
+    f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (valid) v = *(const f16x8*)(src + so);
+    if (isq) {
+      *(f16x8*)(&aq[0][0] + 8 * c) = v;
+    } else {
+      *(f16x8*)(&(isk ? ak : av)[p][d]) = v;
+      *(f16x8*)((isk ? nx.kc : nx.vc) + cache + (long)p * NXA_HD + d) = v;
+    }
+  }
+  wait_vm0();  // the LDS DMA of the cached slots, issued at kernel start, has landed
+  asm volatile("" ::: "memory");
+  const int g = lane >> 4, t = lane & 15;
+  const bool on = g < G && t <= p;
+  float s = -INFINITY;
+  if (on) {
+    float acc = 0.f;
+#pragma unroll 4
+    for (int c = 0; c < NXA_HD / 8; ++c) {
+      const f16x8 qv = *(const f16x8*)(&aq[g][8 * c]);
+      const f16x8 kv = *(const f16x8*)(&ak[t][8 * c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)qv[e] * (float)kv[e];
+    }
+    s = acc * nx.scale;
+  }
+  float m = s;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float pe = on ? expf(s - m) : 0.f;
+  float l = pe;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+  if (g < G) ape[g][t] = (float)(f16)pe;  // P in fp16 for the P V product
+  if (g < G) {
+    const int d0 = 8 * (lane & 15);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u <= p; ++u) {
+      const float w = ape[g][u];
+      const f16x8 vv = *(const f16x8*)(&av[u][d0]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * (float)vv[e];
+    }
+    f16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] = (f16)(acc[e] / l);
+    *(f16x8*)(nx.o + (long)row * nx.o_ld + (long)(kh * G + g) * NXA_HD + d0) = ov;
+  }
+  (void)aj;
+}
+
 __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
     const int64_t* __restrict__ pos, int salt, int64_t* __restrict__ out, long out_stride,
-    const f16* __restrict__ rows, long rows_ld, f16* __restrict__ xo, long x_ld, int D) {
+    const NextPass nx) {
   __shared__ uint32_t hist[2][256];
   __shared__ uint32_t sel[4];  // threshold key, kept count; radix state
   __shared__ __align__(16) uint32_t wtot[SMP_THREADS / 64];
   __shared__ __align__(16) uint32_t wbin[SMP_WBINS_LDS];
   __shared__ int kept_i[SMP_MAXV];
   __shared__ float kept_x[SMP_MAXV];
+  __shared__ __align__(16) f16 a_k[NXA_PAIRS][NXA_SLOTS][NXA_HD];
+  __shared__ __align__(16) f16 a_v[NXA_PAIRS][NXA_SLOTS][NXA_HD];
+  __shared__ __align__(16) f16 a_q[NXA_PAIRS][NXA_G][NXA_HD];
+  __shared__ float a_pe[NXA_PAIRS][NXA_G][NXA_SLOTS];
+  __shared__ int s_tok;
 
   const int n = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const f16* lc = logits + (long)n * ld;
   const f16* lu = logits + (long)(n + N) * ld;
 
@@ -219,6 +321,23 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   if (!noise) {  // seed and pos are only dereferenced on the Philox path (NULL with noise)
     sd = (uint64_t)seed[0];
     p64 = (uint64_t)pos[0];
+  }
+  // the next pass's layer-0 attention: wave 1 + j runs pair j (row n + (j / Hk) N, kv head
+  // j % Hk); its cached slots 0 .. p - 1 (K and V) go to LDS now (LDS DMA, 4 slots per
+  // instruction, lanes past slot p - 1 idle)
+  const int npairs = nx.qkv ? (cfg_on ? 2 : 1) * nx.Hk : 0;
+  const int aj = wv - 1;
+  const int arow = n + (aj / max(nx.Hk, 1)) * N, akh = aj - (aj / max(nx.Hk, 1)) * nx.Hk;
+  const long acache = ((long)arow * nx.Hk + akh) * nx.L * NXA_HD;  // the pair's [L, 128] rows
+  if (aj >= 0 && aj < npairs) {
+    for (int u = 0; 4 * u < nx.p; ++u) {
+      const int t = 4 * u + (lane >> 4);
+      if (t < nx.p) {
+        const uint32_t off = (uint32_t)(((long)t * NXA_HD + 8 * (lane & 15)) * 2);
+        lds_dma16(nx.kc + acache, off, &a_k[aj][4 * u][0]);
+        lds_dma16(nx.vc + acache, off, &a_v[aj][4 * u][0]);
+      }
+    }
   }
 
   // 2. CFG mix in fp16, keys, and the block's largest key
@@ -317,7 +436,14 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     total = select_full(key, lv, temp, topk, hist, sel, wtot, kept_i, kept_x);
   }
   __syncthreads();
-  if (wv != 0) return;
+  if (wv != 0) {
+    if (aj < npairs) {  // a pair wave: the token, then the pair's attention
+      __syncthreads();
+      next_attention(nx, s_tok, V, aj, arow, akh, acache, lane, a_k[aj], a_v[aj], a_q[aj],
+                     a_pe[aj]);
+    }
+    return;
+  }
 
   // 6. wave 0: log_softmax then softmax in fp32 over the kept values (app/engine.py:293-296);
   //    the largest x is the one of the largest key
@@ -362,18 +488,22 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   const uint32_t rb = bi == 0x7FFFFFFF ? 0u : __builtin_bit_cast(uint32_t, bv);
   const uint32_t mb = wave_max_u32(rb);
   bi = (int)wave_min_u32(rb == mb ? (uint32_t)bi : 0xFFFFFFFFu);
+  if (npairs) {  // the token to the pair waves
+    if (lane == 0) s_tok = bi;
+    __syncthreads();
+  }
   if (lane == 0) {
     out[(long)n * out_stride] = bi;
     if (cfg_on) out[(long)(n + N) * out_stride] = bi;
   }
   // 8. the next pass's input row of the sampled token (rows [V, D] precomputed from it) into
   //    x rows n and n + N; zeros if no index won (NaN logits)
-  if (rows) {
+  if (nx.rows) {
     const bool valid = (uint32_t)bi < (uint32_t)V;
-    const f16* src = rows + (long)(valid ? bi : 0) * rows_ld;
-    f16* d0 = xo + (long)n * x_ld;
-    f16* d1 = xo + (long)(n + N) * x_ld;
-    for (int c = 8 * lane; c < D; c += 512) {
+    const f16* src = nx.rows + (long)(valid ? bi : 0) * nx.rows_ld;
+    f16* d0 = nx.x + (long)n * nx.x_ld;
+    f16* d1 = nx.x + (long)(n + N) * nx.x_ld;
+    for (int c = 8 * lane; c < nx.D; c += 512) {
       f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
       if (valid) v = *(const f16x8*)(src + c);
       *(f16x8*)(d0 + c) = v;
@@ -436,7 +566,7 @@ extern "C" int ecd_sample_topk(const void* logits, long ld, int B, int N, float 
   const int cfg_on = (B == 2 * N) ? 1 : 0;
   hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
                      (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
-                     out, out_stride, (const f16*)nullptr, 0L, (f16*)nullptr, 0L, 0);
+                     out, out_stride, NextPass{});
   return ecd_launch_status();
 }
 
@@ -444,8 +574,10 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
                                     float temp, int topk, int V, const float* noise,
                                     const int64_t* seed, const int64_t* pos, int salt,
                                     int64_t* out, long out_stride, const void* rows, long rows_ld,
-                                    int rows_n, void* x, long x_ld, int D, void* stream) {
-  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+                                    int rows_n, void* x, long x_ld, int D, const void* qkv,
+                                    long qkv_ld, int qkv_n, void* kc, void* vc, int L, int p,
+                                    void* o, long o_ld, int Hq, int Hk, void* stream) {
+  const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   if (!rows || !x || rows_n < V || D <= 0 || (D % 8) || rows_ld < D || (rows_ld % 8) ||
       x_ld < D || (x_ld % 8) || !al(rows) || !al(x))
     return ECD_EINVAL;
@@ -454,8 +586,23 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
       (!noise && (!seed || !pos)))
     return ECD_EINVAL;
   const int cfg_on = B == 2 * N ? 1 : 0;
+  if (qkv) {
+    const int nq = (Hq + 2 * Hk) * NXA_HD;
+    if (!kc || !vc || !o || Hk <= 0 || Hq <= 0 || (Hq % Hk) || Hq / Hk > NXA_G ||
+        (1 + cfg_on) * Hk > NXA_PAIRS || p < 0 || p >= L || p >= NXA_SLOTS || qkv_n < V ||
+        qkv_ld < nq || (qkv_ld % 8) || o_ld < Hq * NXA_HD || (o_ld % 8) || !al(qkv) ||
+        !al(kc) || !al(vc) || !al(o))
+      return ECD_EINVAL;
+  }
+  NextPass nx{};
+  nx.rows = (const f16*)rows; nx.rows_ld = rows_ld; nx.x = (f16*)x; nx.x_ld = x_ld; nx.D = D;
+  if (qkv) {
+    nx.qkv = (const f16*)qkv; nx.qkv_ld = qkv_ld; nx.kc = (f16*)kc; nx.vc = (f16*)vc;
+    nx.L = L; nx.p = p; nx.o = (f16*)o; nx.o_ld = o_ld; nx.Hq = Hq; nx.Hk = Hk;
+    nx.scale = 1.0f / sqrtf((float)NXA_HD);
+  }
   hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
                      (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
-                     out, out_stride, (const f16*)rows, rows_ld, (f16*)x, x_ld, D);
+                     out, out_stride, nx);
   return ecd_launch_status();
 }

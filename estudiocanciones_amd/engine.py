@@ -315,14 +315,16 @@ class Stack:
             x = gemm_packed(mm, b.w2.qp, b.w2.sp, b.w2.N, b.w2.K, res=x)
         return krms(x, self.norm)
 
-    def decode(self, x, pos, S, final_norm=True):
+    def decode(self, x, pos, S, final_norm=True, o0=None):
         """Fast path for few rows (app/engine.py:180-211): x [R, D] with R = B*S (row r -> batch
         r // S), pos [R] absolute positions; row r attends [0, pos[r]].
 
         Per layer: rms+qkv+RoPE/KV write (one kernel), attention (+ split combine),
         O projection + residual, rms+w1|w3+SiLU*mul (one kernel), w2 + residual.
         ``final_norm=False`` returns the residual stream before the stack's last RMSNorm, for a
-        consumer that fuses that norm into its own GEMV (the codebook heads)."""
+        consumer that fuses that norm into its own GEMV (the codebook heads).  ``o0``: layer 0's
+        attention output, its q|k|v, RoPE and cache slot already done (by the depth decoder's
+        sampler); the step then starts at layer 0's O projection."""
         if any(b.qkv.qp is None for b in self.blocks):
             h = self.decode_reference(x, pos, S)
             return h if final_norm else None
@@ -330,20 +332,23 @@ class Stack:
         ns = self.nsplit
         t = next((t for t in (self.tail, self.tail2) if t is not None and R == t["M"]), None)
         if self.use_tail and t is not None:
-            x = self._decode_tail(x, pos, S, ns, t)
+            x = self._decode_tail(x, pos, S, ns, t, o0)
             return krms(x, self.norm) if final_norm else x
-        for b in self.blocks:
+        for i, b in enumerate(self.blocks):
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
-            q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
-            rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L, HD,
-                         stream=b.qkv.stream)
-            o = self._attention(b, q, pos, S, ns)
+            if i == 0 and o0 is not None:
+                o = o0
+            else:
+                q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
+                rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk,
+                             L, HD, stream=b.qkv.stream)
+                o = self._attention(b, q, pos, S, ns)
             x = b.o(o, res=x)
             mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2, stream=b.w13.stream)
             x = b.w2(mm, res=x)
         return krms(x, self.norm) if final_norm else x
 
-    def _decode_tail(self, x, pos, S, ns, t):
+    def _decode_tail(self, x, pos, S, ns, t, o0=None):
         """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
         ecd_layer_head launch where the shapes allow attention in the launch, else on their
         own; then one ecd_layer_tail launch per layer: the O projection, the MLP, the next
@@ -360,7 +365,9 @@ class Stack:
                         vc=b.vc, S=S, Hq=b.h, Hk=b.kvh, L=b.kc.shape[2], HD=b.hd)
 
         b0 = self.blocks[0]
-        if att:
+        if o0 is not None:
+            o = o0
+        elif att:
             o = layer_head(x, nxt_of(b0), t["ob"][1], b0.w2.K, t["sync"], t["err"], t["ws"],
                            stream=b0.qkv.stream, no_wait=self.tail_no_wait)
         else:
@@ -497,7 +504,7 @@ class HeartMuLaLite:
         self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
         self.graphs = {}
         self.N = self.B = None
-        self._next_rows = self._xnext = None
+        self._next_rows = self._xnext = self._next_qkv = self._onext = None
 
     def _embed_audio(self, cb, tok):
         """Embedding of codebook ``cb`` for tokens tok [B, 1] -> [B, D] (app/engine.py:307-308)."""
@@ -523,16 +530,21 @@ class HeartMuLaLite:
             samples = forced
 
         # sampled codebooks 1..6: the sampler also writes the next pass's input row (the
-        # precomputed projection of the token's embedding)
+        # precomputed projection of the token's embedding) and, where the table exists, runs
+        # that pass's layer 0 up to its attention output (precomputed q|k|v of the token)
         nxt = self._next_rows if forced is None else None
+        nqkv = self._next_qkv if nxt is not None else None
+        d0 = self.decoder.blocks[0] if nqkv is not None else None
 
-        def pick(i, lg, rows=None):
+        def pick(i, lg, rows=None, qkv=None):
             if logits_out is not None:
                 logits_out.append(lg)
             if forced is None:
+                att = {} if qkv is None else dict(qkv=qkv, kc=d0.kc, vc=d0.vc, p=i + 1,
+                                                  o=self._onext)
                 sample_topk(lg, self.N, cfg, temp, topk, samples[:, i], seed=self._seed, pos=pos,
                             salt=i, noise=None if noise is None else noise[i], rows=rows,
-                            x=None if rows is None else self._xnext)
+                            x=None if rows is None else self._xnext, **att)
             return samples[:, i:i + 1]
 
         c0 = pick(0, self._c0(last_h))
@@ -540,18 +552,20 @@ class HeartMuLaLite:
         h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
             rows = nxt[i - 1] if nxt is not None and i < N_CB - 1 else None
-            ci = pick(i, self._head(i - 1, h), rows)
+            qkv = nqkv[i - 1] if rows is not None and nqkv is not None else None
+            ci = pick(i, self._head(i - 1, h), rows, qkv)
             if i < N_CB - 1:
                 x = self._xnext if rows is not None else self._project(ci, i)
-                h = self._decode(x, self._dpos[i], 1)
+                h = self._decode(x, self._dpos[i], 1, o0=None if qkv is None else self._onext)
         return samples
 
-    def _decode(self, x, pos, S):
-        """Decoder pass; with packed heads the stack's final RMSNorm is left to the head GEMV."""
+    def _decode(self, x, pos, S, o0=None):
+        """Decoder pass; with packed heads the stack's final RMSNorm is left to the head GEMV.
+        ``o0``: layer 0's attention output when the sampler ran layer 0 up to it."""
         if self.audio_head[0].qp is not None and self.decoder.blocks and \
                 self.decoder.blocks[0].qkv.qp is not None:
-            return self.decoder.decode(x, pos, S, final_norm=False)
-        return self.decoder.decode(x, pos, S)
+            return self.decoder.decode(x, pos, S, final_norm=False, o0=o0)
+        return self.decoder.decode(x, pos, S, o0=o0)
 
     def _logits(self, M, N):
         """[M, N] fp16 logits whose rows start 128-byte aligned (the sampler loads 16 B/lane)."""
@@ -615,11 +629,11 @@ class HeartMuLaLite:
         pr, e = self.projection, self.audio_emb
         B = self.B
         if pr.qp is None or self.dt != torch.float16:
-            self._next_rows = self._xnext = None
+            self._next_rows = self._xnext = self._next_qkv = self._onext = None
             return
         if getattr(self, "_next_rows", None) is not None and self._xnext.shape[0] == B:
             return
-        self._next_rows = self._xnext = None
+        self._next_rows = self._xnext = self._next_qkv = self._onext = None
         V = AUDIO_VOCAB
         rows = torch.empty(N_CB - 2, V, pr.N, device=self.dev, dtype=torch.float16)
         tok = torch.arange(V + B, device=self.dev).clamp_(max=V - 1).view(-1, 1)
@@ -630,6 +644,43 @@ class HeartMuLaLite:
                 rows[cb - 1, t0:t0 + n] = y[:n]
         self._next_rows = rows
         self._xnext = torch.empty(B, pr.N, device=self.dev, dtype=torch.float16)
+        self._alloc_next_qkv()
+
+    @torch.no_grad()
+    def _alloc_next_qkv(self):
+        """Layer 0 of decoder pass i (1..6) starts with rms -> q|k|v -> RoPE at position i + 1
+        (app/engine.py:189-199) on the input row of the sampled token: again a function of
+        (codebook, token) and the weights.  qkv[i - 1][t] holds q heads | k heads | v heads of
+        token t (the per-op kernel rms_qkv_rope, 16 tokens per launch), so the sampler can write
+        the cache slot and run that layer's attention itself; only for head_dim 128 and the
+        pair counts the sampler's folded attention takes."""
+        self._next_qkv = self._onext = None
+        d0 = self.decoder.blocks[0] if self.decoder.blocks else None
+        B, V = self.B, AUDIO_VOCAB
+        if d0 is None or d0.qkv.qp is None or d0.hd != 128 or d0.h % d0.kvh or \
+                d0.h // d0.kvh > 4 or (2 if B == 2 * self.N else 1) * d0.kvh > 4 or N_CB - 1 >= 16:
+            return
+        Hq, Hk, HD, L = d0.h, d0.kvh, d0.hd, d0.kc.shape[2]
+        if L < N_CB:
+            return
+        M = 16
+        qkv = torch.empty(N_CB - 2, V, (Hq + 2 * Hk) * HD, device=self.dev, dtype=torch.float16)
+        q = torch.empty(M, Hq * HD, device=self.dev, dtype=torch.float16)
+        kc = torch.zeros(M, Hk, L, HD, device=self.dev, dtype=torch.float16)
+        vc = torch.zeros_like(kc)
+        for cb in range(1, N_CB - 1):
+            p = cb + 1
+            pos = torch.full((M,), p, dtype=torch.int64, device=self.dev)
+            for t0 in range(0, V, M):
+                n = min(M, V - t0)
+                rms_qkv_rope(self._next_rows[cb - 1, t0:t0 + n], d0.n1, d0.qkv.qp, d0.qkv.s8,
+                             self.decoder.rope, pos[:n], q[:n], kc, vc, 1, Hq, Hk, L, HD)
+                dst = qkv[cb - 1, t0:t0 + n]
+                dst[:, :Hq * HD] = q[:n]
+                dst[:, Hq * HD:(Hq + Hk) * HD] = kc[:n, :, p].reshape(n, Hk * HD)
+                dst[:, (Hq + Hk) * HD:] = vc[:n, :, p].reshape(n, Hk * HD)
+        self._next_qkv = qkv
+        self._onext = torch.empty(B, Hq * HD, device=self.dev, dtype=torch.float16)
 
     # -------------------------------------------------- generation
     @torch.inference_mode()

@@ -257,7 +257,7 @@ _silu_mul = _Launcher("_silu_mul", _silu_mul_impl,
 
 # ---------------------------------------------------------------- fused sampler
 def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, noise=None,
-                rows=None, x=None):
+                rows=None, x=None, qkv=None, kc=None, vc=None, p=0, o=None):
     """CFG mix + temperature + top-k + softmax(log_softmax) + Exponential race in one kernel
     (the math of _sample/_guided, app/engine.py:291-305).
 
@@ -268,7 +268,10 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
 
     With ``rows`` [>= V, D] fp16 and ``x`` [B, D] fp16, row b of x also receives rows[token of
     row b] (zeros where the race had no winner): the next decoder pass's input when rows[t]
-    holds projection(embedding of token t) (app/engine.py:343)."""
+    holds projection(embedding of token t) (app/engine.py:343).  With ``qkv`` [>= V,
+    (Hq + 2 Hk) * 128] fp16 as well (the next pass's layer-0 q | k | v of each token at slot
+    ``p``), k and v also go to slot p of the caches ``kc`` / ``vc`` [B, Hk, L, 128] and each
+    row's decode attention over slots 0 .. p goes to ``o`` [B, Hq * 128]."""
     dev = _dev(logits, "sample_topk")
     _f16(logits, "sample_topk logits")
     B, V = logits.shape
@@ -294,10 +297,26 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
     if rows.dim() != 2 or rows.shape[0] < V or rows.shape[1] != D or rows.stride(1) != 1 or \
             x.dim() != 2 or x.shape[0] < B or x.stride(1) != 1:
         raise ValueError("sample_topk: rows must be [>= V, D] and x [>= B, D] with contiguous rows")
+    Hq = Hk = L = 0
+    if qkv is not None:
+        _f16(qkv, "sample_topk qkv")
+        _f16(o, "sample_topk o")
+        _f16(kc, "sample_topk kc")
+        _f16(vc, "sample_topk vc")
+        Hk, L = kc.shape[1], kc.shape[2]
+        Hq = o.shape[1] // 128
+        if kc.dim() != 4 or kc.shape[0] < B or kc.shape[3] != 128 or vc.shape != kc.shape or \
+                not kc.is_contiguous() or not vc.is_contiguous() or o.shape[0] < B or \
+                o.stride(1) != 1 or qkv.dim() != 2 or qkv.shape[1] != (Hq + 2 * Hk) * 128 or \
+                qkv.stride(1) != 1:
+            raise ValueError("sample_topk: qkv [>= V, (Hq + 2 Hk) 128], caches [>= B, Hk, L, 128], "
+                             "o [>= B, Hq 128]")
     _ffi.call("ecd_sample_topk_next", logits.data_ptr(), logits.stride(0), B, N, float(cfg),
               float(temp), int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt),
               out.data_ptr(), out.stride(0), rows.data_ptr(), rows.stride(0), rows.shape[0],
-              x.data_ptr(), x.stride(0), D, stream_ptr(dev))
+              x.data_ptr(), x.stride(0), D, _ptr(qkv), 0 if qkv is None else qkv.stride(0),
+              0 if qkv is None else qkv.shape[0], _ptr(kc), _ptr(vc), L, int(p), _ptr(o),
+              0 if o is None else o.stride(0), Hq, Hk, stream_ptr(dev))
 
 
 # ---------------------------------------------------------------- packed weights + fused GEMVs

@@ -132,17 +132,26 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
                     int V, const float* noise, const int64_t* seed, const int64_t* pos, int salt,
                     int64_t* out, long out_stride, void* stream);
 
-/* ecd_sample_topk, then the next depth-decoder pass's input row of each sampled token copied
- * from rows [rows_n >= V, D] f16 (row stride rows_ld) into x row n (and row n + N with CFG),
- * row stride x_ld; rows and x 16-byte aligned, D, rows_ld and x_ld multiples of 8; a take whose
- * race has no winner (NaN logits) gets a zero row.  With rows[t] = projection(audio embedding
- * of codebook i, token t), precomputed by the projection kernel itself, this replaces _guided +
- * projection(_embed_audio(i, ci)) of one decoder pass (app/engine.py:291-305, 343). */
+/* ecd_sample_topk, then the next depth-decoder pass's input for each sampled token t of take n
+ * (rows n and n + N with CFG):
+ *  - x rows <- rows[t] from rows [rows_n >= V, D] f16 (row stride rows_ld), row stride x_ld;
+ *    rows and x 16-byte aligned, D, rows_ld and x_ld multiples of 8;
+ *  - with qkv != NULL, that pass's layer 0 up to its attention output: q | k | v of t from
+ *    qkv [qkv_n >= V, (Hq + 2 Hk) * 128] f16 (row stride qkv_ld; q heads, k heads, v heads,
+ *    RoPE applied for slot p), k and v into slot p of the caches kc / vc [B, Hk, L, 128], and
+ *    the decode attention of each row over slots 0 .. p into o [B, Hq * 128] (row stride o_ld);
+ *    head_dim 128, Hq / Hk <= 4, (1 or 2 rows) * Hk <= 4, p < min(L, 16).
+ * A take whose race has no winner (NaN logits) gets zero rows.  With rows[t] =
+ * projection(audio embedding of codebook i, token t) and qkv[t] its layer-0 q | k | v at the
+ * pass's position, both precomputed by the engine's own kernels, this replaces _guided +
+ * projection(_embed_audio(i, ci)) + the decoder's layer-0 rms / q|k|v / RoPE / cache write /
+ * attention of one pass (app/engine.py:291-305, 343, 189-199; app/kernels.py:110-153). */
 int ecd_sample_topk_next(const void* logits, long ld, int B, int N, float cfg, float temp,
                          int topk, int V, const float* noise, const int64_t* seed,
                          const int64_t* pos, int salt, int64_t* out, long out_stride,
                          const void* rows, long rows_ld, int rows_n, void* x, long x_ld, int D,
-                         void* stream);
+                         const void* qkv, long qkv_ld, int qkv_n, void* kc, void* vc, int L,
+                         int p, void* o, long o_ld, int Hq, int Hk, void* stream);
 
 /* End of one frame of the song loop, on the device (app/engine.py:419-440: the host's
  * tok/pos copies, out[i + 1] = tok[:N] and the EOS scan, moved inside the captured frame).

@@ -10,6 +10,10 @@ ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "ecdecode.h"
 
 
+
+# ecd_sample_topk_next without the folded attention: qkv .. Hk, stream
+_NOATT = (None, 0, 0, None, None, 0, 0, None, 0, 0, 0, None)
+
 def declared():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -61,15 +65,27 @@ def _taps(*offsets):
     lambda L: L.ecd_gemv_i8p_splitk(16, 64, 16, 16, None, 0, 16, 64, 1, 64, 192, 2, 16, 0, None),  # 3 chunks % 2
     lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
-                                     16, 1024, 8196, 16, 1024, 1024, None),      # rows_n < V
+                                     16, 1024, 8196, 16, 1024, 1024, *_NOATT),   # rows_n < V
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
-                                     16, 1024, 8197, 16, 1024, 1020, None),      # D % 8
+                                     16, 1024, 8197, 16, 1024, 1020, *_NOATT),   # D % 8
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
-                                     24, 1024, 8197, 16, 1024, 1024, None),      # rows not 16-aligned
+                                     24, 1024, 8197, 16, 1024, 1024, *_NOATT),   # rows not 16-aligned
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
-                                     16, 1024, 8197, None, 1024, 1024, None),    # no x
+                                     16, 1024, 8197, None, 1024, 1024, *_NOATT), # no x
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 3, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
-                                     16, 1024, 8197, 16, 1024, 1024, None),      # B != N, 2N
+                                     16, 1024, 8197, 16, 1024, 1024, *_NOATT),   # B != N, 2N
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1024, 16, 1536, 8197, 16, 16, 8, 8,
+                                     16, 1024, 8, 2, None),                      # p = L
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1024, 16, 2048, 8197, 16, 16, 8, 3,
+                                     16, 1536, 12, 2, None),                     # G = 6 > 4
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1024, 16, 2048, 8197, 16, 16, 8, 3,
+                                     16, 1024, 8, 4, None),                      # 2 rows x 4 kv heads
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 1024, 8197, 16, 1024, 1024, 16, 1536, 8197, None, 16, 8,
+                                     3, 16, 1024, 8, 2, None),                   # no k cache
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
     lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0
     lambda L: L.ecd_embed_i8(8, 1, 8, 8, 0, 0, 8197, None, 8, 1, 8, None),        # rows 0

@@ -145,30 +145,36 @@ def test_sampling_with_injected_noise(dev):
 @pytest.mark.parametrize("n_takes", [2, 3])
 def test_next_rows_table_equals_projection(dev, n_takes):
     """Decoder passes 1..6 take their input from the precomputed projection rows (written by
-    the sampler) instead of the projection launch: the frame's logits and tokens are bit-equal
-    to those of the projection path, with and without CFG."""
+    the sampler) instead of the projection launch: logits and tokens bit-equal to those of the
+    projection path, with and without CFG.  With the precomputed layer-0 q|k|v as well (the
+    sampler then writes the cache slot and runs layer 0's attention), the tokens are the same
+    and every head's logits agree to KL < 1e-4."""
     import torch
     bb, dec = tiny_cfgs()
     _, gm = build_pair(dev, bb, dec, n_takes, 32, seed=4)
     assert gm._next_rows is not None and gm._xnext.shape[0] == gm.B
+    assert gm._next_qkv is not None and gm._onext.shape[0] == gm.B
     B, Nt = gm.B, gm.N
     g = rng(8)
     tok = torch.from_numpy(g.integers(0, AUDIO_VOCAB, (B, N_CB))).to(dev)
     noise = torch.from_numpy(g.exponential(1.0, (N_CB, Nt, AUDIO_VOCAB)).astype(np.float32)).to(dev)
-    rows = gm._next_rows
-    runs = []
-    for table in (True, False, True):
-        gm._next_rows = rows if table else None
+    rows, qkv = gm._next_rows, gm._next_qkv
+    runs = {}
+    for name, r, q in (("proj", None, None), ("rows", rows, None), ("qkv", rows, qkv)):
+        gm._next_rows, gm._next_qkv = r, q
         lg = []
         out = gm._step(tok, torch.full((B, 1), 3, dtype=torch.long, device=dev), None, 1.5, 50,
                        1.0, noise=noise, logits_out=lg)
         torch.cuda.synchronize()
-        runs.append((out.clone(), [x.clone() for x in lg]))
-    gm._next_rows = rows
-    for out, lg in runs[1:]:
-        assert torch.equal(out, runs[0][0])
-        for a, b in zip(lg, runs[0][1]):
-            assert torch.equal(a, b)
+        runs[name] = (out.clone(), [x.clone() for x in lg])
+    gm._next_rows, gm._next_qkv = rows, qkv
+    assert torch.equal(runs["rows"][0], runs["proj"][0])
+    for a, b in zip(runs["rows"][1], runs["proj"][1]):
+        assert torch.equal(a, b)
+    assert torch.equal(runs["qkv"][0], runs["proj"][0])
+    for i, (a, b) in enumerate(zip(runs["qkv"][1], runs["proj"][1])):
+        kl = kl_rows(N(b).astype(np.float64), N(a).astype(np.float64))
+        assert kl < 1e-4, (i, kl)
 
 
 def test_graph_replay_matches_eager(dev):

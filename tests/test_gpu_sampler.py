@@ -168,3 +168,43 @@ def test_sampler_next_rows(dev, N, cfg_on, philox):
         assert torch.equal(got, want), (trial, got, want)
         assert torch.equal(x[:B], rows[got]), trial
         assert bool((x[B:] == 7.0).all())
+
+
+@pytest.mark.parametrize("N,cfg_on,p", [(4, True, 2), (4, True, 7), (3, False, 5)])
+def test_sampler_next_layer0_attention(dev, N, cfg_on, p):
+    """ecd_sample_topk_next with the q|k|v rows: per sampled token, k and v land in cache slot p
+    bit for bit (other slots untouched), and o is the decode attention over slots 0 .. p
+    (oracle.kernels.decode_attn_out, one split) within the fp16 kernel bar."""
+    import torch
+    from estudiocanciones_amd.kernels import sample_topk
+    from helpers import assert_close16
+    from oracle.kernels import decode_attn_out
+    g = rng(400 + 10 * N + p)
+    B = 2 * N if cfg_on else N
+    Hq, Hk, HD, L, D = 8, 2, 128, 8, 1024
+    NQ = (Hq + 2 * Hk) * HD
+    rows = T(g.standard_normal((V, D), dtype=np.float32).astype(np.float16), dev)
+    qkv = T(g.standard_normal((V, NQ), dtype=np.float32).astype(np.float16), dev)
+    kc0 = g.standard_normal((B, Hk, L, HD), dtype=np.float32).astype(np.float16)
+    vc0 = g.standard_normal((B, Hk, L, HD), dtype=np.float32).astype(np.float16)
+    kc, vc = T(kc0, dev), T(vc0, dev)
+    o = torch.full((B, Hq * HD), 3.0, dtype=torch.float16, device=dev)
+    x = torch.empty(B, D, dtype=torch.float16, device=dev)
+    logits = T((g.standard_normal((B, V), dtype=np.float32) * 3).astype(np.float16), dev)
+    noise = T(g.exponential(1.0, (N, V)).astype(np.float32), dev)
+    tok = torch.full((B,), -1, dtype=torch.int64, device=dev)
+    sample_topk(logits, N, 1.5, 1.0, 50, tok, noise=noise, rows=rows, x=x, qkv=qkv, kc=kc, vc=vc,
+                p=p, o=o)
+    want_tok = torch.full((B,), -1, dtype=torch.int64, device=dev)
+    sample_topk(logits, N, 1.5, 1.0, 50, want_tok, noise=noise)
+    assert torch.equal(tok, want_tok)
+    assert torch.equal(x, rows[tok])
+    t = tok.cpu().numpy()
+    tq = qkv.cpu().numpy()[t]                       # [B, NQ]: q heads | k heads | v heads
+    kw, vw = kc0.copy(), vc0.copy()
+    kw[:, :, p] = tq[:, Hq * HD:(Hq + Hk) * HD].reshape(B, Hk, HD)
+    vw[:, :, p] = tq[:, (Hq + Hk) * HD:].reshape(B, Hk, HD)
+    assert np.array_equal(kc.cpu().numpy(), kw) and np.array_equal(vc.cpu().numpy(), vw)
+    want = decode_attn_out(tq[:, :Hq * HD], kw, vw, np.full(B, p, np.int64), 1, Hq, Hk, HD,
+                           nsplit=1)
+    assert_close16(o.cpu().numpy(), want, what=f"folded layer-0 attention p={p}")
