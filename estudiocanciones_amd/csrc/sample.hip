@@ -214,23 +214,38 @@ __device__ __forceinline__ void next_attention(const NextPass& nx, int tok, int 
   const int G = nx.Hq / nx.Hk, p = nx.p;
   const bool valid = (uint32_t)tok < (uint32_t)V;
   const f16* src = nx.qkv + (long)(valid ? tok : 0) * nx.qkv_ld;
+  // chunk c (16 bytes) of lane: c = lane + 64 u; q heads first, then k, then v of head kh.
+  // All loads go out first; one wait covers them and the LDS DMA of the cached slots issued at
+  // kernel start, and the stores after it are not waited for.
   const int nq = G * (NXA_HD / 8);  // 16-byte chunks of the pair's q heads
-  for (int c = lane; c < nq + NXA_HD / 4; c += 64) {
+  const int nc = nq + NXA_HD / 4;   // plus k and v
+  static_assert(NXA_G * (NXA_HD / 8) + NXA_HD / 4 <= 128, "two chunks per lane");
+  f16x8 v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int c = lane + 64 * u;
     const bool isq = c < nq, isk = !isq && c < nq + NXA_HD / 8;
     const int d = isq ? 0 : 8 * (c - nq - (isk ? 0 : NXA_HD / 8));
     const long so = isq ? (long)kh * G * NXA_HD + 8 * c
                         : (long)(nx.Hq + (isk ? 0 : nx.Hk) + kh) * NXA_HD + d;
-    f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    if (valid) v = *(const f16x8*)(src + so);
+    v[u] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (valid && c < nc) v[u] = *(const f16x8*)(src + so);
+  }
+  wait_vm0();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int c = lane + 64 * u;
+    if (c >= nc) continue;
+    const bool isq = c < nq, isk = !isq && c < nq + NXA_HD / 8;
+    const int d = isq ? 0 : 8 * (c - nq - (isk ? 0 : NXA_HD / 8));
     if (isq) {
-      *(f16x8*)(&aq[0][0] + 8 * c) = v;
+      *(f16x8*)(&aq[0][0] + 8 * c) = v[u];
     } else {
-      *(f16x8*)(&(isk ? ak : av)[p][d]) = v;
-      *(f16x8*)((isk ? nx.kc : nx.vc) + cache + (long)p * NXA_HD + d) = v;
+      *(f16x8*)(&(isk ? ak : av)[p][d]) = v[u];
+      *(f16x8*)((isk ? nx.kc : nx.vc) + cache + (long)p * NXA_HD + d) = v[u];
     }
   }
-  wait_vm0();  // the LDS DMA of the cached slots, issued at kernel start, has landed
-  asm volatile("" ::: "memory");
   const int g = lane >> 4, t = lane & 15;
   const bool on = g < G && t <= p;
   float s = -INFINITY;
