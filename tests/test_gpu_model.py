@@ -148,7 +148,8 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     the sampler) instead of the projection launch: logits and tokens bit-equal to those of the
     projection path, with and without CFG.  With the precomputed layer-0 q|k|v as well (the
     sampler then writes the cache slot and runs layer 0's attention), the tokens are the same
-    and every head's logits agree to KL < 1e-4."""
+    and every head's logits agree to KL < 1e-4, through the layer tails and through the
+    decoder's per-op kernels alike."""
     import torch
     bb, dec = tiny_cfgs()
     _, gm = build_pair(dev, bb, dec, n_takes, 32, seed=4)
@@ -160,21 +161,25 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     noise = torch.from_numpy(g.exponential(1.0, (N_CB, Nt, AUDIO_VOCAB)).astype(np.float32)).to(dev)
     rows, qkv = gm._next_rows, gm._next_qkv
     runs = {}
-    for name, r, q in (("proj", None, None), ("rows", rows, None), ("qkv", rows, qkv)):
+    for name, r, q, tail in (("proj", None, None, True), ("rows", rows, None, True),
+                             ("qkv", rows, qkv, True), ("qkv_perop", rows, qkv, False)):
         gm._next_rows, gm._next_qkv = r, q
+        gm.decoder.use_tail = tail
         lg = []
         out = gm._step(tok, torch.full((B, 1), 3, dtype=torch.long, device=dev), None, 1.5, 50,
                        1.0, noise=noise, logits_out=lg)
         torch.cuda.synchronize()
         runs[name] = (out.clone(), [x.clone() for x in lg])
     gm._next_rows, gm._next_qkv = rows, qkv
+    gm.decoder.use_tail = True
     assert torch.equal(runs["rows"][0], runs["proj"][0])
     for a, b in zip(runs["rows"][1], runs["proj"][1]):
         assert torch.equal(a, b)
-    assert torch.equal(runs["qkv"][0], runs["proj"][0])
-    for i, (a, b) in enumerate(zip(runs["qkv"][1], runs["proj"][1])):
-        kl = kl_rows(N(b).astype(np.float64), N(a).astype(np.float64))
-        assert kl < 1e-4, (i, kl)
+    for name in ("qkv", "qkv_perop"):
+        assert torch.equal(runs[name][0], runs["proj"][0]), name
+        for i, (a, b) in enumerate(zip(runs[name][1], runs["proj"][1])):
+            kl = kl_rows(N(b).astype(np.float64), N(a).astype(np.float64))
+            assert kl < 1e-4, (name, i, kl)
 
 
 def test_graph_replay_matches_eager(dev):
