@@ -200,6 +200,10 @@ struct NextPass {
   long o_ld;
   int Hq, Hk;
   float scale;
+  const f16* ev;   // rows copied as they are, independent of the token: ev row r -> xe row r
+  long ev_ld;      // (D wide; the depth decoder's first pass: the projected backbone state)
+  f16* xe;
+  long xe_ld;
 };
 
 // Pair (row, kv head) of the next pass's layer-0 attention for the sampled token tok, one wave:
@@ -452,6 +456,13 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   }
   __syncthreads();
   if (wv != 0) {
+    if (wv == SMP_THREADS / 64 - 1 && nx.ev) {  // the last wave: rows n (and n + N) of ev
+      for (int h = 0; h < 1 + cfg_on; ++h) {
+        const f16* s = nx.ev + (long)(n + h * N) * nx.ev_ld;
+        f16* d = nx.xe + (long)(n + h * N) * nx.xe_ld;
+        for (int c = 8 * lane; c < nx.D; c += 512) *(f16x8*)(d + c) = *(const f16x8*)(s + c);
+      }
+    }
     if (aj < npairs) {  // a pair wave: the token, then the pair's attention
       __syncthreads();
       next_attention(nx, s_tok, V, aj, arow, akh, acache, lane, a_k[aj], a_v[aj], a_q[aj],
@@ -591,7 +602,8 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
                                     int64_t* out, long out_stride, const void* rows, long rows_ld,
                                     int rows_n, void* x, long x_ld, int D, const void* qkv,
                                     long qkv_ld, int qkv_n, void* kc, void* vc, int L, int p,
-                                    void* o, long o_ld, int Hq, int Hk, void* stream) {
+                                    void* o, long o_ld, int Hq, int Hk, const void* ev,
+                                    long ev_ld, void* xe, long xe_ld, void* stream) {
   const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   if (!rows || !x || rows_n < V || D <= 0 || (D % 8) || rows_ld < D || (rows_ld % 8) ||
       x_ld < D || (x_ld % 8) || !al(rows) || !al(x))
@@ -609,7 +621,10 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
         !al(kc) || !al(vc) || !al(o))
       return ECD_EINVAL;
   }
+  if (ev && (!xe || ev_ld < D || (ev_ld % 8) || xe_ld < D || (xe_ld % 8) || !al(ev) || !al(xe)))
+    return ECD_EINVAL;
   NextPass nx{};
+  nx.ev = (const f16*)ev; nx.ev_ld = ev_ld; nx.xe = (f16*)xe; nx.xe_ld = xe_ld;
   nx.rows = (const f16*)rows; nx.rows_ld = rows_ld; nx.x = (f16*)x; nx.x_ld = x_ld; nx.D = D;
   if (qkv) {
     nx.qkv = (const f16*)qkv; nx.qkv_ld = qkv_ld; nx.kc = (f16*)kc; nx.vc = (f16*)vc;

@@ -500,6 +500,18 @@ class HeartMuLaLite:
         self.c0_head.pack(stream=True)
         for lin in [self.projection, *self.audio_head]:
             lin.pack()
+        # codebook-0 head and the projection share their input (the backbone state): one GEMV
+        # over [c0 head rows, zero rows up to a multiple of 64, projection rows] gives the
+        # logits and the first decoder pass's projected backbone rows
+        self._c0proj = None
+        c0, pr = self.c0_head, self.projection
+        if c0.qp is not None and pr.qp is not None and c0.K == pr.K:
+            n0 = -(-c0.N // 64) * 64
+            pad = n0 - c0.N
+            self._c0proj = Linear(
+                q8=torch.cat([c0.q8, c0.q8.new_zeros(pad, c0.K), pr.q8]).contiguous(),
+                s8=torch.cat([c0.s8, c0.s8.new_zeros(pad), pr.s8]).contiguous()).pack(stream=True)
+            self._c0proj.n0 = n0
         self.muq_b = f.get("muq_linear.bias").to(dtype)
         self.cb_off = torch.arange(N_CB, device=self.dev) * AUDIO_VOCAB
         self.graphs = {}
@@ -536,22 +548,34 @@ class HeartMuLaLite:
         nqkv = self._next_qkv if nxt is not None else None
         d0 = self.decoder.blocks[0] if nqkv is not None else None
 
-        def pick(i, lg, rows=None, qkv=None):
+        def pick(i, lg, rows=None, qkv=None, x=None, ev=None, xe=None):
             if logits_out is not None:
                 logits_out.append(lg)
             if forced is None:
                 att = {} if qkv is None else dict(qkv=qkv, kc=d0.kc, vc=d0.vc, p=i + 1,
                                                   o=self._onext)
+                if rows is not None and x is None:
+                    x = self._xnext
                 sample_topk(lg, self.N, cfg, temp, topk, samples[:, i], seed=self._seed, pos=pos,
                             salt=i, noise=None if noise is None else noise[i], rows=rows,
-                            x=None if rows is None else self._xnext, **att)
+                            x=x, ev=ev, xe=xe, **att)
             return samples[:, i:i + 1]
 
-        c0 = pick(0, self._c0(last_h))
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
-        h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
+        cp = self._c0proj if nxt is not None else None
+        if cp is not None:
+            # one GEMV for the codebook-0 logits and the projected backbone rows; the sampler
+            # puts those (even rows) and its token's precomputed row (odd rows) into _x0
+            y = torch.empty(B, cp.N, device=self.dev, dtype=torch.float16)
+            gemv_packed(last_h, cp.qp, cp.s8, cp.N, cp.K, out=y, stream=True)
+            pick(0, y[:, :AUDIO_VOCAB], nxt[0], x=self._x0[1::2], ev=y[:, cp.n0:],
+                 xe=self._x0[0::2])
+            h = self._decode(self._x0, self._dpos[0], 2)[1::2]
+        else:
+            c0 = pick(0, self._c0(last_h))
+            h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
         for i in range(1, N_CB):
-            rows = nxt[i - 1] if nxt is not None and i < N_CB - 1 else None
+            rows = nxt[i] if nxt is not None and i < N_CB - 1 else None
             qkv = nqkv[i - 1] if rows is not None and nqkv is not None else None
             ci = pick(i, self._head(i - 1, h), rows, qkv)
             if i < N_CB - 1:
@@ -620,9 +644,10 @@ class HeartMuLaLite:
     @torch.no_grad()
     def _alloc_next_rows(self):
         """The decoder input of passes 1..6 is projection(_embed_audio(i, ci)) (app/engine.py:343),
-        a function of (codebook, token) and the weights only: rows[i - 1][t] holds it for every
-        token t of codebooks i = 1..6 (weight preprocessing, like the packing), and the frame's
-        sampler copies the sampled token's row into the [B, D] buffer ``_xnext``.  Each row comes
+        a function of (codebook, token) and the weights only: rows[i][t] holds it for every
+        token t of codebooks i = 0..6 (weight preprocessing, like the packing), and the frame's
+        sampler copies the sampled token's row into the [B, D] buffer ``_xnext`` (codebook 0:
+        the odd rows of the first pass's [2B, D] input ``_x0``).  Each row comes
         from the frame's own projection launch with B rows (the rows of a launch do not
         interact), so it is bit-equal to the per-frame projection it replaces.  Kept across
         allocations with the same B."""
@@ -635,15 +660,16 @@ class HeartMuLaLite:
             return
         self._next_rows = self._xnext = self._next_qkv = self._onext = None
         V = AUDIO_VOCAB
-        rows = torch.empty(N_CB - 2, V, pr.N, device=self.dev, dtype=torch.float16)
+        rows = torch.empty(N_CB - 1, V, pr.N, device=self.dev, dtype=torch.float16)
         tok = torch.arange(V + B, device=self.dev).clamp_(max=V - 1).view(-1, 1)
-        for cb in range(1, N_CB - 1):
+        for cb in range(N_CB - 1):
             for t0 in range(0, V, B):
                 n = min(B, V - t0)
                 y = embed_gemv_packed(tok[t0:t0 + B], e.table, e.scales, cb, V, pr.qp, pr.s8, pr.N)
-                rows[cb - 1, t0:t0 + n] = y[:n]
+                rows[cb, t0:t0 + n] = y[:n]
         self._next_rows = rows
         self._xnext = torch.empty(B, pr.N, device=self.dev, dtype=torch.float16)
+        self._x0 = torch.empty(2 * B, pr.N, device=self.dev, dtype=torch.float16)
         self._alloc_next_qkv()
 
     @torch.no_grad()
@@ -673,7 +699,7 @@ class HeartMuLaLite:
             pos = torch.full((M,), p, dtype=torch.int64, device=self.dev)
             for t0 in range(0, V, M):
                 n = min(M, V - t0)
-                rms_qkv_rope(self._next_rows[cb - 1, t0:t0 + n], d0.n1, d0.qkv.qp, d0.qkv.s8,
+                rms_qkv_rope(self._next_rows[cb, t0:t0 + n], d0.n1, d0.qkv.qp, d0.qkv.s8,
                              self.decoder.rope, pos[:n], q[:n], kc, vc, 1, Hq, Hk, L, HD)
                 dst = qkv[cb - 1, t0:t0 + n]
                 dst[:, :Hq * HD] = q[:n]

@@ -257,7 +257,7 @@ _silu_mul = _Launcher("_silu_mul", _silu_mul_impl,
 
 # ---------------------------------------------------------------- fused sampler
 def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, noise=None,
-                rows=None, x=None, qkv=None, kc=None, vc=None, p=0, o=None):
+                rows=None, x=None, qkv=None, kc=None, vc=None, p=0, o=None, ev=None, xe=None):
     """CFG mix + temperature + top-k + softmax(log_softmax) + Exponential race in one kernel
     (the math of _sample/_guided, app/engine.py:291-305).
 
@@ -271,7 +271,8 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
     holds projection(embedding of token t) (app/engine.py:343).  With ``qkv`` [>= V,
     (Hq + 2 Hk) * 128] fp16 as well (the next pass's layer-0 q | k | v of each token at slot
     ``p``), k and v also go to slot p of the caches ``kc`` / ``vc`` [B, Hk, L, 128] and each
-    row's decode attention over slots 0 .. p goes to ``o`` [B, Hq * 128]."""
+    row's decode attention over slots 0 .. p goes to ``o`` [B, Hq * 128].  With ``ev`` and
+    ``xe`` ([>= B, D] each), rows of ev are copied to the same rows of xe as they are."""
     dev = _dev(logits, "sample_topk")
     _f16(logits, "sample_topk logits")
     B, V = logits.shape
@@ -311,12 +312,21 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
                 qkv.stride(1) != 1:
             raise ValueError("sample_topk: qkv [>= V, (Hq + 2 Hk) 128], caches [>= B, Hk, L, 128], "
                              "o [>= B, Hq 128]")
+    if (ev is None) != (xe is None):
+        raise ValueError("sample_topk: ev and xe go together")
+    if ev is not None:
+        _f16(ev, "sample_topk ev")
+        _f16(xe, "sample_topk xe")
+        if ev.shape[0] < B or xe.shape[0] < B or ev.shape[1] != D or xe.shape[1] != D or \
+                ev.stride(1) != 1 or xe.stride(1) != 1:
+            raise ValueError("sample_topk: ev and xe must be [>= B, D] with contiguous rows")
     _ffi.call("ecd_sample_topk_next", logits.data_ptr(), logits.stride(0), B, N, float(cfg),
               float(temp), int(topk), V, _ptr(noise), _ptr(seed), _ptr(pos), int(salt),
               out.data_ptr(), out.stride(0), rows.data_ptr(), rows.stride(0), rows.shape[0],
               x.data_ptr(), x.stride(0), D, _ptr(qkv), 0 if qkv is None else qkv.stride(0),
               0 if qkv is None else qkv.shape[0], _ptr(kc), _ptr(vc), L, int(p), _ptr(o),
-              0 if o is None else o.stride(0), Hq, Hk, stream_ptr(dev))
+              0 if o is None else o.stride(0), Hq, Hk, _ptr(ev), 0 if ev is None else ev.stride(0),
+              _ptr(xe), 0 if xe is None else xe.stride(0), stream_ptr(dev))
 
 
 # ---------------------------------------------------------------- packed weights + fused GEMVs

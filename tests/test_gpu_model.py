@@ -147,7 +147,8 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     """Decoder passes 1..6 take their input from the precomputed projection rows (written by
     the sampler) instead of the projection launch: logits and tokens bit-equal to those of the
     projection path, with and without CFG.  With the precomputed layer-0 q|k|v as well (the
-    sampler then writes the cache slot and runs layer 0's attention), the tokens are the same
+    sampler then writes the cache slot and runs layer 0's attention) and the first pass's
+    input from the fused codebook-0 + projection GEMV and the sampler, the tokens are the same
     and every head's logits agree to KL < 1e-4, through the layer tails and through the
     decoder's per-op kernels alike."""
     import torch
@@ -159,18 +160,20 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     g = rng(8)
     tok = torch.from_numpy(g.integers(0, AUDIO_VOCAB, (B, N_CB))).to(dev)
     noise = torch.from_numpy(g.exponential(1.0, (N_CB, Nt, AUDIO_VOCAB)).astype(np.float32)).to(dev)
-    rows, qkv = gm._next_rows, gm._next_qkv
+    rows, qkv, c0p = gm._next_rows, gm._next_qkv, gm._c0proj
+    assert c0p is not None
     runs = {}
     for name, r, q, tail in (("proj", None, None, True), ("rows", rows, None, True),
                              ("qkv", rows, qkv, True), ("qkv_perop", rows, qkv, False)):
         gm._next_rows, gm._next_qkv = r, q
+        gm._c0proj = c0p if q is not None else None
         gm.decoder.use_tail = tail
         lg = []
         out = gm._step(tok, torch.full((B, 1), 3, dtype=torch.long, device=dev), None, 1.5, 50,
                        1.0, noise=noise, logits_out=lg)
         torch.cuda.synchronize()
         runs[name] = (out.clone(), [x.clone() for x in lg])
-    gm._next_rows, gm._next_qkv = rows, qkv
+    gm._next_rows, gm._next_qkv, gm._c0proj = rows, qkv, c0p
     gm.decoder.use_tail = True
     assert torch.equal(runs["rows"][0], runs["proj"][0])
     for a, b in zip(runs["rows"][1], runs["proj"][1]):

@@ -164,10 +164,14 @@ def test_sampler_next_rows(dev, N, cfg_on, philox):
         sample_topk(logits, N, 1.5, 1.0, 50, want, **kw)
         got = torch.full((B,), -1, dtype=torch.int64, device=dev)
         x = torch.full((B + 2, D), 7.0, dtype=torch.float16, device=dev)
-        sample_topk(logits, N, 1.5, 1.0, 50, got, rows=rows, x=x, **kw)
+        # the token-independent copy: ev rows into the even rows of a [2B, D] buffer
+        ev = T(g.standard_normal((B, D), dtype=np.float32).astype(np.float16), dev)
+        x2 = torch.full((2 * B, D), 5.0, dtype=torch.float16, device=dev)
+        sample_topk(logits, N, 1.5, 1.0, 50, got, rows=rows, x=x, ev=ev, xe=x2[0::2], **kw)
         assert torch.equal(got, want), (trial, got, want)
         assert torch.equal(x[:B], rows[got]), trial
         assert bool((x[B:] == 7.0).all())
+        assert torch.equal(x2[0::2], ev) and bool((x2[1::2] == 5.0).all())
 
 
 @pytest.mark.parametrize("N,cfg_on,p", [(4, True, 2), (4, True, 7), (3, False, 5)])
