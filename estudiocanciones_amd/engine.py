@@ -524,12 +524,14 @@ class HeartMuLaLite:
 
     # -------------------------------------------------- one frame (backbone + 7 decoder passes)
     def _frame_fast(self, last_h, cfg, topk, temp, pos=None, forced=None, logits_out=None,
-                    noise=None):
+                    noise=None, normed=True):
         """app/engine.py:328-343.  Sampling is one fused kernel per codebook (CFG, temperature,
         top-k, Exponential race) writing straight into the [B, 8] token tensor; its draws are
         keyed by the seed and the frame position ``pos`` (int64 device tensor, first element).
         ``forced`` [B, 8] replaces the samples (teacher forcing), ``logits_out`` collects the
-        8 logit tensors, ``noise`` [8, N, V] fixes the Exponential draws (tests)."""
+        8 logit tensors, ``noise`` [8, N, V] fixes the Exponential draws (tests).
+        ``normed=False``: last_h is the backbone's residual stream before its final RMSNorm,
+        which the first GEMV then applies itself."""
         B = self.B
         if getattr(self, "_dpos", None) is None or self._dpos[0].shape[0] != 2 * B:
             self._dpos = [torch.arange(2, device=self.dev).repeat(B)] + [
@@ -563,11 +565,18 @@ class HeartMuLaLite:
 
         # decoder pass 0: two rows per batch entry (backbone state, codebook-0 embedding)
         cp = self._c0proj if nxt is not None else None
+        if cp is None and not normed:
+            last_h = krms(last_h, self.backbone.norm)
         if cp is not None:
-            # one GEMV for the codebook-0 logits and the projected backbone rows; the sampler
-            # puts those (even rows) and its token's precomputed row (odd rows) into _x0
+            # one GEMV for the codebook-0 logits and the projected backbone rows (with the
+            # backbone's final RMSNorm as its prologue when last_h is not normed yet); the
+            # sampler puts those (even rows) and its token's precomputed row (odd rows) into _x0
             y = torch.empty(B, cp.N, device=self.dev, dtype=torch.float16)
-            gemv_packed(last_h, cp.qp, cp.s8, cp.N, cp.K, out=y, stream=True)
+            if normed:
+                gemv_packed(last_h, cp.qp, cp.s8, cp.N, cp.K, out=y, stream=True)
+            else:
+                rms_gemv_packed(last_h, self.backbone.norm, cp.qp, cp.s8, cp.N, cp.K,
+                                stream=True, out=y)
             pick(0, y[:, :AUDIO_VOCAB], nxt[0], x=self._x0[1::2], ev=y[:, cp.n0:],
                  xe=self._x0[0::2])
             h = self._decode(self._x0, self._dpos[0], 2)[1::2]
@@ -622,10 +631,14 @@ class HeartMuLaLite:
         return embed_gemv_packed(tok, e.table, e.scales, cb, AUDIO_VOCAB, pr.qp, pr.s8, pr.N, even=ev)
 
     def _step(self, tok, pos, bucket, cfg, topk, temp, **kw):
-        """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349)."""
+        """tok [B, 8] previous frame; pos [B, 1] (app/engine.py:345-349).  Where the frame's
+        first GEMV takes the backbone's final RMSNorm as its prologue, the backbone step returns
+        its residual stream."""
         h = self.audio_emb.sum_codebooks(tok, AUDIO_VOCAB)
-        return self._frame_fast(self.backbone.decode(h, pos[:, 0].contiguous(), 1), cfg, topk, temp,
-                                pos=pos, **kw)
+        fused = kw.get("forced") is None and self._next_rows is not None and \
+            self._c0proj is not None and all(b.qkv.qp is not None for b in self.backbone.blocks)
+        hb = self.backbone.decode(h, pos[:, 0].contiguous(), 1, final_norm=not fused)
+        return self._frame_fast(hb, cfg, topk, temp, pos=pos, normed=not fused, **kw)
 
     # -------------------------------------------------- caches
     def alloc(self, n, L, cfg_scale=1.5, seed=None):
