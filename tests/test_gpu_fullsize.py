@@ -4,6 +4,8 @@
   7 passes of the 4-layer 1024-wide depth decoder (8q/2kv, FFN 8192), batch 8 (4 takes x CFG),
   teacher forced, at attended KV length 750 (eager, then the same frame replayed as a hipGraph)
   and at 3256 (a 256-token prompt plus 3000 frames);
+* the sampled frame (decoder inputs and layer 0 from the samplers, fused codebook-0 GEMV)
+  against the teacher-forced frame on the tokens it sampled;
 * the same frame with the reference's own depth decoder (3 layers, 3072 wide, 8q/4kv, head_dim
   384; app/engine.py:24, :116, :161);
 * the prompt pass at the 3B layer shape, batch 8 x 256 tokens, cache capacity 3514;
@@ -172,6 +174,40 @@ def test_c3_frame_kv3256(dev, c3):
     """The same frame at the end of a 4-minute song: 256-token prompt + 3000 frames."""
     om, gm = c3
     _frame(om, gm, 3256, seed=32)
+
+
+def test_c3_sampled_frame_matches_forced(dev, c3):
+    """The sampled frame at full size runs the decoder passes' inputs and layer 0 from the
+    samplers, the fused codebook-0 + projection GEMV and the backbone's final norm in that
+    GEMV's prologue. The teacher-forced frame with the tokens it sampled runs the projection
+    and head launches instead. Same function up to the fp32 summation order: KL < 1e-4 on all
+    8 heads, and the same backbone cache slot bit for bit."""
+    import torch
+    om, gm = c3
+    n, att = 4, 750
+    gm.alloc(n, att + 258)
+    B = gm.B
+    assert gm._next_rows is not None and gm._next_qkv is not None and gm._c0proj is not None
+    _fill_caches(om, gm, att, seed=41)
+    g = rng(42)
+    tok = torch.from_numpy(g.integers(0, AUDIO_VOCAB, (B, N_CB))).to(dev)
+    pt = torch.full((B, 1), att - 1, dtype=torch.long, device=dev)
+    noise = torch.from_numpy(g.exponential(1.0, (N_CB, n, AUDIO_VOCAB)).astype(np.float32)).to(dev)
+    print("[frame] sampled, kv 750", flush=True)
+    lg_s = []
+    samples = gm._step(tok, pt, None, 1.5, 50, 1.0, noise=noise, logits_out=lg_s).clone()
+    torch.cuda.synchronize()
+    lg_s = [N(x).astype(np.float64) for x in lg_s]
+    slot = [(b.kc[:, :, att - 1].clone(), b.vc[:, :, att - 1].clone()) for b in gm.backbone.blocks]
+    print("[frame] teacher-forced with the sampled tokens, kv 750", flush=True)
+    lg_f = []
+    gm._step(tok, pt, None, 1.5, 50, 1.0, forced=samples, logits_out=lg_f)
+    torch.cuda.synchronize()
+    for i in range(N_CB):
+        kl = kl_rows_max(N(lg_f[i]).astype(np.float64), lg_s[i])
+        assert kl < 1e-4, (i, kl)
+    for b, (k, v) in zip(gm.backbone.blocks, slot):
+        assert torch.equal(b.kc[:, :, att - 1], k) and torch.equal(b.vc[:, :, att - 1], v)
 
 
 def test_reference_decoder_frame_kv750(dev):
