@@ -8,23 +8,24 @@ frame (embedding, backbone, 8 heads, 8 CFG samplings, 7 decoder passes) replayed
 hipGraph.  Random-init weights quantised to int8 per row on the GPU; KV cache prefilled
 with N(0, 1) values; everything resident in HBM before the timed region.
 
-Prints one JSON line: frames/s (value), the GEMV roofline (hipEvent-timed launches of one
-frame's GEMV sequence, algorithmic bytes N*K + 2N + 2MK + 2MN (+2MN residual) per launch),
-the same frame at a second KV length (``target_point``, default 4096: frames/s and the HBM
-fractions of the GEMV family and the decode attention there), the prompt pass, one codec
-detokenize window from codes to audio (``codec_window``: code embedding + 10 CFG Euler steps
-of the 30-layer flow-matching estimator at 744 frames, then the waveform decoder to 2 x 29.76 s
-at 48 kHz), and a CPU baseline: the reference's CPU
-path (numpy float32 restatement) timed on a bounded sample of layers on the host cores and
-scaled to a frame.
+Prints one JSON line: frames/s (value); the roofline of the dominant kernel (the backbone's
+layer-tail launch: algorithmic bytes per launch over its hipEvent-timed mean launch time, the 28
+launches of one frame captured and replayed on their own stream); the GEMV family of one frame
+(every int8-weight launch); the same frame at a second KV length (``target_point``, default
+4096, with the backbone tail's own roofline there); the prompt pass; one codec detokenize
+window from codes to audio (``codec_window``); the isolated C1 kernels; the frame with the
+reference's own depth decoder; and a CPU baseline: the reference's CPU path restated on torch
+(``oracle/cpu_torch.py``: dequantised F.linear, SDPA, the masked decoder, the sampler) timed on
+whole frames on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--kv 750] [--target-kv 4096] [--decoder 1024|ref]
-                    [--no-cpu]
+                    [--song] [--no-cpu]
 
-HBM traffic of the GEMV family (``roofline.traffic``) comes from two rocprofv3 counter runs of
-this script with a calibration copy appended (``--copy-calib-mib``), summarised by
-``--pmc-summary FETCH_CSV WRITE_CSV`` into ``profiles/gemv_family_traffic.json``, which the
-timed run reads back.
+HBM traffic of the backbone tail (``roofline.traffic``) comes from two rocprofv3 counter runs
+of this script with a calibration copy appended (``--copy-calib-mib``), summarised by
+``--pmc-summary FETCH_CSV WRITE_CSV`` into ``profiles/layer_tail_backbone_traffic.json``,
+which the timed run reads back.  ``--trace-summary STATS_CSV`` turns a rocprofv3
+``--kernel-trace --stats`` run of this script into the per-launch-class table of one frame.
 """
 from __future__ import annotations
 
@@ -74,6 +75,12 @@ def parse():
                     help="append one ecd_copy_bytes of this many MiB (counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter_collection.csv files and exit")
+    ap.add_argument("--no-song", dest="song", action="store_false",
+                    help="skip the song leg (generate() over a 256-token prompt and 3000 frames)")
+    ap.add_argument("--song-frames", type=int, default=3000)
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-launch-class table of one frame from a rocprofv3 --kernel-trace "
+                         "csv of this script, and exit")
     ap.add_argument("--pmc-gemm-summary", metavar="CSV",
                     help="summarise the prompt GEMM's MFMA / VALU counters of one rocprofv3 --pmc "
                          "counter_collection.csv and exit")
@@ -222,6 +229,10 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     dt = time.perf_counter() - t0
     fps = steps / dt
     ms = dt / steps * 1e3
+    # a gate wait of a persistent layer-tail launch that gave up leaves its frames undefined
+    if model.tail_error():
+        raise RuntimeError(f"KV {kv}: a layer-tail launch timed out at a gate during the timed "
+                           "frames; the measurement is void")
 
     # ------------------------------------------------ per-kernel roofline of one frame
     # Record every C-ABI launch of one eager frame step, then replay the GEMV-family and the
@@ -230,7 +241,7 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     from estudiocanciones_amd import _ffi
     calls = []
     orig_call = _ffi.call
-    orig_attn = E._attn
+    orig_attn = E.Stack._attention
 
     def rec_call(name, *a):
         calls.append((name, a))
@@ -238,14 +249,11 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
 
     attn_lens = []
 
-    class RecAttn:
-        def __getitem__(self, grid):
-            launch = orig_attn[grid]
-
-            def f(q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale, **kw):
-                attn_lens.append(((pos.cpu() + 1).clamp(0, L).tolist(), q.shape[0], Hq, Hk, kw["HD"]))
-                return launch(q, kc, vc, pos, o, pm, pl, pa, S, Hq, Hk, L, scale, **kw)
-            return f
+    def rec_attn(st, b, q, pos, S, splits=None):
+        # the engine's standalone attention: one ecd_decode_attn launch per call
+        L = b.kc.shape[2]
+        attn_lens.append(((pos.cpu() + 1).clamp(0, L).tolist(), q.shape[0], b.h, b.kvh, b.hd))
+        return orig_attn(st, b, q, pos, S, splits)
 
     # a stack's layer-0 head launch runs that layer's attention: its cache lengths
     head_lens = []
@@ -257,11 +265,11 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
                           nxt["Hk"], nxt["HD"]))
         return orig_head(x, nxt, o_next, F, *a, **kw)
 
-    _ffi.call, E._attn, E.layer_head = rec_call, RecAttn(), rec_head
+    _ffi.call, E.Stack._attention, E.layer_head = rec_call, rec_attn, rec_head
     try:
         model._step(static["tok"], static["pos"], Lcap, 1.5, 50, 1.0)
     finally:
-        _ffi.call, E._attn, E.layer_head = orig_call, orig_attn, orig_head
+        _ffi.call, E.Stack._attention, E.layer_head = orig_call, orig_attn, orig_head
     torch.cuda.synchronize()
 
     def gemv_family_bytes(name, a):
@@ -389,6 +397,9 @@ def main():
     if args.pmc_gemm_summary:
         print(json.dumps(pmc_gemm_summary(args.pmc_gemm_summary), indent=1))
         return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the decode path has no "
                           "multi-GPU mode (takes would shard by data parallelism with no collectives)"}))
@@ -429,6 +440,7 @@ def main():
             "backbone_attn_frac": (round(tp["bb_attn_gbps"] / HBM_PEAK_GBPS, 4)
                                    if tp["bb_attn_gbps"] else None),
             "frame_frac_of_hbm": round(tp["frame_bytes"] * tp["fps"] / 1e9 / HBM_PEAK_GBPS, 4),
+            "backbone_tail": roofline_entry(tp, None),
         }
     fps, ms = main_pt["fps"], main_pt["ms"]
     g_gbps, a_gbps, bb_attn_gbps = main_pt["g_gbps"], main_pt["a_gbps"], main_pt["bb_attn_gbps"]
@@ -530,6 +542,10 @@ def main():
         "codec_window": codec,
         "setup_s": round(t_build, 1),
     }
+    if args.song:
+        tp_ms = target["ms_per_step"] if target else None
+        res["song"] = measure_song(torch, E, model, dev, n, args.song_frames, args.prompt or 256,
+                                   (args.kv, ms), (args.target_kv, tp_ms), g)
     if args.isolated:
         res["isolated"] = measure_isolated(torch, dev)
     res["drop_in"] = measure_drop_in(torch, E, KK, model, dev, n, args.kv, g)
@@ -540,6 +556,104 @@ def main():
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(wcpu, bb, dec, n, args.kv, args.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+
+def measure_song(torch, E, model, dev, n, frames, P, pt_a, pt_b, g):
+    """The 4-minute song regime through HeartMuLaLite.generate (app/engine.py:374-448): a
+    P-token prompt pass, then ``frames`` frames at batch 2n with every frame's tokens forced
+    (random, no EOS, cond and uncond rows alike) so the song runs to its end while the attended
+    KV grows from P to P + frames; CFG 1.5, graph replay with the host's EOS / error read every
+    25 frames.  Reports the alloc-time per-token tables (time and bytes, built once per batch
+    size), the wall time of the whole call, its frame rate, and the host loop's share: 1 - the
+    GPU time the frames need (frame time interpolated linearly in KV between the two timed
+    points ``pt_a``, ``pt_b`` = (kv, ms)) over the measured wall time of the frame loop."""
+    import time as _t
+    B = 2 * n
+    # the tables are kept across allocations with the same batch size: drop them to time a
+    # first allocation
+    model._next_rows = model._xnext = model._next_qkv = model._onext = None
+    torch.cuda.synchronize()
+    t0 = _t.perf_counter()
+    model.alloc(n, P + frames + 258, cfg_scale=1.5)
+    torch.cuda.synchronize()
+    alloc_s = _t.perf_counter() - t0
+    tab_bytes = sum(t.numel() * t.element_size() for t in (model._next_rows, model._next_qkv)
+                    if t is not None)
+    forced = torch.randint(0, E.AUDIO_EOS, (frames + 1, B, E.N_CB), generator=g, device=dev)
+    forced[:, n:] = forced[:, :n]
+    text = torch.randint(0, model.text_emb.table.shape[0], (P,), generator=g, device=dev)
+    marks = []
+    torch.cuda.synchronize()
+    t1 = _t.perf_counter()
+    out = model.generate(text, 3, max_ms=frames * E.FRAME_MS, n=n, forced=forced,
+                         progress=lambda a, b: marks.append(_t.perf_counter()))
+    torch.cuda.synchronize()
+    wall = _t.perf_counter() - t1
+    if model.frames_run != frames or out[0].shape[1] != frames + 1:
+        raise RuntimeError(f"song: ran {model.frames_run} of {frames} frames")
+    # frames 25 .. frames - 25 between the first and last progress marks (graph replays only)
+    loop_s = marks[-1] - marks[0] if len(marks) > 1 else None
+    loop_frames = 25 * (len(marks) - 1)
+    (ka, ma), (kb, mb) = pt_a, pt_b
+    gpu_s = None
+    if loop_s and ma and mb and kb != ka:
+        slope = (mb - ma) / (kb - ka)
+        kv = [P + 25 + i for i in range(loop_frames)]
+        gpu_s = sum(ma + slope * (k - ka) for k in kv) / 1e3
+    return {
+        "workload": (f"generate(): {P}-token prompt, {frames} forced frames (KV {P} -> "
+                     f"{P + frames}), batch {B} ({n} takes x CFG 1.5), graph replay"),
+        "alloc_tables_s": round(alloc_s, 3),
+        "tables_bytes": int(tab_bytes),
+        "wall_s": round(wall, 3),
+        "frames_per_s": round(frames / wall, 2),
+        "loop_frames_per_s": round(loop_frames / loop_s, 2) if loop_s else None,
+        "first_25_frames_s": round(marks[0] - t1, 4) if marks else None,
+        "host_loop_share": round(1 - gpu_s / loop_s, 4) if gpu_s else None,
+        "host_loop_share_basis": "frame time interpolated in KV between the timed points "
+                                 f"{ka} and {kb}",
+    }
+
+
+def trace_summary(path, nframes=10):
+    """One frame's launches by kernel from a rocprofv3 --kernel-trace csv of this script: the
+    dispatches are ordered by start time, frames begin at each embed_sum launch (the frame's
+    first kernel), and the table averages the last ``nframes`` complete graph-replayed frames
+    before the final two: per kernel the time per frame, launches per frame and the mean launch
+    time, plus the frame's span, kernel-time sum and gaps."""
+    import collections
+    import csv
+    import re
+    rows = list(csv.DictReader(open(path, newline="")))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+    def short(name):
+        n = re.sub(r"\(.*", "", name).replace("void ", "")
+        return n[:90]
+    starts = [i for i, r in enumerate(rows) if "embed_sum" in r["Kernel_Name"]]
+    frames = [(starts[k], starts[k + 1]) for k in range(len(starts) - 1)]
+    sel = frames[-(nframes + 2):-2] if len(frames) > nframes + 2 else frames
+    if not sel:
+        raise SystemExit(f"{path}: no complete frame (no two embed_sum launches)")
+    tot, cnt = collections.defaultdict(float), collections.defaultdict(int)
+    gaps = span = 0.0
+    for a, b in sel:
+        prev = None
+        for r in rows[a:b]:
+            t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            k = short(r["Kernel_Name"])
+            tot[k] += (t1 - t0) / 1e3
+            cnt[k] += 1
+            if prev is not None:
+                gaps += (t0 - prev) / 1e3
+            prev = t1
+        span += (int(rows[b - 1]["End_Timestamp"]) - int(rows[a]["Start_Timestamp"])) / 1e3
+    n = len(sel)
+    lines = [f"frames {n}: span {span / n:.1f} us, kernel sum {sum(tot.values()) / n:.1f} us, "
+             f"gaps {gaps / n:.1f} us, launches {sum(cnt.values()) / n:.0f}"]
+    for k, v in sorted(tot.items(), key=lambda kv: -kv[1]):
+        lines.append(f"  {v / n:8.1f} us  {cnt[k] / n:5.0f} x {v / cnt[k]:7.2f} us  {k}")
+    return "\n".join(lines)
 
 
 def measure_codec(torch, dev, steps, seed):
@@ -637,7 +751,11 @@ def measure_isolated(torch, dev, min_bytes=768 << 20):
     serve the repeated reads: GEMV 3072 -> 8192 and 8192 -> 3072 at 1/2/4/8 rows (packed weights
     with streaming loads, the engine's path, and the drop-in int8_mm on row-major weights), and
     GQA decode attention 24q / 8kv, head_dim 128, 16 splits + combine over 512 ... 8192 cached
-    tokens at batch 1 and 8 (every row at position L - 1)."""
+    tokens at batch 1 and 8 (every row at position L - 1), with the reference's grid (``us``)
+    and with the engine's split count (``engine_us``: enough splits for about two waves per
+    CU)."""
+    from estudiocanciones_amd import _ffi
+    from estudiocanciones_amd import engine as E
     from estudiocanciones_amd import kernels as KK
     out = {"gemv": [], "attention": []}
     for N, K in ((8192, 3072), (3072, 8192)):
@@ -682,11 +800,28 @@ def measure_isolated(torch, dev, min_bytes=768 << 20):
                                       G=Hq // Hk, NSPLIT=ns)
                 KK._attn_combine[(B * Hq,)](pm, pl, pa, o, HD=HD, NSPLIT=ns)
             ms = _rotated_time(torch, [lambda kc=kc, vc=vc: one(kc, vc) for kc, vc in zip(kcs, vcs)])
+            # the engine's own split count (grid of about two waves per CU)
+            ens = E.attention_splits(B, Hk, L)
+            epm = torch.empty(B * Hq * ens, device=dev)
+            epl = torch.empty_like(epm)
+            epa = torch.empty(B * Hq * ens, HD, device=dev)
+
+            def eng(kc, vc):
+                st = torch.cuda.current_stream().cuda_stream
+                _ffi.call("ecd_decode_attn", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                          pos.data_ptr(), o.data_ptr(), epm.data_ptr(), epl.data_ptr(),
+                          epa.data_ptr(), B, 1, Hq, Hk, L, HD, ens, sc, st)
+                _ffi.call("ecd_attn_combine", epm.data_ptr(), epl.data_ptr(), epa.data_ptr(),
+                          o.data_ptr(), B * Hq, HD, ens, st)
+            ems = _rotated_time(torch, [lambda kc=kc, vc=vc: eng(kc, vc) for kc, vc in zip(kcs, vcs)])
             alg = attn_bytes(B, Hq, Hk, HD, [L] * B)
             out["attention"].append({"B": B, "L": L, "sets": sets, "algorithmic_bytes": alg,
                                      "us": round(ms * 1e3, 2),
                                      "GBps": round(alg / ms / 1e6, 1),
-                                     "frac": round(alg / ms / 1e6 / HBM_PEAK_GBPS, 4)})
+                                     "frac": round(alg / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                                     "engine_splits": ens,
+                                     "engine_us": round(ems * 1e3, 2),
+                                     "engine_frac": round(alg / ems / 1e6 / HBM_PEAK_GBPS, 4)})
             del kcs, vcs
             torch.cuda.empty_cache()
     return out

@@ -175,13 +175,18 @@ constexpr int SCRATCH_MAX_DEVICES = 64;
 static void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
-static int attn_scratch_ptr(void** out) {
+static int attn_scratch_ptr(void** out, hipStream_t st) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return ECD_ENOTSUP;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // the lookup may load the code object on this device: not while `st` is being captured
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return (int)e;
+    if (cs != hipStreamCaptureStatusNone) return ECD_ENOTSUP;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(attn_scratch));
     if (e != hipSuccess) return (int)e;
@@ -247,7 +252,7 @@ int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const
   const long need = 2 * part + rhs * HD * 4;
   if (need > ATTN_SCRATCH_BYTES) return ECD_ENOMEM;
   void* base = nullptr;
-  const int rc = attn_scratch_ptr(&base);
+  const int rc = attn_scratch_ptr(&base, (hipStream_t)stream);
   if (rc != ECD_OK) return rc;
   float* pm = (float*)base;
   float* pl = (float*)((char*)base + part);

@@ -65,6 +65,7 @@ struct GemvArgs {
   f16* kc;
   f16* vc;
   int S, Hq, Hk, L, HD;
+  int qrows;  // 1: q receives every head of row m as row m of [M, N] (q | k | v), no cache write
   // EPI_SILU
   f16* mm;
   // EPI_PARTIAL: ks K-splits (blockIdx.z), fp32 partial sums [ks][M][N]
@@ -165,7 +166,9 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, int n0, int m0,
     } else {
       o = (f16x4){yv[0], yv[1], yv[2], yv[3]};
     }
-    if (h < a.Hq) {
+    if (a.qrows) {
+      *(f16x4*)(a.q + (long)me * N + nb) = o;
+    } else if (h < a.Hq) {
       *(f16x4*)(a.q + ((long)me * a.Hq + h) * HD + d) = o;
     } else if (pval) {
       const int b = me / a.S;
@@ -940,8 +943,9 @@ int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const v
   a.wp = (const int8_t*)wp; a.s = (const f16*)s; a.M = M; a.K = K; a.dense = flags & 1; a.stream_hint = (flags >> 1) & 1;
   a.N = (Hq + 2 * Hk) * HD;
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
-  a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
-  if (check_common(a) || !x || !nw || !rope || !pos || !q || !kc || !vc || S <= 0 || Hq <= 0 ||
+  a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD; a.qrows = (flags >> 2) & 1;
+  if (check_common(a) || !x || !nw || !rope || !pos || !q || (!a.qrows && (!kc || !vc)) ||
+      S <= 0 || Hq <= 0 ||
       Hk <= 0 || L <= 0 || HD <= 0 || (HD % 4) || (Hq % Hk) || ldx < K || (ldx % 8) ||
       !aligned16(x) || !aligned16(nw))
     return ECD_EINVAL;

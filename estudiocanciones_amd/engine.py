@@ -37,7 +37,8 @@ from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_
                       gemm_rope_packed, gemv_packed, int8_mm, layer_head, layer_tail,
                       layer_tail_supported,
                       layer_tail_ws_bytes, next_power_of_2,
-                      pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_w13_silu,
+                      pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_qkv_rope_rows,
+                      rms_w13_silu,
                       sample_topk, stream_ptr)
 
 AUDIO_VOCAB = 8197
@@ -47,6 +48,21 @@ MUQ_DIM = 512
 DIM = 3072
 TEXT_BOS, TEXT_EOS, AUDIO_EOS, EMPTY_ID = 128000, 128001, 8193, 0
 FRAME_MS = 80
+
+ATT_SHORT = 128        # caches of at most this many slots: one attention split per (row, kv head)
+ATT_SPLITS_MAX = 64   # longest split count of the engine's standalone attention
+ATT_WAVES = 512       # waves the standalone attention grid aims at (two per CU of an MI355X)
+
+
+def attention_splits(R, Hk, L):
+    """Split count of the engine's standalone decode attention over a cache of L slots: one
+    split for short caches, else enough splits that R x Hk x splits waves cover the CUs about
+    twice, at least 16 (fewer splits leave each wave a long serial walk) and at most
+    ATT_SPLITS_MAX."""
+    if L <= ATT_SHORT:
+        return 1
+    return max(16, min(ATT_SPLITS_MAX, -(-ATT_WAVES // max(1, R * Hk))))
+
 
 BACKBONE = dict(layers=28, heads=24, kv_heads=8, max_seq=8192, dim=DIM)
 # the reference's depth decoder (app/engine.py:24; head_dim = 3072 // 8 = 384)
@@ -214,7 +230,7 @@ class Stack:
         self.dim = dim
         self.hd = dim // cfg["heads"]
         self.max_seq = cfg["max_seq"]
-        self.nsplit = 16
+        self.att_ws = None  # split partials of the standalone attention (m | l | acc, fp32)
         self.tail = None   # layer-tail buffers for B-row decode steps
         self.tail2 = None  # the same for 2B rows (two rows per cache), sharing sync, ws and err
         self.use_tail = True
@@ -223,9 +239,15 @@ class Stack:
 
     def alloc(self, B, L, dev, dtype):
         self.rope = rope_cache(self.hd, max(L, 16), device=dev)
-        self.nsplit = 1 if L <= 128 else 16
         for b in self.blocks:
             b.alloc(B, L, dev, dtype)
+        if self.blocks and L > ATT_SHORT:
+            # partials of a decode step of up to 2B rows (two rows per cache) or of a short
+            # prompt through the decode path (at most PROMPT_GEMM_ROWS rows): R rows take
+            # R x attention_splits(R) <= 16 R + ATT_WAVES (row, split) pairs per query head
+            hq = max(b.h for b in self.blocks)
+            n = (16 * max(2 * B, PROMPT_GEMM_ROWS) + ATT_WAVES) * hq
+            self.att_ws = torch.empty(n * (2 + self.hd), device=dev, dtype=torch.float32)
         self.tail = self._tail_buffers(B, dev, dtype, L)
         self.tail2 = None if self.tail is None else \
             self._tail_buffers(2 * B, dev, dtype, L, share=self.tail)
@@ -270,7 +292,7 @@ class Stack:
     def free(self):
         for b in self.blocks:
             b.kc = b.vc = None
-        self.tail = self.tail2 = None
+        self.tail = self.tail2 = self.att_ws = None
 
     def __call__(self, x, pos, attn_len=None, mask=None):
         """Prompt pass (app/engine.py:174-178): x [B, S, D], pos [B, S] absolute positions
@@ -309,7 +331,7 @@ class Stack:
             else:
                 # one split per row: a prompt row attends at most the prompt (no empty splits,
                 # no combine pass); the rows themselves give the parallelism
-                o = self._attention(b, q, pos, S, 1)
+                o = self._attention(b, q, pos, S, splits=1)
             x = gemm_packed(o, b.o.qp, b.o.sp, b.o.N, b.o.K, res=x)
             mm = gemm_silu_packed(krms(x, b.n2), b.w13.qp, b.w13.sp, b.w13.N // 2, b.w13.K)
             x = gemm_packed(mm, b.w2.qp, b.w2.sp, b.w2.N, b.w2.K, res=x)
@@ -329,10 +351,9 @@ class Stack:
             h = self.decode_reference(x, pos, S)
             return h if final_norm else None
         R = x.shape[0]
-        ns = self.nsplit
         t = next((t for t in (self.tail, self.tail2) if t is not None and R == t["M"]), None)
         if self.use_tail and t is not None:
-            x = self._decode_tail(x, pos, S, ns, t, o0)
+            x = self._decode_tail(x, pos, S, t, o0)
             return krms(x, self.norm) if final_norm else x
         for i, b in enumerate(self.blocks):
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
@@ -342,13 +363,13 @@ class Stack:
                 q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
                 rms_qkv_rope(x, b.n1, b.qkv.qp, b.qkv.s8, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk,
                              L, HD, stream=b.qkv.stream)
-                o = self._attention(b, q, pos, S, ns)
+                o = self._attention(b, q, pos, S)
             x = b.o(o, res=x)
             mm = rms_w13_silu(x, b.n2, b.w13.qp, b.w13.sp, b.w13.N // 2, stream=b.w13.stream)
             x = b.w2(mm, res=x)
         return krms(x, self.norm) if final_norm else x
 
-    def _decode_tail(self, x, pos, S, ns, t, o0=None):
+    def _decode_tail(self, x, pos, S, t, o0=None):
         """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
         ecd_layer_head launch where the shapes allow attention in the launch, else on their
         own; then one ecd_layer_tail launch per layer: the O projection, the MLP, the next
@@ -373,7 +394,7 @@ class Stack:
         else:
             rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
                          b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
-            o = self._attention(b0, q, pos, S, ns)
+            o = self._attention(b0, q, pos, S)
         for i, b in enumerate(self.blocks):
             nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
             nxt = None if nb is None else nxt_of(nb)
@@ -383,39 +404,58 @@ class Stack:
                            nxt=nxt, o_next=o_next, stream=b.w13.stream,
                            no_wait=self.tail_no_wait)
             if nb is not None:
-                o = o_next if o_next is not None else self._attention(nb, q, pos, S, ns)
+                o = o_next if o_next is not None else self._attention(nb, q, pos, S)
         return x
 
-    def _attention(self, b, q, pos, S, ns):
+    def _attention(self, b, q, pos, S, splits=None):
+        """Decode attention of block b for the rows of q (row r over cache slots [0, pos[r]],
+        app/kernels.py:110-167).  Caches of at most ATT_SHORT slots, and prompt passes
+        (``splits=1``: the rows give the parallelism), run one split per (row, kv head) that
+        writes o itself.  Longer caches split the attended range so that the grid has about
+        two waves per CU whatever the row count (attention_splits), and one combine launch
+        merges the partials kept in the stack's workspace."""
         R = q.shape[0]
         Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
+        ns = splits if splits is not None else attention_splits(R, Hk, L)
         o = torch.empty_like(q)
-        HDP = next_power_of_2(HD)
-        if ns > 1:
-            pm = torch.empty(R * Hq * ns, device=q.device)
-            pl = torch.empty_like(pm)
-            pa = torch.empty(R * Hq * ns, HD, device=q.device)
-        else:
-            pm = pl = pa = o
-        _attn[(R, Hk, ns)](q, b.kc, b.vc, pos, o, pm, pl, pa, S, Hq, Hk, L, 1.0 / math.sqrt(HD),
-                           HD=HD, HDP=HDP, G=Hq // Hk, BLK=64 if HD <= 128 else 16, NSPLIT=ns,
-                           num_warps=4)
-        if ns > 1:
-            _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, HDP=HDP, NSPLIT=ns)
+        st = stream_ptr(q.device)
+        if ns == 1:
+            _ffi.call("ecd_decode_attn", q.data_ptr(), b.kc.data_ptr(), b.vc.data_ptr(),
+                      pos.data_ptr(), o.data_ptr(), None, None, None, R, S, Hq, Hk, L, HD, 1,
+                      1.0 / math.sqrt(HD), st)
+            return o
+        n = R * Hq * ns
+        if self.att_ws is None or self.att_ws.numel() < n * (2 + HD):
+            raise RuntimeError("Stack._attention: the split workspace is smaller than the call")
+        pm, pl, pa = self.att_ws[:n], self.att_ws[n:2 * n], self.att_ws[2 * n:n * (2 + HD)]
+        _ffi.call("ecd_decode_attn", q.data_ptr(), b.kc.data_ptr(), b.vc.data_ptr(),
+                  pos.data_ptr(), o.data_ptr(), pm.data_ptr(), pl.data_ptr(), pa.data_ptr(), R, S,
+                  Hq, Hk, L, HD, ns, 1.0 / math.sqrt(HD), st)
+        _ffi.call("ecd_attn_combine", pm.data_ptr(), pl.data_ptr(), pa.data_ptr(), o.data_ptr(),
+                  R * Hq, HD, ns, st)
         return o
 
     def decode_reference(self, x, pos, S):
         """The reference's launch sequence (app/engine.py:180-211) through the drop-in kernel
-        entry points of kernels.py (unpacked weights, one launch per reference kernel)."""
+        entry points of kernels.py (unpacked weights, one launch per reference kernel, the
+        reference's attention grid and split count)."""
         R = x.shape[0]
-        ns = self.nsplit
         for b in self.blocks:
             Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
             qkv = int8_mm(krms(x, b.n1), b.qkv.q8, b.qkv.s8)
             q = torch.empty(R, Hq * HD, device=x.device, dtype=x.dtype)
             _rope_cache[(R, Hq + Hk)](qkv, self.rope, pos, q, b.kc, b.vc, S, Hq, Hk, L,
                                       HD=HD, HALF=next_power_of_2(HD // 2))
-            o = self._attention(b, q, pos, S, ns)
+            ns = 1 if L <= ATT_SHORT else 16
+            o = torch.empty_like(q)
+            pm = torch.empty(R * Hq * ns, device=x.device) if ns > 1 else o
+            pl = torch.empty_like(pm) if ns > 1 else o
+            pa = torch.empty(R * Hq * ns, HD, device=x.device) if ns > 1 else o
+            _attn[(R, Hk, ns)](q, b.kc, b.vc, pos, o, pm, pl, pa, S, Hq, Hk, L,
+                               1.0 / math.sqrt(HD), HD=HD, HDP=next_power_of_2(HD), G=Hq // Hk,
+                               BLK=64 if HD <= 128 else 16, NSPLIT=ns, num_warps=4)
+            if ns > 1:
+                _attn_combine[(R * Hq,)](pm, pl, pa, o, HD=HD, HDP=next_power_of_2(HD), NSPLIT=ns)
             x = int8_mm(o, b.o.q8, b.o.s8, x)
             a = int8_mm(krms(x, b.n2), b.w13.q8, b.w13.s8)
             Fd = a.shape[1] // 2
@@ -533,9 +573,6 @@ class HeartMuLaLite:
         ``normed=False``: last_h is the backbone's residual stream before its final RMSNorm,
         which the first GEMV then applies itself."""
         B = self.B
-        if getattr(self, "_dpos", None) is None or self._dpos[0].shape[0] != 2 * B:
-            self._dpos = [torch.arange(2, device=self.dev).repeat(B)] + [
-                torch.full((B,), i + 1, dtype=torch.long, device=self.dev) for i in range(1, N_CB - 1)]
         if forced is None:
             samples = torch.empty(B, N_CB, dtype=torch.long, device=self.dev)
             if pos is None:
@@ -579,17 +616,18 @@ class HeartMuLaLite:
                                 stream=True, out=y)
             pick(0, y[:, :AUDIO_VOCAB], nxt[0], x=self._x0[1::2], ev=y[:, cp.n0:],
                  xe=self._x0[0::2])
-            h = self._decode(self._x0, self._dpos[0], 2)[1::2]
+            h = self._decode(self._x0, self._pass0_pos, 2)[1::2]
         else:
             c0 = pick(0, self._c0(last_h))
-            h = self._decode(self._project(c0, 0, even=last_h), self._dpos[0], 2)[1::2]
+            h = self._decode(self._project(c0, 0, even=last_h), self._pass0_pos, 2)[1::2]
         for i in range(1, N_CB):
             rows = nxt[i] if nxt is not None and i < N_CB - 1 else None
             qkv = nqkv[i - 1] if rows is not None and nqkv is not None else None
             ci = pick(i, self._head(i - 1, h), rows, qkv)
             if i < N_CB - 1:
                 x = self._xnext if rows is not None else self._project(ci, i)
-                h = self._decode(x, self._dpos[i], 1, o0=None if qkv is None else self._onext)
+                h = self._decode(x, self._pass_pos[i - 1], 1,
+                                 o0=None if qkv is None else self._onext)
         return samples
 
     def _decode(self, x, pos, S, o0=None):
@@ -650,6 +688,11 @@ class HeartMuLaLite:
             seed = int(torch.randint(0, 2 ** 62, (1,)).item())
         self._seed = torch.tensor([seed], dtype=torch.int64, device=self.dev)
         self._pos_prompt = torch.zeros(1, dtype=torch.int64, device=self.dev)
+        # depth-decoder slots: pass 0 runs the row pairs (backbone state, codebook-0 token) at
+        # slots 0 and 1 of each take's cache; pass i = 1 .. 6 writes slot i + 1
+        self._pass0_pos = torch.arange(2 * self.B, device=self.dev) % 2
+        self._pass_pos = torch.arange(2, N_CB, device=self.dev).repeat_interleave(self.B) \
+            .view(N_CB - 2, self.B)
         self.backbone.alloc(self.B, L, self.dev, self.dt)
         self.decoder.alloc(self.B, N_CB, self.dev, self.dt)
         self._alloc_next_rows()
@@ -660,10 +703,10 @@ class HeartMuLaLite:
         a function of (codebook, token) and the weights only: rows[i][t] holds it for every
         token t of codebooks i = 0..6 (weight preprocessing, like the packing), and the frame's
         sampler copies the sampled token's row into the [B, D] buffer ``_xnext`` (codebook 0:
-        the odd rows of the first pass's [2B, D] input ``_x0``).  Each row comes
-        from the frame's own projection launch with B rows (the rows of a launch do not
-        interact), so it is bit-equal to the per-frame projection it replaces.  Kept across
-        allocations with the same B."""
+        the odd rows of the first pass's [2B, D] input ``_x0``).  Each row comes from the
+        frame's own projection kernel with its numerics (one launch per codebook over all V
+        tokens; the rows of a launch do not interact), so it is bit-equal to the per-frame
+        projection it replaces.  Kept across allocations with the same B."""
         pr, e = self.projection, self.audio_emb
         B = self.B
         if pr.qp is None or self.dt != torch.float16:
@@ -674,12 +717,11 @@ class HeartMuLaLite:
         self._next_rows = self._xnext = self._next_qkv = self._onext = None
         V = AUDIO_VOCAB
         rows = torch.empty(N_CB - 1, V, pr.N, device=self.dev, dtype=torch.float16)
-        tok = torch.arange(V + B, device=self.dev).clamp_(max=V - 1).view(-1, 1)
+        tok = torch.arange(V, device=self.dev).view(-1, 1)
         for cb in range(N_CB - 1):
-            for t0 in range(0, V, B):
-                n = min(B, V - t0)
-                y = embed_gemv_packed(tok[t0:t0 + B], e.table, e.scales, cb, V, pr.qp, pr.s8, pr.N)
-                rows[cb, t0:t0 + n] = y[:n]
+            # all V tokens in one launch, with the per-row numerics of the frame's B-row launch
+            embed_gemv_packed(tok, e.table, e.scales, cb, V, pr.qp, pr.s8, pr.N, out=rows[cb],
+                              dense=False)
         self._next_rows = rows
         self._xnext = torch.empty(B, pr.N, device=self.dev, dtype=torch.float16)
         self._x0 = torch.empty(2 * B, pr.N, device=self.dev, dtype=torch.float16)
@@ -690,9 +732,10 @@ class HeartMuLaLite:
         """Layer 0 of decoder pass i (1..6) starts with rms -> q|k|v -> RoPE at position i + 1
         (app/engine.py:189-199) on the input row of the sampled token: again a function of
         (codebook, token) and the weights.  qkv[i - 1][t] holds q heads | k heads | v heads of
-        token t (the per-op kernel rms_qkv_rope, 16 tokens per launch), so the sampler can write
-        the cache slot and run that layer's attention itself; only for head_dim 128 and the
-        pair counts the sampler's folded attention takes."""
+        token t (the per-op kernel rms_qkv_rope writing whole rows, one launch per codebook,
+        with the per-row numerics of a decode step), so the sampler can write the cache slot and
+        run that layer's attention itself; only for head_dim 128 and the pair counts the
+        sampler's folded attention takes."""
         self._next_qkv = self._onext = None
         d0 = self.decoder.blocks[0] if self.decoder.blocks else None
         B, V = self.B, AUDIO_VOCAB
@@ -702,22 +745,12 @@ class HeartMuLaLite:
         Hq, Hk, HD, L = d0.h, d0.kvh, d0.hd, d0.kc.shape[2]
         if L < N_CB:
             return
-        M = 16
         qkv = torch.empty(N_CB - 2, V, (Hq + 2 * Hk) * HD, device=self.dev, dtype=torch.float16)
-        q = torch.empty(M, Hq * HD, device=self.dev, dtype=torch.float16)
-        kc = torch.zeros(M, Hk, L, HD, device=self.dev, dtype=torch.float16)
-        vc = torch.zeros_like(kc)
         for cb in range(1, N_CB - 1):
-            p = cb + 1
-            pos = torch.full((M,), p, dtype=torch.int64, device=self.dev)
-            for t0 in range(0, V, M):
-                n = min(M, V - t0)
-                rms_qkv_rope(self._next_rows[cb, t0:t0 + n], d0.n1, d0.qkv.qp, d0.qkv.s8,
-                             self.decoder.rope, pos[:n], q[:n], kc, vc, 1, Hq, Hk, L, HD)
-                dst = qkv[cb - 1, t0:t0 + n]
-                dst[:, :Hq * HD] = q[:n]
-                dst[:, Hq * HD:(Hq + Hk) * HD] = kc[:n, :, p].reshape(n, Hk * HD)
-                dst[:, (Hq + Hk) * HD:] = vc[:n, :, p].reshape(n, Hk * HD)
+            # every token of codebook cb in one launch, its q | k | v row written in place
+            pos = torch.full((V,), cb + 1, dtype=torch.int64, device=self.dev)
+            rms_qkv_rope_rows(self._next_rows[cb], d0.n1, d0.qkv.qp, d0.qkv.s8, self.decoder.rope,
+                              pos, qkv[cb - 1], Hq, Hk, HD, dense=False)
         self._next_qkv = qkv
         self._onext = torch.empty(B, Hq * HD, device=self.dev, dtype=torch.float16)
 
@@ -729,7 +762,9 @@ class HeartMuLaLite:
         token ids ``text`` [P] (int64) and the muq slot index.  Returns [8, T] if n == 1, else a
         list of n such tensors, each take cut before its first frame holding an EOS token.
         ``forced`` [max_ms // 80 + 1, B, 8] int64 on the device replaces the sampled tokens of
-        every frame (teacher forcing a whole song)."""
+        every frame (teacher forcing a whole song).  Every 25 frames (and at the end) the host
+        reads the takes' EOS frames together with the layer tails' error words, and raises
+        RuntimeError if a tail launch timed out at a gate."""
         if seed is not None and seed >= 0:
             torch.manual_seed(seed)
         text = torch.as_tensor(text, dtype=torch.int64)
@@ -761,8 +796,8 @@ class HeartMuLaLite:
         self._advance(first, st, P, n_frames)
 
         key = (B, cap, topk, float(temperature), float(cfg_scale))
-        ends = st["eos"]
         done = n_frames
+        ends = None
         for i in range(n_frames):
             if abort and abort():
                 self.release()
@@ -779,18 +814,40 @@ class HeartMuLaLite:
                 self._advance(self._step(st["tok"], st["pos"], cap, cfg_scale, topk, temperature,
                                          **kw), st, P, n_frames)
             if (i + 1) % 25 == 0 or i == n_frames - 1:
-                ends = st["eos"].tolist()          # the loop's only device -> host read
+                ends = self._song_status(st["eos"])
                 if min(ends) >= 0:
                     done = i + 1
                     break
                 if progress:
                     progress((i + 1) * FRAME_MS / 1000, max_ms / 1000)
-        if torch.is_tensor(ends):
-            ends = ends.tolist()
+        if ends is None:
+            ends = self._song_status(st["eos"])
         self.frames_run = done
         res = [st["out"][: (e if e >= 0 else done + 1), c].t().clone() for c, e in enumerate(ends)]
         self.release()
         return res[0] if n == 1 else res
+
+    def _song_status(self, eos):
+        """Each take's first EOS frame (-1 while it runs) and the layer tails' error words, in
+        one device -> host read (the song loop's only one).  A set error word means a gate wait
+        of a persistent tail launch gave up (a workgroup of its grid was not resident, e.g.
+        another process held CUs): the frames since the last read are undefined, so the gate
+        state is cleared, the caches are released and the song stops with RuntimeError."""
+        errs = [s.tail["err"] for s in (self.backbone, self.decoder) if s.tail is not None]
+        vals = torch.cat([eos, *[e.to(eos.dtype) for e in errs]]).tolist()
+        n = eos.numel()
+        if any(vals[n:]):
+            failed = [nm for nm, v in zip(("backbone", "decoder"), vals[n:]) if v]
+            self.backbone.tail_reset()
+            self.decoder.tail_reset()
+            self.release()
+            raise RuntimeError(f"layer-tail launch of the {' and '.join(failed)} timed out at a "
+                               "gate (its grid was not all resident); the song was stopped")
+        return vals[:n]
+
+    def tail_error(self):
+        """True if a layer-tail launch of either stack timed out since the last reset."""
+        return self.backbone.tail_error() or self.decoder.tail_error()
 
     def _advance(self, samples, st, P, n_frames):
         """Frame bookkeeping on the device: samples -> next input, frame stored, first EOS frame
@@ -826,10 +883,22 @@ class HeartMuLaLite:
         torch.cuda.empty_cache()
 
     def vram_weights(self):
-        tot = 0
-        for st in (self.backbone, self.decoder):
-            for b in st.blocks:
-                tot += sum(l.nbytes for l in (b.qkv, b.o, b.w13, b.w2))
-        tot += self.audio_emb.nbytes + sum(l.nbytes for l in self.audio_head)
-        tot += self.c0_head.nbytes + self.projection.nbytes
-        return tot
+        """Device bytes of the model's weights: every distinct tensor behind the linear layers
+        (int8 codes, scales, packed tile copies, interleaved scales), the embedding tables,
+        norm vectors and biases, and the per-token tables built at alloc."""
+        seen, total = set(), 0
+        lins = [getattr(b, n) for st in (self.backbone, self.decoder) for b in st.blocks
+                for n in ("qkv", "o", "w13", "w2")]
+        lins += [self.projection, self.c0_head, *self.audio_head]
+        if self._c0proj is not None:
+            lins.append(self._c0proj)
+        ts = [t for lin in lins for t in (lin.q8, lin.s8, lin.qp, lin.sp)]
+        ts += [t for e in (self.text_emb, self.audio_emb) for t in (e.w, e.q8, e.s8)]
+        ts += [t for st in (self.backbone, self.decoder) for b in st.blocks for t in (b.n1, b.n2)]
+        ts += [self.backbone.norm, self.decoder.norm, self.uncond, self.muq_b, self._next_rows,
+               self._next_qkv]
+        for t in ts:
+            if t is not None and t.data_ptr() not in seen:
+                seen.add(t.data_ptr())
+                total += t.numel() * t.element_size()
+        return total

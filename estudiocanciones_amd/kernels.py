@@ -529,6 +529,29 @@ def rms_qkv_rope(x, nw, wp, s, rope, pos, q, kc, vc, S, Hq, Hk, L, HD, eps=1e-5,
               M, S, Hq, Hk, L, HD, K, _flags(M, stream), stream_ptr(x.device))
 
 
+def rms_qkv_rope_rows(x, nw, wp, s, rope, pos, out, Hq, Hk, HD, eps=1e-5, dense=False):
+    """rms -> fused q|k|v GEMV -> RoPE of q and k at pos[m] -> out[m] = q | k | v of row m
+    ([M, (Hq + 2Hk) HD], row stride N, no cache write), one kernel for any M.  ``dense=False``
+    keeps the numerics of a decode step of at most 16 rows (per-row scale after the int8 sum)
+    whatever M is."""
+    K = x.shape[1]
+    _check_x(x, K, "rms_qkv_rope_rows")
+    M = x.shape[0]
+    N = (Hq + 2 * Hk) * HD
+    if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+        raise ValueError("rms_qkv_rope_rows: pos must be contiguous int64 [M]")
+    if rope.dim() != 3 or rope.shape[1] != HD // 2 or rope.dtype != torch.float32:
+        raise ValueError("rms_qkv_rope_rows: rope table must be float32 [L, HD/2, 2]")
+    _f16(out, "rms_qkv_rope_rows out")
+    if out.shape != (M, N) or not out.is_contiguous() or out.data_ptr() % 16:
+        raise ValueError(f"rms_qkv_rope_rows: out must be contiguous [{M}, {N}]")
+    L = rope.shape[0]
+    _ffi.call("ecd_rms_qkv_rope", x.data_ptr(), x.stride(0), nw.data_ptr(), float(eps), wp.data_ptr(),
+              s.data_ptr(), rope.data_ptr(), pos.data_ptr(), out.data_ptr(), None, None,
+              M, 1, Hq, Hk, L, HD, K, int(bool(dense)) | 4, stream_ptr(x.device))
+    return out
+
+
 def rms_w13_silu(x, nw, wp, s_il, F, eps=1e-5, stream=False):
     """rms -> [w1 | w3] GEMV on row-interleaved packed weights -> fp16(silu(a)) * b, [M, F]."""
     K = x.shape[1]
@@ -657,10 +680,12 @@ def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait
     return o_next
 
 
-def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False):
+def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream=False, out=None,
+                      dense=None):
     """int8_mm(Emb(tok[:, 0] + cb * vocab), w, s); with ``even`` [B, K] the input rows are the
     interleave (even[b], emb[b]) and the output has 2B rows.  ``table`` holds int8 rows scaled by
-    ``tscale``, or dense fp16 rows when ``tscale`` is None."""
+    ``tscale``, or dense fp16 rows when ``tscale`` is None.  ``out``: a contiguous [M, N] fp16
+    destination; ``dense``: the numerics (None: int8_mm's rule, dense for more than 16 rows)."""
     dev = _dev(tok, "embed_gemv_packed")
     if tok.dtype != torch.int64:
         raise TypeError("embed_gemv_packed: tok must be int64")
@@ -673,8 +698,13 @@ def embed_gemv_packed(tok, table, tscale, cb, vocab, wp, s, N, even=None, stream
         _f16(even, "embed_gemv_packed even")
         if even.shape != (B, K) or not even.is_contiguous() or even.data_ptr() % 16:
             raise ValueError("embed_gemv_packed: even must be contiguous [B, K]")
-    y = torch.empty(M, N, device=dev, dtype=torch.float16)
+    if out is not None:
+        _f16(out, "embed_gemv_packed out")
+        if out.shape != (M, N) or not out.is_contiguous():
+            raise ValueError(f"embed_gemv_packed: out must be contiguous [{M}, {N}]")
+    y = torch.empty(M, N, device=dev, dtype=torch.float16) if out is None else out
+    fl = _flags(M, stream) if dense is None else (int(bool(dense)) | (2 if stream else 0))
     _ffi.call("ecd_embed_gemv_i8p", tok.data_ptr(), tok.stride(0), table.data_ptr(), _ptr(tscale),
               table.shape[0], int(cb), int(vocab), _ptr(even), wp.data_ptr(), s.data_ptr(),
-              y.data_ptr(), N, M, N, K, _flags(M, stream), stream_ptr(dev))
+              y.data_ptr(), N, M, N, K, fl, stream_ptr(dev))
     return y

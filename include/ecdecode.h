@@ -84,7 +84,10 @@ int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o,
  * Same arguments and results as the two calls it replaces (bit for bit).  Returns ECD_ENOMEM
  * when 2 * ceil256(4 * R * Hq * nsplit) + 4 * R * Hq * nsplit * HD bytes exceed 8 MiB (e.g.
  * R = 16, Hq = 24, nsplit = 16, HD = 128 needs 3.2 MB).  The array keeps the last call's
- * contents; calls that overlap on one GPU (two streams at once) race on it. */
+ * contents; calls that overlap on one GPU (two streams at once) race on it.  The first call
+ * with nsplit > 1 on a device looks the array's address up (hipGetSymbolAddress, which may
+ * load the code object) and must not be made while `stream` is being captured: it then
+ * returns ECD_ENOTSUP; later calls on that device may be captured into a hipGraph. */
 int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const int64_t* pos,
                             void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
                             float scale, void* stream);
@@ -205,7 +208,9 @@ int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const v
 
 /* rms -> q|k|v GEMV -> RoPE -> q [M, Hq*HD] and k/v into kc/vc [B, Hk, L, HD] at pos[m]
  * (row m -> batch m / S): app/engine.py:189-192 (krms, b.qkv, _rope_cache) in one kernel.
- * N = (Hq + 2Hk) * HD, HD % 4 == 0; rope [>= L, HD/2, 2] f32. */
+ * N = (Hq + 2Hk) * HD, HD % 4 == 0; rope [>= L, HD/2, 2] f32.  flags: bit 0 dense numerics,
+ * bit 1 streamed weights, bit 2 row output: q is [M, N] and receives q | k | v of row m (RoPE
+ * at pos[m] applied to q and k) as its row m; kc and vc are not written (may be NULL). */
 int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const void* wp,
                      const void* s, const float* rope, const int64_t* pos, void* q, void* kc,
                      void* vc, int M, int S, int Hq, int Hk, int L, int HD, int K, int flags,

@@ -176,30 +176,33 @@ def test_c3_frame_kv3256(dev, c3):
     _frame(om, gm, 3256, seed=32)
 
 
-def test_c3_sampled_frame_matches_forced(dev, c3):
-    """The sampled frame at full size runs the decoder passes' inputs and layer 0 from the
-    samplers, the fused codebook-0 + projection GEMV and the backbone's final norm in that
-    GEMV's prologue. The teacher-forced frame with the tokens it sampled runs the projection
-    and head launches instead. Same function up to the fp32 summation order: KL < 1e-4 on all
-    8 heads, and the same backbone cache slot bit for bit."""
+def _sampled_vs_forced(gm, att, seed, tables):
+    """One sampled frame at position att - 1 against the teacher-forced frame on the tokens it
+    sampled (injected Exponential draws): KL < 1e-4 on all 8 heads, the backbone cache slot bit
+    for bit.  ``tables``: the precomputed per-token tables the sampled path must be using."""
     import torch
-    om, gm = c3
-    n, att = 4, 750
+    n = 4
     gm.alloc(n, att + 258)
     B = gm.B
-    assert gm._next_rows is not None and gm._next_qkv is not None and gm._c0proj is not None
-    _fill_caches(om, gm, att, seed=41)
-    g = rng(42)
-    tok = torch.from_numpy(g.integers(0, AUDIO_VOCAB, (B, N_CB))).to(dev)
-    pt = torch.full((B, 1), att - 1, dtype=torch.long, device=dev)
-    noise = torch.from_numpy(g.exponential(1.0, (N_CB, n, AUDIO_VOCAB)).astype(np.float32)).to(dev)
-    print("[frame] sampled, kv 750", flush=True)
+    assert gm._next_rows is not None and gm._c0proj is not None
+    assert (gm._next_qkv is not None) == ("qkv" in tables)
+    gen = torch.Generator(device=gm.dev)
+    gen.manual_seed(seed)
+    for gb in gm.backbone.blocks:  # (the oracle is not run here)
+        for gc in (gb.kc, gb.vc):
+            gc[:, :, : att - 1] = torch.randn(gc[:, :, : att - 1].shape, generator=gen,
+                                              device=gm.dev).half()
+    g = rng(seed + 1)
+    tok = torch.from_numpy(g.integers(0, AUDIO_VOCAB, (B, N_CB))).to(gm.dev)
+    pt = torch.full((B, 1), att - 1, dtype=torch.long, device=gm.dev)
+    noise = torch.from_numpy(g.exponential(1.0, (N_CB, n, AUDIO_VOCAB)).astype(np.float32)).to(gm.dev)
+    print(f"[frame] sampled, kv {att}", flush=True)
     lg_s = []
     samples = gm._step(tok, pt, None, 1.5, 50, 1.0, noise=noise, logits_out=lg_s).clone()
     torch.cuda.synchronize()
     lg_s = [N(x).astype(np.float64) for x in lg_s]
     slot = [(b.kc[:, :, att - 1].clone(), b.vc[:, :, att - 1].clone()) for b in gm.backbone.blocks]
-    print("[frame] teacher-forced with the sampled tokens, kv 750", flush=True)
+    print(f"[frame] teacher-forced with the sampled tokens, kv {att}", flush=True)
     lg_f = []
     gm._step(tok, pt, None, 1.5, 50, 1.0, forced=samples, logits_out=lg_f)
     torch.cuda.synchronize()
@@ -210,9 +213,34 @@ def test_c3_sampled_frame_matches_forced(dev, c3):
         assert torch.equal(b.kc[:, :, att - 1], k) and torch.equal(b.vc[:, :, att - 1], v)
 
 
-def test_reference_decoder_frame_kv750(dev):
+def test_c3_sampled_frame_matches_forced(dev, c3):
+    """The sampled frame at full size runs the decoder passes' inputs and layer 0 from the
+    samplers, the fused codebook-0 + projection GEMV and the backbone's final norm in that
+    GEMV's prologue. The teacher-forced frame with the tokens it sampled runs the projection
+    and head launches instead. Same function up to the fp32 summation order: KL < 1e-4 on all
+    8 heads, and the same backbone cache slot bit for bit."""
+    _, gm = c3
+    _sampled_vs_forced(gm, 750, 41, tables=("rows", "qkv"))
+
+
+@pytest.fixture(scope="module")
+def cref(dev):
+    return _pair(dev, BB, DEC_REF, seed=22)
+
+
+def test_reference_decoder_sampled_frame_matches_forced(dev, cref):
+    """The sampled path of the reference's own decoder (head_dim 384: no layer-0 q|k|v table,
+    so its passes 1..6 take their input rows from the samplers and start at layer 0's q|k|v;
+    the first pass from the fused codebook-0 + projection GEMV) against its teacher-forced
+    frame on the sampled tokens: KL < 1e-4 on all 8 heads, the backbone cache slot bit for
+    bit."""
+    _, gm = cref
+    _sampled_vs_forced(gm, 750, 43, tables=("rows",))
+
+
+def test_reference_decoder_frame_kv750(dev, cref):
     """The frame with the reference's depth decoder: 3 layers, 3072 wide, 8q/4kv, head_dim 384."""
-    om, gm = _pair(dev, BB, DEC_REF, seed=22)
+    om, gm = cref
     _frame(om, gm, 750, seed=33)
 
 

@@ -163,10 +163,11 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     rows, qkv, c0p = gm._next_rows, gm._next_qkv, gm._c0proj
     assert c0p is not None
     runs = {}
-    for name, r, q, tail in (("proj", None, None, True), ("rows", rows, None, True),
-                             ("qkv", rows, qkv, True), ("qkv_perop", rows, qkv, False)):
+    for name, r, q, cp, tail in (("proj", None, None, None, True), ("rows", rows, None, None, True),
+                                 ("rows_c0proj", rows, None, c0p, True),
+                                 ("qkv", rows, qkv, c0p, True), ("qkv_perop", rows, qkv, c0p, False)):
         gm._next_rows, gm._next_qkv = r, q
-        gm._c0proj = c0p if q is not None else None
+        gm._c0proj = cp
         gm.decoder.use_tail = tail
         lg = []
         out = gm._step(tok, torch.full((B, 1), 3, dtype=torch.long, device=dev), None, 1.5, 50,
@@ -178,7 +179,7 @@ def test_next_rows_table_equals_projection(dev, n_takes):
     assert torch.equal(runs["rows"][0], runs["proj"][0])
     for a, b in zip(runs["rows"][1], runs["proj"][1]):
         assert torch.equal(a, b)
-    for name in ("qkv", "qkv_perop"):
+    for name in ("rows_c0proj", "qkv", "qkv_perop"):
         assert torch.equal(runs[name][0], runs["proj"][0]), name
         for i, (a, b) in enumerate(zip(runs[name][1], runs["proj"][1])):
             kl = kl_rows(N(b).astype(np.float64), N(a).astype(np.float64))
@@ -303,3 +304,31 @@ def test_generate_graph_equals_eager(dev):
     c = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=2)
     for x, y, z in zip(a, b, c):
         assert np.array_equal(N(x), N(y)) and np.array_equal(N(x), N(z))
+
+
+@pytest.mark.parametrize("stack", ["backbone", "decoder"])
+def test_generate_raises_on_tail_timeout(dev, stack):
+    """The song loop reads the layer tails' error words with the EOS frames: with every wait of
+    one stack's tail launches giving up at its first look (forced from the host, so every kernel
+    still exits normally), generate() raises RuntimeError instead of returning tokens; the next
+    song on the same model runs and matches its eager loop."""
+    import torch
+    from estudiocanciones_amd.engine import HeartMuLaLite
+    from estudiocanciones_amd.quant import synthetic_weights
+    cfg = dict(layers=2, heads=8, kv_heads=2, max_seq=2048, dim=1024, ffn=8192)
+    gm = HeartMuLaLite(synthetic_weights(cfg, cfg, device=dev, seed=31, text_vocab=64),
+                       device=dev, backbone=cfg, decoder=cfg)
+    text = rng(9).integers(0, 64, 10)
+    st = getattr(gm, stack)
+    st.tail_no_wait = True
+    with pytest.raises(RuntimeError, match="timed out"):
+        gm.generate(text, 3, max_ms=80 * 3, seed=2, n=4)
+    assert gm.backbone.tail is None and gm.decoder.tail is None  # released
+    st.tail_no_wait = False
+    a = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=4)
+    assert not gm.graphs
+    gm.alloc(4, 16)
+    assert gm.backbone.tail is not None and gm.decoder.tail is not None, "tails not in use"
+    b = gm.generate(text, 3, max_ms=80 * 30, seed=5, n=4, use_graphs=False)
+    for x, y in zip(a, b):
+        assert np.array_equal(N(x), N(y))

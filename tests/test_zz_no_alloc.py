@@ -1,7 +1,8 @@
 """ecd_decode_attn_noalloc (split partials in the library's static device workspace) against
 the allocating pair it replaces, ecd_decode_attn + ecd_attn_combine with caller buffers: the
 outputs are bit-identical on two calls in a row, the second smaller than the first (the
-workspace keeps the first call's contents)."""
+workspace keeps the first call's contents), and under hipGraph capture after a first eager call
+on the device."""
 import math
 
 import numpy as np
@@ -62,3 +63,42 @@ def test_noalloc_attention_refuses_oversized(dev):
     pos = torch.zeros(R, dtype=torch.int64, device=dev)
     with pytest.raises(MemoryError):
         decode_attn_noalloc(q, kc, kc, pos, 1, Hq, Hk, L, 0.1, nsplit=32)
+
+
+def test_noalloc_attention_under_graph_capture(dev):
+    """After one eager call on the device, the call is captured into a hipGraph (nothing
+    allocated in the capture); every replay, with other eager work and syncs in between and new
+    inputs copied into the captured buffers, equals the allocating pair bit for bit."""
+    import torch
+    from estudiocanciones_amd.kernels import decode_attn_noalloc
+    R, S, Hq, Hk, HD, L, ns = 8, 1, 24, 8, 128, 1500, 16
+    B = R // S
+    T = lambda a: torch.from_numpy(a).to(dev)
+    q = T(randn16(90, R, Hq * HD))
+    kc = T(randn16(91, B, Hk, L, HD))
+    vc = T(randn16(92, B, Hk, L, HD))
+    pos = T(rng(93).integers(0, L, R).astype(np.int64))
+    out = torch.empty_like(q)
+    sc = 1 / math.sqrt(HD)
+    decode_attn_noalloc(q, kc, vc, pos, S, Hq, Hk, L, sc, nsplit=ns, out=out)  # eager first call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        decode_attn_noalloc(q, kc, vc, pos, S, Hq, Hk, L, sc, nsplit=ns, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        decode_attn_noalloc(q, kc, vc, pos, S, Hq, Hk, L, sc, nsplit=ns, out=out)
+    for k in range(4):
+        print(f"[noalloc-graph] replay {k}", flush=True)
+        q.copy_(T(randn16(100 + k, R, Hq * HD)))
+        pos.copy_(T(rng(110 + k).integers(0, L, R).astype(np.int64)))
+        # eager work on the same workspace between replays (a smaller call)
+        decode_attn_noalloc(q[:3], kc[:3], vc[:3], pos[:3], S, Hq, Hk, L, sc, nsplit=7)
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        want = _allocating(q, kc, vc, pos, S, Hq, Hk, L, HD, ns)
+        assert torch.equal(out, want), f"replay {k}"
