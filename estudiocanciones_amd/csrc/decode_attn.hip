@@ -83,7 +83,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(
 // o[rh, d] = sum_s w_s pa[rh, s, d] / sum_s w_s pl[rh, s],  w_s = exp(pm[rh, s] - max_s pm)
 // with w_s = 0 for empty splits (app/kernels.py:156-167).  Every partial load of the block is
 // issued before the weights are known, so the kernel costs one memory round trip.
-constexpr int CMB_MAXS = 32;
+constexpr int CMB_MAXS = 64;
 
 // One block per (row, head), one thread per d (blockDim = HD rounded up to 64).
 __global__ __launch_bounds__(512) void attn_combine_kernel(const float* __restrict__ pm,

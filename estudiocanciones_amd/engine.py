@@ -57,11 +57,13 @@ ATT_WAVES = 512       # waves the standalone attention grid aims at (two per CU 
 def attention_splits(R, Hk, L):
     """Split count of the engine's standalone decode attention over a cache of L slots: one
     split for short caches, else enough splits that R x Hk x splits waves cover the CUs about
-    twice, at least 16 (fewer splits leave each wave a long serial walk) and at most
-    ATT_SPLITS_MAX."""
+    twice, but no split shorter than 64 slots (four 16-slot tiles: one wave's loads in flight),
+    at least 16 (fewer splits leave each wave a long serial walk) and at most ATT_SPLITS_MAX
+    (the combine's register path)."""
     if L <= ATT_SHORT:
         return 1
-    return max(16, min(ATT_SPLITS_MAX, -(-ATT_WAVES // max(1, R * Hk))))
+    want = min(-(-ATT_WAVES // max(1, R * Hk)), -(-L // 64))
+    return max(16, min(ATT_SPLITS_MAX, want))
 
 
 BACKBONE = dict(layers=28, heads=24, kv_heads=8, max_seq=8192, dim=DIM)

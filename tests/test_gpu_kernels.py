@@ -183,6 +183,11 @@ ATTN_CASES = [
     (16, 2, 8, 2, 128, 8, 1),
     (4, 1, 8, 2, 128, 300, 7),
     (3, 1, 6, 1, 64, 40, 1),
+    # the engine's split counts for few rows (one row: 64 splits; 40 and 100 exercise the
+    # combine's register path and its loop path)
+    (1, 1, 24, 8, 128, 4096, 64),
+    (2, 1, 24, 8, 128, 2048, 40),
+    (1, 1, 24, 8, 128, 3000, 100),
 ]
 
 
