@@ -139,6 +139,128 @@ __global__ __launch_bounds__(512) void attn_combine_kernel(const float* __restri
   }
 }
 
+// Short caches (the depth decoder's, at most SHORT_L slots) with one split: one wave per (kv
+// head, row) on the VALU, no tiles.  Lane l owns dims [DPL l, DPL l + DPL) of every head
+// (DPL = HD / 64).  All LT >= L slots of the cache (slot indices clamped to L - 1), q and the
+// position are loaded at once (one memory round trip); scores q . k are summed in fp32 over
+// each lane's dims and then across the wave (DPP scans, no branches, so the G x LT sums
+// interleave), scaled, and the softmax is the single-block case of app/kernels.py:111-153:
+// m = max of the attended scores, p = exp(s - m), l = sum of the unrounded p, acc = sum of
+// fp16(p) v in fp32, o = fp16(acc / l).  Only the summation order differs from the tiled kernel.
+constexpr int SHORT_L = 16;
+
+template <int HD, int G, int LT>
+__global__ __launch_bounds__(64) void short_attn_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+    const int64_t* __restrict__ pos, f16* __restrict__ o, int S, int Hq, int Hk, int L,
+    float scale) {
+  static_assert(HD % 128 == 0 && HD <= 512, "an even number of dims per lane");
+  constexpr int DPL = HD / 64;  // dims per lane
+  constexpr int NW = DPL / 2;   // 32-bit words per lane of one row
+  const int lane = threadIdx.x;
+  const int kh = blockIdx.x, r = blockIdx.y;
+  const long cbase = ((long)(r / S) * Hk + kh) * (long)L * HD + DPL * lane;
+  uint32_t kw[LT][NW], vw[LT][NW], qw[G][NW];
+#pragma unroll
+  for (int t = 0; t < LT; ++t) {
+    const long off = cbase + (long)min(t, L - 1) * HD;
+    const uint32_t* kp = (const uint32_t*)(kc + off);
+    const uint32_t* vp = (const uint32_t*)(vc + off);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      kw[t][w] = kp[w];
+      vw[t][w] = vp[w];
+    }
+  }
+  const long hb = (long)r * Hq + kh * G;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint32_t* qp = (const uint32_t*)(q + (hb + g) * HD + DPL * lane);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) qw[g][w] = qp[w];
+  }
+  const long praw = pos[r];
+  const int n = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));  // slots [0, n)
+  float sc[G][LT];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const f16x2 qa = __builtin_bit_cast(f16x2, qw[g][w]);
+        const f16x2 ka = __builtin_bit_cast(f16x2, kw[t][w]);
+        a += (float)qa.x * (float)ka.x;
+        a += (float)qa.y * (float)ka.y;
+      }
+      sc[g][t] = a;
+    }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) sc[g][t] = wave_sum_dpp(sc[g][t]);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) sc[g][t] = t < n ? sc[g][t] * scale : -INFINITY;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < LT; ++t) m = fmaxf(m, sc[g][t]);
+    float l = 0.f;
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < LT; ++t) {
+      const float p = t < n ? __expf(sc[g][t] - m) : 0.f;
+      l += p;
+      const float ph = (float)(f16)p;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        // slots past n contribute nothing (their bits may be anything, even NaN)
+        const f16x2 va = __builtin_bit_cast(f16x2, t < n ? vw[t][w] : 0u);
+        acc[2 * w] += ph * (float)va.x;
+        acc[2 * w + 1] += ph * (float)va.y;
+      }
+    }
+    uint32_t* op = (uint32_t*)(o + (hb + g) * HD + DPL * lane);
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      op[w] = __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
+  }
+}
+
+template <int HD, int LT>
+static int launch_short_l(int G, dim3 grid, hipStream_t st, const f16* q, const f16* kc,
+                          const f16* vc, const int64_t* pos, f16* o, int S, int Hq, int Hk,
+                          int L, float scale) {
+#define ECD_SHORT_G(G_)                                                                         \
+  case G_:                                                                                      \
+    hipLaunchKernelGGL((short_attn_kernel<HD, G_, LT>), grid, dim3(64), 0, st, q, kc, vc, pos, o, \
+                       S, Hq, Hk, L, scale);                                                    \
+    return ECD_OK;
+  switch (G) {
+    ECD_SHORT_G(1)
+    ECD_SHORT_G(2)
+    ECD_SHORT_G(3)
+    ECD_SHORT_G(4)
+    default:
+      return ECD_ENOTSUP;
+  }
+#undef ECD_SHORT_G
+}
+
+template <int HD>
+static int launch_short(int G, dim3 grid, hipStream_t st, const f16* q, const f16* kc,
+                        const f16* vc, const int64_t* pos, f16* o, int S, int Hq, int Hk, int L,
+                        float scale) {
+  if (L <= 8) return launch_short_l<HD, 8>(G, grid, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale);
+  return launch_short_l<HD, SHORT_L>(G, grid, st, q, kc, vc, pos, o, S, Hq, Hk, L, scale);
+}
+
 template <int HD>
 static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* kc,
                      const f16* vc, const int64_t* pos, f16* o, float* pm, float* pl, float* pa,
@@ -217,6 +339,15 @@ int ecd_decode_attn(const void* q, const void* kc, const void* vc, const int64_t
   const f16 *qh = (const f16*)q, *kh = (const f16*)kc, *vh = (const f16*)vc;
   f16* oh = (f16*)o;
   int rc;
+  // one split over a short cache: the VALU kernel (one memory round trip, no tiles)
+  if (nsplit == 1 && L <= SHORT_L && G <= 4 && (HD == 128 || HD == 256 || HD == 384)) {
+    const dim3 sg(Hk, R);
+    rc = HD == 128   ? launch_short<128>(G, sg, st, qh, kh, vh, pos, oh, S, Hq, Hk, L, scale)
+         : HD == 256 ? launch_short<256>(G, sg, st, qh, kh, vh, pos, oh, S, Hq, Hk, L, scale)
+                     : launch_short<384>(G, sg, st, qh, kh, vh, pos, oh, S, Hq, Hk, L, scale);
+    if (rc != ECD_OK) return rc;
+    return ecd_launch_status();
+  }
   switch (HD) {
     case 64:
       rc = launch_hd<64>(G, grid, st, qh, kh, vh, pos, oh, pm, pl, pa, S, Hq, Hk, L, scale, nsplit);

@@ -188,6 +188,10 @@ ATTN_CASES = [
     (1, 1, 24, 8, 128, 4096, 64),
     (2, 1, 24, 8, 128, 2048, 40),
     (1, 1, 24, 8, 128, 3000, 100),
+    # one split over a short cache (<= 16 slots): the VALU kernel
+    (8, 1, 8, 4, 384, 8, 1),
+    (8, 1, 12, 4, 256, 16, 1),
+    (8, 1, 8, 2, 128, 5, 1),
 ]
 
 
