@@ -121,9 +121,10 @@ def time_graph(calls, torch, reps=20):
 
 def is_backbone_tail(name):
     """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6: the
-    frame's 28 tail launches), not its head launch (last template argument true)."""
+    frame's 28 tail launches), not its head launch (the HEAD template argument true)."""
     import re
-    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false, \d+>", name)
+    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false, \d+(, (true|false))?>",
+                          name)
                 or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0ELi\d+E", name))
 
 

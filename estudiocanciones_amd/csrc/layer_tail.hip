@@ -66,6 +66,8 @@ constexpr int MR = 16;               // rows a launch takes (M <= MR; x tiles of
 // LDS bytes per 64-column chunk of an x tile of R rows
 __host__ __device__ constexpr int chb(int R) { return 128 * R; }
 constexpr int ATT_SHORT = 128;       // caches of at most this many slots: one split per pair
+constexpr int VSHORT = 8;            // caches of at most this many slots: the VALU attention
+constexpr int VNEW = 2;              // ... written by at most this many rows per cache (S)
 constexpr int ATT_KB_MAX = 16;       // workgroups per (row, kv head) pair, long caches
 
 struct Args {
@@ -672,6 +674,178 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   bar();  // P(ATT)
 }
 
+// Caches of at most VSHORT slots (the depth decoders'): the next layer's attention on the VALU,
+// one wave per (row, kv head) pair, as the short-cache decode kernel computes it (no tiles, no
+// MFMA): lane l owns dims [DPL l, DPL l + DPL) of every head (DPL = HD / 64, NW = DPL / 2
+// words of two fp16).  Every cached slot below p0, the first slot this launch writes, is final
+// before the launch: for head_dim 128 they are read before the third gate (16 registers); for
+// wider heads, whose words would not fit beside the q|k|v weights, together with the first q
+// polls.  q and the slots from p0 on come from the hand-off words.
+template <int HD>
+struct VPre {
+  static constexpr int NW = HD / 128;
+  static constexpr bool EARLY = NW == 1;  // cached words loaded before the third gate
+  uint32_t k[VSHORT][NW], v[VSHORT][NW];
+  long cbase;  // this lane's first word of the pair's cache [L, HD] (K and V alike)
+  int last;    // the last cached slot below p0 (loads of later slots read it instead)
+  int r, kh;   // row and kv head of the pair
+  int p0;      // the cache's first slot written in this launch (L: none)
+  int n;       // row r attends slots [0, n)
+  bool on;     // this wave runs a pair
+};
+
+template <int HD>
+__device__ __forceinline__ void vatt_load_cached(const Args& a, VPre<HD>& pf) {
+#pragma unroll
+  for (int t = 0; t < VSHORT; ++t) {
+    const long off = pf.cbase + (long)min(t, pf.last) * HD;
+#pragma unroll
+    for (int w = 0; w < VPre<HD>::NW; ++w) {
+      pf.k[t][w] = ((const uint32_t*)(a.kc + off))[w];
+      pf.v[t][w] = ((const uint32_t*)(a.vc + off))[w];
+    }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void vatt_prefetch(const Args& a, int NB, int b, int wv, int lane,
+                                              VPre<HD>& pf) {
+  const int Hk = a.Hk, L = a.L;
+  const int p = b + NB * wv;
+  pf.on = p < a.M * Hk;
+  pf.n = 0;
+  pf.p0 = L;
+  if (!pf.on) return;
+  pf.r = p / Hk;
+  pf.kh = p - pf.r * Hk;
+  const int c = pf.r / a.S;  // the row's cache
+  const long praw = a.pos[c * a.S];
+  pf.p0 = (praw >= 0 && praw < L) ? (int)praw : L;
+  const long pr = a.pos[pf.r];
+  pf.n = (int)(pr + 1 < 0 ? 0 : (pr + 1 > L ? L : pr + 1));
+  // slots past p0 are replaced by hand-off words: their loads read the last cached slot
+  pf.last = max(min(pf.p0, L) - 1, 0);
+  pf.cbase = ((long)c * Hk + pf.kh) * (long)L * HD + (HD / 64) * lane;
+  if constexpr (VPre<HD>::EARLY) vatt_load_cached<HD>(a, pf);
+}
+
+// The pair's attention: q and the new slots polled from the hand-off words of epoch `ep`
+// (bounded by spin_max), scores summed in fp32 over each lane's dims and across the wave, then
+// the single-block softmax of app/kernels.py:111-153 (m = max, p = exp(s - m), l = sum of the
+// unrounded p, acc = sum of fp16(p) v in fp32, o = fp16(acc / l)) into o_next.
+template <int HD, int G>
+__device__ __forceinline__ void vattention_phase(const Args& a, int lane, VPre<HD>& pf,
+                                                 uint32_t ep) {
+  constexpr int NW = VPre<HD>::NW;
+  constexpr int DPL = HD / 64;
+  bar();  // X(ATT)
+  if (!pf.on) {
+    bar();  // P(ATT)
+    return;
+  }
+  const int Hq = a.Hq, Hk = a.Hk;
+  const long NQ = (long)(Hq + 2 * Hk) * HD;
+  const uint64_t* hw = (const uint64_t*)(a.ws + ws_hand_offset(a, gridDim.x));
+  const long c0 = (long)(pf.r / a.S) * a.S;  // the cache's first row
+  if constexpr (!VPre<HD>::EARLY) vatt_load_cached<HD>(a, pf);  // in flight with the first polls
+  uint32_t qw[G][NW], nk[VNEW][NW] = {}, nv[VNEW][NW] = {};
+  bool ok = true;
+  for (int it = 0;; ++it) {
+    bool ready = true;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const uint64_t x =
+            get_tagged(hw + ((pf.r * NQ + (long)(pf.kh * G + g) * HD) >> 1) + NW * lane + w);
+        qw[g][w] = (uint32_t)x;
+        ready = ready && tag_is(x, ep);
+      }
+#pragma unroll
+    for (int i = 0; i < VNEW; ++i)
+      if (pf.p0 + i < pf.n) {  // slot p0 + i from row c0 + i
+        const long j = c0 + i;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const uint64_t xk = get_tagged(hw + ((j * NQ + (long)(Hq + pf.kh) * HD) >> 1) + NW * lane + w);
+          const uint64_t xv =
+              get_tagged(hw + ((j * NQ + (long)(Hq + Hk + pf.kh) * HD) >> 1) + NW * lane + w);
+          nk[i][w] = (uint32_t)xk;
+          nv[i][w] = (uint32_t)xv;
+          ready = ready && tag_is(xk, ep) && tag_is(xv, ep);
+        }
+      }
+    if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+    if (it >= a.spin_max) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (!ok && lane == 0) store_agent(a.err, 1u);
+  // the new slots in place of the cached words read for them
+#pragma unroll
+  for (int t = 0; t < VSHORT; ++t)
+#pragma unroll
+    for (int i = 0; i < VNEW; ++i)
+      if (t == pf.p0 + i)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          pf.k[t][w] = nk[i][w];
+          pf.v[t][w] = nv[i][w];
+        }
+  const int n = pf.n;
+  float sc[G][VSHORT];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < VSHORT; ++t) {
+      float d = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const f16x2 qa = __builtin_bit_cast(f16x2, qw[g][w]);
+        const f16x2 ka = __builtin_bit_cast(f16x2, pf.k[t][w]);
+        d += (float)qa.x * (float)ka.x;
+        d += (float)qa.y * (float)ka.y;
+      }
+      sc[g][t] = d;
+    }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < VSHORT; ++t) sc[g][t] = wave_sum_dpp(sc[g][t]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < VSHORT; ++t) {
+      sc[g][t] = t < n ? sc[g][t] * a.scale : -INFINITY;
+      m = fmaxf(m, sc[g][t]);
+    }
+    float l = 0.f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < VSHORT; ++t) {
+      const float p = t < n ? __expf(sc[g][t] - m) : 0.f;
+      l += p;
+      const float ph = (float)(f16)p;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        // slots past n contribute nothing (their words may hold anything, even NaN)
+        const f16x2 va = __builtin_bit_cast(f16x2, t < n ? pf.v[t][w] : 0u);
+        acc[2 * w] += ph * (float)va.x;
+        acc[2 * w + 1] += ph * (float)va.y;
+      }
+    }
+    uint32_t* op = (uint32_t*)(a.o_next + ((long)pf.r * Hq + pf.kh * G + g) * HD + DPL * lane);
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      op[w] = __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
+  }
+  bar();  // P(ATT)
+}
+
 // Log-sum-exp merge of n <= NMAX partials [i][g][m, l, acc[HD]] (stride `str` floats between
 // partials) for head g and the columns d = lane + 64 k: the weights exp(m_i - max m) (0 for an
 // empty part) and the sums in part order.  Every read is issued before the first use (one
@@ -825,7 +999,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
@@ -866,7 +1040,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     // ------------------------------------------------------------------ compute waves
     // attention splits: two K/V tiles in flight where the register budget allows it (G <= 3)
     constexpr int ARING = AG <= 3 ? 2 : 1;
-    AttPre<(AHD > 0 ? AHD : 32), ARING> pf;
+    // tiled (MFMA) splits, or the VALU path for caches of at most VSHORT slots (VS)
+    AttPre<(AHD > 0 && !VS ? AHD : 32), ARING> pf;
+    VPre<(AHD > 0 && VS ? AHD : 128)> vpf;
     const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
     u32x4 wq[2][CD];
     const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
@@ -961,7 +1137,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
           wait_vm0();
         }
         rms_partial<CD, R>(xs, c0D, lane, wv, ss);
-        if constexpr (AHD > 0) {
+        if constexpr (AHD > 0 && VS) {
+          if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
+        } else if constexpr (AHD > 0) {
           if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
         }
         wait_lgkm0();
@@ -970,7 +1148,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
         // they stream during the third gate, and the loader's hand-off stores after the q|k|v
         // phase do not queue behind them
-        if constexpr (AHD > 0) {
+        if constexpr (AHD > 0 && VS) {
+          if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
+        } else if constexpr (AHD > 0) {
           if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
         }
         // phase QKV (x = rms(xout, n1'))
@@ -992,7 +1172,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       wait_lgkm0();
       bar();  // P(QKV)
     }
-    if constexpr (AHD > 0) {
+    if constexpr (AHD > 0 && VS) {
+      if (att) vattention_phase<AHD, AG>(a, lane, vpf, s_epoch);
+    } else if constexpr (AHD > 0) {
       if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf, s_epoch);
     }
     return;
@@ -1198,8 +1380,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       if (!att) goto done;
       bar();  // X(ATT)
       bar();  // P(ATT)
-      ok = attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)) &&
-           ok;
+      if constexpr (!VS)
+        ok = attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)) &&
+             ok;
     }
   }
 done:
@@ -1218,24 +1401,24 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS>
 int launch(const Args& a, int nb, hipStream_t st) {
   const int xd = CD * CW * chb(R), xf = CF / KS2 * CW * chb(R);
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   // attention: the waves' partials, then the merge's exchange
-  const int ldsA = AHD > 0 ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
+  const int ldsA = AHD > 0 && !VS ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
   int lds = ldsD > ldsF ? ldsD : ldsF;
   if (lds < ldsA) lds = ldsA;
   // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
   static int attr = 0;
   if (lds > attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return (int)e;
     attr = lds;
   }
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -1249,7 +1432,10 @@ using namespace ecd;
 static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
   if (Hk <= 0 || Hq % Hk) return false;
   const int G = Hq / Hk, pairs = M * Hk;
-  if (!(HD == 128 && (G == 3 || G == 4))) return false;
+  // head_dim 128 with 3 or 4 query heads per kv head at any length; head_dim 384 with 2 (the
+  // reference's depth decoder) on caches of at most VSHORT slots (the VALU path)
+  if (!(HD == 128 && (G == 3 || G == 4)) && !(HD == 384 && G == 2 && L <= tail::VSHORT))
+    return false;
   if (L <= tail::ATT_SHORT) return pairs <= nb * tail::CW;
   // KB = nb / pairs workgroups per pair, each merging HD / KB columns
   const int kb = nb / pairs;
@@ -1286,15 +1472,21 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   const int ag = Hq / Hk;
   const int rt = M > 8 ? 16 : 8;  // rows of the x tile
   const bool ntl = (flags >> 1) & 1;
+  const bool vs = L <= tail::VSHORT;  // the VALU attention path
+  if (vs && S > tail::VNEW) return ECD_ENOTSUP;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_, R_)                                          \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_ &&      \
-      rt == R_)                                                                              \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true, R_>(a, nb, st)      \
-               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true, R_>(a, nb, st);
-  ECD_HEAD(6, 16, 4, 1, 128, 3, 8)
-  ECD_HEAD(2, 16, 4, 4, 128, 4, 8)
-  ECD_HEAD(2, 16, 4, 4, 128, 4, 16)
+#define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_, R_, VS_)                                      \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_ &&       \
+      rt == R_ && vs == VS_)                                                                  \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true, R_, VS_>(a, nb, st)  \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true, R_, VS_>(a, nb, st);
+  ECD_HEAD(6, 16, 4, 1, 128, 3, 8, false)
+  ECD_HEAD(6, 16, 4, 1, 128, 3, 8, true)
+  ECD_HEAD(6, 16, 4, 1, 384, 2, 8, true)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 8, false)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 8, true)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 16, false)
+  ECD_HEAD(2, 16, 4, 4, 128, 4, 16, true)
 #undef ECD_HEAD
   return ECD_ENOTSUP;
 }
@@ -1354,22 +1546,28 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   const int ag = o_next ? Hq / Hk : 0;
   const int rt = M > 8 ? 16 : 8;  // rows of the x tile
   const bool ntl = (flags >> 1) & 1;
+  const bool vs = o_next && L <= tail::VSHORT;  // the VALU attention path
+  if (vs && S > tail::VNEW) return ECD_ENOTSUP;
   hipStream_t st = (hipStream_t)stream;
-#define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_, R_)                                          \
-  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ &&     \
-      ag == AG_ && rt == R_)                                                                 \
-    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false, R_>(a, nb, st)     \
-               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false, R_>(a, nb, st);
-  // 3072 -> 2 x 8192 -> 3072: the backbone (with its attention: 24q / 8kv, head_dim 128) and
-  // the reference's depth decoder (head_dim 384: attention launched on its own), up to 8 rows
-  ECD_TAIL(6, 16, 4, 1, 128, 3, 8)
-  ECD_TAIL(6, 16, 4, 1, 0, 0, 8)
+#define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_, R_, VS_)                                      \
+  if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ &&      \
+      ag == AG_ && rt == R_ && vs == VS_)                                                     \
+    return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false, R_, VS_>(a, nb, st) \
+               : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false, R_, VS_>(a, nb, st);
+  // 3072 -> 2 x 8192 -> 3072, up to 8 rows: the backbone (with its attention: 24q / 8kv,
+  // head_dim 128) and the reference's depth decoder (8q / 4kv, head_dim 384, caches of 8 slots)
+  ECD_TAIL(6, 16, 4, 1, 128, 3, 8, false)
+  ECD_TAIL(6, 16, 4, 1, 128, 3, 8, true)
+  ECD_TAIL(6, 16, 4, 1, 384, 2, 8, true)
+  ECD_TAIL(6, 16, 4, 1, 0, 0, 8, false)
   // 1024 -> 2 x 8192 -> 1024: the 1024-wide depth decoder (8q / 2kv, head_dim 128), up to 16
   // rows (its first pass: two rows per cache)
-  ECD_TAIL(2, 16, 4, 4, 128, 4, 8)
-  ECD_TAIL(2, 16, 4, 4, 0, 0, 8)
-  ECD_TAIL(2, 16, 4, 4, 128, 4, 16)
-  ECD_TAIL(2, 16, 4, 4, 0, 0, 16)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 8, false)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 8, true)
+  ECD_TAIL(2, 16, 4, 4, 0, 0, 8, false)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 16, false)
+  ECD_TAIL(2, 16, 4, 4, 128, 4, 16, true)
+  ECD_TAIL(2, 16, 4, 4, 0, 0, 16, false)
 #undef ECD_TAIL
   return ECD_ENOTSUP;
 }

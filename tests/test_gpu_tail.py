@@ -87,6 +87,8 @@ DEC_REF2 = dict(layers=2, heads=8, kv_heads=4, max_seq=2048, dim=3072, ffn=8192)
     (BB3, 8, 4096, "last", True),      # long splits: the new slot in a split's ninth tile
     (DEC3, 8, 8, "spread", False),     # 1024-wide decoder, per-frame cache of 8 slots
     (DEC_REF2, 8, 8, "last", False),   # the reference's decoder: 3072 wide, head_dim 384
+    (DEC_REF2, 8, 8, "spread", False),
+    (BB3, 8, 8, "spread", False),      # backbone shape over an 8-slot cache (VALU attention)
 ])
 def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream):
     import torch
@@ -132,7 +134,8 @@ def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream):
 
 
 @pytest.mark.parametrize("cfg,L,stream", [(dict(BB3, layers=2), 512, True),
-                                          (dict(DEC3, layers=2), 8, False)])
+                                          (dict(DEC3, layers=2), 8, False),
+                                          (DEC_REF2, 8, False)])
 def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
     """The tail path (head launch + tails) against the per-op fused kernels on the same stack
     (same numerics up to the fp32 summation order), then five more launches from identical
@@ -187,7 +190,8 @@ def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
     assert not st.tail_error()
 
 
-@pytest.mark.parametrize("cfg,L", [(dict(BB3, layers=2), 512), (dict(DEC3, layers=2), 8)])
+@pytest.mark.parametrize("cfg,L", [(dict(BB3, layers=2), 512), (dict(DEC3, layers=2), 8),
+                                   (DEC_REF2, 8)])
 def test_tail_timeout_sets_err_and_reset_recovers(dev, cfg, L):
     """The error path, forced from the host: with every wait of the launches giving up at its
     first look (gates, hand-off and merge polls), the launches still end and the error word
