@@ -23,8 +23,8 @@ whole frames on the host cores.
 
 HBM traffic of the backbone tail (``roofline.traffic``) comes from two rocprofv3 counter runs
 of this script with a calibration copy appended (``--copy-calib-mib``), summarised by
-``--pmc-summary FETCH_CSV WRITE_CSV`` into ``profiles/layer_tail_backbone_traffic.json``,
-which the timed run reads back.  ``--trace-summary STATS_CSV`` turns a rocprofv3
+``--pmc-summary FETCH_CSV WRITE_CSV`` into ``profiles/frame_traffic_b8_kv750.json`` (every
+kernel class of the run, the backbone tail first), which the timed run reads back.  ``--trace-summary STATS_CSV`` turns a rocprofv3
 ``--kernel-trace --stats`` run of this script into the per-launch-class table of one frame.
 """
 from __future__ import annotations
@@ -38,7 +38,19 @@ import time
 
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "layer_tail_backbone_traffic.json")
+                            "frame_traffic_b8_kv750.json")
+# the counter runs whose csv files --pmc-summary reads (from the repository root, one MI355X)
+PMC_BENCH = ("python3 bench.py --steps 2 --warmup 1 --no-cpu --target-kv 0 --prompt 0 "
+             "--no-isolated --no-ref-decoder --codec-steps 0 --no-song --copy-calib-mib 256")
+PMC_COMMANDS = [
+    "cd /tmp && export TMPDIR=/tmp && cd <repo>",
+    "timeout -s KILL 600 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch "
+    "-o fetch -- " + PMC_BENCH,
+    "timeout -s KILL 600 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write "
+    "-o write -- " + PMC_BENCH,
+    "python3 bench.py --pmc-summary gpurun_out/pmc_fetch/fetch_counter_collection.csv "
+    "gpurun_out/pmc_write/write_counter_collection.csv --copy-calib-mib 256",
+]
 METRIC = "frames/s (3B backbone + 7 decoder passes) @ batch 8; decode-attn+GEMV HBM GB/s"
 
 
@@ -128,9 +140,19 @@ def is_backbone_tail(name):
                 or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0ELi\d+E", name))
 
 
+def kernel_class(name):
+    """Short class name of a rocprofv3 kernel name: template arguments kept, parameter list and
+    return type dropped (demangled names), or the mangled name as it stands."""
+    import re
+    return re.sub(r"\(.*", "", name).replace("void ", "").strip()
+
+
 def pmc_summary(fetch_csv, write_csv, calib_mib):
-    """HBM bytes per backbone layer-tail launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
-    each scaled by what the counter reads for the calibration copy of known size."""
+    """HBM traffic per launch from two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per
+    dispatch), each scaled by what the counter reads for the calibration copy of known size
+    (ecd_copy_bytes of calib_mib MiB, read once and written once): the backbone layer-tail
+    launch (the roofline's traffic), and every kernel class of the run with its dispatch count,
+    so each launch class of the frame has its own figure."""
     import csv
 
     def per_dispatch(path, counter):
@@ -139,12 +161,11 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
             for r in csv.DictReader(f):
                 if r["Counter_Name"] != counter:
                     continue
-                key = r["Dispatch_Id"]
-                e = rows.setdefault(key, [r["Kernel_Name"], 0.0])
+                e = rows.setdefault(r["Dispatch_Id"], [r["Kernel_Name"], 0.0])
                 e[1] += float(r["Counter_Value"])
         return list(rows.values())
 
-    out = {}
+    out, factors, by_class = {}, {}, {}
     for tag, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
         rows = per_dispatch(path, counter)
         tail = [v for n, v in rows if is_backbone_tail(n)]
@@ -154,13 +175,39 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
                              f"{counter}")
         kib_copy = copy[-1]
         factor = kib_copy / (calib_mib * 1024.0)
+        factors[tag] = factor
         kib = sum(tail) / len(tail)
         out[tag] = {"counter": counter, "tail_dispatches": len(tail),
                     "kib_per_tail_launch": round(kib, 1), "calib_copy_kib": round(kib_copy, 1),
                     "calib_expected_kib": calib_mib * 1024, "factor": round(factor, 4),
                     "bytes_per_tail_launch": int(kib * 1024 / factor)}
+        for n, v in rows:
+            if "copy_bytes_kernel" in n:
+                continue
+            c = by_class.setdefault(kernel_class(n), {"fetch": [], "write": []})
+            c[tag].append(v)
     out["traffic_bytes_per_launch"] = out["fetch"]["bytes_per_tail_launch"] + \
         out["write"]["bytes_per_tail_launch"]
+    classes = []
+    for name, c in by_class.items():
+        if not c["fetch"] or not c["write"]:
+            continue
+        f = sum(c["fetch"]) / len(c["fetch"]) * 1024 / factors["fetch"]
+        w = sum(c["write"]) / len(c["write"]) * 1024 / factors["write"]
+        classes.append({"kernel": name, "dispatches": len(c["fetch"]),
+                        "fetch_bytes_per_launch": int(f), "write_bytes_per_launch": int(w),
+                        "traffic_bytes_per_launch": int(f + w)})
+    classes.sort(key=lambda e: -e["traffic_bytes_per_launch"] * e["dispatches"])
+    out["classes"] = classes
+    out["workload"] = ("frame step: 28-layer 3B backbone + 7 depth-decoder passes (4 layers, 1024 "
+                       "wide), batch 8, KV 750 (bench.py's default frame), plus the run's set-up "
+                       "(weight synthesis and packing, the per-token tables) and its per-kernel "
+                       "timing graphs and drop-in comparison")
+    out["commands"] = PMC_COMMANDS
+    out["note"] = ("FETCH_SIZE and WRITE_SIZE are KiB per dispatch (L2 <-> memory, Infinity Cache "
+                   "hits included); each class averages every dispatch of that kernel in the run "
+                   "and divides by the counter's calibration factor (its reading for the appended "
+                   f"{calib_mib} MiB ecd_copy_bytes over {calib_mib} MiB).")
     return out
 
 
@@ -382,7 +429,7 @@ def roofline_entry(pt, traffic):
         "frac": round(ach / HBM_PEAK_GBPS, 4),
         "traffic": traffic,
         "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per backbone layer-tail dispatch, "
-                           "copy-calibrated (profiles/layer_tail_backbone_traffic.json)")
+                           "copy-calibrated (profiles/frame_traffic_b8_kv750.json)")
                           if traffic else None,
         "avg_launch_us": round(pt["bt_ms"] * 1e3, 3),
         "algorithmic_bytes_per_launch": int(pt["bt_bytes"]),
