@@ -44,13 +44,13 @@
 // Cross-workgroup visibility (CDNA3/4: one L2 per XCD, not coherent across XCDs).  Outputs
 // read by other workgroups in the same launch (x1, mm, xout) are written with agent-scope
 // relaxed atomic stores (global_store ... sc1: written through to memory); after its stores
-// are acknowledged (s_waitcnt vmcnt(0)) the loader arrives at the gate with an atomic add.
-// The gate is two-level: the last of the 32 workgroups of a group (blockIdx % 8) adds to the
-// gate's global count, and the last group writes the go flags, which each workgroup polls
-// with agent-scope loads.  No workgroup reads x1 / mm / xout before its gate has opened, and
+// are acknowledged (s_waitcnt vmcnt(0)) the loader arrives at the gate with an atomic add on
+// its group's counter (the 32 workgroups of blockIdx % 8, one XCD); the last of a group writes
+// the group's done flag once for every group (each copy alone in its line), and each workgroup
+// polls its group's eight copies with agent-scope loads.  No workgroup reads x1 / mm / xout before its gate has opened, and
 // those lines are not in any L2 from earlier in the launch, so plain loads after the gate
 // fetch them from memory.  The gate counters only ever grow, in step with the go value, so
-// one 4 KB sync region serves every launch (each launch reads the go value at start).
+// one 16 KB sync region serves every launch (each launch reads the go value at start).
 // All workgroups are resident at once (grid = CU count, one workgroup per CU by LDS use);
 // every wait on a gate is bounded, and a timeout sets *err and lets the kernel finish.
 #include "attn_core.h"
@@ -97,7 +97,7 @@ struct Args {
   // next layer's attention (ATT kernels): o_next [M, Hq * HD] from q and the caches
   f16* o_next;
   float scale;
-  uint32_t* sync;  // 8 KB gate region, zero before the first launch
+  uint32_t* sync;  // 16 KB gate region, zero before the first launch
   uint32_t* err;   // set to 1 when a gate wait times out
   float* ws;       // workspace, zero before the first launch on `sync`: split-W2 partial sums
                    // [D / 16][KS2][64][4] (KS2 > 1), the attention's per-workgroup partials
@@ -167,29 +167,35 @@ __device__ __forceinline__ long ws_hand_offset(const Args& a, int NB) {
   return ws_att_offset(a.D) + (long)NB * (a.Hq / a.Hk) * (2 + a.HD) * 2;
 }
 
-// Gate words: [0] arrivals of group leaders, [64 (1 + g)] arrivals of group g's workgroups,
-// [64 (1 + g) + 32] go flag of group g (the eight go flags always hold the same value).  The
-// counters are never reset: every use of a gate adds exactly `per` to each group count and 8 to
-// the leader count and moves the go value by one, so the last arrivers are recognised from the
-// go value the workgroup holds (all modulo 2^32; `per` divides 2^32).  Called by one lane after
-// this workgroup's output stores have been acknowledged.
+// Gate words (a 16 KB region): [64 (1 + g)] arrivals of group g's workgroups; flag word
+// [GATE_FLAGS + 32 (8 x + g)] the done flag of group g as read by group x, one word alone in
+// its 128-byte line, so that every line of the region has a single writer (the last arriver of
+// one group) and each waiter polls eight lines of its own, with no second counter level between
+// the last arrival and the flags.  The counters are never reset: every use of a gate adds
+// exactly `per` to each group count and moves every flag by one, so the last arriver of a group
+// is recognised from the go value the workgroup holds (all modulo 2^32; `per` divides 2^32).
+// Called by one lane after this workgroup's output stores have been acknowledged.
+constexpr int GATE_FLAGS = 1024;
+
 __device__ __forceinline__ void gate_arrive(uint32_t* sync, int grp, uint32_t per, uint32_t go) {
   if (add_agent(sync + 64 * (1 + grp)) == (go + 1u) * per - 1u) {
-    if (add_agent(sync) == (go + 1u) * 8u - 1u) {
 #pragma unroll
-      for (int g = 0; g < 8; ++g) store_agent(sync + 64 * (1 + g) + 32, go + 1u);
-    }
+    for (int x = 0; x < 8; ++x) store_agent(sync + GATE_FLAGS + 32 * (8 * x + grp), go + 1u);
   }
 }
 
+// The whole wave: lanes 0..7 poll group grp's view of the eight flags until each has reached
+// go + 1 (a flag may already be one further: a group that passed this gate can complete the
+// next one before a slow waiter looks).  Bounded by spin_max; the same result in every lane.
 __device__ __forceinline__ bool gate_wait(const uint32_t* sync, int grp, uint32_t go,
-                                          int spin_max) {
-  const uint32_t* f = sync + 64 * (1 + grp) + 32;
-  for (int it = 0; ld_sc1(f) == go; ++it) {
+                                          int spin_max, int lane) {
+  const uint32_t* f = sync + GATE_FLAGS + 32 * (8 * grp + (lane & 7));
+  for (int it = 0;; ++it) {
+    const bool done = lane >= 8 || (int32_t)(ld_sc1(f) - (go + 1u)) >= 0;
+    if (__builtin_amdgcn_ballot_w64(!done) == 0) return true;
     if (it >= spin_max) return false;
     __builtin_amdgcn_s_sleep(1);
   }
-  return true;
 }
 
 // LDS DMA as lds_dma16, with agent scope (sc1): the read bypasses the L2, whose miss queue the
@@ -1188,7 +1194,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const uint32_t per = (uint32_t)(NB >> 3);
   bool ok = true;
   uint32_t go = 0;
-  if (lane == 0) go = ld_sc1(a.sync + 64 * (1 + grp) + 32);
+  if (lane == 0) go = ld_sc1(a.sync + GATE_FLAGS + 32 * 8 * grp);  // (all flags equal here)
 
   // epilogue operands that do not depend on this launch's phases
   f16x4 so4 = {}, xr4 = {}, s2v = {};
@@ -1232,11 +1238,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       if (mrow) st_sc1_u64(a.x1 + (long)me * D + 16 * tO + cg, y + xr4);
     }
     wait_vm0();
-    if (lane == 0) {
-      gate_arrive(a.sync, grp, per, go);
-      ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-      ++go;
-    }
+    if (lane == 0) gate_arrive(a.sync, grp, per, go);
+    ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+    ++go;
 
     // phase W13 (the W2 epilogue's residual x1 is final now: read it before the weight stream of
     // the next phases is in flight)
@@ -1263,11 +1267,9 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
           st_sc1_u32(a.mm + (long)me * F + ((16 * (b * NT13 + t) + cg) >> 1), o[t]);
     }
     wait_vm0();
-    if (lane == 0) {
-      gate_arrive(a.sync, grp, per, go);
-      ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-      ++go;
-    }
+    if (lane == 0) gate_arrive(a.sync, grp, per, go);
+    ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+    ++go;
 
     // phase W2
     bar();  // X(W2)
@@ -1317,12 +1319,10 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       // xout stores acknowledged (the split W2's K-parts 1 .. KS2 - 1 stored only tagged words,
       // which need no acknowledgement)
       if (KS2 == 1 || ks2 == 0) wait_vm0();
-      if (lane == 0) {
-        gate_arrive(a.sync, grp, per, go);
-        ok = gate_wait(a.sync, grp, go, a.spin_max) && ok;
-        ++go;
-        s_epoch = go;
-      }
+      if (lane == 0) gate_arrive(a.sync, grp, per, go);
+      ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+      ++go;
+      if (lane == 0) s_epoch = go;
     } else {
       if (lane == 0) s_epoch = go + 1;
     }

@@ -273,7 +273,7 @@ class Stack:
         if share is not None:  # launches in turn on one stream: one gate region and workspace
             sync, err, ws = share["sync"], share["err"], share["ws"]
         else:
-            sync = torch.zeros(2048, device=dev, dtype=torch.int32)
+            sync = torch.zeros(4096, device=dev, dtype=torch.int32)
             err = torch.zeros(1, device=dev, dtype=torch.int32)
             ws = torch.zeros(-(-wsb // 4), device=dev, dtype=torch.float32)
         return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],

@@ -582,7 +582,7 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     rms -> q|k|v -> RoPE -> q, cache slot (:189-192) and, with ``o_next`` [M, Hq * HD], that
     layer's decode attention (:194-204) into o_next.  Writes x1 [M, D], mm [M, F] and the layer
     output xout [M, D] (which must not alias xin, o, x1 or mm).  ``nxt``: dict with n1, wq
-    (packed), sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 2048], zero before
+    (packed), sq, rope, pos, q, kc, vc, S, Hq, Hk, L, HD.  ``sync`` (int32 [>= 4096], zero before
     first use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of
     layer_tail_ws_bytes bytes, zero before first use and kept with its ``sync`` (partials are
     recognised by the sync region's gate count).  ``no_wait``: every wait gives up at once (tests
@@ -600,8 +600,8 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     for t in (o, xin, x1, mm):
         if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * 2:
             raise ValueError("layer_tail: xout must not alias o, xin, x1 or mm")
-    if sync.dtype != torch.int32 or sync.numel() < 2048 or sync.data_ptr() % 256:
-        raise ValueError("layer_tail: sync must be int32 [>= 2048], 256-byte aligned")
+    if sync.dtype != torch.int32 or sync.numel() < 4096 or sync.data_ptr() % 256:
+        raise ValueError("layer_tail: sync must be int32 [>= 4096], 256-byte aligned")
     if err.dtype != torch.int32 or err.numel() < 1:
         raise ValueError("layer_tail: err must be int32 [1]")
     if ws.dtype != torch.float32 or ws.data_ptr() % 16:
@@ -665,8 +665,8 @@ def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait
         raise ValueError("layer_head: rope table must be float32 [>= L, HD/2, 2]")
     if o_next.numel() != M * Hq * HD or not o_next.is_contiguous() or o_next.data_ptr() % 16:
         raise ValueError("layer_head: o_next must be contiguous [M, Hq * HD]")
-    if sync.dtype != torch.int32 or sync.numel() < 2048 or sync.data_ptr() % 256:
-        raise ValueError("layer_head: sync must be int32 [>= 2048], 256-byte aligned")
+    if sync.dtype != torch.int32 or sync.numel() < 4096 or sync.data_ptr() % 256:
+        raise ValueError("layer_head: sync must be int32 [>= 4096], 256-byte aligned")
     if err.dtype != torch.int32 or err.numel() < 1:
         raise ValueError("layer_head: err must be int32 [1]")
     if ws.dtype != torch.float32 or ws.data_ptr() % 16 or \

@@ -245,7 +245,7 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * Same numerics as the per-op entry points up to the fp32 summation order.  wo / w13 / w2 / wq
  * are ecd_pack_i8 copies (w13 interleaved, s13 interleaved the same way); o, xin, x1, mm,
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.
- * sync: an 8 KB, 256-byte aligned region, zero before the first call, kept for later calls (the
+ * sync: a 16 KB, 256-byte aligned region, zero before the first call, kept for later calls (the
  * kernel leaves it reusable); calls sharing a sync region must not overlap in time.  err: a
  * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results, sync
  * and ws then undefined: zero sync, ws and err before the next call).  ws: a 16-byte aligned
