@@ -198,16 +198,11 @@ __device__ __forceinline__ bool gate_wait(const uint32_t* sync, int grp, uint32_
   }
 }
 
-// LDS DMA as lds_dma16, with agent scope (sc1): the read bypasses the L2, whose miss queue the
-// weight stream keeps full, and sees the other workgroups' agent-scope stores.
-__device__ __forceinline__ void lds_dma16_sc1(const void* base, uint32_t off, void* dst) {
-  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
-  uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-               "global_load_lds_dwordx4 %1, %2 sc1\n\ts_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
-}
-
+// Activation copies into LDS are plain LDS DMA (L2-cacheable: the 32 workgroups of an XCD read
+// the same rows, so all but the first hit its L2).  Every XCD's L2 starts a launch without the
+// lines of this launch's activations, and none of x1 / mm / xout is read in a launch before
+// the gate after which its writers' agent-scope stores are acknowledged, so the first read of
+// a line fetches it from memory (the launch's inputs o and xin are final at its start).
 // Activation rows [M, K] (row stride ld halfs) -> LDS x tile of R rows: chunk c (columns 64c ..
 // 64c + 63) occupies chb(R) bytes as [grp 4][row R][16 halfs], grp = the 16-column group, i.e.
 // exactly the B fragments of the two MFMAs of the chunk.  Each compute wave copies its own
@@ -226,7 +221,7 @@ __device__ __forceinline__ void dma_rows(const f16* x, long ld, int M, int c0, u
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int grp = i * (4 / NI) + gl;
-      lds_dma16_sc1(x, (uint32_t)(((long)rs * ld + 64 * (c0 + u) + 16 * grp + 8 * h) * 2),
+      lds_dma16(x, (uint32_t)(((long)rs * ld + 64 * (c0 + u) + 16 * grp + 8 * h) * 2),
                     dst + u * chb(R) + i * 1024);
       if (((u * NI + i) & 15) == 15) wait_vm<32>();  // at most ~48 DMA instructions in flight
     }
@@ -237,7 +232,7 @@ __device__ __forceinline__ void dma_rows(const f16* x, long ld, int M, int c0, u
 template <int C>
 __device__ __forceinline__ void dma_nw(const f16* v, int c0, unsigned char* dst, int lane) {
   static_assert(C * 8 <= 64, "one DMA instruction per wave");
-  if (lane < C * 8) lds_dma16_sc1(v + 64 * c0, (uint32_t)(16 * lane), dst + 128 * c0);
+  if (lane < C * 8) lds_dma16(v + 64 * c0, (uint32_t)(16 * lane), dst + 128 * c0);
 }
 
 // B fragments of chunk c of an R-row tile for this lane (row lane & 15; zero for rows >= R)
