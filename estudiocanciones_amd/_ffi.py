@@ -38,8 +38,8 @@ SIGNATURES = {
                         _P, c_long, _P],
     "ecd_sample_topk_next": [_P, c_long, c_int, c_int, c_float, c_float, c_int, c_int, _P, _P, _P,
                              c_int, _P, c_long, _P, c_long, c_int, _P, c_long, c_int, _P, c_long,
-                             c_int, _P, _P, c_int, c_int, _P, c_long, c_int, c_int, _P, c_long,
-                             _P, c_long, _P],
+                             c_int, _P, _P, c_int, c_int, _P, c_long, c_int, c_int, c_int, _P,
+                             c_long, _P, c_long, _P],
     "ecd_frame_advance": [_P, c_long, _P, c_long, _P, c_long, _P, _P, c_int, c_int, c_int, c_int,
                           c_long, _P],
     "ecd_copy_bytes": [_P, _P, c_long, _P],

@@ -359,4 +359,71 @@ __device__ __forceinline__ void load_q(f16x8 (&qf)[HD / 32], const f16* __restri
   }
 }
 
+// Short-cache attention of one (row, kv head) pair on one wave, on the VALU (no tiles): lane l
+// owns dims [DPL l, DPL l + DPL) of every head (DPL = HD / 64, two per 32-bit word).  kw / vw
+// hold slots 0 .. LT - 1 of K and V (slots from n on are ignored whatever their bits, even
+// NaN), qw the G query heads.  Scores q . k are summed in fp32 over each lane's dims, then across
+// the wave (DPP scans, no branches, so the G x LT sums interleave), scaled, and the softmax is
+// the single-block case of app/kernels.py:111-153: m = max of the attended scores, p =
+// exp(s - m), l = sum of the unrounded p, acc = sum of fp16(p) v in fp32, o = fp16(acc / l).
+// Head g's o goes to dst + g * HD (dst: head 0 of the pair, plus DPL * lane).
+template <int HD, int G, int LT>
+__device__ __forceinline__ void short_attn_wave(const uint32_t (&kw)[LT][HD / 128],
+                                                const uint32_t (&vw)[LT][HD / 128],
+                                                const uint32_t (&qw)[G][HD / 128], int n,
+                                                float scale, f16* dst) {
+  static_assert(HD % 128 == 0 && HD <= 512, "an even number of dims per lane");
+  constexpr int DPL = HD / 64;
+  constexpr int NW = DPL / 2;
+  float sc[G][LT];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const f16x2 qa = __builtin_bit_cast(f16x2, qw[g][w]);
+        const f16x2 ka = __builtin_bit_cast(f16x2, kw[t][w]);
+        a += (float)qa.x * (float)ka.x;
+        a += (float)qa.y * (float)ka.y;
+      }
+      sc[g][t] = a;
+    }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) sc[g][t] = wave_sum_dpp(sc[g][t]);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < LT; ++t) sc[g][t] = t < n ? sc[g][t] * scale : -INFINITY;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < LT; ++t) m = fmaxf(m, sc[g][t]);
+    float l = 0.f;
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < LT; ++t) {
+      const float p = t < n ? __expf(sc[g][t] - m) : 0.f;
+      l += p;
+      const float ph = (float)(f16)p;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const f16x2 va = __builtin_bit_cast(f16x2, t < n ? vw[t][w] : 0u);
+        acc[2 * w] += ph * (float)va.x;
+        acc[2 * w + 1] += ph * (float)va.y;
+      }
+    }
+    uint32_t* op = (uint32_t*)(dst + g * HD);
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      op[w] = __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
+  }
+}
+
 }  // namespace ecd

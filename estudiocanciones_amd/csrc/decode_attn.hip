@@ -140,13 +140,10 @@ __global__ __launch_bounds__(512) void attn_combine_kernel(const float* __restri
 }
 
 // Short caches (the depth decoder's, at most SHORT_L slots) with one split: one wave per (kv
-// head, row) on the VALU, no tiles.  Lane l owns dims [DPL l, DPL l + DPL) of every head
-// (DPL = HD / 64).  All LT >= L slots of the cache (slot indices clamped to L - 1), q and the
-// position are loaded at once (one memory round trip); scores q . k are summed in fp32 over
-// each lane's dims and then across the wave (DPP scans, no branches, so the G x LT sums
-// interleave), scaled, and the softmax is the single-block case of app/kernels.py:111-153:
-// m = max of the attended scores, p = exp(s - m), l = sum of the unrounded p, acc = sum of
-// fp16(p) v in fp32, o = fp16(acc / l).  Only the summation order differs from the tiled kernel.
+// head, row) on the VALU, no tiles (short_attn_wave: lane l owns dims [DPL l, DPL l + DPL) of
+// every head, DPL = HD / 64).  All LT >= L slots of the cache (slot indices clamped to L - 1),
+// q and the position are loaded at once (one memory round trip).  Only the summation order
+// differs from the tiled kernel.
 constexpr int SHORT_L = 16;
 
 template <int HD, int G, int LT>
@@ -181,56 +178,7 @@ __global__ __launch_bounds__(64) void short_attn_kernel(
   }
   const long praw = pos[r];
   const int n = (int)(praw + 1 < 0 ? 0 : (praw + 1 > L ? L : praw + 1));  // slots [0, n)
-  float sc[G][LT];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int t = 0; t < LT; ++t) {
-      float a = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const f16x2 qa = __builtin_bit_cast(f16x2, qw[g][w]);
-        const f16x2 ka = __builtin_bit_cast(f16x2, kw[t][w]);
-        a += (float)qa.x * (float)ka.x;
-        a += (float)qa.y * (float)ka.y;
-      }
-      sc[g][t] = a;
-    }
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int t = 0; t < LT; ++t) sc[g][t] = wave_sum_dpp(sc[g][t]);
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int t = 0; t < LT; ++t) sc[g][t] = t < n ? sc[g][t] * scale : -INFINITY;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < LT; ++t) m = fmaxf(m, sc[g][t]);
-    float l = 0.f;
-    float acc[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-#pragma unroll
-    for (int t = 0; t < LT; ++t) {
-      const float p = t < n ? __expf(sc[g][t] - m) : 0.f;
-      l += p;
-      const float ph = (float)(f16)p;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        // slots past n contribute nothing (their bits may be anything, even NaN)
-        const f16x2 va = __builtin_bit_cast(f16x2, t < n ? vw[t][w] : 0u);
-        acc[2 * w] += ph * (float)va.x;
-        acc[2 * w + 1] += ph * (float)va.y;
-      }
-    }
-    uint32_t* op = (uint32_t*)(o + (hb + g) * HD + DPL * lane);
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-      op[w] = __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
-  }
+  short_attn_wave<HD, G, LT>(kw, vw, qw, n, scale, o + hb * HD + DPL * lane);
 }
 
 template <int HD, int LT>

@@ -1447,7 +1447,8 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   a.n1 = (const f16*)n1; a.wq = (const int8_t*)wq; a.sq = (const f16*)sq;
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
-  a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
+  // attention scale: the fp32 rounding of 1 / sqrt(HD) (the reference passes it as a float)
+  a.o_next = (f16*)o_next; a.scale = HD > 0 ? (float)(1.0 / sqrt((double)HD)) : 0.f;
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
   a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -1512,7 +1513,8 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   a.n1 = (const f16*)n1; a.wq = (const int8_t*)wq; a.sq = (const f16*)sq;
   a.rope = rope; a.pos = pos; a.q = (f16*)q; a.kc = (f16*)kc; a.vc = (f16*)vc;
   a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
-  a.o_next = (f16*)o_next; a.scale = HD > 0 ? 1.0f / sqrtf((float)HD) : 0.f;
+  // attention scale: the fp32 rounding of 1 / sqrt(HD) (the reference passes it as a float)
+  a.o_next = (f16*)o_next; a.scale = HD > 0 ? (float)(1.0 / sqrt((double)HD)) : 0.f;
   a.x1 = (f16*)x1; a.mm = (f16*)mm; a.xout = (f16*)xout;
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
   a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;

@@ -28,7 +28,7 @@
 // countered by (vocab index / 4, take, frame position, salt): graph replays at different
 // frame positions draw fresh numbers without any mutable RNG state.  Tests can inject the
 // draws instead (noise [N, V] fp32).
-#include "common.h"
+#include "attn_core.h"
 
 namespace ecd {
 
@@ -179,12 +179,18 @@ __device__ uint32_t select_full(const uint32_t (&key)[SMP_PER], const f16 (&lv)[
 //  * qkv != NULL: that pass's layer 0 up to its attention output: q | k | v of the token at
 //    slot p (precomputed per token, RoPE applied) -> the cache slot p of kc / vc, and the
 //    decode attention over slots 0 .. p (app/kernels.py:110-153: fp32 scores, exp, fp16 P,
-//    fp32 P V, o = acc / l) -> o rows, head_dim 128.  One wave per (row, kv head) pair; the
-//    pair's cached slots 0 .. p - 1 go to LDS at kernel start, while the sampler runs.
-constexpr int NXA_HD = 128;   // head_dim of the folded attention
+//    fp32 P V, o = acc / l) -> o rows.  One wave per (row, kv head) pair, its cached slots
+//    0 .. p - 1 loaded at kernel start, while the sampler runs: head_dim 128 into LDS (LDS DMA),
+//    head_dim 384 into the wave's registers (48 KB per pair would not fit beside the
+//    sampler's LDS), with the arithmetic of the standalone short-cache kernel.
+constexpr int NXA_HD = 128;   // head_dim of the LDS form
 constexpr int NXA_SLOTS = 16; // cache slots it reads at most (p < 16)
 constexpr int NXA_PAIRS = 4;  // (row, kv head) pairs per take at most
 constexpr int NXA_G = 4;      // query heads per kv head at most
+constexpr int NXV_HD = 384;   // head_dim of the register form
+constexpr int NXV_SLOTS = 8;  // cache slots it holds (p < 8)
+constexpr int NXV_PAIRS = 8;  // pairs per take at most (waves 1 .. 8)
+constexpr int NXV_G = 4;      // query heads per kv head at most
 struct NextPass {
   const f16* rows;
   long rows_ld;
@@ -198,7 +204,7 @@ struct NextPass {
   int L, p;
   f16* o;          // [B, Hq * 128]
   long o_ld;
-  int Hq, Hk;
+  int Hq, Hk, HD;
   float scale;
   const f16* ev;   // rows copied as they are, independent of the token: ev row r -> xe row r
   long ev_ld;      // (D wide; the depth decoder's first pass: the projected backbone state)
@@ -289,6 +295,58 @@ __device__ __forceinline__ void next_attention(const NextPass& nx, int tok, int 
   (void)aj;
 }
 
+// The register form's cached slots: lane l holds dims [HD / 64 l, HD / 64 (l + 1)) of slots
+// 0 .. NXV_SLOTS - 1 of K and V (the slots from p on are filled or masked later).
+template <int HD>
+struct NxvSlots {
+  uint32_t k[NXV_SLOTS][HD / 128], v[NXV_SLOTS][HD / 128];
+};
+
+// Pair (row, kv head) of the next pass's layer-0 attention in the register form, one wave, for
+// the sampled token tok: q of the pair's G heads and the new slot's k and v from the token's
+// precomputed row (zeros if no index won), k and v into cache slot p and into the slot
+// registers, then short_attn_wave over slots 0 .. p into o.
+template <int HD, int G>
+__device__ __forceinline__ void next_attention_reg(const NextPass& nx, int tok, int V, int row,
+                                                   int kh, long cache, int lane,
+                                                   NxvSlots<HD>& sl) {
+  constexpr int NW = HD / 128, DPL = HD / 64;
+  const int p = nx.p;
+  const bool valid = (uint32_t)tok < (uint32_t)V;
+  const f16* src = nx.qkv + (long)(valid ? tok : 0) * nx.qkv_ld + DPL * lane;
+  uint32_t qw[G][NW], kn[NW], vn[NW];
+  const uint32_t* ks = (const uint32_t*)(src + (long)(nx.Hq + kh) * HD);
+  const uint32_t* vs = (const uint32_t*)(src + (long)(nx.Hq + nx.Hk + kh) * HD);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      qw[g][w] = valid ? ((const uint32_t*)(src + (long)(kh * G + g) * HD))[w] : 0u;
+    kn[w] = valid ? ks[w] : 0u;
+    vn[w] = valid ? vs[w] : 0u;
+  }
+  uint32_t* kd = (uint32_t*)(nx.kc + cache + (long)p * HD + DPL * lane);
+  uint32_t* vd = (uint32_t*)(nx.vc + cache + (long)p * HD + DPL * lane);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    kd[w] = kn[w];
+    vd[w] = vn[w];
+  }
+#pragma unroll
+  for (int t = 0; t < NXV_SLOTS; ++t)
+    if (t == p)
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        sl.k[t][w] = kn[w];
+        sl.v[t][w] = vn[w];
+      }
+  short_attn_wave<HD, G, NXV_SLOTS>(sl.k, sl.v, qw, p + 1, nx.scale,
+                                    nx.o + (long)row * nx.o_ld + (long)kh * G * HD + DPL * lane);
+}
+
+// XHD: head_dim of the folded layer-0 attention (128: LDS form, 384: register form); the
+// sampler alone (no qkv) runs the 128 instance.
+template <int XHD>
 __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     const f16* __restrict__ logits, long ld, int N, int cfg_on, float cfg, float temp, int topk,
     int V, const float* __restrict__ noise, const int64_t* __restrict__ seed,
@@ -300,10 +358,12 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   __shared__ __align__(16) uint32_t wbin[SMP_WBINS_LDS];
   __shared__ int kept_i[SMP_MAXV];
   __shared__ float kept_x[SMP_MAXV];
-  __shared__ __align__(16) f16 a_k[NXA_PAIRS][NXA_SLOTS][NXA_HD];
-  __shared__ __align__(16) f16 a_v[NXA_PAIRS][NXA_SLOTS][NXA_HD];
-  __shared__ __align__(16) f16 a_q[NXA_PAIRS][NXA_G][NXA_HD];
-  __shared__ float a_pe[NXA_PAIRS][NXA_G][NXA_SLOTS];
+  static_assert(XHD == NXA_HD || XHD == NXV_HD, "folded attention: head_dim 128 or 384");
+  constexpr int AP = XHD == NXA_HD ? NXA_PAIRS : 1;  // the LDS form's arrays
+  __shared__ __align__(16) f16 a_k[AP][NXA_SLOTS][NXA_HD];
+  __shared__ __align__(16) f16 a_v[AP][NXA_SLOTS][NXA_HD];
+  __shared__ __align__(16) f16 a_q[AP][NXA_G][NXA_HD];
+  __shared__ float a_pe[AP][NXA_G][NXA_SLOTS];
   __shared__ int s_tok;
 
   const int n = blockIdx.x;
@@ -342,20 +402,41 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     p64 = (uint64_t)pos[0];
   }
   // the next pass's layer-0 attention: wave 1 + j runs pair j (row n + (j / Hk) N, kv head
-  // j % Hk); its cached slots 0 .. p - 1 (K and V) go to LDS now (LDS DMA, 4 slots per
-  // instruction, lanes past slot p - 1 idle)
+  // j % Hk); its cached slots 0 .. p - 1 (K and V) are loaded now: head_dim 128 into LDS (LDS
+  // DMA, 4 slots per instruction, lanes past slot p - 1 idle), 384 into registers
   const int npairs = nx.qkv ? (cfg_on ? 2 : 1) * nx.Hk : 0;
   const int aj = wv - 1;
   const int arow = n + (aj / max(nx.Hk, 1)) * N, akh = aj - (aj / max(nx.Hk, 1)) * nx.Hk;
-  const long acache = ((long)arow * nx.Hk + akh) * nx.L * NXA_HD;  // the pair's [L, 128] rows
-  if (aj >= 0 && aj < npairs) {
-    for (int u = 0; 4 * u < nx.p; ++u) {
-      const int t = 4 * u + (lane >> 4);
-      if (t < nx.p) {
-        const uint32_t off = (uint32_t)(((long)t * NXA_HD + 8 * (lane & 15)) * 2);
-        lds_dma16(nx.kc + acache, off, &a_k[aj][4 * u][0]);
-        lds_dma16(nx.vc + acache, off, &a_v[aj][4 * u][0]);
+  const long acache = ((long)arow * nx.Hk + akh) * nx.L * XHD;  // the pair's [L, XHD] rows
+  NxvSlots<XHD == NXV_HD ? NXV_HD : 128> sl;
+  if constexpr (XHD == NXA_HD) {
+    if (aj >= 0 && aj < npairs) {
+      for (int u = 0; 4 * u < nx.p; ++u) {
+        const int t = 4 * u + (lane >> 4);
+        if (t < nx.p) {
+          const uint32_t off = (uint32_t)(((long)t * NXA_HD + 8 * (lane & 15)) * 2);
+          lds_dma16(nx.kc + acache, off, &a_k[aj][4 * u][0]);
+          lds_dma16(nx.vc + acache, off, &a_v[aj][4 * u][0]);
+        }
       }
+    }
+  } else {
+    constexpr int NW = XHD / 128;
+#pragma unroll
+    for (int t = 0; t < NXV_SLOTS; ++t)
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sl.k[t][w] = sl.v[t][w] = 0u;
+    if (aj >= 0 && aj < npairs) {
+      const f16* kb = nx.kc + acache + (XHD / 64) * lane;
+      const f16* vb = nx.vc + acache + (XHD / 64) * lane;
+#pragma unroll
+      for (int t = 0; t < NXV_SLOTS; ++t)
+        if (t < nx.p)
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            sl.k[t][w] = ((const uint32_t*)(kb + (long)t * XHD))[w];
+            sl.v[t][w] = ((const uint32_t*)(vb + (long)t * XHD))[w];
+          }
     }
   }
 
@@ -465,8 +546,17 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     }
     if (aj < npairs) {  // a pair wave: the token, then the pair's attention
       __syncthreads();
-      next_attention(nx, s_tok, V, aj, arow, akh, acache, lane, a_k[aj], a_v[aj], a_q[aj],
-                     a_pe[aj]);
+      if constexpr (XHD == NXA_HD) {
+        next_attention(nx, s_tok, V, aj, arow, akh, acache, lane, a_k[aj], a_v[aj], a_q[aj],
+                       a_pe[aj]);
+      } else {
+        switch (nx.Hq / nx.Hk) {
+          case 1: next_attention_reg<XHD, 1>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
+          case 2: next_attention_reg<XHD, 2>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
+          case 3: next_attention_reg<XHD, 3>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
+          default: next_attention_reg<XHD, 4>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
+        }
+      }
     }
     return;
   }
@@ -590,9 +680,9 @@ extern "C" int ecd_sample_topk(const void* logits, long ld, int B, int N, float 
       (!noise && (!seed || !pos)))
     return ECD_EINVAL;
   const int cfg_on = (B == 2 * N) ? 1 : 0;
-  hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
-                     (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
-                     out, out_stride, NextPass{});
+  hipLaunchKernelGGL(sample_topk_kernel<NXA_HD>, dim3(N), dim3(SMP_THREADS), 0,
+                     (hipStream_t)stream, (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V,
+                     noise, seed, pos, salt, out, out_stride, NextPass{});
   return ecd_launch_status();
 }
 
@@ -602,8 +692,9 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
                                     int64_t* out, long out_stride, const void* rows, long rows_ld,
                                     int rows_n, void* x, long x_ld, int D, const void* qkv,
                                     long qkv_ld, int qkv_n, void* kc, void* vc, int L, int p,
-                                    void* o, long o_ld, int Hq, int Hk, const void* ev,
-                                    long ev_ld, void* xe, long xe_ld, void* stream) {
+                                    void* o, long o_ld, int Hq, int Hk, int HD,
+                                    const void* ev, long ev_ld, void* xe, long xe_ld,
+                                    void* stream) {
   const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
   if (!rows || !x || rows_n < V || D <= 0 || (D % 8) || rows_ld < D || (rows_ld % 8) ||
       x_ld < D || (x_ld % 8) || !al(rows) || !al(x))
@@ -614,11 +705,14 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
     return ECD_EINVAL;
   const int cfg_on = B == 2 * N ? 1 : 0;
   if (qkv) {
-    const int nq = (Hq + 2 * Hk) * NXA_HD;
-    if (!kc || !vc || !o || Hk <= 0 || Hq <= 0 || (Hq % Hk) || Hq / Hk > NXA_G ||
-        (1 + cfg_on) * Hk > NXA_PAIRS || p < 0 || p >= L || p >= NXA_SLOTS || qkv_n < V ||
-        qkv_ld < nq || (qkv_ld % 8) || o_ld < Hq * NXA_HD || (o_ld % 8) || !al(qkv) ||
-        !al(kc) || !al(vc) || !al(o))
+    const bool lds_form = HD == NXA_HD;
+    if (!lds_form && HD != NXV_HD) return ECD_EINVAL;
+    const int nq = (Hq + 2 * Hk) * HD;
+    if (!kc || !vc || !o || Hk <= 0 || Hq <= 0 || (Hq % Hk) ||
+        Hq / Hk > (lds_form ? NXA_G : NXV_G) ||
+        (1 + cfg_on) * Hk > (lds_form ? NXA_PAIRS : NXV_PAIRS) || p < 0 || p >= L ||
+        p >= (lds_form ? NXA_SLOTS : NXV_SLOTS) || qkv_n < V || qkv_ld < nq || (qkv_ld % 8) ||
+        o_ld < Hq * HD || (o_ld % 8) || !al(qkv) || !al(kc) || !al(vc) || !al(o))
       return ECD_EINVAL;
   }
   if (ev && (!xe || ev_ld < D || (ev_ld % 8) || xe_ld < D || (xe_ld % 8) || !al(ev) || !al(xe)))
@@ -628,11 +722,16 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
   nx.rows = (const f16*)rows; nx.rows_ld = rows_ld; nx.x = (f16*)x; nx.x_ld = x_ld; nx.D = D;
   if (qkv) {
     nx.qkv = (const f16*)qkv; nx.qkv_ld = qkv_ld; nx.kc = (f16*)kc; nx.vc = (f16*)vc;
-    nx.L = L; nx.p = p; nx.o = (f16*)o; nx.o_ld = o_ld; nx.Hq = Hq; nx.Hk = Hk;
-    nx.scale = 1.0f / sqrtf((float)NXA_HD);
+    nx.L = L; nx.p = p; nx.o = (f16*)o; nx.o_ld = o_ld; nx.Hq = Hq; nx.Hk = Hk; nx.HD = HD;
+    nx.scale = (float)(1.0 / sqrt((double)HD));  // the fp32 rounding of 1 / sqrt(HD)
   }
-  hipLaunchKernelGGL(sample_topk_kernel, dim3(N), dim3(SMP_THREADS), 0, (hipStream_t)stream,
-                     (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V, noise, seed, pos, salt,
-                     out, out_stride, nx);
+  if (qkv && HD == NXV_HD)
+    hipLaunchKernelGGL(sample_topk_kernel<NXV_HD>, dim3(N), dim3(SMP_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V,
+                       noise, seed, pos, salt, out, out_stride, nx);
+  else
+    hipLaunchKernelGGL(sample_topk_kernel<NXA_HD>, dim3(N), dim3(SMP_THREADS), 0,
+                       (hipStream_t)stream, (const f16*)logits, ld, N, cfg_on, cfg, temp, topk, V,
+                       noise, seed, pos, salt, out, out_stride, nx);
   return ecd_launch_status();
 }

@@ -736,13 +736,16 @@ class HeartMuLaLite:
         (codebook, token) and the weights.  qkv[i - 1][t] holds q heads | k heads | v heads of
         token t (the per-op kernel rms_qkv_rope writing whole rows, one launch per codebook,
         with the per-row numerics of a decode step), so the sampler can write the cache slot and
-        run that layer's attention itself; only for head_dim 128 and the pair counts the
-        sampler's folded attention takes."""
+        run that layer's attention itself; only for the head_dims (128, 384) and the pair
+        counts the sampler's folded attention takes."""
         self._next_qkv = self._onext = None
         d0 = self.decoder.blocks[0] if self.decoder.blocks else None
         B, V = self.B, AUDIO_VOCAB
-        if d0 is None or d0.qkv.qp is None or d0.hd != 128 or d0.h % d0.kvh or \
-                d0.h // d0.kvh > 4 or (2 if B == 2 * self.N else 1) * d0.kvh > 4 or N_CB - 1 >= 16:
+        if d0 is None or d0.qkv.qp is None or d0.hd not in (128, 384) or d0.h % d0.kvh or \
+                d0.h // d0.kvh > 4:
+            return
+        pairs, slots = (4, 16) if d0.hd == 128 else (8, 8)
+        if (2 if B == 2 * self.N else 1) * d0.kvh > pairs or N_CB - 1 >= slots:
             return
         Hq, Hk, HD, L = d0.h, d0.kvh, d0.hd, d0.kc.shape[2]
         if L < N_CB:

@@ -269,10 +269,11 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
     With ``rows`` [>= V, D] fp16 and ``x`` [B, D] fp16, row b of x also receives rows[token of
     row b] (zeros where the race had no winner): the next decoder pass's input when rows[t]
     holds projection(embedding of token t) (app/engine.py:343).  With ``qkv`` [>= V,
-    (Hq + 2 Hk) * 128] fp16 as well (the next pass's layer-0 q | k | v of each token at slot
-    ``p``), k and v also go to slot p of the caches ``kc`` / ``vc`` [B, Hk, L, 128] and each
-    row's decode attention over slots 0 .. p goes to ``o`` [B, Hq * 128].  With ``ev`` and
-    ``xe`` ([>= B, D] each), rows of ev are copied to the same rows of xe as they are."""
+    (Hq + 2 Hk) * HD] fp16 as well (the next pass's layer-0 q | k | v of each token at slot
+    ``p``), k and v also go to slot p of the caches ``kc`` / ``vc`` [B, Hk, L, HD] and each
+    row's decode attention over slots 0 .. p goes to ``o`` [B, Hq * HD] (HD = 128, or 384 with
+    the arithmetic of the short-cache attention kernel).  With ``ev`` and ``xe`` ([>= B, D]
+    each), rows of ev are copied to the same rows of xe as they are."""
     dev = _dev(logits, "sample_topk")
     _f16(logits, "sample_topk logits")
     B, V = logits.shape
@@ -298,20 +299,22 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
     if rows.dim() != 2 or rows.shape[0] < V or rows.shape[1] != D or rows.stride(1) != 1 or \
             x.dim() != 2 or x.shape[0] < B or x.stride(1) != 1:
         raise ValueError("sample_topk: rows must be [>= V, D] and x [>= B, D] with contiguous rows")
-    Hq = Hk = L = 0
+    Hq = Hk = L = HD = 0
     if qkv is not None:
         _f16(qkv, "sample_topk qkv")
         _f16(o, "sample_topk o")
         _f16(kc, "sample_topk kc")
         _f16(vc, "sample_topk vc")
-        Hk, L = kc.shape[1], kc.shape[2]
-        Hq = o.shape[1] // 128
-        if kc.dim() != 4 or kc.shape[0] < B or kc.shape[3] != 128 or vc.shape != kc.shape or \
+        if kc.dim() != 4:
+            raise ValueError("sample_topk: caches must be [>= B, Hk, L, HD]")
+        Hk, L, HD = kc.shape[1], kc.shape[2], kc.shape[3]
+        Hq = o.shape[1] // HD
+        if HD not in (128, 384) or kc.shape[0] < B or vc.shape != kc.shape or \
                 not kc.is_contiguous() or not vc.is_contiguous() or o.shape[0] < B or \
-                o.stride(1) != 1 or qkv.dim() != 2 or qkv.shape[1] != (Hq + 2 * Hk) * 128 or \
+                o.stride(1) != 1 or qkv.dim() != 2 or qkv.shape[1] != (Hq + 2 * Hk) * HD or \
                 qkv.stride(1) != 1:
-            raise ValueError("sample_topk: qkv [>= V, (Hq + 2 Hk) 128], caches [>= B, Hk, L, 128], "
-                             "o [>= B, Hq 128]")
+            raise ValueError("sample_topk: qkv [>= V, (Hq + 2 Hk) HD], caches [>= B, Hk, L, HD], "
+                             "o [>= B, Hq HD], HD 128 or 384")
     if (ev is None) != (xe is None):
         raise ValueError("sample_topk: ev and xe go together")
     if ev is not None:
@@ -325,7 +328,8 @@ def sample_topk(logits, N, cfg, temp, topk, out, seed=None, pos=None, salt=0, no
               out.data_ptr(), out.stride(0), rows.data_ptr(), rows.stride(0), rows.shape[0],
               x.data_ptr(), x.stride(0), D, _ptr(qkv), 0 if qkv is None else qkv.stride(0),
               0 if qkv is None else qkv.shape[0], _ptr(kc), _ptr(vc), L, int(p), _ptr(o),
-              0 if o is None else o.stride(0), Hq, Hk, _ptr(ev), 0 if ev is None else ev.stride(0),
+              0 if o is None else o.stride(0), Hq, Hk, HD, _ptr(ev),
+              0 if ev is None else ev.stride(0),
               _ptr(xe), 0 if xe is None else xe.stride(0), stream_ptr(dev))
 
 

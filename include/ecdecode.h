@@ -140,10 +140,12 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
  *  - x rows <- rows[t] from rows [rows_n >= V, D] f16 (row stride rows_ld), row stride x_ld;
  *    rows and x 16-byte aligned, D, rows_ld and x_ld multiples of 8;
  *  - with qkv != NULL, that pass's layer 0 up to its attention output: q | k | v of t from
- *    qkv [qkv_n >= V, (Hq + 2 Hk) * 128] f16 (row stride qkv_ld; q heads, k heads, v heads,
- *    RoPE applied for slot p), k and v into slot p of the caches kc / vc [B, Hk, L, 128], and
- *    the decode attention of each row over slots 0 .. p into o [B, Hq * 128] (row stride o_ld);
- *    head_dim 128, Hq / Hk <= 4, (1 or 2 rows) * Hk <= 4, p < min(L, 16);
+ *    qkv [qkv_n >= V, (Hq + 2 Hk) * HD] f16 (row stride qkv_ld; q heads, k heads, v heads,
+ *    RoPE applied for slot p), k and v into slot p of the caches kc / vc [B, Hk, L, HD], and
+ *    the decode attention of each row over slots 0 .. p into o [B, Hq * HD] (row stride o_ld);
+ *    Hq / Hk <= 4 and either HD = 128, (1 or 2 rows) * Hk <= 4, p < min(L, 16), or HD = 384
+ *    (the arithmetic of ecd_decode_attn's short-cache kernel), (1 or 2 rows) * Hk <= 8,
+ *    p < min(L, 8); HD is read only with qkv;
  *  - with ev != NULL, xe rows n (and n + N) <- ev rows n (and n + N), D wide (row strides
  *    ev_ld, xe_ld; 16-byte aligned, multiples of 8): rows that do not depend on the token, such
  *    as the first pass's projected backbone state.
@@ -157,8 +159,8 @@ int ecd_sample_topk_next(const void* logits, long ld, int B, int N, float cfg, f
                          const int64_t* pos, int salt, int64_t* out, long out_stride,
                          const void* rows, long rows_ld, int rows_n, void* x, long x_ld, int D,
                          const void* qkv, long qkv_ld, int qkv_n, void* kc, void* vc, int L,
-                         int p, void* o, long o_ld, int Hq, int Hk, const void* ev, long ev_ld,
-                         void* xe, long xe_ld, void* stream);
+                         int p, void* o, long o_ld, int Hq, int Hk, int HD, const void* ev,
+                         long ev_ld, void* xe, long xe_ld, void* stream);
 
 /* End of one frame of the song loop, on the device (app/engine.py:419-440: the host's
  * tok/pos copies, out[i + 1] = tok[:N] and the EOS scan, moved inside the captured frame).

@@ -11,8 +11,8 @@ HEADER = ROOT / "include" / "ecdecode.h"
 
 
 
-# ecd_sample_topk_next without the folded attention: qkv .. Hk, stream
-_NOATT = (None, 0, 0, None, None, 0, 0, None, 0, 0, 0, None, 0, None, 0, None)
+# ecd_sample_topk_next without the folded attention: qkv .. HD, stream
+_NOATT = (None, 0, 0, None, None, 0, 0, None, 0, 0, 0, 0, None, 0, None, 0, None)
 
 def declared():
     text = HEADER.read_text()
@@ -76,19 +76,28 @@ def _taps(*offsets):
                                      16, 1024, 8197, 16, 1024, 1024, *_NOATT),   # B != N, 2N
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 1024, 8197, 16, 1024, 1024, 16, 1536, 8197, 16, 16, 8, 8,
-                                     16, 1024, 8, 2, None, 0, None, 0, None),    # p = L
+                                     16, 1024, 8, 2, 128, None, 0, None, 0, None),  # p = L
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 1024, 8197, 16, 1024, 1024, 16, 2048, 8197, 16, 16, 8, 3,
-                                     16, 1536, 12, 2, None, 0, None, 0, None),   # G = 6 > 4
+                                     16, 1536, 12, 2, 128, None, 0, None, 0, None),  # G = 6 > 4
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 1024, 8197, 16, 1024, 1024, 16, 2048, 8197, 16, 16, 8, 3,
-                                     16, 1024, 8, 4, None, 0, None, 0, None),    # 2 rows x 4 kv heads
+                                     16, 1024, 8, 4, 128, None, 0, None, 0, None),  # 2 x 4 pairs
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 1024, 8197, 16, 1024, 1024, 16, 1536, 8197, None, 16, 8,
-                                     3, 16, 1024, 8, 2, None, 0, None, 0, None), # no k cache
+                                     3, 16, 1024, 8, 2, 128, None, 0, None, 0, None),  # no k cache
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 1024, 8197, 16, 1024, 1024, None, 0, 0, None, None, 0, 0,
-                                     None, 0, 0, 0, 16, 1024, None, 1024, None),  # ev without xe
+                                     None, 0, 0, 0, 0, 16, 1024, None, 1024, None),  # ev without xe
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 3072, 8197, 16, 3072, 3072, 16, 4096, 8197, 16, 16, 8, 3,
+                                     16, 2048, 8, 4, 256, None, 0, None, 0, None),  # head_dim 256
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 3072, 8197, 16, 3072, 3072, 16, 6144, 8197, 16, 16, 16, 8,
+                                     16, 3072, 8, 4, 384, None, 0, None, 0, None),  # 384: p = 8
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 3072, 8197, 16, 3072, 3072, 16, 12288, 8197, 16, 16, 8, 3,
+                                     16, 3072, 8, 8, 384, None, 0, None, 0, None),  # 384: 2 x 8 pairs
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
     lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0
     lambda L: L.ecd_embed_i8(8, 1, 8, 8, 0, 0, 8197, None, 8, 1, 8, None),        # rows 0

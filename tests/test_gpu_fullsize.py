@@ -229,13 +229,13 @@ def cref(dev):
 
 
 def test_reference_decoder_sampled_frame_matches_forced(dev, cref):
-    """The sampled path of the reference's own decoder (head_dim 384: no layer-0 q|k|v table,
-    so its passes 1..6 take their input rows from the samplers and start at layer 0's q|k|v;
-    the first pass from the fused codebook-0 + projection GEMV) against its teacher-forced
-    frame on the sampled tokens: KL < 1e-4 on all 8 heads, the backbone cache slot bit for
-    bit."""
+    """The sampled path of the reference's own decoder (head_dim 384: passes 1..6 take their
+    input rows and layer 0 up to its attention output from the samplers, the register form of
+    the folded attention; the first pass from the fused codebook-0 + projection GEMV) against
+    its teacher-forced frame on the sampled tokens: KL < 1e-4 on all 8 heads, the backbone
+    cache slot bit for bit."""
     _, gm = cref
-    _sampled_vs_forced(gm, 750, 43, tables=("rows",))
+    _sampled_vs_forced(gm, 750, 43, tables=("rows", "qkv"))
 
 
 def test_reference_decoder_frame_kv750(dev, cref):

@@ -174,18 +174,25 @@ def test_sampler_next_rows(dev, N, cfg_on, philox):
         assert torch.equal(x2[0::2], ev) and bool((x2[1::2] == 5.0).all())
 
 
-@pytest.mark.parametrize("N,cfg_on,p", [(4, True, 2), (4, True, 7), (3, False, 5)])
-def test_sampler_next_layer0_attention(dev, N, cfg_on, p):
+@pytest.mark.parametrize("N,cfg_on,p,Hq,Hk,HD,D", [
+    (4, True, 2, 8, 2, 128, 1024), (4, True, 7, 8, 2, 128, 1024), (3, False, 5, 8, 2, 128, 1024),
+    # head_dim 384 (the reference decoder: 8 q / 4 kv heads, 3072 wide), register form
+    (4, True, 2, 8, 4, 384, 3072), (4, True, 7, 8, 4, 384, 3072), (3, False, 4, 8, 4, 384, 3072),
+    (2, True, 6, 4, 4, 384, 3072)])
+def test_sampler_next_layer0_attention(dev, N, cfg_on, p, Hq, Hk, HD, D):
     """ecd_sample_topk_next with the q|k|v rows: per sampled token, k and v land in cache slot p
     bit for bit (other slots untouched), and o is the decode attention over slots 0 .. p
-    (oracle.kernels.decode_attn_out, one split) within the fp16 kernel bar."""
+    (oracle.kernels.decode_attn_out, one split) within the fp16 kernel bar; for head_dim 384,
+    o is bit-equal to the standalone short-cache attention kernel on the updated caches."""
+    import math
     import torch
+    from estudiocanciones_amd import _ffi
     from estudiocanciones_amd.kernels import sample_topk
     from helpers import assert_close16
     from oracle.kernels import decode_attn_out
-    g = rng(400 + 10 * N + p)
+    g = rng(400 + 10 * N + p + HD)
     B = 2 * N if cfg_on else N
-    Hq, Hk, HD, L, D = 8, 2, 128, 8, 1024
+    L = 8
     NQ = (Hq + 2 * Hk) * HD
     rows = T(g.standard_normal((V, D), dtype=np.float32).astype(np.float16), dev)
     qkv = T(g.standard_normal((V, NQ), dtype=np.float32).astype(np.float16), dev)
@@ -211,4 +218,12 @@ def test_sampler_next_layer0_attention(dev, N, cfg_on, p):
     assert np.array_equal(kc.cpu().numpy(), kw) and np.array_equal(vc.cpu().numpy(), vw)
     want = decode_attn_out(tq[:, :Hq * HD], kw, vw, np.full(B, p, np.int64), 1, Hq, Hk, HD,
                            nsplit=1)
-    assert_close16(o.cpu().numpy(), want, what=f"folded layer-0 attention p={p}")
+    assert_close16(o.cpu().numpy(), want, what=f"folded layer-0 attention p={p} HD={HD}")
+    if HD == 384:
+        qt = T(np.ascontiguousarray(tq[:, :Hq * HD]), dev)
+        pos = torch.full((B,), p, dtype=torch.int64, device=dev)
+        o2 = torch.full_like(o, 5.0)
+        _ffi.call("ecd_decode_attn", qt.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(),
+                  o2.data_ptr(), None, None, None, B, 1, Hq, Hk, L, HD, 1, 1.0 / math.sqrt(HD),
+                  torch.cuda.current_stream().cuda_stream)
+        assert torch.equal(o, o2), "register form differs from the short-cache kernel"
