@@ -176,6 +176,13 @@ def test_c3_frame_kv3256(dev, c3):
     _frame(om, gm, 3256, seed=32)
 
 
+def test_c3_frame_kv4096(dev, c3):
+    """The same frame at the target length of 4096 attended slots (the backbone's tails split
+    each (row, kv head) pair's attention over 4 workgroups and 32 waves of 8 tiles)."""
+    om, gm = c3
+    _frame(om, gm, 4096, seed=34)
+
+
 def _sampled_vs_forced(gm, att, seed, tables):
     """One sampled frame at position att - 1 against the teacher-forced frame on the tokens it
     sampled (injected Exponential draws): KL < 1e-4 on all 8 heads, the backbone cache slot bit
@@ -245,12 +252,13 @@ def test_reference_decoder_frame_kv750(dev, cref):
 
 
 def test_c4_prompt_pass_3b_layers(dev):
-    """Prompt pass at the 3B layer shape (2 of its 28 layers): B = 8 rows x 256 tokens through
-    the MFMA GEMMs and the causal flash attention, cache capacity 3514 (app/engine.py:123-178)."""
+    """Prompt pass of the whole 28-layer 3B backbone: B = 8 rows x 256 tokens through the MFMA
+    GEMMs and the causal flash attention, cache capacity 3514 (app/engine.py:123-178)."""
     import torch
     from estudiocanciones_amd.engine import Linear, Stack
     from estudiocanciones_amd.quant import q8_rows
-    cfg = dict(BB, layers=2)
+    cfg = dict(BB)
+    assert cfg["layers"] == 28
     B, P, L = 8, 256, 3514
     g = torch.Generator(device=dev)
     g.manual_seed(41)
@@ -300,8 +308,11 @@ def test_c4_prompt_pass_3b_layers(dev):
     # layer 0's cache is one GEMM deep: the kernel bar
     assert_close16(N(st.blocks[0].kc[:, :, :P]), wc[0][0], what="prompt k cache, layer 0")
     assert_close16(N(st.blocks[0].vc[:, :, :P]), wc[0][1], what="prompt v cache, layer 0")
-    assert_within_noise(N(st.blocks[1].kc[:, :, :P]), wc[1][0], ac[1][0], what="prompt k cache, layer 1")
-    assert_within_noise(N(st.blocks[1].vc[:, :, :P]), wc[1][1], ac[1][1], what="prompt v cache, layer 1")
+    for i in (1, len(st.blocks) - 1):
+        assert_within_noise(N(st.blocks[i].kc[:, :, :P]), wc[i][0], ac[i][0],
+                            what=f"prompt k cache, layer {i}")
+        assert_within_noise(N(st.blocks[i].vc[:, :, :P]), wc[i][1], ac[i][1],
+                            what=f"prompt v cache, layer {i}")
 
 
 # ---------------------------------------------------------------- isolated kernels (C1)
