@@ -798,10 +798,10 @@ def measure_isolated(torch, dev, min_bytes=768 << 20):
     independent buffer sets (>= 16, and > 768 MB in total) that the 256 MB Infinity Cache cannot
     serve the repeated reads: GEMV 3072 -> 8192 and 8192 -> 3072 at 1/2/4/8 rows (packed weights
     with streaming loads, the engine's path, and the drop-in int8_mm on row-major weights), and
-    GQA decode attention 24q / 8kv, head_dim 128, 16 splits + combine over 512 ... 8192 cached
-    tokens at batch 1 and 8 (every row at position L - 1), with the reference's grid (``us``)
-    and with the engine's split count (``engine_us``: enough splits for about two waves per
-    CU)."""
+    GQA decode attention 24q / 8kv, head_dim 128, over 512 ... 8192 cached tokens at batch 1
+    and 8 (every row at position L - 1), with the reference's grid (``us``: 16 splits + the
+    combine launch) and with the engine's (``engine_us``: the split attention and its merge in
+    one launch, attention_kb workgroups of 8 splits per (row, kv head), one workgroup per CU)."""
     from estudiocanciones_amd import _ffi
     from estudiocanciones_amd import engine as E
     from estudiocanciones_amd import kernels as KK
@@ -848,26 +848,24 @@ def measure_isolated(torch, dev, min_bytes=768 << 20):
                                       G=Hq // Hk, NSPLIT=ns)
                 KK._attn_combine[(B * Hq,)](pm, pl, pa, o, HD=HD, NSPLIT=ns)
             ms = _rotated_time(torch, [lambda kc=kc, vc=vc: one(kc, vc) for kc, vc in zip(kcs, vcs)])
-            # the engine's own split count (grid of about two waves per CU)
-            ens = E.attention_splits(B, Hk, L)
-            epm = torch.empty(B * Hq * ens, device=dev)
-            epl = torch.empty_like(epm)
-            epa = torch.empty(B * Hq * ens, HD, device=dev)
+            # the engine's own attention: the split attention and its merge in one launch,
+            # attention_kb workgroups of 8 splits per (row, kv head)
+            ekb = E.attention_kb(B, Hk, L)
+            ews = torch.empty(B * Hq * ekb * (2 + HD), device=dev)
+            ecnt = torch.zeros(B * Hk, device=dev, dtype=torch.int32)
 
             def eng(kc, vc):
                 st = torch.cuda.current_stream().cuda_stream
-                _ffi.call("ecd_decode_attn", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                          pos.data_ptr(), o.data_ptr(), epm.data_ptr(), epl.data_ptr(),
-                          epa.data_ptr(), B, 1, Hq, Hk, L, HD, ens, sc, st)
-                _ffi.call("ecd_attn_combine", epm.data_ptr(), epl.data_ptr(), epa.data_ptr(),
-                          o.data_ptr(), B * Hq, HD, ens, st)
+                _ffi.call("ecd_decode_attn_merged", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                          pos.data_ptr(), o.data_ptr(), ews.data_ptr(), ecnt.data_ptr(), B, 1,
+                          Hq, Hk, L, HD, ekb, sc, st)
             ems = _rotated_time(torch, [lambda kc=kc, vc=vc: eng(kc, vc) for kc, vc in zip(kcs, vcs)])
             alg = attn_bytes(B, Hq, Hk, HD, [L] * B)
             out["attention"].append({"B": B, "L": L, "sets": sets, "algorithmic_bytes": alg,
                                      "us": round(ms * 1e3, 2),
                                      "GBps": round(alg / ms / 1e6, 1),
                                      "frac": round(alg / ms / 1e6 / HBM_PEAK_GBPS, 4),
-                                     "engine_splits": ens,
+                                     "engine_splits": 8 * ekb,
                                      "engine_us": round(ems * 1e3, 2),
                                      "engine_frac": round(alg / ems / 1e6 / HBM_PEAK_GBPS, 4)})
             del kcs, vcs

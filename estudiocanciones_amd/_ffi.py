@@ -29,6 +29,8 @@ SIGNATURES = {
     "ecd_attn_combine": [_P, _P, _P, _P, c_int, c_int, c_int, _P],
     "ecd_decode_attn_noalloc": [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                 c_float, _P],
+    "ecd_decode_attn_merged": [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
+                               c_int, c_int, c_float, _P],
     "ecd_silu_mul": [_P, _P, c_int, c_int, _P],
     "ecd_embed_sum_i8": [_P, _P, _P, c_long, _P, c_int, c_int, c_int, c_int, _P],
     "ecd_embed_i8": [_P, c_long, _P, _P, c_long, c_int, c_int, _P, _P, c_int, c_int, _P],

@@ -231,6 +231,156 @@ static int launch_hd(int G, dim3 grid, hipStream_t st, const f16* q, const f16* 
 #undef ECD_ATTN_G
 }
 
+// ---- The split attention and its merge in one launch (the engine's attention over long caches).
+// A workgroup of MW waves takes MW consecutive splits of one (row, kv head) pair (wave w: split
+// MW kb + w of the pair's KB MW), runs them as decode_attn_kernel does, and merges its waves'
+// partials in LDS by log-sum-exp in wave order.  Its partial (m, l, acc of each query head) goes
+// to the workspace with agent-scope stores (written through to memory); once they are
+// acknowledged, the workgroup counts itself on the pair's counter (an agent-scope atomic).  The
+// workgroup that brings the count to KB merges the KB partials in order (agent-scope loads, so
+// no stale L2 line of another XCD's partial is read) into o and resets the counter, which is
+// zero again for the next call.  No workgroup waits for another: any residency is safe.  The
+// merge steps are those of attn_combine_kernel: M = max m, w = exp(m - M) (0 for empty parts),
+// o = fp16(sum w acc / sum w l), applied twice (waves, then workgroups).
+constexpr int MW = 8;        // waves (splits) per workgroup
+constexpr int MKB_MAX = 32;  // workgroups per pair at most
+
+__device__ __forceinline__ void st_agent_f32(float* p, float v) {
+  __hip_atomic_store((uint32_t*)p, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent_f32(const float* p) {
+  return __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(64 * MW) void decode_attn_merged_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
+    const int64_t* __restrict__ pos, f16* __restrict__ o, float* __restrict__ ws,
+    uint32_t* __restrict__ cnt, int S, int Hq, int Hk, int L, float scale) {
+  constexpr int NDP = SplitStateM<HD, G>::NDP;
+  constexpr int PS = 2 + HD;  // floats of one head's partial: m, l, acc[HD]
+  __shared__ float part[MW][G][PS];
+  __shared__ float s_m[MKB_MAX][G];
+  __shared__ float s_l[MKB_MAX][G];
+  __shared__ uint32_t s_last;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kb = blockIdx.x, KB = gridDim.x, kh = blockIdx.y, r = blockIdx.z;
+  const long cbase = ((long)(r / S) * Hk + kh) * (long)L * HD;
+
+  KVTile<HD> ring[attn_ring(HD)];
+  f16x8 qf[HD / 32];
+  load_q<HD, G>(qf, q, r, Hq, kh, lane);
+  int lo, hi;
+  split_range(pos, r, L, KB * MW, kb * MW + wv, lo, hi);
+  if (lo < hi) kv_load<HD>(ring[0], kc + cbase, vc + cbase, lo, hi - 1, lane);
+  SplitStateM<HD, G> ss;
+  attn_run_m<HD, G, attn_ring(HD)>(ss, qf, ring, kc + cbase, vc + cbase, lo, hi, scale, lane);
+
+  // the wave's partial to LDS: lane (n, grp) holds head n's d = 128 j + 8 (4 grp + i) + b
+  const int n = lane & 15, grp = lane >> 4;
+  if (n < G) {
+    float* pp = part[wv][n];
+    if (grp == 0) {
+      pp[0] = ss.m_run;
+      pp[1] = ss.l_run;
+    }
+#pragma unroll
+    for (int j = 0; j < NDP; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 128 * j + 8 * (4 * grp + i);
+        if (d0 < HD)
+#pragma unroll
+          for (int b = 0; b < 8; ++b) pp[2 + d0 + b] = ss.acc[j][b][i];
+      }
+  }
+  __syncthreads();
+
+  // the workgroup's partial: thread t merges item (g, d) over the MW waves
+  const long pair = (long)r * Hk + kh;
+  float* wsp = ws + pair * KB * G * PS;  // [KB][G][PS] of this pair
+  for (int it = threadIdx.x; it < G * HD; it += 64 * MW) {
+    const int g = it / HD, d = it - g * HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) M = fmaxf(M, part[w][g][0]);
+    float a = 0.f, l = 0.f;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) {
+      const float m = part[w][g][0];
+      const float wt = m > -INFINITY ? __expf(m - M) : 0.f;
+      a += part[w][g][2 + d] * wt;
+      l += part[w][g][1] * wt;
+    }
+    float* dst = wsp + ((long)kb * G + g) * PS;
+    st_agent_f32(dst + 2 + d, a);
+    if (d == 0) {
+      st_agent_f32(dst, M);
+      st_agent_f32(dst + 1, l);
+    }
+  }
+  wait_vm0();  // this thread's partial stores are acknowledged
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(cnt + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (uint32_t)(KB - 1);
+  __syncthreads();
+  if (!s_last) return;
+
+  // the pair's last workgroup: merge the KB partials in order
+  if (threadIdx.x < KB * G) {
+    const int k = threadIdx.x / G, g = threadIdx.x - k * G;
+    s_m[k][g] = ld_agent_f32(wsp + ((long)k * G + g) * PS);
+    s_l[k][g] = ld_agent_f32(wsp + ((long)k * G + g) * PS + 1);
+  }
+  __syncthreads();
+  for (int it = threadIdx.x; it < G * HD; it += 64 * MW) {
+    const int g = it / HD, d = it - g * HD;
+    float av[MKB_MAX];
+#pragma unroll
+    for (int k = 0; k < MKB_MAX; ++k)
+      av[k] = k < KB ? ld_agent_f32(wsp + ((long)k * G + g) * PS + 2 + d) : 0.f;
+    float M = -INFINITY;
+    for (int k = 0; k < KB; ++k) M = fmaxf(M, s_m[k][g]);
+    float a = 0.f, den = 0.f;
+#pragma unroll
+    for (int k = 0; k < MKB_MAX; ++k) {
+      if (k < KB) {
+        const float m = s_m[k][g];
+        const float wt = m > -INFINITY ? __expf(m - M) : 0.f;
+        a += av[k] * wt;
+        den += s_l[k][g] * wt;
+      }
+    }
+    o[((long)r * Hq + kh * G + g) * HD + d] = (f16)(a / den);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HD>
+static int launch_merged(int G, dim3 grid, hipStream_t st, const f16* q, const f16* kc,
+                         const f16* vc, const int64_t* pos, f16* o, float* ws, uint32_t* cnt,
+                         int S, int Hq, int Hk, int L, float scale) {
+#define ECD_MERGED_G(G_)                                                                      \
+  case G_:                                                                                    \
+    hipLaunchKernelGGL((decode_attn_merged_kernel<HD, G_>), grid, dim3(64 * MW), 0, st, q, kc, \
+                       vc, pos, o, ws, cnt, S, Hq, Hk, L, scale);                             \
+    return ECD_OK;
+  switch (G) {
+    ECD_MERGED_G(1)
+    ECD_MERGED_G(2)
+    ECD_MERGED_G(3)
+    ECD_MERGED_G(4)
+    ECD_MERGED_G(8)
+    default:
+      return ECD_ENOTSUP;
+  }
+#undef ECD_MERGED_G
+}
+
 // Split partials of ecd_decode_attn_noalloc, for callers that cannot allocate: one static
 // array per GPU (each device holds its own copy at its own address), laid out as the
 // caller-supplied pm | pl | pa of ecd_decode_attn.  Every used slot is written by the attention
@@ -340,6 +490,35 @@ int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const
                                  stream);
   if (r1 != ECD_OK) return r1;
   return ecd_attn_combine(pm, pl, pa, o, R * Hq, HD, nsplit, stream);
+}
+
+int ecd_decode_attn_merged(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                           void* o, float* ws, uint32_t* cnt, int R, int S, int Hq, int Hk, int L,
+                           int HD, int kb, float scale, void* stream) {
+  if (!q || !kc || !vc || !pos || !o || !ws || !cnt || R <= 0 || S <= 0 || Hq <= 0 || Hk <= 0 ||
+      L <= 0 || HD <= 0 || (Hq % Hk) != 0 || kb < 1 || kb > MKB_MAX || (long)R * Hk > 65535)
+    return ECD_EINVAL;
+  const int G = Hq / Hk;
+  const dim3 grid(kb, Hk, R);
+  hipStream_t st = (hipStream_t)stream;
+  const f16 *qh = (const f16*)q, *kh = (const f16*)kc, *vh = (const f16*)vc;
+  f16* oh = (f16*)o;
+  int rc;
+  switch (HD) {
+    case 128:
+      rc = launch_merged<128>(G, grid, st, qh, kh, vh, pos, oh, ws, cnt, S, Hq, Hk, L, scale);
+      break;
+    case 256:
+      rc = launch_merged<256>(G, grid, st, qh, kh, vh, pos, oh, ws, cnt, S, Hq, Hk, L, scale);
+      break;
+    case 384:
+      rc = launch_merged<384>(G, grid, st, qh, kh, vh, pos, oh, ws, cnt, S, Hq, Hk, L, scale);
+      break;
+    default:
+      rc = ECD_ENOTSUP;
+  }
+  if (rc != ECD_OK) return rc;
+  return ecd_launch_status();
 }
 
 int ecd_attn_combine(const float* pm, const float* pl, const float* pa, void* o, int RH, int HD,

@@ -18,7 +18,10 @@ reference, all deliberate:
 * the prompt arrives as token ids (tokenisation is host string work, out of scope);
 * the text-embedding table lives on the GPU (one gather per song);
 * decode attention over caches of at most 128 slots uses one split (direct output,
-  no combine pass); longer caches use the reference's 16 splits;
+  no combine pass); longer caches run the split attention and its merge in one launch,
+  with enough splits to cover the CUs (``attention_kb``), where the reference launches 16
+  splits and a combine; the reference's launch pair is kept for the drop-in path
+  (``decode_reference``);
 * the song loop keeps its bookkeeping on the device: the captured frame ends with a kernel
   that feeds the tokens back, stores the frame and records each take's first EOS frame, so
   the host only replays the graph and reads N integers every 25 frames.
@@ -49,21 +52,20 @@ DIM = 3072
 TEXT_BOS, TEXT_EOS, AUDIO_EOS, EMPTY_ID = 128000, 128001, 8193, 0
 FRAME_MS = 80
 
-ATT_SHORT = 128        # caches of at most this many slots: one attention split per (row, kv head)
-ATT_SPLITS_MAX = 64   # longest split count of the engine's standalone attention
-ATT_WAVES = 512       # waves the standalone attention grid aims at (two per CU of an MI355X)
+ATT_SHORT = 128      # caches of at most this many slots: one attention split per (row, kv head)
+ATT_WG = 256        # workgroups the merged attention grid aims at (one per CU of an MI355X)
+ATT_KB_MAX = 16     # workgroups per (row, kv head) pair at most (the last one merges them all)
 
 
-def attention_splits(R, Hk, L):
-    """Split count of the engine's standalone decode attention over a cache of L slots: one
-    split for short caches, else enough splits that R x Hk x splits waves cover the CUs about
-    twice, but no split shorter than 64 slots (four 16-slot tiles: one wave's loads in flight),
-    at least 16 (fewer splits leave each wave a long serial walk) and at most ATT_SPLITS_MAX
-    (the combine's register path)."""
-    if L <= ATT_SHORT:
-        return 1
-    want = min(-(-ATT_WAVES // max(1, R * Hk)), -(-L // 64))
-    return max(16, min(ATT_SPLITS_MAX, want))
+def attention_kb(R, Hk, L):
+    """Workgroups per (row, kv head) pair of the engine's decode attention over a cache of L
+    slots (ecd_decode_attn_merged, 8 splits per workgroup): enough that R x Hk x kb workgroups
+    cover the CUs and no split is longer than 128 slots, but no split shorter than one 16-slot
+    tile and at most ATT_KB_MAX (measured on MI355X, 24q / 8kv, head_dim 128: one row at 4096
+    slots takes 11.1 us with 16 workgroups per pair against 12.7 with 32; batch 8 takes
+    31.7 us with 4 against 34.0 with 8, and 58.8 us at 8192 slots with 8 against 60.0 with 4)."""
+    want = max(-(-ATT_WG // max(1, R * Hk)), -(-L // 1024))
+    return max(1, min(ATT_KB_MAX, want, -(-L // 128)))
 
 
 BACKBONE = dict(layers=28, heads=24, kv_heads=8, max_seq=8192, dim=DIM)
@@ -232,7 +234,8 @@ class Stack:
         self.dim = dim
         self.hd = dim // cfg["heads"]
         self.max_seq = cfg["max_seq"]
-        self.att_ws = None  # split partials of the standalone attention (m | l | acc, fp32)
+        self.att_ws = None   # workgroup partials of the standalone attention (fp32)
+        self.att_cnt = None  # its per-(row, kv head) counters (zero between calls)
         self.tail = None   # layer-tail buffers for B-row decode steps
         self.tail2 = None  # the same for 2B rows (two rows per cache), sharing sync, ws and err
         self.use_tail = True
@@ -246,10 +249,12 @@ class Stack:
         if self.blocks and L > ATT_SHORT:
             # partials of a decode step of up to 2B rows (two rows per cache) or of a short
             # prompt through the decode path (at most PROMPT_GEMM_ROWS rows): R rows take
-            # R x attention_splits(R) <= 16 R + ATT_WAVES (row, split) pairs per query head
-            hq = max(b.h for b in self.blocks)
-            n = (16 * max(2 * B, PROMPT_GEMM_ROWS) + ATT_WAVES) * hq
+            # R x Hk x attention_kb(R) workgroups of G head partials, at most ATT_KB_MAX R Hq
+            hq, hk = max(b.h for b in self.blocks), max(b.kvh for b in self.blocks)
+            rmax = max(2 * B, PROMPT_GEMM_ROWS)
+            n = ATT_KB_MAX * rmax * hq
             self.att_ws = torch.empty(n * (2 + self.hd), device=dev, dtype=torch.float32)
+            self.att_cnt = torch.zeros(rmax * hk, device=dev, dtype=torch.int32)
         self.tail = self._tail_buffers(B, dev, dtype, L)
         self.tail2 = None if self.tail is None else \
             self._tail_buffers(2 * B, dev, dtype, L, share=self.tail)
@@ -294,7 +299,7 @@ class Stack:
     def free(self):
         for b in self.blocks:
             b.kc = b.vc = None
-        self.tail = self.tail2 = self.att_ws = None
+        self.tail = self.tail2 = self.att_ws = self.att_cnt = None
 
     def __call__(self, x, pos, attn_len=None, mask=None):
         """Prompt pass (app/engine.py:174-178): x [B, S, D], pos [B, S] absolute positions
@@ -413,28 +418,25 @@ class Stack:
         """Decode attention of block b for the rows of q (row r over cache slots [0, pos[r]],
         app/kernels.py:110-167).  Caches of at most ATT_SHORT slots, and prompt passes
         (``splits=1``: the rows give the parallelism), run one split per (row, kv head) that
-        writes o itself.  Longer caches split the attended range so that the grid has about
-        two waves per CU whatever the row count (attention_splits), and one combine launch
-        merges the partials kept in the stack's workspace."""
+        writes o itself.  Longer caches run the split attention with its merge in the same
+        launch (ecd_decode_attn_merged: attention_kb workgroups of 8 splits per pair, so that
+        the grid covers the CUs whatever the row count), on the stack's workspace."""
         R = q.shape[0]
         Hq, Hk, HD, L = b.h, b.kvh, b.hd, b.kc.shape[2]
-        ns = splits if splits is not None else attention_splits(R, Hk, L)
         o = torch.empty_like(q)
         st = stream_ptr(q.device)
-        if ns == 1:
+        if splits == 1 or L <= ATT_SHORT:
             _ffi.call("ecd_decode_attn", q.data_ptr(), b.kc.data_ptr(), b.vc.data_ptr(),
                       pos.data_ptr(), o.data_ptr(), None, None, None, R, S, Hq, Hk, L, HD, 1,
                       1.0 / math.sqrt(HD), st)
             return o
-        n = R * Hq * ns
-        if self.att_ws is None or self.att_ws.numel() < n * (2 + HD):
-            raise RuntimeError("Stack._attention: the split workspace is smaller than the call")
-        pm, pl, pa = self.att_ws[:n], self.att_ws[n:2 * n], self.att_ws[2 * n:n * (2 + HD)]
-        _ffi.call("ecd_decode_attn", q.data_ptr(), b.kc.data_ptr(), b.vc.data_ptr(),
-                  pos.data_ptr(), o.data_ptr(), pm.data_ptr(), pl.data_ptr(), pa.data_ptr(), R, S,
-                  Hq, Hk, L, HD, ns, 1.0 / math.sqrt(HD), st)
-        _ffi.call("ecd_attn_combine", pm.data_ptr(), pl.data_ptr(), pa.data_ptr(), o.data_ptr(),
-                  R * Hq, HD, ns, st)
+        kb = attention_kb(R, Hk, L)
+        if self.att_ws is None or self.att_ws.numel() < R * Hq * kb * (2 + HD) or \
+                self.att_cnt.numel() < R * Hk:
+            raise RuntimeError("Stack._attention: the attention workspace is smaller than the call")
+        _ffi.call("ecd_decode_attn_merged", q.data_ptr(), b.kc.data_ptr(), b.vc.data_ptr(),
+                  pos.data_ptr(), o.data_ptr(), self.att_ws.data_ptr(), self.att_cnt.data_ptr(),
+                  R, S, Hq, Hk, L, HD, kb, 1.0 / math.sqrt(HD), st)
         return o
 
     def decode_reference(self, x, pos, S):

@@ -92,6 +92,21 @@ int ecd_decode_attn_noalloc(const void* q, const void* kc, const void* vc, const
                             void* o, int R, int S, int Hq, int Hk, int L, int HD, int nsplit,
                             float scale, void* stream);
 
+/* The split decode attention and its merge in one launch: the pair (_attn, _attn_combine) of
+ * app/kernels.py:110-167 as launched at app/engine.py:194-204, for the engine's own attention
+ * over long caches.  Grid (kb, Hk, R) of 8-wave workgroups: each (row, kv head) pair is cut
+ * into 8 kb splits (chunks as in ecd_decode_attn), a workgroup merges its 8 waves' partials,
+ * and the pair's last workgroup to finish merges the kb workgroup partials into o (the
+ * log-sum-exp steps of ecd_attn_combine, applied per workgroup and then across them, so only
+ * the fp32 summation order differs from the pair of launches).
+ *   ws: [R * Hk * kb * (Hq / Hk) * (2 + HD)] f32 workgroup partials (any contents);
+ *   cnt: [R * Hk] uint32 pair counters, zero before the first call; every call leaves them
+ *   zero.  Two calls that run at the same time must not share ws or cnt.
+ *   1 <= kb <= 32; HD in {128, 256, 384}; Hq / Hk in {1, 2, 3, 4, 8}; R * Hk <= 65535. */
+int ecd_decode_attn_merged(const void* q, const void* kc, const void* vc, const int64_t* pos,
+                           void* o, float* ws, uint32_t* cnt, int R, int S, int Hq, int Hk, int L,
+                           int HD, int kb, float scale, void* stream);
+
 /* y[r, c] = f16(f16(silu(x[r, c])) * x[r, F + c]) for x [R, 2F], y [R, F].
  * Replaces _silu_mul (app/kernels.py:171-180), launched at app/engine.py:209. */
 int ecd_silu_mul(const void* x, void* y, int R, int F, void* stream);

@@ -62,6 +62,10 @@ def _taps(*offsets):
     lambda L: L.ecd_attn_combine(None, None, None, None, 1, 128, 16, None),
     lambda L: L.ecd_decode_attn_noalloc(8, 8, 8, 8, None, 1, 1, 8, 2, 8, 128, 16, 0.1, None),   # no o
     lambda L: L.ecd_decode_attn_noalloc(8, 8, 8, 8, 8, 1, 1, 8, 3, 8, 128, 16, 0.1, None),      # Hq % Hk
+    lambda L: L.ecd_decode_attn_merged(8, 8, 8, 8, 8, 8, None, 1, 1, 24, 8, 4096, 128, 4, 0.1, None),  # no cnt
+    lambda L: L.ecd_decode_attn_merged(8, 8, 8, 8, 8, 8, 8, 1, 1, 24, 8, 4096, 128, 0, 0.1, None),     # kb 0
+    lambda L: L.ecd_decode_attn_merged(8, 8, 8, 8, 8, 8, 8, 1, 1, 24, 8, 4096, 128, 33, 0.1, None),    # kb 33
+    lambda L: L.ecd_decode_attn_merged(8, 8, 8, 8, 8, 8, 8, 1, 1, 24, 7, 4096, 128, 4, 0.1, None),     # Hq % Hk
     lambda L: L.ecd_gemv_i8p_splitk(16, 64, 16, 16, None, 0, 16, 64, 1, 64, 192, 2, 16, 0, None),  # 3 chunks % 2
     lambda L: L.ecd_silu_mul(8, 8, 0, 8192, None),
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,

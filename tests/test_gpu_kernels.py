@@ -195,6 +195,53 @@ ATTN_CASES = [
 ]
 
 
+MERGED_CASES = [
+    # R, S, Hq, Hk, HD, L, kb (workgroups of 8 splits per (row, kv head))
+    (1, 1, 24, 8, 128, 4096, 32),  # one row: the engine's 32 workgroups per pair
+    (8, 1, 24, 8, 128, 4096, 4),   # batch 8 at the target length
+    (8, 1, 24, 8, 128, 750, 4),    # ragged positions: some workgroups see empty splits only
+    (2, 1, 24, 8, 128, 300, 3),
+    (4, 2, 8, 2, 128, 1024, 8),    # two rows per cache at consecutive positions
+    (2, 1, 8, 4, 384, 1000, 5),    # head_dim 384
+    (3, 1, 12, 4, 256, 700, 2),
+    (8, 1, 8, 1, 128, 512, 1),     # one workgroup per pair, 8 query heads per kv head
+]
+
+
+@pytest.mark.parametrize("R,S,Hq,Hk,HD,L,kb", MERGED_CASES)
+def test_decode_attn_merged(dev, R, S, Hq, Hk, HD, L, kb):
+    """The split attention and its merge in one launch (ecd_decode_attn_merged) against the
+    oracle's split attention with the same 8 kb splits and the exact softmax, twice in a row
+    (the second call on new queries): the pair counters are zero after each call."""
+    import torch
+    from estudiocanciones_amd import _ffi
+    B = R // S
+    kc = randn16(141, B, Hk, L, HD)
+    vc = randn16(142, B, Hk, L, HD)
+    g = rng(143)
+    if S == 1:
+        pos = g.integers(0, L, R).astype(np.int64)
+        pos[0] = L - 1
+    else:
+        pos = np.tile(np.arange(S, dtype=np.int64), B) + (L - S) // 2
+    kt, vt, pt = T(kc, dev), T(vc, dev), T(pos, dev)
+    G = Hq // Hk
+    ws = torch.full((R * Hk * kb * G * (2 + HD),), float("nan"), device=dev)
+    cnt = torch.zeros(R * Hk, dtype=torch.int32, device=dev)
+    for call in range(2):
+        q = randn16(140 + call, R, Hq * HD)
+        o = torch.empty(R, Hq * HD, dtype=torch.float16, device=dev)
+        _ffi.call("ecd_decode_attn_merged", T(q, dev).data_ptr(), kt.data_ptr(), vt.data_ptr(),
+                  pt.data_ptr(), o.data_ptr(), ws.data_ptr(), cnt.data_ptr(), R, S, Hq, Hk, L, HD,
+                  kb, 1.0 / math.sqrt(HD), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert int(cnt.abs().sum()) == 0, f"pair counters left at {cnt.tolist()}"
+        want = OK.decode_attn_out(q, kc, vc, pos, S, Hq, Hk, HD, nsplit=8 * kb)
+        assert_close16(N(o), want, what=f"merged attn R={R} L={L} HD={HD} kb={kb} call {call}")
+        exact = OK.attention_exact(q, kc, vc, pos, S, Hq, Hk, HD)
+        assert_close16(N(o), exact, what="merged attn vs exact softmax")
+
+
 @pytest.mark.parametrize("R,S,Hq,Hk,HD,L,ns", ATTN_CASES)
 def test_decode_attn(dev, R, S, Hq, Hk, HD, L, ns):
     import torch
