@@ -190,7 +190,7 @@ constexpr int NXA_G = 4;      // query heads per kv head at most
 constexpr int NXV_HD = 384;   // head_dim of the register form
 constexpr int NXV_SLOTS = 8;  // cache slots it holds (p < 8)
 constexpr int NXV_PAIRS = 8;  // pairs per take at most (waves 1 .. 8)
-constexpr int NXV_G = 4;      // query heads per kv head at most
+constexpr int NXV_G = 2;      // query heads per kv head (the reference decoder's 8 / 4)
 struct NextPass {
   const f16* rows;
   long rows_ld;
@@ -295,12 +295,49 @@ __device__ __forceinline__ void next_attention(const NextPass& nx, int tok, int 
   (void)aj;
 }
 
+// A D-wide fp16 row (D <= 512 SMP_RCH, a multiple of 8) copied by one wave: every load issued
+// before the first store (one memory round trip), 16 bytes per lane and chunk; zeros when
+// `valid` is false.
+constexpr int SMP_RCH = 6;  // 16-byte chunks per lane: rows up to 3072 wide
+__device__ __forceinline__ void row_load(f16x8 (&v)[SMP_RCH], const f16* src, int D, bool valid,
+                                         int lane) {
+#pragma unroll
+  for (int i = 0; i < SMP_RCH; ++i) {
+    const int c = 8 * lane + 512 * i;
+    v[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (valid && c < D) v[i] = *(const f16x8*)(src + c);
+  }
+}
+__device__ __forceinline__ void row_store(const f16x8 (&v)[SMP_RCH], f16* d0, f16* d1, int D,
+                                          int lane) {
+#pragma unroll
+  for (int i = 0; i < SMP_RCH; ++i) {
+    const int c = 8 * lane + 512 * i;
+    if (c < D) {
+      *(f16x8*)(d0 + c) = v[i];
+      if (d1) *(f16x8*)(d1 + c) = v[i];
+    }
+  }
+}
+
 // The register form's cached slots: lane l holds dims [HD / 64 l, HD / 64 (l + 1)) of slots
 // 0 .. NXV_SLOTS - 1 of K and V (the slots from p on are filled or masked later).
 template <int HD>
 struct NxvSlots {
   uint32_t k[NXV_SLOTS][HD / 128], v[NXV_SLOTS][HD / 128];
 };
+
+// A lane's HD / 64 halves (NW 32-bit words) of one row as one load (dwordx3 for head_dim 384):
+// one memory instruction per row instead of NW.
+template <int NW>
+__device__ __forceinline__ void ld_words(uint32_t (&w)[NW], const f16* p) {
+  struct Words {
+    uint32_t v[NW];
+  } t;
+  __builtin_memcpy(&t, p, sizeof(t));
+#pragma unroll
+  for (int i = 0; i < NW; ++i) w[i] = t.v[i];
+}
 
 // Pair (row, kv head) of the next pass's layer-0 attention in the register form, one wave, for
 // the sampled token tok: q of the pair's G heads and the new slot's k and v from the token's
@@ -332,15 +369,17 @@ __device__ __forceinline__ void next_attention_reg(const NextPass& nx, int tok, 
     kd[w] = kn[w];
     vd[w] = vn[w];
   }
+  // slot p takes the token's k and v: selects on values (a store at index p would move the
+  // slot registers to scratch memory)
+  uint32_t kw[NXV_SLOTS][NW], vw[NXV_SLOTS][NW];
 #pragma unroll
   for (int t = 0; t < NXV_SLOTS; ++t)
-    if (t == p)
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        sl.k[t][w] = kn[w];
-        sl.v[t][w] = vn[w];
-      }
-  short_attn_wave<HD, G, NXV_SLOTS>(sl.k, sl.v, qw, p + 1, nx.scale,
+    for (int w = 0; w < NW; ++w) {
+      kw[t][w] = t == p ? kn[w] : sl.k[t][w];
+      vw[t][w] = t == p ? vn[w] : sl.v[t][w];
+    }
+  short_attn_wave<HD, G, NXV_SLOTS>(kw, vw, qw, p + 1, nx.scale,
                                     nx.o + (long)row * nx.o_ld + (long)kh * G * HD + DPL * lane);
 }
 
@@ -420,24 +459,6 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
         }
       }
     }
-  } else {
-    constexpr int NW = XHD / 128;
-#pragma unroll
-    for (int t = 0; t < NXV_SLOTS; ++t)
-#pragma unroll
-      for (int w = 0; w < NW; ++w) sl.k[t][w] = sl.v[t][w] = 0u;
-    if (aj >= 0 && aj < npairs) {
-      const f16* kb = nx.kc + acache + (XHD / 64) * lane;
-      const f16* vb = nx.vc + acache + (XHD / 64) * lane;
-#pragma unroll
-      for (int t = 0; t < NXV_SLOTS; ++t)
-        if (t < nx.p)
-#pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            sl.k[t][w] = ((const uint32_t*)(kb + (long)t * XHD))[w];
-            sl.v[t][w] = ((const uint32_t*)(vb + (long)t * XHD))[w];
-          }
-    }
   }
 
   // 2. CFG mix in fp16, keys, and the block's largest key
@@ -459,6 +480,28 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
     kmx = max(kmx, key[j]);
   }
   kmx = wave_max_u32(kmx);
+  if constexpr (XHD == NXV_HD) {
+    // register form: the cached slots, once this wave's logits are in (issued earlier they would
+    // queue ahead of the block's logits loads).  Every slot register is loaded, from slot
+    // min(t, p - 1) (slot 0 when p = 0): no branch, so all the loads are in flight together;
+    // slot p takes the token's k and v later and the slots past it are masked.
+    constexpr int NW = XHD / 128;
+    if (aj >= 0 && aj < npairs) {
+      const f16* kb = nx.kc + acache + (XHD / 64) * lane;
+      const f16* vb = nx.vc + acache + (XHD / 64) * lane;
+      const int last = nx.p > 0 ? nx.p - 1 : 0;
+#pragma unroll
+      for (int t = 0; t < NXV_SLOTS; ++t) {
+        ld_words<NW>(sl.k[t], kb + (long)min(t, last) * XHD);
+        ld_words<NW>(sl.v[t], vb + (long)min(t, last) * XHD);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NXV_SLOTS; ++t)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sl.k[t][w] = sl.v[t][w] = 0u;
+    }
+  }
   if (lane == 0) wtot[wv] = kmx;
   for (int b = tid; b < SMP_WBINS_LDS / 4; b += SMP_THREADS)
     ((u32x4*)wbin)[b] = (u32x4){0u, 0u, 0u, 0u};
@@ -539,9 +582,9 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   if (wv != 0) {
     if (wv == SMP_THREADS / 64 - 1 && nx.ev) {  // the last wave: rows n (and n + N) of ev
       for (int h = 0; h < 1 + cfg_on; ++h) {
-        const f16* s = nx.ev + (long)(n + h * N) * nx.ev_ld;
-        f16* d = nx.xe + (long)(n + h * N) * nx.xe_ld;
-        for (int c = 8 * lane; c < nx.D; c += 512) *(f16x8*)(d + c) = *(const f16x8*)(s + c);
+        f16x8 v[SMP_RCH];
+        row_load(v, nx.ev + (long)(n + h * N) * nx.ev_ld, nx.D, true, lane);
+        row_store(v, nx.xe + (long)(n + h * N) * nx.xe_ld, nullptr, nx.D, lane);
       }
     }
     if (aj < npairs) {  // a pair wave: the token, then the pair's attention
@@ -550,12 +593,7 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
         next_attention(nx, s_tok, V, aj, arow, akh, acache, lane, a_k[aj], a_v[aj], a_q[aj],
                        a_pe[aj]);
       } else {
-        switch (nx.Hq / nx.Hk) {
-          case 1: next_attention_reg<XHD, 1>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
-          case 2: next_attention_reg<XHD, 2>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
-          case 3: next_attention_reg<XHD, 3>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
-          default: next_attention_reg<XHD, 4>(nx, s_tok, V, arow, akh, acache, lane, sl); break;
-        }
+        next_attention_reg<XHD, NXV_G>(nx, s_tok, V, arow, akh, acache, lane, sl);
       }
     }
     return;
@@ -616,15 +654,10 @@ __global__ __launch_bounds__(SMP_THREADS) void sample_topk_kernel(
   //    x rows n and n + N; zeros if no index won (NaN logits)
   if (nx.rows) {
     const bool valid = (uint32_t)bi < (uint32_t)V;
-    const f16* src = nx.rows + (long)(valid ? bi : 0) * nx.rows_ld;
-    f16* d0 = nx.x + (long)n * nx.x_ld;
-    f16* d1 = nx.x + (long)(n + N) * nx.x_ld;
-    for (int c = 8 * lane; c < nx.D; c += 512) {
-      f16x8 v = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (valid) v = *(const f16x8*)(src + c);
-      *(f16x8*)(d0 + c) = v;
-      if (cfg_on) *(f16x8*)(d1 + c) = v;
-    }
+    f16x8 v[SMP_RCH];
+    row_load(v, nx.rows + (long)(valid ? bi : 0) * nx.rows_ld, nx.D, valid, lane);
+    row_store(v, nx.x + (long)n * nx.x_ld, cfg_on ? nx.x + (long)(n + N) * nx.x_ld : nullptr,
+              nx.D, lane);
   }
 }
 
@@ -696,7 +729,8 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
                                     const void* ev, long ev_ld, void* xe, long xe_ld,
                                     void* stream) {
   const auto al = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
-  if (!rows || !x || rows_n < V || D <= 0 || (D % 8) || rows_ld < D || (rows_ld % 8) ||
+  if (!rows || !x || rows_n < V || D <= 0 || D > 512 * SMP_RCH || (D % 8) || rows_ld < D ||
+      (rows_ld % 8) ||
       x_ld < D || (x_ld % 8) || !al(rows) || !al(x))
     return ECD_EINVAL;
   if (!logits || !out || N <= 0 || V <= 0 || V > SMP_MAXV || ld < V || topk <= 0 || topk > V ||
@@ -709,7 +743,7 @@ extern "C" int ecd_sample_topk_next(const void* logits, long ld, int B, int N, f
     if (!lds_form && HD != NXV_HD) return ECD_EINVAL;
     const int nq = (Hq + 2 * Hk) * HD;
     if (!kc || !vc || !o || Hk <= 0 || Hq <= 0 || (Hq % Hk) ||
-        Hq / Hk > (lds_form ? NXA_G : NXV_G) ||
+        (lds_form ? Hq / Hk > NXA_G : Hq / Hk != NXV_G) ||
         (1 + cfg_on) * Hk > (lds_form ? NXA_PAIRS : NXV_PAIRS) || p < 0 || p >= L ||
         p >= (lds_form ? NXA_SLOTS : NXV_SLOTS) || qkv_n < V || qkv_ld < nq || (qkv_ld % 8) ||
         o_ld < Hq * HD || (o_ld % 8) || !al(qkv) || !al(kc) || !al(vc) || !al(o))

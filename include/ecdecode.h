@@ -153,7 +153,7 @@ int ecd_sample_topk(const void* logits, long ld, int B, int N, float cfg, float 
 /* ecd_sample_topk, then the next depth-decoder pass's input for each sampled token t of take n
  * (rows n and n + N with CFG):
  *  - x rows <- rows[t] from rows [rows_n >= V, D] f16 (row stride rows_ld), row stride x_ld;
- *    rows and x 16-byte aligned, D, rows_ld and x_ld multiples of 8;
+ *    rows and x 16-byte aligned, D (at most 3072), rows_ld and x_ld multiples of 8;
  *  - with qkv != NULL, that pass's layer 0 up to its attention output: q | k | v of t from
  *    qkv [qkv_n >= V, (Hq + 2 Hk) * HD] f16 (row stride qkv_ld; q heads, k heads, v heads,
  *    RoPE applied for slot p), k and v into slot p of the caches kc / vc [B, Hk, L, HD], and

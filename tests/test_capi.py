@@ -102,6 +102,11 @@ def _taps(*offsets):
     lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
                                      16, 3072, 8197, 16, 3072, 3072, 16, 12288, 8197, 16, 16, 8, 3,
                                      16, 3072, 8, 8, 384, None, 0, None, 0, None),  # 384: 2 x 8 pairs
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 3072, 8197, 16, 3072, 3072, 16, 4608, 8197, 16, 16, 8, 3,
+                                     16, 1536, 4, 4, 384, None, 0, None, 0, None),  # 384: G = 1
+    lambda L: L.ecd_sample_topk_next(16, 8256, 8, 4, 1.5, 1.0, 50, 8197, 16, None, None, 0, 16, 1,
+                                     16, 4096, 8197, 16, 4096, 4096, *_NOATT),      # D > 3072
     lambda L: L.ecd_embed_sum_i8(None, 8, 8, 65576, 8, 1, 8, 8, 8197, None),
     lambda L: L.ecd_embed_i8(8, 0, 8, 8, 65576, 0, 8197, None, 8, 1, 8, None),    # stride 0
     lambda L: L.ecd_embed_i8(8, 1, 8, 8, 0, 0, 8197, None, 8, 1, 8, None),        # rows 0

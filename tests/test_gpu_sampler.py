@@ -178,7 +178,7 @@ def test_sampler_next_rows(dev, N, cfg_on, philox):
     (4, True, 2, 8, 2, 128, 1024), (4, True, 7, 8, 2, 128, 1024), (3, False, 5, 8, 2, 128, 1024),
     # head_dim 384 (the reference decoder: 8 q / 4 kv heads, 3072 wide), register form
     (4, True, 2, 8, 4, 384, 3072), (4, True, 7, 8, 4, 384, 3072), (3, False, 4, 8, 4, 384, 3072),
-    (2, True, 6, 4, 4, 384, 3072)])
+    (2, True, 6, 4, 2, 384, 3072)])
 def test_sampler_next_layer0_attention(dev, N, cfg_on, p, Hq, Hk, HD, D):
     """ecd_sample_topk_next with the q|k|v rows: per sampled token, k and v land in cache slot p
     bit for bit (other slots untouched), and o is the decode attention over slots 0 .. p
