@@ -180,8 +180,8 @@ __device__ uint32_t select_full(const uint32_t (&key)[SMP_PER], const f16 (&lv)[
 //    slot p (precomputed per token, RoPE applied) -> the cache slot p of kc / vc, and the
 //    decode attention over slots 0 .. p (app/kernels.py:110-153: fp32 scores, exp, fp16 P,
 //    fp32 P V, o = acc / l) -> o rows.  One wave per (row, kv head) pair, its cached slots
-//    0 .. p - 1 loaded at kernel start, while the sampler runs: head_dim 128 into LDS (LDS DMA),
-//    head_dim 384 into the wave's registers (48 KB per pair would not fit beside the
+//    0 .. p - 1 loaded while the sampler runs: head_dim 128 into LDS (LDS DMA, at kernel start),
+//    head_dim 384 into the wave's registers (86 KB for 8 pairs would not fit beside the
 //    sampler's LDS), with the arithmetic of the standalone short-cache kernel.
 constexpr int NXA_HD = 128;   // head_dim of the LDS form
 constexpr int NXA_SLOTS = 16; // cache slots it reads at most (p < 16)
@@ -197,12 +197,12 @@ struct NextPass {
   f16* x;
   long x_ld;
   int D;
-  const f16* qkv;  // [>= V, (Hq + 2 Hk) * 128]: q heads | k heads | v heads per token
+  const f16* qkv;  // [>= V, (Hq + 2 Hk) * HD]: q heads | k heads | v heads per token
   long qkv_ld;
-  f16* kc;         // [B, Hk, L, 128]
+  f16* kc;         // [B, Hk, L, HD]
   f16* vc;
   int L, p;
-  f16* o;          // [B, Hq * 128]
+  f16* o;          // [B, Hq * HD]
   long o_ld;
   int Hq, Hk, HD;
   float scale;
