@@ -1,8 +1,7 @@
 // Layer tail of a decode stack as one persistent launch per layer (gfx950).
 //
-// One launch computes, for a few rows (M <= 8, or 16 on 1024-wide layers), what the reference
-// runs as five launches plus the next layer's first ones (app/engine.py:189-209; kernels
-// app/kernels.py:11-180):
+// One launch computes, for a few rows (M <= 16), what the reference runs as five launches plus
+// the next layer's first ones (app/engine.py:189-209; kernels app/kernels.py:11-180):
 //
 //   phase O    x1   = x + fp16(s_o * (W_o o))                      o-projection + residual
 //   phase W13  mm   = fp16(silu(a)) * b,  a | b = fp16(s * (W1|W3 rms(x1, n2)))
@@ -336,6 +335,33 @@ __device__ __forceinline__ void mfma_chunks(f32x4 (&acc)[NT], const u32x4 (&w)[N
     for (int t = 0; t < NT; ++t) {
       f16x8 wa, wb;
       i8x16_to_f16_biased(w[t][u], wa, wb);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, fb, acc[t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] -= corr;
+}
+
+// acc[t] += W_t x over the weight chunks [U0, U0 + CN) of this wave (w[t][U0 ..]), whose x
+// fragments sit at LDS chunks [c0, c0 + CN): mfma_chunks on part of the registers, no RMS.
+template <int NT, int C, int R, int U0, int CN>
+__device__ __forceinline__ void mfma_chunks_part(f32x4 (&acc)[NT], const u32x4 (&w)[NT][C],
+                                                 const unsigned char* xs, int c0, int lane) {
+  static_assert(U0 + CN <= C, "chunks within the registers");
+  const f16 kb = (f16)1152.0f;
+  const f16x8 bias = (f16x8){kb, kb, kb, kb, kb, kb, kb, kb};
+  f32x4 corr = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < CN; ++u) {
+    f16x8 fa, fb;
+    xfrag<R>(xs, c0 + u, lane, fa, fb);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fa, corr, 0, 0, 0);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(bias, fb, corr, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f16x8 wa, wb;
+      i8x16_to_f16_biased(w[t][U0 + u], wa, wb);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, fa, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, fb, acc[t], 0, 0, 0);
     }
@@ -991,9 +1017,16 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
   return ok;
 }
 
+// W2 phase rounds: a workgroup's K part of mm (C2 chunks per wave) is copied and multiplied in
+// two rounds of half the chunks where the whole part would take more than 128 KB of LDS (16-row
+// tiles of the 3072-wide layers: 256 KB)
+__host__ __device__ constexpr int w2_rounds(int C2, int R) {
+  return C2 * CW * chb(R) > 128 * 1024 ? 2 : 1;
+}
+
 // LDS map (bytes), per phase, for K = D columns: x tile [0, XD), norm weights [XD, XD + 2D),
-// row sums [XD + 2D, + 512), partials after that; for the W2 phase (K = F): x tile [0, XF),
-// partials [XF, XF + 8 KB).  A phase's partials never overlap its own x tile or norm weights
+// row sums [XD + 2D, + 512), partials after that; for the W2 phase (K = F): x tile [0, XF)
+// (one round's chunks), partials [XF, XF + 8 KB).  A phase's partials never overlap its own x tile or norm weights
 // (some waves still read those while others store partials); the next phase's x tile may
 // overlap them (the loader has read the partials before it releases the next phase).
 //
@@ -1006,6 +1039,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
   constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
   constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
+  constexpr int W2H = w2_rounds(C2, R), CH = C2 / W2H;  // W2 rounds, chunks per round
+  static_assert(C2 % W2H == 0, "whole chunks per round");
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NB = gridDim.x, b = blockIdx.x;
@@ -1035,7 +1070,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   unsigned char* nws = smem + XD;
   float* ss = (float*)(smem + XD + 2 * D);
   unsigned char* psD = smem + XD + 2 * D + 512;  // partials of the K = D phases
-  unsigned char* psF = smem + C2 * CW * chb(R);  // partials of the W2 phase
+  unsigned char* psF = smem + CH * CW * chb(R);  // partials of the W2 phase
 
   if (wv < CW) {
     // ------------------------------------------------------------------ compute waves
@@ -1109,12 +1144,25 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
 
       // phase W2 (x = mm)
       bar();  // X(W2): mm is complete
-      // the workgroup's K part of mm: chunks c0F .. of F, at LDS chunks wv * C2 ..
-      dma_rows<C2, R>(a.mm, F, M, c0F, xs + wv * C2 * chb(R), lane);
-      wait_vm0();
-      {
+      if constexpr (W2H == 1) {
+        // the workgroup's K part of mm: chunks c0F .. of F, at LDS chunks wv * C2 ..
+        dma_rows<C2, R>(a.mm, F, M, c0F, xs + wv * C2 * chb(R), lane);
+        wait_vm0();
         f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
         if (t2 >= 0) mfma_chunks<1, C2, R>(acc, w2, xs, nws, wv * C2, lane, 0.f, false);
+        put_partials<1>(psF, acc, wv, lane);
+      } else {
+        // in rounds of CH chunks through this wave's LDS chunks wv * CH ..: a round's copy goes
+        // out once the wave's LDS reads of the previous round are done (each wave reads only
+        // its own chunks, so no barrier between rounds)
+        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+        static_for<W2H>([&](auto hc) {
+          constexpr int h = decltype(hc)::value;
+          if constexpr (h > 0) wait_lgkm0();
+          dma_rows<CH, R>(a.mm, F, M, c0F + h * CH, xs + wv * CH * chb(R), lane);
+          wait_vm0();
+          if (t2 >= 0) mfma_chunks_part<1, C2, R, h * CH, CH>(acc, w2, xs, wv * CH, lane);
+        });
         put_partials<1>(psF, acc, wv, lane);
       }
       wait_lgkm0();
@@ -1398,7 +1446,7 @@ int device_cus() {
 
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS>
 int launch(const Args& a, int nb, hipStream_t st) {
-  const int xd = CD * CW * chb(R), xf = CF / KS2 * CW * chb(R);
+  const int xd = CD * CW * chb(R), xf = CF / KS2 / w2_rounds(CF / KS2, R) * CW * chb(R);
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   // attention: the waves' partials, then the merge's exchange
@@ -1424,13 +1472,15 @@ using namespace ecd;
 
 // Attention in the launch: (head_dim, query heads per kv head) instantiated, and the work split
 // fits the grid (long caches: NB / pairs workgroups per (row, kv head) pair).
-static bool tail_att_ok(int nb, int M, int Hq, int Hk, int HD, int L) {
+static bool tail_att_ok(int nb, int M, int D, int Hq, int Hk, int HD, int L) {
   if (Hk <= 0 || Hq % Hk) return false;
   const int G = Hq / Hk, pairs = M * Hk;
   // head_dim 128 with 3 or 4 query heads per kv head at any length; head_dim 384 with 2 (the
   // reference's depth decoder) on caches of at most VSHORT slots (the VALU path)
   if (!(HD == 128 && (G == 3 || G == 4)) && !(HD == 384 && G == 2 && L <= tail::VSHORT))
     return false;
+  // 3072-wide layers take more than 8 rows only as the reference decoder's first pass
+  if (D == 3072 && M > 8 && !(HD == 384 && G == 2 && L <= tail::VSHORT)) return false;
   if (L <= tail::ATT_SHORT) return pairs <= nb * tail::CW;
   // KB = nb / pairs workgroups per pair, each merging HD / KB columns
   const int kb = nb / pairs;
@@ -1462,7 +1512,7 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW;
   const int t13 = 2 * F / 16;
   if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb) return ECD_ENOTSUP;
-  if ((Hq + 2 * Hk) * HD / 16 > 2 * nb || !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
+  if ((Hq + 2 * Hk) * HD / 16 > 2 * nb || !tail_att_ok(nb, M, D, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
   const int ag = Hq / Hk;
@@ -1479,6 +1529,7 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   ECD_HEAD(6, 16, 4, 1, 128, 3, 8, false)
   ECD_HEAD(6, 16, 4, 1, 128, 3, 8, true)
   ECD_HEAD(6, 16, 4, 1, 384, 2, 8, true)
+  ECD_HEAD(6, 16, 4, 1, 384, 2, 16, true)
   ECD_HEAD(2, 16, 4, 4, 128, 4, 8, false)
   ECD_HEAD(2, 16, 4, 4, 128, 4, 8, true)
   ECD_HEAD(2, 16, 4, 4, 128, 4, 16, false)
@@ -1535,7 +1586,7 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   if (nb <= 0 || (nb % 8) || D / 16 > nb || t13 % nb)
     return ECD_ENOTSUP;
   if (wq && (Hq + 2 * Hk) * HD / 16 > 2 * nb) return ECD_ENOTSUP;
-  if (o_next && !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
+  if (o_next && !tail_att_ok(nb, M, D, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   const int nt13 = t13 / nb;
   // W2 has D / 16 tiles: with four times as many CUs, K is split over 4 workgroups per tile
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
@@ -1552,11 +1603,15 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
     return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, false, R_, VS_>(a, nb, st) \
                : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, false, R_, VS_>(a, nb, st);
   // 3072 -> 2 x 8192 -> 3072, up to 8 rows: the backbone (with its attention: 24q / 8kv,
-  // head_dim 128) and the reference's depth decoder (8q / 4kv, head_dim 384, caches of 8 slots)
+  // head_dim 128) and the reference's depth decoder (8q / 4kv, head_dim 384, caches of 8 slots);
+  // 16 rows (the reference decoder's first pass: two rows per cache) with the VALU attention
+  // or none
   ECD_TAIL(6, 16, 4, 1, 128, 3, 8, false)
   ECD_TAIL(6, 16, 4, 1, 128, 3, 8, true)
   ECD_TAIL(6, 16, 4, 1, 384, 2, 8, true)
   ECD_TAIL(6, 16, 4, 1, 0, 0, 8, false)
+  ECD_TAIL(6, 16, 4, 1, 384, 2, 16, true)
+  ECD_TAIL(6, 16, 4, 1, 0, 0, 16, false)
   // 1024 -> 2 x 8192 -> 1024: the 1024-wide depth decoder (8q / 2kv, head_dim 128), up to 16
   // rows (its first pass: two rows per cache)
   ECD_TAIL(2, 16, 4, 4, 128, 4, 8, false)
@@ -1580,11 +1635,11 @@ extern "C" int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int
   const int cd = D / 64 / tail::CW, cf = F / 64 / tail::CW, t13 = 2 * F / 16;
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
   if (D / 16 > nb || t13 % nb || cf != 16 || t13 / nb != 4 ||
-      !((cd == 6 && ks2 == 1 && M <= 8) || (cd == 2 && ks2 == 4)))
+      !((cd == 6 && ks2 == 1) || (cd == 2 && ks2 == 4)))
     return ECD_ENOTSUP;
   if (Hq <= 0 || Hk <= 0 || (Hq % Hk) || HD <= 0 || (HD % 4) || (Hq + 2 * Hk) * HD % 16 ||
       (Hq + 2 * Hk) * HD / 16 > 2 * nb)
     return ECD_ENOTSUP;
-  if (attention && !tail_att_ok(nb, M, Hq, Hk, HD, L)) return ECD_ENOTSUP;
+  if (attention && !tail_att_ok(nb, M, D, Hq, Hk, HD, L)) return ECD_ENOTSUP;
   return ECD_OK;
 }

@@ -845,8 +845,7 @@ class HeartMuLaLite:
         n = eos.numel()
         if any(vals[n:]):
             failed = [nm for nm, v in zip(("backbone", "decoder"), vals[n:]) if v]
-            self.backbone.tail_reset()
-            self.decoder.tail_reset()
+            self.tail_reset()
             self.release()
             raise RuntimeError(f"layer-tail launch of the {' and '.join(failed)} timed out at a "
                                "gate (its grid was not all resident); the song was stopped")
@@ -855,6 +854,12 @@ class HeartMuLaLite:
     def tail_error(self):
         """True if a layer-tail launch of either stack timed out since the last reset."""
         return self.backbone.tail_error() or self.decoder.tail_error()
+
+    def tail_reset(self):
+        """Zero both stacks' gate regions, workspaces and error words (their contents are
+        undefined after a timeout)."""
+        self.backbone.tail_reset()
+        self.decoder.tail_reset()
 
     def _advance(self, samples, st, P, n_frames):
         """Frame bookkeeping on the device: samples -> next input, frame stored, first EOS frame

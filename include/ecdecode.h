@@ -247,7 +247,7 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
                        const void* s, void* y, long ldy, int M, int N, int K, int flags,
                        void* stream);
 
-/* The tail of one decode layer plus the next layer's first steps, as ONE launch (M <= 8 rows):
+/* The tail of one decode layer plus the next layer's first steps, as ONE launch (M <= 16 rows):
  *   x1 = xin + int8_mm(o, wo, so)                      app/engine.py:206 (b.o with residual)
  *   mm = fp16(silu(a)) * b, a|b = int8_mm(rms(x1, n2), w13, s13)     :207-208 (krms, b.w13,
  *                                                                      _silu_mul)
@@ -256,9 +256,10 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  *   (:189-192): q [M, Hq*HD], k/v into kc/vc [B, Hk, L, HD] at pos (row m -> m / S); and, when
  *   o_next is not NULL, that layer's decode attention (ecd_decode_attn + ecd_attn_combine,
  *   :194-204, scale 1/sqrt(HD)) into o_next [M, Hq * HD] -- for head_dim 128 with 3 or 4 query
- *   heads per kv head (ecd_layer_tail_supported tells); with several rows per cache (S > 1)
- *   the rows of a cache hold consecutive positions p .. p + S - 1.  M <= 8 rows for the
- *   3072-wide shape, M <= 16 for the 1024-wide one (ecd_layer_tail_supported tells).
+ *   heads per kv head, or head_dim 384 with 2 on caches of at most 8 slots
+ *   (ecd_layer_tail_supported tells); with several rows per cache (S > 1) the rows of a cache
+ *   hold consecutive positions p .. p + S - 1.  M <= 16 rows; the 3072-wide shape takes more
+ *   than 8 rows with the head_dim-384 attention or none (the reference decoder's first pass).
  * Same numerics as the per-op entry points up to the fp32 summation order.  wo / w13 / w2 / wq
  * are ecd_pack_i8 copies (w13 interleaved, s13 interleaved the same way); o, xin, x1, mm,
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.

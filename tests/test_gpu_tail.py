@@ -228,15 +228,17 @@ def test_tail_timeout_sets_err_and_reset_recovers(dev, cfg, L):
     assert (err > bound).mean() <= 1e-3 and (err <= 3 * bound).all()
 
 
-@pytest.mark.parametrize("first", [True, False])
-def test_tail_two_rows_per_cache_vs_oracle(dev, first):
+@pytest.mark.parametrize("cfg,first", [(DEC3, True), (DEC3, False), (DEC_REF2, True),
+                                       (DEC_REF2, False)])
+def test_tail_two_rows_per_cache_vs_oracle(dev, cfg, first):
     """Two rows per cache (the depth decoder's first pass: S = 2, 2B rows at consecutive
     positions p, p + 1 of each cache) through the head launch and the 16-row tails: the output
     against the oracle's per-op composition and against the per-op kernels, and the slots each
-    layer's launch wrote."""
+    layer's launch wrote.  Both decoders: 1024 wide (head_dim 128) and the reference's 3072 wide
+    (head_dim 384, the W2 phase's 16-row tile in two rounds)."""
     import torch
-    cfg, B, L = DEC3, 8, 8
-    ost, st = _stacks(dev, cfg, seed=31 + int(first), B=B, L=L, stream=False)
+    B, L = 8, 8
+    ost, st = _stacks(dev, cfg, seed=31 + int(first) + cfg["dim"], B=B, L=L, stream=False)
     assert st.tail2 is not None and st.tail2["att"]
     _fill(ost, st, seed=32, upto=L)
     kv0 = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
