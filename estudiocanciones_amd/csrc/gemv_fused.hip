@@ -792,6 +792,16 @@ static Cfg pick_plain(int N, int K) {
   return c;
 }
 
+// RMS prologue with a plain store (the codebook heads: 8197 columns, 513 tiles): from 512 to 767
+// tiles, 3 tiles per workgroup, so that the busiest CU streams 3 tiles instead of 4 (171
+// workgroups instead of 129; two per CU for some would double their share).
+static Cfg pick_rms(int N, int K) {
+  Cfg c = pick(N, K);
+  const int ntiles = (N + 15) / 16;
+  if (ntiles >= 512 && ntiles < 768) c.nt = 3;
+  return c;
+}
+
 constexpr int LDS_MAX = 160 * 1024;
 
 template <int NT, int KW, int PRO, int EPI, bool NTL>
@@ -829,6 +839,7 @@ static int launch_ntl(const GemvArgs& a, Cfg c, hipStream_t st) {
   ECD_FCASE(1, 16)
   ECD_FCASE(2, 8)
   ECD_FCASE(2, 16)
+  ECD_FCASE(3, 8)
   ECD_FCASE(4, 8)
   ECD_FCASE(4, 16)
 #undef ECD_FCASE
@@ -941,7 +952,7 @@ int ecd_rms_gemv_i8p(const void* x, long ldx, const void* nw, float eps, const v
   if (check_common(a) || !x || !nw || !y || ldx < K || (ldx % 8) || !aligned16(x) ||
       !aligned16(nw) || ldy < N)
     return ECD_EINVAL;
-  return launch<PRO_RMS, EPI_STORE>(a, pick(N, K), (hipStream_t)stream);
+  return launch<PRO_RMS, EPI_STORE>(a, pick_rms(N, K), (hipStream_t)stream);
 }
 
 int ecd_rms_qkv_rope(const void* x, long ldx, const void* nw, float eps, const void* wp,

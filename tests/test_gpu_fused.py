@@ -67,10 +67,12 @@ def test_gemv_packed_every_tile_config_and_chunk_count(dev):
 
 
 @pytest.mark.parametrize("M,N,K", [(8, 8197, 1024), (8, 8197, 512), (16, 9000, 64), (20, 8197, 1024),
-                                   (8, 300, 1024)])
+                                   (8, 300, 1024), (8, 8197, 3072), (8, 11269, 3072),
+                                   (8, 12300, 1024)])
 def test_rms_gemv_packed_shapes(dev, M, N, K):
     """RMS prologue on the shapes that take the register-x kernel (8 waves, <= 2 chunks per
-    wave) and on those that stay on the LDS tile."""
+    wave) and on those that stay on the LDS tile; 513-767 tiles run 3 tiles per workgroup (the
+    codebook heads, and codebook 0's head with the decoder projection)."""
     from estudiocanciones_amd.kernels import pack_i8, rms_gemv_packed
     q, s = qweights(7 + K, N, K)
     x = randn16(8 + K, M, K, std=2.0)
