@@ -25,23 +25,31 @@ struct KVTile {
   f16x8 v[4][NDP];
 };
 
+template <bool NT>
+__device__ __forceinline__ f16x8 ld_kv8(const f16* p) {
+  if (NT) return __builtin_nontemporal_load((const f16x8*)p);
+  return *(const f16x8*)p;
+}
+
 // Loads the tile at t0 with token indices clamped to `lim` (any valid slot).  Tokens past the
 // attended range are masked by attn_run, so a tile may be loaded before that range is known.
-template <int HD>
+// NT: nontemporal loads (the slots are read once per step: they then do not displace what the
+// Infinity Cache holds for later launches).
+template <int HD, bool NT = false>
 __device__ __forceinline__ void kv_load(KVTile<HD>& t, const f16* __restrict__ kb,
                                         const f16* __restrict__ vb, int t0, int lim, int lane) {
   const int row = lane & 15;
   const int grp = lane >> 4;
   const f16* kp = kb + (long)min(t0 + row, lim) * HD + 8 * grp;
 #pragma unroll
-  for (int i = 0; i < KVTile<HD>::NKC; ++i) t.k[i] = *(const f16x8*)(kp + 32 * i);
+  for (int i = 0; i < KVTile<HD>::NKC; ++i) t.k[i] = ld_kv8<NT>(kp + 32 * i);
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) {
     const f16* vp = vb + (long)min(t0 + 4 * grp + rr, lim) * HD + 8 * row;
 #pragma unroll
     for (int j = 0; j < KVTile<HD>::NDP; ++j) {
       if (8 * (row + 16 * j) < HD)
-        t.v[rr][j] = *(const f16x8*)(vp + 128 * j);
+        t.v[rr][j] = ld_kv8<NT>(vp + 128 * j);
       else
         t.v[rr][j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
     }
@@ -257,8 +265,8 @@ __device__ __forceinline__ void attn_tile_m(SplitStateM<HD, G>& ss, float& m_run
 }
 
 // attn_run with the MFMA P V product (same ring of tiles; PRE: the first RING tiles already in
-// ring[0 .. RING - 1], else only ring[0]).
-template <int HD, int G, int RING, bool PRE = false>
+// ring[0 .. RING - 1], else only ring[0]; NT: the tiles it loads nontemporal).
+template <int HD, int G, int RING, bool PRE = false, bool NT = false>
 __device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (&qf)[HD / 32],
                                            KVTile<HD> (&ring)[RING], const f16* __restrict__ kb,
                                            const f16* __restrict__ vb, int lo, int hi, float scale,
@@ -273,14 +281,14 @@ __device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (
   const int ntiles = hi > lo ? (hi - lo + 15) / 16 : 0;
 #pragma unroll
   for (int r = 1; r < RING; ++r)
-    if (!PRE && r < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
+    if (!PRE && r < ntiles) kv_load<HD, NT>(ring[r], kb, vb, lo + 16 * r, hi - 1, lane);
   for (int base = 0; base < ntiles; base += RING) {
 #pragma unroll
     for (int r = 0; r < RING; ++r) {
       const int i = base + r;
       if (i < ntiles) {
         attn_tile_m<HD, G>(ss, m_run, l_run, qf, ring[r], lo + 16 * i, hi, scale, lane);
-        if (i + RING < ntiles) kv_load<HD>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
+        if (i + RING < ntiles) kv_load<HD, NT>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
       }
     }
   }

@@ -97,7 +97,7 @@ struct Args {
   f16* o_next;
   float scale;
   uint32_t* sync;  // 16 KB gate region, zero before the first launch
-  uint32_t* err;   // set to 1 when a gate wait times out
+  uint32_t* err;   // made nonzero when a wait times out (bit 0 and the wait's ERR_ bit)
   float* ws;       // workspace, zero before the first launch on `sync`: split-W2 partial sums
                    // [D / 16][KS2][64][4] (KS2 > 1), the attention's per-workgroup partials
                    // [NB][G][2 + HD] (long caches) and the q|k|v hand-off [MR][Hq + 2 Hk][HD],
@@ -144,6 +144,13 @@ __device__ __forceinline__ uint32_t add_agent(uint32_t* p) {
 }
 __device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Error word: bit 0 when any wait gave up, and one bit naming each wait that did.
+constexpr uint32_t ERR_GATE_A = 2, ERR_GATE_B = 4, ERR_GATE_C = 8, ERR_SPLIT_W2 = 16,
+                   ERR_HAND_VS = 32, ERR_HAND_Q = 64, ERR_NEW_SLOT = 128, ERR_MERGE = 256;
+__device__ __forceinline__ void flag_err(uint32_t* err, uint32_t sites) {
+  __hip_atomic_fetch_or(err, 1u | sites, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Tagged words: 32 bits of data (one fp32, or two fp16) and the launch's epoch in one 8-byte
@@ -515,7 +522,7 @@ struct AttPre {
 // write consecutive slots p0 .. p0 + S - 1 (p0 = the position of its first row), and every slot
 // below p0 is final before the launch: the split's cache part stops below p0, and its tokens
 // from p0 on come from the hand-off, so no line of a slot written here is read.
-template <int HD, int RING>
+template <int HD, int RING, bool KNT>
 __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int wv, int lane,
                                              AttPre<HD, RING>& pf) {
   const int Hk = a.Hk, L = a.L;
@@ -545,7 +552,17 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
   pf.nlo = max(pf.lo, pf.p0);
   pf.nhi = pf.hi;
   pf.hi = min(pf.hi, pf.p0);
-  if (pf.lo < pf.hi) kv_load<HD>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.hi - 1, lane);
+  // Nontemporal slot loads (the slots are read once per step): they then stream without
+  // displacing what the Infinity Cache holds for the frame's other launches.  Always with KNT
+  // (the caller's choice: the depth decoder's weights stay resident), else for splits of more
+  // than two tiles (caches of more than ~1000 slots); the two tiles of a short split load
+  // faster as plain loads
+  if (pf.lo < pf.hi) {
+    if (KNT || pf.hi - pf.lo > 32)
+      kv_load<HD, true>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.hi - 1, lane);
+    else
+      kv_load<HD, false>(pf.ring[0], a.kc + pf.cbase, a.vc + pf.cbase, pf.lo, pf.hi - 1, lane);
+  }
 }
 
 // load_q from the hand-off words (row r's q at ((r * NQ + head * HD + d) / 2), two fp16 each),
@@ -636,7 +653,7 @@ __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x
 // one per workgroup, and the pair's KB workgroups merge those (attention_merge).  Same
 // arithmetic as the split-combine kernel, summed in two levels.  q and the new K/V slots come
 // from the hand-off words of epoch `ep` (no gate after the q|k|v phase).
-template <int HD, int G, int RING>
+template <int HD, int G, int RING, bool KNT>
 __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
                                                 int lane, AttPre<HD, RING>& pf, uint32_t ep) {
   constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
@@ -651,12 +668,14 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   const int NQ = (Hq + 2 * a.Hk) * HD;
   const uint64_t* hw = (const uint64_t*)(a.ws + ws_hand_offset(a, gridDim.x));
   // splits of more than two tiles: the ring's other tiles go out before the q polls (the
-  // polls then wait behind them in the CU's queue, which pays only when the stream is long)
+  // polls then wait behind them in the CU's queue, which pays only when the stream is long),
+  // as nontemporal loads (as in att_prefetch)
   const int ntiles = pf.hi > pf.lo ? (pf.hi - pf.lo + 15) / 16 : 0;
   const bool early = ntiles > 2;
   if (early) {
 #pragma unroll
-    for (int r = 1; r < RING; ++r) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
+    for (int r = 1; r < RING; ++r)
+      kv_load<HD, true>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
   }
   // the split's new slots: slot t from row (cache's first row + t - p0); the first one's K and
   // V words go out with the q polls (one round trip)
@@ -673,23 +692,24 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
     nv = get_tagged(hv + lane);
   }
   f16x8 qf[HD / 32];
-  bool ok = load_q_hand<HD, G>(qf, hw, pf.r, NQ, pf.kh, ep, lane, a.spin_max);
+  uint32_t bad = load_q_hand<HD, G>(qf, hw, pf.r, NQ, pf.kh, ep, lane, a.spin_max) ? 0u : ERR_HAND_Q;
   if (!early) {
 #pragma unroll
     for (int r = 1; r < RING; ++r)
-      if (r < ntiles) kv_load<HD>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
+      if (r < ntiles) kv_load<HD, KNT>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
   }
   SplitStateM<HD, G> ss;
-  attn_run_m<HD, G, RING, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
+  attn_run_m<HD, G, RING, true, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
   for (int t = pf.nlo; t < pf.nhi; ++t) {
     if (t > pf.nlo) {
       hkv(t, hk, hv);
       nk = get_tagged(hk + lane);
       nv = get_tagged(hv + lane);
     }
-    ok = attn_new_slot<HD, G>(ss, qf, hk, hv, ep, t, a.scale, lane, a.spin_max, nk, nv) && ok;
+    if (!attn_new_slot<HD, G>(ss, qf, hk, hv, ep, t, a.scale, lane, a.spin_max, nk, nv))
+      bad |= ERR_NEW_SLOT;
   }
-  if (!ok && lane == 0) store_agent(a.err, 1u);
+  if (bad && lane == 0) flag_err(a.err, bad);
   if (a.L <= ATT_SHORT) {
     attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
     bar();  // P(ATT)
@@ -809,7 +829,7 @@ __device__ __forceinline__ void vattention_phase(const Args& a, int lane, VPre<H
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  if (!ok && lane == 0) store_agent(a.err, 1u);
+  if (!ok && lane == 0) flag_err(a.err, ERR_HAND_VS);
   // the new slots in place of the cached words read for them
 #pragma unroll
   for (int t = 0; t < VSHORT; ++t)
@@ -1033,7 +1053,8 @@ __host__ __device__ constexpr int w2_rounds(int C2, int R) {
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
+          bool KNT>
 __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
@@ -1189,7 +1210,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         if constexpr (AHD > 0 && VS) {
           if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
         } else if constexpr (AHD > 0) {
-          if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+          if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
         }
         wait_lgkm0();
         bar();  // X(QKV)
@@ -1200,7 +1221,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         if constexpr (AHD > 0 && VS) {
           if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
         } else if constexpr (AHD > 0) {
-          if (att) att_prefetch<AHD, ARING>(a, NB, b, wv, lane, pf);
+          if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
         }
         // phase QKV (x = rms(xout, n1'))
         bar();  // X(QKV): xout is complete
@@ -1224,7 +1245,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     if constexpr (AHD > 0 && VS) {
       if (att) vattention_phase<AHD, AG>(a, lane, vpf, s_epoch);
     } else if constexpr (AHD > 0) {
-      if (att) attention_phase<AHD, AG, ARING>(a, smem, wv, lane, pf, s_epoch);
+      if (att) attention_phase<AHD, AG, ARING, KNT>(a, smem, wv, lane, pf, s_epoch);
     }
     return;
   }
@@ -1235,7 +1256,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const bool mrow = me < M;
   const int grp = b & 7;
   const uint32_t per = (uint32_t)(NB >> 3);
-  bool ok = true;
+  uint32_t bad = 0;  // the waits that gave up (error-word bits)
   uint32_t go = 0;
   if (lane == 0) go = ld_sc1(a.sync + GATE_FLAGS + 32 * 8 * grp);  // (all flags equal here)
 
@@ -1282,7 +1303,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     }
     wait_vm0();
     if (lane == 0) gate_arrive(a.sync, grp, per, go);
-    ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+    if (!gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane))
+      bad |= ERR_GATE_A;
     ++go;
 
     // phase W13 (the W2 epilogue's residual x1 is final now: read it before the weight stream of
@@ -1311,7 +1333,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     }
     wait_vm0();
     if (lane == 0) gate_arrive(a.sync, grp, per, go);
-    ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+    if (!gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane))
+      bad |= ERR_GATE_B;
     ++go;
 
     // phase W2
@@ -1347,7 +1370,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
             if (__builtin_amdgcn_ballot_w64(!got) == 0 || it >= a.spin_max) break;
             __builtin_amdgcn_s_sleep(1);
           }
-          ok = ok && __builtin_amdgcn_ballot_w64(!got) == 0;
+          if (__builtin_amdgcn_ballot_w64(!got) != 0) bad |= ERR_SPLIT_W2;
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[e] += __builtin_bit_cast(float, (uint32_t)w[e]);
         }
@@ -1363,7 +1386,8 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       // which need no acknowledgement)
       if (KS2 == 1 || ks2 == 0) wait_vm0();
       if (lane == 0) gate_arrive(a.sync, grp, per, go);
-      ok = gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane) && ok;
+      if (!gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane))
+        bad |= ERR_GATE_C;
       ++go;
       if (lane == 0) s_epoch = go;
     } else {
@@ -1424,12 +1448,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       bar();  // X(ATT)
       bar();  // P(ATT)
       if constexpr (!VS)
-        ok = attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)) &&
-             ok;
+        if (!attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)))
+          bad |= ERR_MERGE;
     }
   }
 done:
-  if (lane == 0 && !ok) store_agent(a.err, 1u);
+  if (lane == 0 && bad) flag_err(a.err, bad);
 }
 
 int device_cus() {
@@ -1444,7 +1468,8 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
+          bool KNT = false>
 int launch(const Args& a, int nb, hipStream_t st) {
   const int xd = CD * CW * chb(R), xf = CF / KS2 / w2_rounds(CF / KS2, R) * CW * chb(R);
   const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
@@ -1456,12 +1481,12 @@ int launch(const Args& a, int nb, hipStream_t st) {
   // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
   static int attr = 0;
   if (lds > attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS>,
+    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return (int)e;
     attr = lds;
   }
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS>), dim3(nb), dim3(NTHR), lds, st, a);
+  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT>), dim3(nb), dim3(NTHR), lds, st, a);
   return ecd_launch_status();
 }
 
@@ -1520,12 +1545,17 @@ extern "C" int ecd_layer_head(const void* xin, const void* n1, const void* wq, c
   const bool ntl = (flags >> 1) & 1;
   const bool vs = L <= tail::VSHORT;  // the VALU attention path
   if (vs && S > tail::VNEW) return ECD_ENOTSUP;
+  const bool knt = (flags >> 3) & 1;  // nontemporal cache-slot loads for every split
   hipStream_t st = (hipStream_t)stream;
 #define ECD_HEAD(CD_, CF_, NT_, KS_, AHD_, AG_, R_, VS_)                                      \
   if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && HD == AHD_ && ag == AG_ &&       \
       rt == R_ && vs == VS_)                                                                  \
     return ntl ? tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, true, true, R_, VS_>(a, nb, st)  \
                : tail::launch<CD_, CF_, NT_, KS_, AHD_, AG_, false, true, R_, VS_>(a, nb, st);
+  if (knt && cd == 6 && cf == 16 && nt13 == 4 && ks2 == 1 && HD == 128 && ag == 3 && rt == 8 &&
+      !vs)
+    return ntl ? tail::launch<6, 16, 4, 1, 128, 3, true, true, 8, false, true>(a, nb, st)
+               : tail::launch<6, 16, 4, 1, 128, 3, false, true, 8, false, true>(a, nb, st);
   ECD_HEAD(6, 16, 4, 1, 128, 3, 8, false)
   ECD_HEAD(6, 16, 4, 1, 128, 3, 8, true)
   ECD_HEAD(6, 16, 4, 1, 384, 2, 8, true)
@@ -1596,7 +1626,12 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   const bool ntl = (flags >> 1) & 1;
   const bool vs = o_next && L <= tail::VSHORT;  // the VALU attention path
   if (vs && S > tail::VNEW) return ECD_ENOTSUP;
+  const bool knt = (flags >> 3) & 1;  // nontemporal cache-slot loads for every split
   hipStream_t st = (hipStream_t)stream;
+  if (knt && o_next && cd == 6 && cf == 16 && nt13 == 4 && ks2 == 1 && HD == 128 && ag == 3 &&
+      rt == 8 && !vs)
+    return ntl ? tail::launch<6, 16, 4, 1, 128, 3, true, false, 8, false, true>(a, nb, st)
+               : tail::launch<6, 16, 4, 1, 128, 3, false, false, 8, false, true>(a, nb, st);
 #define ECD_TAIL(CD_, CF_, NT_, KS_, AHD_, AG_, R_, VS_)                                      \
   if (cd == CD_ && cf == CF_ && nt13 == NT_ && ks2 == KS_ && (o_next ? HD : 0) == AHD_ &&      \
       ag == AG_ && rt == R_ && vs == VS_)                                                     \

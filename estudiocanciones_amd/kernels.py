@@ -580,7 +580,7 @@ def layer_tail_ws_bytes(D, Hq, Hk, HD):
 
 
 def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws, nxt=None,
-               o_next=None, eps=1e-5, stream=False, no_wait=False):
+               o_next=None, eps=1e-5, stream=False, no_wait=False, kv_nt=False):
     """One launch for the tail of a decode layer (app/engine.py:206-210: O projection +
     residual, rms -> w1|w3 -> SiLU * mul, w2 + residual) and, with ``nxt``, the next layer's
     rms -> q|k|v -> RoPE -> q, cache slot (:189-192) and, with ``o_next`` [M, Hq * HD], that
@@ -590,7 +590,9 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
     first use) and ``err`` (int32 [1]) persist between calls; ``ws``: float32 workspace of
     layer_tail_ws_bytes bytes, zero before first use and kept with its ``sync`` (partials are
     recognised by the sync region's gate count).  ``no_wait``: every wait gives up at once (tests
-    of the error path: err becomes 1 and sync, ws and err must be zeroed before the next call)."""
+    of the error path: err becomes 1 and sync, ws and err must be zeroed before the next call).
+    ``kv_nt``: the attention reads every cache slot with nontemporal loads (else only splits of
+    more than 32 slots), for callers whose other data should stay in the Infinity Cache."""
     dev = _dev(o, "layer_tail")
     M, D = o.shape
     F = mm.shape[1]
@@ -640,16 +642,17 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
               _ptr(o_next), x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(),
               err.data_ptr(),
               ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
-              _flags(M, stream) | (4 if no_wait else 0), stream_ptr(dev))
+              _flags(M, stream) | (4 if no_wait else 0) | (8 if kv_nt else 0), stream_ptr(dev))
     return xout
 
 
-def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait=False):
+def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait=False,
+               kv_nt=False):
     """A stack's first layer up to its attention as one launch (app/engine.py:189-204 for layer
     0): rms(x, n1) -> q|k|v -> RoPE -> q and the cache slot, and the decode attention into
     o_next [M, Hq * HD].  ``nxt`` as for layer_tail (that layer's n1, wq, ..., S = 1); F: the
-    stack's FFN width; sync, err, ws: the stack's layer_tail buffers; ``no_wait`` as for
-    layer_tail."""
+    stack's FFN width; sync, err, ws: the stack's layer_tail buffers; ``no_wait`` and
+    ``kv_nt`` as for layer_tail."""
     dev = _dev(x, "layer_head")
     M, D = x.shape
     _f16(x, "layer_head x")
@@ -680,7 +683,7 @@ def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait
               n["sq"].data_ptr(), n["rope"].data_ptr(), pos.data_ptr(), n["q"].data_ptr(),
               kc.data_ptr(), n["vc"].data_ptr(), o_next.data_ptr(), sync.data_ptr(),
               err.data_ptr(), ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
-              _flags(M, stream) | (4 if no_wait else 0), stream_ptr(dev))
+              _flags(M, stream) | (4 if no_wait else 0) | (8 if kv_nt else 0), stream_ptr(dev))
     return o_next
 
 

@@ -265,15 +265,19 @@ int ecd_embed_gemv_i8p(const int64_t* tok, long tok_stride, const void* table, c
  * xout, o_next 16-byte aligned, row stride D (mm: F).  xout must not alias xin, o, x1 or mm.
  * sync: a 16 KB, 256-byte aligned region, zero before the first call, kept for later calls (the
  * kernel leaves it reusable); calls sharing a sync region must not overlap in time.  err: a
- * 4-byte word set to 1 if a workgroup waited longer than its bound for the others (results, sync
- * and ws then undefined: zero sync, ws and err before the next call).  ws: a 16-byte aligned
+ * 4-byte word made nonzero if a workgroup waited longer than its bound for the others (bit 0,
+ * plus one bit per wait that gave up: 2 / 4 / 8 the three gates, 16 the split-W2 parts, 32 / 64
+ * the q|k|v hand-off of the VALU / MFMA attention, 128 a new cache slot, 256 the attention
+ * merge; results, sync and ws then undefined: zero sync, ws and err before the next call).
+ * ws: a 16-byte aligned
  * workspace of ecd_layer_tail_ws_bytes bytes, zero before the first call and kept with its sync
  * region (a launch recognises its split-W2 parts and attention partials by the region's gate
- * count; calls on
- * another sync region must use another ws).  The grid is one workgroup per CU with all
- * workgroups resident.  flags bit 1: nontemporal weight loads; bit 2: no waiting at all (every
- * wait gives up at its first look: tests of the error path).  No reference counterpart as one
- * call: it replaces up to seven reference launches. */
+ * count; calls on another sync region must use another ws).  The grid is one workgroup per CU
+ * with all workgroups resident.  flags bit 1: nontemporal weight loads; bit 2: no waiting at all
+ * (every wait gives up at its first look: tests of the error path); bit 3: nontemporal
+ * cache-slot loads for every attention split (without it only splits of more than 32 slots
+ * load nontemporal; honoured for head_dim 128 with 3 query heads per kv head, 8 rows).  No
+ * reference counterpart as one call: it replaces up to seven reference launches. */
 int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* so,
                    const void* n2, const void* w13, const void* s13, const void* w2,
                    const void* s2, const void* n1, const void* wq, const void* sq,
@@ -289,9 +293,9 @@ int ecd_layer_tail(const void* o, const void* xin, const void* wo, const void* s
  * ecd_rms_qkv_rope + ecd_decode_attn (+ ecd_attn_combine) for the shapes
  * ecd_layer_tail_supported(M, D, F, Hq, Hk, HD, L, 1) accepts (S > 1: the rows of a cache hold
  * consecutive positions, as for ecd_layer_tail); F is
- * the stack's FFN width (the launch shape).  sync, err and ws as for ecd_layer_tail, shared
- * with the stack's ecd_layer_tail calls (the launch moves the gate count on by one).  No
- * reference counterpart as one call. */
+ * the stack's FFN width (the launch shape).  sync, err, ws and flags as for ecd_layer_tail,
+ * sync, err and ws shared with the stack's ecd_layer_tail calls (the launch moves the gate count
+ * on by one).  No reference counterpart as one call. */
 int ecd_layer_head(const void* xin, const void* n1, const void* wq, const void* sq,
                    const float* rope, const int64_t* pos, void* q, void* kc, void* vc,
                    void* o_next, void* sync, void* err, void* ws, int M, int D, int F, int S,

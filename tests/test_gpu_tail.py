@@ -81,19 +81,21 @@ DEC3 = dict(layers=3, heads=8, kv_heads=2, max_seq=2048, dim=1024, ffn=8192)
 DEC_REF2 = dict(layers=2, heads=8, kv_heads=4, max_seq=2048, dim=3072, ffn=8192)
 
 
-@pytest.mark.parametrize("cfg,B,L,pos_kind,stream", [
-    (BB3, 8, 1024, "spread", True),    # backbone shape, 8 rows, positions 0 .. L - 1
-    (BB3, 2, 1024, "last", True),      # the C0 rows
-    (BB3, 8, 4096, "last", True),      # long splits: the new slot in a split's ninth tile
-    (DEC3, 8, 8, "spread", False),     # 1024-wide decoder, per-frame cache of 8 slots
-    (DEC_REF2, 8, 8, "last", False),   # the reference's decoder: 3072 wide, head_dim 384
-    (DEC_REF2, 8, 8, "spread", False),
-    (BB3, 8, 8, "spread", False),      # backbone shape over an 8-slot cache (VALU attention)
+@pytest.mark.parametrize("cfg,B,L,pos_kind,stream,kv_nt", [
+    (BB3, 8, 1024, "spread", True, False),  # backbone shape, 8 rows, positions 0 .. L - 1
+    (BB3, 8, 1024, "spread", True, True),   # the same, every cache slot read nontemporal
+    (BB3, 2, 1024, "last", True, False),    # the C0 rows
+    (BB3, 8, 4096, "last", True, False),    # long splits: the new slot in a split's ninth tile
+    (DEC3, 8, 8, "spread", False, False),   # 1024-wide decoder, per-frame cache of 8 slots
+    (DEC_REF2, 8, 8, "last", False, False),  # the reference's decoder: 3072 wide, head_dim 384
+    (DEC_REF2, 8, 8, "spread", False, False),
+    (BB3, 8, 8, "spread", False, False),    # backbone shape over an 8-slot cache (VALU attention)
 ])
-def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream):
+def test_tail_stack_vs_oracle(dev, cfg, B, L, pos_kind, stream, kv_nt):
     import torch
     from estudiocanciones_amd.kernels import layer_tail_supported
     ost, st = _stacks(dev, cfg, seed=cfg["dim"] + B, B=B, L=L, stream=stream)
+    st.tail_kv_nt = kv_nt
     hd = cfg["dim"] // cfg["heads"]
     assert layer_tail_supported(B, cfg["dim"], cfg["ffn"], cfg["heads"], cfg["kv_heads"], hd)
     assert st.tail is not None
@@ -216,7 +218,9 @@ def test_tail_timeout_sets_err_and_reset_recovers(dev, cfg, L):
     st.tail_no_wait = True
     st.decode(x, pos, 1)
     torch.cuda.synchronize()
-    assert st.tail_error()
+    e = st.tail_error()
+    # bit 0 and the bits of the waits that gave up (gates, parts, hand-off, slots, merge)
+    assert e & 1 and e & 0x1FE and not e & ~0x1FF, hex(e)
     st.tail_no_wait = False
     st.tail_reset()
     reset()
