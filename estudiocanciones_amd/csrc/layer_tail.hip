@@ -173,6 +173,16 @@ __device__ __forceinline__ long ws_hand_offset(const Args& a, int NB) {
   return ws_att_offset(a.D) + (long)NB * (a.Hq / a.Hk) * (2 + a.HD) * 2;
 }
 
+// Pause between two looks of a poll: short while a wait is young (a gate resolves within a few
+// microseconds), longer once it has lasted ~100 us, so that waiters of a late workgroup do not
+// keep the lines its own stores and atomics go to busy with their reads.
+__device__ __forceinline__ void poll_pause(int it) {
+  if (it < 256)
+    __builtin_amdgcn_s_sleep(1);
+  else
+    __builtin_amdgcn_s_sleep(32);
+}
+
 // Gate words (a 16 KB region): [64 (1 + g)] arrivals of group g's workgroups; flag word
 // [GATE_FLAGS + 32 (8 x + g)] the done flag of group g as read by group x, one word alone in
 // its 128-byte line, so that every line of the region has a single writer (the last arriver of
@@ -200,7 +210,7 @@ __device__ __forceinline__ bool gate_wait(const uint32_t* sync, int grp, uint32_
     const bool done = lane >= 8 || (int32_t)(ld_sc1(f) - (go + 1u)) >= 0;
     if (__builtin_amdgcn_ballot_w64(!done) == 0) return true;
     if (it >= spin_max) return false;
-    __builtin_amdgcn_s_sleep(1);
+    poll_pause(it);
   }
 }
 
@@ -592,7 +602,7 @@ __device__ __forceinline__ bool load_q_hand(f16x8 (&qf)[HD / 32], const uint64_t
       ok = false;
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    poll_pause(it);
   }
 #pragma unroll
   for (int i = 0; i < HD / 32; ++i)
@@ -619,7 +629,7 @@ __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x
       ok = false;
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    poll_pause(it);
     wk = get_tagged(hk + lane);
     wv = get_tagged(hv + lane);
   }
@@ -827,7 +837,7 @@ __device__ __forceinline__ void vattention_phase(const Args& a, int lane, VPre<H
       ok = false;
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    poll_pause(it);
   }
   if (!ok && lane == 0) flag_err(a.err, ERR_HAND_VS);
   // the new slots in place of the cached words read for them
@@ -1009,7 +1019,7 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
       ok = false;
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
+    poll_pause(it);
   }
   // exchange through LDS after the waves' partials (one wave: LDS accesses stay in order)
   float* sv = (float*)smem + CW * G * PW;  // [KB][G][cw]
@@ -1368,7 +1378,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
             for (int e = 0; e < 4; ++e) w[e] = get_tagged(wt + k * 256 + e);
             got = tag_is(w[0], ep2) && tag_is(w[1], ep2) && tag_is(w[2], ep2) && tag_is(w[3], ep2);
             if (__builtin_amdgcn_ballot_w64(!got) == 0 || it >= a.spin_max) break;
-            __builtin_amdgcn_s_sleep(1);
+            poll_pause(it);
           }
           if (__builtin_amdgcn_ballot_w64(!got) != 0) bad |= ERR_SPLIT_W2;
 #pragma unroll
