@@ -264,13 +264,24 @@ __device__ __forceinline__ void attn_tile_m(SplitStateM<HD, G>& ss, float& m_run
     }
 }
 
+// A tile staged in LDS in kv_load's register order (16 bytes of lane l at src + 1024 j + 16 l:
+// K fragments j < 4, V rows j - 4) back into registers (head_dim 128).
+__device__ __forceinline__ void kv_unstage(KVTile<128>& t, const unsigned char* src, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t.k[i] = *(const f16x8*)(src + 1024 * i + 16 * lane);
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) t.v[rr][0] = *(const f16x8*)(src + 1024 * (4 + rr) + 16 * lane);
+}
+
 // attn_run with the MFMA P V product (same ring of tiles; PRE: the first RING tiles already in
-// ring[0 .. RING - 1], else only ring[0]; NT: the tiles it loads nontemporal).
-template <int HD, int G, int RING, bool PRE = false, bool NT = false>
+// ring[0 .. RING - 1], else only ring[0]; NT: the tiles it loads nontemporal; STG with lt set:
+// tile 2 was staged in LDS at lt and is read from there into its ring slot instead of loaded).
+template <int HD, int G, int RING, bool PRE = false, bool NT = false, bool STG = false>
 __device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (&qf)[HD / 32],
                                            KVTile<HD> (&ring)[RING], const f16* __restrict__ kb,
                                            const f16* __restrict__ vb, int lo, int hi, float scale,
-                                           int lane) {
+                                           int lane, const unsigned char* lt = nullptr) {
+  static_assert(!STG || (HD == 128 && RING == 2), "staged tile: head_dim 128, two-tile ring");
   constexpr int NDP = SplitStateM<HD, G>::NDP;
   float m_run = -INFINITY;
   float l_run = 0.f;
@@ -287,8 +298,12 @@ __device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (
     for (int r = 0; r < RING; ++r) {
       const int i = base + r;
       if (i < ntiles) {
+        if constexpr (STG) {
+          if (lt && i == 2) kv_unstage(*(KVTile<128>*)&ring[r], lt, lane);
+        }
         attn_tile_m<HD, G>(ss, m_run, l_run, qf, ring[r], lo + 16 * i, hi, scale, lane);
-        if (i + RING < ntiles) kv_load<HD, NT>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
+        if (i + RING < ntiles && !(STG && lt && i + RING == 2))
+          kv_load<HD, NT>(ring[r], kb, vb, lo + 16 * (i + RING), hi - 1, lane);
       }
     }
   }

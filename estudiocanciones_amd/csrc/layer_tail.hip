@@ -525,6 +525,7 @@ struct AttPre {
   int p0;        // the cache's first slot written in this launch (L: none)
   int nlo, nhi;  // the split's tokens written in this launch, taken from the hand-off
   bool on;       // this wave runs a split
+  bool staged;   // its third tile is copied into the wave's LDS slot (kv_stage)
 };
 
 // Split of this wave -- short caches: pair b + NB * wave, one split; long caches: pair and part
@@ -550,6 +551,7 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
     sp = kq * CW + wv;
   }
   pf.on = p < pairs;
+  pf.staged = false;
   pf.lo = pf.hi = pf.nlo = pf.nhi = 0;
   if (!pf.on) return;
   pf.r = p / Hk;
@@ -575,6 +577,62 @@ __device__ __forceinline__ void att_prefetch(const Args& a, int NB, int b, int w
   }
 }
 
+// LDS slot (8 KB) of wave w's staged K/V tile: after the q|k|v phase's map (x tile, norm
+// weights, row sums, the partials of two tiles) up to the W2 phase's x tile, then after the W2
+// phase's partials.  Nothing else uses these bytes from the q|k|v phase to the attention's end.
+template <int CD, int R, int CH>
+__device__ __forceinline__ int stage_slot(int w) {
+  constexpr int s0 = CD * CW * chb(R) + 2 * 64 * CD * CW + 512 + CW * 2 * 1024;
+  constexpr int e0 = CH * CW * chb(R);
+  constexpr int n0 = e0 > s0 ? (e0 - s0) / 8192 : 0;
+  constexpr int s1 = e0 + CW * 1024;
+  return w < n0 ? s0 + 8192 * w : s1 + 8192 * (w - n0);
+}
+template <int CD, int R, int CH>
+constexpr int stage_end() {
+  constexpr int s0 = CD * CW * chb(R) + 2 * 64 * CD * CW + 512 + CW * 2 * 1024;
+  constexpr int e0 = CH * CW * chb(R);
+  constexpr int n0 = e0 > s0 ? (e0 - s0) / 8192 : 0;
+  return n0 >= CW ? s0 + 8192 * CW : e0 + CW * 1024 + 8192 * (CW - n0);
+}
+
+// One LDS DMA of 16 bytes per lane, nontemporal (lds_dma16 with the nt bit).
+__device__ __forceinline__ void lds_dma16_nt(const void* base, uint32_t off, void* dst) {
+  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2 nt\n\ts_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(la) : "memory");
+}
+
+// A wave-uniform pointer in scalar registers (the LDS DMA takes its base there).  readfirstlane
+// returns a signed int: each half goes through uint32_t before widening, or a low half with its
+// top bit set would sign-extend over the high half.
+__device__ __forceinline__ const f16* uniform_ptr(const f16* p) {
+  const uint64_t u = (uint64_t)p;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+  return (const f16*)(((uint64_t)hi << 32) | (uint64_t)lo);
+}
+
+// The split's tile at t0 (tokens clamped to lim) into this wave's LDS slot dst, in kv_load's
+// register order: DMA instruction j moves lane l's 16 bytes to dst + 1024 j + 16 l (the K
+// fragments for j < 4, V rows j - 4 after them); kv_unstage (attn_core.h) reads them back.  The
+// slots are read once per step: nontemporal.
+__device__ __forceinline__ void kv_stage(const f16* kb, const f16* vb, int t0, int lim, int lane,
+                                         unsigned char* dst) {
+  constexpr int HD = 128;
+  const int row = lane & 15, grp = lane >> 4;
+  const f16* k0 = uniform_ptr(kb);
+  const f16* v0 = uniform_ptr(vb);
+  const uint32_t ko = (uint32_t)(((long)min(t0 + row, lim) * HD + 8 * grp) * 2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lds_dma16_nt(k0, ko + 64 * i, dst + 1024 * i);
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr)
+    lds_dma16_nt(v0, (uint32_t)(((long)min(t0 + 4 * grp + rr, lim) * HD + 8 * row) * 2),
+                 dst + 1024 * (4 + rr));
+}
 // load_q from the hand-off words (row r's q at ((r * NQ + head * HD + d) / 2), two fp16 each),
 // polled until every word this lane needs carries the epoch (bounded by spin_max).
 template <int HD, int G>
@@ -665,7 +723,8 @@ __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x
 // from the hand-off words of epoch `ep` (no gate after the q|k|v phase).
 template <int HD, int G, int RING, bool KNT>
 __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
-                                                int lane, AttPre<HD, RING>& pf, uint32_t ep) {
+                                                int lane, AttPre<HD, RING>& pf, uint32_t ep,
+                                                const unsigned char* lt) {
   constexpr int PW = 2 + HD;  // floats per head of a partial: m, l, acc[HD]
   const int Hq = a.Hq;
   bar();  // X(ATT): the loader has read the q|k|v partials (LDS is free)
@@ -709,7 +768,9 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
       if (r < ntiles) kv_load<HD, KNT>(pf.ring[r], kb, vb, pf.lo + 16 * r, pf.hi - 1, lane);
   }
   SplitStateM<HD, G> ss;
-  attn_run_m<HD, G, RING, true, true>(ss, qf, pf.ring, kb, vb, pf.lo, pf.hi, a.scale, lane);
+  attn_run_m<HD, G, RING, true, true, HD == 128 && RING == 2>(ss, qf, pf.ring, kb, vb, pf.lo,
+                                                             pf.hi, a.scale, lane,
+                                                             pf.staged ? lt : nullptr);
   for (int t = pf.nlo; t < pf.nhi; ++t) {
     if (t > pf.nlo) {
       hkv(t, hk, hv);
@@ -1110,6 +1171,18 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     // tiled (MFMA) splits, or the VALU path for caches of at most VSHORT slots (VS)
     AttPre<(AHD > 0 && !VS ? AHD : 32), ARING> pf;
     VPre<(AHD > 0 && VS ? AHD : 128)> vpf;
+    // long splits (more than two tiles) of the 8-row MFMA attention: the third tile goes into
+    // an LDS slot of the wave during the q|k|v phase, so that it has arrived when q is seen
+    constexpr bool STAGE = AHD == 128 && !VS && ARING == 2 && R == 8;
+    unsigned char* lt = smem + stage_slot<CD, R, CH>(wv);
+    auto stage = [&]() {
+      if constexpr (STAGE) {
+        if (att && pf.on && pf.hi - pf.lo > 32) {
+          pf.staged = true;
+          kv_stage(a.kc + pf.cbase, a.vc + pf.cbase, pf.lo + 32, pf.hi - 1, lane, lt);
+        }
+      }
+    };
     const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
     u32x4 wq[2][CD];
     const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
@@ -1221,6 +1294,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
           if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
         } else if constexpr (AHD > 0) {
           if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
+          stage();
         }
         wait_lgkm0();
         bar();  // X(QKV)
@@ -1238,6 +1312,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         dma_rows<CD, R>(a.xout, D, M, c0D, xs + c0D * chb(R), lane);
         dma_nw<CD>(a.n1, c0D, nws, lane);
         wait_vm0();
+        stage();
         rms_partial<CD, R>(xs, c0D, lane, wv, ss);
         wait_lgkm0();
       }
@@ -1255,7 +1330,7 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
     if constexpr (AHD > 0 && VS) {
       if (att) vattention_phase<AHD, AG>(a, lane, vpf, s_epoch);
     } else if constexpr (AHD > 0) {
-      if (att) attention_phase<AHD, AG, ARING, KNT>(a, smem, wv, lane, pf, s_epoch);
+      if (att) attention_phase<AHD, AG, ARING, KNT>(a, smem, wv, lane, pf, s_epoch, lt);
     }
     return;
   }
@@ -1488,6 +1563,10 @@ int launch(const Args& a, int nb, hipStream_t st) {
   const int ldsA = AHD > 0 && !VS ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
   int lds = ldsD > ldsF ? ldsD : ldsF;
   if (lds < ldsA) lds = ldsA;
+  // the staged K/V tiles of long attention splits (8-row MFMA attention)
+  constexpr int C2 = CF / KS2, CH = C2 / w2_rounds(C2, R);
+  constexpr int lde = AHD == 128 && !VS && AG <= 3 && R == 8 ? stage_end<CD, R, CH>() : 0;
+  if (lds < lde) lds = lde;
   // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
   static int attr = 0;
   if (lds > attr) {
