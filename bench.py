@@ -135,7 +135,7 @@ def is_backbone_tail(name):
     """rocprofv3 kernel name (demangled or not) of the backbone's layer-tail kernel (CD = 6: the
     frame's 28 tail launches), not its head launch (the HEAD template argument true)."""
     import re
-    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false, \d+(, (true|false))?>",
+    return bool(re.search(r"layer_tail_kernel<6, (\d+, ){5}(true|false), false, \d+(, (true|false)){0,2}>",
                           name)
                 or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0ELi\d+E", name))
 
@@ -392,8 +392,10 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
 
     g_ms_launch = time_graph([relaunch(n, a) for n, a, _ in gemv_calls], torch)
     g_ms_total = g_ms_launch * len(gemv_calls)
-    # the dominant kernel: the backbone's layer-tail launches (width 3072), all of one shape
-    bt = [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_tail" and a[25] == 3072]
+    # the dominant kernel: the backbone's layer-tail launches (recognised by their O-projection
+    # weights: the reference decoder's tails are 3072 wide too), all of one shape
+    bb_wo = {b.o.qp.data_ptr() for b in model.backbone.blocks}
+    bt = [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_tail" and a[2] in bb_wo]
     bt_ms = time_graph([relaunch(n, a) for n, a, _ in bt], torch) if bt else None
     bt_bytes = sum(b for _, _, b in bt) / len(bt) if bt else None
     bt_att = bool(bt) and bool(bt[0][1][17])
