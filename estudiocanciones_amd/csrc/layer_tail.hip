@@ -1154,8 +1154,13 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const int ks2 = KS2 == 1 ? 0 : b % KS2;
   const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
   const int xtra = TQ - NB;
-  const int tq0 = b < TQ ? b : -1;
-  const int tq1 = (xtra > 0 && b >= NB - xtra) ? NB + (b - (NB - xtra)) : -1;
+  // The two 16-column tiles whose hand-off words share a 128-byte line (tiles 2j, 2j + 1) go to
+  // workgroups 8 apart, i.e. to one XCD: no line is written in pieces from two XCDs, which
+  // agent-scope loads could read stale.  A permutation within each aligned block of 16.
+  auto paired = [](int i) { return (i & ~15) + 2 * (i & 7) + ((i >> 3) & 1); };
+  const int tq0 = b < TQ ? (b < (TQ & ~15) ? paired(b) : b) : -1;
+  const int xb = b - (NB - xtra);  // this workgroup's index among those with a second tile
+  const int tq1 = (xtra > 0 && xb >= 0) ? NB + (xb < (xtra & ~15) ? paired(xb) : xb) : -1;
 
   const int XD = nchD * chb(R);
   unsigned char* xs = smem;
