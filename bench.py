@@ -269,7 +269,9 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     # kernel's first dispatch in the process, under rocprofv3) is reported and the gate regions
     # are cleared before the replays; a timeout in the replays voids the measurement below.
     if model.tail_error():
-        print(f"KV {kv}: a layer-tail launch of the eager warm-up frame timed out at a gate; "
+        print(f"KV {kv}: a layer-tail launch of the eager warm-up frame timed out at a gate "
+              f"(error words: backbone {model.backbone.tail_error():#x}, decoder "
+              f"{model.decoder.tail_error():#x}); "
               "gate regions cleared before the timed frames", file=sys.stderr, flush=True)
         model.tail_reset()
 
@@ -286,8 +288,10 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     ms = dt / steps * 1e3
     # a gate wait of a persistent layer-tail launch that gave up leaves its frames undefined
     if model.tail_error():
+        eb, ed = model.backbone.tail_error(), model.decoder.tail_error()
         raise RuntimeError(f"KV {kv}: a layer-tail launch timed out at a gate during the timed "
-                           "frames; the measurement is void")
+                           f"frames (error words: backbone {eb:#x}, decoder {ed:#x}); the "
+                           "measurement is void")
 
     # ------------------------------------------------ per-kernel roofline of one frame
     # Record every C-ABI launch of one eager frame step, then replay the GEMV-family and the
@@ -352,6 +356,14 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
                 Nq = (Hq + 2 * Hk) * HD
                 b += Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD
             return b
+        if name == "ecd_layer_stack":
+            # nl layer tails in one launch: every layer's O, MLP, and all but the last layer's
+            # next-layer rms -> q|k|v (their attention is counted by tail_attn_bytes)
+            nl, M, D, F, Hq, Hk, HD = a[1], a[10], a[11], a[12], a[14], a[15], a[17]
+            b = (D * D + 2 * D + 6 * M * D) + (2 * F * D + 4 * F + 2 * M * D + 2 * D + 2 * M * F) \
+                + (D * F + 2 * D + 2 * M * F + 4 * M * D)
+            Nq = (Hq + 2 * Hk) * HD
+            return nl * b + (nl - 1) * (Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD)
         if name == "ecd_layer_head":
             # rms -> q|k|v of layer 0 (its attention is counted by tail_attn_bytes)
             M, D, Hq, Hk, HD = a[13], a[14], a[17], a[18], a[20]
@@ -380,6 +392,9 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
         elif n == "ecd_layer_tail" and a[17]:
             lens, R, Hq, Hk, HD = last
             tail_att[i] = attn_bytes(R, Hq, Hk, HD, lens)
+        elif n == "ecd_layer_stack":
+            lens, R, Hq, Hk, HD = last
+            tail_att[i] = (a[1] - 1) * attn_bytes(R, Hq, Hk, HD, lens)
     gemv_calls = [(n, a, gemv_family_bytes(n, a) + tail_att.get(i, 0))
                   for i, (n, a) in enumerate(calls) if gemv_family_bytes(n, a)]
     attn_calls = [(n, a) for n, a in calls if n == "ecd_decode_attn"]

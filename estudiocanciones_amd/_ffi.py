@@ -98,6 +98,11 @@ SIGNATURES = {
                        c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P],
     "ecd_layer_tail_supported": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
     "ecd_layer_tail_ws_bytes": [c_int, c_int, c_int, c_int],
+    "ecd_layer_stack_plan": [_P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P, _P],
+    "ecd_layer_stack_plan_bytes": [c_int],
+    "ecd_layer_stack_supported": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    "ecd_layer_stack": [_P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int,
+                        c_int, c_int, c_int, c_int, c_float, c_int, _P],
 }
 
 _lib = None
@@ -120,7 +125,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = c_long if name.startswith("ecd_packed_bytes") or \
-                name == "ecd_layer_tail_ws_bytes" else c_int
+                name in ("ecd_layer_tail_ws_bytes", "ecd_layer_stack_plan_bytes") else c_int
         handle.ecd_version.argtypes = []
         handle.ecd_version.restype = ctypes.c_char_p
         _lib = handle

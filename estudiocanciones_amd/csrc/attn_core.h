@@ -311,8 +311,9 @@ __device__ __forceinline__ void attn_run_m(SplitStateM<HD, G>& ss, const f16x8 (
   ss.l_run = l_run;
 }
 
-// Head g's normalised output o = acc / l as fp16 to dst[g * HD + d] (lanes of heads < G).
-template <int HD, int G>
+// Head g's normalised output o = acc / l as fp16 to dst[g * HD + d] (lanes of heads < G); WT:
+// agent-scope stores.
+template <int HD, int G, bool WT = false>
 __device__ __forceinline__ void attn_store_o_m(const SplitStateM<HD, G>& ss, f16* dst, int lane) {
   const int n = lane & 15, grp = lane >> 4;
   if (n >= G) return;
@@ -325,7 +326,17 @@ __device__ __forceinline__ void attn_store_o_m(const SplitStateM<HD, G>& ss, f16
         f16x8 ov;
 #pragma unroll
         for (int b = 0; b < 8; ++b) ov[b] = (f16)(ss.acc[j][b][i] / ss.l_run);
-        *(f16x8*)(dst + n * HD + d0) = ov;
+        if constexpr (WT) {
+          // written through to memory (agent scope): read by other XCDs in the same launch
+          const u32x4 u = __builtin_bit_cast(u32x4, ov);
+          uint64_t* q = (uint64_t*)(dst + n * HD + d0);
+          __hip_atomic_store(q, (uint64_t)u.x | ((uint64_t)u.y << 32), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(q + 1, (uint64_t)u.z | ((uint64_t)u.w << 32), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          *(f16x8*)(dst + n * HD + d0) = ov;
+        }
       }
     }
 }

@@ -107,6 +107,27 @@ struct Args {
   int spin_max;
 };
 
+// One layer of a stack launch: its weights and buffers (the fields of Args that change from
+// layer to layer; o and xin of layer l > 0 are o_next and xout of layer l - 1)
+struct LayerRec {
+  const int8_t* wo;
+  const f16* so;
+  const f16* n2;
+  const int8_t* w13;
+  const f16* s13;
+  const int8_t* w2;
+  const f16* s2;
+  const f16* n1;
+  const int8_t* wq;
+  const f16* sq;
+  f16* kc;
+  f16* vc;
+  f16* x1;
+  f16* mm;
+  f16* xout;
+  f16* o_next;
+};
+
 __device__ __forceinline__ void bar() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -148,7 +169,8 @@ __device__ __forceinline__ void store_agent(uint32_t* p, uint32_t v) {
 
 // Error word: bit 0 when any wait gave up, and one bit naming each wait that did.
 constexpr uint32_t ERR_GATE_A = 2, ERR_GATE_B = 4, ERR_GATE_C = 8, ERR_SPLIT_W2 = 16,
-                   ERR_HAND_VS = 32, ERR_HAND_Q = 64, ERR_NEW_SLOT = 128, ERR_MERGE = 256;
+                   ERR_HAND_VS = 32, ERR_HAND_Q = 64, ERR_NEW_SLOT = 128, ERR_MERGE = 256,
+                   ERR_GATE_O = 512;
 __device__ __forceinline__ void flag_err(uint32_t* err, uint32_t sites) {
   __hip_atomic_fetch_or(err, 1u | sites, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -721,7 +743,7 @@ __device__ __forceinline__ bool attn_new_slot(SplitStateM<HD, G>& ss, const f16x
 // one per workgroup, and the pair's KB workgroups merge those (attention_merge).  Same
 // arithmetic as the split-combine kernel, summed in two levels.  q and the new K/V slots come
 // from the hand-off words of epoch `ep` (no gate after the q|k|v phase).
-template <int HD, int G, int RING, bool KNT>
+template <int HD, int G, int RING, bool KNT, bool WT>
 __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* smem, int wv,
                                                 int lane, AttPre<HD, RING>& pf, uint32_t ep,
                                                 const unsigned char* lt) {
@@ -782,7 +804,8 @@ __device__ __forceinline__ void attention_phase(const Args& a, unsigned char* sm
   }
   if (bad && lane == 0) flag_err(a.err, bad);
   if (a.L <= ATT_SHORT) {
-    attn_store_o_m<HD, G>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
+    attn_store_o_m<HD, G, WT>(ss, a.o_next + ((long)pf.r * Hq + pf.kh * G) * HD, lane);
+    if constexpr (WT) wait_vm0();  // o acknowledged before the loader's next gate
     bar();  // P(ATT)
     return;
   }
@@ -851,7 +874,7 @@ __device__ __forceinline__ void vatt_prefetch(const Args& a, int NB, int b, int 
 // (bounded by spin_max), scores summed in fp32 over each lane's dims and across the wave, then
 // the single-block softmax of app/kernels.py:111-153 (m = max, p = exp(s - m), l = sum of the
 // unrounded p, acc = sum of fp16(p) v in fp32, o = fp16(acc / l)) into o_next.
-template <int HD, int G>
+template <int HD, int G, bool WT>
 __device__ __forceinline__ void vattention_phase(const Args& a, int lane, VPre<HD>& pf,
                                                  uint32_t ep) {
   constexpr int NW = VPre<HD>::NW;
@@ -958,9 +981,16 @@ __device__ __forceinline__ void vattention_phase(const Args& a, int lane, VPre<H
     }
     uint32_t* op = (uint32_t*)(a.o_next + ((long)pf.r * Hq + pf.kh * G + g) * HD + DPL * lane);
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      op[w] = __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t ov =
+          __builtin_bit_cast(uint32_t, (f16x2){(f16)(acc[2 * w] / l), (f16)(acc[2 * w + 1] / l)});
+      if constexpr (WT)
+        __hip_atomic_store(op + w, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        op[w] = ov;
+    }
   }
+  if constexpr (WT) wait_vm0();  // o acknowledged before the loader's next gate
   bar();  // P(ATT)
 }
 
@@ -1021,7 +1051,7 @@ __device__ __forceinline__ void lse_merge(const float* src, int n, int str, int 
 // spin_max; lanes spread over parts x columns, G * HD / 64 value words and one (m, l) pair each,
 // exchanged through LDS): the log-sum-exp sums of the per-op combine, parts in order, with no
 // counter and no wait for this workgroup's own stores.  Returns false if a poll gave up.
-template <int HD, int G>
+template <int HD, int G, bool WT>
 __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* smem, int NB, int b,
                                                 int lane, uint32_t epoch) {
   static_assert(HD % 64 == 0, "value words spread evenly over the lanes");
@@ -1103,7 +1133,12 @@ __device__ __forceinline__ bool attention_merge(const Args& a, unsigned char* sm
       ls += sml[2 * (i * G + g) + 1] * w;
       acc += sv[i * gc + u] * w;
     }
-    a.o_next[((long)r * a.Hq + kh * G + g) * HD + kq * cw + (u - g * cw)] = (f16)(acc / ls);
+    f16* dst = a.o_next + ((long)r * a.Hq + kh * G + g) * HD + kq * cw + (u - g * cw);
+    if constexpr (WT)
+      __hip_atomic_store((uint16_t*)dst, __builtin_bit_cast(uint16_t, (f16)(acc / ls)),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      *dst = (f16)(acc / ls);
   }
   return ok;
 }
@@ -1124,18 +1159,43 @@ __host__ __device__ constexpr int w2_rounds(int C2, int R) {
 // Weight issue order of a compute wave (its vector-memory queue, in order): W_O and W13 at the
 // start (and W2 where registers allow), then W2 and the next layer's q|k|v right after the W13
 // MFMAs, so the weight stream does not wait for the gates.
+//
+// The lane index, opaque to the optimiser: in a stack launch the per-lane offsets derived from it
+// are then computed inside each layer instead of being hoisted out of the layer loop and kept
+// live (in registers the layer's weights need) across all of it.
+__device__ __forceinline__ int lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+// The same for the wave index and the workgroup index (scalars), and what derives from them
+__device__ __forceinline__ int wave_id() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return __builtin_amdgcn_readfirstlane(t >> 6);
+}
+__device__ __forceinline__ int block_id() {
+  int b = blockIdx.x;
+  asm volatile("" : "+v"(b));
+  return __builtin_amdgcn_readfirstlane(b);
+}
+
+// One layer: tail_compute runs it on the compute waves, tail_loader on the loader wave (the two
+// meet at the same barriers in the same order).  `go` (loader lane 0): the gate count this
+// workgroup has reached; `bad`: the error bits of the loader's waits.  STK: a layer of a stack
+// launch, whose attention output goes to memory by agent-scope stores; og: the layer's o is the
+// previous layer's attention output from this launch, complete at the o gate (the weights go
+// out before it).
 template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
-          bool KNT>
-__global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
+          bool KNT, bool STK>
+__device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
+                                             const uint32_t& s_epoch, bool og, int wv) {
   constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
   constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
   constexpr int W2H = w2_rounds(C2, R), CH = C2 / W2H;  // W2 rounds, chunks per round
   static_assert(C2 % W2H == 0, "whole chunks per round");
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int NB = gridDim.x, b = blockIdx.x;
+  const int lane = lane_id();
+  const int NB = gridDim.x, b = block_id();
   const int D = a.D, F = a.F, M = a.M;
   const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
   const bool has_next = a.wq != nullptr;
@@ -1169,176 +1229,224 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   unsigned char* psD = smem + XD + 2 * D + 512;  // partials of the K = D phases
   unsigned char* psF = smem + CH * CW * chb(R);  // partials of the W2 phase
 
-  if (wv < CW) {
-    // ------------------------------------------------------------------ compute waves
-    // attention splits: two K/V tiles in flight where the register budget allows it (G <= 3)
-    constexpr int ARING = AG <= 3 ? 2 : 1;
-    // tiled (MFMA) splits, or the VALU path for caches of at most VSHORT slots (VS)
-    AttPre<(AHD > 0 && !VS ? AHD : 32), ARING> pf;
-    VPre<(AHD > 0 && VS ? AHD : 128)> vpf;
-    // long splits (more than two tiles) of the 8-row MFMA attention: the third tile goes into
-    // an LDS slot of the wave during the q|k|v phase, so that it has arrived when q is seen
-    constexpr bool STAGE = AHD == 128 && !VS && ARING == 2 && R == 8;
-    unsigned char* lt = smem + stage_slot<CD, R, CH>(wv);
-    auto stage = [&]() {
-      if constexpr (STAGE) {
-        if (att && pf.on && pf.hi - pf.lo > 32) {
-          pf.staged = true;
-          kv_stage(a.kc + pf.cbase, a.vc + pf.cbase, pf.lo + 32, pf.hi - 1, lane, lt);
-        }
+  // ------------------------------------------------------------------ compute waves
+  // attention splits: two K/V tiles in flight where the register budget allows it (G <= 3)
+  constexpr int ARING = AG <= 3 ? 2 : 1;
+  // tiled (MFMA) splits, or the VALU path for caches of at most VSHORT slots (VS)
+  AttPre<(AHD > 0 && !VS ? AHD : 32), ARING> pf;
+  VPre<(AHD > 0 && VS ? AHD : 128)> vpf;
+  // long splits (more than two tiles) of the 8-row MFMA attention: the third tile goes into
+  // an LDS slot of the wave during the q|k|v phase, so that it has arrived when q is seen
+  constexpr bool STAGE = AHD == 128 && !VS && ARING == 2 && R == 8;
+  unsigned char* lt = smem + stage_slot<CD, R, CH>(wv);
+  auto stage = [&]() {
+    if constexpr (STAGE) {
+      if (att && pf.on && pf.hi - pf.lo > 32) {
+        pf.staged = true;
+        kv_stage(a.kc + pf.cbase, a.vc + pf.cbase, pf.lo + 32, pf.hi - 1, lane, lt);
       }
-    };
-    const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
-    u32x4 wq[2][CD];
-    const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
-    if constexpr (!HEAD) {
-      // this wave's slice of the attention output first (the inputs of this launch are final)
-      dma_rows<CD, R>(a.o, D, M, c0D, xs + c0D * chb(R), lane);
-      u32x4 wo[1][CD];
-      u32x4 w13[NT13][CD];
-      const int to_t[1] = {tO < 0 ? 0 : tO};
-      int t13[NT13];
+    }
+  };
+  const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
+  u32x4 wq[2][CD];
+  const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
+  if constexpr (!HEAD) {
+    // this wave's slice of the attention output first (the inputs of this launch are final)
+    if (!og) dma_rows<CD, R>(a.o, D, M, c0D, xs + c0D * chb(R), lane);
+    u32x4 wo[1][CD];
+    u32x4 w13[NT13][CD];
+    const int to_t[1] = {tO < 0 ? 0 : tO};
+    int t13[NT13];
 #pragma unroll
-      for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
-      if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
-      load_w_chunks<NT13, CD, NTL, 0, 1, 0>(w13, a.w13, t13, nchD, c0D, lane);
+    for (int t = 0; t < NT13; ++t) t13[t] = b * NT13 + t;
+    if (tO >= 0) load_w<1, CD, NTL>(wo, a.wo, to_t, nchD, c0D, lane);
+    load_w_chunks<NT13, CD, NTL, 0, 1, 0>(w13, a.w13, t13, nchD, c0D, lane);
+    if (og) {
+      bar();  // X(O): the previous layer's attention output is complete
+      dma_rows<CD, R>(a.o, D, M, c0D, xs + c0D * chb(R), lane);
+    }
 
-      // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
-      // wait for this wave's o slice and W_O (the NT13 W13 loads issued after them may fly on)
-      {
-        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-        if (tO >= 0) {
-          wait_vm<NT13>();
-          mfma_chunks<1, CD, R>(acc, wo, xs, nws, c0D, lane, 0.f, false);
-        }
-        put_partials<1>(psD, acc, wv, lane);
+    // phase O (x = o, already final: no gate).  Only waves with an O tile read the x tile; they
+    // wait for this wave's o slice and W_O (the NT13 W13 loads issued after them may fly on)
+    {
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      if (tO >= 0) {
+        if (og) wait_vm0();
+        else wait_vm<NT13>();
+        mfma_chunks<1, CD, R>(acc, wo, xs, nws, c0D, lane, 0.f, false);
+      }
+      put_partials<1>(psD, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(O)
+    load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
+    u32x4 w2[1][C2];
+    const int t2_t[1] = {t2 < 0 ? 0 : t2};
+
+    // phase W13 (x = rms(x1, n2))
+    bar();  // X(W13): x1 is complete
+    dma_rows<CD, R>(a.x1, D, M, c0D, xs + c0D * chb(R), lane);
+    dma_nw<CD>(a.n2, c0D, nws, lane);
+    wait_vm0();
+    rms_partial<CD, R>(xs, c0D, lane, wv, ss);
+    wait_lgkm0();
+    bar();  // S(W13)
+    {
+      const float inv = rms_inv<R>(ss, lane, D, a.eps);
+      f32x4 acc[NT13];
+#pragma unroll
+      for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
+      mfma_chunks_then<NT13, CD, R>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if (t2 >= 0)
+          load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
+                                                                            c0F, lane);
+      });
+      put_partials<NT13>(psD, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(W13)
+
+    // the next layer's q|k|v weights go out during the second gate, into the registers the
+    // W13 phase freed (HBM would idle there otherwise)
+    if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+    else if (tq0 >= 0)
+      load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
+                                           nchD, c0D, lane);
+
+    // phase W2 (x = mm)
+    bar();  // X(W2): mm is complete
+    if constexpr (W2H == 1) {
+      // the workgroup's K part of mm: chunks c0F .. of F, at LDS chunks wv * C2 ..
+      dma_rows<C2, R>(a.mm, F, M, c0F, xs + wv * C2 * chb(R), lane);
+      wait_vm0();
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      if (t2 >= 0) mfma_chunks<1, C2, R>(acc, w2, xs, nws, wv * C2, lane, 0.f, false);
+      put_partials<1>(psF, acc, wv, lane);
+    } else {
+      // in rounds of CH chunks through this wave's LDS chunks wv * CH ..: a round's copy goes
+      // out once the wave's LDS reads of the previous round are done (each wave reads only
+      // its own chunks, so no barrier between rounds)
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      static_for<W2H>([&](auto hc) {
+        constexpr int h = decltype(hc)::value;
+        if constexpr (h > 0) wait_lgkm0();
+        dma_rows<CH, R>(a.mm, F, M, c0F + h * CH, xs + wv * CH * chb(R), lane);
+        wait_vm0();
+        if (t2 >= 0) mfma_chunks_part<1, C2, R, h * CH, CH>(acc, w2, xs, wv * CH, lane);
+      });
+      put_partials<1>(psF, acc, wv, lane);
+    }
+    wait_lgkm0();
+    bar();  // P(W2)
+  }
+
+  if (has_next) {
+    if constexpr (HEAD) {
+      // head launch (x = xin, final at launch start): x slice, then the layer's q|k|v
+      // weights, the only weights (all at once); the RMS waits for the x slice only
+      dma_rows<CD, R>(a.xin, D, M, c0D, xs + c0D * chb(R), lane);
+      dma_nw<CD>(a.n1, c0D, nws, lane);
+      if (tq1 >= 0) {
+        load_w_chunks<2, CD, NTL, 0, CD, 0>(wq, a.wq, tq_t, nchD, c0D, lane);
+        wait_vm<2 * CD>();
+      } else if (tq0 >= 0) {
+        load_w_chunks<1, CD, NTL, 0, CD, 0>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
+                                            nchD, c0D, lane);
+        wait_vm<CD>();
+      } else {
+        wait_vm0();
+      }
+      rms_partial<CD, R>(xs, c0D, lane, wv, ss);
+      if constexpr (AHD > 0 && VS) {
+        if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
+      } else if constexpr (AHD > 0) {
+        if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
+        stage();
       }
       wait_lgkm0();
-      bar();  // P(O)
-      load_w_chunks<NT13, CD, NTL, 1, CD, LA>(w13, a.w13, t13, nchD, c0D, lane);
-      u32x4 w2[1][C2];
-      const int t2_t[1] = {t2 < 0 ? 0 : t2};
-
-      // phase W13 (x = rms(x1, n2))
-      bar();  // X(W13): x1 is complete
-      dma_rows<CD, R>(a.x1, D, M, c0D, xs + c0D * chb(R), lane);
-      dma_nw<CD>(a.n2, c0D, nws, lane);
+      bar();  // X(QKV)
+    } else {
+      // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
+      // they stream during the third gate, and the loader's hand-off stores after the q|k|v
+      // phase do not queue behind them
+      if constexpr (AHD > 0 && VS) {
+        if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
+      } else if constexpr (AHD > 0) {
+        if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
+      }
+      // phase QKV (x = rms(xout, n1'))
+      bar();  // X(QKV): xout is complete
+      dma_rows<CD, R>(a.xout, D, M, c0D, xs + c0D * chb(R), lane);
+      dma_nw<CD>(a.n1, c0D, nws, lane);
       wait_vm0();
+      stage();
       rms_partial<CD, R>(xs, c0D, lane, wv, ss);
       wait_lgkm0();
-      bar();  // S(W13)
-      {
-        const float inv = rms_inv<R>(ss, lane, D, a.eps);
-        f32x4 acc[NT13];
-#pragma unroll
-        for (int t = 0; t < NT13; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        // W2's chunks go out during the W13 MFMAs, into the registers each finished chunk frees
-        mfma_chunks_then<NT13, CD, R>(acc, w13, xs, nws, c0D, lane, inv, true, [&](auto uc) {
-          constexpr int u = decltype(uc)::value;
-          if (t2 >= 0)
-            load_w_chunks<1, C2, NTL, (u * C2) / CD, ((u + 1) * C2) / CD, LA>(w2, a.w2, t2_t, nchF,
-                                                                              c0F, lane);
-        });
-        put_partials<NT13>(psD, acc, wv, lane);
-      }
-      wait_lgkm0();
-      bar();  // P(W13)
-
-      // the next layer's q|k|v weights go out during the second gate, into the registers the
-      // W13 phase freed (HBM would idle there otherwise)
-      if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
-      else if (tq0 >= 0)
-        load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
-                                             nchD, c0D, lane);
-
-      // phase W2 (x = mm)
-      bar();  // X(W2): mm is complete
-      if constexpr (W2H == 1) {
-        // the workgroup's K part of mm: chunks c0F .. of F, at LDS chunks wv * C2 ..
-        dma_rows<C2, R>(a.mm, F, M, c0F, xs + wv * C2 * chb(R), lane);
-        wait_vm0();
-        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-        if (t2 >= 0) mfma_chunks<1, C2, R>(acc, w2, xs, nws, wv * C2, lane, 0.f, false);
-        put_partials<1>(psF, acc, wv, lane);
-      } else {
-        // in rounds of CH chunks through this wave's LDS chunks wv * CH ..: a round's copy goes
-        // out once the wave's LDS reads of the previous round are done (each wave reads only
-        // its own chunks, so no barrier between rounds)
-        f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-        static_for<W2H>([&](auto hc) {
-          constexpr int h = decltype(hc)::value;
-          if constexpr (h > 0) wait_lgkm0();
-          dma_rows<CH, R>(a.mm, F, M, c0F + h * CH, xs + wv * CH * chb(R), lane);
-          wait_vm0();
-          if (t2 >= 0) mfma_chunks_part<1, C2, R, h * CH, CH>(acc, w2, xs, wv * CH, lane);
-        });
-        put_partials<1>(psF, acc, wv, lane);
-      }
-      wait_lgkm0();
-      bar();  // P(W2)
     }
-
-    if (has_next) {
-      if constexpr (HEAD) {
-        // head launch (x = xin, final at launch start): x slice, then the layer's q|k|v
-        // weights, the only weights (all at once); the RMS waits for the x slice only
-        dma_rows<CD, R>(a.xin, D, M, c0D, xs + c0D * chb(R), lane);
-        dma_nw<CD>(a.n1, c0D, nws, lane);
-        if (tq1 >= 0) {
-          load_w_chunks<2, CD, NTL, 0, CD, 0>(wq, a.wq, tq_t, nchD, c0D, lane);
-          wait_vm<2 * CD>();
-        } else if (tq0 >= 0) {
-          load_w_chunks<1, CD, NTL, 0, CD, 0>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
-                                              nchD, c0D, lane);
-          wait_vm<CD>();
-        } else {
-          wait_vm0();
-        }
-        rms_partial<CD, R>(xs, c0D, lane, wv, ss);
-        if constexpr (AHD > 0 && VS) {
-          if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
-        } else if constexpr (AHD > 0) {
-          if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
-          stage();
-        }
-        wait_lgkm0();
-        bar();  // X(QKV)
-      } else {
-        // the next layer's first K/V tiles go out into the registers the W2 phase leaves free:
-        // they stream during the third gate, and the loader's hand-off stores after the q|k|v
-        // phase do not queue behind them
-        if constexpr (AHD > 0 && VS) {
-          if (att) vatt_prefetch<AHD>(a, NB, b, wv, lane, vpf);
-        } else if constexpr (AHD > 0) {
-          if (att) att_prefetch<AHD, ARING, KNT>(a, NB, b, wv, lane, pf);
-        }
-        // phase QKV (x = rms(xout, n1'))
-        bar();  // X(QKV): xout is complete
-        dma_rows<CD, R>(a.xout, D, M, c0D, xs + c0D * chb(R), lane);
-        dma_nw<CD>(a.n1, c0D, nws, lane);
-        wait_vm0();
-        stage();
-        rms_partial<CD, R>(xs, c0D, lane, wv, ss);
-        wait_lgkm0();
-      }
-      bar();  // S(QKV)
-      const float inv = rms_inv<R>(ss, lane, D, a.eps);
-      f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
-      if (tq1 >= 0) mfma_chunks<2, CD, R>(acc, wq, xs, nws, c0D, lane, inv, true);
-      else if (tq0 >= 0)
-        mfma_chunks<1, CD, R>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv,
-                              true);
-      put_partials<2>(psD, acc, wv, lane);
-      wait_lgkm0();
-      bar();  // P(QKV)
-    }
-    if constexpr (AHD > 0 && VS) {
-      if (att) vattention_phase<AHD, AG>(a, lane, vpf, s_epoch);
-    } else if constexpr (AHD > 0) {
-      if (att) attention_phase<AHD, AG, ARING, KNT>(a, smem, wv, lane, pf, s_epoch, lt);
-    }
-    return;
+    bar();  // S(QKV)
+    const float inv = rms_inv<R>(ss, lane, D, a.eps);
+    f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
+    if (tq1 >= 0) mfma_chunks<2, CD, R>(acc, wq, xs, nws, c0D, lane, inv, true);
+    else if (tq0 >= 0)
+      mfma_chunks<1, CD, R>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv,
+                            true);
+    put_partials<2>(psD, acc, wv, lane);
+    wait_lgkm0();
+    bar();  // P(QKV)
   }
+  if constexpr (AHD > 0 && VS) {
+    if (att) vattention_phase<AHD, AG, STK>(a, lane, vpf, s_epoch);
+  } else if constexpr (AHD > 0) {
+    if (att) attention_phase<AHD, AG, ARING, KNT, STK>(a, smem, wv, lane, pf, s_epoch, lt);
+  }
+
+}
+
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
+          bool KNT, bool STK>
+__device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, uint32_t& s_epoch,
+                                            uint32_t& go, uint32_t& bad, bool og) {
+  constexpr int LA = 3;        // weight loads in flight per compute wave (paced issue)
+  constexpr int C2 = CF / KS2;  // W2 chunks per compute wave (K split over KS2 workgroups)
+  constexpr int W2H = w2_rounds(C2, R), CH = C2 / W2H;  // W2 rounds, chunks per round
+  static_assert(C2 % W2H == 0, "whole chunks per round");
+  const int lane = lane_id();
+  const int wv = wave_id();
+  const int NB = gridDim.x, b = block_id();
+  const int D = a.D, F = a.F, M = a.M;
+  const int nchD = CD * CW, nchF = CF * CW;  // D / 64, F / 64
+  const bool has_next = a.wq != nullptr;
+  // the next layer's attention runs in this launch (AHD > 0: its head_dim; AG query heads per
+  // kv head), on q and the new K/V slots handed off in tagged words; caches
+  // longer than ATT_SHORT slots are split over the KB workgroups of each (row, kv head) pair and
+  // their 8 compute waves
+  const bool att = AHD > 0 && has_next;
+
+  // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
+  const int TO = D >> 4;
+  const int tO = b - (NB - TO);    // >= 0: one O tile
+  // W2 (D / 16 tiles too): tile b (KS2 == 1), or tile b / KS2, K-part b % KS2 (host: D / 16 *
+  // KS2 == NB), whose partial sums the K-part 0 workgroup adds up
+  const int t2 = KS2 == 1 ? (b < TO ? b : -1) : b / KS2;
+  const int ks2 = KS2 == 1 ? 0 : b % KS2;
+  const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
+  const int xtra = TQ - NB;
+  // The two 16-column tiles whose hand-off words share a 128-byte line (tiles 2j, 2j + 1) go to
+  // workgroups 8 apart, i.e. to one XCD: no line is written in pieces from two XCDs, which
+  // agent-scope loads could read stale.  A permutation within each aligned block of 16.
+  auto paired = [](int i) { return (i & ~15) + 2 * (i & 7) + ((i >> 3) & 1); };
+  const int tq0 = b < TQ ? (b < (TQ & ~15) ? paired(b) : b) : -1;
+  const int xb = b - (NB - xtra);  // this workgroup's index among those with a second tile
+  const int tq1 = (xtra > 0 && xb >= 0) ? NB + (xb < (xtra & ~15) ? paired(xb) : xb) : -1;
+
+  const int XD = nchD * chb(R);
+  unsigned char* xs = smem;
+  unsigned char* nws = smem + XD;
+  float* ss = (float*)(smem + XD + 2 * D);
+  unsigned char* psD = smem + XD + 2 * D + 512;  // partials of the K = D phases
+  unsigned char* psF = smem + CH * CW * chb(R);  // partials of the W2 phase
 
   // -------------------------------------------------------------------- loader wave
   const int me = lane & 15;        // output row of this lane's epilogue slot
@@ -1346,9 +1454,12 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
   const bool mrow = me < M;
   const int grp = b & 7;
   const uint32_t per = (uint32_t)(NB >> 3);
-  uint32_t bad = 0;  // the waits that gave up (error-word bits)
-  uint32_t go = 0;
-  if (lane == 0) go = ld_sc1(a.sync + GATE_FLAGS + 32 * 8 * grp);  // (all flags equal here)
+  if (og) {
+    // the o gate: this workgroup's stores of the previous layer's attention output (the merge's,
+    // and its compute waves', acknowledged before their last barrier) are acknowledged
+    wait_vm0();
+    if (lane == 0) gate_arrive(a.sync, grp, per, go);
+  }
 
   // epilogue operands that do not depend on this launch's phases
   f16x4 so4 = {}, xr4 = {}, s2v = {};
@@ -1382,6 +1493,13 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
         for (int r = 0; r < 4; ++r) cs[i][r] = c[r];
       }
     }
+  }
+
+  if (og) {
+    if (!gate_wait(a.sync, grp, __builtin_amdgcn_readfirstlane(go), a.spin_max, lane))
+      bad |= ERR_GATE_O;
+    ++go;
+    bar();  // X(O)
   }
 
   if constexpr (!HEAD) {
@@ -1534,16 +1652,87 @@ __global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
       if (dst) *(f16x4*)dst = o;
     }
     if constexpr (AHD > 0) {
-      if (!att) goto done;
+      if (!att) return;
       bar();  // X(ATT)
       bar();  // P(ATT)
       if constexpr (!VS)
-        if (!attention_merge<AHD, AG>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)))
+        if (!attention_merge<AHD, AG, STK>(a, smem, NB, b, lane, __builtin_amdgcn_readfirstlane(go)))
           bad |= ERR_MERGE;
     }
   }
-done:
-  if (lane == 0 && bad) flag_err(a.err, bad);
+}
+
+// One launch per layer tail (a head launch: HEAD).
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
+          bool KNT>
+__global__ __launch_bounds__(NTHR) void layer_tail_kernel(const Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ uint32_t s_epoch;  // this launch's epoch (loader -> compute waves)
+  if (threadIdx.x < CW * 64) {
+    tail_compute<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT, false>(
+        a, smem, s_epoch, false, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    return;
+  }
+  const bool ld0 = threadIdx.x == CW * 64;  // the loader's lane 0
+  uint32_t go = 0, bad = 0;
+  if (ld0) go = ld_sc1(a.sync + GATE_FLAGS + 32 * 8 * (blockIdx.x & 7));  // (all flags equal here)
+  tail_loader<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT, false>(a, smem, s_epoch, go, bad,
+                                                                         false);
+  if (ld0 && bad) flag_err(a.err, bad);
+}
+
+// Layer l of a stack: the shared fields of a0 with the record's pointers (o and xin of l > 0 from
+// layer l - 1's record).  The records are read through the constant address space: they do not
+// change during the launch, scalar loads fetch them, and the compiler takes the pointers read
+// from there to be global memory (global, not flat, instructions).
+typedef const __attribute__((address_space(4))) LayerRec CLayerRec;
+typedef const __attribute__((address_space(4))) Args CArgs;
+__device__ __forceinline__ Args stack_args(const LayerRec* plan, int l) {
+  CLayerRec* c = (CLayerRec*)plan;
+  // the shared fields are read from the kernel arguments again for every layer (an opaque
+  // pointer to them), not held in scalar registers across the layer loop
+  Args a;
+#if __HIP_DEVICE_COMPILE__  // (the host pass only parses this function)
+  CArgs* ap = (CArgs*)__builtin_amdgcn_kernarg_segment_ptr();  // a0: the first argument
+  asm volatile("" : "+s"(ap));
+  __builtin_memcpy(&a, ap, sizeof(Args));
+#endif
+  a.wo = c[l].wo; a.so = c[l].so; a.n2 = c[l].n2; a.w13 = c[l].w13; a.s13 = c[l].s13;
+  a.w2 = c[l].w2; a.s2 = c[l].s2; a.n1 = c[l].n1; a.wq = c[l].wq; a.sq = c[l].sq;
+  a.kc = c[l].kc; a.vc = c[l].vc; a.x1 = c[l].x1; a.mm = c[l].mm; a.xout = c[l].xout;
+  a.o_next = c[l].o_next;
+  if (l > 0) {
+    a.o = c[l - 1].o_next;
+    a.xin = c[l - 1].xout;
+  }
+  return a;
+}
+
+// A stack of layer tails in one launch: layer l's attention output (its o_next) is layer l + 1's
+// o, and its output xout is layer l + 1's input.  Between two layers the workgroups meet at one
+// more gate (o complete) instead of a launch boundary, and the next layer's O and first W13
+// weights stream while they wait.  Every activation buffer of a stack is its layer's own, so no
+// XCD's L2 holds a line of one before its writers have finished it.
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT>
+__global__ __launch_bounds__(NTHR) void layer_stack_kernel(const Args a0,
+                                                           const LayerRec* __restrict__ plan,
+                                                           int nl) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ uint32_t s_epoch;
+  if (threadIdx.x < CW * 64) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (int l = 0; l < nl; ++l)
+      tail_compute<CD, CF, NT13, KS2, AHD, AG, NTL, false, R, VS, KNT, true>(
+          stack_args(plan, l), smem, s_epoch, l > 0, wv);
+    return;
+  }
+  const bool ld0 = threadIdx.x == CW * 64;
+  uint32_t go = 0, bad = 0;
+  if (ld0) go = ld_sc1(a0.sync + GATE_FLAGS + 32 * 8 * (blockIdx.x & 7));
+  for (int l = 0; l < nl; ++l)
+    tail_loader<CD, CF, NT13, KS2, AHD, AG, NTL, false, R, VS, KNT, true>(
+        stack_args(plan, l), smem, s_epoch, go, bad, l > 0);
+  if (ld0 && bad) flag_err(a0.err, bad);
 }
 
 int device_cus() {
@@ -1558,11 +1747,12 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
-          bool KNT = false>
-int launch(const Args& a, int nb, hipStream_t st) {
+// Dynamic LDS bytes of a launch: the phases' x tiles, norm weights, row sums and partials, the
+// attention's partials and merge exchange, the staged K/V tiles of long splits
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, int R, bool VS>
+int tail_lds(int D) {
   const int xd = CD * CW * chb(R), xf = CF / KS2 / w2_rounds(CF / KS2, R) * CW * chb(R);
-  const int ldsD = xd + 2 * a.D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
+  const int ldsD = xd + 2 * D + 512 + CW * (NT13 > 2 ? NT13 : 2) * 1024;
   const int ldsF = xf + CW * 1024;
   // attention: the waves' partials, then the merge's exchange
   const int ldsA = AHD > 0 && !VS ? (CW * AG * (2 + AHD) + AG * AHD + 2 * ATT_KB_MAX * AG) * 4 : 0;
@@ -1572,15 +1762,38 @@ int launch(const Args& a, int nb, hipStream_t st) {
   constexpr int C2 = CF / KS2, CH = C2 / w2_rounds(C2, R);
   constexpr int lde = AHD == 128 && !VS && AG <= 3 && R == 8 ? stage_end<CD, R, CH>() : 0;
   if (lds < lde) lds = lde;
-  // dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it)
-  static int attr = 0;
+  return lds;
+}
+
+// dynamic LDS beyond the default limit (the kernel's static LDS comes on top of it), raised once
+// per kernel to the largest size launched
+inline int raise_lds(const void* fn, int lds, int& attr) {
   if (lds > attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return (int)e;
     attr = lds;
   }
-  hipLaunchKernelGGL((layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT>), dim3(nb), dim3(NTHR), lds, st, a);
+  return 0;
+}
+
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, bool HEAD, int R, bool VS,
+          bool KNT = false>
+int launch(const Args& a, int nb, hipStream_t st) {
+  const int lds = tail_lds<CD, CF, NT13, KS2, AHD, AG, R, VS>(a.D);
+  static int attr = 0;
+  const auto fn = layer_tail_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, HEAD, R, VS, KNT>;
+  if (const int rc = raise_lds((const void*)fn, lds, attr)) return rc;
+  hipLaunchKernelGGL(fn, dim3(nb), dim3(NTHR), lds, st, a);
+  return ecd_launch_status();
+}
+
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT>
+int launch_stack(const Args& a, const LayerRec* plan, int nl, int nb, hipStream_t st) {
+  const int lds = tail_lds<CD, CF, NT13, KS2, AHD, AG, R, VS>(a.D);
+  static int attr = 0;
+  const auto fn = layer_stack_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT>;
+  if (const int rc = raise_lds((const void*)fn, lds, attr)) return rc;
+  hipLaunchKernelGGL(fn, dim3(nb), dim3(NTHR), lds, st, a, plan, nl);
   return ecd_launch_status();
 }
 
@@ -1750,6 +1963,116 @@ extern "C" int ecd_layer_tail(const void* o, const void* xin, const void* wo, co
   ECD_TAIL(2, 16, 4, 4, 128, 4, 16, true)
   ECD_TAIL(2, 16, 4, 4, 0, 0, 16, false)
 #undef ECD_TAIL
+  return ECD_ENOTSUP;
+}
+
+// Stack launches: the instantiated shapes, the depth decoders' (their layers are short, so the
+// launch boundary is a large part of each).  The backbone keeps one launch per layer: looped over
+// its layers, its 3072-wide tail with the MFMA attention needs more than the 168 registers a
+// lane has at three waves per SIMD, and the spills cost more than the boundaries.  0: not
+// instantiated, else an index for ecd_layer_stack's dispatch.
+static int stack_kind(int nb, int M, int D, int F, int Hq, int Hk, int HD, int L, bool ntl, bool knt) {
+  if (nb <= 0 || (nb % 8) || M < 1 || M > tail::MR || Hk <= 0 || (Hq % Hk) || D <= 0 ||
+      (D % 512) || F != 8192 || !tail_att_ok(nb, M, D, Hq, Hk, HD, L))
+    return 0;
+  const int cd = D / 64 / tail::CW, ag = Hq / Hk, rt = M > 8 ? 16 : 8;
+  const bool vs = L <= tail::VSHORT;
+  const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
+  if (2 * F / 16 != 4 * nb || (Hq + 2 * Hk) * HD / 16 > 2 * nb) return 0;
+  // the reference depth decoder: 3072 wide, 8q / 4kv, head_dim 384, 8-slot caches
+  if (cd == 6 && ks2 == 1 && HD == 384 && ag == 2 && vs && !ntl && !knt) return rt == 8 ? 3 : 4;
+  // the 1024-wide depth decoder: 8q / 2kv, head_dim 128, 8-slot caches
+  if (cd == 2 && ks2 == 4 && HD == 128 && ag == 4 && vs && !ntl && !knt) return rt == 8 ? 5 : 6;
+  return 0;
+}
+
+extern "C" int ecd_layer_stack_supported(int M, int D, int F, int Hq, int Hk, int HD, int L,
+                                         int flags) {
+  return stack_kind(tail::device_cus(), M, D, F, Hq, Hk, HD, L, (flags >> 1) & 1,
+                    (flags >> 3) & 1)
+             ? ECD_OK
+             : ECD_ENOTSUP;
+}
+
+extern "C" long ecd_layer_stack_plan_bytes(int nl) {
+  return nl > 0 ? (long)nl * (long)sizeof(tail::LayerRec) : 0;
+}
+
+extern "C" int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, int F, int Hq, int Hk,
+                                    int HD, void* plan, void* stream) {
+  static_assert(sizeof(tail::LayerRec) == 16 * sizeof(void*), "16 pointers per layer");
+  if (!layers || !plan || nl < 1 || nl > ECD_STACK_MAX || M < 1 || M > tail::MR || D <= 0 ||
+      F <= 0 || Hq <= 0 || Hk <= 0 || HD <= 0 || ((uintptr_t)plan & 15))
+    return ECD_EINVAL;
+  const tail::LayerRec* r = (const tail::LayerRec*)layers;
+  auto al = [](const void* p) { return p && ((uintptr_t)p & 15) == 0; };
+  auto apart = [](const void* p, long pb, const void* q, long qb) {
+    const uintptr_t a = (uintptr_t)p, c = (uintptr_t)q;
+    return a + pb <= c || c + qb <= a;
+  };
+  const long bx = 2L * M * D, bm = 2L * M * F, bo = 2L * M * Hq * HD;
+  for (int l = 0; l < nl; ++l) {
+    const tail::LayerRec& e = r[l];
+    if (!al(e.wo) || !e.so || !al(e.n2) || !al(e.w13) || !e.s13 || !al(e.w2) || !e.s2 ||
+        !al(e.x1) || !al(e.mm) || !al(e.xout))
+      return ECD_EINVAL;
+    // every layer but the last runs the next layer's q|k|v and attention (its o_next is the
+    // next layer's o); the last may or may not
+    const bool nxt = e.wq != nullptr;
+    if (l + 1 < nl && (!nxt || !e.o_next)) return ECD_EINVAL;
+    if (nxt && (!al(e.n1) || !al(e.wq) || !e.sq || !e.kc || !e.vc || !al(e.o_next)))
+      return ECD_EINVAL;
+    if (!nxt && e.o_next) return ECD_EINVAL;
+    // a layer's outputs are its own: no two of x1, mm, xout, o_next overlap, here or in any other
+    // layer of the stack
+    const void* out[4] = {e.x1, e.mm, e.xout, e.o_next};
+    const long ob[4] = {bx, bm, bx, bo};
+    for (int k = 0; k <= l; ++k) {
+      const tail::LayerRec& f = r[k];
+      const void* o2[4] = {f.x1, f.mm, f.xout, f.o_next};
+      for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) {
+          if (k == l && j <= i) continue;
+          if (out[i] && o2[j] && !apart(out[i], ob[i], o2[j], ob[j])) return ECD_EINVAL;
+        }
+    }
+  }
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipMemcpyAsync(plan, layers, (size_t)nl * sizeof(tail::LayerRec),
+                                hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  return e == hipSuccess ? ECD_OK : (int)e;
+}
+
+extern "C" int ecd_layer_stack(const void* plan, int nl, const void* o, const void* xin,
+                               const float* rope, const int64_t* pos, void* q, void* sync,
+                               void* err, void* ws, int M, int D, int F, int S, int Hq, int Hk,
+                               int L, int HD, float eps, int flags, void* stream) {
+  auto al = [](const void* p) { return p && ((uintptr_t)p & 15) == 0; };
+  if (!al(plan) || nl < 1 || nl > ECD_STACK_MAX || !al(o) || !al(xin) || !rope || !pos || !q ||
+      !sync || ((uintptr_t)sync & 255) || !err || !al(ws) || S <= 0 || L <= 0 || (HD % 4))
+    return ECD_EINVAL;
+  const int nb = tail::device_cus();
+  const bool ntl = (flags >> 1) & 1, knt = (flags >> 3) & 1;
+  const int kind = stack_kind(nb, M, D, F, Hq, Hk, HD, L, ntl, knt);
+  if (!kind) return ECD_ENOTSUP;
+  if (L <= tail::VSHORT && S > tail::VNEW) return ECD_ENOTSUP;
+  tail::Args a = {};
+  a.o = (const f16*)o; a.xin = (const f16*)xin;
+  a.rope = rope; a.pos = pos; a.q = (f16*)q;
+  a.S = S; a.Hq = Hq; a.Hk = Hk; a.L = L; a.HD = HD;
+  // attention scale: the fp32 rounding of 1 / sqrt(HD) (the reference passes it as a float)
+  a.scale = (float)(1.0 / sqrt((double)HD));
+  a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
+  a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;
+  const tail::LayerRec* pl = (const tail::LayerRec*)plan;
+  hipStream_t st = (hipStream_t)stream;
+  switch (kind) {
+    case 3: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 8, true, false>(a, pl, nl, nb, st);
+    case 4: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 16, true, false>(a, pl, nl, nb, st);
+    case 5: return tail::launch_stack<2, 16, 4, 4, 128, 4, false, 8, true, false>(a, pl, nl, nb, st);
+    case 6: return tail::launch_stack<2, 16, 4, 4, 128, 4, false, 16, true, false>(a, pl, nl, nb, st);
+  }
   return ECD_ENOTSUP;
 }
 

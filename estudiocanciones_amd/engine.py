@@ -37,8 +37,8 @@ import torch
 from . import _ffi
 from .kernels import (_attn, _attn_combine, _rope_cache, _silu_mul, cdiv, embed_gemv_packed,
                       gemm_packed, gemm_silu_packed, gemv_packed_splitk, prefill_attn,
-                      gemm_rope_packed, gemv_packed, int8_mm, layer_head, layer_tail,
-                      layer_tail_supported,
+                      gemm_rope_packed, gemv_packed, int8_mm, layer_head, layer_stack,
+                      layer_stack_plan, layer_stack_supported, layer_tail, layer_tail_supported,
                       layer_tail_ws_bytes, next_power_of_2,
                       pack_i8, rms as krms, rms_gemv_packed, rms_qkv_rope, rms_qkv_rope_rows,
                       rms_w13_silu,
@@ -55,7 +55,14 @@ FRAME_MS = 80
 ATT_SHORT = 128      # caches of at most this many slots: one attention split per (row, kv head)
 ATT_WG = 256        # workgroups the merged attention grid aims at (one per CU of an MI355X)
 ATT_KB_MAX = 16     # workgroups per (row, kv head) pair at most (the last one merges them all)
+STACK_MAX = 64      # layers of one ecd_layer_stack launch at most
 DECODER_RESIDENT = 160 << 20  # weight bytes of a decoder pass kept in the 256 MB Infinity Cache
+
+
+def _overlap(a, b):
+    """True when the storage of tensors a and b overlaps."""
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
 
 
 def attention_kb(R, Hk, L):
@@ -243,6 +250,7 @@ class Stack:
         self.tail_attention = True  # the next layer's attention inside the tail launch
         self.tail_no_wait = False   # tests of the error path: every wait in the launches gives up
         self.tail_kv_nt = False     # the launches' attention reads every cache slot nontemporal
+        self.use_stack = True       # all layer tails of a decode step as one launch where supported
 
     def alloc(self, B, L, dev, dtype):
         self.rope = rope_cache(self.hd, max(L, 16), device=dev)
@@ -283,9 +291,34 @@ class Stack:
             sync = torch.zeros(4096, device=dev, dtype=torch.int32)
             err = torch.zeros(1, device=dev, dtype=torch.int32)
             ws = torch.zeros(-(-wsb // 4), device=dev, dtype=torch.float32)
-        return dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
-                    q=e(b0.h * b0.hd), sync=sync, err=err, ws=ws,
-                    att=att, ob=[e(b0.h * b0.hd), e(b0.h * b0.hd)] if att else None)
+        t = dict(M=M, x1=e(self.dim), mm=e(F), xb=[e(self.dim), e(self.dim)],
+                 q=e(b0.h * b0.hd), sync=sync, err=err, ws=ws,
+                 att=att, ob=[e(b0.h * b0.hd), e(b0.h * b0.hd)] if att else None, plan=None)
+        L0 = b0.kc.shape[2]
+        stream = b0.w13.stream
+        if att and len(self.blocks) <= STACK_MAX and any(
+                layer_stack_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd, L0, stream, nt)
+                for nt in (False, True)):
+            self._stack_buffers(t, M, F, dev, dtype)
+        return t
+
+    def _stack_buffers(self, t, M, F, dev, dtype):
+        """Buffers and plan of the one-launch layer stack (ecd_layer_stack): every layer its own
+        x1, mm, output and attention output (a launch writes no buffer twice), the records of
+        the layers in a device plan."""
+        nl, b0 = len(self.blocks), self.blocks[0]
+        ew = lambda n: torch.empty(nl, M, n, device=dev, dtype=dtype)  # noqa: E731
+        x1s, mms, xs, obs = ew(self.dim), ew(F), ew(self.dim), ew(b0.h * b0.hd)
+        layers = []
+        for i, b in enumerate(self.blocks):
+            nb = self.blocks[i + 1] if i + 1 < nl else None
+            rec = dict(wo=b.o.qp, so=b.o.s8, n2=b.n2, w13=b.w13.qp, s13=b.w13.sp, w2=b.w2.qp,
+                       s2=b.w2.s8, x1=x1s[i], mm=mms[i], xout=xs[i])
+            if nb is not None:
+                rec.update(n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, kc=nb.kc, vc=nb.vc, o_next=obs[i])
+            layers.append(rec)
+        t["plan"] = layer_stack_plan(layers, M, self.dim, F, b0.h, b0.kvh, b0.hd, dev)
+        t["stack"] = dict(x1=x1s, mm=mms, xs=xs, obs=obs)
 
     def tail_error(self):
         """The error word of this stack's layer-tail launches (host sync): nonzero if one timed
@@ -382,9 +415,10 @@ class Stack:
     def _decode_tail(self, x, pos, S, t, o0=None):
         """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
         ecd_layer_head launch where the shapes allow attention in the launch, else on their
-        own; then one ecd_layer_tail launch per layer: the O projection, the MLP, the next
-        layer's rms + q|k|v + RoPE + cache write and (where the shapes allow) that layer's
-        attention, else attention (+ split combine) as its own launches.  Returns the last
+        own; then all layer tails as one ecd_layer_stack launch where supported, else one
+        ecd_layer_tail launch per layer: the O projection, the MLP, the next layer's rms +
+        q|k|v + RoPE + cache write and (where the shapes allow) that layer's attention, else
+        attention (+ split combine) as its own launches.  Returns the last
         layer's output (a buffer of the stack, valid until the next decode call).  With several
         rows per cache (S > 1) the rows of a cache hold consecutive positions.  ``t``: the
         buffers for R rows."""
@@ -405,6 +439,15 @@ class Stack:
             rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
                          b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
             o = self._attention(b0, q, pos, S)
+        L0, F = b0.kc.shape[2], b0.w2.K
+        if att and self.use_stack and t["plan"] is not None and layer_stack_supported(
+                t["M"], self.dim, F, b0.h, b0.kvh, b0.hd, L0, b0.w13.stream, self.tail_kv_nt) \
+                and not any(_overlap(v, u) for v in (x, o) for u in t["stack"].values()):
+            nl = len(self.blocks)
+            return layer_stack(t["plan"], nl, o, x, t["stack"]["xs"][nl - 1], self.rope, pos, q,
+                               t["sync"], t["err"], t["ws"], S, b0.h, b0.kvh, L0, b0.hd, F,
+                               stream=b0.w13.stream, no_wait=self.tail_no_wait,
+                               kv_nt=self.tail_kv_nt)
         for i, b in enumerate(self.blocks):
             nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
             nxt = None if nb is None else nxt_of(nb)

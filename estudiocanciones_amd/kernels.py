@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _ffi
@@ -641,6 +642,73 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
               n2.data_ptr(), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *nargs,
               _ptr(o_next), x1.data_ptr(), mm.data_ptr(), xout.data_ptr(), sync.data_ptr(),
               err.data_ptr(),
+              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
+              _flags(M, stream) | (4 if no_wait else 0) | (8 if kv_nt else 0), stream_ptr(dev))
+    return xout
+
+
+# order of a layer record of ecd_layer_stack (ecd_layer_rec)
+STACK_FIELDS = ("wo", "so", "n2", "w13", "s13", "w2", "s2", "n1", "wq", "sq", "kc", "vc", "x1",
+                "mm", "xout", "o_next")
+
+
+def layer_stack_supported(M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
+    """True when ``layer_stack`` runs these shapes with these weight / cache-load modes."""
+    return _ffi.lib().ecd_layer_stack_supported(
+        int(M), int(D), int(F), int(Hq), int(Hk), int(HD), int(L),
+        (2 if stream else 0) | (8 if kv_nt else 0)) == _ffi.ECD_OK
+
+
+def layer_stack_plan(layers, M, D, F, Hq, Hk, HD, dev):
+    """The device plan of a layer stack: ``layers`` is a list of dicts with the tensors of
+    STACK_FIELDS (n1, wq, sq, kc, vc, o_next None only for the last layer).  The library checks
+    the records (alignment, every layer but the last running the next layer's attention, all
+    outputs disjoint) and copies them to the returned uint8 device tensor."""
+    nl = len(layers)
+    rec = np.zeros((nl, len(STACK_FIELDS)), np.uint64)
+    for i, lay in enumerate(layers):
+        for j, f in enumerate(STACK_FIELDS):
+            t = lay.get(f)
+            rec[i, j] = 0 if t is None else t.data_ptr()
+    nb = int(_ffi.lib().ecd_layer_stack_plan_bytes(nl))
+    plan = torch.empty(max(nb, 16), device=dev, dtype=torch.uint8)
+    _ffi.call("ecd_layer_stack_plan", rec.ctypes.data, nl, M, D, F, Hq, Hk, HD, plan.data_ptr(),
+              stream_ptr(dev))
+    return plan
+
+
+def layer_stack(plan, nl, o, xin, xout, rope, pos, q, sync, err, ws, S, Hq, Hk, L, HD, F,
+                eps=1e-5, stream=False, no_wait=False, kv_nt=False):
+    """The nl layer tails of ``plan`` (layer_stack_plan) as one launch: layer 0 starts from o
+    [M, Hq * HD] and xin [M, D]; each layer's attention output and result feed the next layer.
+    Returns ``xout``, the last layer's output buffer of the plan.  rope, pos, q, sync, err, ws,
+    ``no_wait`` and ``kv_nt`` as for layer_tail (sync, err and ws shared with the stack's other
+    layer-tail launches)."""
+    dev = _dev(o, "layer_stack")
+    M, D = xin.shape
+    for t, n in ((o, "o"), (xin, "xin")):
+        _f16(t, f"layer_stack {n}")
+        if not t.is_contiguous() or t.data_ptr() % 16:
+            raise ValueError(f"layer_stack: {n} must be contiguous and 16-byte aligned")
+    if o.numel() != M * Hq * HD:
+        raise ValueError("layer_stack: o must be [M, Hq * HD]")
+    if pos.dtype != torch.int64 or pos.numel() != M or not pos.is_contiguous():
+        raise ValueError("layer_stack: pos must be contiguous int64 [M]")
+    if q.numel() != M * Hq * HD or not q.is_contiguous():
+        raise ValueError("layer_stack: q must be contiguous [M, Hq * HD]")
+    if rope.shape[0] < L or rope.shape[1] != HD // 2:
+        raise ValueError("layer_stack: rope table must be float32 [>= L, HD/2, 2]")
+    if sync.dtype != torch.int32 or sync.numel() < 4096 or sync.data_ptr() % 256:
+        raise ValueError("layer_stack: sync must be int32 [>= 4096], 256-byte aligned")
+    if err.dtype != torch.int32 or err.numel() < 1:
+        raise ValueError("layer_stack: err must be int32 [1]")
+    if ws.dtype != torch.float32 or ws.data_ptr() % 16 or \
+            ws.numel() * 4 < layer_tail_ws_bytes(D, Hq, Hk, HD):
+        raise ValueError("layer_stack: ws must be float32, 16-byte aligned, layer_tail_ws_bytes")
+    if plan.dtype != torch.uint8 or plan.numel() < int(_ffi.lib().ecd_layer_stack_plan_bytes(nl)):
+        raise ValueError("layer_stack: plan must come from layer_stack_plan for nl layers")
+    _ffi.call("ecd_layer_stack", plan.data_ptr(), nl, o.data_ptr(), xin.data_ptr(),
+              rope.data_ptr(), pos.data_ptr(), q.data_ptr(), sync.data_ptr(), err.data_ptr(),
               ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
               _flags(M, stream) | (4 if no_wait else 0) | (8 if kv_nt else 0), stream_ptr(dev))
     return xout

@@ -2,8 +2,9 @@
  * ecdecode.h -- C ABI of the MI355X (gfx950) per-frame decode path.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t passed as
- * `void* stream` (0 = the null stream).  Nothing allocates, frees or synchronises, so a
- * caller may capture any sequence of these calls into one hipGraph.  Tensors are dense,
+ * `void* stream` (0 = the null stream).  Nothing allocates, frees or synchronises (except the
+ * set-up call ecd_layer_stack_plan, which copies a plan and waits for it), so a caller may
+ * capture any sequence of the other calls into one hipGraph.  Tensors are dense,
  * row-major, fp16 unless stated ("f16" below is IEEE binary16 stored as 16 bits).
  *
  * Return value: 0 on success; ECD_EINVAL (-22) for an argument rejected on the host before
@@ -309,6 +310,57 @@ int ecd_layer_tail_supported(int M, int D, int F, int Hq, int Hk, int HD, int L,
 /* Bytes of the ecd_layer_tail workspace for these shapes on the current device.  No reference
  * counterpart. */
 long ecd_layer_tail_ws_bytes(int D, int Hq, int Hk, int HD);
+
+/* Layer stacks: nl consecutive ecd_layer_tail calls of one decode step as ONE launch (the loop
+ * over layers of app/engine.py:186-210 from layer 0's O projection on).  Layer l's attention
+ * output (its o_next) is layer l + 1's o and its xout is layer l + 1's xin; between layers the
+ * launch's workgroups meet at one more gate instead of a launch boundary, and the next layer's
+ * weights stream during it.  A layer is described by the pointers of ecd_layer_tail that change
+ * from layer to layer, in this order: */
+typedef struct ecd_layer_rec {
+  const void* wo;   /* packed W_O, scales, post-attention norm weights */
+  const void* so;
+  const void* n2;
+  const void* w13;  /* packed row-interleaved w1 | w3, scales; packed w2, scales */
+  const void* s13;
+  const void* w2;
+  const void* s2;
+  const void* n1;   /* the next layer's input norm, packed q|k|v and scales, K/V caches; */
+  const void* wq;   /* NULL (with n1, sq, kc, vc, o_next) only for the stack's last layer */
+  const void* sq;
+  void* kc;
+  void* vc;
+  void* x1;         /* this layer's outputs: [M, D], [M, F], [M, D]; o_next [M, Hq * HD] */
+  void* mm;
+  void* xout;
+  void* o_next;
+} ecd_layer_rec;
+#define ECD_STACK_MAX 64 /* layers per stack */
+
+/* Checks nl records on the host and copies them to plan (device memory of
+ * ecd_layer_stack_plan_bytes(nl) bytes, 16-byte aligned), synchronously on stream.  Every layer
+ * but the last must run the next layer's q|k|v and attention; the outputs x1, mm, xout and
+ * o_next of all layers must be pairwise disjoint (within one launch no buffer is written twice,
+ * so no XCD's L2 can hold an older copy of a line it reads).  No reference counterpart. */
+int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, int F, int Hq, int Hk,
+                         int HD, void* plan, void* stream);
+long ecd_layer_stack_plan_bytes(int nl);
+
+/* ECD_OK when ecd_layer_stack runs these shapes with these flags (bit 1 streamed weights, bit 3
+ * nontemporal cache-slot loads) on the current device: the two depth decoders (3072 wide with
+ * head_dim 384, 1024 wide with head_dim 128; caches of at most 8 slots; up to 16 rows; weights
+ * not streamed).  No reference counterpart. */
+int ecd_layer_stack_supported(int M, int D, int F, int Hq, int Hk, int HD, int L, int flags);
+
+/* One launch for the nl layers of plan (written by ecd_layer_stack_plan): layer 0 starts from o
+ * and xin [M, D]; the result is the last layer's xout.  rope, pos, q, sync, err, ws, the shapes,
+ * eps and flags as for ecd_layer_tail, shared by every layer (err bit 512: an o gate gave up);
+ * q receives the last q|k|v step's queries.  Replaces nl ecd_layer_tail calls; no reference
+ * counterpart as one call. */
+int ecd_layer_stack(const void* plan, int nl, const void* o, const void* xin, const float* rope,
+                    const int64_t* pos, void* q, void* sync, void* err, void* ws, int M, int D,
+                    int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
+                    void* stream);
 
 /* Prompt-pass GEMM (many rows) on packed weights: y = fp16(x @ fp16(q * s)^T) (+ res as an
  * fp16 add) -- the dense numerics of int8_mm for M > 16 (app/kernels.py:46-49), used by the

@@ -176,6 +176,53 @@ def test_host_argument_validation(call):
     assert call(_ffi.lib()) == _ffi.ECD_EINVAL
 
 
+def _stack_records(nl, M=8, D=3072, F=8192, HD=384, Hq=8):
+    """Host layer records of ecd_layer_stack_plan with fake, disjoint, aligned addresses."""
+    import numpy as np
+    rec = np.zeros((nl, 16), np.uint64)
+    base = 1 << 32
+    for i in range(nl):
+        rec[i, :12] = 256                                # weights, norms, caches: any aligned
+        rec[i, 12] = base + i * (1 << 24)                # x1
+        rec[i, 13] = base + i * (1 << 24) + (1 << 20)    # mm
+        rec[i, 14] = base + i * (1 << 24) + (2 << 20)    # xout
+        rec[i, 15] = base + i * (1 << 24) + (3 << 20)    # o_next
+    rec[nl - 1, 7:12] = 0                                # the last layer: no next layer
+    rec[nl - 1, 15] = 0
+    return rec
+
+
+@pytest.mark.parametrize("case", ["nl0", "mid_no_next", "last_o_next_without_wq", "overlap",
+                                  "cross_layer_overlap", "misaligned", "plan_misaligned"])
+def test_layer_stack_plan_rejects_bad_records(case):
+    """ecd_layer_stack_plan checks every record on the host before copying the plan: a middle
+    layer without the next layer's q|k|v and attention, outputs that overlap (within a layer or
+    across layers), unaligned buffers; and ecd_layer_stack rejects a bad layer count."""
+    from estudiocanciones_amd import _ffi
+    L = _ffi.lib()
+    nl = 3
+    rec = _stack_records(nl)
+    plan = 4096
+    if case == "nl0":
+        assert L.ecd_layer_stack(plan, 0, 256, 256, 256, 256, 256, 256, 256, 256, 8, 3072, 8192,
+                                 1, 8, 4, 8, 384, 1e-5, 0, None) == _ffi.ECD_EINVAL
+        return
+    if case == "mid_no_next":
+        rec[1, 8] = 0                        # wq of a middle layer
+    elif case == "last_o_next_without_wq":
+        rec[nl - 1, 15] = rec[nl - 1, 14] + (1 << 16)
+    elif case == "overlap":
+        rec[1, 13] = rec[1, 12] + 64         # mm inside x1
+    elif case == "cross_layer_overlap":
+        rec[2, 14] = rec[0, 15]              # layer 2's xout on layer 0's o_next
+    elif case == "misaligned":
+        rec[0, 12] += 8
+    elif case == "plan_misaligned":
+        plan = 4104
+    rc = L.ecd_layer_stack_plan(rec.ctypes.data, nl, 8, 3072, 8192, 8, 4, 384, plan, None)
+    assert rc == _ffi.ECD_EINVAL
+
+
 def test_python_wrappers_refuse_cpu_tensors():
     """The product path has no CPU fallback: CPU tensors raise instead of computing."""
     import torch
