@@ -105,6 +105,11 @@ struct Args {
   int M, D, F;
   float eps;
   int spin_max;
+  // a layer stack's last layer may end in a codebook head instead of the next layer's q|k|v:
+  // y [M, yn] (row stride yld) = fp16(s_q * (Wq rms(xout, n1))), no attention (y == nullptr:
+  // no head)
+  f16* y;
+  int yn, yld;
 };
 
 // One layer of a stack launch: its weights and buffers (the fields of Args that change from
@@ -126,6 +131,7 @@ struct LayerRec {
   f16* mm;
   f16* xout;
   f16* o_next;
+  f16* y;  // the last layer only: the codebook head's output (wq, sq, n1 its weights and norm)
 };
 
 __device__ __forceinline__ void bar() {
@@ -1203,7 +1209,12 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
   // kv head), on q and the new K/V slots handed off in tagged words; caches
   // longer than ATT_SHORT slots are split over the KB workgroups of each (row, kv head) pair and
   // their 8 compute waves
-  const bool att = AHD > 0 && has_next;
+  // YH: a 1024-wide decoder stack whose last layer may end in the codebook head (a.y set): its
+  // q|k|v step is then the head GEMV on rms(xout, n1) into y, with no attention after it
+  constexpr bool YH = STK && CD == 2 && VS;
+  constexpr int NQ3 = YH ? 3 : 2;  // q|k|v (head) tiles a workgroup may take
+  const bool yh = YH && a.y != nullptr;
+  const bool att = AHD > 0 && has_next && !yh;
 
   // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
   const int TO = D >> 4;
@@ -1212,8 +1223,8 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
   // KS2 == NB), whose partial sums the K-part 0 workgroup adds up
   const int t2 = KS2 == 1 ? (b < TO ? b : -1) : b / KS2;
   const int ks2 = KS2 == 1 ? 0 : b % KS2;
-  const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
-  const int xtra = TQ - NB;
+  const int TQ = !has_next ? 0 : yh ? (a.yn + 15) >> 4 : ((a.Hq + 2 * a.Hk) * a.HD) >> 4;
+  const int xtra = min(TQ, 2 * NB) - NB;
   // The two 16-column tiles whose hand-off words share a 128-byte line (tiles 2j, 2j + 1) go to
   // workgroups 8 apart, i.e. to one XCD: no line is written in pieces from two XCDs, which
   // agent-scope loads could read stale.  A permutation within each aligned block of 16.
@@ -1221,6 +1232,8 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
   const int tq0 = b < TQ ? (b < (TQ & ~15) ? paired(b) : b) : -1;
   const int xb = b - (NB - xtra);  // this workgroup's index among those with a second tile
   const int tq1 = (xtra > 0 && xb >= 0) ? NB + (xb < (xtra & ~15) ? paired(xb) : xb) : -1;
+  // a head's tiles past 2 NB (8197 columns: one) are the first workgroups' third tiles
+  const int tq2 = YH && b < TQ - 2 * NB ? 2 * NB + b : -1;
 
   const int XD = nchD * chb(R);
   unsigned char* xs = smem;
@@ -1248,8 +1261,13 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
     }
   };
   const int c0D = wv * CD, c0F = ks2 * (C2 * CW) + wv * C2;
-  u32x4 wq[2][CD];
-  const int tq_t[2] = {tq0 < 0 ? 0 : tq0, tq1 < 0 ? 0 : tq1};
+  u32x4 wq[NQ3][CD];
+  int tq_t[NQ3];
+  tq_t[0] = tq0 < 0 ? 0 : tq0;
+  tq_t[1] = tq1 < 0 ? 0 : tq1;
+  if constexpr (YH) tq_t[NQ3 - 1] = tq2 < 0 ? 0 : tq2;
+  auto wq2 = [&]() -> u32x4(&)[2][CD] { return *(u32x4(*)[2][CD])wq; };
+  auto tq2_t = [&]() -> const int(&)[2] { return *(const int(*)[2])tq_t; };
   if constexpr (!HEAD) {
     // this wave's slice of the attention output first (the inputs of this launch are final)
     if (!og) dma_rows<CD, R>(a.o, D, M, c0D, xs + c0D * chb(R), lane);
@@ -1310,7 +1328,8 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
 
     // the next layer's q|k|v weights go out during the second gate, into the registers the
     // W13 phase freed (HBM would idle there otherwise)
-    if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+    if (YH && tq2 >= 0) load_w_chunks<NQ3, CD, NTL, 0, CD, LA>(wq, a.wq, tq_t, nchD, c0D, lane);
+    else if (tq1 >= 0) load_w_chunks<2, CD, NTL, 0, CD, LA>(wq2(), a.wq, tq2_t(), nchD, c0D, lane);
     else if (tq0 >= 0)
       load_w_chunks<1, CD, NTL, 0, CD, LA>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
                                            nchD, c0D, lane);
@@ -1349,7 +1368,7 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
       dma_rows<CD, R>(a.xin, D, M, c0D, xs + c0D * chb(R), lane);
       dma_nw<CD>(a.n1, c0D, nws, lane);
       if (tq1 >= 0) {
-        load_w_chunks<2, CD, NTL, 0, CD, 0>(wq, a.wq, tq_t, nchD, c0D, lane);
+        load_w_chunks<2, CD, NTL, 0, CD, 0>(wq2(), a.wq, tq2_t(), nchD, c0D, lane);
         wait_vm<2 * CD>();
       } else if (tq0 >= 0) {
         load_w_chunks<1, CD, NTL, 0, CD, 0>(*(u32x4(*)[1][CD])wq, a.wq, *(const int(*)[1])tq_t,
@@ -1387,12 +1406,16 @@ __device__ __forceinline__ void tail_compute(const Args& a, unsigned char* smem,
     }
     bar();  // S(QKV)
     const float inv = rms_inv<R>(ss, lane, D, a.eps);
-    f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
-    if (tq1 >= 0) mfma_chunks<2, CD, R>(acc, wq, xs, nws, c0D, lane, inv, true);
+    f32x4 acc[NQ3];
+#pragma unroll
+    for (int t = 0; t < NQ3; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (YH && tq2 >= 0) mfma_chunks<NQ3, CD, R>(acc, wq, xs, nws, c0D, lane, inv, true);
+    else if (tq1 >= 0)
+      mfma_chunks<2, CD, R>(*(f32x4(*)[2])acc, wq2(), xs, nws, c0D, lane, inv, true);
     else if (tq0 >= 0)
       mfma_chunks<1, CD, R>(*(f32x4(*)[1])acc, *(u32x4(*)[1][CD])wq, xs, nws, c0D, lane, inv,
                             true);
-    put_partials<2>(psD, acc, wv, lane);
+    put_partials<NQ3>(psD, acc, wv, lane);
     wait_lgkm0();
     bar();  // P(QKV)
   }
@@ -1422,7 +1445,12 @@ __device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, 
   // kv head), on q and the new K/V slots handed off in tagged words; caches
   // longer than ATT_SHORT slots are split over the KB workgroups of each (row, kv head) pair and
   // their 8 compute waves
-  const bool att = AHD > 0 && has_next;
+  // YH: a 1024-wide decoder stack whose last layer may end in the codebook head (a.y set): its
+  // q|k|v step is then the head GEMV on rms(xout, n1) into y, with no attention after it
+  constexpr bool YH = STK && CD == 2 && VS;
+  constexpr int NQ3 = YH ? 3 : 2;  // q|k|v (head) tiles a workgroup may take
+  const bool yh = YH && a.y != nullptr;
+  const bool att = AHD > 0 && has_next && !yh;
 
   // tiles of this workgroup (host: D / 16 <= NB, 2F / 16 == NT13 * NB, TQ <= 2 NB)
   const int TO = D >> 4;
@@ -1431,8 +1459,8 @@ __device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, 
   // KS2 == NB), whose partial sums the K-part 0 workgroup adds up
   const int t2 = KS2 == 1 ? (b < TO ? b : -1) : b / KS2;
   const int ks2 = KS2 == 1 ? 0 : b % KS2;
-  const int TQ = has_next ? ((a.Hq + 2 * a.Hk) * a.HD) >> 4 : 0;
-  const int xtra = TQ - NB;
+  const int TQ = !has_next ? 0 : yh ? (a.yn + 15) >> 4 : ((a.Hq + 2 * a.Hk) * a.HD) >> 4;
+  const int xtra = min(TQ, 2 * NB) - NB;
   // The two 16-column tiles whose hand-off words share a 128-byte line (tiles 2j, 2j + 1) go to
   // workgroups 8 apart, i.e. to one XCD: no line is written in pieces from two XCDs, which
   // agent-scope loads could read stale.  A permutation within each aligned block of 16.
@@ -1440,6 +1468,8 @@ __device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, 
   const int tq0 = b < TQ ? (b < (TQ & ~15) ? paired(b) : b) : -1;
   const int xb = b - (NB - xtra);  // this workgroup's index among those with a second tile
   const int tq1 = (xtra > 0 && xb >= 0) ? NB + (xb < (xtra & ~15) ? paired(xb) : xb) : -1;
+  // a head's tiles past 2 NB (8197 columns: one) are the first workgroups' third tiles
+  const int tq2 = YH && b < TQ - 2 * NB ? 2 * NB + b : -1;
 
   const int XD = nchD * chb(R);
   unsigned char* xs = smem;
@@ -1474,17 +1504,24 @@ __device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, 
     if (t2 >= 0) s2v = *(const f16x4*)(a.s2 + 16 * t2 + cg);
   }
   const int HD = a.HD, L = a.L;
-  const int tq[2] = {tq0, tq1};
-  f16x4 sqv[2] = {};
-  float cs[2][4] = {};
+  const int tq[3] = {tq0, tq1, tq2};
+  f16x4 sqv[NQ3] = {};
+  float cs[NQ3][4] = {};
   long p_raw = 0;
   if (has_next) {
     if (mrow) p_raw = a.pos[me];
     const long pc = p_raw < 0 ? 0 : (p_raw >= L ? L - 1 : p_raw);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NQ3; ++i) {
       if (tq[i] < 0) continue;
       const int nb = 16 * tq[i] + cg;
+      if (yh) {
+        // the head's last tile reaches past its yn columns: clamped scale reads (the columns past
+        // yn are not stored)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sqv[i][r] = a.sq[min(nb + r, a.yn - 1)];
+        continue;
+      }
       sqv[i] = *(const f16x4*)(a.sq + nb);
       const int h = nb / HD, d = nb - h * HD;
       if (h < a.Hq + a.Hk) {
@@ -1619,10 +1656,17 @@ __device__ __forceinline__ void tail_loader(const Args& a, unsigned char* smem, 
     const int NQ = (a.Hq + 2 * a.Hk) * HD;
     uint64_t* hw = (uint64_t*)(a.ws + ws_hand_offset(a, NB));
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NQ3; ++i) {
       if (tq[i] < 0) continue;
-      const f16x4 y = scale4(sum_partials<2>(psD, i, lane), sqv[i]);
+      const f16x4 y = scale4(sum_partials<NQ3>(psD, i, lane), sqv[i]);
       if (!mrow) continue;
+      if (yh) {  // the codebook head: logits of row me, columns nb .. nb + 3 (those below yn)
+        const int nb = 16 * tq[i] + cg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < a.yn) a.y[(long)me * a.yld + nb + r] = y[r];
+        continue;
+      }
       const int nb = 16 * tq[i] + cg;
       const int h = nb / HD, d = nb - h * HD;
       f16x4 o;
@@ -1701,6 +1745,7 @@ __device__ __forceinline__ Args stack_args(const LayerRec* plan, int l) {
   a.w2 = c[l].w2; a.s2 = c[l].s2; a.n1 = c[l].n1; a.wq = c[l].wq; a.sq = c[l].sq;
   a.kc = c[l].kc; a.vc = c[l].vc; a.x1 = c[l].x1; a.mm = c[l].mm; a.xout = c[l].xout;
   a.o_next = c[l].o_next;
+  a.y = c[l].y;
   if (l > 0) {
     a.o = c[l - 1].o_next;
     a.xin = c[l - 1].xout;
@@ -1999,10 +2044,10 @@ extern "C" long ecd_layer_stack_plan_bytes(int nl) {
 }
 
 extern "C" int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, int F, int Hq, int Hk,
-                                    int HD, void* plan, void* stream) {
-  static_assert(sizeof(tail::LayerRec) == 16 * sizeof(void*), "16 pointers per layer");
+                                    int HD, int yld, void* plan, void* stream) {
+  static_assert(sizeof(tail::LayerRec) == 17 * sizeof(void*), "17 pointers per layer");
   if (!layers || !plan || nl < 1 || nl > ECD_STACK_MAX || M < 1 || M > tail::MR || D <= 0 ||
-      F <= 0 || Hq <= 0 || Hk <= 0 || HD <= 0 || ((uintptr_t)plan & 15))
+      F <= 0 || Hq <= 0 || Hk <= 0 || HD <= 0 || yld < 0 || ((uintptr_t)plan & 15))
     return ECD_EINVAL;
   const tail::LayerRec* r = (const tail::LayerRec*)layers;
   auto al = [](const void* p) { return p && ((uintptr_t)p & 15) == 0; };
@@ -2010,28 +2055,35 @@ extern "C" int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, in
     const uintptr_t a = (uintptr_t)p, c = (uintptr_t)q;
     return a + pb <= c || c + qb <= a;
   };
-  const long bx = 2L * M * D, bm = 2L * M * F, bo = 2L * M * Hq * HD;
+  const long bx = 2L * M * D, bm = 2L * M * F, bo = 2L * M * Hq * HD, by = 2L * M * yld;
   for (int l = 0; l < nl; ++l) {
     const tail::LayerRec& e = r[l];
     if (!al(e.wo) || !e.so || !al(e.n2) || !al(e.w13) || !e.s13 || !al(e.w2) || !e.s2 ||
         !al(e.x1) || !al(e.mm) || !al(e.xout))
       return ECD_EINVAL;
     // every layer but the last runs the next layer's q|k|v and attention (its o_next is the
-    // next layer's o); the last may or may not
+    // next layer's o); the last may or may not, or may end in a codebook head (y: the 1024-wide
+    // decoder only, wq / sq / n1 the head's weights and norm, no caches or attention)
     const bool nxt = e.wq != nullptr;
-    if (l + 1 < nl && (!nxt || !e.o_next)) return ECD_EINVAL;
-    if (nxt && (!al(e.n1) || !al(e.wq) || !e.sq || !e.kc || !e.vc || !al(e.o_next)))
-      return ECD_EINVAL;
-    if (!nxt && e.o_next) return ECD_EINVAL;
-    // a layer's outputs are its own: no two of x1, mm, xout, o_next overlap, here or in any other
-    // layer of the stack
-    const void* out[4] = {e.x1, e.mm, e.xout, e.o_next};
-    const long ob[4] = {bx, bm, bx, bo};
+    if (e.y) {
+      if (l + 1 < nl || D != 1024 || yld <= 0 || !al(e.y) || !al(e.n1) || !al(e.wq) || !e.sq || e.kc ||
+          e.vc || e.o_next)
+        return ECD_EINVAL;
+    } else {
+      if (l + 1 < nl && (!nxt || !e.o_next)) return ECD_EINVAL;
+      if (nxt && (!al(e.n1) || !al(e.wq) || !e.sq || !e.kc || !e.vc || !al(e.o_next)))
+        return ECD_EINVAL;
+      if (!nxt && e.o_next) return ECD_EINVAL;
+    }
+    // a layer's outputs are its own: no two of x1, mm, xout, o_next, y overlap, here or in any
+    // other layer of the stack
+    const void* out[5] = {e.x1, e.mm, e.xout, e.o_next, e.y};
+    const long ob[5] = {bx, bm, bx, bo, by};
     for (int k = 0; k <= l; ++k) {
       const tail::LayerRec& f = r[k];
-      const void* o2[4] = {f.x1, f.mm, f.xout, f.o_next};
-      for (int i = 0; i < 4; ++i)
-        for (int j = 0; j < 4; ++j) {
+      const void* o2[5] = {f.x1, f.mm, f.xout, f.o_next, f.y};
+      for (int i = 0; i < 5; ++i)
+        for (int j = 0; j < 5; ++j) {
           if (k == l && j <= i) continue;
           if (out[i] && o2[j] && !apart(out[i], ob[i], o2[j], ob[j])) return ECD_EINVAL;
         }
@@ -2047,15 +2099,19 @@ extern "C" int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, in
 extern "C" int ecd_layer_stack(const void* plan, int nl, const void* o, const void* xin,
                                const float* rope, const int64_t* pos, void* q, void* sync,
                                void* err, void* ws, int M, int D, int F, int S, int Hq, int Hk,
-                               int L, int HD, float eps, int flags, void* stream) {
+                               int L, int HD, int yn, int yld, float eps, int flags,
+                               void* stream) {
   auto al = [](const void* p) { return p && ((uintptr_t)p & 15) == 0; };
   if (!al(plan) || nl < 1 || nl > ECD_STACK_MAX || !al(o) || !al(xin) || !rope || !pos || !q ||
-      !sync || ((uintptr_t)sync & 255) || !err || !al(ws) || S <= 0 || L <= 0 || (HD % 4))
+      !sync || ((uintptr_t)sync & 255) || !err || !al(ws) || S <= 0 || L <= 0 || (HD % 4) ||
+      yn < 0 || yld < yn)
     return ECD_EINVAL;
   const int nb = tail::device_cus();
   const bool ntl = (flags >> 1) & 1, knt = (flags >> 3) & 1;
   const int kind = stack_kind(nb, M, D, F, Hq, Hk, HD, L, ntl, knt);
   if (!kind) return ECD_ENOTSUP;
+  // a codebook head in the last layer: at most three 16-column tiles per workgroup
+  if (yn > 48 * nb) return ECD_ENOTSUP;
   if (L <= tail::VSHORT && S > tail::VNEW) return ECD_ENOTSUP;
   tail::Args a = {};
   a.o = (const f16*)o; a.xin = (const f16*)xin;
@@ -2065,6 +2121,7 @@ extern "C" int ecd_layer_stack(const void* plan, int nl, const void* o, const vo
   a.scale = (float)(1.0 / sqrt((double)HD));
   a.sync = (uint32_t*)sync; a.err = (uint32_t*)err; a.ws = (float*)ws;
   a.M = M; a.D = D; a.F = F; a.eps = eps; a.spin_max = (flags & 4) ? 0 : 1 << 17;
+  a.yn = yn; a.yld = yld;
   const tail::LayerRec* pl = (const tail::LayerRec*)plan;
   hipStream_t st = (hipStream_t)stream;
   switch (kind) {

@@ -308,17 +308,49 @@ class Stack:
         the layers in a device plan."""
         nl, b0 = len(self.blocks), self.blocks[0]
         ew = lambda n: torch.empty(nl, M, n, device=dev, dtype=dtype)  # noqa: E731
-        x1s, mms, xs, obs = ew(self.dim), ew(F), ew(self.dim), ew(b0.h * b0.hd)
+        t["stack"] = dict(x1=ew(self.dim), mm=ew(F), xs=ew(self.dim), obs=ew(b0.h * b0.hd))
+        t["plan"] = layer_stack_plan(self._stack_records(t), M, self.dim, F, b0.h, b0.kvh, b0.hd,
+                                     dev)
+        t["hplans"] = {}
+
+    def _stack_records(self, t):
+        """The layer records of a stack plan over the buffers of t["stack"]."""
+        st, nl = t["stack"], len(self.blocks)
         layers = []
         for i, b in enumerate(self.blocks):
             nb = self.blocks[i + 1] if i + 1 < nl else None
             rec = dict(wo=b.o.qp, so=b.o.s8, n2=b.n2, w13=b.w13.qp, s13=b.w13.sp, w2=b.w2.qp,
-                       s2=b.w2.s8, x1=x1s[i], mm=mms[i], xout=xs[i])
+                       s2=b.w2.s8, x1=st["x1"][i], mm=st["mm"][i], xout=st["xs"][i])
             if nb is not None:
-                rec.update(n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, kc=nb.kc, vc=nb.vc, o_next=obs[i])
+                rec.update(n1=nb.n1, wq=nb.qkv.qp, sq=nb.qkv.s8, kc=nb.kc, vc=nb.vc,
+                           o_next=st["obs"][i])
             layers.append(rec)
-        t["plan"] = layer_stack_plan(layers, M, self.dim, F, b0.h, b0.kvh, b0.hd, dev)
-        t["stack"] = dict(x1=x1s, mm=mms, xs=xs, obs=obs)
+        return layers
+
+    def head_plans(self, heads):
+        """Stack plans that end in a codebook head: ``heads`` maps an index to (packed head
+        Linear, logits buffer [M, N] with 16-byte aligned rows).  The last layer's record then
+        runs rms(xout, stack norm) -> head GEMV into the buffer (the 1024-wide decoder; other
+        stacks keep the head as its own launch).  Used by decode_head."""
+        t = self.tail
+        if t is None or t.get("plan") is None or self.dim != 1024:
+            return
+        b0, F = self.blocks[0], self.blocks[0].w2.K
+        for i, (hd, y) in heads.items():
+            layers = self._stack_records(t)
+            layers[-1].update(n1=self.norm, wq=hd.qp, sq=hd.s8, y=y)
+            t["hplans"][i] = (layer_stack_plan(layers, t["M"], self.dim, F, b0.h, b0.kvh, b0.hd,
+                                               y.device), y)
+
+    def decode_head(self, x, pos, S, head, o0=None):
+        """One decode step whose last layer ends in codebook head ``head`` (head_plans): the
+        logits buffer of that head, or None when the step cannot run as such a stack launch
+        (the caller then runs decode and the head GEMV)."""
+        R = x.shape[0]
+        t = self.tail
+        if t is None or R != t["M"] or head not in t.get("hplans", {}) or not self.use_tail:
+            return None
+        return self._decode_tail(x, pos, S, t, o0, head=head)
 
     def tail_error(self):
         """The error word of this stack's layer-tail launches (host sync): nonzero if one timed
@@ -412,7 +444,7 @@ class Stack:
             x = b.w2(mm, res=x)
         return krms(x, self.norm) if final_norm else x
 
-    def _decode_tail(self, x, pos, S, t, o0=None):
+    def _decode_tail(self, x, pos, S, t, o0=None, head=None):
         """Layer 0's rms + q|k|v + RoPE + cache write and attention run first: one
         ecd_layer_head launch where the shapes allow attention in the launch, else on their
         own; then all layer tails as one ecd_layer_stack launch where supported, else one
@@ -421,7 +453,8 @@ class Stack:
         attention (+ split combine) as its own launches.  Returns the last
         layer's output (a buffer of the stack, valid until the next decode call).  With several
         rows per cache (S > 1) the rows of a cache hold consecutive positions.  ``t``: the
-        buffers for R rows."""
+        buffers for R rows.  ``head``: run the stack plan that ends in that codebook head and
+        return its logits (None when the stack launch cannot run; nothing is launched then)."""
         q = t["q"]
         att = t["att"] and self.tail_attention
 
@@ -430,6 +463,15 @@ class Stack:
                         vc=b.vc, S=S, Hq=b.h, Hk=b.kvh, L=b.kc.shape[2], HD=b.hd)
 
         b0 = self.blocks[0]
+        L0, F = b0.kc.shape[2], b0.w2.K
+
+        def stack_ok(o):
+            return att and self.use_stack and t["plan"] is not None and layer_stack_supported(
+                t["M"], self.dim, F, b0.h, b0.kvh, b0.hd, L0, b0.w13.stream, self.tail_kv_nt) \
+                and not any(_overlap(v, u) for v in (x, o) for u in t["stack"].values())
+
+        if head is not None and not stack_ok(o0 if o0 is not None else t["ob"][1]):
+            return None
         if o0 is not None:
             o = o0
         elif att:
@@ -439,15 +481,13 @@ class Stack:
             rms_qkv_rope(x, b0.n1, b0.qkv.qp, b0.qkv.s8, self.rope, pos, q, b0.kc, b0.vc, S, b0.h,
                          b0.kvh, b0.kc.shape[2], b0.hd, stream=b0.qkv.stream)
             o = self._attention(b0, q, pos, S)
-        L0, F = b0.kc.shape[2], b0.w2.K
-        if att and self.use_stack and t["plan"] is not None and layer_stack_supported(
-                t["M"], self.dim, F, b0.h, b0.kvh, b0.hd, L0, b0.w13.stream, self.tail_kv_nt) \
-                and not any(_overlap(v, u) for v in (x, o) for u in t["stack"].values()):
+        if stack_ok(o):
             nl = len(self.blocks)
-            return layer_stack(t["plan"], nl, o, x, t["stack"]["xs"][nl - 1], self.rope, pos, q,
+            plan, y = t["hplans"][head] if head is not None else (t["plan"], None)
+            return layer_stack(plan, nl, o, x, t["stack"]["xs"][nl - 1], self.rope, pos, q,
                                t["sync"], t["err"], t["ws"], S, b0.h, b0.kvh, L0, b0.hd, F,
                                stream=b0.w13.stream, no_wait=self.tail_no_wait,
-                               kv_nt=self.tail_kv_nt)
+                               kv_nt=self.tail_kv_nt, y=y)
         for i, b in enumerate(self.blocks):
             nb = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
             nxt = None if nb is None else nxt_of(nb)
@@ -617,6 +657,7 @@ class HeartMuLaLite:
         self.graphs = {}
         self.N = self.B = None
         self._next_rows = self._xnext = self._next_qkv = self._onext = None
+        self._hlog = None  # logits buffers of the heads that run inside the decoder's stack
 
     def _embed_audio(self, cb, tok):
         """Embedding of codebook ``cb`` for tokens tok [B, 1] -> [B, D] (app/engine.py:307-308)."""
@@ -680,23 +721,36 @@ class HeartMuLaLite:
         else:
             c0 = pick(0, self._c0(last_h))
             h = self._decode(self._project(c0, 0, even=last_h), self._pass0_pos, 2)[1::2]
+        lg = self._head(0, h)
         for i in range(1, N_CB):
             rows = nxt[i] if nxt is not None and i < N_CB - 1 else None
             qkv = nqkv[i - 1] if rows is not None and nqkv is not None else None
-            ci = pick(i, self._head(i - 1, h), rows, qkv)
+            ci = pick(i, lg, rows, qkv)
             if i < N_CB - 1:
                 x = self._xnext if rows is not None else self._project(ci, i)
-                h = self._decode(x, self._pass_pos[i - 1], 1,
-                                 o0=None if qkv is None else self._onext)
+                lg = self._decode_head(x, self._pass_pos[i - 1], i,
+                                       o0=None if qkv is None else self._onext)
         return samples
+
+    def _packed_decoder(self):
+        return self.audio_head[0].qp is not None and bool(self.decoder.blocks) and \
+            self.decoder.blocks[0].qkv.qp is not None
 
     def _decode(self, x, pos, S, o0=None):
         """Decoder pass; with packed heads the stack's final RMSNorm is left to the head GEMV.
         ``o0``: layer 0's attention output when the sampler ran layer 0 up to it."""
-        if self.audio_head[0].qp is not None and self.decoder.blocks and \
-                self.decoder.blocks[0].qkv.qp is not None:
+        if self._packed_decoder():
             return self.decoder.decode(x, pos, S, final_norm=False, o0=o0)
         return self.decoder.decode(x, pos, S, o0=o0)
+
+    def _decode_head(self, x, pos, i, o0=None):
+        """Decoder pass i (1 .. 6, one row per take) and audio_head[i] of its output: one
+        layer-stack launch that ends in the head where its plan exists, else the pass and the
+        head GEMV."""
+        lg = None
+        if self._hlog is not None:
+            lg = self.decoder.decode_head(x, pos, 1, i, o0=o0)
+        return lg if lg is not None else self._head(i, self._decode(x, pos, 1, o0=o0))
 
     def _logits(self, M, N):
         """[M, N] fp16 logits whose rows start 128-byte aligned (the sampler loads 16 B/lane)."""
@@ -755,6 +809,12 @@ class HeartMuLaLite:
             .view(N_CB - 2, self.B)
         self.backbone.alloc(self.B, L, self.dev, self.dt)
         self.decoder.alloc(self.B, N_CB, self.dev, self.dt)
+        # passes 1 .. 6 end in their codebook head inside the decoder's stack launch where the
+        # stack supports it: one logits buffer per head
+        self._hlog = None
+        if self._packed_decoder():
+            self._hlog = {i: self._logits(self.B, AUDIO_VOCAB) for i in range(1, N_CB - 1)}
+            self.decoder.head_plans({i: (self.audio_head[i], y) for i, y in self._hlog.items()})
         self._alloc_next_rows()
 
     @torch.no_grad()

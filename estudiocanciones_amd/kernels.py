@@ -649,7 +649,7 @@ def layer_tail(o, xin, wo, so, n2, w13, s13, w2, s2, x1, mm, xout, sync, err, ws
 
 # order of a layer record of ecd_layer_stack (ecd_layer_rec)
 STACK_FIELDS = ("wo", "so", "n2", "w13", "s13", "w2", "s2", "n1", "wq", "sq", "kc", "vc", "x1",
-                "mm", "xout", "o_next")
+                "mm", "xout", "o_next", "y")
 
 
 def layer_stack_supported(M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
@@ -661,29 +661,36 @@ def layer_stack_supported(M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
 
 def layer_stack_plan(layers, M, D, F, Hq, Hk, HD, dev):
     """The device plan of a layer stack: ``layers`` is a list of dicts with the tensors of
-    STACK_FIELDS (n1, wq, sq, kc, vc, o_next None only for the last layer).  The library checks
-    the records (alignment, every layer but the last running the next layer's attention, all
-    outputs disjoint) and copies them to the returned uint8 device tensor."""
+    STACK_FIELDS (n1, wq, sq, kc, vc, o_next None only for the last layer; ``y``, a [M, N] view
+    with 16-byte aligned rows, only in the last layer of a 1024-wide stack: it then ends in a
+    codebook head with n1, wq, sq the head's norm, packed weights and scales, and no caches).
+    The library checks the records (alignment, every layer but the last running the next layer's
+    attention, all outputs disjoint) and copies them to the returned uint8 device tensor."""
     nl = len(layers)
     rec = np.zeros((nl, len(STACK_FIELDS)), np.uint64)
     for i, lay in enumerate(layers):
         for j, f in enumerate(STACK_FIELDS):
             t = lay.get(f)
             rec[i, j] = 0 if t is None else t.data_ptr()
+    y = layers[-1].get("y")
+    yld = 0 if y is None else y.stride(0)
+    if y is not None and (y.stride(1) != 1 or yld % 8 or y.shape[0] != M):
+        raise ValueError("layer_stack_plan: y must be [M, N], unit column stride, 16-byte rows")
     nb = int(_ffi.lib().ecd_layer_stack_plan_bytes(nl))
     plan = torch.empty(max(nb, 16), device=dev, dtype=torch.uint8)
-    _ffi.call("ecd_layer_stack_plan", rec.ctypes.data, nl, M, D, F, Hq, Hk, HD, plan.data_ptr(),
-              stream_ptr(dev))
+    _ffi.call("ecd_layer_stack_plan", rec.ctypes.data, nl, M, D, F, Hq, Hk, HD, yld,
+              plan.data_ptr(), stream_ptr(dev))
     return plan
 
 
 def layer_stack(plan, nl, o, xin, xout, rope, pos, q, sync, err, ws, S, Hq, Hk, L, HD, F,
-                eps=1e-5, stream=False, no_wait=False, kv_nt=False):
+                eps=1e-5, stream=False, no_wait=False, kv_nt=False, y=None):
     """The nl layer tails of ``plan`` (layer_stack_plan) as one launch: layer 0 starts from o
     [M, Hq * HD] and xin [M, D]; each layer's attention output and result feed the next layer.
-    Returns ``xout``, the last layer's output buffer of the plan.  rope, pos, q, sync, err, ws,
-    ``no_wait`` and ``kv_nt`` as for layer_tail (sync, err and ws shared with the stack's other
-    layer-tail launches)."""
+    Returns ``xout``, the last layer's output buffer of the plan, or ``y``, the logits of a plan
+    that ends in a codebook head (the plan's y).  rope, pos, q, sync, err, ws, ``no_wait`` and
+    ``kv_nt`` as for layer_tail (sync, err and ws shared with the stack's other layer-tail
+    launches)."""
     dev = _dev(o, "layer_stack")
     M, D = xin.shape
     for t, n in ((o, "o"), (xin, "xin")):
@@ -709,9 +716,10 @@ def layer_stack(plan, nl, o, xin, xout, rope, pos, q, sync, err, ws, S, Hq, Hk, 
         raise ValueError("layer_stack: plan must come from layer_stack_plan for nl layers")
     _ffi.call("ecd_layer_stack", plan.data_ptr(), nl, o.data_ptr(), xin.data_ptr(),
               rope.data_ptr(), pos.data_ptr(), q.data_ptr(), sync.data_ptr(), err.data_ptr(),
-              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, float(eps),
+              ws.data_ptr(), M, D, F, S, Hq, Hk, L, HD, 0 if y is None else y.shape[1],
+              0 if y is None else y.stride(0), float(eps),
               _flags(M, stream) | (4 if no_wait else 0) | (8 if kv_nt else 0), stream_ptr(dev))
-    return xout
+    return xout if y is None else y
 
 
 def layer_head(x, nxt, o_next, F, sync, err, ws, eps=1e-5, stream=False, no_wait=False,

@@ -334,16 +334,19 @@ typedef struct ecd_layer_rec {
   void* mm;
   void* xout;
   void* o_next;
-} ecd_layer_rec;
+  void* y;          /* the last layer of a 1024-wide stack only, or NULL: it ends in a codebook */
+} ecd_layer_rec;    /* head, y [M, yn] (row stride yld) = fp16(s * (w rms(xout, n1))) with n1, */
+                    /* wq, sq the head's norm, packed weights and scales (no kc, vc, o_next) */
 #define ECD_STACK_MAX 64 /* layers per stack */
 
 /* Checks nl records on the host and copies them to plan (device memory of
  * ecd_layer_stack_plan_bytes(nl) bytes, 16-byte aligned), synchronously on stream.  Every layer
- * but the last must run the next layer's q|k|v and attention; the outputs x1, mm, xout and
- * o_next of all layers must be pairwise disjoint (within one launch no buffer is written twice,
- * so no XCD's L2 can hold an older copy of a line it reads).  No reference counterpart. */
+ * but the last must run the next layer's q|k|v and attention; the outputs x1, mm, xout, o_next
+ * and y of all layers must be pairwise disjoint (within one launch no buffer is written twice,
+ * so no XCD's L2 can hold an older copy of a line it reads); yld: the row stride of y (0: no
+ * head).  No reference counterpart. */
 int ecd_layer_stack_plan(const void* layers, int nl, int M, int D, int F, int Hq, int Hk,
-                         int HD, void* plan, void* stream);
+                         int HD, int yld, void* plan, void* stream);
 long ecd_layer_stack_plan_bytes(int nl);
 
 /* ECD_OK when ecd_layer_stack runs these shapes with these flags (bit 1 streamed weights, bit 3
@@ -353,14 +356,15 @@ long ecd_layer_stack_plan_bytes(int nl);
 int ecd_layer_stack_supported(int M, int D, int F, int Hq, int Hk, int HD, int L, int flags);
 
 /* One launch for the nl layers of plan (written by ecd_layer_stack_plan): layer 0 starts from o
- * and xin [M, D]; the result is the last layer's xout.  rope, pos, q, sync, err, ws, the shapes,
- * eps and flags as for ecd_layer_tail, shared by every layer (err bit 512: an o gate gave up);
- * q receives the last q|k|v step's queries.  Replaces nl ecd_layer_tail calls; no reference
- * counterpart as one call. */
+ * and xin [M, D]; the result is the last layer's xout (and, with a head record, its logits y:
+ * yn columns, row stride yld; yn = 0 without).  rope, pos, q, sync, err, ws, the shapes, eps
+ * and flags as for ecd_layer_tail, shared by every layer (err bit 512: an o gate gave up); q
+ * receives the last q|k|v step's queries.  Replaces nl ecd_layer_tail calls (and the head's
+ * ecd_rms_gemv_i8p); no reference counterpart as one call. */
 int ecd_layer_stack(const void* plan, int nl, const void* o, const void* xin, const float* rope,
                     const int64_t* pos, void* q, void* sync, void* err, void* ws, int M, int D,
-                    int F, int S, int Hq, int Hk, int L, int HD, float eps, int flags,
-                    void* stream);
+                    int F, int S, int Hq, int Hk, int L, int HD, int yn, int yld, float eps,
+                    int flags, void* stream);
 
 /* Prompt-pass GEMM (many rows) on packed weights: y = fp16(x @ fp16(q * s)^T) (+ res as an
  * fp16 add) -- the dense numerics of int8_mm for M > 16 (app/kernels.py:46-49), used by the

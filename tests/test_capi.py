@@ -179,7 +179,7 @@ def test_host_argument_validation(call):
 def _stack_records(nl, M=8, D=3072, F=8192, HD=384, Hq=8):
     """Host layer records of ecd_layer_stack_plan with fake, disjoint, aligned addresses."""
     import numpy as np
-    rec = np.zeros((nl, 16), np.uint64)
+    rec = np.zeros((nl, 17), np.uint64)
     base = 1 << 32
     for i in range(nl):
         rec[i, :12] = 256                                # weights, norms, caches: any aligned
@@ -193,7 +193,9 @@ def _stack_records(nl, M=8, D=3072, F=8192, HD=384, Hq=8):
 
 
 @pytest.mark.parametrize("case", ["nl0", "mid_no_next", "last_o_next_without_wq", "overlap",
-                                  "cross_layer_overlap", "misaligned", "plan_misaligned"])
+                                  "cross_layer_overlap", "misaligned", "plan_misaligned",
+                                  "head_not_last", "head_3072_wide", "head_with_cache",
+                                  "head_overlaps"])
 def test_layer_stack_plan_rejects_bad_records(case):
     """ecd_layer_stack_plan checks every record on the host before copying the plan: a middle
     layer without the next layer's q|k|v and attention, outputs that overlap (within a layer or
@@ -205,7 +207,7 @@ def test_layer_stack_plan_rejects_bad_records(case):
     plan = 4096
     if case == "nl0":
         assert L.ecd_layer_stack(plan, 0, 256, 256, 256, 256, 256, 256, 256, 256, 8, 3072, 8192,
-                                 1, 8, 4, 8, 384, 1e-5, 0, None) == _ffi.ECD_EINVAL
+                                 1, 8, 4, 8, 384, 0, 0, 1e-5, 0, None) == _ffi.ECD_EINVAL
         return
     if case == "mid_no_next":
         rec[1, 8] = 0                        # wq of a middle layer
@@ -219,7 +221,20 @@ def test_layer_stack_plan_rejects_bad_records(case):
         rec[0, 12] += 8
     elif case == "plan_misaligned":
         plan = 4104
-    rc = L.ecd_layer_stack_plan(rec.ctypes.data, nl, 8, 3072, 8192, 8, 4, 384, plan, None)
+    D, yld = 3072, 0
+    if case.startswith("head"):
+        D, yld = 1024, 8256
+        rec[nl - 1, 7:10] = 256                          # the head's norm, weights, scales
+        rec[nl - 1, 16] = (1 << 40)                      # y
+        if case == "head_not_last":
+            rec[0, 16] = (1 << 41)
+        elif case == "head_3072_wide":
+            D = 3072
+        elif case == "head_with_cache":
+            rec[nl - 1, 10] = 256
+        elif case == "head_overlaps":
+            rec[nl - 1, 16] = rec[1, 12]                 # y on a layer's x1
+    rc = L.ecd_layer_stack_plan(rec.ctypes.data, nl, 8, D, 8192, 8, 4, 384, yld, plan, None)
     assert rc == _ffi.ECD_EINVAL
 
 
