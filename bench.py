@@ -359,11 +359,13 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
         if name == "ecd_layer_stack":
             # nl layer tails in one launch: every layer's O, MLP, and all but the last layer's
             # next-layer rms -> q|k|v (their attention is counted by tail_attn_bytes)
-            nl, M, D, F, Hq, Hk, HD = a[1], a[10], a[11], a[12], a[14], a[15], a[17]
+            # (and, with a codebook head in the last layer, yn = a[18] > 0: its RMS-prologue GEMV)
+            nl, M, D, F, Hq, Hk, HD, yn = a[1], a[10], a[11], a[12], a[14], a[15], a[17], a[18]
             b = (D * D + 2 * D + 6 * M * D) + (2 * F * D + 4 * F + 2 * M * D + 2 * D + 2 * M * F) \
                 + (D * F + 2 * D + 2 * M * F + 4 * M * D)
             Nq = (Hq + 2 * Hk) * HD
-            return nl * b + (nl - 1) * (Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD)
+            hb = yn * D + 2 * yn + 2 * M * D + 2 * D + 2 * M * yn if yn else 0
+            return nl * b + (nl - 1) * (Nq * D + 2 * Nq + 2 * M * D + 2 * D + 2 * M * Nq + 4 * M * HD) + hb
         if name == "ecd_layer_head":
             # rms -> q|k|v of layer 0 (its attention is counted by tail_attn_bytes)
             M, D, Hq, Hk, HD = a[13], a[14], a[17], a[18], a[20]
