@@ -37,9 +37,14 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
 
 
+# per-file additions: the layer-stack launch keeps constants and addresses inside its layer loop
+# (hoisted out of it, they would hold registers across every layer)
+FILE_FLAGS = {"layer_stack.hip": ["-mllvm", "-disable-machine-licm"]}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJDIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
