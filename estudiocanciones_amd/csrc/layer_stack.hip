@@ -5,11 +5,10 @@
 
 using namespace ecd;
 
-// Stack launches: the instantiated shapes, the depth decoders' (their layers are short, so the
-// launch boundary is a large part of each).  The backbone keeps one launch per layer: looped over
-// its layers, its 3072-wide tail with the MFMA attention needs more than the 168 registers a
-// lane has at three waves per SIMD, and the spills cost more than the boundaries.  0: not
-// instantiated, else an index for ecd_layer_stack's dispatch.
+// Stack launches: the instantiated shapes.  The depth decoders take all their layers in one
+// launch; the backbone takes two layers per launch, unrolled (looped over its layers, its
+// 3072-wide tail with the MFMA attention needs more than the 168 registers a lane has at three
+// waves per SIMD).  0: not instantiated, else an index for ecd_layer_stack's dispatch.
 static int stack_kind(int nb, int M, int D, int F, int Hq, int Hk, int HD, int L, bool ntl, bool knt) {
   if (nb <= 0 || (nb % 8) || M < 1 || M > tail::MR || Hk <= 0 || (Hq % Hk) || D <= 0 ||
       (D % 512) || F != 8192 || !tail_att_ok(nb, M, D, Hq, Hk, HD, L))
@@ -18,6 +17,8 @@ static int stack_kind(int nb, int M, int D, int F, int Hq, int Hk, int HD, int L
   const bool vs = L <= tail::VSHORT;
   const int ks2 = (nb % (D / 16) == 0 && nb / (D / 16) == 4) ? 4 : 1;
   if (2 * F / 16 != 4 * nb || (Hq + 2 * Hk) * HD / 16 > 2 * nb) return 0;
+  // the backbone: 3072 wide, 24q / 8kv, head_dim 128, streamed weights, up to 8 rows
+  if (cd == 6 && ks2 == 1 && HD == 128 && ag == 3 && rt == 8 && !vs && ntl) return knt ? 2 : 1;
   // the reference depth decoder: 3072 wide, 8q / 4kv, head_dim 384, 8-slot caches
   if (cd == 6 && ks2 == 1 && HD == 384 && ag == 2 && vs && !ntl && !knt) return rt == 8 ? 3 : 4;
   // the 1024-wide depth decoder: 8q / 2kv, head_dim 128, 8-slot caches
@@ -25,10 +26,15 @@ static int stack_kind(int nb, int M, int D, int F, int Hq, int Hk, int HD, int L
   return 0;
 }
 
-extern "C" int ecd_layer_stack_supported(int M, int D, int F, int Hq, int Hk, int HD, int L,
-                                         int flags) {
-  switch (stack_kind(tail::device_cus(), M, D, F, Hq, Hk, HD, L, (flags >> 1) & 1,
-                     (flags >> 3) & 1)) {
+extern "C" int ecd_layer_stack_supported(int nl, int M, int D, int F, int Hq, int Hk, int HD,
+                                         int L, int flags) {
+  const int kind = stack_kind(tail::device_cus(), M, D, F, Hq, Hk, HD, L, (flags >> 1) & 1,
+                              (flags >> 3) & 1);
+  // the backbone's two-layer launches take an even number of layers
+  if (nl < 1 || nl > ECD_STACK_MAX || ((kind == 1 || kind == 2) && nl % 2)) return ECD_ENOTSUP;
+  switch (kind) {
+    case 1: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, false, 2>() ? ECD_OK : ECD_ENOTSUP;
+    case 2: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, true, 2>() ? ECD_OK : ECD_ENOTSUP;
     case 3: return tail::stack_scratch_free<6, 16, 4, 1, 384, 2, false, 8, true, false>() ? ECD_OK : ECD_ENOTSUP;
     case 4: return tail::stack_scratch_free<6, 16, 4, 1, 384, 2, false, 16, true, false>() ? ECD_OK : ECD_ENOTSUP;
     case 5: return tail::stack_scratch_free<2, 16, 4, 4, 128, 4, false, 8, true, false>() ? ECD_OK : ECD_ENOTSUP;
@@ -123,6 +129,8 @@ extern "C" int ecd_layer_stack(const void* plan, int nl, const void* o, const vo
   const tail::LayerRec* pl = (const tail::LayerRec*)plan;
   hipStream_t st = (hipStream_t)stream;
   switch (kind) {
+    case 1: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, false, 2>(a, pl, nl, nb, st);
+    case 2: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, true, 2>(a, pl, nl, nb, st);
     case 3: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 8, true, false>(a, pl, nl, nb, st);
     case 4: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 16, true, false>(a, pl, nl, nb, st);
     case 5: return tail::launch_stack<2, 16, 4, 4, 128, 4, false, 8, true, false>(a, pl, nl, nb, st);

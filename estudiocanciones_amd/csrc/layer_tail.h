@@ -1747,7 +1747,7 @@ __device__ __forceinline__ Args stack_args(const LayerRec* plan, int l) {
   a.kc = c[l].kc; a.vc = c[l].vc; a.x1 = c[l].x1; a.mm = c[l].mm; a.xout = c[l].xout;
   a.o_next = c[l].o_next;
   a.y = c[l].y;
-  if (l > 0) {
+  if (l > 0 || a.o == nullptr) {  // (l = 0 without o: a later part of a longer plan)
     a.o = c[l - 1].o_next;
     a.xin = c[l - 1].xout;
   }
@@ -1759,7 +1759,10 @@ __device__ __forceinline__ Args stack_args(const LayerRec* plan, int l) {
 // more gate (o complete) instead of a launch boundary, and the next layer's O and first W13
 // weights stream while they wait.  Every activation buffer of a stack is its layer's own, so no
 // XCD's L2 holds a line of one before its writers have finished it.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT>
+// NLU > 0: exactly NLU layers, unrolled (straight-line code: no layer loop whose
+// loop-invariant values would be held in registers across it); nl is then NLU.
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT,
+          int NLU = 0>
 __global__ __launch_bounds__(NTHR) void layer_stack_kernel(const Args a0,
                                                            const LayerRec* __restrict__ plan,
                                                            int nl) {
@@ -1767,17 +1770,27 @@ __global__ __launch_bounds__(NTHR) void layer_stack_kernel(const Args a0,
   __shared__ uint32_t s_epoch;
   if (threadIdx.x < CW * 64) {
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for (int l = 0; l < nl; ++l)
+    auto layer = [&](int l) __attribute__((always_inline)) {
       tail_compute<CD, CF, NT13, KS2, AHD, AG, NTL, false, R, VS, KNT, true>(
           stack_args(plan, l), smem, s_epoch, l > 0, wv);
+    };
+    if constexpr (NLU > 0)
+      static_for<NLU>([&](auto lc) { layer(decltype(lc)::value); });
+    else
+      for (int l = 0; l < nl; ++l) layer(l);
     return;
   }
   const bool ld0 = threadIdx.x == CW * 64;
   uint32_t go = 0, bad = 0;
   if (ld0) go = ld_sc1(a0.sync + GATE_FLAGS + 32 * 8 * (blockIdx.x & 7));
-  for (int l = 0; l < nl; ++l)
+  auto layer = [&](int l) __attribute__((always_inline)) {
     tail_loader<CD, CF, NT13, KS2, AHD, AG, NTL, false, R, VS, KNT, true>(
         stack_args(plan, l), smem, s_epoch, go, bad, l > 0);
+  };
+  if constexpr (NLU > 0)
+    static_for<NLU>([&](auto lc) { layer(decltype(lc)::value); });
+  else
+    for (int l = 0; l < nl; ++l) layer(l);
   if (ld0 && bad) flag_err(a0.err, bad);
 }
 
@@ -1836,26 +1849,41 @@ int launch(const Args& a, int nb, hipStream_t st) {
 // A stack instantiation runs only if its code needs no scratch memory: the dispatcher may hold
 // back waves whose scratch is not yet available, and a persistent launch must have every
 // workgroup resident (register spills would also break its pipelined weight stream).  Cached.
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT>
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT,
+          int NLU = 0>
 bool stack_scratch_free() {
   static int ok = -1;
   if (ok < 0) {
     hipFuncAttributes fa;
-    const auto fn = layer_stack_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT>;
+    const auto fn = layer_stack_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT, NLU>;
     ok = hipFuncGetAttributes(&fa, (const void*)fn) == hipSuccess && fa.localSizeBytes == 0;
   }
   return ok;
 }
 
-template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT>
+// NLU > 0: the nl layers as nl / NLU launches of NLU layers each (the parts after the first
+// take their o and xin from the record before them: Args o == nullptr).
+template <int CD, int CF, int NT13, int KS2, int AHD, int AG, bool NTL, int R, bool VS, bool KNT,
+          int NLU = 0>
 int launch_stack(const Args& a, const LayerRec* plan, int nl, int nb, hipStream_t st) {
-  if (!stack_scratch_free<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT>()) return ECD_ENOTSUP;
+  if (NLU > 0 && nl % NLU) return ECD_ENOTSUP;
+  if (!stack_scratch_free<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT, NLU>()) return ECD_ENOTSUP;
   const int lds = tail_lds<CD, CF, NT13, KS2, AHD, AG, R, VS>(a.D);
   static int attr = 0;
-  const auto fn = layer_stack_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT>;
+  const auto fn = layer_stack_kernel<CD, CF, NT13, KS2, AHD, AG, NTL, R, VS, KNT, NLU>;
   if (const int rc = raise_lds((const void*)fn, lds, attr)) return rc;
-  hipLaunchKernelGGL(fn, dim3(nb), dim3(NTHR), lds, st, a, plan, nl);
-  return ecd_launch_status();
+  if constexpr (NLU == 0) {
+    hipLaunchKernelGGL(fn, dim3(nb), dim3(NTHR), lds, st, a, plan, nl);
+    return ecd_launch_status();
+  } else {
+    Args ak = a;
+    for (int k = 0; k < nl; k += NLU) {
+      if (k > 0) ak.o = ak.xin = nullptr;
+      hipLaunchKernelGGL(fn, dim3(nb), dim3(NTHR), lds, st, ak, plan + k, NLU);
+      if (const int rc = ecd_launch_status()) return rc;
+    }
+    return 0;
+  }
 }
 
 }  // namespace tail

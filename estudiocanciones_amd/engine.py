@@ -297,7 +297,8 @@ class Stack:
         L0 = b0.kc.shape[2]
         stream = b0.w13.stream
         if att and len(self.blocks) <= STACK_MAX and any(
-                layer_stack_supported(M, self.dim, F, b0.h, b0.kvh, b0.hd, L0, stream, nt)
+                layer_stack_supported(len(self.blocks), M, self.dim, F, b0.h, b0.kvh, b0.hd, L0,
+                                      stream, nt)
                 for nt in (False, True)):
             self._stack_buffers(t, M, F, dev, dtype)
         return t
@@ -467,7 +468,8 @@ class Stack:
 
         def stack_ok(o):
             return att and self.use_stack and t["plan"] is not None and layer_stack_supported(
-                t["M"], self.dim, F, b0.h, b0.kvh, b0.hd, L0, b0.w13.stream, self.tail_kv_nt) \
+                len(self.blocks), t["M"], self.dim, F, b0.h, b0.kvh, b0.hd, L0, b0.w13.stream,
+                self.tail_kv_nt) \
                 and not any(_overlap(v, u) for v in (x, o) for u in t["stack"].values())
 
         if head is not None and not stack_ok(o0 if o0 is not None else t["ob"][1]):

@@ -652,10 +652,11 @@ STACK_FIELDS = ("wo", "so", "n2", "w13", "s13", "w2", "s2", "n1", "wq", "sq", "k
                 "mm", "xout", "o_next", "y")
 
 
-def layer_stack_supported(M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
-    """True when ``layer_stack`` runs these shapes with these weight / cache-load modes."""
+def layer_stack_supported(nl, M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
+    """True when ``layer_stack`` runs nl layers of these shapes with these weight / cache-load
+    modes."""
     return _ffi.lib().ecd_layer_stack_supported(
-        int(M), int(D), int(F), int(Hq), int(Hk), int(HD), int(L),
+        int(nl), int(M), int(D), int(F), int(Hq), int(Hk), int(HD), int(L),
         (2 if stream else 0) | (8 if kv_nt else 0)) == _ffi.ECD_OK
 
 
