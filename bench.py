@@ -140,6 +140,14 @@ def is_backbone_tail(name):
                 or re.search(r"layer_tail_kernelILi6E(Li\d+E){5}Lb[01]ELb0ELi\d+E", name))
 
 
+def is_backbone_stack(name):
+    """rocprofv3 kernel name of the backbone's layer-stack kernel (CD = 6, head_dim 128: several
+    backbone layer tails per launch)."""
+    import re
+    return bool(re.search(r"layer_stack_kernel<6, (\d+, ){3}128, 3, ", name)
+                or re.search(r"layer_stack_kernelILi6E(Li\d+E){3}Li128ELi3E", name))
+
+
 def kernel_class(name):
     """Short class name of a rocprofv3 kernel name: template arguments kept, parameter list and
     return type dropped (demangled names), or the mangled name as it stands."""
@@ -168,7 +176,9 @@ def pmc_summary(fetch_csv, write_csv, calib_mib):
     out, factors, by_class = {}, {}, {}
     for tag, path, counter in (("fetch", fetch_csv, "FETCH_SIZE"), ("write", write_csv, "WRITE_SIZE")):
         rows = per_dispatch(path, counter)
-        tail = [v for n, v in rows if is_backbone_tail(n)]
+        # the backbone's dominant launch: its layer-stack kernel where it runs, else its tail
+        tail = [v for n, v in rows if is_backbone_stack(n)] or \
+            [v for n, v in rows if is_backbone_tail(n)]
         copy = [v for n, v in rows if "copy_bytes_kernel" in n]
         if not tail or not copy:
             raise SystemExit(f"{path}: no backbone layer-tail or calibration-copy dispatches with "
@@ -409,13 +419,26 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
 
     g_ms_launch = time_graph([relaunch(n, a) for n, a, _ in gemv_calls], torch)
     g_ms_total = g_ms_launch * len(gemv_calls)
-    # the dominant kernel: the backbone's layer-tail launches (recognised by their O-projection
-    # weights: the reference decoder's tails are 3072 wide too), all of one shape
+    # the dominant kernel: the backbone's layer-stack launches (one call of the 28 layers, 7 per
+    # kernel launch; recognised by the backbone's plan), or its layer-tail launches (recognised
+    # by their O-projection weights: the reference decoder's tails are 3072 wide too)
+    bb_plans = {t["plan"].data_ptr() for t in (model.backbone.tail, model.backbone.tail2)
+                if t is not None and t.get("plan") is not None}
+    bs = [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_stack" and a[0] in bb_plans]
     bb_wo = {b.o.qp.data_ptr() for b in model.backbone.blocks}
-    bt = [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_tail" and a[2] in bb_wo]
-    bt_ms = time_graph([relaunch(n, a) for n, a, _ in bt], torch) if bt else None
-    bt_bytes = sum(b for _, _, b in bt) / len(bt) if bt else None
-    bt_att = bool(bt) and bool(bt[0][1][17])
+    bt = bs or [(n, a, b) for n, a, b in gemv_calls if n == "ecd_layer_tail" and a[2] in bb_wo]
+    # kernel launches per recorded call (a stack call of nl layers: nl / layers-per-launch)
+    from estudiocanciones_amd.kernels import layer_stack_layers_per_launch as lpl
+    bt_k = [1 if n == "ecd_layer_tail" else
+            a[1] // lpl(a[1], a[10], a[11], a[12], a[14], a[15], a[17], a[16], bool(a[21] & 2),
+                        bool(a[21] & 8))
+            for n, a, _ in bt]
+    bt_ms = time_graph([relaunch(n, a) for n, a, _ in bt], torch) * len(bt) / sum(bt_k) \
+        if bt else None
+    bt_bytes = sum(b for _, _, b in bt) / sum(bt_k) if bt else None
+    bt_att = bool(bt) and (bool(bs) or bool(bt[0][1][17]))
+    bt_stack = bool(bs)
+    bt_lpl = bs[0][1][1] // bt_k[0] if bs else 1
     bb_idx = [i for i, b in enumerate(attn_b) if b > 10e6]
     # (no standalone attention launch is left when every layer's attention runs in a launch)
     a_ms_launch = time_graph([relaunch(*c) for c in attn_calls], torch) if attn_calls else 0.0
@@ -433,7 +456,8 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
                 bb_attn_gbps=bb_attn_gbps, gemv_b=gemv_b, attn_b=attn_b, g_avg_us=g_avg_us,
                 g_bytes_avg=g_bytes_avg, g_ms_total=g_ms_total, a_ms_total=a_ms_total,
                 a_ms_launch=a_ms_launch, frame_bytes=frame_bytes, launches=launches,
-                bt_ms=bt_ms, bt_bytes=bt_bytes, bt_n=len(bt), bt_att=bt_att)
+                bt_ms=bt_ms, bt_bytes=bt_bytes, bt_n=sum(bt_k), bt_att=bt_att, bt_stack=bt_stack,
+                bt_lpl=bt_lpl)
 
 
 def roofline_entry(pt, traffic):
@@ -446,16 +470,19 @@ def roofline_entry(pt, traffic):
     ach = pt["bt_bytes"] / (pt["bt_ms"] * 1e-3) / 1e9
     what = "O + MLP + next layer's rms+q|k|v+RoPE" + (" + its decode attention"
                                                       if pt["bt_att"] else "")
+    kern = (f"layer_stack_kernel, backbone width 3072, {pt['bt_lpl']} layers per launch (each "
+            f"{what})" if pt.get("bt_stack") else f"layer_tail_kernel, backbone width 3072 ({what})")
     return {
         "bound": "hbm",
-        "kernel": f"layer_tail_kernel, backbone width 3072 ({what})",
+        "kernel": kern,
         "achieved": round(ach, 1),
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(ach / HBM_PEAK_GBPS, 4),
         "traffic": traffic,
-        "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per backbone layer-tail dispatch, "
-                           "copy-calibrated (profiles/frame_traffic_b8_kv750.json)")
+        "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE per backbone layer-stack (or "
+                           "layer-tail) dispatch, copy-calibrated "
+                           "(profiles/frame_traffic_b8_kv750.json)")
                           if traffic else None,
         "avg_launch_us": round(pt["bt_ms"] * 1e3, 3),
         "algorithmic_bytes_per_launch": int(pt["bt_bytes"]),
@@ -592,8 +619,9 @@ def main():
         "tokens_per_s": round(fps * E.N_CB * n, 1),
         "roofline": roofline_entry(main_pt, traffic),
         "gemv_family": {
-            "kernels": ("every int8-weight GEMV launch of one frame: layer tails, rms+q|k|v+RoPE, "
-                        "rms+w1|w3+SiLU, plain / split-K GEMVs, codebook heads"),
+            "kernels": ("every int8-weight GEMV call of one frame (C-ABI calls; a layer-stack call "
+                        "counts once): layer stacks and tails, rms+q|k|v+RoPE, rms+w1|w3+SiLU, "
+                        "plain / split-K GEMVs, codebook heads"),
             "achieved_GBps": round(g_gbps, 1),
             "frac": round(g_gbps / HBM_PEAK_GBPS, 4),
             "avg_launch_us": round(g_avg_us, 3),

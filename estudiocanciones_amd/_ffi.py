@@ -101,6 +101,8 @@ SIGNATURES = {
     "ecd_layer_stack_plan": [_P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P, _P],
     "ecd_layer_stack_plan_bytes": [c_int],
     "ecd_layer_stack_supported": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int],
+    "ecd_layer_stack_layers_per_launch": [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                          c_int],
     "ecd_layer_stack": [_P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int,
                         c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P],
 }

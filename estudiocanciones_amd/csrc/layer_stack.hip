@@ -5,8 +5,13 @@
 
 using namespace ecd;
 
+// Backbone layers per launch, unrolled: 28 layers as 4 launches (measured against 2 and 4 layers
+// per launch: 557.8 / 561.2 / 563.1 frames/s at KV 750; 14 per launch adds 0.1% for twice the
+// code and build time).
+constexpr int BB_NLU = 7;
+
 // Stack launches: the instantiated shapes.  The depth decoders take all their layers in one
-// launch; the backbone takes two layers per launch, unrolled (looped over its layers, its
+// launch; the backbone takes BB_NLU layers per launch, unrolled (looped over its layers, its
 // 3072-wide tail with the MFMA attention needs more than the 168 registers a lane has at three
 // waves per SIMD).  0: not instantiated, else an index for ecd_layer_stack's dispatch.
 static int stack_kind(int nb, int M, int D, int F, int Hq, int Hk, int HD, int L, bool ntl, bool knt) {
@@ -30,17 +35,25 @@ extern "C" int ecd_layer_stack_supported(int nl, int M, int D, int F, int Hq, in
                                          int L, int flags) {
   const int kind = stack_kind(tail::device_cus(), M, D, F, Hq, Hk, HD, L, (flags >> 1) & 1,
                               (flags >> 3) & 1);
-  // the backbone's two-layer launches take an even number of layers
-  if (nl < 1 || nl > ECD_STACK_MAX || ((kind == 1 || kind == 2) && nl % 2)) return ECD_ENOTSUP;
+  // the backbone's launches take BB_NLU layers each
+  if (nl < 1 || nl > ECD_STACK_MAX || ((kind == 1 || kind == 2) && nl % BB_NLU)) return ECD_ENOTSUP;
   switch (kind) {
-    case 1: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, false, 2>() ? ECD_OK : ECD_ENOTSUP;
-    case 2: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, true, 2>() ? ECD_OK : ECD_ENOTSUP;
+    case 1: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, false, BB_NLU>() ? ECD_OK : ECD_ENOTSUP;
+    case 2: return tail::stack_scratch_free<6, 16, 4, 1, 128, 3, true, 8, false, true, BB_NLU>() ? ECD_OK : ECD_ENOTSUP;
     case 3: return tail::stack_scratch_free<6, 16, 4, 1, 384, 2, false, 8, true, false>() ? ECD_OK : ECD_ENOTSUP;
     case 4: return tail::stack_scratch_free<6, 16, 4, 1, 384, 2, false, 16, true, false>() ? ECD_OK : ECD_ENOTSUP;
     case 5: return tail::stack_scratch_free<2, 16, 4, 4, 128, 4, false, 8, true, false>() ? ECD_OK : ECD_ENOTSUP;
     case 6: return tail::stack_scratch_free<2, 16, 4, 4, 128, 4, false, 16, true, false>() ? ECD_OK : ECD_ENOTSUP;
   }
   return ECD_ENOTSUP;
+}
+
+extern "C" int ecd_layer_stack_layers_per_launch(int nl, int M, int D, int F, int Hq, int Hk,
+                                                 int HD, int L, int flags) {
+  if (ecd_layer_stack_supported(nl, M, D, F, Hq, Hk, HD, L, flags) != ECD_OK) return ECD_ENOTSUP;
+  const int kind = stack_kind(tail::device_cus(), M, D, F, Hq, Hk, HD, L, (flags >> 1) & 1,
+                              (flags >> 3) & 1);
+  return kind == 1 || kind == 2 ? BB_NLU : nl;
 }
 
 extern "C" long ecd_layer_stack_plan_bytes(int nl) {
@@ -129,8 +142,8 @@ extern "C" int ecd_layer_stack(const void* plan, int nl, const void* o, const vo
   const tail::LayerRec* pl = (const tail::LayerRec*)plan;
   hipStream_t st = (hipStream_t)stream;
   switch (kind) {
-    case 1: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, false, 2>(a, pl, nl, nb, st);
-    case 2: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, true, 2>(a, pl, nl, nb, st);
+    case 1: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, false, BB_NLU>(a, pl, nl, nb, st);
+    case 2: return tail::launch_stack<6, 16, 4, 1, 128, 3, true, 8, false, true, BB_NLU>(a, pl, nl, nb, st);
     case 3: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 8, true, false>(a, pl, nl, nb, st);
     case 4: return tail::launch_stack<6, 16, 4, 1, 384, 2, false, 16, true, false>(a, pl, nl, nb, st);
     case 5: return tail::launch_stack<2, 16, 4, 4, 128, 4, false, 8, true, false>(a, pl, nl, nb, st);

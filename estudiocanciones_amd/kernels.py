@@ -660,6 +660,14 @@ def layer_stack_supported(nl, M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False)
         (2 if stream else 0) | (8 if kv_nt else 0)) == _ffi.ECD_OK
 
 
+def layer_stack_layers_per_launch(nl, M, D, F, Hq, Hk, HD, L, stream=False, kv_nt=False):
+    """Layers per kernel launch of a ``layer_stack`` call (0 when not supported)."""
+    r = _ffi.lib().ecd_layer_stack_layers_per_launch(
+        int(nl), int(M), int(D), int(F), int(Hq), int(Hk), int(HD), int(L),
+        (2 if stream else 0) | (8 if kv_nt else 0))
+    return max(int(r), 0)
+
+
 def layer_stack_plan(layers, M, D, F, Hq, Hk, HD, dev):
     """The device plan of a layer stack: ``layers`` is a list of dicts with the tensors of
     STACK_FIELDS (n1, wq, sq, kc, vc, o_next None only for the last layer; ``y``, a [M, N] view

@@ -351,12 +351,17 @@ long ecd_layer_stack_plan_bytes(int nl);
 
 /* ECD_OK when ecd_layer_stack runs nl layers of these shapes with these flags (bit 1 streamed
  * weights, bit 3 nontemporal cache-slot loads) on the current device: the backbone (3072 wide,
- * 24q / 8kv, head_dim 128, streamed weights, up to 8 rows, an even number of layers: two per
+ * 24q / 8kv, head_dim 128, streamed weights, up to 8 rows, a multiple of 7 layers: 7 per
  * launch) and the two depth decoders (3072 wide with head_dim 384, 1024 wide with head_dim 128;
  * caches of at most 8 slots; up to 16 rows; weights not streamed; all layers in one launch).
  * No reference counterpart. */
 int ecd_layer_stack_supported(int nl, int M, int D, int F, int Hq, int Hk, int HD, int L,
                               int flags);
+
+/* Layers per kernel launch of an ecd_layer_stack call with these arguments (nl / that many
+ * launches), or ECD_ENOTSUP.  No reference counterpart. */
+int ecd_layer_stack_layers_per_launch(int nl, int M, int D, int F, int Hq, int Hk, int HD, int L,
+                                      int flags);
 
 /* One launch for the nl layers of plan (written by ecd_layer_stack_plan): layer 0 starts from o
  * and xin [M, D]; the result is the last layer's xout (and, with a head record, its logits y:

@@ -283,8 +283,8 @@ def test_tail_two_rows_per_cache_vs_oracle(dev, cfg, first):
 
 
 @pytest.mark.parametrize("cfg,L,stream,kv_nt,S", [
-    (dict(BB3, layers=4), 1024, True, False, 1),  # backbone shape, two launches of two layers
-    (dict(BB3, layers=2), 4096, True, True, 1),   # long splits (staged third tile), NT slot loads
+    (dict(BB3, layers=14), 1024, True, False, 1),  # backbone shape, two launches of 7 layers
+    (dict(BB3, layers=7), 4096, True, True, 1),    # long splits (staged third tile), NT slot loads
     (dict(DEC3, layers=4), 8, False, False, 1),   # 1024-wide decoder, VALU attention
     (dict(DEC3, layers=4), 8, False, False, 2),   # its first pass: two rows per cache
     (dict(DEC_REF2, layers=3), 8, False, False, 1),  # the reference decoder, head_dim 384
@@ -329,8 +329,8 @@ def test_layer_stack_equals_per_layer_tails(dev, cfg, L, stream, kv_nt, S):
         assert not st.tail_error()
         return out, [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
 
-    # the backbone's stack takes its layers two per launch
-    assert not layer_stack_supported(3, B, 3072, 8192, 24, 8, 128, 1024, True, False)
+    # the backbone's stack takes its layers 7 per launch
+    assert not layer_stack_supported(4, B, 3072, 8192, 24, 8, 128, 1024, True, False)
     want, wkv = run(False)
     for rep in range(3):
         got, gkv = run(True)
