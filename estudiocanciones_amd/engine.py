@@ -330,14 +330,18 @@ class Stack:
 
     def head_plans(self, heads):
         """Stack plans that end in a codebook head: ``heads`` maps an index to (packed head
-        Linear, logits buffer [M, N] with 16-byte aligned rows).  The last layer's record then
-        runs rms(xout, stack norm) -> head GEMV into the buffer (the 1024-wide decoder; other
-        stacks keep the head as its own launch).  Used by decode_head."""
-        t = self.tail
-        if t is None or t.get("plan") is None or self.dim != 1024:
+        Linear, logits buffer [M, N] with 16-byte aligned rows; M selects the buffers of B or 2B
+        rows).  The last layer's record then runs rms(xout, stack norm) -> head GEMV into the
+        buffer (the 1024-wide decoder; other stacks keep the head as its own launch).  Used by
+        decode_head."""
+        if self.dim != 1024:
             return
         b0, F = self.blocks[0], self.blocks[0].w2.K
         for i, (hd, y) in heads.items():
+            t = next((t for t in (self.tail, self.tail2)
+                      if t is not None and t["M"] == y.shape[0]), None)
+            if t is None or t.get("plan") is None:
+                continue
             layers = self._stack_records(t)
             layers[-1].update(n1=self.norm, wq=hd.qp, sq=hd.s8, y=y)
             t["hplans"][i] = (layer_stack_plan(layers, t["M"], self.dim, F, b0.h, b0.kvh, b0.hd,
@@ -348,8 +352,8 @@ class Stack:
         logits buffer of that head, or None when the step cannot run as such a stack launch
         (the caller then runs decode and the head GEMV)."""
         R = x.shape[0]
-        t = self.tail
-        if t is None or R != t["M"] or head not in t.get("hplans", {}) or not self.use_tail:
+        t = next((t for t in (self.tail, self.tail2) if t is not None and R == t["M"]), None)
+        if t is None or head not in t.get("hplans", {}) or not self.use_tail:
             return None
         return self._decode_tail(x, pos, S, t, o0, head=head)
 
@@ -719,11 +723,10 @@ class HeartMuLaLite:
                                 stream=True, out=y)
             pick(0, y[:, :AUDIO_VOCAB], nxt[0], x=self._x0[1::2], ev=y[:, cp.n0:],
                  xe=self._x0[0::2])
-            h = self._decode(self._x0, self._pass0_pos, 2)[1::2]
+            lg = self._decode_head0(self._x0)
         else:
             c0 = pick(0, self._c0(last_h))
-            h = self._decode(self._project(c0, 0, even=last_h), self._pass0_pos, 2)[1::2]
-        lg = self._head(0, h)
+            lg = self._decode_head0(self._project(c0, 0, even=last_h))
         for i in range(1, N_CB):
             rows = nxt[i] if nxt is not None and i < N_CB - 1 else None
             qkv = nqkv[i - 1] if rows is not None and nqkv is not None else None
@@ -744,6 +747,17 @@ class HeartMuLaLite:
         if self._packed_decoder():
             return self.decoder.decode(x, pos, S, final_norm=False, o0=o0)
         return self.decoder.decode(x, pos, S, o0=o0)
+
+    def _decode_head0(self, x):
+        """The first decoder pass (two rows per take) and audio_head[0] of its odd rows: one
+        layer-stack launch that ends in the head (on all rows) where its plan exists, else the
+        pass and the head GEMV on the odd rows."""
+        lg = None
+        if self._hlog is not None:
+            lg = self.decoder.decode_head(x, self._pass0_pos, 2, 0)
+        if lg is not None:
+            return lg[1::2]
+        return self._head(0, self._decode(x, self._pass0_pos, 2)[1::2])
 
     def _decode_head(self, x, pos, i, o0=None):
         """Decoder pass i (1 .. 6, one row per take) and audio_head[i] of its output: one
@@ -815,7 +829,9 @@ class HeartMuLaLite:
         # stack supports it: one logits buffer per head
         self._hlog = None
         if self._packed_decoder():
+            # (the first pass's head runs on its 2B rows; the odd ones are the codebook-1 logits)
             self._hlog = {i: self._logits(self.B, AUDIO_VOCAB) for i in range(1, N_CB - 1)}
+            self._hlog[0] = self._logits(2 * self.B, AUDIO_VOCAB)
             self.decoder.head_plans({i: (self.audio_head[i], y) for i, y in self._hlog.items()})
         self._alloc_next_rows()
 

@@ -355,13 +355,14 @@ def test_layer_stack_equals_per_layer_tails(dev, cfg, L, stream, kv_nt, S):
     assert not st.tail_error()
 
 
-@pytest.mark.parametrize("nblocks,N", [(4, 8197), (2, 8197), (4, 3000)])
-def test_layer_stack_with_codebook_head(dev, nblocks, N):
+@pytest.mark.parametrize("nblocks,N,S", [(4, 8197, 1), (2, 8197, 1), (4, 3000, 1), (4, 8197, 2)])
+def test_layer_stack_with_codebook_head(dev, nblocks, N, S):
     """A 1024-wide decoder stack whose last layer ends in a codebook head (rms(x', norm) ->
     int8 head GEMV into logits rows of stride 8256): against the stack's output through the
     separate RMS-prologue GEMV.  Same numerics up to the fp32 summation order of the rms sum,
     so the fp16 bar holds for all but a few logits, 3x it for all; the caches match bit for bit.
-    8197 columns: 513 tiles, the first workgroup takes a third."""
+    8197 columns: 513 tiles, the first workgroup takes a third.  S = 2: the first decoder
+    pass's shape (two rows per cache, 16 rows)."""
     import torch
     from estudiocanciones_amd.engine import Linear
     from estudiocanciones_amd.kernels import rms_gemv_packed
@@ -373,7 +374,7 @@ def test_layer_stack_with_codebook_head(dev, nblocks, N):
     g.manual_seed(53)
     q8, s8 = q8_rows(torch.randn(N, 1024, generator=g, device=dev) * 0.02)
     head = Linear(q8=q8, s8=s8.to(torch.float16)).pack()
-    y = torch.empty(B, -(-N // 64) * 64, device=dev, dtype=torch.float16)[:, :N]
+    y = torch.empty(S * B, -(-N // 64) * 64, device=dev, dtype=torch.float16)[:, :N]
     st.head_plans({3: (head, y)})
     kv0 = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
 
@@ -382,15 +383,19 @@ def test_layer_stack_with_codebook_head(dev, nblocks, N):
             b.kc.copy_(k)
             b.vc.copy_(v)
 
-    p = rng(54).integers(0, L, B).astype(np.int64)
+    if S == 1:
+        p = rng(54).integers(0, L, B).astype(np.int64)
+    else:  # a row pair per cache at consecutive slots
+        p = rng(54).integers(0, L - 1, B)
+        p = np.stack([p, p + 1], 1).reshape(-1).astype(np.int64)
     pos = torch.from_numpy(p).to(dev)
-    x = torch.from_numpy(randn16(55, B, 1024)).to(dev)
-    h = st.decode(x, pos, 1, final_norm=False)
+    x = torch.from_numpy(randn16(55, S * B, 1024)).to(dev)
+    h = st.decode(x, pos, S, final_norm=False)
     want = N_(rms_gemv_packed(h, st.norm, head.qp, head.s8, N, 1024)).astype(np.float32)
     wkv = [(b.kc.clone(), b.vc.clone()) for b in st.blocks]
     for rep in range(2):
         reset()
-        got = st.decode_head(x, pos, 1, 3)
+        got = st.decode_head(x, pos, S, 3)
         torch.cuda.synchronize()
         assert got is not None and got.data_ptr() == y.data_ptr()
         assert not st.tail_error()
@@ -401,7 +406,7 @@ def test_layer_stack_with_codebook_head(dev, nblocks, N):
         for i, ((gk, gv2), (wk, wv)) in enumerate(zip([(b.kc, b.vc) for b in st.blocks], wkv)):
             assert torch.equal(gk, wk) and torch.equal(gv2, wv), f"layer {i} caches differ"
     # no plan for this head index: the caller falls back
-    assert st.decode_head(x, pos, 1, 4) is None
+    assert st.decode_head(x, pos, S, 4) is None
 
 
 def N_(t):
