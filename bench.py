@@ -275,9 +275,10 @@ def measure_point(torch, E, model, dev, n, kv, steps, warmup, g):
     static = dict(tok=tok, pos=torch.full((B, 1), kv - 1, dtype=torch.long, device=dev))
     graph, out = model._capture(static, Lcap, 1.5, 50, 1.0)
     torch.cuda.synchronize()
-    # The capture's eager warm-up frame is not measured.  A gate timeout there (seen only on a
-    # kernel's first dispatch in the process, under rocprofv3) is reported and the gate regions
-    # are cleared before the replays; a timeout in the replays voids the measurement below.
+    # The capture's eager warm-up frame is not measured.  A gate timeout there (seen on a
+    # kernel's first dispatch on a stream) is reported and the gate regions are cleared before
+    # the replays (the engine's capture does so itself, with a RuntimeWarning); a timeout in the
+    # replays voids the measurement below.
     if model.tail_error():
         print(f"KV {kv}: a layer-tail launch of the eager warm-up frame timed out at a gate "
               f"(error words: backbone {model.backbone.tail_error():#x}, decoder "

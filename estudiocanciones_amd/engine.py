@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import json
 import math
+import warnings
 from pathlib import Path
 
 import torch
@@ -1013,6 +1014,15 @@ class HeartMuLaLite:
         with torch.cuda.stream(s):
             self._step(static["tok"], static["pos"], bucket, cfg, topk, temp, **kw)
         torch.cuda.current_stream(self.dev).wait_stream(s)
+        # a layer-tail wait that gave up in this warm-up (seen on a persistent kernel's first
+        # dispatch on a stream): its outputs are discarded and the replays redo its cache
+        # writes, so the gate regions are cleared; a timeout in a replay still raises (the song
+        # loop reads the error words)
+        if self.tail_error():
+            warnings.warn("a layer-tail wait of the capture's eager warm-up gave up (error words "
+                          f"backbone {self.backbone.tail_error():#x}, decoder "
+                          f"{self.decoder.tail_error():#x}); gate regions cleared", RuntimeWarning)
+            self.tail_reset()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, pool=getattr(self, "_pool", None)):
             out = self._step(static["tok"], static["pos"], bucket, cfg, topk, temp, **kw)

@@ -104,3 +104,15 @@ def assert_within_noise(got, want, want_alt, what="", factor=3.0, atol=ATOL, rto
         f"{what}: max error {eg.max():.3e} vs oracle re-association {en.max():.3e}"
     assert fg <= factor * fn + max(1e-3, 4.0 / eg.size), \
         f"{what}: {fg:.4%} outside the kernel bar vs oracle re-association {fn:.4%}"
+
+
+def clear_warmup_timeout(st, what=""):
+    """After the eager warm-up of a graph capture (a side stream: the kernels' first dispatch
+    there): a layer-tail wait that gave up in it is reported and the gate regions cleared, as
+    the engine's capture does (its results are discarded, the replays redo its cache writes).
+    The replays themselves must then run without one."""
+    e = st.tail_error()
+    if e:
+        print(f"[warm-up] {what}: a layer-tail wait of the capture's warm-up gave up "
+              f"(error word {e:#x}); gate regions cleared", flush=True)
+        st.tail_reset()

@@ -8,7 +8,8 @@ handed to the oracle as codes and bf16 scales."""
 import numpy as np
 import pytest
 
-from helpers import ATOL, RTOL, assert_close16, assert_within_noise, randn16, rng
+from helpers import (ATOL, RTOL, assert_close16, assert_within_noise, clear_warmup_timeout,
+                     randn16, rng)
 from oracle import kernels as OK
 from oracle.model import OLinear, OStack
 
@@ -181,6 +182,7 @@ def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
     with torch.cuda.stream(s):
         st.decode(x, pos, 1)
     torch.cuda.current_stream(dev).wait_stream(s)
+    clear_warmup_timeout(st, "tail path")
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
         gout = st.decode(x, pos, 1)
@@ -189,7 +191,7 @@ def test_tail_matches_per_op_kernels_and_repeats(dev, cfg, L, stream):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(gout, outs[0]), "graph replay of the tail path differs from eager"
-    assert not st.tail_error()
+        assert not st.tail_error()
 
 
 @pytest.mark.parametrize("cfg,L", [(dict(BB3, layers=2), 512), (dict(DEC3, layers=2), 8),
@@ -344,6 +346,7 @@ def test_layer_stack_equals_per_layer_tails(dev, cfg, L, stream, kv_nt, S):
     with torch.cuda.stream(s):
         st.decode(x, pos, S)
     torch.cuda.current_stream(dev).wait_stream(s)
+    clear_warmup_timeout(st, "stack path")
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
         gout = st.decode(x, pos, S)
@@ -352,7 +355,7 @@ def test_layer_stack_equals_per_layer_tails(dev, cfg, L, stream, kv_nt, S):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(gout, want), "graph replay of the stack path differs"
-    assert not st.tail_error()
+        assert not st.tail_error()
 
 
 @pytest.mark.parametrize("nblocks,N,S", [(4, 8197, 1), (2, 8197, 1), (4, 3000, 1), (4, 8197, 2)])
